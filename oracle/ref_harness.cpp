@@ -1,0 +1,218 @@
+// Test infrastructure only: a harness that compiles the reference's own CPU
+// engine (TenzoEngine.cpp, read in place from the reference checkout) and
+// exposes its hot-path functions through a flat C ABI, so tests can produce
+// golden vectors and bench.py can time the reference CPU path as a baseline.
+// Nothing in the product (tenzo_amd/) links or loads this library.
+//
+// The include below pulls the reference translation unit into this one, which
+// makes its anonymous-namespace helpers (build_lut, compute_from_lut,
+// rms_norm_raw, pack_ternary_weights_raw) callable from here.
+#include "runtime/TenzoEngine.cpp"
+
+#include <cstdint>
+#include <cstring>
+#include <vector>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+using tenzo::FusedKVCache;
+using tenzo::TenzoEngineImpl;
+using tenzo::Vec256i;
+
+extern "C" {
+
+// build_lut (TenzoEngine.cpp:22-62): returns absmax/31 and the 32-byte LUT
+// record per k-pair (K/2 * 32 bytes).
+float ref_build_lut(const float* x, int64_t K, int8_t* lut_out) {
+    std::vector<Vec256i> lut(K / 2);
+    float inv = tenzo::build_lut(x, K, reinterpret_cast<__m256i*>(lut.data()));
+    std::memcpy(lut_out, lut.data(), static_cast<size_t>(K / 2) * 32);
+    return inv;
+}
+
+// build_lut + compute_from_lut (TenzoEngine.cpp:22-146, as called at :1585-1586).
+void ref_tl1_gemv(const float* x, const int8_t* w, int64_t K, int64_t N,
+                  float w_scale, float* y) {
+    std::vector<Vec256i> lut(K / 2);
+    float inv = tenzo::build_lut(x, K, reinterpret_cast<__m256i*>(lut.data()));
+    tenzo::compute_from_lut(reinterpret_cast<const __m256i*>(lut.data()), w, N / 64,
+                            K / 2, y, inv * w_scale);
+}
+
+// Same, with total scale 1.0 so y = float(acc) exactly; returns the int32
+// accumulators (|acc| <= 31*K < 2^24, so the float round trip is exact).
+float ref_tl1_gemv_acc(const float* x, const int8_t* w, int64_t K, int64_t N,
+                       int32_t* acc) {
+    std::vector<Vec256i> lut(K / 2);
+    std::vector<float> y(N);
+    float inv = tenzo::build_lut(x, K, reinterpret_cast<__m256i*>(lut.data()));
+    tenzo::compute_from_lut(reinterpret_cast<const __m256i*>(lut.data()), w, N / 64,
+                            K / 2, y.data(), 1.0f);
+    for (int64_t n = 0; n < N; ++n) acc[n] = static_cast<int32_t>(y[n]);
+    return inv;
+}
+
+// rms_norm_raw (TenzoEngine.cpp:148-166).
+void ref_rms_norm(const float* x, const float* w, float* y, int dim, float eps) {
+    tenzo::rms_norm_raw(x, w, y, dim, eps);
+}
+
+// pack_ternary_weights_raw (TenzoEngine.cpp:1842-1884): HF [N/4][K] 2-bit -> TL1.
+void ref_pack_raw(const uint8_t* raw, int64_t N, int64_t K, int8_t* out) {
+    std::vector<int8_t> p = tenzo::pack_ternary_weights_raw(raw, N, K);
+    std::memcpy(out, p.data(), p.size());
+}
+
+// FusedKVCache::forward_attention_raw (TenzoEngine.cpp:447-919), int8_fused mode,
+// one layer. The caller's cache arrays ([Hkv][max_seq][128] codes, [Hkv][max_seq]
+// fp32 scales) are copied in, the call appends at position pos, and the cache
+// (with the appended token), the rotated q/k and the output are copied back.
+void ref_attention_int8(int Hq, int Hkv, int max_seq, int pos,
+                        float* q, float* k, float* v,
+                        int8_t* kc, int8_t* vc, float* ks, float* vs,
+                        float* out) {
+    FusedKVCache c(1, Hq, Hkv, 128, max_seq, "int8_fused");
+    size_t n_el = static_cast<size_t>(Hkv) * max_seq * 128;
+    size_t n_sc = static_cast<size_t>(Hkv) * max_seq;
+    std::memcpy(c.int8_k.data(), kc, n_el);
+    std::memcpy(c.int8_v.data(), vc, n_el);
+    std::memcpy(c.int8_k_scales.data(), ks, n_sc * 4);
+    std::memcpy(c.int8_v_scales.data(), vs, n_sc * 4);
+    c.cur_seq_len = pos;
+    c.forward_attention_raw(0, q, k, v, out);
+    std::memcpy(kc, c.int8_k.data(), n_el);
+    std::memcpy(vc, c.int8_v.data(), n_el);
+    std::memcpy(ks, c.int8_k_scales.data(), n_sc * 4);
+    std::memcpy(vs, c.int8_v_scales.data(), n_sc * 4);
+}
+
+// Quantized GEMV free functions (TenzoEngine.cpp:1022-1175).
+void ref_q4_0(const float* a, const uint8_t* w, float* y, int K, int N) {
+    tenzo::compute_linear_gguf_q4_0(a, w, y, K, N);
+}
+void ref_q8_0(const float* a, const uint8_t* w, float* y, int K, int N) {
+    tenzo::compute_linear_gguf_q8_0(a, w, y, K, N);
+}
+void ref_gptq(const float* a, const uint32_t* qw, const float* s, const uint32_t* qz,
+              float* y, int K, int N, int group) {
+    tenzo::compute_linear_gptq(a, qw, s, qz, y, K, N, group);
+}
+void ref_awq(const float* a, const uint32_t* qw, const float* s, const uint32_t* qz,
+             float* y, int K, int N, int group) {
+    tenzo::compute_linear_awq(a, qw, s, qz, y, K, N, group);
+}
+
+// ---- Whole engine (TenzoEngine.cpp:1215-1838) through the reference's C API ----
+
+void* ref_engine_create(int H, int Hq, int Hkv, int L, int F, int V, int max_seq) {
+    tenzo_config_t cfg = tenzo_default_config();
+    cfg.hidden_size = H;
+    cfg.num_q_heads = Hq;
+    cfg.num_kv_heads = Hkv;
+    cfg.head_dim = 128;
+    cfg.num_layers = L;
+    cfg.ffn_dim = F;
+    cfg.vocab_size = V;
+    cfg.max_seq_len = max_seq;
+    cfg.kv_mode = "int8_fused";
+    cfg.device = "cpu";
+    return tenzo_create_engine(&cfg);
+}
+
+void ref_engine_destroy(void* e) { tenzo_destroy_engine(static_cast<tenzo_engine_t>(e)); }
+
+int ref_engine_set_layer(void* e, int l, const tenzo_layer_weights_t* w) {
+    return tenzo_set_layer_weights(static_cast<tenzo_engine_t>(e), l, w);
+}
+
+int ref_engine_set_head(void* e, const int8_t* W, const float* s, const float* final_norm,
+                        int V, int H) {
+    auto* eng = static_cast<tenzo_engine_t>(e);
+    int st = tenzo_set_lm_head_i8(eng, W, s, V, H);
+    if (st) return st;
+    return tenzo_set_final_norm(eng, final_norm);
+}
+
+// Prefill the int8 cache directly (public FusedKVCache state) instead of running
+// seq_len prefill steps. Arrays are [L][Hkv][max_seq][128] / [L][Hkv][max_seq].
+void ref_engine_set_kv(void* e, const int8_t* kc, const int8_t* vc, const float* ks,
+                       const float* vs, int seq_len) {
+    FusedKVCache& c = static_cast<tenzo_engine_t>(e)->impl->kv_cache;
+    std::memcpy(c.int8_k.data(), kc, c.int8_k.size());
+    std::memcpy(c.int8_v.data(), vc, c.int8_v.size());
+    std::memcpy(c.int8_k_scales.data(), ks, c.int8_k_scales.size() * 4);
+    std::memcpy(c.int8_v_scales.data(), vs, c.int8_v_scales.size() * 4);
+    c.cur_seq_len = seq_len;
+}
+
+void ref_engine_get_kv(void* e, int8_t* kc, int8_t* vc, float* ks, float* vs) {
+    FusedKVCache& c = static_cast<tenzo_engine_t>(e)->impl->kv_cache;
+    std::memcpy(kc, c.int8_k.data(), c.int8_k.size());
+    std::memcpy(vc, c.int8_v.data(), c.int8_v.size());
+    std::memcpy(ks, c.int8_k_scales.data(), c.int8_k_scales.size() * 4);
+    std::memcpy(vs, c.int8_v_scales.data(), c.int8_v_scales.size() * 4);
+}
+
+int ref_engine_seq_len(void* e) { return tenzo_get_seq_len(static_cast<tenzo_engine_t>(e)); }
+
+// One greedy decode step (temperature 0, penalty 1.0); copies the logits out
+// when logits is non-null and returns the token.
+int ref_engine_step(void* e, int token, float* logits) {
+    auto* eng = static_cast<tenzo_engine_t>(e);
+    tenzo_sampling_params_t p = tenzo_default_sampling_params();
+    p.temperature = 0.0f;
+    p.repetition_penalty = 1.0f;
+    int tok = tenzo_generate_step(eng, token, &p, nullptr, 0);
+    if (logits) {
+        const auto& ls = eng->impl->logits_scratch;
+        std::memcpy(logits, ls.data(), ls.size() * 4);
+    }
+    return tok;
+}
+
+int ref_engine_prefill(void* e, int token) {
+    return tenzo_prefill_token(static_cast<tenzo_engine_t>(e), token);
+}
+
+// Hidden state after the layers of the last step (buf_x), for stage checks.
+void ref_engine_hidden(void* e, float* x) {
+    auto* eng = static_cast<tenzo_engine_t>(e);
+    std::memcpy(x, eng->impl->buf_x.data(), eng->impl->config.hidden_size * 4);
+}
+
+// Stage-level access for tracing one step: embedding, one layer, and the
+// engine's scratch buffers by index (TenzoEngine.h:216-230 order).
+void ref_engine_embed(void* e, int token) {
+    static_cast<tenzo_engine_t>(e)->impl->embedding_lookup(token);
+}
+void ref_engine_layer(void* e, int l) {
+    static_cast<tenzo_engine_t>(e)->impl->forward_layer_raw(l);
+}
+void ref_engine_finish(void* e) {
+    auto* impl = static_cast<tenzo_engine_t>(e)->impl.get();
+    impl->kv_cache.increment_seq_len(1);
+    impl->compute_logits();
+}
+int ref_engine_buf(void* e, int which, float* out) {
+    auto* impl = static_cast<tenzo_engine_t>(e)->impl.get();
+    std::vector<float>* bufs[] = {
+        &impl->buf_x, &impl->buf_norm_x, &impl->buf_q, &impl->buf_k, &impl->buf_v,
+        &impl->buf_attn_out, &impl->buf_attn_sub, &impl->buf_out, &impl->buf_h1,
+        &impl->buf_post_norm, &impl->buf_gate, &impl->buf_up, &impl->buf_act,
+        &impl->buf_ffn_norm, &impl->buf_down, &impl->logits_scratch};
+    if (which < 0 || which >= 16) return -1;
+    std::vector<float>& b = *bufs[which];
+    std::memcpy(out, b.data(), b.size() * 4);
+    return static_cast<int>(b.size());
+}
+
+int ref_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+}  // extern "C"

@@ -1,0 +1,156 @@
+/*
+ * tenzo_oracle.h - CPU restatement of Tenzo's quantized decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker. The product
+ * (tenzo_amd/, libtenzo_hip.so) never calls it.
+ *
+ * Every function restates one reference function (file:line into the reference
+ * checkout, src/runtime/TenzoEngine.cpp unless noted). Plain scalar C, built with
+ * -ffp-contract=off so that the only fused multiply-adds are the explicit fmaf()
+ * calls, which stand where the reference's AVX2 code issues _mm256_fmadd_ps.
+ *
+ * Pinning (how each function is checked, in tests/test_oracle.py):
+ *   orc_tl1_pack, orc_tl1_pack_raw   reference packers' layout (golden vectors
+ *                                    from the compiled reference) + brute-force
+ *                                    unpack round trip
+ *   orc_quant31, orc_build_lut       compiled-reference goldens (bit-exact LUT
+ *                                    bytes and scale) + closed form
+ *   orc_tl1_gemv_i32 / orc_tl1_gemv  closed form sum_k W[n,k]*a_k (dense brute
+ *                                    force) + compiled-reference goldens (bit-exact)
+ *   orc_rms_norm                     fp64 brute force (1e-6 rel) + compiled
+ *                                    reference (1e-6 rel; its summation order is
+ *                                    compiler-defined under -ffast-math)
+ *   orc_kv_quant                     compiled-reference goldens (bit-exact codes)
+ *                                    + special cases (all-zero, single spike)
+ *   orc_rope_table, orc_rope_apply   compiled reference (bit-exact rotated q/k) +
+ *                                    fp64 closed form
+ *   orc_attn_int8                    fp64 brute-force softmax attention over the
+ *                                    dequantized cache (1e-3) + compiled reference
+ *                                    + ctx=1 special case
+ *   orc_lm_head                      closed-form int32 dot + compiled reference
+ *   orc_q4_0, orc_q8_0, orc_gptq,
+ *   orc_awq                          fp64 brute force of each dequant formula +
+ *                                    compiled-reference goldens (layout conventions)
+ *   orc_q4_0_q8act, orc_quantize_q8_0  no reference counterpart: closed form
+ *                                    (fp64 brute force of the block formula); the
+ *                                    Q8_0 quantizer follows llama.cpp's published
+ *                                    quantize_row_q8_0 and is "parity unpinned"
+ *                                    against any reference output
+ *   orc_decode_step                  compiled reference whole-engine step on small
+ *                                    configs (logits 1e-3, greedy token equal)
+ *   orc_argmax                       brute force (first maximum)
+ */
+#ifndef TENZO_ORACLE_H
+#define TENZO_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- fp16 helpers (IEEE binary16, round to nearest even) ---- */
+float orc_f16_to_f32(uint16_t h);
+uint16_t orc_f32_to_f16(float f);
+
+/* ---- TL1 packing ---- */
+/* Dense ternary [N][K] in {-1,0,1} -> TL1 [N/64][K/2][32]
+ * (PybindModule.cpp:315-355). */
+void orc_tl1_pack(const int8_t* tern, int64_t N, int64_t K, uint8_t* out);
+/* HF 2-bit [N/4][K] (row r at byte r/4, shift 2*(r%4)) -> TL1 (TenzoEngine.cpp:1842-1884). */
+void orc_tl1_pack_raw(const uint8_t* raw, int64_t N, int64_t K, uint8_t* out);
+/* TL1 -> dense ternary [N][K] (inverse of orc_tl1_pack). */
+void orc_tl1_unpack(const uint8_t* w, int64_t N, int64_t K, int8_t* tern);
+
+/* ---- activation quantization for TL1 (build_lut, TenzoEngine.cpp:22-62) ---- */
+/* codes[k] = round(x[k] * (31/absmax)); returns absmax/31. */
+float orc_quant31(const float* x, int64_t K, int8_t* codes);
+/* The 32-byte LUT record per k-pair, as build_lut writes it. */
+void orc_build_lut(const int8_t* codes, int64_t K, int8_t* lut);
+
+/* ---- TL1 GEMV (compute_single_block / compute_from_lut, :64-146) ---- */
+void orc_tl1_gemv_i32(const uint8_t* w, const int8_t* codes, int64_t N, int64_t K,
+                      int32_t* acc);
+/* y[n] = float(acc[n]) * (absmax/31 * w_scale); acc optional. Returns absmax/31. */
+float orc_tl1_gemv(const float* x, const uint8_t* w, int64_t N, int64_t K, float w_scale,
+                   float* y, int32_t* acc);
+
+/* ---- RMSNorm (rms_norm_raw, :148-166) ---- */
+/* Sum of squares in a fixed order: 256 strided partials p[t] = fma-accumulated
+ * x[t], x[t+256], ..., then a balanced pairwise tree over p[0..255]. */
+float orc_sumsq(const float* x, int64_t n);
+void orc_rms_norm(const float* x, const float* w, float* y, int64_t dim, float eps);
+
+/* ---- INT8 KV cache (FusedKVCache, TenzoEngine.h:60-115, .cpp:506-533) ---- */
+/* codes = clamp(round(x/s)), s = max(1e-8, amax)/127; returns s. */
+float orc_kv_quant(const float* x, int d, int8_t* codes);
+/* RoPE angle table for one position (:454-504 formula, theta as a parameter):
+ * cs[i] = cosf(pos*f_i), cs[d/2+i] = sinf(pos*f_i) with f_i = 1/theta^(2i/d)
+ * evaluated as the reference build does: expf(-(2i/d) * logf(theta)) in fp32,
+ * angle = (float)pos * f_i in fp32, glibc cosf/sinf. */
+void orc_rope_table(float theta, int head_dim, int pos, float* cs);
+/* In-place NeoX half-split rotation of nheads heads (:460-504). */
+void orc_rope_apply(float* x, int nheads, int head_dim, const float* cs);
+/* Decode attention over t in [0, seq_len) for Hq query heads, GQA map
+ * kvh = qh / (Hq/Hkv) (:657-919, int8 branches). Cache arrays are
+ * [Hkv][max_seq][128] codes and [Hkv][max_seq] fp32 scales. */
+void orc_attn_int8(const float* q, const int8_t* kc, const int8_t* vc, const float* ks,
+                   const float* vs, int Hq, int Hkv, int max_seq, int seq_len,
+                   float* out);
+/* forward_attention_raw as a whole: RoPE on q/k (in place), quantize-append k/v
+ * at pos (scale stored as fp32, or fp16-rounded when f16_scales != 0), then
+ * attention over pos+1 tokens. */
+void orc_attention_step(float* q, float* k, const float* v, int8_t* kc, int8_t* vc,
+                        float* ks, float* vs, int Hq, int Hkv, int max_seq, int pos,
+                        const float* rope_cs, int f16_scales, float* out);
+
+/* ---- int8 LM head (compute_logits, :1634-1720), input already normalized ---- */
+/* Returns s_x; codes optional. */
+float orc_lm_head(const float* xn, const int8_t* W, const float* scales, int64_t V,
+                  int64_t H, float* logits, int8_t* codes);
+int orc_argmax(const float* logits, int64_t V);
+/* embedding_lookup int8 branch (:1294-1316). */
+void orc_embed_i8(const int8_t* E, const float* scales, int64_t H, int token, float* x);
+
+/* ---- quantized GEMVs (:1022-1175) ---- */
+void orc_q4_0(const float* a, const uint8_t* w, float* y, int K, int N);
+void orc_q8_0(const float* a, const uint8_t* w, float* y, int K, int N);
+void orc_gptq(const float* a, const uint32_t* qweight, const float* scales,
+              const uint32_t* qzeros, float* y, int K, int N, int group);
+void orc_awq(const float* a, const uint32_t* qweight, const float* scales,
+             const uint32_t* qzeros, float* y, int K, int N, int group);
+/* Q8_0 activation blocks (34 B: fp16 d + 32 int8), llama.cpp quantize_row_q8_0. */
+void orc_quantize_q8_0(const float* x, int K, uint8_t* out);
+/* Q4_0 weights x Q8_0 activations (closed form; no reference counterpart). */
+void orc_q4_0_q8act(const uint8_t* qa, const uint8_t* w, float* y, int K, int N);
+
+/* ---- whole decode step (forward_layer_raw :1522-1632, generate_step :1821-1838) ---- */
+typedef struct {
+    int hidden, n_q_heads, n_kv_heads, n_layers, ffn, vocab, max_seq;
+    float eps;            /* 1e-5 (rms_norm_raw default) */
+    int f16_kv_scales;    /* store KV scales rounded to fp16 */
+    /* per layer, TL1 [N/64][K/2][32] */
+    const uint8_t** q_w; const uint8_t** k_w; const uint8_t** v_w; const uint8_t** o_w;
+    const uint8_t** gate_w; const uint8_t** up_w; const uint8_t** down_w;
+    const float* scales;  /* [n_layers][7]: q,k,v,o,gate,up,down */
+    const float** in_norm; const float** attn_sub_norm; const float** post_norm;
+    const float** ffn_sub_norm;
+    const float* final_norm;
+    const int8_t* embed;  /* [vocab][hidden] int8, tied LM head */
+    const float* embed_scales;
+    /* KV cache state, [n_layers][n_kv_heads][max_seq][128] / [..][max_seq] */
+    int8_t* kc; int8_t* vc; float* ks; float* vs;
+} orc_model_t;
+
+/* Runs one token through all layers at position pos (appending to the cache),
+ * then the LM head; writes logits (vocab) and the final hidden state (hidden),
+ * either may be null. rope_cs is the per-position table (head_dim floats).
+ * Returns the greedy token. */
+int orc_decode_step(const orc_model_t* m, int token, int pos, const float* rope_cs,
+                    float* logits, float* hidden);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,244 @@
+"""Writes tests/golden/*.npz: input/output vectors of the reference's own CPU
+path, produced by the reference engine compiled in place from the reference
+checkout (oracle/_ref/libtenzo_ref.so, built by ``make -C oracle ref``).
+
+Run in the development container (the reference checkout is not present on
+the GPU box):  python tests/golden/make_golden.py
+
+Each fixture stores every input it was made from, so the tests never need to
+regenerate inputs. Seeds are fixed per fixture.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+import oracle  # noqa: E402
+from tenzo_amd import formats, synth  # noqa: E402
+
+OUT = os.path.dirname(os.path.abspath(__file__))
+P = oracle._ptr
+
+
+def save(name, **arrays):
+    path = os.path.join(OUT, name + ".npz")
+    np.savez_compressed(path, **arrays)
+    print(f"wrote {path} ({os.path.getsize(path)} B)")
+
+
+def tl1_fixture():
+    R = oracle.ref()
+    rng = np.random.default_rng(101)
+    out = {}
+    for tag, (N, K) in {"a": (128, 2560), "b": (64, 6912), "c": (192, 64)}.items():
+        tern = rng.integers(-1, 2, size=(N, K)).astype(np.int8)
+        w = formats.tl1_pack(tern)
+        x = rng.standard_normal(K).astype(np.float32)
+        if tag == "c":
+            x[5] = 0.0
+            x *= np.float32(1e-7)  # below the 1e-6 absmax floor
+        w_scale = synth.latent_scale(rng)
+        y = np.empty(N, np.float32)
+        R.ref_tl1_gemv(P(x), P(w), K, N, w_scale, P(y))
+        acc = np.empty(N, np.int32)
+        inv = R.ref_tl1_gemv_acc(P(x), P(w), K, N, P(acc))
+        lut = np.empty(K // 2 * 32, np.int8)
+        inv2 = R.ref_build_lut(P(x), K, P(lut))
+        assert inv == inv2
+        out.update({f"{tag}_tern": tern, f"{tag}_w": w, f"{tag}_x": x,
+                    f"{tag}_w_scale": np.float32(w_scale), f"{tag}_y": y, f"{tag}_acc": acc,
+                    f"{tag}_inv": np.float32(inv), f"{tag}_lut": lut})
+    save("tl1_gemv", **out)
+
+
+def pack_raw_fixture():
+    R = oracle.ref()
+    rng = np.random.default_rng(102)
+    N, K = 128, 96
+    tern = rng.integers(-1, 2, size=(N, K)).astype(np.int8)
+    raw = formats.hf_pack_2bit(tern)
+    out = np.empty(N * K // 4, np.int8)
+    R.ref_pack_raw(P(raw), N, K, P(out))
+    save("tl1_pack_raw", tern=tern, raw=raw, N=np.int64(N), K=np.int64(K), packed=out.view(np.uint8))
+
+
+def rmsnorm_fixture():
+    R = oracle.ref()
+    rng = np.random.default_rng(103)
+    out = {}
+    for dim in (2560, 6912, 64):
+        x = (rng.standard_normal(dim) * 3).astype(np.float32)
+        w = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+        y = np.empty(dim, np.float32)
+        R.ref_rms_norm(P(x), P(w), P(y), dim, np.float32(1e-5))
+        y0 = np.empty(dim, np.float32)
+        R.ref_rms_norm(P(x), None, P(y0), dim, np.float32(1e-5))
+        out.update({f"x{dim}": x, f"w{dim}": w, f"y{dim}": y, f"ynow{dim}": y0})
+    save("rmsnorm", **out)
+
+
+def attention_fixture():
+    R = oracle.ref()
+    rng = np.random.default_rng(104)
+    out = {}
+    for tag, (Hq, Hkv, max_seq, pos) in {"a": (20, 5, 48, 37), "b": (4, 1, 8, 0),
+                                         "c": (8, 2, 300, 299)}.items():
+        D = 128
+        kc = np.zeros((Hkv, max_seq, D), np.int8)
+        vc = np.zeros_like(kc)
+        ks = np.zeros((Hkv, max_seq), np.float32)
+        vs = np.zeros_like(ks)
+        if pos:
+            c, s = synth.kv_quantize(rng.standard_normal((Hkv, pos, D)).astype(np.float32))
+            kc[:, :pos], ks[:, :pos] = c, synth.f16_round(s)
+            c, s = synth.kv_quantize(rng.standard_normal((Hkv, pos, D)).astype(np.float32))
+            vc[:, :pos], vs[:, :pos] = c, synth.f16_round(s)
+        q = rng.standard_normal(Hq * D).astype(np.float32)
+        k = rng.standard_normal(Hkv * D).astype(np.float32)
+        v = rng.standard_normal(Hkv * D).astype(np.float32)
+        ins = dict(q=q.copy(), k=k.copy(), v=v.copy(), kc=kc.copy(), vc=vc.copy(),
+                   ks=ks.copy(), vs=vs.copy())
+        o = np.empty(Hq * D, np.float32)
+        R.ref_attention_int8(Hq, Hkv, max_seq, pos, P(q), P(k), P(v), P(kc), P(vc), P(ks),
+                             P(vs), P(o))
+        for n, a in ins.items():
+            out[f"{tag}_in_{n}"] = a
+        out.update({f"{tag}_dims": np.array([Hq, Hkv, max_seq, pos], np.int64),
+                    f"{tag}_out": o, f"{tag}_q_rot": q, f"{tag}_k_rot": k, f"{tag}_kc": kc,
+                    f"{tag}_vc": vc, f"{tag}_ks": ks, f"{tag}_vs": vs})
+    save("attention", **out)
+
+
+def quant_gemv_fixture():
+    R = oracle.ref()
+    rng = np.random.default_rng(105)
+    K, N, G = 512, 64, 128
+    out = {"dims": np.array([K, N, G], np.int64)}
+    a = rng.standard_normal(K).astype(np.float16).astype(np.float32)
+    out["a"] = a
+    # Q4_0 / Q8_0
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    d = np.abs(rng.normal(0, 0.01, size=(N, K // 32))).astype(np.float16)
+    w4 = formats.q4_0_pack(q, d)
+    y = np.empty(N, np.float32)
+    R.ref_q4_0(P(a), P(w4), P(y), K, N)
+    out.update(q4_w=w4, q4_y=y.copy())
+    q8 = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    w8 = formats.q8_0_pack(q8, d)
+    R.ref_q8_0(P(a), P(w8), P(y), K, N)
+    out.update(q8_w=w8, q8_y=y.copy())
+    # GPTQ / AWQ
+    qk = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
+    zeros = rng.integers(0, 16, size=(K // G, N), dtype=np.uint8)
+    scales = synth.f16_round(np.abs(rng.normal(0, 0.01, size=(K // G, N))))
+    qw, qz = formats.gptq_pack(qk, zeros)
+    R.ref_gptq(P(a), P(qw), P(scales), P(qz), P(y), K, N, G)
+    out.update(gptq_qweight=qw, gptq_qzeros=qz, scales=scales, gptq_y=y.copy())
+    qw, qz = formats.awq_pack(qk, zeros)
+    R.ref_awq(P(a), P(qw), P(scales), P(qz), P(y), K, N, G)
+    out.update(awq_qweight=qw, awq_qzeros=qz, awq_y=y.copy())
+    save("quant_gemv", **out)
+
+
+def layer_struct(sm, l):
+    lw = sm.layers[l]
+    ptr = lambda a: ctypes.cast(a.ctypes.data, ctypes.c_void_p)  # noqa: E731
+
+    class W(ctypes.Structure):
+        _fields_ = [
+            ("q_w", ctypes.c_void_p), ("q_scale", ctypes.c_float),
+            ("k_w", ctypes.c_void_p), ("k_scale", ctypes.c_float),
+            ("v_w", ctypes.c_void_p), ("v_scale", ctypes.c_float),
+            ("out_w", ctypes.c_void_p), ("out_scale", ctypes.c_float),
+            ("gate_w", ctypes.c_void_p), ("gate_scale", ctypes.c_float),
+            ("up_w", ctypes.c_void_p), ("up_scale", ctypes.c_float),
+            ("down_w", ctypes.c_void_p), ("down_scale", ctypes.c_float),
+            ("in_norm", ctypes.c_void_p), ("attn_sub_norm", ctypes.c_void_p),
+            ("post_norm", ctypes.c_void_p), ("ffn_sub_norm", ctypes.c_void_p),
+        ]
+    w = W()
+    for p, f in zip(synth.PROJ, ["q", "k", "v", "out", "gate", "up", "down"]):
+        setattr(w, f + "_w", ptr(lw.tl1[p]))
+        setattr(w, f + "_scale", float(lw.scale[p]))
+    for f in ["in_norm", "attn_sub_norm", "post_norm", "ffn_sub_norm"]:
+        setattr(w, f, ptr(getattr(lw, f)))
+    return w
+
+
+def run_ref_engine(sm, tokens):
+    """Greedy steps of the compiled reference engine at theta 10000 (hard-coded there)."""
+    R = oracle.ref()
+    c = sm.cfg
+    e = R.ref_engine_create(c.hidden, c.n_q_heads, c.n_kv_heads, c.n_layers, c.ffn, c.vocab,
+                            c.max_seq)
+    keep = [layer_struct(sm, l) for l in range(c.n_layers)]
+    for l, w in enumerate(keep):
+        assert R.ref_engine_set_layer(e, l, ctypes.byref(w)) == 0
+    assert R.ref_engine_set_head(e, P(sm.embed), P(sm.embed_scales), P(sm.final_norm), c.vocab,
+                                 c.hidden) == 0
+    R.ref_engine_set_kv(e, P(sm.kc), P(sm.vc), P(sm.ks), P(sm.vs), sm.ctx)
+    logits, hidden, out_tok = [], [], []
+    for t in tokens:
+        lg = np.empty(c.vocab, np.float32)
+        tok = R.ref_engine_step(e, int(t), P(lg))
+        h = np.empty(c.hidden, np.float32)
+        R.ref_engine_hidden(e, P(h))
+        logits.append(lg)
+        hidden.append(h)
+        out_tok.append(tok)
+    kc, vc = np.empty_like(sm.kc), np.empty_like(sm.vc)
+    ks, vs = np.empty_like(sm.ks), np.empty_like(sm.vs)
+    R.ref_engine_get_kv(e, P(kc), P(vc), P(ks), P(vs))
+    R.ref_engine_destroy(e)
+    return np.array(out_tok), np.stack(logits), np.stack(hidden), (kc, vc, ks, vs)
+
+
+TINY = synth.DecodeConfig(hidden=256, n_q_heads=2, n_kv_heads=1, n_layers=2, ffn=512,
+                          vocab=512, max_seq=16, theta=10000.0)
+
+
+def decode_fixture():
+    sm = synth.make_model(TINY, seed=106, ctx=5)
+    tokens = np.array([7, 300, 42], np.int64)
+    out_tok, logits, hidden, (kc, vc, ks, vs) = run_ref_engine(sm, tokens)
+    arrays = {"tokens": tokens, "out_tokens": out_tok, "logits": logits, "hidden": hidden,
+              "kc_out": kc, "vc_out": vc, "ks_out": ks, "vs_out": vs,
+              "ctx": np.int64(sm.ctx), "kc": sm.kc, "vc": sm.vc, "ks": sm.ks, "vs": sm.vs,
+              "final_norm": sm.final_norm, "embed": sm.embed, "embed_scales": sm.embed_scales}
+    for l, lw in enumerate(sm.layers):
+        for p in synth.PROJ:
+            arrays[f"l{l}_{p}"] = lw.tl1[p]
+            arrays[f"l{l}_{p}_scale"] = np.float32(lw.scale[p])
+        for f in ["in_norm", "attn_sub_norm", "post_norm", "ffn_sub_norm"]:
+            arrays[f"l{l}_{f}"] = getattr(lw, f)
+    save("decode_tiny", **arrays)
+
+
+def load_tiny_model(z) -> synth.SynthModel:
+    """Rebuilds the decode fixture's model from its stored arrays."""
+    layers = []
+    for l in range(TINY.n_layers):
+        layers.append(synth.LayerWeights(
+            {p: z[f"l{l}_{p}"] for p in synth.PROJ},
+            {p: np.float32(z[f"l{l}_{p}_scale"]) for p in synth.PROJ},
+            z[f"l{l}_in_norm"], z[f"l{l}_attn_sub_norm"], z[f"l{l}_post_norm"],
+            z[f"l{l}_ffn_sub_norm"]))
+    return synth.SynthModel(TINY, layers, z["final_norm"], z["embed"], z["embed_scales"],
+                            z["kc"].copy(), z["vc"].copy(), z["ks"].copy(), z["vs"].copy(),
+                            int(z["ctx"]))
+
+
+if __name__ == "__main__":
+    oracle.build(ref=True)
+    tl1_fixture()
+    pack_raw_fixture()
+    rmsnorm_fixture()
+    attention_fixture()
+    quant_gemv_fixture()
+    decode_fixture()

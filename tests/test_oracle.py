@@ -1,0 +1,459 @@
+"""Pins the CPU oracle (oracle/tenzo_oracle.c) before anything is checked
+against it: golden vectors of the compiled reference (tests/golden/*.npz),
+the live compiled reference where it is built (marker ``ref``), and closed
+forms / brute force chosen so that a dropped term, a wrong sign or index, or a
+transposed operand fails.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tenzo_amd import formats, synth
+from tests.golden.make_golden import TINY, load_tiny_model, run_ref_engine
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def gold(name):
+    return np.load(os.path.join(GOLD, name + ".npz"))
+
+
+def round_half_away(x):
+    x = np.asarray(x, np.float64)
+    return np.sign(x) * np.floor(np.abs(x) + 0.5)
+
+
+# ---------------------------------------------------------------- fp16 -----
+
+def test_f16_conversions_match_ieee():
+    L = oracle.lib()
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = allh.view(np.float16).astype(np.float32)
+    got = np.array([L.orc_f16_to_f32(int(h)) for h in allh[::7]], np.float32)
+    np.testing.assert_array_equal(got.view(np.uint32)[~np.isnan(ref[::7])],
+                                  ref[::7].view(np.uint32)[~np.isnan(ref[::7])])
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([rng.standard_normal(3000) * 10.0 ** rng.integers(-8, 5, 3000),
+                         [6.1035156e-05, 5.9604645e-08, 65504.0, 65520.0, 2.9802322e-08]])
+    xs = xs.astype(np.float32)
+    got = np.array([L.orc_f32_to_f16(float(x)) for x in xs], np.uint16)
+    np.testing.assert_array_equal(got, xs.astype(np.float16).view(np.uint16))
+
+
+# ---------------------------------------------------------------- TL1 ------
+
+def test_tl1_pack_matches_golden_and_brute_force():
+    z = gold("tl1_gemv")
+    for tag in "abc":
+        tern, w = z[f"{tag}_tern"], z[f"{tag}_w"]
+        N, K = tern.shape
+        np.testing.assert_array_equal(oracle.tl1_pack(tern), w)
+        np.testing.assert_array_equal(formats.tl1_pack(tern), w)
+        np.testing.assert_array_equal(oracle.tl1_unpack(w, N, K), tern)
+        np.testing.assert_array_equal(formats.tl1_unpack(w, N, K), tern)
+    # brute force of the byte map on one hand-made block
+    tern = np.zeros((64, 4), np.int8)
+    tern[3, 2], tern[3, 3], tern[35, 2], tern[35, 3] = 1, -1, -1, 1
+    w = oracle.tl1_pack(tern).reshape(1, 2, 32)
+    # row 3 cols (2,3) = (+1,-1): idx (1+1)|(0<<2) = 2; row 35 = (-1,+1): 0|(2<<2) = 8
+    assert w[0, 1, 3] == (2 | (8 << 4))
+    assert w[0, 0, 3] == (1 | (1 << 2)) * 17  # zeros: idx 5 in both nibbles
+
+
+def test_tl1_pack_raw_matches_golden():
+    z = gold("tl1_pack_raw")
+    N, K = int(z["N"]), int(z["K"])
+    np.testing.assert_array_equal(oracle.tl1_pack_raw(z["raw"], N, K), z["packed"])
+    np.testing.assert_array_equal(oracle.tl1_pack(z["tern"]), z["packed"])
+    np.testing.assert_array_equal(formats.hf_pack_2bit(z["tern"]), z["raw"])
+
+
+def test_quant31_and_lut_match_golden():
+    z = gold("tl1_gemv")
+    for tag in "abc":
+        x = z[f"{tag}_x"]
+        codes, inv = oracle.quant31(x)
+        assert inv.view(np.uint32) == z[f"{tag}_inv"].view(np.uint32)
+        np.testing.assert_array_equal(oracle.build_lut(codes), z[f"{tag}_lut"])
+        # closed form: a_k = round(x_k * 31 / absmax), absmax floored at 1e-6
+        amax = max(np.float32(1e-6), np.abs(x).max())
+        np.testing.assert_array_equal(
+            codes, round_half_away(x * (np.float32(31) / amax)).astype(np.int8))
+        assert np.abs(codes).max() <= 31
+
+
+def test_lut_entries_closed_form():
+    codes = np.array([31, -31, 5, 0, -7, 12], np.int8)
+    lut = oracle.build_lut(codes).reshape(3, 32)
+    for k in range(3):
+        a0, a1 = int(codes[2 * k]), int(codes[2 * k + 1])
+        for w0 in (-1, 0, 1):
+            for w1 in (-1, 0, 1):
+                idx = (w0 + 1) | ((w1 + 1) << 2)
+                assert lut[k, idx] == w0 * a0 + w1 * a1 == lut[k, idx + 16]
+
+
+@pytest.mark.parametrize("N,K", [(64, 2), (64, 64), (128, 258), (64, 6912)])
+def test_tl1_gemv_i32_equals_dense_dot(N, K):
+    rng = np.random.default_rng(N + K)
+    tern = rng.integers(-1, 2, size=(N, K)).astype(np.int8)
+    codes = rng.integers(-31, 32, size=K).astype(np.int8)
+    acc = oracle.tl1_gemv_i32(oracle.tl1_pack(tern), codes, N, K)
+    np.testing.assert_array_equal(acc, tern.astype(np.int64) @ codes.astype(np.int64))
+
+
+def test_tl1_gemv_matches_golden_bit_exact():
+    z = gold("tl1_gemv")
+    for tag in "abc":
+        w, x = z[f"{tag}_w"], z[f"{tag}_x"]
+        N = z[f"{tag}_acc"].size
+        y, acc, inv = oracle.tl1_gemv(x, w, N, float(z[f"{tag}_w_scale"]))
+        np.testing.assert_array_equal(acc, z[f"{tag}_acc"])
+        np.testing.assert_array_equal(y.view(np.uint32), z[f"{tag}_y"].view(np.uint32))
+        # one fp32 multiply: y = float(acc) * (inv * w_scale)
+        tot = np.float32(inv * z[f"{tag}_w_scale"])
+        np.testing.assert_array_equal(y, acc.astype(np.float32) * tot)
+
+
+# ---------------------------------------------------------------- RMSNorm --
+
+def test_sumsq_order_is_the_documented_tree():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(6912).astype(np.float32)
+    p = np.zeros(256, np.float32)
+    for t in range(256):
+        s = np.float32(0)
+        for v in x[t::256]:
+            s = np.float32(np.float64(v) * np.float64(v) + np.float64(s))  # exact fma, rounded once
+        p[t] = s
+    while p.size > 1:
+        p = (p[0::2] + p[1::2]).astype(np.float32)
+    assert oracle.sumsq(x) == p[0]
+
+
+def test_rms_norm_matches_golden_and_fp64():
+    z = gold("rmsnorm")
+    for dim in (2560, 6912, 64):
+        x, w = z[f"x{dim}"], z[f"w{dim}"]
+        y = oracle.rms_norm(x, w)
+        np.testing.assert_allclose(y, z[f"y{dim}"], rtol=2e-6, atol=0)
+        np.testing.assert_allclose(oracle.rms_norm(x, None), z[f"ynow{dim}"], rtol=2e-6)
+        x64 = x.astype(np.float64)
+        exact = x64 / np.sqrt((x64 * x64).mean() + 1e-5) * w
+        np.testing.assert_allclose(y, exact, rtol=2e-6)
+
+
+# ---------------------------------------------------------------- KV / RoPE
+
+def test_kv_quant_special_cases():
+    codes, s = oracle.kv_quant(np.zeros(128, np.float32))
+    assert s == np.float32(1e-8) * np.float32(1.0 / 127.0) and not codes.any()
+    x = np.zeros(128, np.float32)
+    x[17] = -3.5
+    codes, s = oracle.kv_quant(x)
+    assert codes[17] == -127 and np.count_nonzero(codes) == 1
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal(128).astype(np.float32)
+    codes, s = oracle.kv_quant(x)
+    c2, s2 = synth.kv_quantize(x)
+    np.testing.assert_array_equal(codes, c2)
+    assert s == s2
+
+
+def test_rope_closed_form():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal(3 * 128).astype(np.float32)
+    for pos in (0, 1, 37, 4095):
+        cs = oracle.rope_table(10000.0, pos)
+        y = oracle.rope_apply(x, cs).reshape(3, 128).astype(np.float64)
+        i = np.arange(64)
+        ang = pos / 10000.0 ** (2 * i / 128)
+        xr = x.reshape(3, 128).astype(np.float64)
+        e0 = xr[:, :64] * np.cos(ang) - xr[:, 64:] * np.sin(ang)
+        e1 = xr[:, :64] * np.sin(ang) + xr[:, 64:] * np.cos(ang)
+        tol = 1e-6 + pos * 1.2e-7  # fp32 rounding of the angle grows with pos
+        np.testing.assert_allclose(y[:, :64], e0, atol=tol * 4)
+        np.testing.assert_allclose(y[:, 64:], e1, atol=tol * 4)
+        if pos == 0:
+            np.testing.assert_array_equal(y.astype(np.float32).reshape(-1), x)
+
+
+def attention_fp64(q, kc, vc, ks, vs, Hq, Hkv, seq_len):
+    D = 128
+    out = np.zeros((Hq, D))
+    for qh in range(Hq):
+        h = qh // (Hq // Hkv)
+        K = kc[h, :seq_len].astype(np.float64) * ks[h, :seq_len, None]
+        V = vc[h, :seq_len].astype(np.float64) * vs[h, :seq_len, None]
+        s = K @ q[qh * D:(qh + 1) * D].astype(np.float64) / np.sqrt(D)
+        p = np.exp(s - s.max())
+        out[qh] = (p / p.sum()) @ V
+    return out.reshape(-1)
+
+
+def test_attention_step_matches_golden():
+    z = gold("attention")
+    for tag in "abc":
+        Hq, Hkv, max_seq, pos = (int(v) for v in z[f"{tag}_dims"])
+        kc, vc = z[f"{tag}_in_kc"].copy(), z[f"{tag}_in_vc"].copy()
+        ks, vs = z[f"{tag}_in_ks"].copy(), z[f"{tag}_in_vs"].copy()
+        cs = oracle.rope_table(10000.0, pos)
+        out, q_rot, k_rot = oracle.attention_step(
+            z[f"{tag}_in_q"], z[f"{tag}_in_k"], z[f"{tag}_in_v"], kc, vc, ks, vs, Hq, Hkv,
+            max_seq, pos, cs, f16_scales=False)
+        np.testing.assert_array_equal(q_rot, z[f"{tag}_q_rot"])
+        np.testing.assert_array_equal(k_rot, z[f"{tag}_k_rot"])
+        np.testing.assert_allclose(out, z[f"{tag}_out"], rtol=1e-4, atol=1e-5)
+        # codes of the appended token are bit-exact end to end
+        np.testing.assert_array_equal(kc[:, pos], z[f"{tag}_kc"][:, pos])
+        np.testing.assert_array_equal(vc[:, pos], z[f"{tag}_vc"][:, pos])
+        # the appended token: codes from identical rotated k/v are bit-exact
+        ref_k = z[f"{tag}_k_rot"].reshape(Hkv, 128)
+        for h in range(Hkv):
+            c, s = oracle.kv_quant(ref_k[h])
+            np.testing.assert_array_equal(c, z[f"{tag}_kc"][h, pos])
+            assert s == z[f"{tag}_ks"][h, pos]
+            c, s = oracle.kv_quant(z[f"{tag}_in_v"].reshape(Hkv, 128)[h])
+            np.testing.assert_array_equal(c, z[f"{tag}_vc"][h, pos])
+            assert s == z[f"{tag}_vs"][h, pos]
+        # the earlier cache is untouched
+        np.testing.assert_array_equal(kc[:, :pos], z[f"{tag}_in_kc"][:, :pos])
+        # fp64 brute force over the dequantized cache
+        exact = attention_fp64(q_rot, kc, vc, ks, vs, Hq, Hkv, pos + 1)
+        np.testing.assert_allclose(out, exact, rtol=1e-4, atol=1e-5)
+
+
+def test_attention_single_token_is_dequantized_v():
+    rng = np.random.default_rng(13)
+    Hq, Hkv, max_seq = 8, 2, 4
+    kc = np.zeros((Hkv, max_seq, 128), np.int8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((Hkv, max_seq), np.float32)
+    vs = np.zeros_like(ks)
+    q = rng.standard_normal(Hq * 128).astype(np.float32)
+    k = rng.standard_normal(Hkv * 128).astype(np.float32)
+    v = rng.standard_normal(Hkv * 128).astype(np.float32)
+    out, _, _ = oracle.attention_step(q, k, v, kc, vc, ks, vs, Hq, Hkv, max_seq, 0,
+                                      oracle.rope_table(10000.0, 0))
+    for qh in range(Hq):
+        h = qh // 4
+        np.testing.assert_array_equal(out[qh * 128:(qh + 1) * 128],
+                                      vc[h, 0].astype(np.float32) * vs[h, 0])
+
+
+# ---------------------------------------------------------------- LM head --
+
+def test_lm_head_closed_form():
+    rng = np.random.default_rng(17)
+    V, H = 300, 512
+    E = rng.normal(0, 0.02, size=(V, H)).astype(np.float32)
+    W, s = synth.head_quantize(E)
+    x = rng.standard_normal(H).astype(np.float32)
+    logits, codes, s_x = oracle.lm_head(x, W, s)
+    amax = max(np.float32(1e-8), np.abs(x).max())
+    assert s_x == amax * np.float32(1.0 / 127.0)
+    np.testing.assert_array_equal(
+        codes, np.clip(round_half_away(x * (np.float32(127) / amax)), -128, 127).astype(np.int8))
+    acc = W.astype(np.int64) @ codes.astype(np.int64)
+    np.testing.assert_array_equal(logits, acc.astype(np.float32) * (s_x * s))
+    assert oracle.argmax(logits) == int(np.argmax(logits))
+    tie = np.array([1.0, 3.0, 3.0, 2.0], np.float32)
+    assert oracle.argmax(tie) == 1
+
+
+# ---------------------------------------------------------------- quant GEMV
+
+def dequant_q4_0(w, K, N):
+    blk = w.reshape(N, K // 32, 18)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+    qs = blk[:, :, 2:]
+    q = np.concatenate([qs & 15, qs >> 4], axis=2).astype(np.float64) - 8
+    return (q * d[:, :, None]).reshape(N, K)
+
+
+def test_quant_gemv_match_golden_and_fp64():
+    z = gold("quant_gemv")
+    K, N, G = (int(v) for v in z["dims"])
+    a = z["a"]
+    y = oracle.q4_0(a, z["q4_w"], K, N)
+    np.testing.assert_allclose(y, z["q4_y"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(y, dequant_q4_0(z["q4_w"], K, N) @ a, rtol=1e-4, atol=1e-5)
+    y = oracle.q8_0(a, z["q8_w"], K, N)
+    np.testing.assert_allclose(y, z["q8_y"], rtol=1e-5, atol=1e-6)
+    blk = z["q8_w"].reshape(N, K // 32, 34)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float64)[:, :, 0]
+    W8 = (blk[:, :, 2:].view(np.int8).astype(np.float64) * d[:, :, None]).reshape(N, K)
+    np.testing.assert_allclose(y, W8 @ a, rtol=1e-4, atol=1e-5)
+    scales = z["scales"]
+    for kind, fn in (("gptq", oracle.gptq), ("awq", oracle.awq)):
+        qw, qz = z[f"{kind}_qweight"], z[f"{kind}_qzeros"]
+        y = fn(a, qw, scales, qz, K, N, G)
+        np.testing.assert_allclose(y, z[f"{kind}_y"], rtol=1e-4, atol=1e-5)
+        # fp64 brute force with independently decoded codes/zeros
+        Wd = np.zeros((K, N))
+        for k in range(K):
+            g = k // G
+            for n in range(N):
+                if kind == "gptq":
+                    q = (int(qw[k // 8, n]) >> (4 * (k % 8))) & 15
+                    zz = ((int(qz[g // 8, n]) >> (4 * (g % 8))) & 15) + 1
+                else:
+                    e = formats.AWQ_ORDER.index(k % 8)
+                    q = (int(qw[k // 8, n]) >> (4 * e)) & 15
+                    zz = (int(qz[g, n // 8]) >> (4 * (n % 8))) & 15
+                Wd[k, n] = (q - zz) * scales[g, n]
+        np.testing.assert_allclose(y, a.astype(np.float64) @ Wd, rtol=1e-4, atol=1e-5)
+
+
+def test_q4_0_q8act_closed_form():
+    rng = np.random.default_rng(19)
+    K, N = 256, 32
+    q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
+    d = np.abs(rng.normal(0, 0.01, size=(N, K // 32))).astype(np.float16)
+    w = formats.q4_0_pack(q, d)
+    x = rng.standard_normal(K).astype(np.float32)
+    qa = oracle.quantize_q8_0(x)
+    np.testing.assert_array_equal(qa, formats.quantize_q8_0(x))
+    y = oracle.q4_0_q8act(qa, w, K, N)
+    ab = qa.reshape(K // 32, 34)
+    da = ab[:, :2].copy().view(np.float16).astype(np.float64)[:, 0]
+    a8 = ab[:, 2:].view(np.int8).astype(np.float64)
+    exact = np.zeros(N)
+    for b in range(K // 32):
+        exact += d[:, b].astype(np.float64) * da[b] * ((q[:, b * 32:(b + 1) * 32].astype(np.float64) - 8) @ a8[b])
+    np.testing.assert_allclose(y, exact, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- decode ---
+
+def test_decode_step_matches_golden():
+    z = gold("decode_tiny")
+    sm = load_tiny_model(z)
+    om = oracle.OracleModel(sm, f16_kv_scales=False)
+    for i, t in enumerate(z["tokens"]):
+        tok, logits, hidden = om.step(int(t), sm.ctx + i, TINY.theta)
+        np.testing.assert_allclose(hidden, z["hidden"][i], rtol=1e-3, atol=1e-3)
+        np.testing.assert_allclose(logits, z["logits"][i], rtol=1e-3, atol=1e-4)
+        assert tok == z["out_tokens"][i]
+    # appended KV codes: same codes except where a rounding tie flipped (reported)
+    n = sm.ctx + len(z["tokens"])
+    diff = om.kc[:, :, sm.ctx:n] != z["kc_out"][:, :, sm.ctx:n]
+    assert diff.mean() < 0.01
+    assert np.abs(om.kc[:, :, sm.ctx:n].astype(int) - z["kc_out"][:, :, sm.ctx:n]).max() <= 1
+
+
+@pytest.mark.ref
+def test_oracle_against_live_reference_random_shapes():
+    R = oracle.ref()
+    P = oracle._ptr
+    rng = np.random.default_rng(23)
+    for _ in range(5):
+        N = 64 * int(rng.integers(1, 5))
+        K = 2 * int(rng.integers(1, 700))
+        tern = rng.integers(-1, 2, size=(N, K)).astype(np.int8)
+        w = oracle.tl1_pack(tern)
+        x = (rng.standard_normal(K) * rng.uniform(0.01, 10)).astype(np.float32)
+        acc = np.empty(N, np.int32)
+        inv = R.ref_tl1_gemv_acc(P(x), P(w), K, N, P(acc))
+        y, acc2, inv2 = oracle.tl1_gemv(x, w, N, 0.0123)
+        np.testing.assert_array_equal(acc, acc2)
+        assert np.float32(inv) == inv2
+        yr = np.empty(N, np.float32)
+        R.ref_tl1_gemv(P(x), P(w), K, N, np.float32(0.0123), P(yr))
+        np.testing.assert_array_equal(y, yr)
+
+
+STAGES = ["x", "norm_x", "q", "k", "v", "attn_out", "attn_sub", "out", "h1", "post_norm",
+          "gate", "up", "act", "ffn_norm", "down"]
+
+
+@pytest.mark.ref
+def test_decode_stages_against_live_reference():
+    """Teacher-forced: every stage of forward_layer_raw is fed the reference's
+    own input for that stage and must reproduce the reference's output -
+    bit-exact for everything downstream of integer codes, 2e-6 for the norms
+    (summation order) and 1e-5 for attention (fp32 reduction order)."""
+    import ctypes
+    from tests.golden.make_golden import layer_struct
+    R = oracle.ref()
+    P = oracle._ptr
+    c = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=3, ffn=1024,
+                           vocab=1024, max_seq=32, theta=10000.0)
+    sm = synth.make_model(c, seed=31, ctx=9)
+    e = R.ref_engine_create(c.hidden, c.n_q_heads, c.n_kv_heads, c.n_layers, c.ffn, c.vocab,
+                            c.max_seq)
+    keep = [layer_struct(sm, l) for l in range(c.n_layers)]
+    for l, w in enumerate(keep):
+        R.ref_engine_set_layer(e, l, ctypes.byref(w))
+    R.ref_engine_set_head(e, P(sm.embed), P(sm.embed_scales), P(sm.final_norm), c.vocab, c.hidden)
+    R.ref_engine_set_kv(e, P(sm.kc), P(sm.vc), P(sm.ks), P(sm.vs), sm.ctx)
+
+    def buf(i):
+        out = np.empty(max(16384, c.vocab), np.float32)
+        R.ref_engine_buf(e, i, P(out))
+        return out
+
+    H, F, qd, kvd = c.hidden, c.ffn, c.q_dim, c.kv_dim
+    pos = sm.ctx
+    cs = oracle.rope_table(10000.0, pos)
+    kc, vc, ks, vs = sm.kc.copy(), sm.vc.copy(), sm.ks.copy(), sm.vs.copy()
+    R.ref_engine_embed(e, 3)
+    x0 = np.empty(H, np.float32)
+    oracle.lib().orc_embed_i8(P(sm.embed), P(sm.embed_scales), H, 3, P(x0))
+    np.testing.assert_array_equal(buf(0)[:H], x0)
+
+    def lin(name, lw, inp, N, K):
+        codes, inv = oracle.quant31(inp)
+        acc = oracle.tl1_gemv_i32(lw.tl1[name], codes, N, K)
+        return acc.astype(np.float32) * np.float32(inv * lw.scale[name])
+
+    for l in range(c.n_layers):
+        lw = sm.layers[l]
+        x = buf(0)[:H].copy()
+        R.ref_engine_layer(e, l)
+        r = {n: buf(i) for i, n in enumerate(STAGES)}
+        np.testing.assert_allclose(oracle.rms_norm(x, lw.in_norm), r["norm_x"][:H], rtol=2e-6)
+        q = lin("q", lw, r["norm_x"][:H], qd, H)
+        k = lin("k", lw, r["norm_x"][:H], kvd, H)
+        v = lin("v", lw, r["norm_x"][:H], kvd, H)
+        np.testing.assert_array_equal(v, r["v"][:kvd])
+        attn, q_rot, k_rot = oracle.attention_step(q, k, v, kc[l], vc[l], ks[l], vs[l],
+                                                   c.n_q_heads, c.n_kv_heads, c.max_seq, pos, cs)
+        np.testing.assert_array_equal(q_rot, r["q"][:qd])
+        np.testing.assert_array_equal(k_rot, r["k"][:kvd])
+        np.testing.assert_allclose(attn, r["attn_out"][:qd], rtol=1e-5, atol=1e-6)
+        np.testing.assert_allclose(oracle.rms_norm(r["attn_out"][:H], lw.attn_sub_norm),
+                                   r["attn_sub"][:H], rtol=2e-6)
+        np.testing.assert_array_equal(lin("o", lw, r["attn_sub"][:H], H, H), r["out"][:H])
+        np.testing.assert_array_equal((x + r["out"][:H]).astype(np.float32), r["h1"][:H])
+        np.testing.assert_allclose(oracle.rms_norm(r["h1"][:H], lw.post_norm), r["post_norm"][:H],
+                                   rtol=2e-6)
+        g = lin("gate", lw, r["post_norm"][:H], F, H)
+        u = lin("up", lw, r["post_norm"][:H], F, H)
+        np.testing.assert_array_equal(g, r["gate"][:F])
+        np.testing.assert_array_equal(u, r["up"][:F])
+        relu = np.maximum(g, np.float32(0))
+        np.testing.assert_array_equal(((relu * relu) * u).astype(np.float32), r["act"][:F])
+        np.testing.assert_allclose(oracle.rms_norm(r["act"][:F], lw.ffn_sub_norm),
+                                   r["ffn_norm"][:F], rtol=2e-6)
+        np.testing.assert_array_equal(lin("down", lw, r["ffn_norm"][:F], H, F), r["down"][:H])
+        np.testing.assert_array_equal((r["h1"][:H] + r["down"][:H]).astype(np.float32),
+                                      buf(0)[:H])
+    # appended KV codes and scales are bit-exact
+    rk, rv = np.empty_like(sm.kc), np.empty_like(sm.vc)
+    rks, rvs = np.empty_like(sm.ks), np.empty_like(sm.vs)
+    R.ref_engine_get_kv(e, P(rk), P(rv), P(rks), P(rvs))
+    np.testing.assert_array_equal(rk, kc)
+    np.testing.assert_array_equal(rv, vc)
+    np.testing.assert_array_equal(rks, ks)
+    np.testing.assert_array_equal(rvs, vs)
+    # LM head from the reference's final hidden state
+    xf = buf(0)[:H].copy()
+    R.ref_engine_finish(e)
+    logits_ref = buf(15)[:c.vocab]
+    xn = oracle.rms_norm(xf, sm.final_norm)
+    lg, _, _ = oracle.lm_head(xn, sm.embed, sm.embed_scales)
+    np.testing.assert_allclose(lg, logits_ref, rtol=1e-5, atol=1e-6)
+    R.ref_engine_destroy(e)
