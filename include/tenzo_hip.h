@@ -1,0 +1,202 @@
+/*
+ * tenzo_hip.h - C ABI of the MI355X (gfx950) decode hot path.
+ *
+ * Operator-level entry points: every pointer is DEVICE memory unless stated,
+ * sizes are element counts, `stream` is a hipStream_t passed as void*
+ * (NULL = the null stream). Calls are stream-ordered and asynchronous; no
+ * exception crosses the ABI. Return value: 0 on success or a negative
+ * tenzo_status_t (include/tenzo.h); tenzo_hip_last_error() gives the message.
+ * The caller owns every buffer it passes. Scratch memory (split-K partial
+ * sums, attention partials) is owned by the library, one region per device,
+ * grown on demand; calls that overlap on one device must be issued on one
+ * stream.
+ *
+ * Each entry point names the reference function it replaces (file:line into
+ * the reference checkout, src/runtime/ unless noted).
+ */
+#ifndef TENZO_HIP_H
+#define TENZO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define TENZO_HIP_API __attribute__((visibility("default")))
+#else
+#define TENZO_HIP_API
+#endif
+
+/* Per-token activation quantization parameters, device resident (8 bytes). */
+typedef struct {
+    float inv_scale; /* absmax/31 (TL1) or absmax/127 (LM head), as fp32 */
+    int32_t code_sum; /* sum of the int8 codes (TL1 kernels use it) */
+} tenzo_hip_actq_t;
+
+TENZO_HIP_API const char* tenzo_hip_version(void);
+TENZO_HIP_API const char* tenzo_hip_last_error(void);
+/* Number of visible HIP devices (0 when none). */
+TENZO_HIP_API int tenzo_hip_device_count(void);
+/* Frees the library-owned scratch of the current device. */
+TENZO_HIP_API int tenzo_hip_release_scratch(void);
+
+/* ---- TL1 ternary GEMV -------------------------------------------------- */
+
+/* Bytes of the device layout that tenzo_hip_tl1_repack writes for an N x K
+ * matrix: (N/64) * ceil(K/64) * 1024. */
+TENZO_HIP_API size_t tenzo_hip_tl1_packed_bytes(int64_t N, int64_t K);
+
+/* Repacks TL1 blocks [N/64][K/2][32] (the layout compute_single_block reads,
+ * TenzoEngine.cpp:64-127, written by PybindModule.cpp:315-355 and
+ * TenzoEngine.cpp:1842-1884) into the device GEMV layout. N % 64 == 0,
+ * K % 2 == 0. */
+TENZO_HIP_API int tenzo_hip_tl1_repack(const uint8_t* w_tl1, void* w_packed, int64_t N,
+                                       int64_t K, void* stream);
+
+/* Activation quantization of build_lut (TenzoEngine.cpp:22-62) for M tokens
+ * of K values: codes[m][k] = round(x * 31/absmax), written with a row stride
+ * of ceil(K/64)*64 (zero padded); q[m] = {absmax/31, sum of codes}. When
+ * norm_w is non-null or do_norm is set, x is first replaced by
+ * rms_norm_raw(x, norm_w, eps) (TenzoEngine.cpp:148-166) and, if y_out is
+ * non-null, the normalized values are written there. */
+TENZO_HIP_API int tenzo_hip_rmsnorm_quant31(const float* x, const float* norm_w, int do_norm,
+                                            float eps, int64_t M, int64_t K, int8_t* codes,
+                                            tenzo_hip_actq_t* q, float* y_out, void* stream);
+
+/* TL1 GEMV on quantized activations (compute_from_lut, TenzoEngine.cpp:129-146):
+ * acc[m][n] = sum_k W[n][k] * codes[m][k] (exact int32),
+ * y[m][n] = float(acc) * (q[m].inv_scale * w_scale). acc_out may be null. */
+TENZO_HIP_API int tenzo_hip_bitlinear_tl1(const int8_t* codes, const tenzo_hip_actq_t* q,
+                                          const void* w_packed, float w_scale, int64_t M,
+                                          int64_t N, int64_t K, float* y, int32_t* acc_out,
+                                          void* stream);
+
+/* executeBitLinearTL1(act, w, out, M, K, N, scale) (ROCmRuntime.h:20-28) on
+ * device pointers: quantize each of the M activation rows then run the TL1
+ * GEMV over the packed weights. */
+TENZO_HIP_API int tenzo_hip_bitlinear_tl1_f32(const float* x, const void* w_packed,
+                                              float w_scale, int64_t M, int64_t N, int64_t K,
+                                              float* y, void* stream);
+
+/* executeRMSNorm(in, w, out, dim, eps) (ROCmRuntime.h:31-37) on device pointers. */
+TENZO_HIP_API int tenzo_hip_rmsnorm(const float* x, const float* w, float* y, int64_t dim,
+                                    float eps, void* stream);
+
+/* ---- INT8 KV-cache decode attention ------------------------------------ */
+
+/* One decode step of FusedKVCache::forward_attention_raw (TenzoEngine.cpp:447-919,
+ * int8_fused mode) for B sequences at the same position pos:
+ *   q [B][Hq][128], k_new / v_new [B][Hkv][128] fp32;
+ *   cache codes kc / vc [B][Hkv][max_seq][128] int8,
+ *   scales ks / vs [B][Hkv][max_seq] fp16 (fp32 in the reference);
+ *   rope_cs: cos[64] then sin[64] for position pos (tenzo_hip_rope_table);
+ * RoPE is applied to q and k_new, k_new/v_new are quantized and appended at
+ * pos, and out [B][Hq][128] receives attention over positions 0..pos.
+ * q_rot / k_rot, when non-null, receive the rotated q / k (they must not
+ * alias q / k_new). GQA: query head h reads kv head h / (Hq/Hkv). */
+TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
+                                             const float* v_new, int8_t* kc, int8_t* vc,
+                                             uint16_t* ks, uint16_t* vs, const float* rope_cs,
+                                             int B, int Hq, int Hkv, int max_seq, int pos,
+                                             float* out, float* q_rot, float* k_rot,
+                                             void* stream);
+
+/* HOST function: fills cs[pos - pos0][0..127] = cos/sin table rows for
+ * positions pos0 .. pos0+n_pos-1 with the reference's RoPE angles
+ * (TenzoEngine.cpp:465-469; theta is 10000 there and a parameter here). */
+TENZO_HIP_API void tenzo_hip_rope_table(float theta, int head_dim, int pos0, int n_pos,
+                                        float* cs_host);
+
+/* ---- Quantized GEMVs (TenzoEngine.cpp:1022-1175) ------------------------ */
+
+/* act_dtype / scale_dtype: 0 = fp32, 1 = fp16. B activation rows
+ * ([B][K]), outputs [B][N] fp32. */
+
+/* compute_linear_gguf_q4_0 (:1022-1075): w [N][K/32] blocks of 18 bytes. */
+TENZO_HIP_API int tenzo_hip_gemv_q4_0(const void* act, int act_dtype, const uint8_t* w,
+                                      float* y, int K, int N, int B, void* stream);
+/* Q4_0 weights x Q8_0 activations (no reference counterpart: the reference
+ * has only fp32 activations for Q4_0): qa = B rows of K/32 blocks of 34 bytes. */
+TENZO_HIP_API int tenzo_hip_gemv_q4_0_q8_0(const uint8_t* qa, const uint8_t* w, float* y,
+                                           int K, int N, int B, void* stream);
+/* compute_linear_gptq (:1117-1143): qweight [K/8][N] u32, scales [K/g][N],
+ * qzeros [ceil(K/g/8)][N] u32 (nibble g%8, zero = nibble + 1). */
+TENZO_HIP_API int tenzo_hip_gemv_gptq(const void* act, int act_dtype, const uint32_t* qweight,
+                                      const void* scales, int scale_dtype,
+                                      const uint32_t* qzeros, float* y, int K, int N,
+                                      int group, int B, void* stream);
+/* compute_linear_awq (:1146-1175): qweight [K/8][N] (nibble e holds element
+ * k + {0,2,4,6,1,3,5,7}[e]), scales [K/g][N], qzeros [K/g][N/8]. */
+TENZO_HIP_API int tenzo_hip_gemv_awq(const void* act, int act_dtype, const uint32_t* qweight,
+                                     const void* scales, int scale_dtype,
+                                     const uint32_t* qzeros, float* y, int K, int N, int group,
+                                     int B, void* stream);
+
+/* ---- int8 LM head, embedding, greedy sampling -------------------------- */
+
+/* Bytes of the device layout tenzo_hip_i8_rows_repack writes for V x H:
+ * ceil(V/64) * (H/16) * 1024. */
+TENZO_HIP_API size_t tenzo_hip_i8_packed_bytes(int64_t V, int64_t H);
+/* Row-major int8 [V][H] (H % 16 == 0) -> device LM-head layout. */
+TENZO_HIP_API int tenzo_hip_i8_rows_repack(const int8_t* w, void* w_packed, int64_t V,
+                                           int64_t H, void* stream);
+/* compute_logits (TenzoEngine.cpp:1634-1720): final rms_norm_raw(x, norm_w),
+ * int8 activation quantization (absmax/127), logits[v] =
+ * float(sum x_i8 * W[v]) * (s_x * scales[v]). */
+TENZO_HIP_API int tenzo_hip_lm_head_i8(const float* x, const float* norm_w, float eps,
+                                       const void* w_packed, const float* scales,
+                                       float* logits, int64_t V, int64_t H, void* stream);
+/* Greedy branch of sample_top_k_top_p (TenzoEngine.cpp:1745-1755): index of
+ * the first maximum, written to *out_idx (device int32). */
+TENZO_HIP_API int tenzo_hip_argmax(const float* logits, int64_t V, int32_t* out_idx,
+                                   void* stream);
+/* embedding_lookup, int8 branch (TenzoEngine.cpp:1294-1316), reading the
+ * table in the LM-head device layout: x = float(E[token]) * scales[token].
+ * token is read from device memory (token_dev). */
+TENZO_HIP_API int tenzo_hip_embed_i8(const void* w_packed, const float* scales,
+                                     const int32_t* token_dev, int64_t V, int64_t H, float* x,
+                                     void* stream);
+
+/* ---- host-pointer shims of the reference ROCm operator surface ----------
+ * Synchronous, host memory in and out, return 1 on success and 0 on failure,
+ * like ROCmRuntime::execute* (ROCmRuntime.h:20-37). Packed weights are cached
+ * on the device keyed by the host pointer (the caller keeps them unchanged). */
+TENZO_HIP_API int tenzo_hip_execute_bitlinear_tl1(const float* act, const uint8_t* w,
+                                                  float* out, size_t M, size_t K, size_t N,
+                                                  float scale);
+TENZO_HIP_API int tenzo_hip_execute_rmsnorm(const float* in, const float* w, float* out,
+                                            size_t dim, float eps);
+
+/* ---- engine extensions (the engine itself is include/tenzo.h) ----------- */
+struct tenzo_engine_opaque;
+/* Copies a prefilled INT8 KV cache (codes [L][Hkv][seq_len][128], fp16 scales
+ * [L][Hkv][seq_len]) into the engine and sets its sequence length; pointers
+ * are device memory when is_device, else host. Mirrors writing the public
+ * FusedKVCache state (TenzoEngine.h:60-115). */
+TENZO_HIP_API int tenzo_hip_engine_set_kv(struct tenzo_engine_opaque* e, const int8_t* kc,
+                                          const int8_t* vc, const uint16_t* ks,
+                                          const uint16_t* vs, int seq_len, int is_device);
+/* Reads back the cache (same layout, seq_len positions). */
+TENZO_HIP_API int tenzo_hip_engine_get_kv(struct tenzo_engine_opaque* e, int8_t* kc,
+                                          int8_t* vc, uint16_t* ks, uint16_t* vs, int seq_len);
+/* RoPE theta (the reference hard-codes 10000; BitNet-2B uses 500000). */
+TENZO_HIP_API int tenzo_hip_engine_set_rope_theta(struct tenzo_engine_opaque* e, float theta);
+/* Copies the last step's logits (vocab fp32) to host memory. */
+TENZO_HIP_API int tenzo_hip_engine_get_logits(struct tenzo_engine_opaque* e, float* logits);
+/* Copies an engine buffer to host memory, by name: "x", "q", "k", "v",
+ * "attn_out", "h1", "gate", "up", "act", "down" (last layer of the last step). */
+TENZO_HIP_API int tenzo_hip_engine_get_buffer(struct tenzo_engine_opaque* e, const char* name,
+                                              float* out, int64_t n);
+/* Runs the decode step through a captured HIP graph (1, default) or eager
+ * launches (0). */
+TENZO_HIP_API int tenzo_hip_engine_use_graph(struct tenzo_engine_opaque* e, int on);
+/* The engine's HIP stream (hipStream_t as void*). */
+TENZO_HIP_API void* tenzo_hip_engine_stream(struct tenzo_engine_opaque* e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TENZO_HIP_H */

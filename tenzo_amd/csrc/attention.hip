@@ -1,0 +1,416 @@
+// INT8 KV-cache decode attention on gfx950 (FusedKVCache::forward_attention_raw,
+// reference src/runtime/TenzoEngine.cpp:447-919, int8_fused branches).
+//
+// One workgroup per (context chunk, kv head, sequence). It holds the G query
+// heads that share the kv head (GQA), so each K/V byte is read from HBM once
+// for all of them. Within a chunk: RoPE on q (and, for the chunk that holds
+// the new token, on k), quantize-append of the new k/v, then
+//   scores   s[g][t] = (q_g . k_t) * (s_k[t] / sqrt(128))
+//   weights  p[g][t] = exp(s[g][t] - m_chunk[g]),  l[g] = sum_t p[g][t]
+//   values   o[g][d] = sum_t p[g][t] * s_v[t] * v_t[d]
+// and the chunk partials (m, l, o) are merged by a combine kernel
+// (out = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c).
+//
+// Lane mapping (both passes): a wave takes 8 tokens at a time; lane l reads
+// 16 bytes = dims (l%8)*16 .. +15 of token l/8, so one wave load is 1 KiB of
+// contiguous cache rows.
+#include "attention.h"
+#include "common.h"
+
+namespace tz {
+
+constexpr int kD = 128;
+constexpr float kScaleFactor = 0.08838834764831845f;  // 1/sqrt(128)
+
+struct AttnArgs {
+    const float* q;      // [B][Hq][128]
+    const float* k_new;  // [B][Hkv][128]
+    const float* v_new;
+    int8_t* kc;          // [B][Hkv][max_seq][128] (batch stride given below)
+    int8_t* vc;
+    uint16_t* ks;        // [B][Hkv][max_seq]
+    uint16_t* vs;
+    const float* rope;   // cos[64] | sin[64], per position when rope_indexed
+    const int* pos_dev;  // position read from device memory when non-null
+    int pos;
+    int rope_indexed;
+    int Hq, Hkv, max_seq, T;
+    int64_t cache_batch_stride;  // elements between sequences' caches
+    float* out;          // [B][Hq][128] (used when nchunks == 1)
+    float* part;         // [B][Hq][max_chunks][130] partials
+    int max_chunks;
+    float* q_rot;        // optional
+    float* k_rot;        // optional
+};
+
+__device__ __forceinline__ void unpack16(const uint4 v, float* f) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) f[4 * i + j] = (float)(int8_t)((w[i] >> (8 * j)) & 0xff);
+    }
+}
+
+// KV append quantization (:516-531 as built): s = amax*(1/127), code =
+// clamp(round(x * (127/amax)), -128, 127). 64 lanes x 2 values.
+__device__ __forceinline__ void quant_kv_pair(float x0, float x1, int8_t* codes_out,
+                                              int lane, float* s_out) {
+    float amax = fmaxf(fabsf(x0), fabsf(x1));
+    amax = fmaxf(wave_max(amax), 1e-8f);
+    const float inv = __fdiv_rn(127.0f, amax);
+    float r0 = roundf(__fmul_rn(x0, inv));
+    float r1 = roundf(__fmul_rn(x1, inv));
+    r0 = fminf(fmaxf(r0, -128.0f), 127.0f);
+    r1 = fminf(fmaxf(r1, -128.0f), 127.0f);
+    codes_out[lane] = (int8_t)r0;
+    codes_out[lane + 64] = (int8_t)r1;
+    *s_out = __fmul_rn(amax, 1.0f / 127.0f);
+}
+
+template <int G>
+__global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
+    __shared__ float qs[G][kD];
+    __shared__ float sc[G][kMaxChunk];
+    __shared__ float ow[4][G][kD];
+    __shared__ float mstat[G], lstat[G];
+    __shared__ __align__(16) int8_t newk[kD];
+    __shared__ __align__(16) int8_t newv[kD];
+    __shared__ float news[2];
+
+    const int c = blockIdx.x;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+    const int seq_len = pos + 1;
+    const int t0 = c * a.T;
+    if (t0 >= seq_len) return;  // chunks past the context (fixed-size graph grids)
+    const int t1 = min(t0 + a.T, seq_len);
+    const int nt = t1 - t0;
+    const int nchunks = (seq_len + a.T - 1) / a.T;
+    const float* rope = a.rope + (a.rope_indexed ? (int64_t)pos * kD : 0);
+
+    // ---- RoPE on the G query heads (:460-481) ----
+    for (int i = tid; i < G * 64; i += 256) {
+        const int g = i >> 6, j = i & 63;
+        const int qh = h * G + g;
+        const float* qv = a.q + ((int64_t)b * a.Hq + qh) * kD;
+        const float x0 = qv[j], x1 = qv[j + 64];
+        const float cs = rope[j], sn = rope[64 + j];
+        const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+        const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+        qs[g][j] = r0;
+        qs[g][j + 64] = r1;
+        if (a.q_rot && c == 0) {
+            float* qr = a.q_rot + ((int64_t)b * a.Hq + qh) * kD;
+            qr[j] = r0;
+            qr[j + 64] = r1;
+        }
+    }
+    // ---- new token: RoPE on k, quantize-append k and v (:482-533) ----
+    const bool has_new = pos >= t0 && pos < t1;
+    const int64_t cache_head = (int64_t)b * a.cache_batch_stride + (int64_t)h * a.max_seq;
+    if (has_new && wave < 2) {
+        const float* src = (wave == 0 ? a.k_new : a.v_new) + ((int64_t)b * a.Hkv + h) * kD;
+        float x0 = src[lane], x1 = src[lane + 64];
+        if (wave == 0) {
+            const float cs = rope[lane], sn = rope[64 + lane];
+            const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+            const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+            x0 = r0;
+            x1 = r1;
+            if (a.k_rot) {
+                float* kr = a.k_rot + ((int64_t)b * a.Hkv + h) * kD;
+                kr[lane] = r0;
+                kr[lane + 64] = r1;
+            }
+        }
+        float s;
+        quant_kv_pair(x0, x1, wave == 0 ? newk : newv, lane, &s);
+        const uint16_t sh = float_to_half_bits(s);
+        int8_t* dst = (wave == 0 ? a.kc : a.vc) + (cache_head + pos) * kD;
+        dst[lane] = (wave == 0 ? newk : newv)[lane];
+        dst[lane + 64] = (wave == 0 ? newk : newv)[lane + 64];
+        if (lane == 0) {
+            (wave == 0 ? a.ks : a.vs)[cache_head + pos] = sh;
+            news[wave] = half_bits_to_float(sh);
+        }
+    }
+    __syncthreads();
+
+    const int sub = lane >> 3;       // token within the wave's group of 8
+    const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
+    const int8_t* kbase = a.kc + cache_head * kD;
+    const int8_t* vbase = a.vc + cache_head * kD;
+    const uint16_t* ksb = a.ks + cache_head;
+    const uint16_t* vsb = a.vs + cache_head;
+
+    // ---- scores (:678-694) ----
+    {
+        float qr[G][16];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) qr[g][j] = qs[g][d0 + j];
+        for (int tb = wave * 8; tb < nt; tb += 32) {
+            const int tl = tb + sub;
+            const int t = t0 + tl;
+            float kf[16];
+            float skf = 0.0f;
+            if (tl < nt) {
+                uint4 kv;
+                if (t == pos) {
+                    kv = *reinterpret_cast<const uint4*>(newk + d0);
+                    skf = news[0];
+                } else {
+                    kv = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
+                    skf = half_bits_to_float(ksb[t]);
+                }
+                unpack16(kv, kf);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) kf[j] = 0.0f;
+            }
+            float p[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
+                s += __shfl_xor(s, 1, 64);
+                s += __shfl_xor(s, 2, 64);
+                s += __shfl_xor(s, 4, 64);
+                p[g] = s;
+            }
+            if (tl < nt) {
+                const float f = __fmul_rn(skf, kScaleFactor);
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    if ((lane & 7) == (g & 7)) sc[g][tl] = __fmul_rn(p[g], f);
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- chunk softmax statistics (:824-830) ----
+    for (int g = wave; g < G; g += 4) {
+        float m = -1e30f;
+        for (int i = lane; i < nt; i += 64) m = fmaxf(m, sc[g][i]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int i = lane; i < nt; i += 64) {
+            const float e = expf(sc[g][i] - m);
+            sc[g][i] = e;
+            l += e;
+        }
+        l = wave_sum_tree(l);
+        if (lane == 0) {
+            mstat[g] = m;
+            lstat[g] = l;
+        }
+    }
+    __syncthreads();
+
+    // ---- weighted values (:842-851) ----
+    float acc[G][16];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+    for (int tb = wave * 8; tb < nt; tb += 32) {
+        const int tl = tb + sub;
+        const int t = t0 + tl;
+        if (tl < nt) {
+            uint4 vv;
+            float svf;
+            if (t == pos) {
+                vv = *reinterpret_cast<const uint4*>(newv + d0);
+                svf = news[1];
+            } else {
+                vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
+                svf = half_bits_to_float(vsb[t]);
+            }
+            float vf[16];
+            unpack16(vv, vf);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float wgt = __fmul_rn(sc[g][tl], svf);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
+            }
+        }
+    }
+    // reduce over the 8 token lanes that share dims (lane bits 3..5)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float v = acc[g][j];
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            acc[g][j] = v;
+        }
+    if (lane < 8) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
+    }
+    __syncthreads();
+    for (int i = tid; i < G * kD; i += 256) {
+        const int g = i >> 7, d = i & 127;
+        const float o = (ow[0][g][d] + ow[1][g][d]) + (ow[2][g][d] + ow[3][g][d]);
+        const int qh = h * G + g;
+        if (nchunks == 1) {
+            a.out[((int64_t)b * a.Hq + qh) * kD + d] = __fdiv_rn(o, lstat[g]);
+        } else {
+            float* pp = a.part + (((int64_t)b * a.Hq + qh) * a.max_chunks + c) * kPartStride;
+            pp[2 + d] = o;
+            if (d == 0) {
+                pp[0] = mstat[g];
+                pp[1] = lstat[g];
+            }
+        }
+    }
+}
+
+// Merge of the chunk partials; one 128-thread block per (query head, sequence).
+__global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
+    const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
+    const int nchunks = (pos + 1 + a.T - 1) / a.T;
+    if (nchunks == 1) return;  // the chunk kernel wrote the output
+    const float* pp = a.part + ((int64_t)b * a.Hq + qh) * a.max_chunks * kPartStride;
+    float M = -1e30f;
+    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, pp[c * kPartStride]);
+    float L = 0.0f, o = 0.0f;
+    for (int c = 0; c < nchunks; ++c) {
+        const float e = expf(pp[c * kPartStride] - M);
+        L = __builtin_fmaf(e, pp[c * kPartStride + 1], L);
+        o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
+    }
+    a.out[((int64_t)b * a.Hq + qh) * kD + d] = __fdiv_rn(o, L);
+}
+
+int attn_pick_chunk(int seq_len, int Hkv, int B) {
+    // ~512 workgroups over the chip, chunks of 32..kMaxChunk tokens.
+    const int64_t target = ceil_div(512, (int64_t)Hkv * B);
+    int64_t T = ceil_div(seq_len, target);
+    T = ceil_div(T, 32) * 32;
+    if (T < 32) T = 32;
+    if (T > kMaxChunk) T = kMaxChunk;
+    return (int)T;
+}
+
+int launch_attn(const AttnLaunch& L, hipStream_t st) {
+    const int G = L.Hq / L.Hkv;
+    AttnArgs a{};
+    a.q = L.q;
+    a.k_new = L.k_new;
+    a.v_new = L.v_new;
+    a.kc = L.kc;
+    a.vc = L.vc;
+    a.ks = L.ks;
+    a.vs = L.vs;
+    a.rope = L.rope;
+    a.pos_dev = L.pos_dev;
+    a.pos = L.pos;
+    a.rope_indexed = L.rope_indexed;
+    a.Hq = L.Hq;
+    a.Hkv = L.Hkv;
+    a.max_seq = L.max_seq;
+    a.T = L.T;
+    a.cache_batch_stride = (int64_t)L.Hkv * L.max_seq;
+    a.out = L.out;
+    a.max_chunks = L.max_chunks;
+    a.q_rot = L.q_rot;
+    a.k_rot = L.k_rot;
+    const size_t part_bytes = (size_t)L.B * L.Hq * L.max_chunks * kPartStride * 4;
+    if (L.max_chunks > 1) {
+        a.part = L.part ? L.part : (float*)Scratch::get(kScratchAttn, part_bytes, st);
+        if (!a.part) return TENZO_ERROR_OUT_OF_MEMORY;
+    }
+    dim3 grid(L.max_chunks, L.Hkv, L.B);
+    switch (G) {
+        case 1: hipLaunchKernelGGL(attn_int8_chunk_kernel<1>, grid, dim3(256), 0, st, a); break;
+        case 2: hipLaunchKernelGGL(attn_int8_chunk_kernel<2>, grid, dim3(256), 0, st, a); break;
+        case 4: hipLaunchKernelGGL(attn_int8_chunk_kernel<4>, grid, dim3(256), 0, st, a); break;
+        case 8: hipLaunchKernelGGL(attn_int8_chunk_kernel<8>, grid, dim3(256), 0, st, a); break;
+        default:
+            set_error("attention: query heads per kv head must be 1, 2, 4 or 8 (got %d)", G);
+            return TENZO_ERROR_UNSUPPORTED;
+    }
+    int rc = launch_status("attn_int8_chunk_kernel");
+    if (rc) return rc;
+    if (L.max_chunks > 1) {
+        hipLaunchKernelGGL(attn_combine_kernel, dim3(L.Hq, L.B), dim3(128), 0, st, a);
+        rc = launch_status("attn_combine_kernel");
+    }
+    return rc;
+}
+
+}  // namespace tz
+
+using namespace tz;
+
+extern "C" {
+
+TENZO_HIP_API void tenzo_hip_rope_table(float theta, int head_dim, int pos0, int n_pos,
+                                        float* cs) {
+    // The reference evaluates freq = 1/powf(theta, 2i/d) under -ffast-math as
+    // expf(-(2i/d) * logf(theta)) and takes glibc cosf/sinf of the fp32 angle
+    // pos * freq (TenzoEngine.cpp:465-469 as built).
+    const int half = head_dim / 2;
+    const float ln_theta = logf(theta);
+    for (int p = 0; p < n_pos; ++p) {
+        float* row = cs + (int64_t)p * head_dim;
+        for (int i = 0; i < half; ++i) {
+            const float e = (float)(2 * i) / (float)head_dim;
+            const float freq = expf(-e * ln_theta);
+            const float angle = (float)(pos0 + p) * freq;
+            row[i] = cosf(angle);
+            row[half + i] = sinf(angle);
+        }
+    }
+}
+
+TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
+                                             const float* v_new, int8_t* kc, int8_t* vc,
+                                             uint16_t* ks, uint16_t* vs, const float* rope_cs,
+                                             int B, int Hq, int Hkv, int max_seq, int pos,
+                                             float* out, float* q_rot, float* k_rot,
+                                             void* stream) {
+    TZ_CHECK(q && k_new && v_new && kc && vc && ks && vs && rope_cs && out,
+             "attn_int8_decode: null pointer");
+    TZ_CHECK(B > 0 && B <= 65535 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0,
+             "attn_int8_decode: bad head counts (Hq=%d Hkv=%d)", Hq, Hkv);
+    TZ_CHECK(pos >= 0 && pos < max_seq, "attn_int8_decode: pos %d outside [0, %d)", pos,
+             max_seq);
+    TZ_CHECK(q_rot != q && k_rot != k_new, "attn_int8_decode: q_rot/k_rot must not alias q/k");
+    AttnLaunch L{};
+    L.q = q;
+    L.k_new = k_new;
+    L.v_new = v_new;
+    L.kc = kc;
+    L.vc = vc;
+    L.ks = ks;
+    L.vs = vs;
+    L.rope = rope_cs;
+    L.pos = pos;
+    L.B = B;
+    L.Hq = Hq;
+    L.Hkv = Hkv;
+    L.max_seq = max_seq;
+    L.T = attn_pick_chunk(pos + 1, Hkv, B);
+    L.max_chunks = (int)ceil_div(pos + 1, L.T);
+    L.out = out;
+    L.q_rot = q_rot;
+    L.k_rot = k_rot;
+    return launch_attn(L, (hipStream_t)stream);
+}
+
+}  // extern "C"

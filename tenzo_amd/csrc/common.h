@@ -1,0 +1,150 @@
+// Shared device helpers and host plumbing for libtenzo_hip.so (gfx950).
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/tenzo.h"
+#include "../../include/tenzo_hip.h"
+
+namespace tz {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- host ----
+
+// Thread-local error message behind tenzo_hip_last_error().
+void set_error(const char* fmt, ...);
+// Maps a HIP error to a status (and records the message).
+int hip_fail(hipError_t e, const char* what);
+
+#define TZ_HIP(call)                                            \
+    do {                                                        \
+        hipError_t e_ = (call);                                 \
+        if (e_ != hipSuccess) return ::tz::hip_fail(e_, #call); \
+    } while (0)
+
+#define TZ_CHECK(cond, ...)                       \
+    do {                                          \
+        if (!(cond)) {                            \
+            ::tz::set_error(__VA_ARGS__);         \
+            return TENZO_ERROR_INVALID_ARGUMENT;  \
+        }                                         \
+    } while (0)
+
+// Checks the launch that was just issued.
+int launch_status(const char* what);
+
+// Library-owned scratch, one region per device, grown on demand. Regions are
+// zero-filled when (re)allocated; users that need zero-initialised memory
+// restore zeros before they return (the split-K accumulators do).
+struct Scratch {
+    // Returns a device pointer of at least `bytes` for slot `slot` on the
+    // current device, or nullptr (error recorded).
+    static void* get(int slot, size_t bytes, hipStream_t stream);
+};
+enum ScratchSlot {
+    kScratchGemvAcc = 0,   // int32 split-K accumulators + counters
+    kScratchAttn = 1,      // attention partials
+    kScratchAct = 2,       // quantized activations of the *_f32 entry points
+    kScratchTmp = 3,
+    kScratchSlots = 4
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// --------------------------------------------------------------- device ---
+
+// Sum over a wave with a butterfly in increasing lane distance: lane pairs
+// (0,1), (2,3), ... are added first, so the result is the balanced pairwise
+// tree over the 64 lanes in lane order, identical in every lane.
+__device__ __forceinline__ float wave_sum_tree(float v) {
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+// Sum of squares of x[0..n) in the fixed order shared with the CPU oracle
+// (orc_sumsq): thread t of 256 fma-accumulates x[t], x[t+256], ...; then a
+// balanced pairwise tree over the 256 partials in thread order. Must be
+// called by all threads of a 256-thread block; `red` is 4 floats of LDS.
+__device__ __forceinline__ float block256_sumsq(const float* __restrict__ x, int64_t n,
+                                                float* red) {
+    const int t = threadIdx.x;
+    float s = 0.0f;
+    for (int64_t i = t; i < n; i += 256) s = __builtin_fmaf(x[i], x[i], s);
+    s = wave_sum_tree(s);
+    if ((t & 63) == 0) red[t >> 6] = s;
+    __syncthreads();
+    float r = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return r;
+}
+
+// Block-wide max / integer sum for 256 threads (order-independent).
+__device__ __forceinline__ float block256_max(float v, float* red) {
+    v = wave_max(v);
+    const int t = threadIdx.x;
+    if ((t & 63) == 0) red[t >> 6] = v;
+    __syncthreads();
+    float r = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    return r;
+}
+
+__device__ __forceinline__ int block256_sum_i32(int v, int* red) {
+    v = wave_sum_i32(v);
+    const int t = threadIdx.x;
+    if ((t & 63) == 0) red[t >> 6] = v;
+    __syncthreads();
+    int r = red[0] + red[1] + red[2] + red[3];
+    __syncthreads();
+    return r;
+}
+
+// inv_rms of rms_norm_raw (TenzoEngine.cpp:154): 1 / sqrt(ss/dim + eps), each
+// operation correctly rounded.
+__device__ __forceinline__ float inv_rms_from_sumsq(float ss, int64_t dim, float eps) {
+    float mean = __fdiv_rn(ss, (float)dim);
+    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+}
+
+// y = x * inv_rms * w evaluated left to right (TenzoEngine.cpp:158).
+__device__ __forceinline__ float norm_apply(float x, float inv_rms, const float* __restrict__ w,
+                                            int64_t i) {
+    float v = __fmul_rn(x, inv_rms);
+    return w ? __fmul_rn(v, w[i]) : v;
+}
+
+// Signed 8-bit dot of 4 lanes + accumulator (v_dot4_i32_i8).
+__device__ __forceinline__ int sdot4(uint32_t a, int32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, b, c, false);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+__device__ __forceinline__ float i8_to_f32(int v) { return (float)v; }
+
+}  // namespace tz

@@ -1,0 +1,392 @@
+// 4-bit quantized GEMVs on gfx950: GGUF Q4_0 (fp32/fp16 or Q8_0
+// activations), GPTQ and AWQ (reference src/runtime/TenzoEngine.cpp:1022-1175).
+#include "common.h"
+
+namespace tz {
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v);
+template <>
+__device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float to_f32<uint16_t>(uint16_t v) { return half_bits_to_float(v); }
+
+// ------------------------------------------------------------------------
+// Q4_0: rows of K/32 blocks of 18 bytes (fp16 d, then 16 bytes: low nibble of
+// byte j is element j, high nibble element j+16), y_n = sum_b d_b * sum_j
+// a_j (q_j - 8). Rows start 16-byte aligned whenever K % 256 == 0 (row
+// stride 18*K/32), and 8 consecutive blocks are 144 bytes = 9 x 16, so a lane
+// takes groups of 8 blocks with nine 16-byte loads. LPR lanes share a row
+// (power of two); a 256-thread block holds 256/LPR rows. The activation row
+// is staged in LDS as fp32.
+// ------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t byte_at(const uint32_t* dw, int o) {
+    return (dw[o >> 2] >> (8 * (o & 3))) & 0xffu;
+}
+
+__device__ __forceinline__ float q4_block_dot(const uint32_t* dw, int off, const float* a) {
+    // block at byte offset `off` of the 36-dword window; a = its 32 activations
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const uint32_t byte = byte_at(dw, off + 2 + j);
+        s = __builtin_fmaf(a[j], (float)((int)(byte & 15u) - 8), s);
+        s = __builtin_fmaf(a[16 + j], (float)((int)(byte >> 4) - 8), s);
+    }
+    return s;
+}
+
+template <typename TA, int LPR>
+__global__ void __launch_bounds__(256)
+q4_0_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __restrict__ y,
+            int K, int N) {
+    extern __shared__ float a_s[];
+    const int b = blockIdx.y;
+    for (int i = threadIdx.x; i < K; i += 256) a_s[i] = to_f32<TA>(act[(int64_t)b * K + i]);
+    __syncthreads();
+    constexpr int RPB = 256 / LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    const int nbk = K / 32;
+    const int ngroups = (nbk + 7) / 8;
+    float acc = 0.0f;
+    if (row < N) {
+        const uint8_t* rowp = w + (int64_t)row * nbk * 18;
+        for (int g = sub; g < ngroups; g += LPR) {
+            const int b0 = g * 8;
+            if (b0 + 8 <= nbk && (((uintptr_t)(rowp + b0 * 18)) & 15) == 0) {
+                uint32_t dw[36];
+                const uint4* p = reinterpret_cast<const uint4*>(rowp + b0 * 18);
+#pragma unroll
+                for (int i = 0; i < 9; ++i) {
+                    const uint4 v = p[i];
+                    dw[4 * i] = v.x;
+                    dw[4 * i + 1] = v.y;
+                    dw[4 * i + 2] = v.z;
+                    dw[4 * i + 3] = v.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t dbits = byte_at(dw, 18 * i) | (byte_at(dw, 18 * i + 1) << 8);
+                    const float d = half_bits_to_float((uint16_t)dbits);
+                    acc = __builtin_fmaf(q4_block_dot(dw, 18 * i, a_s + (b0 + i) * 32), d, acc);
+                }
+            } else {
+                for (int bb = b0; bb < nbk && bb < b0 + 8; ++bb) {
+                    const uint8_t* blk = rowp + bb * 18;
+                    uint32_t dw[5];
+                    // 18 bytes, 2-byte aligned: assemble from halfwords
+                    const uint16_t* hp = reinterpret_cast<const uint16_t*>(blk);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dw[i] = hp[2 * i] | ((uint32_t)hp[2 * i + 1] << 16);
+                    dw[4] = hp[8];
+                    const float d = half_bits_to_float((uint16_t)(dw[0] & 0xffffu));
+                    acc = __builtin_fmaf(q4_block_dot(dw, 0, a_s + bb * 32), d, acc);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+}
+
+// Q4_0 weights x Q8_0 activations: per block the exact int32 dot
+// sum_j (q_j - 8) qa_j = dot4(q, qa) - 8 * sum_j qa_j, then an fp32 FMA with
+// d_w * d_a. Activations staged in LDS as codes + fp32 scales + code sums.
+template <int LPR>
+__global__ void __launch_bounds__(256)
+q4_0_q8_kernel(const uint8_t* __restrict__ qa, const uint8_t* __restrict__ w,
+               float* __restrict__ y, int K, int N) {
+    extern __shared__ int32_t smem[];
+    const int nbk = K / 32;
+    int32_t* codes = smem;                                    // nbk * 8 words
+    float* da = reinterpret_cast<float*>(smem + nbk * 8);     // nbk
+    int32_t* csum = smem + nbk * 9;                           // nbk
+    const int b = blockIdx.y;
+    const uint8_t* qab = qa + (int64_t)b * nbk * 34;
+    for (int i = threadIdx.x; i < nbk * 8; i += 256) {
+        const int blk = i >> 3, j = (i & 7) * 4;
+        const uint8_t* p = qab + blk * 34 + 2 + j;
+        codes[i] = (int32_t)((uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+                             ((uint32_t)p[3] << 24));
+    }
+    for (int i = threadIdx.x; i < nbk; i += 256) {
+        const uint8_t* p = qab + i * 34;
+        da[i] = half_bits_to_float((uint16_t)(p[0] | (p[1] << 8)));
+        int s = 0;
+        for (int j = 0; j < 32; ++j) s += (int8_t)p[2 + j];
+        csum[i] = s;
+    }
+    __syncthreads();
+    constexpr int RPB = 256 / LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    float acc = 0.0f;
+    if (row < N) {
+        const uint8_t* rowp = w + (int64_t)row * nbk * 18;
+        for (int bb = sub; bb < nbk; bb += LPR) {
+            const uint16_t* hp = reinterpret_cast<const uint16_t*>(rowp + bb * 18);
+            uint32_t q[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) q[i] = hp[1 + 2 * i] | ((uint32_t)hp[2 + 2 * i] << 16);
+            const float dw = half_bits_to_float(hp[0]);
+            const int32_t* c = codes + bb * 8;
+            int s = 0;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                s = sdot4(q[i] & 0x0f0f0f0fu, c[i], s);          // elements 4i..4i+3
+                s = sdot4((q[i] >> 4) & 0x0f0f0f0fu, c[4 + i], s);  // elements 16+4i..
+            }
+            s -= 8 * csum[bb];
+            acc = __builtin_fmaf((float)s, __fmul_rn(dw, da[bb]), acc);
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+}
+
+// ------------------------------------------------------------------------
+// GPTQ / AWQ: qweight [K/8][N] u32, lane = output column n (coalesced 256 B
+// per wave per k-octet). Split-K: block (column tile of 256, split s) covers
+// k in [s*KC, (s+1)*KC), a multiple of the group size; B activation rows are
+// staged in LDS as fp32 and every dequantized weight feeds all B rows.
+// Partials go to scratch and the last split block of a column tile adds them
+// in split order, so results are deterministic.
+// ------------------------------------------------------------------------
+
+template <bool AWQ, typename TA, typename TS, int BMAX>
+__global__ void __launch_bounds__(256)
+gq_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
+          const TS* __restrict__ scales, const uint32_t* __restrict__ qzeros,
+          float* __restrict__ y, int K, int N, int group, int B, int KC, int splits,
+          float* __restrict__ part, uint32_t* __restrict__ cnt) {
+    extern __shared__ float a_s[];  // [B][KC]
+    __shared__ int is_last;
+    const int tile = blockIdx.x;
+    const int sp = blockIdx.y;
+    const int k0 = sp * KC;
+    const int k1 = min(K, k0 + KC);
+    const int nk = k1 - k0;
+    for (int i = threadIdx.x; i < B * nk; i += 256) {
+        const int bb = i / nk, kk = i - bb * nk;
+        a_s[bb * KC + kk] = to_f32<TA>(act[(int64_t)bb * K + k0 + kk]);
+    }
+    __syncthreads();
+    const int n = tile * 256 + threadIdx.x;
+    float acc[BMAX];
+#pragma unroll
+    for (int bb = 0; bb < BMAX; ++bb) acc[bb] = 0.0f;
+    if (n < N) {
+        for (int g0 = k0; g0 < k1; g0 += group) {
+            const int g = g0 / group;
+            const float s = to_f32<TS>(scales[(int64_t)g * N + n]);
+            int z;
+            if (AWQ) {
+                z = (int)((qzeros[(int64_t)g * (N / 8) + n / 8] >> (4 * (n % 8))) & 15u);
+            } else {
+                z = (int)((qzeros[(int64_t)(g / 8) * N + n] >> (4 * (g % 8))) & 15u) + 1;
+            }
+            const int gend = min(k1, g0 + group);
+            for (int k = g0; k < gend; k += 8) {
+                const uint32_t qw = qweight[(int64_t)(k / 8) * N + n];
+                float wd[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    wd[e] = __fmul_rn((float)((int)((qw >> (4 * e)) & 15u) - z), s);
+                const int kl = k - k0;
+#pragma unroll
+                for (int bb = 0; bb < BMAX; ++bb) {
+                    if (bb < B) {
+                        const float* ab = a_s + bb * KC + kl;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const int o = AWQ ? ((e & 3) * 2 + (e >> 2)) : e;  // {0,2,4,6,1,3,5,7}
+                            acc[bb] = __builtin_fmaf(ab[o], wd[e], acc[bb]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if (splits == 1) {
+        if (n < N)
+            for (int bb = 0; bb < B && bb < BMAX; ++bb) y[(int64_t)bb * N + n] = acc[bb];
+        return;
+    }
+    if (n < N)
+        for (int bb = 0; bb < B && bb < BMAX; ++bb)
+            part[((int64_t)sp * B + bb) * N + n] = acc[bb];
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicAdd(&cnt[tile], 1u) == (unsigned)(splits - 1);
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    if (n < N) {
+        for (int bb = 0; bb < B && bb < BMAX; ++bb) {
+            float s = 0.0f;
+            for (int q = 0; q < splits; ++q)
+                s += __hip_atomic_load(&part[((int64_t)q * B + bb) * N + n], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            y[(int64_t)bb * N + n] = s;
+        }
+    }
+    if (threadIdx.x == 0) atomicExch(&cnt[tile], 0u);
+}
+
+// ------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------
+
+static int pick_lpr(int ngroups) {
+    int l = 1;
+    while (l < ngroups && l < 64) l <<= 1;
+    return l;
+}
+
+template <typename TA>
+static int launch_q4_0(const TA* act, const uint8_t* w, float* y, int K, int N, int B,
+                       hipStream_t st) {
+    const int nbk = K / 32;
+    const int lpr = pick_lpr((nbk + 7) / 8);
+    const size_t smem = (size_t)K * 4;
+    dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
+#define Q4_CASE(L)                                                                   \
+    case L:                                                                          \
+        hipLaunchKernelGGL((q4_0_kernel<TA, L>), grid, dim3(256), smem, st, act, w, y, K, N); \
+        break;
+    switch (lpr) {
+        Q4_CASE(1) Q4_CASE(2) Q4_CASE(4) Q4_CASE(8) Q4_CASE(16) Q4_CASE(32) Q4_CASE(64)
+    }
+#undef Q4_CASE
+    return launch_status("q4_0_kernel");
+}
+
+template <bool AWQ, typename TA, typename TS>
+static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
+                     const uint32_t* qzeros, float* y, int K, int N, int group, int B,
+                     hipStream_t st) {
+    const int tiles = (int)ceil_div(N, 256);
+    // split K (in whole groups) until there are ~1024 blocks
+    const int ngroups = (int)ceil_div(K, group);
+    int splits = (int)ceil_div(1024, tiles);
+    if (splits > ngroups) splits = ngroups;
+    if (splits < 1) splits = 1;
+    const int gps = (int)ceil_div(ngroups, splits);
+    splits = (int)ceil_div(ngroups, gps);
+    const int KC = gps * group;
+    float* part = nullptr;
+    uint32_t* cnt = nullptr;
+    if (splits > 1) {
+        const size_t bytes = (size_t)splits * B * N * 4 + (size_t)tiles * 4;
+        char* ws = (char*)Scratch::get(kScratchTmp, bytes, st);
+        if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+        part = (float*)ws;
+        cnt = (uint32_t*)(ws + (size_t)splits * B * N * 4);
+    }
+    const size_t smem = (size_t)B * KC * 4;
+    if (smem > 64 * 1024) {
+        set_error("gptq/awq: batch x group chunk too large for LDS (%zu bytes)", smem);
+        return TENZO_ERROR_UNSUPPORTED;
+    }
+    dim3 grid((unsigned)tiles, (unsigned)splits);
+#define GQ_CASE(BM)                                                                          \
+    if (B <= BM) {                                                                           \
+        hipLaunchKernelGGL((gq_kernel<AWQ, TA, TS, BM>), grid, dim3(256), smem, st, act,      \
+                           qweight, scales, qzeros, y, K, N, group, B, KC, splits, part, cnt); \
+        return launch_status(AWQ ? "awq_kernel" : "gptq_kernel");                            \
+    }
+    GQ_CASE(1) GQ_CASE(2) GQ_CASE(4) GQ_CASE(8)
+#undef GQ_CASE
+    set_error("gptq/awq: batch %d > 8 not supported", B);
+    return TENZO_ERROR_UNSUPPORTED;
+}
+
+template <bool AWQ>
+static int dispatch_gq(const void* act, int act_dtype, const uint32_t* qweight,
+                       const void* scales, int scale_dtype, const uint32_t* qzeros, float* y,
+                       int K, int N, int group, int B, hipStream_t st) {
+    if (act_dtype == 0 && scale_dtype == 0)
+        return launch_gq<AWQ>((const float*)act, qweight, (const float*)scales, qzeros, y, K, N,
+                              group, B, st);
+    if (act_dtype == 0 && scale_dtype == 1)
+        return launch_gq<AWQ>((const float*)act, qweight, (const uint16_t*)scales, qzeros, y, K,
+                              N, group, B, st);
+    if (act_dtype == 1 && scale_dtype == 0)
+        return launch_gq<AWQ>((const uint16_t*)act, qweight, (const float*)scales, qzeros, y, K,
+                              N, group, B, st);
+    return launch_gq<AWQ>((const uint16_t*)act, qweight, (const uint16_t*)scales, qzeros, y, K,
+                          N, group, B, st);
+}
+
+}  // namespace tz
+
+using namespace tz;
+
+extern "C" {
+
+TENZO_HIP_API int tenzo_hip_gemv_q4_0(const void* act, int act_dtype, const uint8_t* w,
+                                      float* y, int K, int N, int B, void* stream) {
+    TZ_CHECK(act && w && y, "gemv_q4_0: null pointer");
+    TZ_CHECK(K > 0 && K % 32 == 0 && N > 0 && B > 0 && B <= 65535,
+             "gemv_q4_0: need K %% 32 == 0 (K=%d)", K);
+    TZ_CHECK(K <= 16384, "gemv_q4_0: K=%d above the LDS staging limit 16384", K);
+    TZ_CHECK(act_dtype == 0 || act_dtype == 1, "gemv_q4_0: act_dtype must be 0 or 1");
+    hipStream_t st = (hipStream_t)stream;
+    if (act_dtype == 0) return launch_q4_0((const float*)act, w, y, K, N, B, st);
+    return launch_q4_0((const uint16_t*)act, w, y, K, N, B, st);
+}
+
+TENZO_HIP_API int tenzo_hip_gemv_q4_0_q8_0(const uint8_t* qa, const uint8_t* w, float* y,
+                                           int K, int N, int B, void* stream) {
+    TZ_CHECK(qa && w && y, "gemv_q4_0_q8_0: null pointer");
+    TZ_CHECK(K > 0 && K % 32 == 0 && N > 0 && B > 0 && B <= 65535,
+             "gemv_q4_0_q8_0: need K %% 32 == 0");
+    const int nbk = K / 32;
+    const size_t smem = (size_t)nbk * 10 * 4;
+    TZ_CHECK(smem <= 64 * 1024, "gemv_q4_0_q8_0: K=%d too large", K);
+    const int lpr = pick_lpr(nbk / 4 > 0 ? nbk / 4 : 1);
+    dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
+    hipStream_t st = (hipStream_t)stream;
+#define Q8_CASE(L)                                                                           \
+    case L:                                                                                  \
+        hipLaunchKernelGGL((q4_0_q8_kernel<L>), grid, dim3(256), smem, st, qa, w, y, K, N); \
+        break;
+    switch (lpr) {
+        Q8_CASE(1) Q8_CASE(2) Q8_CASE(4) Q8_CASE(8) Q8_CASE(16) Q8_CASE(32) Q8_CASE(64)
+    }
+#undef Q8_CASE
+    return launch_status("q4_0_q8_kernel");
+}
+
+TENZO_HIP_API int tenzo_hip_gemv_gptq(const void* act, int act_dtype, const uint32_t* qweight,
+                                      const void* scales, int scale_dtype,
+                                      const uint32_t* qzeros, float* y, int K, int N,
+                                      int group, int B, void* stream) {
+    TZ_CHECK(act && qweight && scales && qzeros && y, "gemv_gptq: null pointer");
+    TZ_CHECK(K > 0 && K % 8 == 0 && N > 0 && group > 0 && group % 8 == 0 && B >= 1 && B <= 8,
+             "gemv_gptq: need K %% 8 == 0, group %% 8 == 0, 1 <= B <= 8");
+    TZ_CHECK((act_dtype == 0 || act_dtype == 1) && (scale_dtype == 0 || scale_dtype == 1),
+             "gemv_gptq: dtype codes must be 0 (fp32) or 1 (fp16)");
+    return dispatch_gq<false>(act, act_dtype, qweight, scales, scale_dtype, qzeros, y, K, N,
+                              group, B, (hipStream_t)stream);
+}
+
+TENZO_HIP_API int tenzo_hip_gemv_awq(const void* act, int act_dtype, const uint32_t* qweight,
+                                     const void* scales, int scale_dtype,
+                                     const uint32_t* qzeros, float* y, int K, int N, int group,
+                                     int B, void* stream) {
+    TZ_CHECK(act && qweight && scales && qzeros && y, "gemv_awq: null pointer");
+    TZ_CHECK(K > 0 && K % 8 == 0 && N > 0 && N % 8 == 0 && group > 0 && group % 8 == 0 &&
+                 B >= 1 && B <= 8,
+             "gemv_awq: need K %% 8 == 0, N %% 8 == 0, group %% 8 == 0, 1 <= B <= 8");
+    TZ_CHECK((act_dtype == 0 || act_dtype == 1) && (scale_dtype == 0 || scale_dtype == 1),
+             "gemv_awq: dtype codes must be 0 (fp32) or 1 (fp16)");
+    return dispatch_gq<true>(act, act_dtype, qweight, scales, scale_dtype, qzeros, y, K, N,
+                             group, B, (hipStream_t)stream);
+}
+
+}  // extern "C"

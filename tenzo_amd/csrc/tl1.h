@@ -1,0 +1,32 @@
+// Internal interface of the TL1 kernels (used by the C ABI and the engine).
+#pragma once
+
+#include "common.h"
+
+namespace tz {
+
+// Per-row output scales of a GEMV over row-concatenated matrices (fused
+// Q|K|V or gate|up): rows [end[j-1], end[j]) use scale[j].
+struct RowScales {
+    int64_t end[4];
+    float scale[4];
+    int n;
+    static RowScales single(float s) {
+        RowScales r{};
+        r.end[0] = INT64_MAX;
+        r.scale[0] = s;
+        r.n = 1;
+        return r;
+    }
+};
+
+int launch_tl1_repack(const uint8_t* w_tl1, void* w_packed, int64_t N, int64_t K,
+                      hipStream_t st);
+int launch_quant31(const float* x, const float* norm_w, bool do_norm, float eps, int64_t M,
+                   int64_t K, int8_t* codes, tenzo_hip_actq_t* q, float* y_out, hipStream_t st);
+int launch_tl1_gemv(const int8_t* codes, const tenzo_hip_actq_t* q, const void* w_packed,
+                    const RowScales& rs, int64_t M, int64_t N, int64_t K, float* y,
+                    int32_t* acc_out, hipStream_t st, int splits);
+int tl1_pick_splits(int64_t nb, int64_t KS, int64_t M);
+
+}  // namespace tz

@@ -1,0 +1,404 @@
+// TL1 ternary GEMV on gfx950: device weight layout, activation quantization
+// (optionally fused with RMSNorm) and a split-K GEMV on v_dot4_i32_i8.
+//
+// Reference: src/runtime/TenzoEngine.cpp:22-166 (build_lut,
+// compute_single_block, compute_from_lut, rms_norm_raw).
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "common.h"
+#include "tl1.h"
+
+namespace tz {
+
+// ------------------------------------------------------------------------
+// Device layout. For row block b (64 rows) and super-chunk s (64 columns)
+// there are 64 x 16 bytes: the 16 bytes of row r hold its 64 columns as four
+// dwords; dword q covers columns 64s+16q+c (c = 0..15) as 2-bit codes
+// u = w + 1 in {0, 1, 2} at bit 8*(c%4) + 2*(c/4). So (dword >> 2j) & 0x03030303
+// has the codes of columns 16q+4j .. 16q+4j+3 in byte order, ready for one
+// v_dot4 against four consecutive activation codes, and
+//     sum_k w_k a_k = sum_k u_k a_k - sum_k a_k.
+// A wave reads one super-chunk of its row block as 1 KiB contiguous (lane =
+// row); columns past K are padded with u = 1 (w = 0).
+// ------------------------------------------------------------------------
+
+__global__ void tl1_repack_kernel(const uint8_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                  int64_t nb, int64_t kh, int64_t KS) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nb * KS * 256) return;
+    const int q = (int)(idx & 3);
+    const int r = (int)((idx >> 2) & 63);
+    const int64_t bs = idx >> 8;
+    const int64_t s = bs % KS;
+    const int64_t b = bs / KS;
+    uint32_t out = 0;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int64_t kp = s * 32 + q * 8 + m;  // column pair (2kp, 2kp+1)
+        uint32_t nib = 5u;                      // (w0, w1) = (0, 0)
+        if (kp < kh) {
+            const uint32_t byte = src[(b * kh + kp) * 32 + (r & 31)];
+            nib = (r < 32) ? (byte & 15u) : (byte >> 4);
+        }
+        const int c0 = 2 * m, c1 = 2 * m + 1;
+        out |= (nib & 3u) << (8 * (c0 & 3) + 2 * (c0 >> 2));
+        out |= (nib >> 2) << (8 * (c1 & 3) + 2 * (c1 >> 2));
+    }
+    dst[idx] = out;
+}
+
+// ------------------------------------------------------------------------
+// Activation quantization (build_lut, :28-42), one 256-thread block per token.
+// MODE 0: codes of x; MODE 1: codes of rms_norm_raw(x, w); MODE 2: only the
+// normalized vector (executeRMSNorm).
+// ------------------------------------------------------------------------
+template <int MODE>
+__global__ void __launch_bounds__(256)
+quant31_kernel(const float* __restrict__ x, const float* __restrict__ w, float eps, int64_t K,
+               int64_t Kp, int8_t* __restrict__ codes, tenzo_hip_actq_t* __restrict__ q,
+               float* __restrict__ y_out) {
+    __shared__ float redf[4];
+    __shared__ int redi[4];
+    const int t = threadIdx.x;
+    const int64_t m = blockIdx.x;
+    const float* xm = x + m * K;
+    float inv_rms = 1.0f;
+    if (MODE >= 1) inv_rms = inv_rms_from_sumsq(block256_sumsq(xm, K, redf), K, eps);
+    if (MODE == 2) {
+        for (int64_t i = t; i < K; i += 256) y_out[m * K + i] = norm_apply(xm[i], inv_rms, w, i);
+        return;
+    }
+    float amax = 1e-6f;
+    for (int64_t i = t; i < K; i += 256) {
+        const float v = MODE == 1 ? norm_apply(xm[i], inv_rms, w, i) : xm[i];
+        amax = fmaxf(amax, fabsf(v));
+    }
+    amax = block256_max(amax, redf);
+    const float scale_act = __fdiv_rn(31.0f, amax);
+    int csum = 0;
+    int8_t* cm = codes + m * Kp;
+    for (int64_t i = t; i < Kp; i += 256) {
+        int c = 0;
+        if (i < K) {
+            const float v = MODE == 1 ? norm_apply(xm[i], inv_rms, w, i) : xm[i];
+            if (MODE == 1 && y_out) y_out[m * K + i] = v;
+            c = (int)roundf(__fmul_rn(v, scale_act));
+        }
+        cm[i] = (int8_t)c;
+        csum += c;
+    }
+    csum = block256_sum_i32(csum, redi);
+    if (t == 0) {
+        q[m].inv_scale = __fmul_rn(amax, 1.0f / 31.0f);  // absmax/31 as the reference build
+        q[m].code_sum = csum;
+    }
+}
+
+// ------------------------------------------------------------------------
+// GEMV. Grid (row_blocks * splits, M); 256 threads = 4 waves. A block owns
+// one row block (lane = row) and a contiguous range of super-chunks, which
+// its 4 waves interleave. Activation codes are wave-uniform and come in
+// through scalar loads. Partial int32 sums are exact: with splits > 1 they
+// are added atomically into a zeroed accumulator and the last block of the
+// row block converts and re-zeroes it.
+// ------------------------------------------------------------------------
+
+__device__ __forceinline__ int dot16(const uint4 v, const int32_t* __restrict__ a, int acc) {
+    const uint32_t M = 0x03030303u;
+    acc = sdot4(v.x & M, a[0], acc);
+    acc = sdot4((v.x >> 2) & M, a[1], acc);
+    acc = sdot4((v.x >> 4) & M, a[2], acc);
+    acc = sdot4((v.x >> 6) & M, a[3], acc);
+    acc = sdot4(v.y & M, a[4], acc);
+    acc = sdot4((v.y >> 2) & M, a[5], acc);
+    acc = sdot4((v.y >> 4) & M, a[6], acc);
+    acc = sdot4((v.y >> 6) & M, a[7], acc);
+    acc = sdot4(v.z & M, a[8], acc);
+    acc = sdot4((v.z >> 2) & M, a[9], acc);
+    acc = sdot4((v.z >> 4) & M, a[10], acc);
+    acc = sdot4((v.z >> 6) & M, a[11], acc);
+    acc = sdot4(v.w & M, a[12], acc);
+    acc = sdot4((v.w >> 2) & M, a[13], acc);
+    acc = sdot4((v.w >> 4) & M, a[14], acc);
+    acc = sdot4((v.w >> 6) & M, a[15], acc);
+    return acc;
+}
+
+__device__ __forceinline__ void tl1_finalize(int tot, int64_t m, int64_t row, int64_t N,
+                                             const tenzo_hip_actq_t* __restrict__ aq,
+                                             const RowScales& rs, float* __restrict__ y,
+                                             int32_t* __restrict__ acc_out) {
+    const tenzo_hip_actq_t a = aq[m];
+    const int v = tot - a.code_sum;
+    int j = 0;
+    while (j < rs.n - 1 && row >= rs.end[j]) ++j;
+    y[m * N + row] = (float)v * __fmul_rn(a.inv_scale, rs.scale[j]);  // :1554, :118-126
+    if (acc_out) acc_out[m * N + row] = v;
+}
+
+__global__ void __launch_bounds__(256)
+tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
+                const tenzo_hip_actq_t* __restrict__ aq, int64_t N, int64_t KS, int splits,
+                RowScales rs, float* __restrict__ y, int32_t* __restrict__ acc_out,
+                int32_t* __restrict__ ws_acc, uint32_t* __restrict__ ws_cnt) {
+    __shared__ int red[4][64];
+    __shared__ int is_last;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t nb = N >> 6;
+    const int64_t b = blockIdx.x / splits;
+    const int sp = (int)(blockIdx.x - b * splits);
+    const int64_t m = blockIdx.y;
+    const int64_t per = (KS + splits - 1) / splits;
+    const int64_t s0 = sp * per;
+    const int64_t s1 = s0 + per < KS ? s0 + per : KS;
+    const uint4* wb = w + b * KS * 64 + lane;
+    const int32_t* a32 = reinterpret_cast<const int32_t*>(codes + m * KS * 64);
+
+    int acc = 0;
+    int64_t s = s0 + wave;
+    for (; s + 4 < s1; s += 8) {
+        const uint4 v0 = wb[s * 64];
+        const uint4 v1 = wb[(s + 4) * 64];
+        acc = dot16(v0, a32 + s * 16, acc);
+        acc = dot16(v1, a32 + (s + 4) * 16, acc);
+    }
+    if (s < s1) acc = dot16(wb[s * 64], a32 + s * 16, acc);
+
+    red[wave][lane] = acc;
+    __syncthreads();
+    const int64_t row = b * 64 + lane;
+    if (splits == 1) {
+        if (wave == 0) {
+            const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+            tl1_finalize(tot, m, row, N, aq, rs, y, acc_out);
+        }
+        return;
+    }
+    if (wave == 0) {
+        const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+        atomicAdd(&ws_acc[m * N + row], tot);
+    }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = atomicAdd(&ws_cnt[m * nb + b], 1u);
+        is_last = prev == (unsigned)(splits - 1);
+    }
+    __syncthreads();
+    if (is_last && wave == 0) {
+        __threadfence();
+        const int tot = atomicExch(&ws_acc[m * N + row], 0);
+        tl1_finalize(tot, m, row, N, aq, rs, y, acc_out);
+        if (lane == 0) atomicExch(&ws_cnt[m * nb + b], 0u);
+    }
+}
+
+// ------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------
+
+int tl1_pick_splits(int64_t nb, int64_t KS, int64_t M) {
+    // Aim at ~4 blocks per CU of the 256, with at least one super-chunk per
+    // wave of every block.
+    int64_t want = ceil_div(1024, nb * M);
+    int64_t cap = KS / 4 > 0 ? KS / 4 : 1;
+    if (want > cap) want = cap;
+    if (want < 1) want = 1;
+    return (int)want;
+}
+
+int launch_quant31(const float* x, const float* norm_w, bool do_norm, float eps, int64_t M,
+                   int64_t K, int8_t* codes, tenzo_hip_actq_t* q, float* y_out,
+                   hipStream_t st) {
+    const int64_t Kp = ceil_div(K, 64) * 64;
+    if (do_norm)
+        hipLaunchKernelGGL(quant31_kernel<1>, dim3((unsigned)M), dim3(256), 0, st, x, norm_w,
+                           eps, K, Kp, codes, q, y_out);
+    else
+        hipLaunchKernelGGL(quant31_kernel<0>, dim3((unsigned)M), dim3(256), 0, st, x, norm_w,
+                           eps, K, Kp, codes, q, y_out);
+    return launch_status("quant31_kernel");
+}
+
+int launch_tl1_gemv(const int8_t* codes, const tenzo_hip_actq_t* q, const void* w_packed,
+                    const RowScales& rs, int64_t M, int64_t N, int64_t K, float* y,
+                    int32_t* acc_out, hipStream_t st, int splits) {
+    const int64_t nb = N / 64;
+    const int64_t KS = ceil_div(K, 64);
+    if (splits <= 0) splits = tl1_pick_splits(nb, KS, M);
+    if (splits > KS) splits = (int)KS;
+    int32_t* ws_acc = nullptr;
+    uint32_t* ws_cnt = nullptr;
+    if (splits > 1) {
+        const size_t bytes = (size_t)(M * N + M * nb) * 4;
+        char* ws = (char*)Scratch::get(kScratchGemvAcc, bytes, st);
+        if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+        ws_acc = (int32_t*)ws;
+        ws_cnt = (uint32_t*)(ws + (size_t)M * N * 4);
+    }
+    hipLaunchKernelGGL(tl1_gemv_kernel, dim3((unsigned)(nb * splits), (unsigned)M), dim3(256),
+                       0, st, (const uint4*)w_packed, codes, q, N, KS, splits, rs, y, acc_out,
+                       ws_acc, ws_cnt);
+    return launch_status("tl1_gemv_kernel");
+}
+
+int launch_tl1_repack(const uint8_t* w_tl1, void* w_packed, int64_t N, int64_t K,
+                      hipStream_t st) {
+    const int64_t nb = N / 64, kh = K / 2, KS = ceil_div(K, 64);
+    const int64_t total = nb * KS * 256;
+    hipLaunchKernelGGL(tl1_repack_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
+                       st, w_tl1, (uint32_t*)w_packed, nb, kh, KS);
+    return launch_status("tl1_repack_kernel");
+}
+
+}  // namespace tz
+
+using namespace tz;
+
+namespace {
+std::mutex g_shim_mu;
+struct ShimWeights {
+    void* packed = nullptr;
+    int64_t N = 0, K = 0;
+};
+std::map<const void*, ShimWeights> g_shim_cache;
+
+int shim_upload(const uint8_t* w, int64_t N, int64_t K, void** out) {
+    auto it = g_shim_cache.find(w);
+    if (it != g_shim_cache.end() && it->second.N == N && it->second.K == K) {
+        *out = it->second.packed;
+        return TENZO_SUCCESS;
+    }
+    if (it != g_shim_cache.end()) {
+        TZ_HIP(hipFree(it->second.packed));
+        g_shim_cache.erase(it);
+    }
+    const size_t raw = (size_t)N * K / 4;
+    void* staging = nullptr;
+    void* packed = nullptr;
+    TZ_HIP(hipMalloc(&staging, raw));
+    TZ_HIP(hipMalloc(&packed, tenzo_hip_tl1_packed_bytes(N, K)));
+    TZ_HIP(hipMemcpy(staging, w, raw, hipMemcpyHostToDevice));
+    int st = launch_tl1_repack((const uint8_t*)staging, packed, N, K, nullptr);
+    if (st) return st;
+    TZ_HIP(hipDeviceSynchronize());
+    TZ_HIP(hipFree(staging));
+    g_shim_cache[w] = ShimWeights{packed, N, K};
+    *out = packed;
+    return TENZO_SUCCESS;
+}
+}  // namespace
+
+extern "C" {
+
+TENZO_HIP_API size_t tenzo_hip_tl1_packed_bytes(int64_t N, int64_t K) {
+    return (size_t)(N / 64) * (size_t)ceil_div(K, 64) * 1024;
+}
+
+TENZO_HIP_API int tenzo_hip_tl1_repack(const uint8_t* w_tl1, void* w_packed, int64_t N,
+                                       int64_t K, void* stream) {
+    TZ_CHECK(w_tl1 && w_packed, "tl1_repack: null pointer");
+    TZ_CHECK(N > 0 && K > 0 && N % 64 == 0 && K % 2 == 0,
+             "tl1_repack: need N %% 64 == 0 and K %% 2 == 0 (N=%lld K=%lld)", (long long)N,
+             (long long)K);
+    return launch_tl1_repack(w_tl1, w_packed, N, K, (hipStream_t)stream);
+}
+
+TENZO_HIP_API int tenzo_hip_rmsnorm_quant31(const float* x, const float* norm_w, int do_norm,
+                                            float eps, int64_t M, int64_t K, int8_t* codes,
+                                            tenzo_hip_actq_t* q, float* y_out, void* stream) {
+    TZ_CHECK(x && codes && q, "rmsnorm_quant31: null pointer");
+    TZ_CHECK(M > 0 && M <= 65535 && K > 0, "rmsnorm_quant31: bad sizes");
+    return launch_quant31(x, norm_w, do_norm || norm_w, eps, M, K, codes, q, y_out,
+                          (hipStream_t)stream);
+}
+
+TENZO_HIP_API int tenzo_hip_bitlinear_tl1(const int8_t* codes, const tenzo_hip_actq_t* q,
+                                          const void* w_packed, float w_scale, int64_t M,
+                                          int64_t N, int64_t K, float* y, int32_t* acc_out,
+                                          void* stream) {
+    TZ_CHECK(codes && q && w_packed && y, "bitlinear_tl1: null pointer");
+    TZ_CHECK(M > 0 && M <= 65535 && N > 0 && N % 64 == 0 && K > 0,
+             "bitlinear_tl1: need N %% 64 == 0 (N=%lld)", (long long)N);
+    RowScales rs = RowScales::single(w_scale);
+    return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, acc_out, (hipStream_t)stream, 0);
+}
+
+TENZO_HIP_API int tenzo_hip_bitlinear_tl1_f32(const float* x, const void* w_packed,
+                                              float w_scale, int64_t M, int64_t N, int64_t K,
+                                              float* y, void* stream) {
+    TZ_CHECK(x && w_packed && y, "bitlinear_tl1_f32: null pointer");
+    TZ_CHECK(M > 0 && M <= 65535 && N > 0 && N % 64 == 0 && K > 0,
+             "bitlinear_tl1_f32: need N %% 64 == 0");
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t Kp = ceil_div(K, 64) * 64;
+    char* ws = (char*)Scratch::get(kScratchAct, (size_t)(M * Kp + M * 8 + 256), st);
+    if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+    tenzo_hip_actq_t* q = (tenzo_hip_actq_t*)ws;
+    int8_t* codes = (int8_t*)(ws + ((M * 8 + 255) / 256) * 256);
+    int rc = launch_quant31(x, nullptr, false, 0.0f, M, K, codes, q, nullptr, st);
+    if (rc) return rc;
+    RowScales rs = RowScales::single(w_scale);
+    return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, nullptr, st, 0);
+}
+
+TENZO_HIP_API int tenzo_hip_rmsnorm(const float* x, const float* w, float* y, int64_t dim,
+                                    float eps, void* stream) {
+    TZ_CHECK(x && y && dim > 0, "rmsnorm: bad arguments");
+    hipLaunchKernelGGL(quant31_kernel<2>, dim3(1), dim3(256), 0, (hipStream_t)stream, x, w, eps,
+                       dim, dim, (int8_t*)nullptr, (tenzo_hip_actq_t*)nullptr, y);
+    return launch_status("rmsnorm");
+}
+
+TENZO_HIP_API int tenzo_hip_execute_bitlinear_tl1(const float* act, const uint8_t* w,
+                                                  float* out, size_t M, size_t K, size_t N,
+                                                  float scale) {
+    if (!act || !w || !out || M == 0 || N % 64 || K % 2) {
+        set_error("execute_bitlinear_tl1: bad arguments");
+        return 0;
+    }
+    std::lock_guard<std::mutex> lk(g_shim_mu);
+    void* packed = nullptr;
+    if (shim_upload(w, (int64_t)N, (int64_t)K, &packed)) return 0;
+    float* dx = nullptr;
+    float* dy = nullptr;
+    if (hipMalloc(&dx, M * K * 4) != hipSuccess) return 0;
+    if (hipMalloc(&dy, M * N * 4) != hipSuccess) {
+        (void)hipFree(dx);
+        return 0;
+    }
+    bool ok = hipMemcpy(dx, act, M * K * 4, hipMemcpyHostToDevice) == hipSuccess &&
+              tenzo_hip_bitlinear_tl1_f32(dx, packed, scale, (int64_t)M, (int64_t)N,
+                                          (int64_t)K, dy, nullptr) == 0 &&
+              hipMemcpy(out, dy, M * N * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    return ok ? 1 : 0;
+}
+
+TENZO_HIP_API int tenzo_hip_execute_rmsnorm(const float* in, const float* w, float* out,
+                                            size_t dim, float eps) {
+    if (!in || !out || dim == 0) {
+        set_error("execute_rmsnorm: bad arguments");
+        return 0;
+    }
+    float* dx = nullptr;
+    float* dw = nullptr;
+    float* dy = nullptr;
+    bool ok = hipMalloc(&dx, dim * 4) == hipSuccess && hipMalloc(&dy, dim * 4) == hipSuccess &&
+              (!w || hipMalloc(&dw, dim * 4) == hipSuccess) &&
+              hipMemcpy(dx, in, dim * 4, hipMemcpyHostToDevice) == hipSuccess &&
+              (!w || hipMemcpy(dw, w, dim * 4, hipMemcpyHostToDevice) == hipSuccess) &&
+              tenzo_hip_rmsnorm(dx, w ? dw : nullptr, dy, (int64_t)dim, eps, nullptr) == 0 &&
+              hipMemcpy(out, dy, dim * 4, hipMemcpyDeviceToHost) == hipSuccess;
+    if (dx) (void)hipFree(dx);
+    if (dw) (void)hipFree(dw);
+    if (dy) (void)hipFree(dy);
+    return ok ? 1 : 0;
+}
+
+}  // extern "C"
