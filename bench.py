@@ -1,0 +1,313 @@
+"""Decode-throughput benchmark of the MI355X hot path (one GPU).
+
+Workload: one BitNet-b1.58-2B-shaped greedy decode
+step at batch 1 and 4096 tokens of context - 30 layers of TL1 ternary
+projections (hidden 2560, FFN 6912, 20 q / 5 kv heads of 128), INT8 KV cache
+with fp16 scales prefilled with 4096 quantized N(0,1) tokens, int8 LM head over
+vocab 128256, RoPE theta 500000. Weights are random-init of that architecture,
+generated on the device. Every timed step goes through the engine's C API
+(tenzo_generate_step: embed, 30 layers, LM head, greedy argmax, token back to
+the host) at position 4096 (the cache is rewound between steps).
+
+Prints ONE JSON line: tok/s, the step's HBM bytes / time against the 8 TB/s
+peak, a roofline entry for the dominant kernel (its algorithmic bytes / its
+mean launch time, both measured here with HIP events on the stream the kernel
+runs on), and the reference CPU path (oracle/_ref, compiled from the
+reference's own sources) timed on a bounded sample on the host cores.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 4096] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+SEED = 2
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--ctx", type=int, default=4096)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--eager", action="store_true", help="launch stages without the HIP graph")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------- synthetic
+
+def tl1_random_dev(torch, n_bytes, gen):
+    """TL1 bytes of iid ternary weights (P = 1/3 each) generated on the GPU."""
+    v = torch.randint(0, 9, (2, n_bytes), dtype=torch.uint8, device="cuda", generator=gen)
+    nib = (v % 3) | ((v // 3) << 2)
+    return (nib[0] | (nib[1] << 4)).contiguous()
+
+
+def build_model(torch, cfg, ctx):
+    from tenzo_amd import engine, synth
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED)
+    rng = np.random.default_rng(SEED)
+    e = engine.Engine(cfg)
+    host = {"layers": []}
+    for l in range(cfg.n_layers):
+        tl1 = {p: tl1_random_dev(torch, n * k // 4, gen)
+               for p, (n, k) in ((p, cfg.proj_shape(p)) for p in synth.PROJ)}
+        scale = {p: synth.latent_scale(rng) for p in synth.PROJ}
+        norms = {f: (1.0 + 0.1 * rng.standard_normal(cfg.ffn if f == "ffn_sub_norm" else
+                                                    cfg.hidden)).astype(np.float32)
+                 for f in ("in_norm", "attn_sub_norm", "post_norm", "ffn_sub_norm")}
+        w = engine.LayerWeights()
+        for p, f in zip(synth.PROJ, ["q", "k", "v", "out", "gate", "up", "down"]):
+            setattr(w, f + "_w", tl1[p].data_ptr())
+            setattr(w, f + "_scale", float(scale[p]))
+        for f, a in norms.items():
+            setattr(w, f, a.ctypes.data)
+        e._check(e.L.tenzo_set_layer_weights(e.h, l, ctypes.byref(w)), "set_layer_weights")
+        host["layers"].append((tl1, scale, norms))
+    final_norm = (1.0 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32)
+    e._check(e.L.tenzo_set_final_norm(e.h, final_norm.ctypes.data), "set_final_norm")
+    # LM head / tied embedding: latent N(0, 0.02), per-row int8 (load_model_from_files rule)
+    V, H = cfg.vocab, cfg.hidden
+    head = torch.empty((V, H), dtype=torch.int8, device="cuda")
+    hs = torch.empty(V, dtype=torch.float32, device="cuda")
+    for r0 in range(0, V, 16384):
+        E = torch.randn((min(16384, V - r0), H), device="cuda", generator=gen) * 0.02
+        amax = E.abs().amax(dim=1).clamp_min(1e-8)
+        s = amax * (1.0 / 127.0)
+        head[r0:r0 + E.shape[0]] = torch.clamp(torch.round(E * (127.0 / amax)[:, None]),
+                                               -127, 127).to(torch.int8)
+        hs[r0:r0 + E.shape[0]] = s
+    e._check(e.L.tenzo_set_lm_head_i8(e.h, head.data_ptr(), hs.data_ptr(), V, H),
+             "set_lm_head_i8")
+    # INT8 KV cache: ctx tokens of N(0,1) per (layer, kv head), quantized per token
+    L, Hkv = cfg.n_layers, cfg.n_kv_heads
+    kc = torch.empty((L, Hkv, ctx, 128), dtype=torch.int8, device="cuda")
+    vc = torch.empty_like(kc)
+    ks = torch.empty((L, Hkv, ctx), dtype=torch.float16, device="cuda")
+    vs = torch.empty_like(ks)
+    for c, s in ((kc, ks), (vc, vs)):
+        for l in range(L):
+            x = torch.randn((Hkv, ctx, 128), device="cuda", generator=gen)
+            amax = x.abs().amax(dim=2).clamp_min(1e-8)
+            c[l] = torch.clamp(torch.round(x * (127.0 / amax)[..., None]), -128, 127).to(torch.int8)
+            s[l] = (amax * (1.0 / 127.0)).half()
+    e.set_kv_device(kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(), ctx)
+    e.set_rope_theta(cfg.theta)
+    torch.cuda.synchronize()
+    host.update(final_norm=final_norm, head=head, hs=hs, kc=kc, vc=vc, ks=ks, vs=vs)
+    return e, host
+
+
+# ------------------------------------------------------------------- roofline
+
+def graph_time(torch, fn, reps):
+    """Mean duration of one fn() call: fn's launches are captured into a HIP
+    graph (no host overhead between them) and the graph is replayed reps times
+    between two HIP events on the replay stream."""
+    fn()  # first call outside the capture (allocates any library scratch)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    s = torch.cuda.current_stream()
+    g.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(s)
+    for _ in range(reps):
+        g.replay()
+    end.record(s)
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / reps
+
+
+def tl1_roofline(torch, cfg, host):
+    """The TL1 GEMV as the engine runs it per token: 4 launches per layer over
+    every layer's own weights (521 MB, so the reads come from HBM), replayed
+    from a graph and timed with HIP events (the time includes the gaps between
+    launches). Algorithmic bytes per launch = packed ternary weights N*K/4 +
+    int8 activation codes + fp32 outputs."""
+    from tenzo_amd import ops
+    H, F, qd, kvd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim
+    shapes = [(qd + 2 * kvd, H), (H, H), (2 * F, H), (H, F)]
+    packed = []
+    for tl1, _, _ in host["layers"]:
+        cat_qkv = torch.cat([tl1["q"], tl1["k"], tl1["v"]])
+        cat_gu = torch.cat([tl1["gate"], tl1["up"]])
+        mats = [cat_qkv, tl1["o"], cat_gu, tl1["down"]]
+        packed.append([ops.tl1_repack(m, n, k) for m, (n, k) in zip(mats, shapes)])
+    xs = {k: torch.randn(k, device="cuda") for k in (H, F)}
+    qs = {k: ops.rmsnorm_quant31(xs[k], None) for k in (H, F)}
+    ys = {n: torch.empty(n, device="cuda") for n, _ in shapes}
+    def one_token():
+        for layer in packed:
+            for wp, (n, k) in zip(layer, shapes):
+                codes, q, _ = qs[k]
+                ops.bitlinear_tl1_into(codes, q, wp, 0.0159, n, k, ys[n])
+
+    t = graph_time(torch, one_token, 5)
+    launches = len(packed) * len(shapes)
+    alg = sum(n * k // 4 + (k + 63) // 64 * 64 + n * 4 for n, k in shapes) * len(packed)
+    return {"kernel": "tl1_gemv_kernel", "launches_per_token": launches,
+            "mean_launch_us": t / launches * 1e6, "alg_bytes_per_launch": alg / launches,
+            "achieved_gbs": alg / t / 1e9}
+
+
+def head_roofline(torch, cfg, host):
+    """The int8 LM-head GEMV (engine path: fused greedy argmax) over the
+    model's 328 MB table. Algorithmic bytes = table + row scales + codes +
+    logits."""
+    from tenzo_amd import ops
+    V, H = cfg.vocab, cfg.hidden
+    wp = ops.i8_rows_repack(host["head"], V, H)
+    x = torch.randn(H, device="cuda")
+    codes, q = ops.actquant127(x)
+    logits = torch.empty(V, device="cuda")
+    idx = torch.empty(1, dtype=torch.int32, device="cuda")
+    t = graph_time(torch, lambda: ops.lm_head_i8_codes_into(codes, q, wp, host["hs"], V, H,
+                                                            logits, idx), 20)
+    alg = V * H + V * 4 + H + V * 4
+    return {"kernel": "lm_head_i8_kernel", "launches_per_token": 1, "mean_launch_us": t * 1e6,
+            "alg_bytes_per_launch": alg, "achieved_gbs": alg / t / 1e9}
+
+
+# ---------------------------------------------------------------- CPU leg
+
+def cpu_baseline(torch, cfg, host, ctx, seconds):
+    """The reference's own CPU engine (oracle/_ref/libtenzo_ref.so, compiled
+    from the reference sources with its flags) on the same weights and cache,
+    timed on a bounded sample of greedy decode steps at position ctx."""
+    import oracle
+    if not oracle.ref_available():
+        return {"value": None, "unit": "tok/s", "cores": 0, "kind": "reference",
+                "sample": "oracle/_ref not built on this host"}
+    from tenzo_amd import synth
+    R = oracle.ref()
+    P = oracle._ptr
+    L, Hkv = cfg.n_layers, cfg.n_kv_heads
+    layers = []
+    for tl1, scale, norms in host["layers"]:
+        lw = synth.LayerWeights({p: tl1[p].cpu().numpy() for p in synth.PROJ}, scale,
+                                norms["in_norm"], norms["attn_sub_norm"], norms["post_norm"],
+                                norms["ffn_sub_norm"])
+        layers.append(lw)
+    max_seq = ctx + 8
+    kc = np.zeros((L, Hkv, max_seq, 128), np.int8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((L, Hkv, max_seq), np.float32)
+    vs = np.zeros_like(ks)
+    kc[:, :, :ctx] = host["kc"].cpu().numpy()
+    vc[:, :, :ctx] = host["vc"].cpu().numpy()
+    ks[:, :, :ctx] = host["ks"].float().cpu().numpy()
+    vs[:, :, :ctx] = host["vs"].float().cpu().numpy()
+    sm = synth.SynthModel(synth.DecodeConfig(max_seq=max_seq), layers, host["final_norm"],
+                          host["head"].cpu().numpy(), host["hs"].cpu().numpy(), kc, vc, ks, vs,
+                          ctx)
+    e = R.ref_engine_create(cfg.hidden, cfg.n_q_heads, cfg.n_kv_heads, L, cfg.ffn, cfg.vocab,
+                            max_seq)
+    keep = [oracle.ref_layer_struct(sm, l) for l in range(L)]
+    for l, w in enumerate(keep):
+        R.ref_engine_set_layer(e, l, ctypes.byref(w))
+    R.ref_engine_set_head(e, P(sm.embed), P(sm.embed_scales), P(sm.final_norm), cfg.vocab,
+                          cfg.hidden)
+    times = []
+    tok = 1
+    t_end = time.perf_counter() + seconds
+    while len(times) < 2 or (time.perf_counter() < t_end and len(times) < 50):
+        R.ref_engine_set_kv(e, P(kc), P(vc), P(ks), P(vs), ctx)
+        t0 = time.perf_counter()
+        tok = R.ref_engine_step(e, tok, None)
+        times.append(time.perf_counter() - t0)
+    threads = R.ref_num_threads()
+    R.ref_engine_destroy(e)
+    med = float(np.median(times[1:] if len(times) > 2 else times))
+    return {"value": 1.0 / med, "unit": "tok/s", "cores": int(threads), "kind": "reference",
+            "sample": f"{len(times)} greedy decode steps at position {ctx} of the same model "
+                      f"(median {med * 1e3:.1f} ms/token; reference TenzoEngine.cpp compiled "
+                      f"with its own flags, OpenMP {threads} threads)"}
+
+
+# ------------------------------------------------------------------- main
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not implemented)"}))
+        sys.exit(2)
+    import torch
+    from tenzo_amd import synth
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU (the decode path has no CPU fallback)")
+    cfg = synth.BITNET_2B
+    ctx = args.ctx
+    e, host = build_model(torch, cfg, ctx)
+    e.use_graph(not args.eager)
+
+    tok = 1
+    for _ in range(args.warmup):
+        e.rewind(ctx)
+        tok = e.step(tok)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        e.rewind(ctx)
+        tok = e.step(tok)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms = dt / args.steps * 1e3
+    tok_s = args.steps / dt
+
+    step_bytes = cfg.step_bytes(ctx + 1)["total"]
+    step_gbs = step_bytes / (dt / args.steps) / 1e9
+
+    rl_tl1 = tl1_roofline(torch, cfg, host)
+    rl_head = head_roofline(torch, cfg, host)
+    # the dominant kernel: the larger share of the step
+    dom = max((rl_tl1, rl_head), key=lambda r: r["mean_launch_us"] * r["launches_per_token"])
+    roofline = {"bound": "hbm", "kernel": dom["kernel"],
+                "achieved": round(dom["achieved_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(dom["achieved_gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                "alg_bytes_per_launch": int(dom["alg_bytes_per_launch"]),
+                "mean_launch_us": round(dom["mean_launch_us"], 2)}
+    cpu = None if args.no_cpu else cpu_baseline(torch, cfg, host, ctx, args.cpu_seconds)
+
+    out = {
+        "metric": "decode tok/s BitNet-2B-shape bs=1 ctx 4k; GEMV+attn HBM GB/s % of peak",
+        "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8/ternary (int32 acc, fp32 out)",
+        "data": "synthetic (random-init BitNet-2B-shaped weights, N(0,1) KV prefill)",
+        "config": {"workload": "BitNet-b1.58-2B-shaped greedy decode step, batch 1, "
+                               f"context {ctx}, INT8 KV fp16 scales, int8 LM head",
+                   "layers": cfg.n_layers, "hidden": cfg.hidden, "ffn": cfg.ffn,
+                   "heads": [cfg.n_q_heads, cfg.n_kv_heads, 128], "vocab": cfg.vocab,
+                   "rope_theta": cfg.theta, "graph": not args.eager},
+        "step_hbm_bytes": step_bytes, "step_gbs": round(step_gbs, 1),
+        "step_frac_of_peak": round(step_gbs / PEAK_HBM_GBS, 4),
+        "roofline": roofline,
+        "kernels": {"tl1_gemv": {k: (round(v, 2) if isinstance(v, float) else v)
+                                 for k, v in rl_tl1.items()},
+                    "lm_head_i8": {k: (round(v, 2) if isinstance(v, float) else v)
+                                   for k, v in rl_head.items()}},
+        "cpu_baseline": cpu,
+    }
+    e.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

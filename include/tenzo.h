@@ -9,8 +9,13 @@
  *   - the decode step runs on the GPU whatever `device` says (this library
  *     has no CPU path); `kv_mode` must be "int8_fused" (or NULL);
  *   - weights are copied to device memory when they are set, so the caller may
- *     free its host copies afterwards (the reference keeps non-owning
- *     pointers to layer weights and the final norm);
+ *     free its copies afterwards (the reference keeps non-owning pointers to
+ *     layer weights and the final norm); the pointers may be host or device
+ *     memory;
+ *   - a null engine/weights pointer, a missing q/k/v/out matrix, a token
+ *     outside [0, vocab), a step on a full KV cache or a step before the
+ *     weights are set return an error (-1 from generate_step) instead of
+ *     the reference's undefined behaviour;
  *   - tenzo_create_engine returns NULL when no GPU is usable or the config is
  *     unsupported (the reference never returns NULL);
  *   - sampling with temperature > 0 is not provided yet: generate_step returns

@@ -149,6 +149,21 @@ TENZO_HIP_API int tenzo_hip_i8_rows_repack(const int8_t* w, void* w_packed, int6
 TENZO_HIP_API int tenzo_hip_lm_head_i8(const float* x, const float* norm_w, float eps,
                                        const void* w_packed, const float* scales,
                                        float* logits, int64_t V, int64_t H, void* stream);
+/* The activation quantization of compute_logits (TenzoEngine.cpp:1666-1678)
+ * for M rows of K values, after rms_norm_raw(x, norm_w, eps) when norm_w is
+ * non-null or do_norm is set: codes[m][k] = clamp(round(x * 127/absmax),
+ * -128, 127) (row stride K, K % 16 == 0), q[m] = {absmax/127, sum of codes}. */
+TENZO_HIP_API int tenzo_hip_rmsnorm_quant127(const float* x, const float* norm_w, int do_norm,
+                                             float eps, int64_t M, int64_t K, int8_t* codes,
+                                             tenzo_hip_actq_t* q, void* stream);
+/* The int8 GEMV of compute_logits (TenzoEngine.cpp:1689-1718) on codes from
+ * tenzo_hip_rmsnorm_quant127: logits[v] = float(sum codes * W[v]) *
+ * (q->inv_scale * scales[v]); when out_idx is non-null the same launch also
+ * writes the greedy argmax (first maximum, TenzoEngine.cpp:1745-1755). */
+TENZO_HIP_API int tenzo_hip_lm_head_i8_codes(const int8_t* codes, const tenzo_hip_actq_t* q,
+                                             const void* w_packed, const float* scales,
+                                             float* logits, int64_t V, int64_t H,
+                                             int32_t* out_idx, void* stream);
 /* Greedy branch of sample_top_k_top_p (TenzoEngine.cpp:1745-1755): index of
  * the first maximum, written to *out_idx (device int32). */
 TENZO_HIP_API int tenzo_hip_argmax(const float* logits, int64_t V, int32_t* out_idx,
@@ -182,12 +197,19 @@ TENZO_HIP_API int tenzo_hip_engine_set_kv(struct tenzo_engine_opaque* e, const i
 /* Reads back the cache (same layout, seq_len positions). */
 TENZO_HIP_API int tenzo_hip_engine_get_kv(struct tenzo_engine_opaque* e, int8_t* kc,
                                           int8_t* vc, uint16_t* ks, uint16_t* vs, int seq_len);
+/* Rewinds the sequence to seq_len <= the current length (positions past it
+ * are overwritten by the next steps), e.g. to roll back rejected tokens or to
+ * decode repeatedly at one position. No reference counterpart (the reference
+ * only resets to 0, TenzoEngine.cpp:1249-1255). */
+TENZO_HIP_API int tenzo_hip_engine_set_seq_len(struct tenzo_engine_opaque* e, int seq_len);
 /* RoPE theta (the reference hard-codes 10000; BitNet-2B uses 500000). */
 TENZO_HIP_API int tenzo_hip_engine_set_rope_theta(struct tenzo_engine_opaque* e, float theta);
 /* Copies the last step's logits (vocab fp32) to host memory. */
 TENZO_HIP_API int tenzo_hip_engine_get_logits(struct tenzo_engine_opaque* e, float* logits);
-/* Copies an engine buffer to host memory, by name: "x", "q", "k", "v",
- * "attn_out", "h1", "gate", "up", "act", "down" (last layer of the last step). */
+/* Copies an engine buffer to host memory, by name: "x" (hidden state),
+ * "qkv" (pre-RoPE q | k | v), "attn_out", "h1", "gate_up" (gate | up),
+ * "logits" - the last layer's values of the last step. n is the capacity of
+ * out in floats. */
 TENZO_HIP_API int tenzo_hip_engine_get_buffer(struct tenzo_engine_opaque* e, const char* name,
                                               float* out, int64_t n);
 /* Runs the decode step through a captured HIP graph (1, default) or eager

@@ -326,6 +326,31 @@ def q4_0_q8act(qa, w, K, N):
     return y
 
 
+class RefLayerWeights(ctypes.Structure):
+    """The reference's tenzo_layer_weights_t (include/tenzo.h:75-87)."""
+    _fields_ = [
+        ("q_w", _P), ("q_scale", _F), ("k_w", _P), ("k_scale", _F),
+        ("v_w", _P), ("v_scale", _F), ("out_w", _P), ("out_scale", _F),
+        ("gate_w", _P), ("gate_scale", _F), ("up_w", _P), ("up_scale", _F),
+        ("down_w", _P), ("down_scale", _F),
+        ("in_norm", _P), ("attn_sub_norm", _P), ("post_norm", _P), ("ffn_sub_norm", _P),
+    ]
+
+
+def ref_layer_struct(sm, l):
+    """tenzo_layer_weights_t of layer l of a tenzo_amd.synth.SynthModel (the
+    arrays must stay alive while the reference engine uses them)."""
+    lw = sm.layers[l]
+    w = RefLayerWeights()
+    for p, f in zip(("q", "k", "v", "o", "gate", "up", "down"),
+                    ("q", "k", "v", "out", "gate", "up", "down")):
+        setattr(w, f + "_w", _ptr(lw.tl1[p]).value)
+        setattr(w, f + "_scale", float(lw.scale[p]))
+    for f in ("in_norm", "attn_sub_norm", "post_norm", "ffn_sub_norm"):
+        setattr(w, f, _ptr(getattr(lw, f)).value)
+    return w
+
+
 class Model(ctypes.Structure):
     """Mirror of orc_model_t."""
     _fields_ = [

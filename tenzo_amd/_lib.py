@@ -39,11 +39,14 @@ SIGNATURES = {
     "tenzo_hip_i8_rows_repack": (_I, [_P, _P, _I64, _I64, _P]),
     "tenzo_hip_lm_head_i8": (_I, [_P, _P, _F, _P, _P, _P, _I64, _I64, _P]),
     "tenzo_hip_argmax": (_I, [_P, _I64, _P, _P]),
+    "tenzo_hip_rmsnorm_quant127": (_I, [_P, _P, _I, _F, _I64, _I64, _P, _P, _P]),
+    "tenzo_hip_lm_head_i8_codes": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     "tenzo_hip_embed_i8": (_I, [_P, _P, _P, _I64, _I64, _P, _P]),
     "tenzo_hip_execute_bitlinear_tl1": (_I, [_P, _P, _P, _SZ, _SZ, _SZ, _F]),
     "tenzo_hip_execute_rmsnorm": (_I, [_P, _P, _P, _SZ, _F]),
     "tenzo_hip_engine_set_kv": (_I, [_P, _P, _P, _P, _P, _I, _I]),
     "tenzo_hip_engine_get_kv": (_I, [_P, _P, _P, _P, _P, _I]),
+    "tenzo_hip_engine_set_seq_len": (_I, [_P, _I]),
     "tenzo_hip_engine_set_rope_theta": (_I, [_P, _F]),
     "tenzo_hip_engine_get_logits": (_I, [_P, _P]),
     "tenzo_hip_engine_get_buffer": (_I, [_P, _S, _P, _I64]),
@@ -51,6 +54,9 @@ SIGNATURES = {
     "tenzo_hip_engine_stream": (_P, [_P]),
     # include/tenzo.h
     "tenzo_get_version": (_S, []),
+    # struct returns: restype set by tenzo_amd.engine
+    "tenzo_default_config": (None, []),
+    "tenzo_default_sampling_params": (None, []),
     "tenzo_create_engine": (_P, [_P]),
     "tenzo_destroy_engine": (None, [_P]),
     "tenzo_reset": (None, [_P]),

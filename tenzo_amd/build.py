@@ -23,6 +23,8 @@ ARCH = os.environ.get("TENZO_OFFLOAD_ARCH", "gfx950")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-fvisibility=hidden",
+    # every rounding step is explicit: a*b+c is not fused unless written as fmaf
+    "-ffp-contract=off",
     # no packed-fp32 instructions (v_pk_{add,mul,fma}_f32) in device code
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-warning-option",

@@ -52,7 +52,8 @@ enum ScratchSlot {
     kScratchAttn = 1,      // attention partials
     kScratchAct = 2,       // quantized activations of the *_f32 entry points
     kScratchTmp = 3,
-    kScratchSlots = 4
+    kScratchHead = 4,      // argmax partials + counter
+    kScratchSlots = 5
 };
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -118,11 +119,16 @@ __device__ __forceinline__ int block256_sum_i32(int v, int* red) {
     return r;
 }
 
+// The library is compiled with -ffp-contract=off, so a*b+c is two rounded
+// operations unless written as __builtin_fmaf; HIP's default '/' and sqrtf
+// are correctly rounded (__fsqrt_rn is not: without
+// OCML_BASIC_ROUNDED_OPERATIONS it maps to the native approximation).
+
 // inv_rms of rms_norm_raw (TenzoEngine.cpp:154): 1 / sqrt(ss/dim + eps), each
 // operation correctly rounded.
 __device__ __forceinline__ float inv_rms_from_sumsq(float ss, int64_t dim, float eps) {
-    float mean = __fdiv_rn(ss, (float)dim);
-    return __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    const float mean = ss / (float)dim;
+    return 1.0f / sqrtf(mean + eps);
 }
 
 // y = x * inv_rms * w evaluated left to right (TenzoEngine.cpp:158).

@@ -1,0 +1,718 @@
+// The engine behind include/tenzo.h on an MI355X: the reference's
+// TenzoEngineImpl (src/runtime/TenzoEngine.h:195-262, TenzoEngine.cpp:1215-1838
+// and the C API at :2086-2204) with every stage of the decode step on the GPU.
+//
+// All state is device resident: TL1 weights in the GEMV layout (Q|K|V and
+// gate|up concatenated along rows so each pair is one launch), norm vectors,
+// the int8 LM head, the INT8 KV cache [L][Hkv][max_seq][128] with fp16
+// scales, a RoPE cos/sin table per position, and the activation buffers. One
+// decode step is
+//   embed ; per layer:
+//     actquant(in_norm)        -> codes           (rms_norm_raw + build_lut)
+//     TL1 GEMV Q|K|V           -> qkv             (:1547-1572)
+//     attention chunks+combine -> attn            (:1578, RoPE/append/softmax)
+//     actquant(attn_sub_norm)  -> codes           (:1582-1585)
+//     TL1 GEMV O + residual    -> h1 = x + o      (:1586-1590)
+//     actquant(post_norm)      -> codes           (:1594-1596)
+//     TL1 GEMV gate|up         -> gu              (:1598-1614)
+//     actquant(relu^2*up, ffn_sub_norm) -> codes  (:1616-1624)
+//     TL1 GEMV down + residual -> x = h1 + down   (:1625-1628)
+//   actquant(final_norm, +-127) ; LM head + fused greedy argmax (:1634-1755)
+// and is replayed from a captured HIP graph (position and token are read
+// from device memory, so one graph serves every position of a chunk size).
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "attention.h"
+#include "common.h"
+#include "lm_head.h"
+#include "tl1.h"
+
+using namespace tz;
+
+namespace {
+
+constexpr int kD = 128;
+
+struct DevLayer {
+    void* qkv = nullptr;   // TL1 GEMV layout, rows Q | K | V
+    void* o = nullptr;
+    void* gu = nullptr;    // rows gate | up
+    void* down = nullptr;
+    float sc[7] = {};      // q, k, v, o, gate, up, down
+    float* norm[4] = {};   // in, attn_sub, post, ffn_sub (null = no weight)
+    bool mlp = false;
+    bool set = false;
+};
+
+}  // namespace
+
+struct tenzo_engine_opaque {
+    tenzo_config_t cfg{};
+    std::string kv_mode, device;
+    int dev = 0;
+    hipStream_t st = nullptr;
+    int H = 0, Hq = 0, Hkv = 0, L = 0, F = 0, V = 0, max_seq = 0, qd = 0, kvd = 0;
+    float eps = 1e-5f;
+    float theta = 10000.0f;  // the reference hard-codes 10000 (TenzoEngine.cpp:456,466)
+
+    std::vector<DevLayer> layers;
+    std::vector<void*> allocs;  // everything to free at destroy
+    float* final_norm = nullptr;
+    int head_kind = 0;          // 0 none, 1 int8, 2 fp32
+    void* head_i8 = nullptr;
+    float* head_scales = nullptr;
+    float* head_f32 = nullptr;
+
+    int8_t* kc = nullptr;
+    int8_t* vc = nullptr;
+    uint16_t* ks = nullptr;
+    uint16_t* vs = nullptr;
+
+    float* x = nullptr;
+    float* qkv = nullptr;
+    float* attn = nullptr;
+    float* h1 = nullptr;
+    float* gu = nullptr;
+    float* xn = nullptr;
+    float* logits = nullptr;
+    int8_t* codes = nullptr;
+    tenzo_hip_actq_t* aq = nullptr;
+    void* gemv_ws = nullptr;
+    float* attn_part = nullptr;
+    void* am_ws = nullptr;
+    int32_t* io_dev = nullptr;   // [0] token, [1] position, [2] result token
+    int32_t* io_host = nullptr;  // pinned mirror
+    int32_t* pen_dev = nullptr;  // past tokens for the repetition penalty
+    int pen_cap = 0;
+    float* rope = nullptr;       // [max_seq][128]
+
+    int seq_len = 0;
+    bool use_graph = true;
+    std::map<std::pair<int, int>, hipGraphExec_t> graphs;  // (T, with head)
+
+};
+
+namespace {
+
+int alloc_tracked(tenzo_engine_t e, void** p, size_t bytes, bool zero) {
+    void* v = nullptr;
+    TZ_HIP(hipMalloc(&v, bytes < 256 ? 256 : bytes));
+    e->allocs.push_back(v);
+    if (zero) TZ_HIP(hipMemset(v, 0, bytes < 256 ? 256 : bytes));
+    *p = v;
+    return TENZO_SUCCESS;
+}
+
+template <typename T>
+int alloc_t(tenzo_engine_t e, T** p, size_t bytes, bool zero = false) {
+    void* v = nullptr;
+    int rc = alloc_tracked(e, &v, bytes, zero);
+    *p = static_cast<T*>(v);
+    return rc;
+}
+
+void drop_graphs(tenzo_engine_t e) {
+    for (auto& kv : e->graphs) (void)hipGraphExecDestroy(kv.second);
+    e->graphs.clear();
+}
+
+int upload_rope(tenzo_engine_t e) {
+    std::vector<float> cs((size_t)e->max_seq * kD);
+    tenzo_hip_rope_table(e->theta, kD, 0, e->max_seq, cs.data());
+    TZ_HIP(hipMemcpy(e->rope, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    return TENZO_SUCCESS;
+}
+
+// Uploads `rows` TL1 rows [N/64][K/2][32] and repacks them into `dst` at row
+// block offset `row0` (row0 % 64 == 0) of a matrix with K columns.
+int upload_tl1(tenzo_engine_t e, const int8_t* host, int64_t N, int64_t K, void* dst,
+               int64_t row0) {
+    void* staging = nullptr;
+    const size_t raw = (size_t)N * K / 4;
+    TZ_HIP(hipMalloc(&staging, raw));
+    int rc = TENZO_SUCCESS;
+    if (hipMemcpy(staging, host, raw, hipMemcpyDefault) != hipSuccess) {
+        set_error("set_layer_weights: copy to device failed");
+        rc = TENZO_ERROR_OUT_OF_MEMORY;
+    }
+    if (!rc) {
+        char* out = (char*)dst + (size_t)(row0 / 64) * ceil_div(K, 64) * 1024;
+        rc = launch_tl1_repack((const uint8_t*)staging, out, N, K, e->st);
+    }
+    if (hipStreamSynchronize(e->st) != hipSuccess && !rc) rc = TENZO_ERROR_UNSUPPORTED;
+    (void)hipFree(staging);
+    return rc;
+}
+
+int upload_vec(tenzo_engine_t e, const float* host, int64_t n, float** dst) {
+    if (!host) {
+        *dst = nullptr;
+        return TENZO_SUCCESS;
+    }
+    if (!*dst) {
+        int rc = alloc_t(e, dst, (size_t)n * 4);
+        if (rc) return rc;
+    }
+    TZ_HIP(hipMemcpy(*dst, host, (size_t)n * 4, hipMemcpyDefault));
+    return TENZO_SUCCESS;
+}
+
+bool ready(tenzo_engine_t e, bool need_head) {
+    for (int l = 0; l < e->L; ++l)
+        if (!e->layers[l].set) {
+            set_error("layer %d has no weights (tenzo_set_layer_weights)", l);
+            return false;
+        }
+    if (need_head && e->head_kind == 0) {
+        set_error("no LM head (tenzo_set_lm_head_i8 / _f32)");
+        return false;
+    }
+    if (e->head_kind == 0) {
+        set_error("no embedding table (the LM head is the tied embedding)");
+        return false;
+    }
+    return true;
+}
+
+__global__ void copy_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+// One layer (forward_layer_raw, TenzoEngine.cpp:1522-1632).
+int enqueue_layer(tenzo_engine_t e, int l, int T, int max_chunks) {
+    const DevLayer& w = e->layers[l];
+    hipStream_t st = e->st;
+    const int64_t KpH = ceil_div(e->H, 64) * 64;
+    int rc;
+    // 1-3: in-norm, activation quantization, fused Q|K|V
+    if ((rc = launch_actquant(1, 31, e->x, w.norm[0], e->eps, 1, e->H, KpH, e->codes, e->aq,
+                              nullptr, st)))
+        return rc;
+    RowScales rs{};
+    rs.n = 3;
+    rs.end[0] = e->qd;
+    rs.end[1] = e->qd + e->kvd;
+    rs.end[2] = INT64_MAX;
+    rs.scale[0] = w.sc[0];
+    rs.scale[1] = w.sc[1];
+    rs.scale[2] = w.sc[2];
+    if ((rc = launch_tl1_gemv(e->codes, e->aq, w.qkv, rs, 1, e->qd + 2 * e->kvd, e->H, e->qkv,
+                              nullptr, nullptr, st, 0, e->gemv_ws)))
+        return rc;
+    // 4: RoPE, INT8 append at the device-held position, attention
+    AttnLaunch a{};
+    a.q = e->qkv;
+    a.k_new = e->qkv + e->qd;
+    a.v_new = e->qkv + e->qd + e->kvd;
+    const size_t head_off = (size_t)l * e->Hkv * e->max_seq;
+    a.kc = e->kc + head_off * kD;
+    a.vc = e->vc + head_off * kD;
+    a.ks = e->ks + head_off;
+    a.vs = e->vs + head_off;
+    a.rope = e->rope;
+    a.rope_indexed = 1;
+    a.pos_dev = e->io_dev + 1;
+    a.B = 1;
+    a.Hq = e->Hq;
+    a.Hkv = e->Hkv;
+    a.max_seq = e->max_seq;
+    a.T = T;
+    a.max_chunks = max_chunks;
+    a.out = e->attn;
+    a.part = e->attn_part;
+    if ((rc = launch_attn(a, st))) return rc;
+    // 5-7: attn sub-norm, O projection, residual 1
+    if ((rc = launch_actquant(1, 31, e->attn, w.norm[1], e->eps, 1, e->H, KpH, e->codes, e->aq,
+                              nullptr, st)))
+        return rc;
+    if ((rc = launch_tl1_gemv(e->codes, e->aq, w.o, RowScales::single(w.sc[3]), 1, e->H, e->H,
+                              e->h1, e->x, nullptr, st, 0, e->gemv_ws)))
+        return rc;
+    if (!w.mlp) {  // :1629-1631
+        hipLaunchKernelGGL(copy_kernel, dim3((unsigned)ceil_div(e->H, 256)), dim3(256), 0, st,
+                           e->h1, e->x, (int64_t)e->H);
+        return launch_status("copy_kernel");
+    }
+    // 8: post-norm, fused gate|up, relu^2 * up, ffn sub-norm, down, residual 2
+    if ((rc = launch_actquant(1, 31, e->h1, w.norm[2], e->eps, 1, e->H, KpH, e->codes, e->aq,
+                              nullptr, st)))
+        return rc;
+    RowScales gs{};
+    gs.n = 2;
+    gs.end[0] = e->F;
+    gs.end[1] = INT64_MAX;
+    gs.scale[0] = w.sc[4];
+    gs.scale[1] = w.sc[5];
+    if ((rc = launch_tl1_gemv(e->codes, e->aq, w.gu, gs, 1, 2 * e->F, e->H, e->gu, nullptr,
+                              nullptr, st, 0, e->gemv_ws)))
+        return rc;
+    const int64_t KpF = ceil_div(e->F, 64) * 64;
+    if ((rc = launch_actquant(3, 31, e->gu, w.norm[3], e->eps, 1, e->F, KpF, e->codes, e->aq,
+                              nullptr, st)))
+        return rc;
+    return launch_tl1_gemv(e->codes, e->aq, w.down, RowScales::single(w.sc[6]), 1, e->H, e->F,
+                           e->x, e->h1, nullptr, st, 0, e->gemv_ws);
+}
+
+// compute_logits (:1634-1720) + the greedy branch of the sampler (:1745-1755).
+int enqueue_head(tenzo_engine_t e) {
+    hipStream_t st = e->st;
+    ArgmaxWs am = argmax_ws_at(e->am_ws, e->V, e->io_dev + 2);
+    int rc;
+    if (e->head_kind == 1) {
+        if ((rc = launch_actquant(1, 127, e->x, e->final_norm, e->eps, 1, e->H, e->H, e->codes,
+                                  e->aq, nullptr, st)))
+            return rc;
+        return launch_lm_head_i8(e->codes, e->aq, e->head_i8, e->head_scales, e->logits, e->V,
+                                 e->H, am, st);
+    }
+    if ((rc = launch_rmsnorm(e->x, e->final_norm, e->xn, e->H, e->eps, st))) return rc;
+    if ((rc = launch_lm_head_f32(e->xn, e->head_f32, e->logits, e->V, e->H, st))) return rc;
+    return launch_argmax(e->logits, e->V, am, st);
+}
+
+int enqueue_step(tenzo_engine_t e, bool head, int T, int max_chunks) {
+    int rc = e->head_kind == 1
+                 ? launch_embed_i8(e->head_i8, e->head_scales, e->io_dev, e->V, e->H, e->x, e->st)
+                 : launch_embed_f32(e->head_f32, e->io_dev, e->V, e->H, e->x, e->st);
+    if (rc) return rc;
+    for (int l = 0; l < e->L; ++l)
+        if ((rc = enqueue_layer(e, l, T, max_chunks))) return rc;
+    return head ? enqueue_head(e) : TENZO_SUCCESS;
+}
+
+// Runs one token through the layers (and the head) at position seq_len.
+int run_step(tenzo_engine_t e, int token, bool head) {
+    if (!ready(e, head)) return TENZO_ERROR_INVALID_ARGUMENT;
+    if (token < 0 || token >= e->V) {
+        set_error("token %d outside [0, %d)", token, e->V);
+        return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    if (e->seq_len >= e->max_seq) {
+        set_error("KV cache full (%d positions)", e->max_seq);
+        return TENZO_ERROR_OUT_OF_MEMORY;
+    }
+    TZ_HIP(hipSetDevice(e->dev));
+    const int pos = e->seq_len;
+    const int T = attn_pick_chunk(pos + 1, e->Hkv, 1);
+    e->io_host[0] = token;
+    e->io_host[1] = pos;
+    TZ_HIP(hipMemcpyAsync(e->io_dev, e->io_host, 8, hipMemcpyHostToDevice, e->st));
+    int rc;
+    if (e->use_graph) {
+        const int max_chunks = (int)ceil_div(e->max_seq, T);
+        auto key = std::make_pair(T, head ? 1 : 0);
+        auto it = e->graphs.find(key);
+        if (it == e->graphs.end()) {
+            hipGraph_t g = nullptr;
+            TZ_HIP(hipStreamBeginCapture(e->st, hipStreamCaptureModeThreadLocal));
+            rc = enqueue_step(e, head, T, max_chunks);
+            hipError_t ce = hipStreamEndCapture(e->st, &g);
+            if (rc) {
+                if (g) (void)hipGraphDestroy(g);
+                return rc;
+            }
+            if (ce != hipSuccess) return hip_fail(ce, "hipStreamEndCapture");
+            hipGraphExec_t ex = nullptr;
+            hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+            (void)hipGraphDestroy(g);
+            if (ie != hipSuccess) return hip_fail(ie, "hipGraphInstantiate");
+            it = e->graphs.emplace(key, ex).first;
+        }
+        TZ_HIP(hipGraphLaunch(it->second, e->st));
+    } else {
+        if ((rc = enqueue_step(e, head, T, (int)ceil_div(pos + 1, T)))) return rc;
+    }
+    return TENZO_SUCCESS;
+}
+
+}  // namespace
+
+extern "C" {
+
+TENZO_API const char* tenzo_get_version(void) { return TENZO_VERSION_STRING; }
+
+TENZO_API tenzo_config_t tenzo_default_config(void) {
+    // TenzoEngine.cpp:2092-2105
+    tenzo_config_t c;
+    c.hidden_size = 2560;
+    c.num_q_heads = 20;
+    c.num_kv_heads = 5;
+    c.head_dim = 128;
+    c.num_layers = 30;
+    c.ffn_dim = 6912;
+    c.vocab_size = 128256;
+    c.max_seq_len = 8192;
+    c.kv_mode = "int8_fused";
+    c.device = "rocm";
+    return c;
+}
+
+TENZO_API tenzo_sampling_params_t tenzo_default_sampling_params(void) {
+    // TenzoEngine.cpp:2107-2114
+    tenzo_sampling_params_t p;
+    p.temperature = 0.7f;
+    p.top_p = 0.9f;
+    p.top_k = 40;
+    p.repetition_penalty = 1.15f;
+    return p;
+}
+
+TENZO_API void tenzo_destroy_engine(tenzo_engine_t e);
+
+TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
+    tenzo_config_t c = config ? *config : tenzo_default_config();
+    const std::string kv = c.kv_mode ? c.kv_mode : "int8_fused";
+    if (kv != "int8_fused") {
+        set_error("kv_mode \"%s\" is not provided on the GPU (int8_fused only)", kv.c_str());
+        return nullptr;
+    }
+    const int H = c.hidden_size, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
+    if (c.head_dim != kD || H <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv ||
+        (Hq / Hkv != 1 && Hq / Hkv != 2 && Hq / Hkv != 4 && Hq / Hkv != 8) || Hq * kD != H ||
+        H % 64 || c.ffn_dim <= 0 || c.ffn_dim % 64 || c.num_layers <= 0 || c.vocab_size <= 0 ||
+        c.max_seq_len <= 0) {
+        set_error("unsupported config: need head_dim 128, hidden = q_heads*128, hidden and "
+                  "ffn multiples of 64, q_heads/kv_heads in {1,2,4,8}");
+        return nullptr;
+    }
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev == 0) {
+        set_error("no HIP device");
+        return nullptr;
+    }
+    auto* e = new tenzo_engine_opaque();
+    e->cfg = c;
+    e->kv_mode = kv;
+    e->device = c.device ? c.device : "rocm";
+    e->cfg.kv_mode = e->kv_mode.c_str();
+    e->cfg.device = e->device.c_str();
+    e->H = H;
+    e->Hq = Hq;
+    e->Hkv = Hkv;
+    e->L = c.num_layers;
+    e->F = c.ffn_dim;
+    e->V = c.vocab_size;
+    e->max_seq = c.max_seq_len;
+    e->qd = Hq * kD;
+    e->kvd = Hkv * kD;
+    e->layers.resize(e->L);
+    bool ok = hipGetDevice(&e->dev) == hipSuccess && hipStreamCreate(&e->st) == hipSuccess;
+    const size_t cache = (size_t)e->L * Hkv * e->max_seq;
+    const int Tmin = 32;
+    const size_t parts = (size_t)Hq * ceil_div(e->max_seq, Tmin) * kPartStride * 4;
+    const int64_t Fp = ceil_div(e->F, 64) * 64;
+    const size_t ws = tl1_ws_bytes(1, 2 * e->F > e->qd + 2 * e->kvd ? 2 * e->F
+                                                                    : e->qd + 2 * e->kvd);
+    ok = ok && !alloc_t(e, &e->kc, cache * kD, true) && !alloc_t(e, &e->vc, cache * kD, true) &&
+         !alloc_t(e, &e->ks, cache * 2, true) && !alloc_t(e, &e->vs, cache * 2, true) &&
+         !alloc_t(e, &e->x, (size_t)H * 4) && !alloc_t(e, &e->qkv, (size_t)(e->qd + 2 * e->kvd) * 4) &&
+         !alloc_t(e, &e->attn, (size_t)e->qd * 4) && !alloc_t(e, &e->h1, (size_t)H * 4) &&
+         !alloc_t(e, &e->gu, (size_t)2 * e->F * 4) && !alloc_t(e, &e->xn, (size_t)H * 4) &&
+         !alloc_t(e, &e->logits, (size_t)e->V * 4) &&
+         !alloc_t(e, &e->codes, (size_t)(Fp > H ? Fp : ceil_div(H, 64) * 64), true) &&
+         !alloc_t(e, &e->aq, 256) && !alloc_t(e, &e->gemv_ws, ws, true) &&
+         !alloc_t(e, &e->attn_part, parts) &&
+         !alloc_t(e, &e->am_ws, argmax_ws_bytes(e->V), true) &&
+         !alloc_t(e, &e->io_dev, 256, true) &&
+         !alloc_t(e, &e->rope, (size_t)e->max_seq * kD * 4);
+    if (ok) {
+        void* h = nullptr;
+        ok = hipHostMalloc(&h, 256, hipHostMallocDefault) == hipSuccess;
+        e->io_host = static_cast<int32_t*>(h);
+    }
+    ok = ok && !upload_rope(e);
+    if (!ok) {
+        tenzo_destroy_engine(e);
+        return nullptr;
+    }
+    return e;
+}
+
+TENZO_API void tenzo_destroy_engine(tenzo_engine_t e) {
+    if (!e) return;
+    (void)hipSetDevice(e->dev);
+    if (e->st) (void)hipStreamSynchronize(e->st);
+    drop_graphs(e);
+    for (void* p : e->allocs) (void)hipFree(p);
+    if (e->io_host) (void)hipHostFree(e->io_host);
+    if (e->st) (void)hipStreamDestroy(e->st);
+    delete e;
+}
+
+TENZO_API void tenzo_reset(tenzo_engine_t e) {
+    // TenzoEngine.cpp:1249-1255 / :213-215: only the sequence length
+    if (e) e->seq_len = 0;
+}
+
+TENZO_API int tenzo_get_seq_len(tenzo_engine_t e) { return e ? e->seq_len : 0; }
+
+TENZO_API tenzo_status_t tenzo_set_layer_weights(tenzo_engine_t e, int l,
+                                                 const tenzo_layer_weights_t* w) {
+    if (!e || !w) return TENZO_ERROR_INVALID_ARGUMENT;
+    if (l < 0 || l >= e->L) return TENZO_SUCCESS;  // ignored, as TenzoEngine.cpp:1258
+    if (!w->q_w || !w->k_w || !w->v_w || !w->out_w) {
+        set_error("set_layer_weights: q/k/v/out weights are required");
+        return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    if (hipSetDevice(e->dev) != hipSuccess) return TENZO_ERROR_UNSUPPORTED;
+    DevLayer& d = e->layers[l];
+    const int64_t H = e->H, F = e->F, qd = e->qd, kvd = e->kvd;
+    const int64_t KSH = ceil_div(H, 64), KSF = ceil_div(F, 64);
+    int rc = TENZO_SUCCESS;
+    if (!d.qkv) rc = alloc_tracked(e, &d.qkv, (size_t)((qd + 2 * kvd) / 64) * KSH * 1024, false);
+    if (!rc && !d.o) rc = alloc_tracked(e, &d.o, (size_t)(H / 64) * KSH * 1024, false);
+    if (!rc) rc = upload_tl1(e, w->q_w, qd, H, d.qkv, 0);
+    if (!rc) rc = upload_tl1(e, w->k_w, kvd, H, d.qkv, qd);
+    if (!rc) rc = upload_tl1(e, w->v_w, kvd, H, d.qkv, qd + kvd);
+    if (!rc) rc = upload_tl1(e, w->out_w, H, H, d.o, 0);
+    d.mlp = w->gate_w && w->up_w && w->down_w;
+    if (!rc && d.mlp) {
+        if (!d.gu) rc = alloc_tracked(e, &d.gu, (size_t)(2 * F / 64) * KSH * 1024, false);
+        if (!rc && !d.down) rc = alloc_tracked(e, &d.down, (size_t)(H / 64) * KSF * 1024, false);
+        if (!rc) rc = upload_tl1(e, w->gate_w, F, H, d.gu, 0);
+        if (!rc) rc = upload_tl1(e, w->up_w, F, H, d.gu, F);
+        if (!rc) rc = upload_tl1(e, w->down_w, H, F, d.down, 0);
+    }
+    const float* nv[4] = {w->in_norm, w->attn_sub_norm, w->post_norm, w->ffn_sub_norm};
+    const int64_t nd[4] = {H, H, H, F};
+    for (int i = 0; i < 4 && !rc; ++i) rc = upload_vec(e, nv[i], nd[i], &d.norm[i]);
+    if (rc) return (tenzo_status_t)rc;
+    const float sc[7] = {w->q_scale, w->k_scale, w->v_scale, w->out_scale,
+                         w->gate_scale, w->up_scale, w->down_scale};
+    std::memcpy(d.sc, sc, sizeof(sc));
+    d.set = true;
+    drop_graphs(e);  // scales are captured in the graph's kernel arguments
+    return TENZO_SUCCESS;
+}
+
+TENZO_API tenzo_status_t tenzo_set_final_norm(tenzo_engine_t e, const float* norm_w) {
+    if (!e || !norm_w) return TENZO_ERROR_INVALID_ARGUMENT;
+    if (hipSetDevice(e->dev) != hipSuccess) return TENZO_ERROR_UNSUPPORTED;
+    float* before = e->final_norm;
+    int rc = upload_vec(e, norm_w, e->H, &e->final_norm);
+    if (before != e->final_norm) drop_graphs(e);
+    return (tenzo_status_t)rc;
+}
+
+TENZO_API tenzo_status_t tenzo_set_lm_head_i8(tenzo_engine_t e, const int8_t* w,
+                                              const float* scales, int vocab, int hidden) {
+    if (!e || !w || !scales) return TENZO_ERROR_INVALID_ARGUMENT;
+    if (vocab != e->V || hidden != e->H) {
+        set_error("set_lm_head_i8: table %dx%d does not match the config %dx%d", vocab, hidden,
+                  e->V, e->H);
+        return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    if (hipSetDevice(e->dev) != hipSuccess) return TENZO_ERROR_UNSUPPORTED;
+    int rc = TENZO_SUCCESS;
+    if (!e->head_i8)
+        rc = alloc_tracked(e, &e->head_i8, tenzo_hip_i8_packed_bytes(e->V, e->H), false);
+    if (!rc && !e->head_scales) rc = alloc_t(e, &e->head_scales, (size_t)e->V * 4);
+    if (rc) return (tenzo_status_t)rc;
+    void* staging = nullptr;
+    const size_t bytes = (size_t)e->V * e->H;
+    if (hipMalloc(&staging, bytes) != hipSuccess) return TENZO_ERROR_OUT_OF_MEMORY;
+    bool ok = hipMemcpy(staging, w, bytes, hipMemcpyDefault) == hipSuccess &&
+              launch_i8_repack((const int8_t*)staging, e->head_i8, e->V, e->H, e->st) == 0 &&
+              hipStreamSynchronize(e->st) == hipSuccess &&
+              hipMemcpy(e->head_scales, scales, (size_t)e->V * 4, hipMemcpyDefault) ==
+                  hipSuccess;
+    (void)hipFree(staging);
+    if (!ok) return TENZO_ERROR_OUT_OF_MEMORY;
+    e->head_kind = 1;
+    drop_graphs(e);
+    return TENZO_SUCCESS;
+}
+
+TENZO_API tenzo_status_t tenzo_set_lm_head_f32(tenzo_engine_t e, const float* w, int vocab,
+                                               int hidden) {
+    if (!e || !w) return TENZO_ERROR_INVALID_ARGUMENT;
+    if (vocab != e->V || hidden != e->H) {
+        set_error("set_lm_head_f32: table %dx%d does not match the config %dx%d", vocab, hidden,
+                  e->V, e->H);
+        return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    if (hipSetDevice(e->dev) != hipSuccess) return TENZO_ERROR_UNSUPPORTED;
+    int rc = TENZO_SUCCESS;
+    if (!e->head_f32) rc = alloc_t(e, &e->head_f32, (size_t)e->V * e->H * 4);
+    if (rc) return (tenzo_status_t)rc;
+    if (hipMemcpy(e->head_f32, w, (size_t)e->V * e->H * 4, hipMemcpyDefault) != hipSuccess)
+        return TENZO_ERROR_OUT_OF_MEMORY;
+    e->head_kind = 2;
+    drop_graphs(e);
+    return TENZO_SUCCESS;
+}
+
+TENZO_API tenzo_status_t tenzo_load_model(tenzo_engine_t e, const char* weights_path,
+                                          const char* mlir_path) {
+    if (!e || !weights_path || !mlir_path) return TENZO_ERROR_INVALID_ARGUMENT;
+    set_error("tenzo_load_model: the weights.bin/model.mlir loader is not provided; install "
+              "weights with tenzo_set_layer_weights and tenzo_set_lm_head_i8");
+    return TENZO_ERROR_UNSUPPORTED;
+}
+
+TENZO_API tenzo_status_t tenzo_prefill_token(tenzo_engine_t e, int token) {
+    if (!e) return TENZO_ERROR_INVALID_ARGUMENT;
+    int rc = run_step(e, token, false);
+    if (rc) return (tenzo_status_t)rc;
+    if (hipStreamSynchronize(e->st) != hipSuccess) {
+        set_error("prefill_token: %s", hipGetErrorString(hipGetLastError()));
+        return TENZO_ERROR_UNSUPPORTED;
+    }
+    e->seq_len += 1;  // :1816-1818
+    return TENZO_SUCCESS;
+}
+
+TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,
+                                  const tenzo_sampling_params_t* params, const int* past,
+                                  int past_len) {
+    if (!e) return -1;
+    const float temperature = params ? params->temperature : 0.7f;
+    const float penalty = params ? params->repetition_penalty : 1.15f;
+    if (temperature > 0.0f) {
+        set_error("generate_step: sampling with temperature > 0 is not provided (greedy only)");
+        return -1;
+    }
+    if (run_step(e, cur_token, true)) return -1;
+    if (penalty != 1.0f && past && past_len > 0) {
+        // :1735-1743 on the device, then the greedy argmax again
+        hipStream_t st = e->st;
+        if (past_len > e->pen_cap) {
+            if (e->pen_dev) {
+                (void)hipStreamSynchronize(st);
+                (void)hipFree(e->pen_dev);
+            }
+            if (hipMalloc(&e->pen_dev, (size_t)past_len * 4) != hipSuccess) {
+                e->pen_dev = nullptr;
+                e->pen_cap = 0;
+                set_error("generate_step: out of memory for past tokens");
+                return -1;
+            }
+            e->pen_cap = past_len;
+        }
+        ArgmaxWs am = argmax_ws_at(e->am_ws, e->V, e->io_dev + 2);
+        if (hipMemcpyAsync(e->pen_dev, past, (size_t)past_len * 4, hipMemcpyHostToDevice, st) !=
+                hipSuccess ||
+            launch_rep_penalty(e->logits, e->V, e->pen_dev, past_len, penalty, st) ||
+            launch_argmax(e->logits, e->V, am, st))
+            return -1;
+    }
+    if (hipMemcpyAsync(e->io_host + 2, e->io_dev + 2, 4, hipMemcpyDeviceToHost, e->st) !=
+            hipSuccess ||
+        hipStreamSynchronize(e->st) != hipSuccess) {
+        set_error("generate_step: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
+    e->seq_len += 1;  // :1833-1835
+    return e->io_host[2];
+}
+
+// ---- engine extensions (include/tenzo_hip.h) ----
+
+TENZO_HIP_API int tenzo_hip_engine_set_kv(tenzo_engine_t e, const int8_t* kc, const int8_t* vc,
+                                          const uint16_t* ks, const uint16_t* vs, int seq_len,
+                                          int is_device) {
+    TZ_CHECK(e && kc && vc && ks && vs, "engine_set_kv: null pointer");
+    TZ_CHECK(seq_len >= 0 && seq_len <= e->max_seq, "engine_set_kv: seq_len %d outside [0, %d]",
+             seq_len, e->max_seq);
+    TZ_HIP(hipSetDevice(e->dev));
+    if (seq_len > 0) {
+        const hipMemcpyKind k = is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+        const size_t rows = (size_t)e->L * e->Hkv;
+        TZ_HIP(hipMemcpy2DAsync(e->kc, (size_t)e->max_seq * kD, kc, (size_t)seq_len * kD,
+                                (size_t)seq_len * kD, rows, k, e->st));
+        TZ_HIP(hipMemcpy2DAsync(e->vc, (size_t)e->max_seq * kD, vc, (size_t)seq_len * kD,
+                                (size_t)seq_len * kD, rows, k, e->st));
+        TZ_HIP(hipMemcpy2DAsync(e->ks, (size_t)e->max_seq * 2, ks, (size_t)seq_len * 2,
+                                (size_t)seq_len * 2, rows, k, e->st));
+        TZ_HIP(hipMemcpy2DAsync(e->vs, (size_t)e->max_seq * 2, vs, (size_t)seq_len * 2,
+                                (size_t)seq_len * 2, rows, k, e->st));
+        TZ_HIP(hipStreamSynchronize(e->st));
+    }
+    e->seq_len = seq_len;
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_get_kv(tenzo_engine_t e, int8_t* kc, int8_t* vc, uint16_t* ks,
+                                          uint16_t* vs, int seq_len) {
+    TZ_CHECK(e && kc && vc && ks && vs, "engine_get_kv: null pointer");
+    TZ_CHECK(seq_len > 0 && seq_len <= e->max_seq, "engine_get_kv: bad seq_len %d", seq_len);
+    TZ_HIP(hipSetDevice(e->dev));
+    const size_t rows = (size_t)e->L * e->Hkv;
+    TZ_HIP(hipStreamSynchronize(e->st));
+    TZ_HIP(hipMemcpy2D(kc, (size_t)seq_len * kD, e->kc, (size_t)e->max_seq * kD,
+                       (size_t)seq_len * kD, rows, hipMemcpyDeviceToHost));
+    TZ_HIP(hipMemcpy2D(vc, (size_t)seq_len * kD, e->vc, (size_t)e->max_seq * kD,
+                       (size_t)seq_len * kD, rows, hipMemcpyDeviceToHost));
+    TZ_HIP(hipMemcpy2D(ks, (size_t)seq_len * 2, e->ks, (size_t)e->max_seq * 2,
+                       (size_t)seq_len * 2, rows, hipMemcpyDeviceToHost));
+    TZ_HIP(hipMemcpy2D(vs, (size_t)seq_len * 2, e->vs, (size_t)e->max_seq * 2,
+                       (size_t)seq_len * 2, rows, hipMemcpyDeviceToHost));
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_set_seq_len(tenzo_engine_t e, int seq_len) {
+    TZ_CHECK(e, "engine_set_seq_len: null engine");
+    TZ_CHECK(seq_len >= 0 && seq_len <= e->seq_len,
+             "engine_set_seq_len: %d outside [0, %d] (only rewinding is allowed)", seq_len,
+             e->seq_len);
+    e->seq_len = seq_len;
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_set_rope_theta(tenzo_engine_t e, float theta) {
+    TZ_CHECK(e && theta > 0.0f, "engine_set_rope_theta: bad arguments");
+    TZ_HIP(hipSetDevice(e->dev));
+    TZ_HIP(hipStreamSynchronize(e->st));
+    e->theta = theta;
+    return upload_rope(e);
+}
+
+TENZO_HIP_API int tenzo_hip_engine_get_logits(tenzo_engine_t e, float* logits) {
+    TZ_CHECK(e && logits, "engine_get_logits: null pointer");
+    TZ_HIP(hipSetDevice(e->dev));
+    TZ_HIP(hipStreamSynchronize(e->st));
+    TZ_HIP(hipMemcpy(logits, e->logits, (size_t)e->V * 4, hipMemcpyDeviceToHost));
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_get_buffer(tenzo_engine_t e, const char* name, float* out,
+                                              int64_t n) {
+    TZ_CHECK(e && name && out, "engine_get_buffer: null pointer");
+    struct B {
+        const char* n;
+        const float* p;
+        int64_t len;
+    } bufs[] = {{"x", e->x, e->H},
+                {"qkv", e->qkv, e->qd + 2 * e->kvd},
+                {"attn_out", e->attn, e->qd},
+                {"h1", e->h1, e->H},
+                {"gate_up", e->gu, 2 * (int64_t)e->F},
+                {"logits", e->logits, e->V}};
+    for (const B& b : bufs) {
+        if (std::strcmp(b.n, name) == 0) {
+            TZ_CHECK(n >= b.len, "engine_get_buffer: %s needs %lld floats", name,
+                     (long long)b.len);
+            TZ_HIP(hipSetDevice(e->dev));
+            TZ_HIP(hipStreamSynchronize(e->st));
+            TZ_HIP(hipMemcpy(out, b.p, (size_t)b.len * 4, hipMemcpyDeviceToHost));
+            return TENZO_SUCCESS;
+        }
+    }
+    set_error("engine_get_buffer: unknown buffer \"%s\"", name);
+    return TENZO_ERROR_INVALID_ARGUMENT;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_use_graph(tenzo_engine_t e, int on) {
+    TZ_CHECK(e, "engine_use_graph: null engine");
+    e->use_graph = on != 0;
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API void* tenzo_hip_engine_stream(tenzo_engine_t e) { return e ? e->st : nullptr; }
+
+}  // extern "C"

@@ -1,0 +1,404 @@
+// int8 LM head, greedy argmax and embedding lookup on gfx950
+// (reference src/runtime/TenzoEngine.cpp:1294-1316 embedding_lookup,
+// :1634-1720 compute_logits, :1735-1755 repetition penalty + greedy branch of
+// sample_top_k_top_p).
+//
+// Device layout of the int8 [V][H] table: for row block b (64 rows) and
+// column chunk c (16 columns) there are 64 x 16 bytes, row r's 16 bytes at
+// offset r*16. A wave reads one chunk of its row block as 1 KiB contiguous
+// (lane = row) and takes the matching 16 activation codes as 4 wave-uniform
+// dwords, so each lane issues four v_dot4_i32_i8 per 16-byte load. Rows past
+// V are zero.
+#include "lm_head.h"
+#include "tl1.h"
+
+namespace tz {
+
+// ------------------------------------------------------------------ repack --
+
+__global__ void i8_repack_kernel(const int8_t* __restrict__ src, uint32_t* __restrict__ dst,
+                                 int64_t V, int64_t H, int64_t nb) {
+    // one dword of the packed layout per thread
+    const int64_t HC = H / 16;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nb * HC * 256) return;
+    const int q = (int)(idx & 3);
+    const int r = (int)((idx >> 2) & 63);
+    const int64_t bc = idx >> 8;
+    const int64_t c = bc % HC;
+    const int64_t b = bc / HC;
+    const int64_t row = b * 64 + r;
+    uint32_t v = 0;
+    if (row < V) {
+        const uint8_t* p = reinterpret_cast<const uint8_t*>(src) + row * H + c * 16 + q * 4;
+        v = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) |
+            ((uint32_t)p[3] << 24);
+    }
+    dst[idx] = v;
+}
+
+// ------------------------------------------------------------------ argmax --
+
+// First maximum: the larger value wins, equal values go to the smaller index
+// (the sequential scan at :1745-1755 keeps the first of equal maxima).
+__device__ __forceinline__ void am_combine(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const float ov = __shfl_xor(v, o, kWave);
+        const int oi = __shfl_xor(i, o, kWave);
+        am_combine(v, i, ov, oi);
+    }
+}
+
+// Called by every thread of a 256-thread block once the block's partial is in
+// am.part[blockIdx.x]. The last block to arrive reduces all nparts partials
+// into *am.out_idx and re-arms the counter.
+__device__ void argmax_finish(const ArgmaxWs& am, int nparts) {
+    __shared__ int is_last;
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicAdd(am.counter, 1u) == (unsigned)(nparts - 1);
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    float v = -INFINITY;
+    int i = INT_MAX;
+    for (int p = threadIdx.x; p < nparts; p += 256) {
+        const float pv = __hip_atomic_load(&am.part[p].x, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        const float pi = __hip_atomic_load(&am.part[p].y, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+        am_combine(v, i, pv, __float_as_int(pi));
+    }
+    wave_argmax(v, i);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        rv[wave] = v;
+        ri[wave] = i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) am_combine(rv[0], ri[0], rv[w], ri[w]);
+        *am.out_idx = ri[0];
+        atomicExch(am.counter, 0u);
+    }
+}
+
+constexpr int kArgmaxPerBlock = 4096;
+
+__global__ void __launch_bounds__(256)
+argmax_kernel(const float* __restrict__ logits, int64_t V, ArgmaxWs am) {
+    const int64_t base = (int64_t)blockIdx.x * kArgmaxPerBlock;
+    const int64_t end = base + kArgmaxPerBlock < V ? base + kArgmaxPerBlock : V;
+    float v = -INFINITY;
+    int i = INT_MAX;
+    for (int64_t k = base + threadIdx.x; k < end; k += 256) am_combine(v, i, logits[k], (int)k);
+    wave_argmax(v, i);
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        rv[wave] = v;
+        ri[wave] = i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) am_combine(rv[0], ri[0], rv[w], ri[w]);
+        am.part[blockIdx.x] = make_float2(rv[0], __int_as_float(ri[0]));
+    }
+    argmax_finish(am, (int)gridDim.x);
+}
+
+// ----------------------------------------------------------------- LM head --
+
+// One block per 64-row block; its 4 waves split the H/16 chunks and reduce
+// through LDS. int32 sums are exact; logit = float(acc) * (s_x * s_v) (:1718).
+__global__ void __launch_bounds__(256)
+lm_head_i8_kernel(const uint4* __restrict__ w, const int32_t* __restrict__ codes,
+                  const tenzo_hip_actq_t* __restrict__ aq, const float* __restrict__ scales,
+                  float* __restrict__ logits, int64_t V, int64_t HC, ArgmaxWs am) {
+    __shared__ int red[4][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t b = blockIdx.x;
+    const uint4* wb = w + b * HC * 64 + lane;
+    int acc0 = 0, acc1 = 0;
+    int64_t c = wave;
+    for (; c + 12 < HC; c += 16) {
+        const uint4 v0 = wb[c * 64];
+        const uint4 v1 = wb[(c + 4) * 64];
+        const uint4 v2 = wb[(c + 8) * 64];
+        const uint4 v3 = wb[(c + 12) * 64];
+        const int32_t* a0 = codes + c * 4;
+        acc0 = sdot4(v0.x, a0[0], acc0);
+        acc0 = sdot4(v0.y, a0[1], acc0);
+        acc0 = sdot4(v0.z, a0[2], acc0);
+        acc0 = sdot4(v0.w, a0[3], acc0);
+        acc1 = sdot4(v1.x, a0[16], acc1);
+        acc1 = sdot4(v1.y, a0[17], acc1);
+        acc1 = sdot4(v1.z, a0[18], acc1);
+        acc1 = sdot4(v1.w, a0[19], acc1);
+        acc0 = sdot4(v2.x, a0[32], acc0);
+        acc0 = sdot4(v2.y, a0[33], acc0);
+        acc0 = sdot4(v2.z, a0[34], acc0);
+        acc0 = sdot4(v2.w, a0[35], acc0);
+        acc1 = sdot4(v3.x, a0[48], acc1);
+        acc1 = sdot4(v3.y, a0[49], acc1);
+        acc1 = sdot4(v3.z, a0[50], acc1);
+        acc1 = sdot4(v3.w, a0[51], acc1);
+    }
+    for (; c < HC; c += 4) {
+        const uint4 v0 = wb[c * 64];
+        const int32_t* a0 = codes + c * 4;
+        acc0 = sdot4(v0.x, a0[0], acc0);
+        acc0 = sdot4(v0.y, a0[1], acc0);
+        acc0 = sdot4(v0.z, a0[2], acc0);
+        acc0 = sdot4(v0.w, a0[3], acc0);
+    }
+    red[wave][lane] = acc0 + acc1;
+    __syncthreads();
+    if (wave == 0) {
+        const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+        const int64_t row = b * 64 + lane;
+        float val = -INFINITY;
+        if (row < V) {
+            val = (float)tot * __fmul_rn(aq->inv_scale, scales[row]);
+            logits[row] = val;
+        }
+        if (am.out_idx) {
+            int idx = (int)row;
+            wave_argmax(val, idx);
+            if (lane == 0) am.part[b] = make_float2(val, __int_as_float(idx));
+        }
+    }
+    if (am.out_idx) argmax_finish(am, (int)gridDim.x);
+}
+
+// fp32 table: one wave per row, float4 loads along H, fp32 FMA and a wave sum.
+__global__ void __launch_bounds__(256)
+lm_head_f32_kernel(const float* __restrict__ xn, const float* __restrict__ E,
+                   float* __restrict__ logits, int64_t V, int64_t H) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= V) return;
+    const float* er = E + row * H;
+    float s = 0.0f;
+    if ((H & 3) == 0) {
+        const float4* e4 = reinterpret_cast<const float4*>(er);
+        const float4* x4 = reinterpret_cast<const float4*>(xn);
+        for (int64_t i = lane; i < H / 4; i += 64) {
+            const float4 e = e4[i], x = x4[i];
+            s = __builtin_fmaf(x.x, e.x, s);
+            s = __builtin_fmaf(x.y, e.y, s);
+            s = __builtin_fmaf(x.z, e.z, s);
+            s = __builtin_fmaf(x.w, e.w, s);
+        }
+    } else {
+        for (int64_t i = lane; i < H; i += 64) s = __builtin_fmaf(xn[i], er[i], s);
+    }
+    s = wave_sum_tree(s);
+    if (lane == 0) logits[row] = s;
+}
+
+// --------------------------------------------------------------- embedding --
+
+__global__ void embed_i8_kernel(const uint8_t* __restrict__ w, const float* __restrict__ scales,
+                                const int32_t* __restrict__ token_dev, int64_t V, int64_t H,
+                                float* __restrict__ x) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H) return;
+    const int tok = *token_dev;
+    if (tok < 0 || (int64_t)tok >= V) {
+        x[i] = 0.0f;
+        return;
+    }
+    const int64_t b = tok >> 6, r = tok & 63, c = i >> 4;
+    const int8_t e = (int8_t)w[((b * (H / 16) + c) * 64 + r) * 16 + (i & 15)];
+    x[i] = __fmul_rn((float)e, scales[tok]);  // :1300-1315
+}
+
+__global__ void embed_f32_kernel(const float* __restrict__ E, const int32_t* __restrict__ token_dev,
+                                 int64_t V, int64_t H, float* __restrict__ x) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H) return;
+    const int tok = *token_dev;
+    x[i] = (tok < 0 || (int64_t)tok >= V) ? 0.0f : E[(int64_t)tok * H + i];
+}
+
+// :1735-1743, sequential so that repeated tokens compound as in the reference.
+__global__ void rep_penalty_kernel(float* __restrict__ logits, int64_t V,
+                                   const int32_t* __restrict__ tokens, int n, float penalty) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    for (int k = 0; k < n; ++k) {
+        const int t = tokens[k];
+        if (t >= 0 && (int64_t)t < V) {
+            const float l = logits[t];
+            logits[t] = l > 0.0f ? __fdiv_rn(l, penalty) : __fmul_rn(l, penalty);
+        }
+    }
+}
+
+// -------------------------------------------------------------------- host --
+
+static int64_t head_blocks(int64_t V) { return ceil_div(V, 64); }
+static int64_t argmax_blocks(int64_t V) { return ceil_div(V, kArgmaxPerBlock); }
+
+// Workspace: the counter at offset 0 (the same place whatever V is, so a
+// region reused across calls of different V keeps a zero counter), then the
+// partials from offset 256.
+size_t argmax_ws_bytes(int64_t V) {
+    int64_t n = head_blocks(V);
+    if (argmax_blocks(V) > n) n = argmax_blocks(V);
+    return 256 + (size_t)ceil_div(n * 8, 256) * 256;
+}
+
+ArgmaxWs argmax_ws_at(void* base, int64_t V, int32_t* out_idx) {
+    (void)V;
+    ArgmaxWs am;
+    am.counter = reinterpret_cast<uint32_t*>(base);
+    am.part = reinterpret_cast<float2*>(reinterpret_cast<char*>(base) + 256);
+    am.out_idx = out_idx;
+    return am;
+}
+
+int launch_i8_repack(const int8_t* w, void* w_packed, int64_t V, int64_t H, hipStream_t st) {
+    const int64_t nb = head_blocks(V);
+    const int64_t total = nb * (H / 16) * 256;
+    hipLaunchKernelGGL(i8_repack_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0, st,
+                       w, (uint32_t*)w_packed, V, H, nb);
+    return launch_status("i8_repack_kernel");
+}
+
+int launch_lm_head_i8(const int8_t* codes, const tenzo_hip_actq_t* aq, const void* w_packed,
+                      const float* scales, float* logits, int64_t V, int64_t H,
+                      const ArgmaxWs& am, hipStream_t st) {
+    hipLaunchKernelGGL(lm_head_i8_kernel, dim3((unsigned)head_blocks(V)), dim3(256), 0, st,
+                       (const uint4*)w_packed, (const int32_t*)codes, aq, scales, logits, V,
+                       H / 16, am);
+    return launch_status("lm_head_i8_kernel");
+}
+
+int launch_lm_head_f32(const float* xn, const float* E, float* logits, int64_t V, int64_t H,
+                       hipStream_t st) {
+    hipLaunchKernelGGL(lm_head_f32_kernel, dim3((unsigned)ceil_div(V, 4)), dim3(256), 0, st, xn,
+                       E, logits, V, H);
+    return launch_status("lm_head_f32_kernel");
+}
+
+int launch_argmax(const float* logits, int64_t V, const ArgmaxWs& am, hipStream_t st) {
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)argmax_blocks(V)), dim3(256), 0, st, logits,
+                       V, am);
+    return launch_status("argmax_kernel");
+}
+
+int launch_embed_i8(const void* w_packed, const float* scales, const int32_t* token_dev,
+                    int64_t V, int64_t H, float* x, hipStream_t st) {
+    hipLaunchKernelGGL(embed_i8_kernel, dim3((unsigned)ceil_div(H, 256)), dim3(256), 0, st,
+                       (const uint8_t*)w_packed, scales, token_dev, V, H, x);
+    return launch_status("embed_i8_kernel");
+}
+
+int launch_embed_f32(const float* E, const int32_t* token_dev, int64_t V, int64_t H, float* x,
+                     hipStream_t st) {
+    hipLaunchKernelGGL(embed_f32_kernel, dim3((unsigned)ceil_div(H, 256)), dim3(256), 0, st, E,
+                       token_dev, V, H, x);
+    return launch_status("embed_f32_kernel");
+}
+
+int launch_rep_penalty(float* logits, int64_t V, const int32_t* tokens, int n, float penalty,
+                       hipStream_t st) {
+    hipLaunchKernelGGL(rep_penalty_kernel, dim3(1), dim3(64), 0, st, logits, V, tokens, n,
+                       penalty);
+    return launch_status("rep_penalty_kernel");
+}
+
+}  // namespace tz
+
+using namespace tz;
+
+extern "C" {
+
+TENZO_HIP_API size_t tenzo_hip_i8_packed_bytes(int64_t V, int64_t H) {
+    return (size_t)ceil_div(V, 64) * (size_t)(H / 16) * 1024;
+}
+
+TENZO_HIP_API int tenzo_hip_i8_rows_repack(const int8_t* w, void* w_packed, int64_t V,
+                                           int64_t H, void* stream) {
+    TZ_CHECK(w && w_packed, "i8_rows_repack: null pointer");
+    TZ_CHECK(V > 0 && H > 0 && H % 16 == 0, "i8_rows_repack: need H %% 16 == 0 (H=%lld)",
+             (long long)H);
+    return launch_i8_repack(w, w_packed, V, H, (hipStream_t)stream);
+}
+
+TENZO_HIP_API int tenzo_hip_lm_head_i8(const float* x, const float* norm_w, float eps,
+                                       const void* w_packed, const float* scales,
+                                       float* logits, int64_t V, int64_t H, void* stream) {
+    TZ_CHECK(x && w_packed && scales && logits, "lm_head_i8: null pointer");
+    TZ_CHECK(V > 0 && V <= INT32_MAX && H > 0 && H % 16 == 0,
+             "lm_head_i8: need H %% 16 == 0 (H=%lld)", (long long)H);
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)Scratch::get(kScratchAct, (size_t)H + 256, st);
+    if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+    tenzo_hip_actq_t* q = (tenzo_hip_actq_t*)ws;
+    int8_t* codes = (int8_t*)(ws + 256);
+    // final rms_norm_raw (:1638) then the int8 activation quantization (:1666-1678)
+    int rc = launch_actquant(1, 127, x, norm_w, eps, 1, H, H, codes, q, nullptr, st);
+    if (rc) return rc;
+    return launch_lm_head_i8(codes, q, w_packed, scales, logits, V, H, ArgmaxWs{}, st);
+}
+
+TENZO_HIP_API int tenzo_hip_rmsnorm_quant127(const float* x, const float* norm_w, int do_norm,
+                                             float eps, int64_t M, int64_t K, int8_t* codes,
+                                             tenzo_hip_actq_t* q, void* stream) {
+    TZ_CHECK(x && codes && q, "rmsnorm_quant127: null pointer");
+    TZ_CHECK(M > 0 && M <= 65535 && K > 0 && K % 16 == 0,
+             "rmsnorm_quant127: need K %% 16 == 0 (K=%lld)", (long long)K);
+    return launch_actquant(do_norm || norm_w ? 1 : 0, 127, x, norm_w, eps, M, K, K, codes, q,
+                           nullptr, (hipStream_t)stream);
+}
+
+TENZO_HIP_API int tenzo_hip_lm_head_i8_codes(const int8_t* codes, const tenzo_hip_actq_t* q,
+                                             const void* w_packed, const float* scales,
+                                             float* logits, int64_t V, int64_t H,
+                                             int32_t* out_idx, void* stream) {
+    TZ_CHECK(codes && q && w_packed && scales && logits, "lm_head_i8_codes: null pointer");
+    TZ_CHECK(V > 0 && V <= INT32_MAX && H > 0 && H % 16 == 0,
+             "lm_head_i8_codes: need H %% 16 == 0 (H=%lld)", (long long)H);
+    TZ_CHECK(((uintptr_t)codes & 3) == 0, "lm_head_i8_codes: codes must be 4-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    ArgmaxWs am{};
+    if (out_idx) {
+        void* ws = Scratch::get(kScratchHead, argmax_ws_bytes(V), st);
+        if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+        am = argmax_ws_at(ws, V, out_idx);
+    }
+    return launch_lm_head_i8(codes, q, w_packed, scales, logits, V, H, am, st);
+}
+
+TENZO_HIP_API int tenzo_hip_argmax(const float* logits, int64_t V, int32_t* out_idx,
+                                   void* stream) {
+    TZ_CHECK(logits && out_idx && V > 0 && V <= INT32_MAX, "argmax: bad arguments");
+    hipStream_t st = (hipStream_t)stream;
+    void* ws = Scratch::get(kScratchHead, argmax_ws_bytes(V), st);
+    if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+    return launch_argmax(logits, V, argmax_ws_at(ws, V, out_idx), st);
+}
+
+TENZO_HIP_API int tenzo_hip_embed_i8(const void* w_packed, const float* scales,
+                                     const int32_t* token_dev, int64_t V, int64_t H, float* x,
+                                     void* stream) {
+    TZ_CHECK(w_packed && scales && token_dev && x, "embed_i8: null pointer");
+    TZ_CHECK(V > 0 && H > 0 && H % 16 == 0, "embed_i8: need H %% 16 == 0");
+    return launch_embed_i8(w_packed, scales, token_dev, V, H, x, (hipStream_t)stream);
+}
+
+}  // extern "C"

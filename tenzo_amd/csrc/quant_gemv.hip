@@ -281,11 +281,14 @@ static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
     float* part = nullptr;
     uint32_t* cnt = nullptr;
     if (splits > 1) {
-        const size_t bytes = (size_t)splits * B * N * 4 + (size_t)tiles * 4;
+        // counters first, at a fixed offset: they are left at zero, while the
+        // partials behind them are not cleared between calls
+        const size_t cnt_bytes = (size_t)ceil_div((int64_t)tiles * 4, 256) * 256;
+        const size_t bytes = cnt_bytes + (size_t)splits * B * N * 4;
         char* ws = (char*)Scratch::get(kScratchTmp, bytes, st);
         if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
-        part = (float*)ws;
-        cnt = (uint32_t*)(ws + (size_t)splits * B * N * 4);
+        cnt = (uint32_t*)ws;
+        part = (float*)(ws + cnt_bytes);
     }
     const size_t smem = (size_t)B * KC * 4;
     if (smem > 64 * 1024) {

@@ -51,48 +51,84 @@ __global__ void tl1_repack_kernel(const uint8_t* __restrict__ src, uint32_t* __r
 }
 
 // ------------------------------------------------------------------------
-// Activation quantization (build_lut, :28-42), one 256-thread block per token.
+// Activation quantization, one 256-thread block per token.
+//   QMAX 31  : build_lut (:28-42): amax floor 1e-6, code = round(v * (31/amax)),
+//              inv_scale = amax * (1/31) (the reference build folds the divide).
+//   QMAX 127 : compute_logits (:1666-1678): amax floor 1e-8, code =
+//              clamp(round(v * (127/amax)), -128, 127), inv_scale = amax * (1/127).
 // MODE 0: codes of x; MODE 1: codes of rms_norm_raw(x, w); MODE 2: only the
-// normalized vector (executeRMSNorm).
+// normalized vector (executeRMSNorm); MODE 3: x holds gate | up (2K values)
+// and the row is act = max(0, gate)^2 * up (:1616-1620) before the norm.
 // ------------------------------------------------------------------------
 template <int MODE>
+__device__ __forceinline__ float act_in(const float* __restrict__ xm, int64_t K, int64_t i) {
+    if (MODE == 3) {
+        const float r = fmaxf(0.0f, xm[i]);
+        return __fmul_rn(__fmul_rn(r, r), xm[K + i]);
+    }
+    return xm[i];
+}
+
+template <int MODE>
+__device__ __forceinline__ float act_sumsq(const float* __restrict__ xm, int64_t K, float* red) {
+    if (MODE != 3) return block256_sumsq(xm, K, red);
+    // same order as block256_sumsq, on the relu^2 * up values
+    const int t = threadIdx.x;
+    float s = 0.0f;
+    for (int64_t i = t; i < K; i += 256) {
+        const float v = act_in<3>(xm, K, i);
+        s = __builtin_fmaf(v, v, s);
+    }
+    s = wave_sum_tree(s);
+    if ((t & 63) == 0) red[t >> 6] = s;
+    __syncthreads();
+    float r = (red[0] + red[1]) + (red[2] + red[3]);
+    __syncthreads();
+    return r;
+}
+
+template <int MODE, int QMAX>
 __global__ void __launch_bounds__(256)
-quant31_kernel(const float* __restrict__ x, const float* __restrict__ w, float eps, int64_t K,
-               int64_t Kp, int8_t* __restrict__ codes, tenzo_hip_actq_t* __restrict__ q,
-               float* __restrict__ y_out) {
+actquant_kernel(const float* __restrict__ x, const float* __restrict__ w, float eps, int64_t K,
+                int64_t Kp, int8_t* __restrict__ codes, tenzo_hip_actq_t* __restrict__ q,
+                float* __restrict__ y_out) {
     __shared__ float redf[4];
     __shared__ int redi[4];
     const int t = threadIdx.x;
     const int64_t m = blockIdx.x;
-    const float* xm = x + m * K;
+    const float* xm = x + m * (MODE == 3 ? 2 * K : K);
     float inv_rms = 1.0f;
-    if (MODE >= 1) inv_rms = inv_rms_from_sumsq(block256_sumsq(xm, K, redf), K, eps);
+    if (MODE >= 1) inv_rms = inv_rms_from_sumsq(act_sumsq<MODE>(xm, K, redf), K, eps);
     if (MODE == 2) {
         for (int64_t i = t; i < K; i += 256) y_out[m * K + i] = norm_apply(xm[i], inv_rms, w, i);
         return;
     }
-    float amax = 1e-6f;
+    float amax = QMAX == 31 ? 1e-6f : 1e-8f;
     for (int64_t i = t; i < K; i += 256) {
-        const float v = MODE == 1 ? norm_apply(xm[i], inv_rms, w, i) : xm[i];
+        const float a = act_in<MODE>(xm, K, i);
+        const float v = MODE >= 1 ? norm_apply(a, inv_rms, w, i) : a;
         amax = fmaxf(amax, fabsf(v));
     }
     amax = block256_max(amax, redf);
-    const float scale_act = __fdiv_rn(31.0f, amax);
+    const float scale_act = __fdiv_rn((float)QMAX, amax);
     int csum = 0;
     int8_t* cm = codes + m * Kp;
     for (int64_t i = t; i < Kp; i += 256) {
         int c = 0;
         if (i < K) {
-            const float v = MODE == 1 ? norm_apply(xm[i], inv_rms, w, i) : xm[i];
-            if (MODE == 1 && y_out) y_out[m * K + i] = v;
-            c = (int)roundf(__fmul_rn(v, scale_act));
+            const float a = act_in<MODE>(xm, K, i);
+            const float v = MODE >= 1 ? norm_apply(a, inv_rms, w, i) : a;
+            if (MODE >= 1 && y_out) y_out[m * K + i] = v;
+            float r = roundf(__fmul_rn(v, scale_act));
+            if (QMAX == 127) r = fminf(fmaxf(r, -128.0f), 127.0f);
+            c = (int)r;
         }
         cm[i] = (int8_t)c;
         csum += c;
     }
     csum = block256_sum_i32(csum, redi);
     if (t == 0) {
-        q[m].inv_scale = __fmul_rn(amax, 1.0f / 31.0f);  // absmax/31 as the reference build
+        q[m].inv_scale = __fmul_rn(amax, 1.0f / (float)QMAX);
         q[m].code_sum = csum;
     }
 }
@@ -127,22 +163,27 @@ __device__ __forceinline__ int dot16(const uint4 v, const int32_t* __restrict__ 
     return acc;
 }
 
+// y = float(acc) * (inv_scale * w_scale) (:1554, :118-126), plus the residual
+// add of :1590 / :1628 when resid is given (resid + y, one fp32 add).
 __device__ __forceinline__ void tl1_finalize(int tot, int64_t m, int64_t row, int64_t N,
                                              const tenzo_hip_actq_t* __restrict__ aq,
-                                             const RowScales& rs, float* __restrict__ y,
+                                             const RowScales& rs, float* y,
+                                             const float* resid,
                                              int32_t* __restrict__ acc_out) {
     const tenzo_hip_actq_t a = aq[m];
     const int v = tot - a.code_sum;
     int j = 0;
     while (j < rs.n - 1 && row >= rs.end[j]) ++j;
-    y[m * N + row] = (float)v * __fmul_rn(a.inv_scale, rs.scale[j]);  // :1554, :118-126
+    float out = (float)v * __fmul_rn(a.inv_scale, rs.scale[j]);
+    if (resid) out = __fadd_rn(resid[m * N + row], out);
+    y[m * N + row] = out;
     if (acc_out) acc_out[m * N + row] = v;
 }
 
 __global__ void __launch_bounds__(256)
 tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
                 const tenzo_hip_actq_t* __restrict__ aq, int64_t N, int64_t KS, int splits,
-                RowScales rs, float* __restrict__ y, int32_t* __restrict__ acc_out,
+                RowScales rs, float* y, const float* resid, int32_t* __restrict__ acc_out,
                 int32_t* __restrict__ ws_acc, uint32_t* __restrict__ ws_cnt) {
     __shared__ int red[4][64];
     __shared__ int is_last;
@@ -174,7 +215,7 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
     if (splits == 1) {
         if (wave == 0) {
             const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
-            tl1_finalize(tot, m, row, N, aq, rs, y, acc_out);
+            tl1_finalize(tot, m, row, N, aq, rs, y, resid, acc_out);
         }
         return;
     }
@@ -192,7 +233,7 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
     if (is_last && wave == 0) {
         __threadfence();
         const int tot = atomicExch(&ws_acc[m * N + row], 0);
-        tl1_finalize(tot, m, row, N, aq, rs, y, acc_out);
+        tl1_finalize(tot, m, row, N, aq, rs, y, resid, acc_out);
         if (lane == 0) atomicExch(&ws_cnt[m * nb + b], 0u);
     }
 }
@@ -211,22 +252,42 @@ int tl1_pick_splits(int64_t nb, int64_t KS, int64_t M) {
     return (int)want;
 }
 
+int launch_actquant(int mode, int qmax, const float* x, const float* norm_w, float eps,
+                    int64_t M, int64_t K, int64_t Kp, int8_t* codes, tenzo_hip_actq_t* q,
+                    float* y_out, hipStream_t st) {
+    const dim3 grid((unsigned)M), blk(256);
+#define AQ_CASE(MO, QM)                                                                  \
+    if (mode == MO && qmax == QM) {                                                      \
+        hipLaunchKernelGGL((actquant_kernel<MO, QM>), grid, blk, 0, st, x, norm_w, eps, K, Kp, \
+                           codes, q, y_out);                                             \
+        return launch_status("actquant_kernel");                                         \
+    }
+    AQ_CASE(0, 31) AQ_CASE(1, 31) AQ_CASE(3, 31) AQ_CASE(0, 127) AQ_CASE(1, 127)
+#undef AQ_CASE
+    set_error("actquant: unsupported mode %d / range %d", mode, qmax);
+    return TENZO_ERROR_UNSUPPORTED;
+}
+
+int launch_rmsnorm(const float* x, const float* w, float* y, int64_t dim, float eps,
+                   hipStream_t st) {
+    hipLaunchKernelGGL((actquant_kernel<2, 31>), dim3(1), dim3(256), 0, st, x, w, eps, dim, dim,
+                       (int8_t*)nullptr, (tenzo_hip_actq_t*)nullptr, y);
+    return launch_status("rmsnorm");
+}
+
 int launch_quant31(const float* x, const float* norm_w, bool do_norm, float eps, int64_t M,
                    int64_t K, int8_t* codes, tenzo_hip_actq_t* q, float* y_out,
                    hipStream_t st) {
-    const int64_t Kp = ceil_div(K, 64) * 64;
-    if (do_norm)
-        hipLaunchKernelGGL(quant31_kernel<1>, dim3((unsigned)M), dim3(256), 0, st, x, norm_w,
-                           eps, K, Kp, codes, q, y_out);
-    else
-        hipLaunchKernelGGL(quant31_kernel<0>, dim3((unsigned)M), dim3(256), 0, st, x, norm_w,
-                           eps, K, Kp, codes, q, y_out);
-    return launch_status("quant31_kernel");
+    return launch_actquant(do_norm ? 1 : 0, 31, x, norm_w, eps, M, K, ceil_div(K, 64) * 64,
+                           codes, q, y_out, st);
 }
+
+size_t tl1_ws_bytes(int64_t M, int64_t N) { return (size_t)(M * N + M * (N / 64)) * 4; }
 
 int launch_tl1_gemv(const int8_t* codes, const tenzo_hip_actq_t* q, const void* w_packed,
                     const RowScales& rs, int64_t M, int64_t N, int64_t K, float* y,
-                    int32_t* acc_out, hipStream_t st, int splits) {
+                    const float* resid, int32_t* acc_out, hipStream_t st, int splits,
+                    void* ws) {
     const int64_t nb = N / 64;
     const int64_t KS = ceil_div(K, 64);
     if (splits <= 0) splits = tl1_pick_splits(nb, KS, M);
@@ -234,15 +295,14 @@ int launch_tl1_gemv(const int8_t* codes, const tenzo_hip_actq_t* q, const void* 
     int32_t* ws_acc = nullptr;
     uint32_t* ws_cnt = nullptr;
     if (splits > 1) {
-        const size_t bytes = (size_t)(M * N + M * nb) * 4;
-        char* ws = (char*)Scratch::get(kScratchGemvAcc, bytes, st);
+        if (!ws) ws = Scratch::get(kScratchGemvAcc, tl1_ws_bytes(M, N), st);
         if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
         ws_acc = (int32_t*)ws;
-        ws_cnt = (uint32_t*)(ws + (size_t)M * N * 4);
+        ws_cnt = (uint32_t*)((char*)ws + (size_t)M * N * 4);
     }
     hipLaunchKernelGGL(tl1_gemv_kernel, dim3((unsigned)(nb * splits), (unsigned)M), dim3(256),
-                       0, st, (const uint4*)w_packed, codes, q, N, KS, splits, rs, y, acc_out,
-                       ws_acc, ws_cnt);
+                       0, st, (const uint4*)w_packed, codes, q, N, KS, splits, rs, y, resid,
+                       acc_out, ws_acc, ws_cnt);
     return launch_status("tl1_gemv_kernel");
 }
 
@@ -325,7 +385,8 @@ TENZO_HIP_API int tenzo_hip_bitlinear_tl1(const int8_t* codes, const tenzo_hip_a
     TZ_CHECK(M > 0 && M <= 65535 && N > 0 && N % 64 == 0 && K > 0,
              "bitlinear_tl1: need N %% 64 == 0 (N=%lld)", (long long)N);
     RowScales rs = RowScales::single(w_scale);
-    return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, acc_out, (hipStream_t)stream, 0);
+    return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, nullptr, acc_out,
+                           (hipStream_t)stream, 0, nullptr);
 }
 
 TENZO_HIP_API int tenzo_hip_bitlinear_tl1_f32(const float* x, const void* w_packed,
@@ -343,15 +404,13 @@ TENZO_HIP_API int tenzo_hip_bitlinear_tl1_f32(const float* x, const void* w_pack
     int rc = launch_quant31(x, nullptr, false, 0.0f, M, K, codes, q, nullptr, st);
     if (rc) return rc;
     RowScales rs = RowScales::single(w_scale);
-    return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, nullptr, st, 0);
+    return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, nullptr, nullptr, st, 0, nullptr);
 }
 
 TENZO_HIP_API int tenzo_hip_rmsnorm(const float* x, const float* w, float* y, int64_t dim,
                                     float eps, void* stream) {
     TZ_CHECK(x && y && dim > 0, "rmsnorm: bad arguments");
-    hipLaunchKernelGGL(quant31_kernel<2>, dim3(1), dim3(256), 0, (hipStream_t)stream, x, w, eps,
-                       dim, dim, (int8_t*)nullptr, (tenzo_hip_actq_t*)nullptr, y);
-    return launch_status("rmsnorm");
+    return launch_rmsnorm(x, w, y, dim, eps, (hipStream_t)stream);
 }
 
 TENZO_HIP_API int tenzo_hip_execute_bitlinear_tl1(const float* act, const uint8_t* w,

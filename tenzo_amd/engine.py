@@ -1,0 +1,216 @@
+"""ctypes binding of the engine C API (include/tenzo.h plus the engine
+extensions in include/tenzo_hip.h), mirroring the reference's C API
+(``include/tenzo.h:92-193``, implemented at ``TenzoEngine.cpp:2086-2204``).
+
+``Engine`` owns one ``tenzo_engine_t``; weights come from host numpy arrays in
+the reference's formats (TL1 blocks, int8 LM head with per-row scales) and are
+copied to the device when set. Every decode step runs on the GPU.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib, synth
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+
+class Config(ctypes.Structure):
+    """tenzo_config_t (reference include/tenzo.h:53-64)."""
+    _fields_ = [("hidden_size", _I), ("num_q_heads", _I), ("num_kv_heads", _I),
+                ("head_dim", _I), ("num_layers", _I), ("ffn_dim", _I), ("vocab_size", _I),
+                ("max_seq_len", _I), ("kv_mode", ctypes.c_char_p), ("device", ctypes.c_char_p)]
+
+
+class SamplingParams(ctypes.Structure):
+    """tenzo_sampling_params_t (reference include/tenzo.h:66-72)."""
+    _fields_ = [("temperature", _F), ("top_p", _F), ("top_k", _I),
+                ("repetition_penalty", _F)]
+
+
+class LayerWeights(ctypes.Structure):
+    """tenzo_layer_weights_t (reference include/tenzo.h:75-87)."""
+    _fields_ = [("q_w", _P), ("q_scale", _F), ("k_w", _P), ("k_scale", _F),
+                ("v_w", _P), ("v_scale", _F), ("out_w", _P), ("out_scale", _F),
+                ("gate_w", _P), ("gate_scale", _F), ("up_w", _P), ("up_scale", _F),
+                ("down_w", _P), ("down_scale", _F),
+                ("in_norm", _P), ("attn_sub_norm", _P), ("post_norm", _P),
+                ("ffn_sub_norm", _P)]
+
+
+def _sig(L):
+    L.tenzo_default_config.restype = Config
+    L.tenzo_default_config.argtypes = []
+    L.tenzo_default_sampling_params.restype = SamplingParams
+    L.tenzo_default_sampling_params.argtypes = []
+    return L
+
+
+def lib():
+    return _sig(_lib.load())
+
+
+def default_config() -> Config:
+    return lib().tenzo_default_config()
+
+
+def default_sampling_params() -> SamplingParams:
+    return lib().tenzo_default_sampling_params()
+
+
+def config_from(cfg: synth.DecodeConfig) -> Config:
+    c = default_config()
+    c.hidden_size, c.num_q_heads, c.num_kv_heads = cfg.hidden, cfg.n_q_heads, cfg.n_kv_heads
+    c.head_dim, c.num_layers, c.ffn_dim = synth.HEAD_DIM, cfg.n_layers, cfg.ffn
+    c.vocab_size, c.max_seq_len = cfg.vocab, cfg.max_seq
+    c.kv_mode = b"int8_fused"
+    c.device = b"rocm"
+    return c
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"]
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+class Engine:
+    """One device-resident decode engine."""
+
+    def __init__(self, cfg: synth.DecodeConfig | Config):
+        self.L = lib()
+        self.cfg = cfg if isinstance(cfg, Config) else config_from(cfg)
+        self.h = self.L.tenzo_create_engine(ctypes.byref(self.cfg))
+        if not self.h:
+            raise RuntimeError("tenzo_create_engine failed: " +
+                               self.L.tenzo_hip_last_error().decode(errors="replace"))
+
+    # -- lifecycle --
+    def close(self):
+        if self.h:
+            self.L.tenzo_destroy_engine(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, rc, what):
+        _lib.check(rc, what)
+
+    # -- weights --
+    def set_layer(self, l: int, lw: synth.LayerWeights, mlp: bool = True):
+        w = LayerWeights()
+        names = ["q", "k", "v", "out", "gate", "up", "down"]
+        for p, f in zip(synth.PROJ, names):
+            arr = lw.tl1[p] if (mlp or p not in ("gate", "up", "down")) else None
+            setattr(w, f + "_w", _ptr(arr).value if arr is not None else None)
+            setattr(w, f + "_scale", float(lw.scale[p]))
+        for f in ["in_norm", "attn_sub_norm", "post_norm", "ffn_sub_norm"]:
+            arr = getattr(lw, f)
+            setattr(w, f, _ptr(arr).value if arr is not None else None)
+        self._check(self.L.tenzo_set_layer_weights(self.h, l, ctypes.byref(w)),
+                    "tenzo_set_layer_weights")
+
+    def set_model(self, sm: synth.SynthModel, kv: bool = True):
+        for l, lw in enumerate(sm.layers):
+            self.set_layer(l, lw)
+        self._check(self.L.tenzo_set_final_norm(self.h, _ptr(sm.final_norm)),
+                    "tenzo_set_final_norm")
+        c = sm.cfg
+        self._check(self.L.tenzo_set_lm_head_i8(self.h, _ptr(sm.embed), _ptr(sm.embed_scales),
+                                                c.vocab, c.hidden), "tenzo_set_lm_head_i8")
+        if kv:
+            self.set_kv_from(sm)
+        self.set_rope_theta(c.theta)
+
+    def set_kv_from(self, sm: synth.SynthModel):
+        n = sm.ctx
+        kc = np.ascontiguousarray(sm.kc[:, :, :n])
+        vc = np.ascontiguousarray(sm.vc[:, :, :n])
+        ks = np.ascontiguousarray(sm.ks[:, :, :n].astype(np.float16)).view(np.uint16)
+        vs = np.ascontiguousarray(sm.vs[:, :, :n].astype(np.float16)).view(np.uint16)
+        self.set_kv(kc, vc, ks, vs, n)
+
+    def set_kv(self, kc, vc, ks, vs, seq_len: int):
+        """Host arrays [L][Hkv][seq_len][128] int8 and [L][Hkv][seq_len] fp16 bits."""
+        self._check(self.L.tenzo_hip_engine_set_kv(self.h, _ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs),
+                                                   seq_len, 0), "engine_set_kv")
+
+    def set_kv_device(self, kc_ptr, vc_ptr, ks_ptr, vs_ptr, seq_len: int):
+        self._check(self.L.tenzo_hip_engine_set_kv(self.h, kc_ptr, vc_ptr, ks_ptr, vs_ptr,
+                                                   seq_len, 1), "engine_set_kv")
+
+    def get_kv(self, seq_len: int):
+        c = self.cfg
+        shape = (c.num_layers, c.num_kv_heads, seq_len)
+        kc = np.empty(shape + (128,), np.int8)
+        vc = np.empty_like(kc)
+        ks = np.empty(shape, np.uint16)
+        vs = np.empty_like(ks)
+        self._check(self.L.tenzo_hip_engine_get_kv(self.h, _ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs),
+                                                   seq_len), "engine_get_kv")
+        return kc, vc, ks.view(np.float16).astype(np.float32), vs.view(np.float16).astype(np.float32)
+
+    def set_rope_theta(self, theta: float):
+        self._check(self.L.tenzo_hip_engine_set_rope_theta(self.h, theta), "set_rope_theta")
+
+    def use_graph(self, on: bool):
+        self._check(self.L.tenzo_hip_engine_use_graph(self.h, int(bool(on))), "use_graph")
+
+    # -- decode --
+    @property
+    def seq_len(self) -> int:
+        return int(self.L.tenzo_get_seq_len(self.h))
+
+    def reset(self):
+        self.L.tenzo_reset(self.h)
+
+    def rewind(self, seq_len: int):
+        self._check(self.L.tenzo_hip_engine_set_seq_len(self.h, int(seq_len)), "set_seq_len")
+
+    def prefill(self, token: int):
+        self._check(self.L.tenzo_prefill_token(self.h, int(token)), "tenzo_prefill_token")
+
+    def step(self, token: int, temperature: float = 0.0, penalty: float = 1.0,
+             past=None, top_k: int = 40, top_p: float = 0.9) -> int:
+        p = SamplingParams(temperature, top_p, top_k, penalty)
+        past_arr = None if past is None else np.ascontiguousarray(past, np.int32)
+        n = 0 if past_arr is None else past_arr.size
+        tok = self.L.tenzo_generate_step(self.h, int(token), ctypes.byref(p), _ptr(past_arr), n)
+        if tok < 0:
+            raise RuntimeError("tenzo_generate_step failed: " +
+                               self.L.tenzo_hip_last_error().decode(errors="replace"))
+        return int(tok)
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.cfg.vocab_size, np.float32)
+        self._check(self.L.tenzo_hip_engine_get_logits(self.h, _ptr(out)), "get_logits")
+        return out
+
+    def buffer(self, name: str) -> np.ndarray:
+        c = self.cfg
+        n = max(c.vocab_size, 2 * c.ffn_dim, c.hidden_size + 2 * c.num_kv_heads * 128)
+        out = np.empty(n, np.float32)
+        self._check(self.L.tenzo_hip_engine_get_buffer(self.h, name.encode(), _ptr(out), n),
+                    f"get_buffer({name})")
+        sizes = {"x": c.hidden_size, "qkv": c.hidden_size + 2 * c.num_kv_heads * 128,
+                 "attn_out": c.hidden_size, "h1": c.hidden_size, "gate_up": 2 * c.ffn_dim,
+                 "logits": c.vocab_size}
+        return out[:sizes[name]].copy()
+
+    def stream(self) -> int:
+        return int(self.L.tenzo_hip_engine_stream(self.h) or 0)

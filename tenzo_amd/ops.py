@@ -91,6 +91,16 @@ def bitlinear_tl1(codes: torch.Tensor, q: torch.Tensor, w_packed: torch.Tensor, 
     return y, acc
 
 
+def bitlinear_tl1_into(codes: torch.Tensor, q: torch.Tensor, w_packed: torch.Tensor,
+                       w_scale: float, N: int, K: int, y: torch.Tensor) -> torch.Tensor:
+    """bitlinear_tl1 writing into a caller-owned y (no allocation per call)."""
+    M = codes.shape[0]
+    _lib.check(_lib.load().tenzo_hip_bitlinear_tl1(
+        _ptr(codes), _ptr(q), _ptr(w_packed), w_scale, M, N, K, _ptr(y), None, _stream()),
+        "bitlinear_tl1")
+    return y
+
+
 def bitlinear_tl1_f32(x: torch.Tensor, w_packed: torch.Tensor, w_scale: float, N: int,
                       K: int) -> torch.Tensor:
     """executeBitLinearTL1(act, w, out, M, K, N, scale) on device tensors."""
@@ -194,6 +204,30 @@ def lm_head_i8(x, norm_w, w_packed, scales, V: int, H: int, eps: float = 1e-5):
     _lib.check(_lib.load().tenzo_hip_lm_head_i8(_ptr(x), _ptr(norm_w), eps, _ptr(w_packed),
                                                 _ptr(scales), _ptr(logits), V, H, _stream()),
                "lm_head_i8")
+    return logits
+
+
+def actquant127(x: torch.Tensor, norm_w: torch.Tensor | None = None, eps: float = 1e-5):
+    """compute_logits' activation quantization of each row of x ([M][K] or
+    [K]), after rms_norm_raw when norm_w is given. Returns (codes int8 [M][K],
+    actq int32 [M][2])."""
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    codes = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    q = torch.empty((M, 2), dtype=torch.int32, device=x.device)
+    _lib.check(_lib.load().tenzo_hip_rmsnorm_quant127(
+        _ptr(x2), _ptr(norm_w), int(norm_w is not None), eps, M, K, _ptr(codes), _ptr(q),
+        _stream()), "rmsnorm_quant127")
+    return codes, q
+
+
+def lm_head_i8_codes_into(codes, q, w_packed, scales, V: int, H: int, logits,
+                          idx=None):
+    """The LM-head GEMV on precomputed codes into caller-owned logits (and the
+    fused greedy argmax into idx when given)."""
+    _lib.check(_lib.load().tenzo_hip_lm_head_i8_codes(
+        _ptr(codes), _ptr(q), _ptr(w_packed), _ptr(scales), _ptr(logits), V, H, _ptr(idx),
+        _stream()), "lm_head_i8_codes")
     return logits
 
 

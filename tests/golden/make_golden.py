@@ -147,28 +147,7 @@ def quant_gemv_fixture():
 
 
 def layer_struct(sm, l):
-    lw = sm.layers[l]
-    ptr = lambda a: ctypes.cast(a.ctypes.data, ctypes.c_void_p)  # noqa: E731
-
-    class W(ctypes.Structure):
-        _fields_ = [
-            ("q_w", ctypes.c_void_p), ("q_scale", ctypes.c_float),
-            ("k_w", ctypes.c_void_p), ("k_scale", ctypes.c_float),
-            ("v_w", ctypes.c_void_p), ("v_scale", ctypes.c_float),
-            ("out_w", ctypes.c_void_p), ("out_scale", ctypes.c_float),
-            ("gate_w", ctypes.c_void_p), ("gate_scale", ctypes.c_float),
-            ("up_w", ctypes.c_void_p), ("up_scale", ctypes.c_float),
-            ("down_w", ctypes.c_void_p), ("down_scale", ctypes.c_float),
-            ("in_norm", ctypes.c_void_p), ("attn_sub_norm", ctypes.c_void_p),
-            ("post_norm", ctypes.c_void_p), ("ffn_sub_norm", ctypes.c_void_p),
-        ]
-    w = W()
-    for p, f in zip(synth.PROJ, ["q", "k", "v", "out", "gate", "up", "down"]):
-        setattr(w, f + "_w", ptr(lw.tl1[p]))
-        setattr(w, f + "_scale", float(lw.scale[p]))
-    for f in ["in_norm", "attn_sub_norm", "post_norm", "ffn_sub_norm"]:
-        setattr(w, f, ptr(getattr(lw, f)))
-    return w
+    return oracle.ref_layer_struct(sm, l)
 
 
 def run_ref_engine(sm, tokens):

@@ -1,0 +1,191 @@
+"""The engine (include/tenzo.h on the GPU) against the CPU oracle's decode step
+and the compiled reference's whole-engine goldens.
+
+Bars: every integer stage (activation codes, TL1 int32 sums, KV codes) is
+bit-exact given identical inputs; attention is an fp32 reduction in another
+order (1e-3), so chained steps are compared at 1e-3 on the hidden state and
+logits, and the greedy tokens must agree."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tenzo_amd import synth
+from tests.golden.make_golden import TINY, load_tiny_model
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def eng_mod():
+    import torch
+    assert torch.cuda.is_available(), "GPU test needs a visible GPU"
+    from tenzo_amd import engine
+    return engine
+
+
+def rel(a, b):
+    return np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30)
+
+
+CFG = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=3, ffn=1024,
+                         vocab=2048, max_seq=64, theta=10000.0)
+
+
+@pytest.mark.parametrize("graph", [True, False])
+def test_engine_steps_match_oracle(eng_mod, graph):
+    sm = synth.make_model(CFG, seed=41, ctx=9)
+    om = oracle.OracleModel(sm, f16_kv_scales=True)
+    with eng_mod.Engine(CFG) as e:
+        e.set_model(sm)
+        e.use_graph(graph)
+        assert e.seq_len == 9
+        tok = 5
+        for i in range(6):
+            print(f"step {i} graph={graph}", flush=True)
+            got = e.step(tok)
+            ref_tok, ref_logits, ref_hidden = om.step(tok, sm.ctx + i, CFG.theta)
+            assert rel(e.buffer("x"), ref_hidden) < 1e-3
+            assert rel(e.logits(), ref_logits) < 1e-3
+            assert got == ref_tok
+            tok = got
+        assert e.seq_len == 15
+        # appended KV codes agree except for rare rounding-tie flips of +-1
+        kc, vc, ks, vs = e.get_kv(15)
+        for g, r in ((kc, om.kc), (vc, om.vc)):
+            new_g, new_r = g[:, :, 9:15].astype(int), r[:, :, 9:15].astype(int)
+            assert (new_g != new_r).mean() < 0.01 and np.abs(new_g - new_r).max() <= 1
+        np.testing.assert_array_equal(kc[:, :, :9], sm.kc[:, :, :9])
+
+
+def test_engine_first_layer_stages_bit_exact(eng_mod):
+    """One layer, stage by stage from the engine's own buffers: QKV from the
+    embedded token, O/residual, gate|up and down/residual are bit-exact."""
+    cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=2, n_layers=1, ffn=1024,
+                             vocab=512, max_seq=32, theta=10000.0)
+    sm = synth.make_model(cfg, seed=43, ctx=4)
+    lw = sm.layers[0]
+    with eng_mod.Engine(cfg) as e:
+        e.set_model(sm)
+        e.step(77)
+        x0 = sm.embed[77].astype(np.float32) * sm.embed_scales[77]
+
+        def lin(name, inp, N, K):
+            codes, inv = oracle.quant31(inp)
+            acc = oracle.tl1_gemv_i32(lw.tl1[name], codes, N, K)
+            return acc.astype(np.float32) * np.float32(inv * lw.scale[name])
+
+        H, F = cfg.hidden, cfg.ffn
+        xn = oracle.rms_norm(x0, lw.in_norm)
+        qkv = np.concatenate([lin("q", xn, cfg.q_dim, H), lin("k", xn, cfg.kv_dim, H),
+                              lin("v", xn, cfg.kv_dim, H)])
+        np.testing.assert_array_equal(e.buffer("qkv"), qkv)
+        attn = e.buffer("attn_out")
+        h1 = (x0 + lin("o", oracle.rms_norm(attn, lw.attn_sub_norm), H, H)).astype(np.float32)
+        np.testing.assert_array_equal(e.buffer("h1"), h1)
+        pn = oracle.rms_norm(h1, lw.post_norm)
+        gu = np.concatenate([lin("gate", pn, F, H), lin("up", pn, F, H)])
+        np.testing.assert_array_equal(e.buffer("gate_up"), gu)
+        g, u = gu[:F], gu[F:]
+        act = (np.maximum(g, np.float32(0)) ** 2 * u).astype(np.float32)
+        x1 = (h1 + lin("down", oracle.rms_norm(act, lw.ffn_sub_norm), H, F)).astype(np.float32)
+        np.testing.assert_array_equal(e.buffer("x"), x1)
+        # attention of this step against the oracle from the same q/k/v
+        kc, vc = sm.kc[0].copy(), sm.vc[0].copy()
+        ks, vs = sm.ks[0].copy(), sm.vs[0].copy()
+        out, _, _ = oracle.attention_step(qkv[:cfg.q_dim], qkv[cfg.q_dim:cfg.q_dim + cfg.kv_dim],
+                                          qkv[cfg.q_dim + cfg.kv_dim:], kc, vc, ks, vs,
+                                          cfg.n_q_heads, cfg.n_kv_heads, cfg.max_seq, 4,
+                                          oracle.rope_table(cfg.theta, 4), f16_scales=True)
+        assert rel(attn, out) < 1e-5
+
+
+def test_engine_against_reference_goldens(eng_mod):
+    """The compiled reference engine's own greedy steps (decode_tiny fixture)."""
+    z = np.load(os.path.join(GOLD, "decode_tiny.npz"))
+    sm = load_tiny_model(z)
+    with eng_mod.Engine(TINY) as e:
+        e.set_model(sm)
+        for i, t in enumerate(z["tokens"]):
+            tok = e.step(int(t))
+            assert rel(e.buffer("x"), z["hidden"][i]) < 1e-3
+            assert rel(e.logits(), z["logits"][i]) < 1e-3
+            assert tok == z["out_tokens"][i]
+
+
+def test_engine_prefill_then_decode_equals_steps(eng_mod):
+    sm = synth.make_model(CFG, seed=45, ctx=0)
+    toks = [3, 9, 27, 81, 243]
+    with eng_mod.Engine(CFG) as a, eng_mod.Engine(CFG) as b:
+        a.set_model(sm)
+        b.set_model(sm)
+        for t in toks[:-1]:
+            a.prefill(t)
+            b.step(t)
+        assert a.seq_len == b.seq_len == len(toks) - 1
+        assert a.step(toks[-1]) == b.step(toks[-1])
+        np.testing.assert_array_equal(a.logits(), b.logits())
+        a.reset()
+        assert a.seq_len == 0
+
+
+def test_engine_repetition_penalty(eng_mod):
+    sm = synth.make_model(CFG, seed=47, ctx=3)
+    with eng_mod.Engine(CFG) as e:
+        e.set_model(sm)
+        e.step(11)
+        base = e.logits()
+        e.reset()
+        e.set_kv_from(sm)
+        best = int(np.argmax(base))
+        past = [best, best, 4]
+        tok = e.step(11, penalty=1.3, past=past)
+        pen = base.copy()
+        for t in past:  # TenzoEngine.cpp:1735-1743, applied per occurrence
+            pen[t] = pen[t] / np.float32(1.3) if pen[t] > 0 else pen[t] * np.float32(1.3)
+        np.testing.assert_array_equal(e.logits(), pen)
+        assert tok == oracle.argmax(pen)
+
+
+def test_engine_f32_lm_head(eng_mod):
+    from tenzo_amd import _lib
+    import ctypes
+    cfg = synth.DecodeConfig(hidden=256, n_q_heads=2, n_kv_heads=1, n_layers=1, ffn=512,
+                             vocab=300, max_seq=16, theta=10000.0)
+    sm = synth.make_model(cfg, seed=49, ctx=2)
+    E = np.random.default_rng(3).normal(0, 0.02, size=(cfg.vocab, cfg.hidden)).astype(np.float32)
+    with eng_mod.Engine(cfg) as e:
+        e.set_model(sm)
+        L = _lib.load()
+        assert L.tenzo_set_lm_head_f32(e.h, ctypes.c_void_p(E.ctypes.data), cfg.vocab,
+                                       cfg.hidden) == 0
+        tok = e.step(17)
+        xn = oracle.rms_norm(e.buffer("x"), sm.final_norm)
+        ref = E.astype(np.float64) @ xn.astype(np.float64)
+        assert rel(e.logits(), ref) < 1e-5
+        assert tok == int(np.argmax(e.logits()))
+
+
+def test_engine_error_paths(eng_mod):
+    from tenzo_amd import _lib
+    import ctypes
+    L = _lib.load()
+    cfg = synth.DecodeConfig(hidden=256, n_q_heads=2, n_kv_heads=1, n_layers=1, ffn=512,
+                             vocab=300, max_seq=4, theta=10000.0)
+    sm = synth.make_model(cfg, seed=51, ctx=0)
+    with eng_mod.Engine(cfg) as e:
+        # no weights yet: the step is refused, not run
+        p = eng_mod.SamplingParams(0.0, 0.9, 40, 1.0)
+        assert L.tenzo_generate_step(e.h, 1, ctypes.byref(p), None, 0) == -1
+        e.set_model(sm)
+        assert L.tenzo_generate_step(e.h, cfg.vocab, ctypes.byref(p), None, 0) == -1  # bad token
+        for t in range(4):
+            e.step(t)
+        assert L.tenzo_generate_step(e.h, 1, ctypes.byref(p), None, 0) == -1  # cache full
+        assert b"full" in L.tenzo_hip_last_error()
+        assert L.tenzo_set_layer_weights(None, 0, None) == -1
+    bad = eng_mod.config_from(cfg)
+    bad.kv_mode = b"tl1_fused"
+    assert not L.tenzo_create_engine(ctypes.byref(bad))
