@@ -5,9 +5,12 @@ step at batch 1 and 4096 tokens of context - 30 layers of TL1 ternary
 projections (hidden 2560, FFN 6912, 20 q / 5 kv heads of 128), INT8 KV cache
 with fp16 scales prefilled with 4096 quantized N(0,1) tokens, int8 LM head over
 vocab 128256, RoPE theta 500000. Weights are random-init of that architecture,
-generated on the device. Every timed step goes through the engine's C API
-(tenzo_generate_step: embed, 30 layers, LM head, greedy argmax, token back to
-the host) at position 4096 (the cache is rewound between steps).
+generated on the device. A step is the whole token: embedding, 30 layers, LM
+head and greedy argmax. The timed run is `--steps` greedy tokens decoded back
+to back from position 4096 with each token fed to the next step on the
+device (tenzo_hip_engine_decode); the rate of the reference API's per-token
+loop (tenzo_generate_step, token returned to the host, cache rewound to 4096
+each time) is reported beside it.
 
 Prints ONE JSON line: tok/s, the step's HBM bytes / time against the 8 TB/s
 peak, a roofline entry for the dominant kernel (its algorithmic bytes / its
@@ -43,7 +46,9 @@ def parse():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--eager", action="store_true", help="launch stages without the HIP graph")
+    ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
+                    help="engine execution mode (one persistent kernel per token, or one "
+                         "kernel per stage replayed from a HIP graph / launched eagerly)")
     return ap.parse_args()
 
 
@@ -255,34 +260,48 @@ def main():
     cfg = synth.BITNET_2B
     ctx = args.ctx
     e, host = build_model(torch, cfg, ctx)
-    e.use_graph(not args.eager)
+    e.set_mode(args.mode)
+    mode = e.mode
 
+    # warm up (also captures graphs / loads code), then the timed decode:
+    # `steps` greedy tokens chained on the device from position ctx
     tok = 1
-    for _ in range(args.warmup):
+    if args.warmup:
         e.rewind(ctx)
-        tok = e.step(tok)
+        e.decode(tok, args.warmup)
+    e.rewind(ctx)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
-        e.rewind(ctx)
-        tok = e.step(tok)
+    toks, ev_ms = e.decode(tok, args.steps)
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     ms = dt / args.steps * 1e3
     tok_s = args.steps / dt
+    # the reference API's loop: one tenzo_generate_step (token back to the
+    # host) per token, at position ctx
+    api_steps = max(5, args.steps // 5)
+    e.rewind(ctx)
+    t0 = time.perf_counter()
+    for _ in range(api_steps):
+        e.rewind(ctx)
+        tok = e.step(tok)
+    api_tok_s = api_steps / (time.perf_counter() - t0)
 
-    step_bytes = cfg.step_bytes(ctx + 1)["total"]
+    # algorithmic HBM bytes of a step at the mean context of the timed run
+    step_bytes = cfg.step_bytes(ctx + 1 + args.steps // 2)["total"]
     step_gbs = step_bytes / (dt / args.steps) / 1e9
 
+    # the dominant kernel: the decode step itself (one launch per token in the
+    # persistent mode); its mean duration from HIP events on the engine stream
+    kern_s = ev_ms / 1e3 / args.steps
+    dom_name = "decode_step_kernel" if mode == "persistent" else "decode step (stage kernels)"
+    roofline = {"bound": "hbm", "kernel": dom_name,
+                "achieved": round(step_bytes / kern_s / 1e9, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(step_bytes / kern_s / 1e9 / PEAK_HBM_GBS, 4),
+                "traffic": None, "alg_bytes_per_launch": int(step_bytes),
+                "mean_launch_us": round(kern_s * 1e6, 2)}
     rl_tl1 = tl1_roofline(torch, cfg, host)
     rl_head = head_roofline(torch, cfg, host)
-    # the dominant kernel: the larger share of the step
-    dom = max((rl_tl1, rl_head), key=lambda r: r["mean_launch_us"] * r["launches_per_token"])
-    roofline = {"bound": "hbm", "kernel": dom["kernel"],
-                "achieved": round(dom["achieved_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(dom["achieved_gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
-                "alg_bytes_per_launch": int(dom["alg_bytes_per_launch"]),
-                "mean_launch_us": round(dom["mean_launch_us"], 2)}
     cpu = None if args.no_cpu else cpu_baseline(torch, cfg, host, ctx, args.cpu_seconds)
 
     out = {
@@ -295,14 +314,15 @@ def main():
                                f"context {ctx}, INT8 KV fp16 scales, int8 LM head",
                    "layers": cfg.n_layers, "hidden": cfg.hidden, "ffn": cfg.ffn,
                    "heads": [cfg.n_q_heads, cfg.n_kv_heads, 128], "vocab": cfg.vocab,
-                   "rope_theta": cfg.theta, "graph": not args.eager},
+                   "rope_theta": cfg.theta, "engine_mode": mode},
         "step_hbm_bytes": step_bytes, "step_gbs": round(step_gbs, 1),
         "step_frac_of_peak": round(step_gbs / PEAK_HBM_GBS, 4),
         "roofline": roofline,
-        "kernels": {"tl1_gemv": {k: (round(v, 2) if isinstance(v, float) else v)
-                                 for k, v in rl_tl1.items()},
-                    "lm_head_i8": {k: (round(v, 2) if isinstance(v, float) else v)
-                                   for k, v in rl_head.items()}},
+        "api_generate_step_tok_s": round(api_tok_s, 2),
+        "stage_kernels": {"tl1_gemv": {k: (round(v, 2) if isinstance(v, float) else v)
+                                       for k, v in rl_tl1.items()},
+                          "lm_head_i8": {k: (round(v, 2) if isinstance(v, float) else v)
+                                         for k, v in rl_head.items()}},
         "cpu_baseline": cpu,
     }
     e.close()

@@ -212,8 +212,34 @@ TENZO_HIP_API int tenzo_hip_engine_get_logits(struct tenzo_engine_opaque* e, flo
  * out in floats. */
 TENZO_HIP_API int tenzo_hip_engine_get_buffer(struct tenzo_engine_opaque* e, const char* name,
                                               float* out, int64_t n);
-/* Runs the decode step through a captured HIP graph (1, default) or eager
- * launches (0). */
+/* How a decode step is executed (no reference counterpart; the results are
+ * the same up to fp32 reduction order in attention):
+ *   2 (default) one persistent cooperative kernel per token, stages separated
+ *     by in-kernel barriers (needs cooperative launch, an int8 LM head, MLP
+ *     weights in every layer, hidden and ffn <= 8192; otherwise mode 1 runs);
+ *   1 one kernel per stage, replayed from a captured HIP graph;
+ *   0 one kernel per stage, launched eagerly. */
+TENZO_HIP_API int tenzo_hip_engine_set_mode(struct tenzo_engine_opaque* e, int mode);
+/* The mode the next step will use (after the fallback above). */
+TENZO_HIP_API int tenzo_hip_engine_get_mode(struct tenzo_engine_opaque* e);
+/* Greedy decode of n tokens with the tokens chained on the device (no host
+ * round trip per token; no reference counterpart - the reference's decode
+ * loop calls tenzo_generate_step per token): step i consumes token (i = 0)
+ * or step i-1's greedy token, at position seq_len + i. out (host, n ints)
+ * receives the n greedy tokens; *ms (optional) the HIP-event time of the n
+ * steps on the engine stream. Repetition penalty and sampling are not
+ * applied. */
+TENZO_HIP_API int tenzo_hip_engine_decode(struct tenzo_engine_opaque* e, int token, int n,
+                                          int32_t* out, float* ms);
+/* Step trace of the persistent kernel (mode 2; no reference counterpart):
+ * while on, each step records for every stage s (5 per layer, then the LM
+ * head) and workgroup w the wall-clock ticks (100 MHz) at which w reached
+ * and left the barrier after s: out[(s * nwg + w) * 2 + {0, 1}].
+ * get_trace returns the word count (out may be null to query it) or -1. */
+TENZO_HIP_API int tenzo_hip_engine_trace(struct tenzo_engine_opaque* e, int on);
+TENZO_HIP_API int64_t tenzo_hip_engine_get_trace(struct tenzo_engine_opaque* e, uint64_t* out,
+                                                 int64_t n);
+/* use_graph(1) = set_mode(1), use_graph(0) = set_mode(0). */
 TENZO_HIP_API int tenzo_hip_engine_use_graph(struct tenzo_engine_opaque* e, int on);
 /* The engine's HIP stream (hipStream_t as void*). */
 TENZO_HIP_API void* tenzo_hip_engine_stream(struct tenzo_engine_opaque* e);

@@ -51,6 +51,11 @@ SIGNATURES = {
     "tenzo_hip_engine_get_logits": (_I, [_P, _P]),
     "tenzo_hip_engine_get_buffer": (_I, [_P, _S, _P, _I64]),
     "tenzo_hip_engine_use_graph": (_I, [_P, _I]),
+    "tenzo_hip_engine_set_mode": (_I, [_P, _I]),
+    "tenzo_hip_engine_get_mode": (_I, [_P]),
+    "tenzo_hip_engine_trace": (_I, [_P, _I]),
+    "tenzo_hip_engine_decode": (_I, [_P, _I, _I, _P, _P]),
+    "tenzo_hip_engine_get_trace": (_I64, [_P, _P, _I64]),
     "tenzo_hip_engine_stream": (_P, [_P]),
     # include/tenzo.h
     "tenzo_get_version": (_S, []),

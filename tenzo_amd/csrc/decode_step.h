@@ -1,0 +1,66 @@
+// Internal interface of the persistent decode-step kernel (used by the engine).
+#pragma once
+
+#include "common.h"
+
+namespace tz {
+
+// Per-layer device pointers and scales (an array of these lives in HBM).
+// Slot s of mat/norm belongs to the stage that reads it: 0 Q|K|V (in_norm),
+// 1 O (attn_sub_norm), 2 gate|up (post_norm), 3 down (ffn_sub_norm).
+struct DsLayer {
+    const uint4* mat[4];   // TL1 GEMV layout; Q|K|V and gate|up row-concatenated
+    const float* norm[4];  // null = no weight
+    float sc[7];           // q, k, v, o, gate, up, down
+};
+
+struct DsParams {
+    const DsLayer* layers;
+    const float* final_norm;
+    const uint4* head;          // packed int8 LM head (lm_head.hip layout)
+    const float* head_scales;
+    const float* rope;          // [max_seq][128] cos | sin
+    int8_t* kc;                 // [L][Hkv][max_seq][128]
+    int8_t* vc;
+    uint16_t* ks;               // [L][Hkv][max_seq] fp16
+    uint16_t* vs;
+    float* x;                   // [H] hidden state
+    float* qkv;                 // [qd + 2 kvd]
+    float* attn;                // [qd]
+    float* h1;                  // [H]
+    float* gu;                  // [2F]
+    float* logits;              // [V]
+    float* part;                // [Hkv][C][G][kDsPartStride] attention partials
+    float2* am_part;            // [nwg] argmax partials
+    unsigned* sync;             // ds_sync_words() words, zero before each launch
+    int32_t* io;                // [0] token in, [2] greedy token out (also copied to [0])
+    int32_t* out_tokens;        // optional: the greedy token is also stored at [step]
+    int step;
+    int H, F, Hq, Hkv, L, V, max_seq;
+    int pos, C, T;              // this step's position and attention chunking
+    int nwg;
+    int with_head;              // 0: stop after the layers (prefill)
+    float eps;
+    // optional step trace: for stage s and workgroup w, [(s * nwg + w) * 2]
+    // = wall clock (100 MHz) when w arrives at the barrier after stage s,
+    // [.. + 1] = when it leaves it
+    uint64_t* trace;
+};
+
+constexpr int kDsThreads = 256;
+constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
+constexpr int kDsCounters = 16;
+
+// uint32 words of the sync region for L layers and Hkv kv heads.
+size_t ds_sync_words(int L, int Hkv);
+// Workgroup count the kernel runs with on the current device (a multiple of
+// kDsCounters, all co-resident), or 0 when cooperative launch is unavailable.
+int ds_grid_size();
+// Attention chunking (C chunks of T tokens per kv head) for context ctx.
+void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T);
+// Launches one decode step (cooperative). The sync region must be zero.
+int launch_decode_step(const DsParams& p, int G, hipStream_t st);
+// Error word of the sync region (non-zero after an aborted step).
+size_t ds_error_word(int L, int Hkv);
+
+}  // namespace tz

@@ -18,8 +18,11 @@
 //     actquant(relu^2*up, ffn_sub_norm) -> codes  (:1616-1624)
 //     TL1 GEMV down + residual -> x = h1 + down   (:1625-1628)
 //   actquant(final_norm, +-127) ; LM head + fused greedy argmax (:1634-1755)
-// and is replayed from a captured HIP graph (position and token are read
-// from device memory, so one graph serves every position of a chunk size).
+// By default the whole step runs as ONE persistent cooperative kernel
+// (decode_step.hip) with in-kernel barriers between the stages above; the
+// same stages as separate kernels, replayed from a captured HIP graph
+// (position and token read from device memory, one graph per attention chunk
+// size) or launched eagerly, remain selectable (tenzo_hip_engine_set_mode).
 #include <cstring>
 #include <map>
 #include <string>
@@ -27,6 +30,7 @@
 
 #include "attention.h"
 #include "common.h"
+#include "decode_step.h"
 #include "lm_head.h"
 #include "tl1.h"
 
@@ -90,8 +94,20 @@ struct tenzo_engine_opaque {
     float* rope = nullptr;       // [max_seq][128]
 
     int seq_len = 0;
-    bool use_graph = true;
+    int mode = 2;                // 0 eager kernels, 1 HIP graph, 2 persistent kernel
     std::map<std::pair<int, int>, hipGraphExec_t> graphs;  // (T, with head)
+
+    // persistent decode kernel
+    int ds_nwg = 0;              // 0: not available on this device
+    DsLayer* ds_layers = nullptr;  // device array [L]
+    bool ds_layers_dirty = true;
+    unsigned* ds_sync = nullptr;
+    float* ds_part = nullptr;
+    float2* ds_am = nullptr;
+    size_t ds_sync_bytes = 0;
+    int32_t* dec_out = nullptr;  // device tokens of tenzo_hip_engine_decode
+    int dec_cap = 0;
+    uint64_t* ds_trace = nullptr;  // step trace (tenzo_hip_engine_trace), null when off
 
 };
 
@@ -175,6 +191,17 @@ bool ready(tenzo_engine_t e, bool need_head) {
         return false;
     }
     return true;
+}
+
+// Between chained steps: the greedy token becomes the next input, the
+// position advances.
+__global__ void chain_kernel(int32_t* io, int32_t* out) {
+    if (threadIdx.x == 0) {
+        const int t = io[2];
+        io[0] = t;
+        io[1] += 1;
+        *out = t;
+    }
 }
 
 __global__ void copy_kernel(const float* __restrict__ src, float* __restrict__ dst, int64_t n) {
@@ -285,6 +312,84 @@ int enqueue_step(tenzo_engine_t e, bool head, int T, int max_chunks) {
     return head ? enqueue_head(e) : TENZO_SUCCESS;
 }
 
+// Whether the persistent kernel can run this model as loaded.
+bool ds_usable(tenzo_engine_t e) {
+    if (e->ds_nwg <= 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192) return false;
+    for (const DevLayer& d : e->layers)
+        if (!d.mlp) return false;
+    return true;
+}
+
+int ds_sync_layers(tenzo_engine_t e) {
+    if (!e->ds_layers_dirty) return TENZO_SUCCESS;
+    std::vector<DsLayer> h(e->L);
+    for (int l = 0; l < e->L; ++l) {
+        const DevLayer& d = e->layers[l];
+        h[l].mat[0] = (const uint4*)d.qkv;
+        h[l].mat[1] = (const uint4*)d.o;
+        h[l].mat[2] = (const uint4*)d.gu;
+        h[l].mat[3] = (const uint4*)d.down;
+        for (int i = 0; i < 4; ++i) h[l].norm[i] = d.norm[i];
+        for (int i = 0; i < 7; ++i) h[l].sc[i] = d.sc[i];
+    }
+    TZ_HIP(hipMemcpy(e->ds_layers, h.data(), h.size() * sizeof(DsLayer), hipMemcpyHostToDevice));
+    e->ds_layers_dirty = false;
+    return TENZO_SUCCESS;
+}
+
+int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = nullptr,
+                   int step = 0) {
+    int rc = ds_sync_layers(e);
+    if (rc) return rc;
+    DsParams p{};
+    p.layers = e->ds_layers;
+    p.final_norm = e->final_norm;
+    p.head = (const uint4*)e->head_i8;
+    p.head_scales = e->head_scales;
+    p.rope = e->rope;
+    p.kc = e->kc;
+    p.vc = e->vc;
+    p.ks = e->ks;
+    p.vs = e->vs;
+    p.x = e->x;
+    p.qkv = e->qkv;
+    p.attn = e->attn;
+    p.h1 = e->h1;
+    p.gu = e->gu;
+    p.logits = e->logits;
+    p.part = e->ds_part;
+    p.am_part = e->ds_am;
+    p.sync = e->ds_sync;
+    p.io = e->io_dev;
+    p.H = e->H;
+    p.F = e->F;
+    p.Hq = e->Hq;
+    p.Hkv = e->Hkv;
+    p.L = e->L;
+    p.V = e->V;
+    p.max_seq = e->max_seq;
+    p.pos = pos;
+    ds_chunking(pos + 1, e->Hkv, e->ds_nwg, &p.C, &p.T);
+    p.nwg = e->ds_nwg;
+    p.with_head = head ? 1 : 0;
+    p.eps = e->eps;
+    p.trace = e->ds_trace;
+    p.out_tokens = out_tokens;
+    p.step = step;
+    TZ_HIP(hipMemsetAsync(e->ds_sync, 0, e->ds_sync_bytes, e->st));
+    return launch_decode_step(p, e->Hq / e->Hkv, e->st);
+}
+
+// After a persistent step: the kernel's error word (non-zero when a wait
+// timed out and the step was abandoned), copied next to the result token.
+int ds_check(tenzo_engine_t e) {
+    if (e->io_host[3] != 0) {
+        set_error("decode step aborted: an in-kernel wait timed out (engine state is invalid)");
+        return TENZO_ERROR_UNSUPPORTED;
+    }
+    return TENZO_SUCCESS;
+}
+
 // Runs one token through the layers (and the head) at position seq_len.
 int run_step(tenzo_engine_t e, int token, bool head) {
     if (!ready(e, head)) return TENZO_ERROR_INVALID_ARGUMENT;
@@ -303,7 +408,12 @@ int run_step(tenzo_engine_t e, int token, bool head) {
     e->io_host[1] = pos;
     TZ_HIP(hipMemcpyAsync(e->io_dev, e->io_host, 8, hipMemcpyHostToDevice, e->st));
     int rc;
-    if (e->use_graph) {
+    e->io_host[3] = 0;
+    if (e->mode == 2 && ds_usable(e)) {
+        if ((rc = run_persistent(e, head, pos))) return rc;
+        TZ_HIP(hipMemcpyAsync(e->io_host + 3, e->ds_sync + ds_error_word(e->L, e->Hkv), 4,
+                              hipMemcpyDeviceToHost, e->st));
+    } else if (e->mode >= 1) {
         const int max_chunks = (int)ceil_div(e->max_seq, T);
         auto key = std::make_pair(T, head ? 1 : 0);
         auto it = e->graphs.find(key);
@@ -426,6 +536,21 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
         e->io_host = static_cast<int32_t*>(h);
     }
     ok = ok && !upload_rope(e);
+    if (ok) {
+        e->ds_nwg = ds_grid_size();
+        if (e->ds_nwg > 0) {
+            const int G = Hq / Hkv;
+            int cmax = (e->ds_nwg * 3 / 4) / Hkv;
+            const int cseq = (int)ceil_div(e->max_seq, 1024);
+            if (cseq > cmax) cmax = cseq;
+            if (cmax < 1) cmax = 1;
+            e->ds_sync_bytes = ds_sync_words(e->L, Hkv) * 4;
+            ok = !alloc_t(e, &e->ds_layers, sizeof(DsLayer) * e->L) &&
+                 !alloc_t(e, &e->ds_sync, e->ds_sync_bytes, true) &&
+                 !alloc_t(e, &e->ds_part, (size_t)Hkv * cmax * G * kDsPartStride * 4) &&
+                 !alloc_t(e, &e->ds_am, (size_t)e->ds_nwg * sizeof(float2));
+        }
+    }
     if (!ok) {
         tenzo_destroy_engine(e);
         return nullptr;
@@ -439,6 +564,8 @@ TENZO_API void tenzo_destroy_engine(tenzo_engine_t e) {
     if (e->st) (void)hipStreamSynchronize(e->st);
     drop_graphs(e);
     for (void* p : e->allocs) (void)hipFree(p);
+    if (e->ds_trace) (void)hipFree(e->ds_trace);
+    if (e->dec_out) (void)hipFree(e->dec_out);
     if (e->io_host) (void)hipHostFree(e->io_host);
     if (e->st) (void)hipStreamDestroy(e->st);
     delete e;
@@ -486,6 +613,7 @@ TENZO_API tenzo_status_t tenzo_set_layer_weights(tenzo_engine_t e, int l,
                          w->gate_scale, w->up_scale, w->down_scale};
     std::memcpy(d.sc, sc, sizeof(sc));
     d.set = true;
+    e->ds_layers_dirty = true;
     drop_graphs(e);  // scales are captured in the graph's kernel arguments
     return TENZO_SUCCESS;
 }
@@ -563,6 +691,7 @@ TENZO_API tenzo_status_t tenzo_prefill_token(tenzo_engine_t e, int token) {
         set_error("prefill_token: %s", hipGetErrorString(hipGetLastError()));
         return TENZO_ERROR_UNSUPPORTED;
     }
+    if ((rc = ds_check(e))) return (tenzo_status_t)rc;
     e->seq_len += 1;  // :1816-1818
     return TENZO_SUCCESS;
 }
@@ -607,11 +736,84 @@ TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,
         set_error("generate_step: %s", hipGetErrorString(hipGetLastError()));
         return -1;
     }
+    if (ds_check(e)) return -1;
     e->seq_len += 1;  // :1833-1835
     return e->io_host[2];
 }
 
 // ---- engine extensions (include/tenzo_hip.h) ----
+
+TENZO_HIP_API int tenzo_hip_engine_decode(tenzo_engine_t e, int token, int n, int32_t* out,
+                                          float* ms) {
+    TZ_CHECK(e && out && n > 0, "engine_decode: bad arguments");
+    if (!ready(e, true)) return TENZO_ERROR_INVALID_ARGUMENT;
+    TZ_CHECK(token >= 0 && token < e->V, "engine_decode: token %d outside [0, %d)", token, e->V);
+    TZ_CHECK(e->seq_len + n <= e->max_seq, "engine_decode: %d steps from position %d exceed "
+             "max_seq %d", n, e->seq_len, e->max_seq);
+    TZ_HIP(hipSetDevice(e->dev));
+    if (n > e->dec_cap) {
+        if (e->dec_out) {
+            TZ_HIP(hipStreamSynchronize(e->st));
+            TZ_HIP(hipFree(e->dec_out));
+            e->dec_out = nullptr;
+            e->dec_cap = 0;
+        }
+        TZ_HIP(hipMalloc(&e->dec_out, (size_t)n * 4));
+        e->dec_cap = n;
+    }
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    TZ_HIP(hipEventCreate(&t0));
+    TZ_HIP(hipEventCreate(&t1));
+    e->io_host[0] = token;
+    e->io_host[3] = 0;
+    int rc = TENZO_SUCCESS;
+    if (hipMemcpyAsync(e->io_dev, e->io_host, 4, hipMemcpyHostToDevice, e->st) != hipSuccess ||
+        hipEventRecord(t0, e->st) != hipSuccess)
+        rc = TENZO_ERROR_UNSUPPORTED;
+    const bool persistent = e->mode == 2 && ds_usable(e);
+    for (int i = 0; i < n && !rc; ++i) {
+        const int pos = e->seq_len + i;
+        if (persistent) {
+            rc = run_persistent(e, true, pos, e->dec_out, i);
+        } else {
+            // stage kernels: token and position chained on the device
+            const int T = attn_pick_chunk(pos + 1, e->Hkv, 1);
+            if (i == 0) {
+                e->io_host[1] = pos;
+                if (hipMemcpyAsync(e->io_dev + 1, e->io_host + 1, 4, hipMemcpyHostToDevice,
+                                   e->st) != hipSuccess) {
+                    rc = TENZO_ERROR_UNSUPPORTED;
+                    break;
+                }
+            }
+            rc = enqueue_step(e, true, T, (int)ceil_div(pos + 1, T));
+            if (!rc) {
+                hipLaunchKernelGGL(chain_kernel, dim3(1), dim3(64), 0, e->st, e->io_dev,
+                                   e->dec_out + i);
+                rc = launch_status("chain_kernel");
+            }
+        }
+    }
+    if (!rc && hipEventRecord(t1, e->st) != hipSuccess) rc = TENZO_ERROR_UNSUPPORTED;
+    if (!rc && persistent)
+        if (hipMemcpyAsync(e->io_host + 3, e->ds_sync + ds_error_word(e->L, e->Hkv), 4,
+                           hipMemcpyDeviceToHost, e->st) != hipSuccess)
+            rc = TENZO_ERROR_UNSUPPORTED;
+    if (!rc && hipMemcpyAsync(out, e->dec_out, (size_t)n * 4, hipMemcpyDeviceToHost, e->st) !=
+                   hipSuccess)
+        rc = TENZO_ERROR_UNSUPPORTED;
+    if (hipStreamSynchronize(e->st) != hipSuccess && !rc) rc = TENZO_ERROR_UNSUPPORTED;
+    if (!rc && ms) (void)hipEventElapsedTime(ms, t0, t1);
+    (void)hipEventDestroy(t0);
+    (void)hipEventDestroy(t1);
+    if (rc) {
+        if (rc == TENZO_ERROR_UNSUPPORTED) set_error("engine_decode: %s", hipGetErrorString(hipGetLastError()));
+        return rc;
+    }
+    if ((rc = ds_check(e))) return rc;
+    e->seq_len += n;
+    return TENZO_SUCCESS;
+}
 
 TENZO_HIP_API int tenzo_hip_engine_set_kv(tenzo_engine_t e, const int8_t* kc, const int8_t* vc,
                                           const uint16_t* ks, const uint16_t* vs, int seq_len,
@@ -709,10 +911,53 @@ TENZO_HIP_API int tenzo_hip_engine_get_buffer(tenzo_engine_t e, const char* name
 
 TENZO_HIP_API int tenzo_hip_engine_use_graph(tenzo_engine_t e, int on) {
     TZ_CHECK(e, "engine_use_graph: null engine");
-    e->use_graph = on != 0;
+    e->mode = on ? 1 : 0;
     return TENZO_SUCCESS;
 }
 
+TENZO_HIP_API int tenzo_hip_engine_set_mode(tenzo_engine_t e, int mode) {
+    TZ_CHECK(e, "engine_set_mode: null engine");
+    TZ_CHECK(mode >= 0 && mode <= 2, "engine_set_mode: mode %d not in {0, 1, 2}", mode);
+    e->mode = mode;
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_get_mode(tenzo_engine_t e) {
+    if (!e) return -1;
+    return e->mode == 2 && !ds_usable(e) ? 1 : e->mode;
+}
+
 TENZO_HIP_API void* tenzo_hip_engine_stream(tenzo_engine_t e) { return e ? e->st : nullptr; }
+
+static size_t trace_words(tenzo_engine_t e) {
+    return (size_t)(5 * e->L + 1) * (size_t)(e->ds_nwg > 0 ? e->ds_nwg : 1) * 2;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_trace(tenzo_engine_t e, int on) {
+    TZ_CHECK(e, "engine_trace: null engine");
+    TZ_HIP(hipSetDevice(e->dev));
+    if (on && !e->ds_trace) {
+        TZ_CHECK(e->ds_nwg > 0, "engine_trace: the persistent decode kernel is not available");
+        void* p = nullptr;
+        TZ_HIP(hipMalloc(&p, trace_words(e) * 8));
+        TZ_HIP(hipMemset(p, 0, trace_words(e) * 8));
+        e->ds_trace = static_cast<uint64_t*>(p);
+    } else if (!on && e->ds_trace) {
+        TZ_HIP(hipStreamSynchronize(e->st));
+        TZ_HIP(hipFree(e->ds_trace));
+        e->ds_trace = nullptr;
+    }
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int64_t tenzo_hip_engine_get_trace(tenzo_engine_t e, uint64_t* out, int64_t n) {
+    if (!e || !e->ds_trace) return -1;
+    const int64_t words = (int64_t)trace_words(e);
+    if (!out) return words;
+    if (n < words || hipStreamSynchronize(e->st) != hipSuccess ||
+        hipMemcpy(out, e->ds_trace, (size_t)words * 8, hipMemcpyDeviceToHost) != hipSuccess)
+        return -1;
+    return words;
+}
 
 }  // extern "C"

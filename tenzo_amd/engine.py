@@ -171,6 +171,17 @@ class Engine:
     def use_graph(self, on: bool):
         self._check(self.L.tenzo_hip_engine_use_graph(self.h, int(bool(on))), "use_graph")
 
+    MODES = {"eager": 0, "graph": 1, "persistent": 2}
+
+    def set_mode(self, mode: str):
+        """'persistent' (default), 'graph' or 'eager'."""
+        self._check(self.L.tenzo_hip_engine_set_mode(self.h, self.MODES[mode]), "set_mode")
+
+    @property
+    def mode(self) -> str:
+        m = int(self.L.tenzo_hip_engine_get_mode(self.h))
+        return {v: k for k, v in self.MODES.items()}[m]
+
     # -- decode --
     @property
     def seq_len(self) -> int:
@@ -196,6 +207,15 @@ class Engine:
                                self.L.tenzo_hip_last_error().decode(errors="replace"))
         return int(tok)
 
+    def decode(self, token: int, n: int):
+        """n greedy steps chained on the device; returns (tokens, ms of the n
+        steps by HIP events on the engine stream)."""
+        out = np.empty(n, np.int32)
+        ms = ctypes.c_float(0.0)
+        self._check(self.L.tenzo_hip_engine_decode(self.h, int(token), int(n), _ptr(out),
+                                                   ctypes.byref(ms)), "engine_decode")
+        return out, float(ms.value)
+
     def logits(self) -> np.ndarray:
         out = np.empty(self.cfg.vocab_size, np.float32)
         self._check(self.L.tenzo_hip_engine_get_logits(self.h, _ptr(out)), "get_logits")
@@ -211,6 +231,22 @@ class Engine:
                  "attn_out": c.hidden_size, "h1": c.hidden_size, "gate_up": 2 * c.ffn_dim,
                  "logits": c.vocab_size}
         return out[:sizes[name]].copy()
+
+    def trace(self, on: bool = True):
+        """Record per-stage barrier timestamps of the persistent kernel."""
+        self._check(self.L.tenzo_hip_engine_trace(self.h, int(bool(on))), "engine_trace")
+
+    def get_trace(self) -> np.ndarray:
+        """[stages][nwg][2] wall-clock ticks (100 MHz): reach / leave the
+        barrier after each stage, for the last step."""
+        n = int(self.L.tenzo_hip_engine_get_trace(self.h, None, 0))
+        if n < 0:
+            raise RuntimeError("no trace (call trace(True) first)")
+        out = np.empty(n, np.uint64)
+        if self.L.tenzo_hip_engine_get_trace(self.h, _ptr(out), n) != n:
+            raise RuntimeError("get_trace failed")
+        stages = 5 * self.cfg.num_layers + 1
+        return out.reshape(stages, -1, 2)
 
     def stream(self) -> int:
         return int(self.L.tenzo_hip_engine_stream(self.h) or 0)

@@ -34,17 +34,18 @@ CFG = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=3, ffn=
                          vocab=2048, max_seq=64, theta=10000.0)
 
 
-@pytest.mark.parametrize("graph", [True, False])
-def test_engine_steps_match_oracle(eng_mod, graph):
+@pytest.mark.parametrize("mode", ["persistent", "graph", "eager"])
+def test_engine_steps_match_oracle(eng_mod, mode):
     sm = synth.make_model(CFG, seed=41, ctx=9)
     om = oracle.OracleModel(sm, f16_kv_scales=True)
     with eng_mod.Engine(CFG) as e:
         e.set_model(sm)
-        e.use_graph(graph)
+        e.set_mode(mode)
+        assert e.mode == mode
         assert e.seq_len == 9
         tok = 5
         for i in range(6):
-            print(f"step {i} graph={graph}", flush=True)
+            print(f"step {i} mode={mode}", flush=True)
             got = e.step(tok)
             ref_tok, ref_logits, ref_hidden = om.step(tok, sm.ctx + i, CFG.theta)
             assert rel(e.buffer("x"), ref_hidden) < 1e-3
@@ -58,6 +59,73 @@ def test_engine_steps_match_oracle(eng_mod, graph):
             new_g, new_r = g[:, :, 9:15].astype(int), r[:, :, 9:15].astype(int)
             assert (new_g != new_r).mean() < 0.01 and np.abs(new_g - new_r).max() <= 1
         np.testing.assert_array_equal(kc[:, :, :9], sm.kc[:, :, :9])
+
+
+@pytest.mark.parametrize("hidden,Hq,Hkv,ctx", [(512, 4, 4, 30), (512, 4, 2, 300), (1024, 8, 1, 700),
+                                               (1024, 8, 8, 4000), (512, 4, 1, 1)])
+def test_persistent_head_layouts_and_context(eng_mod, hidden, Hq, Hkv, ctx):
+    """Persistent kernel for every GQA group size (1, 2, 4, 8), a context whose
+    chunks are longer than the preloaded rounds (8 kv heads at 4000), and a
+    first token (context 1)."""
+    cfg = synth.DecodeConfig(hidden=hidden, n_q_heads=Hq, n_kv_heads=Hkv, n_layers=2, ffn=768,
+                             vocab=1000, max_seq=ctx + 4, theta=10000.0)
+    print(f"persistent H={hidden} Hq={Hq} Hkv={Hkv} ctx={ctx}", flush=True)
+    sm = synth.make_model(cfg, seed=ctx + Hkv, ctx=ctx - 1)
+    om = oracle.OracleModel(sm, f16_kv_scales=True)
+    with eng_mod.Engine(cfg) as e:
+        e.set_model(sm)
+        assert e.mode == "persistent"
+        tok = 17
+        for i in range(3):
+            got = e.step(tok)
+            ref_tok, ref_logits, ref_hidden = om.step(tok, sm.ctx + i, cfg.theta)
+            assert rel(e.buffer("x"), ref_hidden) < 1e-3
+            assert rel(e.logits(), ref_logits) < 1e-3
+            assert got == ref_tok
+            tok = got
+
+
+def test_modes_agree(eng_mod):
+    """Persistent, graph and eager steps of one model: integer stages equal,
+    fp32 outputs equal up to the attention reduction order."""
+    sm = synth.make_model(CFG, seed=53, ctx=20)
+    outs = {}
+    for mode in ("persistent", "graph", "eager"):
+        with eng_mod.Engine(CFG) as e:
+            e.set_model(sm)
+            e.set_mode(mode)
+            toks = [e.step(t) for t in (3, 1, 4, 1, 5)]
+            outs[mode] = (toks, e.logits(), e.buffer("x"), e.get_kv(25))
+    p, g, z = outs["persistent"], outs["graph"], outs["eager"]
+    assert p[0] == g[0] == z[0]
+    np.testing.assert_array_equal(g[1], z[1])  # same kernels, same chunking
+    assert rel(p[1], g[1]) < 1e-5 and rel(p[2], g[2]) < 1e-5
+    for a, b in zip(p[3], g[3]):
+        assert (np.asarray(a) != np.asarray(b)).mean() < 0.01
+
+
+@pytest.mark.parametrize("mode", ["persistent", "graph", "eager"])
+def test_chained_decode_equals_steps(eng_mod, mode):
+    """tenzo_hip_engine_decode (tokens fed back on the device) produces the
+    same tokens, logits and cache as one generate_step per token."""
+    sm = synth.make_model(CFG, seed=57, ctx=11)
+    with eng_mod.Engine(CFG) as a, eng_mod.Engine(CFG) as b:
+        a.set_model(sm)
+        b.set_model(sm)
+        a.set_mode(mode)
+        b.set_mode(mode)
+        toks, ms = a.decode(7, 9)
+        assert ms > 0 and a.seq_len == 20
+        ref, t = [], 7
+        for _ in range(9):
+            t = b.step(t)
+            ref.append(t)
+        assert list(toks) == ref
+        np.testing.assert_array_equal(a.logits(), b.logits())
+        for x, y in zip(a.get_kv(20), b.get_kv(20)):
+            np.testing.assert_array_equal(x, y)
+        # the next step continues from the chained state
+        assert a.step(int(toks[-1])) == b.step(ref[-1])
 
 
 def test_engine_first_layer_stages_bit_exact(eng_mod):
