@@ -216,13 +216,13 @@ float orc_tl1_gemv(const float* x, const uint8_t* w, int64_t N, int64_t K, float
 /* ------------------------------------------------------------------------- */
 
 float orc_sumsq(const float* x, int64_t n) {
-    float p[256];
-    for (int t = 0; t < 256; ++t) {
+    float p[1024];
+    for (int t = 0; t < 1024; ++t) {
         float s = 0.0f;
-        for (int64_t i = t; i < n; i += 256) s = fmaf(x[i], x[i], s);
+        for (int64_t i = t; i < n; i += 1024) s = fmaf(x[i], x[i], s);
         p[t] = s;
     }
-    for (int w = 128; w >= 1; w >>= 1)       /* balanced pairwise tree */
+    for (int w = 512; w >= 1; w >>= 1)       /* balanced pairwise tree */
         for (int t = 0; t < w; ++t) p[t] = p[2 * t] + p[2 * t + 1];
     return p[0];
 }

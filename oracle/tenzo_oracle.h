@@ -77,8 +77,10 @@ float orc_tl1_gemv(const float* x, const uint8_t* w, int64_t N, int64_t K, float
                    float* y, int32_t* acc);
 
 /* ---- RMSNorm (rms_norm_raw, :148-166) ---- */
-/* Sum of squares in a fixed order: 256 strided partials p[t] = fma-accumulated
- * x[t], x[t+256], ..., then a balanced pairwise tree over p[0..255]. */
+/* Sum of squares in a fixed order: 1024 strided partials p[t] = fma-accumulated
+ * x[t], x[t+1024], ..., then a balanced pairwise tree over p[0..1023]. (The
+ * reference's order is compiler-chosen under -ffast-math; this one is pinned to
+ * it at 2e-6 and is the order every GPU kernel of this repo uses.) */
 float orc_sumsq(const float* x, int64_t n);
 void orc_rms_norm(const float* x, const float* w, float* y, int64_t dim, float eps);
 

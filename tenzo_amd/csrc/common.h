@@ -82,14 +82,22 @@ __device__ __forceinline__ float wave_max(float v) {
 }
 
 // Sum of squares of x[0..n) in the fixed order shared with the CPU oracle
-// (orc_sumsq): thread t of 256 fma-accumulates x[t], x[t+256], ...; then a
-// balanced pairwise tree over the 256 partials in thread order. Must be
+// (orc_sumsq): 1024 strided partials p[m] = fma-accumulated x[m], x[m+1024],
+// ...; then a balanced pairwise tree over p[0..1023] in index order. Thread t
+// of 256 owns p[4t..4t+3] (and adds them as the tree's first two levels); the
+// butterfly over the wave and the 4-wave sum are the remaining levels. Must be
 // called by all threads of a 256-thread block; `red` is 4 floats of LDS.
 __device__ __forceinline__ float block256_sumsq(const float* __restrict__ x, int64_t n,
                                                 float* red) {
     const int t = threadIdx.x;
-    float s = 0.0f;
-    for (int64_t i = t; i < n; i += 256) s = __builtin_fmaf(x[i], x[i], s);
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+    for (int64_t i = 4 * t; i < n; i += 1024) {
+        p0 = __builtin_fmaf(x[i], x[i], p0);
+        if (i + 1 < n) p1 = __builtin_fmaf(x[i + 1], x[i + 1], p1);
+        if (i + 2 < n) p2 = __builtin_fmaf(x[i + 2], x[i + 2], p2);
+        if (i + 3 < n) p3 = __builtin_fmaf(x[i + 3], x[i + 3], p3);
+    }
+    float s = (p0 + p1) + (p2 + p3);
     s = wave_sum_tree(s);
     if ((t & 63) == 0) red[t >> 6] = s;
     __syncthreads();

@@ -33,12 +33,15 @@ struct DsParams {
     float* part;                // [Hkv][C][G][kDsPartStride] attention partials
     float2* am_part;            // [nwg] argmax partials
     unsigned* sync;             // ds_sync_words() words, zero before each launch
+    int* acc;                   // ds_acc_words() int32 GEMV accumulators, zero before
+                                // each launch: per layer q|k|v, o, gate|up, down
     int32_t* io;                // [0] token in, [2] greedy token out (also copied to [0])
     int32_t* out_tokens;        // optional: the greedy token is also stored at [step]
     int step;
     int H, F, Hq, Hkv, L, V, max_seq;
     int pos, C, T;              // this step's position and attention chunking
     int nwg;
+    int split[4];               // K slices per row block of the QKV, O, GU, DOWN GEMVs
     int with_head;              // 0: stop after the layers (prefill)
     float eps;
     // optional step trace: for stage s and workgroup w, [(s * nwg + w) * 2]
@@ -51,8 +54,14 @@ constexpr int kDsThreads = 256;
 constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
 constexpr int kDsCounters = 16;
 
-// uint32 words of the sync region for L layers and Hkv kv heads.
+// uint32 words of the sync region for L layers and Hkv kv heads (a multiple of
+// 64, so the accumulators can follow it in one allocation).
 size_t ds_sync_words(int L, int Hkv);
+// int32 words of the accumulator region.
+size_t ds_acc_words(int L, int H, int F, int Hq, int Hkv);
+// K slices per row block for each GEMV stage (fills p.split from the shapes
+// and p.nwg).
+void ds_plan_splits(DsParams& p);
 // Workgroup count the kernel runs with on the current device (a multiple of
 // kDsCounters, all co-resident), or 0 when cooperative launch is unavailable.
 int ds_grid_size();

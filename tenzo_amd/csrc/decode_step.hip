@@ -5,38 +5,53 @@
 // whole step.
 //
 // Schedule. The step is a sequence of stages: per layer QKV, ATT, O, GU
-// (gate|up), DOWN, then HEAD. Each stage has a list of tasks (a 64-row block
-// of a TL1 matrix, an attention chunk of one kv head, a row block of the LM
-// head); stage s's tasks go to workgroups off_s, off_s+1, ... (mod nwg) with
-// off_{s+1} = off_s + ntasks_s, so consecutive stages mostly use different
-// workgroups. A workgroup issues the loads of its weight tile first thing in a
-// stage, so they are in flight while it reads and normalizes the stage input.
-// Per stage each CU reads at most ~110 KB of weights: the critical path is the
-// chain of barriers and input reads, not bandwidth.
+// (gate|up), DOWN, then HEAD. Each stage has a list of tasks; stage s's tasks
+// go to workgroups off_s, off_s+1, ... (mod nwg) with off_{s+1} = off_s +
+// ntasks_s, so consecutive stages mostly use different workgroups. A GEMV
+// task is one K slice of a 64-row block of a TL1 matrix: the row blocks of
+// the Q|K|V, O and down projections are split along K so that every CU has a
+// task, and the slices' exact int32 sums meet in an accumulator through
+// integer atomics (addition of integers is exact, so the result does not
+// depend on the order of arrival). An attention task is a chunk of the
+// context of one kv head; an LM-head task a 64-row block.
 //
-// Synchronisation. Stage outputs are written with device-coherent stores and
-// read with device-coherent loads (sc1: through to the memory side, so no
-// L2 write-back / invalidate fence is needed); before arriving at a barrier
-// every wave waits for its stores to be acknowledged (s_waitcnt). The barrier
-// is 16 counters on separate 256-byte lines (one per workgroup residue mod
-// 16) polled together by one wave. The attention split-K combine is done by
+// Data flow. GEMV outputs stay as int32 accumulators; the stage that reads
+// them applies the epilogue y = float(acc - code_sum) * (inv_scale * w_scale)
+// (the GEMV's own rounding steps) using the (inv_scale, code_sum) record the
+// producing stage published, and adds the residual. Each stage input is built
+// in registers (thread t owns float4 groups t, t+256, ...), normalized and
+// quantized there: the RMSNorm sum of squares follows the fixed 1024-partial
+// order of the CPU oracle, which is exactly this ownership. Vectors later
+// stages need as floats (x, h1, q|k|v, gate|up) are stored by the workgroups
+// of the stage that builds them, 64-element slices spread over those
+// workgroups.
+//
+// Latency. A workgroup issues the read-only loads of a stage (its first
+// weight or KV tile, the norm weights) together with the loads of the stage
+// input, so each stage costs one memory round trip before its arithmetic.
+//
+// Synchronisation. Data produced inside the launch is written with
+// device-coherent stores / atomics and read with device-coherent loads (sc1:
+// served from the memory side, so no L2 write-back / invalidate fence is
+// needed); before arriving at a barrier every wave waits for its stores to be
+// acknowledged (s_waitcnt). The barrier is 16 counters on separate 256-byte
+// lines polled together by one wave. The attention split-K merge is done by
 // the last workgroup to finish a kv head (a per-head arrival counter). Every
 // wait is bounded: on timeout a workgroup raises the error word and all
 // others abort at their next poll, so the grid always drains.
 //
 // Arithmetic is the reference's, in the same rounding steps as the
-// multi-kernel path (tl1.hip, attention.hip, lm_head.hip): RMSNorm with the
-// fixed 256-partial summation order, +-31 / +-127 activation codes, exact
-// int32 TL1 / int8 sums, fp32 epilogues.
+// multi-kernel path (tl1.hip, attention.hip, lm_head.hip).
 #include "attention.h"
 #include "decode_step.h"
 
 namespace tz {
 namespace {
 
-constexpr int kT = kDsThreads;   // 512 threads = 8 waves
+constexpr int kT = kDsThreads;   // 256 threads = 4 waves
 constexpr int kW = kT / 64;
-constexpr int kPF = 10;          // tile uint4 per lane preloaded (all of K <= 2560)
+constexpr int kPF = 10;          // tile uint4 per lane preloaded
+constexpr int kJ = 8;            // float4 groups per thread: vectors up to 8192
 constexpr int kNC = kDsCounters;
 constexpr int kD = 128;
 constexpr int kPS = kDsPartStride;  // partial record: m, l, -, -, o[128]
@@ -46,9 +61,23 @@ constexpr int kAR = 4;           // attention rounds preloaded in registers
 constexpr unsigned kSpinLimit = 1u << 22;
 constexpr float kAttnScale = 0.08838834764831845f;  // 1/sqrt(128)
 
+// threadIdx.x behind an empty asm: values derived from it are recomputed in
+// each stage instead of being hoisted out of the stage loop (which would keep
+// them live, in registers, for the whole kernel).
+__device__ __forceinline__ int ltid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+// The wave index, known to the compiler to be the same in every lane.
+__device__ __forceinline__ int lwave() { return __builtin_amdgcn_readfirstlane(ltid() >> 6); }
+
 enum Stage { S_QKV = 0, S_ATT = 1, S_O = 2, S_GU = 3, S_DOWN = 4, S_HEAD = 5 };
 
 __device__ __forceinline__ float ldc(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ldci(const int* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void stc(float* p, float v) {
@@ -57,115 +86,82 @@ __device__ __forceinline__ void stc(float* p, float v) {
 __device__ __forceinline__ unsigned ldcu(const unsigned* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void stcu(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
-// Device-coherent 16-byte loads through a raw buffer resource (cache policy
-// sc1: the read is served from the memory side, as the relaxed agent-scope
-// atomics above). Lanes past the resource's byte count read zeros.
+// Device-coherent 16-byte loads and stores through a raw buffer resource
+// (cache policy sc1: served from / written through to the memory side, as the
+// relaxed agent-scope atomics above). Loads past the resource's byte count
+// read zeros.
 typedef float f4v __attribute__((ext_vector_type(4)));
+typedef int i4v __attribute__((ext_vector_type(4)));
+typedef unsigned u4v __attribute__((ext_vector_type(4)));
 constexpr int kRsrcWord3 = 0x00020000;  // raw buffer, gfx9 family
+constexpr int kSc1 = 16;                // cache-policy bit sc1
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, kRsrcWord3);
 }
 __device__ __forceinline__ f4v ldc16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-    return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+    return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1));
 }
-
-// dst[0..n) = src[0..n) (n % 4 == 0, src 16-byte aligned), all loads of a
-// thread issued before any is used.
-__device__ __forceinline__ void load_vec(float* dst, const float* src, int n) {
-    constexpr int U = 8;
-    const __amdgpu_buffer_rsrc_t r = rsrc(src, (uint32_t)n * 4);
-    const int n4 = n >> 2;
-    for (int base = threadIdx.x; base < n4; base += U * kDsThreads) {
-        f4v v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = ldc16(r, (uint32_t)(base + u * kDsThreads) * 16);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = base + u * kDsThreads;
-            if (i < n4) {
-                dst[4 * i] = v[u].x;
-                dst[4 * i + 1] = v[u].y;
-                dst[4 * i + 2] = v[u].z;
-                dst[4 * i + 3] = v[u].w;
-            }
-        }
-    }
+__device__ __forceinline__ i4v ldc16i(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(i4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kSc1));
 }
-
-// dst[0..n) = src[0..n) for read-only data (the norm weights), plain loads
-// issued together. n % 4 == 0, src 16-byte aligned.
-__device__ __forceinline__ void load_ro(float* dst, const float* __restrict__ src, int n) {
-    constexpr int U = 8;
-    const int n4 = n >> 2;
-    const float4* s4 = reinterpret_cast<const float4*>(src);
-    for (int base = threadIdx.x; base < n4; base += U * kDsThreads) {
-        float4 v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = base + u * kDsThreads;
-            if (i < n4) v[u] = s4[i];
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int i = base + u * kDsThreads;
-            if (i < n4) {
-                dst[4 * i] = v[u].x;
-                dst[4 * i + 1] = v[u].y;
-                dst[4 * i + 2] = v[u].z;
-                dst[4 * i + 3] = v[u].w;
-            }
-        }
-    }
+__device__ __forceinline__ int ldc4i(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kSc1);
 }
-
-// dst[i] = max(0, gate[i])^2 * up[i] (:1616-1620) for the gate | up vector.
-__device__ __forceinline__ void load_act(float* dst, const float* gu, int F) {
-    constexpr int U = 8;
-    const __amdgpu_buffer_rsrc_t r = rsrc(gu, (uint32_t)F * 8);
-    const int n4 = F >> 2;
-    for (int base = threadIdx.x; base < n4; base += U * kDsThreads) {
-        f4v g[U], u[U];
-#pragma unroll
-        for (int k = 0; k < U; ++k) {
-            const uint32_t off = (uint32_t)(base + k * kDsThreads) * 16;
-            g[k] = ldc16(r, off);
-            u[k] = ldc16(r, off + (uint32_t)F * 4);
-        }
-#pragma unroll
-        for (int k = 0; k < U; ++k) {
-            const int i = base + k * kDsThreads;
-            if (i < n4) {
-                const float gg[4] = {g[k].x, g[k].y, g[k].z, g[k].w};
-                const float uu[4] = {u[k].x, u[k].y, u[k].z, u[k].w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float rr = fmaxf(0.0f, gg[j]);
-                    dst[4 * i + j] = (rr * rr) * uu[j];
-                }
-            }
-        }
-    }
+// Plain (cached) loads of read-only data through a resource: out-of-range
+// lanes read zeros, so no branch is needed around them.
+__device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ uint32_t ld2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0);
+}
+__device__ __forceinline__ void stc16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v) {
+    const f4v w = {v.x, v.y, v.z, v.w};
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4v, w), r, byte_off, 0, kSc1);
 }
 
 // ---------------------------------------------------------------- layout --
+
+// The per-layer descriptors are read-only for the whole launch: reading them
+// through the constant address space lets the compiler use scalar loads.
+typedef __attribute__((address_space(4))) const DsLayer* LayerPtr;
+__device__ __forceinline__ LayerPtr layer(const DsParams& p, int l) {
+    return (LayerPtr)(p.layers + l);
+}
 
 __host__ __device__ inline size_t w_err(int, int) { return (size_t)kNC * 64; }
 __host__ __device__ inline size_t w_am(int, int) { return (size_t)(kNC + 1) * 64; }
 __host__ __device__ inline size_t w_head(int l, int h, int Hkv) {
     return (size_t)(kNC + 2 + l * Hkv + h) * 64;
 }
+// (inv_scale, code_sum) of the activation codes of GEMV stage `slot` of layer l
+__host__ __device__ inline size_t w_rec(int l, int slot, int L, int Hkv) {
+    return (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)(l * 4 + slot) * 2;
+}
+
+// Accumulator region of one layer: q|k|v, o, gate|up, down (int32 each).
+struct AccOff {
+    int o, gu, down, stride;
+};
+__host__ __device__ inline AccOff acc_off(int H, int F, int Hq, int Hkv) {
+    AccOff a;
+    a.o = (Hq + 2 * Hkv) * kD;
+    a.gu = a.o + H;
+    a.down = a.gu + 2 * F;
+    a.stride = a.down + H;
+    return a;
+}
 
 struct Shared {
-    float xs[8192];                 // stage input / normalized values
-    float ws[8192];                 // RMSNorm weights of the stage
     int8_t codes[8192] __attribute__((aligned(16)));
     int red_i[kW][64];
-    float red_f[kW];
-    int red_i8[kW];
-    float inv_scale;
-    int code_sum;
+    float red_a[kW], red_b[kW];
+    int red_c[kW];
     int flag;
 };
 
@@ -187,16 +183,17 @@ union SharedAll {
 
 // -------------------------------------------------------------- schedule --
 
-__device__ __forceinline__ int ntasks(const DsParams& p, int st) {
-    const int qd = p.Hq * kD, kvd = p.Hkv * kD;
-    switch (st) {
-        case S_QKV: return (qd + 2 * kvd) / 64;
-        case S_ATT: return p.Hkv * p.C;
-        case S_O: return p.H / 64;
-        case S_GU: return 2 * p.F / 64;
-        case S_DOWN: return p.H / 64;
-        default: return (p.V + 63) / 64;
-    }
+// Rows of the GEMV of stage slot 0..3 (QKV, O, GU, DOWN) and its K.
+__host__ __device__ inline int gemv_rows(int slot, int H, int F, int Hq, int Hkv) {
+    return slot == 0 ? (Hq + 2 * Hkv) * kD : slot == 2 ? 2 * F : H;
+}
+__host__ __device__ inline int gemv_k(int slot, int H, int F) { return slot == 3 ? F : H; }
+
+__device__ __forceinline__ int ntasks(const DsParams& p, int kind) {
+    if (kind == S_ATT) return p.Hkv * p.C;
+    if (kind == S_HEAD) return p.with_head ? (p.V + 63) / 64 : p.H / 64;
+    const int slot = kind == S_QKV ? 0 : kind - 1;
+    return gemv_rows(slot, p.H, p.F, p.Hq, p.Hkv) / 64 * p.split[slot];
 }
 
 // Stage index s = 5*layer + kind for the layers, 5*L for the head.
@@ -228,9 +225,7 @@ __device__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
                     break;
                 }
                 if (spins > kSpinLimit) {
-                    if (l == 0)
-                        __hip_atomic_store(p.sync + w_err(p.L, p.Hkv), 1u, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                    if (l == 0) stcu(p.sync + w_err(p.L, p.Hkv), 1u);
                     abort = true;
                     break;
                 }
@@ -242,82 +237,264 @@ __device__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
     return *s_abort == 0;
 }
 
+// ----------------------------------------------------------- prefetch -----
+
+// Loads kPF chunks per lane of K slice [c0, c1) of TL1 row block rb (KS
+// super-chunks of 64 columns per row block; wave w takes chunks c0+w, c0+w+4,
+// ...). Chunks past c1 read zeros.
+__device__ __forceinline__ void load_tl1_tile(uint4 (&pf)[kPF], const uint4* __restrict__ W,
+                                              int rb, int KS, int c0, int c1) {
+    const int lane = ltid() & 63, wave = lwave();
+    const __amdgpu_buffer_rsrc_t r =
+        rsrc(W + (size_t)rb * KS * 64, (uint32_t)c1 * 64 * 16);
+#pragma unroll
+    for (int i = 0; i < kPF; ++i)
+        pf[i] = ld16(r, (uint32_t)((c0 + wave + kW * i) * 64 + lane) * 16);
+}
+
+// Attention tile: the first kAR rounds of kRT tokens; lane (wave, l) holds 16
+// bytes of token r*kRT + wave*8 + l/8 at dims (l%8)*16 of K (pf[2r]) and V
+// (pf[2r+1]) and its two fp16 scales (pfs[r]). Tokens past the chunk read
+// zeros; the new token's slot is read but not used. Later rounds are read in
+// the loops that use them.
+__device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[kAR],
+                                              const DsParams& p, int l, int h, int c) {
+    const int lane = ltid() & 63, wave = lwave();
+    const int t0 = c * p.T;
+    const int nt = min(p.T, p.pos + 1 - t0);
+    const size_t tok0 = ((size_t)l * p.Hkv + h) * p.max_seq + t0;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(p.kc + tok0 * kD, (uint32_t)nt * kD);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(p.vc + tok0 * kD, (uint32_t)nt * kD);
+    const __amdgpu_buffer_rsrc_t rks = rsrc(p.ks + tok0, (uint32_t)nt * 2);
+    const __amdgpu_buffer_rsrc_t rvs = rsrc(p.vs + tok0, (uint32_t)nt * 2);
+    const int d0 = (lane & 7) * 16;
+#pragma unroll
+    for (int r = 0; r < kAR; ++r) {
+        const int tl = r * kRT + wave * 8 + (lane >> 3);
+        pf[2 * r] = ld16(rk, (uint32_t)(tl * kD + d0));
+        pf[2 * r + 1] = ld16(rv, (uint32_t)(tl * kD + d0));
+        pfs[r] = ld2(rks, (uint32_t)tl * 2) | (ld2(rvs, (uint32_t)tl * 2) << 16);
+    }
+}
+
+// Norm weights (thread t: float4 groups t + 256 j; zeros past K) into registers.
+__device__ __forceinline__ void load_norm_w(float4 (&w)[kJ], const float* nw, int K) {
+    if (!nw) return;
+    const __amdgpu_buffer_rsrc_t r = rsrc(nw, (uint32_t)K * 4);
+    const int t = ltid();
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const f4v v = __builtin_bit_cast(
+            f4v, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(t + kT * j) * 16, 0, 0));
+        w[j] = make_float4(v.x, v.y, v.z, v.w);
+    }
+}
+
 // ------------------------------------------------------------ prologue ----
 
-// Sum of squares of xs[0..K) in the order of the CPU oracle (orc_sumsq):
-// threads 0..255 accumulate strided partials, then a balanced tree.
-__device__ __forceinline__ float wg_sumsq(const float* xs, int K, float* red) {
-    const int t = threadIdx.x;
-    float s = 0.0f;
-    if (t < 256)
-        for (int i = t; i < K; i += 256) s = __builtin_fmaf(xs[i], xs[i], s);
-    s = wave_sum_tree(s);
-    if ((t & 63) == 0 && t < 256) red[t >> 6] = s;
-    __syncthreads();
-    const float r = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return r;
+__device__ __forceinline__ void read_rec(const DsParams& p, int l, int slot, float& inv,
+                                         int& csum) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(p.sync + w_rec(l, slot, p.L, p.Hkv), 8);
+    inv = __int_as_float(ldc4i(r, 0));
+    csum = ldc4i(r, 4);
 }
 
-__device__ __forceinline__ float wg_max(float v, float* red) {
-    v = wave_max(v);
-    const int t = threadIdx.x;
-    if ((t & 63) == 0) red[t >> 6] = v;
-    __syncthreads();
-    float r = red[0];
+// Element of a GEMV output from its accumulator (TenzoEngine.cpp:1554,
+// :118-126): float(acc - code_sum) * (inv_scale * w_scale).
+__device__ __forceinline__ float gemv_y(int a, int csum, float invsc) {
+    return (float)(a - csum) * invsc;
+}
+
+// The loaders below issue all kJ loads of a thread unconditionally (lanes past
+// K read zeros through the resource bounds) and leave zeros in v past K, so
+// no branch joins sit between the loads and their uses.
+
+// v = base + GEMV output (the residual adds :1590, :1628); the output's code
+// record is that of GEMV stage `slot` of layer l, w_scale its weight scale.
+__device__ __forceinline__ void load_resid(float4 (&v)[kJ], const DsParams& p, const float* base,
+                                           const int* acc, int K, int l, int slot, float wsc) {
+    const int t = ltid(), K4 = K >> 2;
+    const __amdgpu_buffer_rsrc_t rb = rsrc(base, (uint32_t)K * 4);
+    const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)K * 4);
+    f4v b[kJ];
+    i4v a[kJ];
 #pragma unroll
-    for (int w = 1; w < kW; ++w) r = fmaxf(r, red[w]);
-    __syncthreads();
-    return r;
-}
-
-__device__ __forceinline__ int wg_sum_i(int v, int* red) {
-    v = wave_sum_i32(v);
-    const int t = threadIdx.x;
-    if ((t & 63) == 0) red[t >> 6] = v;
-    __syncthreads();
-    int r = 0;
+    for (int j = 0; j < kJ; ++j) {
+        b[j] = ldc16(rb, (uint32_t)(t + kT * j) * 16);
+        a[j] = ldc16i(ra, (uint32_t)(t + kT * j) * 16);
+    }
+    float inv;
+    int csum;
+    read_rec(p, l, slot, inv, csum);
+    const float invsc = inv * wsc;
 #pragma unroll
-    for (int w = 0; w < kW; ++w) r += red[w];
-    __syncthreads();
-    return r;
+    for (int j = 0; j < kJ; ++j) {
+        const bool in = t + kT * j < K4;
+        v[j].x = in ? b[j].x + gemv_y(a[j].x, csum, invsc) : 0.0f;
+        v[j].y = in ? b[j].y + gemv_y(a[j].y, csum, invsc) : 0.0f;
+        v[j].z = in ? b[j].z + gemv_y(a[j].z, csum, invsc) : 0.0f;
+        v[j].w = in ? b[j].w + gemv_y(a[j].w, csum, invsc) : 0.0f;
+    }
 }
 
-// xs[0..K) holds the stage input. Normalizes in place (rms_norm_raw with
-// weight w, :148-166) and quantizes to codes (QMAX 31: build_lut :28-42,
-// QMAX 127: compute_logits :1666-1678), codes zero-padded to a multiple of 64.
-// w is the LDS copy of the norm weights, or null for none.
+__device__ __forceinline__ void load_plain(float4 (&v)[kJ], const float* src, int K) {
+    const int t = ltid();
+    const __amdgpu_buffer_rsrc_t r = rsrc(src, (uint32_t)K * 4);
+    f4v b[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) b[j] = ldc16(r, (uint32_t)(t + kT * j) * 16);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) v[j] = make_float4(b[j].x, b[j].y, b[j].z, b[j].w);
+}
+
+// embedding_lookup (:1294-1316) of token io[0] from the packed int8 LM head
+// (lm_head.hip layout: [V/64][H/16][64 rows][16 bytes]).
+__device__ __forceinline__ void load_embed(float4 (&v)[kJ], const DsParams& p) {
+    const int t = ltid(), K4 = p.H >> 2;
+    const int tok = p.io[0];
+    const float es = p.head_scales[tok];
+    const uint8_t* hb = reinterpret_cast<const uint8_t*>(p.head);
+    const size_t b = tok >> 6, r = tok & 63;
+    // row r of block b: 16 bytes every 1 KiB
+    const __amdgpu_buffer_rsrc_t rr = rsrc(hb + (b * (p.H / 16) * 64 + r) * 16,
+                                           (uint32_t)(p.H / 16) * 1024);
+    uint32_t w[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const int i = 4 * (t + kT * j);
+        w[j] = __builtin_amdgcn_raw_buffer_load_b32(rr, (uint32_t)((i >> 4) * 1024 + (i & 15)), 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const bool in = t + kT * j < K4;
+        v[j].x = in ? (float)(int8_t)(w[j] & 0xff) * es : 0.0f;
+        v[j].y = in ? (float)(int8_t)((w[j] >> 8) & 0xff) * es : 0.0f;
+        v[j].z = in ? (float)(int8_t)((w[j] >> 16) & 0xff) * es : 0.0f;
+        v[j].w = in ? (float)(int8_t)(w[j] >> 24) * es : 0.0f;
+    }
+}
+
+// Stores the 64-element slices of v (K elements, float4 groups as owned
+// above) whose index, counted from slice0, is f modulo m, into dst.
+__device__ __forceinline__ void store_slices(float* dst, const float4 (&v)[kJ], int K, int slice0,
+                                             int f, int m) {
+    const int t = ltid(), K4 = K >> 2;
+    const __amdgpu_buffer_rsrc_t r = rsrc(dst, (uint32_t)K * 4);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const int q = t + kT * j;
+        if (q < K4 && (slice0 + (q >> 4)) % m == f) stc16(r, (uint32_t)q * 16, v[j]);
+    }
+}
+
+// relu(gate)^2 * up (:1616-1620) from the gate|up accumulators; the gate and
+// up values are also stored as floats (slices as in store_slices).
+__device__ __forceinline__ void load_act(float4 (&v)[kJ], const DsParams& p, const int* acc,
+                                         int l, float wg, float wu, int f, int m) {
+    const int t = ltid(), F = p.F, K4 = F >> 2;
+    const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)F * 8);
+    const __amdgpu_buffer_rsrc_t rg = rsrc(p.gu, (uint32_t)F * 8);
+    i4v g[kJ], u[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        g[j] = ldc16i(ra, (uint32_t)(t + kT * j) * 16);
+        u[j] = ldc16i(ra, (uint32_t)(t + kT * j) * 16 + (uint32_t)F * 4);
+    }
+    float inv;
+    int csum;
+    read_rec(p, l, 2, inv, csum);
+    const float sg = inv * wg, su = inv * wu;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const int q = t + kT * j;
+        const bool in = q < K4;
+        const float4 gv = make_float4(gemv_y(g[j].x, csum, sg), gemv_y(g[j].y, csum, sg),
+                                      gemv_y(g[j].z, csum, sg), gemv_y(g[j].w, csum, sg));
+        const float4 uv = make_float4(gemv_y(u[j].x, csum, su), gemv_y(u[j].y, csum, su),
+                                      gemv_y(u[j].z, csum, su), gemv_y(u[j].w, csum, su));
+        if (in && (q >> 4) % m == f) stc16(rg, (uint32_t)q * 16, gv);
+        if (in && (F / 64 + (q >> 4)) % m == f) stc16(rg, (uint32_t)q * 16 + (uint32_t)F * 4, uv);
+        float r;
+        r = fmaxf(0.0f, gv.x);
+        v[j].x = in ? (r * r) * uv.x : 0.0f;
+        r = fmaxf(0.0f, gv.y);
+        v[j].y = in ? (r * r) * uv.y : 0.0f;
+        r = fmaxf(0.0f, gv.z);
+        v[j].z = in ? (r * r) * uv.z : 0.0f;
+        r = fmaxf(0.0f, gv.w);
+        v[j].w = in ? (r * r) * uv.w : 0.0f;
+    }
+}
+
 template <int QMAX>
-__device__ void norm_quant(SharedAll& sh, int K, const float* w, float eps) {
-    Shared& s = sh.s;
-    const int t = threadIdx.x;
-    const float inv_rms = inv_rms_from_sumsq(wg_sumsq(s.xs, K, s.red_f), K, eps);
-    float amax = QMAX == 31 ? 1e-6f : 1e-8f;
-    for (int i = t; i < K; i += kT) {
-        const float y = norm_apply(s.xs[i], inv_rms, w, i);
-        s.xs[i] = y;
-        amax = fmaxf(amax, fabsf(y));
-    }
-    amax = wg_max(amax, s.red_f);
-    const float scale = (float)QMAX / amax;
-    const int Kp = (K + 63) & ~63;
-    int csum = 0;
-    for (int i = t; i < Kp; i += kT) {
-        int c = 0;
-        if (i < K) {
-            float r = roundf(s.xs[i] * scale);
-            if (QMAX == 127) r = fminf(fmaxf(r, -128.0f), 127.0f);
-            c = (int)r;
+__device__ __forceinline__ int act_code(float y, float scale) {
+    float r = roundf(y * scale);
+    if (QMAX == 127) r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return (int)r;
+}
+
+// Normalizes v (K elements, zeros past K; rms_norm_raw :148-166 with weight w
+// when has_w) and quantizes it into s.codes (QMAX 31: build_lut :28-42; QMAX 127:
+// compute_logits :1666-1678). The sum of squares is taken in the fixed order
+// of the CPU oracle (orc_sumsq): thread t's chains p0..p3 over its groups are
+// the partials 4t..4t+3, then the balanced tree in index order.
+template <int QMAX>
+__device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const float4 (&w)[kJ],
+                                           bool has_w, int K, float eps, float& inv_out,
+                                           int& csum_out) {
+    const int t = ltid(), lane = t & 63, wave = lwave();
+    const int J = ((K >> 2) + kT - 1) / kT;  // groups in use (wave-uniform)
+    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < J) {
+            p0 = __builtin_fmaf(v[j].x, v[j].x, p0);
+            p1 = __builtin_fmaf(v[j].y, v[j].y, p1);
+            p2 = __builtin_fmaf(v[j].z, v[j].z, p2);
+            p3 = __builtin_fmaf(v[j].w, v[j].w, p3);
         }
-        s.codes[i] = (int8_t)c;
-        csum += c;
-    }
-    csum = wg_sum_i(csum, s.red_i8);
-    if (t == 0) {
-        s.inv_scale = amax * (1.0f / (float)QMAX);
-        s.code_sum = csum;
-    }
+    float ss = wave_sum_tree((p0 + p1) + (p2 + p3));
+    if (lane == 0) s.red_a[wave] = ss;
     __syncthreads();
+    static_assert(kW == 4, "the cross-wave sums below are for 4 waves");
+    ss = (s.red_a[0] + s.red_a[1]) + (s.red_a[2] + s.red_a[3]);
+    const float inv_rms = inv_rms_from_sumsq(ss, K, eps);
+    float amax = QMAX == 31 ? 1e-6f : 1e-8f;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < J) {
+            float4 y = make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
+                                   __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
+            if (has_w) {
+                y.x = __fmul_rn(y.x, w[j].x);
+                y.y = __fmul_rn(y.y, w[j].y);
+                y.z = __fmul_rn(y.z, w[j].z);
+                y.w = __fmul_rn(y.w, w[j].w);
+            }
+            v[j] = y;
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+        }
+    amax = wave_max(amax);
+    if (lane == 0) s.red_b[wave] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
+    const float scale = (float)QMAX / amax;
+    int csum = 0;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < J) {
+            const int c0 = act_code<QMAX>(v[j].x, scale), c1 = act_code<QMAX>(v[j].y, scale);
+            const int c2 = act_code<QMAX>(v[j].z, scale), c3 = act_code<QMAX>(v[j].w, scale);
+            *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) =
+                (uint32_t)(c0 & 0xff) | ((uint32_t)(c1 & 0xff) << 8) |
+                ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24);
+            csum += (c0 + c1) + (c2 + c3);
+        }
+    csum = wave_sum_i32(csum);
+    if (lane == 0) s.red_c[wave] = csum;
+    __syncthreads();
+    csum_out = (s.red_c[0] + s.red_c[1]) + (s.red_c[2] + s.red_c[3]);
+    inv_out = amax * (1.0f / (float)QMAX);
 }
 
 // ---------------------------------------------------------------- GEMV ----
@@ -345,44 +522,29 @@ __device__ __forceinline__ int dot64(const uint4 v, const int4* c4, int acc) {
     return acc;
 }
 
-// Loads the first kPF chunks per lane of TL1 row block rb (KS super-chunks).
-__device__ __forceinline__ void load_tl1_tile(uint4* pf, const uint4* __restrict__ W, int rb,
-                                              int KS) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint4* base = W + (size_t)rb * KS * 64 + lane;
-#pragma unroll
-    for (int i = 0; i < kPF; ++i) {
-        const int c = wave + kW * i;
-        if (c < KS) pf[i] = base[(size_t)c * 64];
-    }
-}
-
-// One TL1 row block: returns the exact int32 sum sum_k u_k a_k (u = w+1) in
-// wave 0, lane = row (other waves: 0).
-__device__ __forceinline__ int tl1_rowblock(SharedAll& sh, const uint4* cur,
-                                            const uint4* __restrict__ W, int rb, int KS) {
-    Shared& s = sh.s;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// K slice [c0, c1) of one TL1 row block: returns the exact int32 sum
+// sum_k u_k a_k (u = w+1) over the slice in wave 0, lane = row (other waves: 0).
+__device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
+                                            const uint4* __restrict__ W, int rb, int KS, int c0,
+                                            int c1) {
+    const int lane = ltid() & 63, wave = lwave();
     const int4* c4 = reinterpret_cast<const int4*>(s.codes);
     int acc = 0;
 #pragma unroll
     for (int i = 0; i < kPF; ++i) {
-        const int c = wave + kW * i;
-        if (c < KS) acc = dot64(cur[i], c4 + c * 4, acc);
+        const int c = c0 + wave + kW * i;
+        if (c < c1) acc = dot64(cur[i], c4 + c * 4, acc);
     }
-    // K beyond the preloaded window (the down projection): 8 loads in flight
-    const uint4* base = W + (size_t)rb * KS * 64 + lane;
-    for (int c0 = wave + kW * kPF; c0 < KS; c0 += 8 * kW) {
+    // K beyond the preloaded window: 8 loads in flight (past c1: zeros)
+    const __amdgpu_buffer_rsrc_t r = rsrc(W + (size_t)rb * KS * 64, (uint32_t)c1 * 64 * 16);
+    for (int cc = c0 + wave + kW * kPF; cc < c1; cc += 8 * kW) {
         uint4 v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int c = c0 + u * kW;
-            if (c < KS) v[u] = base[(size_t)c * 64];
-        }
+        for (int u = 0; u < 8; ++u) v[u] = ld16(r, (uint32_t)((cc + u * kW) * 64 + lane) * 16);
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int c = c0 + u * kW;
-            if (c < KS) acc = dot64(v[u], c4 + c * 4, acc);
+            const int c = cc + u * kW;
+            if (c < c1) acc = dot64(v[u], c4 + c * 4, acc);
         }
     }
     s.red_i[wave][lane] = acc;
@@ -394,6 +556,66 @@ __device__ __forceinline__ int tl1_rowblock(SharedAll& sh, const uint4* cur,
     }
     __syncthreads();
     return tot;
+}
+
+// One GEMV stage (QKV, O, GU or DOWN) of layer l for a workgroup whose first
+// task is `first` (< n): builds the stage input, stores the slices of it
+// later stages read, normalizes and quantizes it, publishes the code record
+// (task 0) and adds its tasks' K-slice sums into the accumulators.
+__device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int first, int n) {
+    Shared& s = sh.s;
+    const int tid = ltid(), lane = tid & 63, wave = lwave();
+    const LayerPtr Lw = layer(p, l);
+    const int slot = kind == S_QKV ? 0 : kind - 1;
+    const int K = gemv_k(slot, p.H, p.F);
+    const int m = min(n, p.nwg);
+    const AccOff ao = acc_off(p.H, p.F, p.Hq, p.Hkv);
+    int* accl = p.acc + (size_t)l * ao.stride;
+    const int S = p.split[slot];
+    const int KS = K / 64, KSs = (KS + S - 1) / S;
+    const uint4* W = Lw->mat[slot];
+    // read-only loads first (the first weight tile, the norm weights), then
+    // the stage input: one round trip for all of them
+    uint4 tile[kPF];
+    {
+        const int c0 = (first % S) * KSs;
+        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs));
+    }
+    float4 nwr[kJ];
+    load_norm_w(nwr, Lw->norm[slot], K);
+    float4 xv[kJ];
+    if (kind == S_QKV) {
+        if (l == 0) {
+            load_embed(xv, p);
+        } else {
+            load_resid(xv, p, p.h1, accl - ao.stride + ao.down, K, l - 1, 3, layer(p, l - 1)->sc[6]);
+        }
+        store_slices(p.x, xv, K, 0, first, m);
+    } else if (kind == S_O) {
+        load_plain(xv, p.attn, K);
+    } else if (kind == S_GU) {
+        load_resid(xv, p, p.x, accl + ao.o, K, l, 1, Lw->sc[3]);
+        store_slices(p.h1, xv, K, 0, first, m);
+    } else {
+        load_act(xv, p, accl + ao.gu, l, Lw->sc[4], Lw->sc[5], first, m);
+    }
+    float inv;
+    int csum;
+    norm_quant<31>(s, xv, nwr, Lw->norm[slot] != nullptr, K, p.eps, inv, csum);
+    if (first == 0 && tid == 0) {
+        unsigned* r = p.sync + w_rec(l, slot, p.L, p.Hkv);
+        stcu(r, __float_as_uint(inv));
+        stcu(r + 1, (unsigned)csum);
+    }
+    int* out = accl + (slot == 0 ? 0 : slot == 1 ? ao.o : slot == 2 ? ao.gu : ao.down);
+    for (int t = first; t < n; t += p.nwg) {
+        const int rb = t / S, c0 = (t % S) * KSs, c1 = min(KS, c0 + KSs);
+        if (t != first) load_tl1_tile(tile, W, rb, KS, c0, c1);
+        const int tot = tl1_rowblock(s, tile, W, rb, KS, c0, c1);
+        if (wave == 0)
+            __hip_atomic_fetch_add(out + rb * 64 + lane, tot, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // ----------------------------------------------------------- attention ----
@@ -419,59 +641,79 @@ __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
         for (int j = 0; j < 4; ++j) f[4 * i + j] = (float)(int8_t)((w[i] >> (8 * j)) & 0xff);
 }
 
-// Attention tile: the first kAR rounds of kRT tokens; lane (wave, l) holds 16
-// bytes of token r*kRT + wave*8 + l/8 at dims (l%8)*16 of K (pf[2r]) and V
-// (pf[2r+1]) and its two fp16 scales (pfs[r]). Later rounds are read in the
-// loops that use them.
-__device__ __forceinline__ void load_att_tile(uint4* pf, uint32_t* pfs, const DsParams& p,
-                                              int l, int h, int c) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int t0 = c * p.T;
-    const int ctx = p.pos + 1;
-    const int nt = min(p.T, ctx - t0);
-    const size_t head = ((size_t)l * p.Hkv + h) * p.max_seq;
-    const int d0 = (lane & 7) * 16;
-#pragma unroll
-    for (int r = 0; r < kAR; ++r) {
-        const int tl = r * kRT + wave * 8 + (lane >> 3);
-        const int t = t0 + tl;
-        if (tl < nt && t != p.pos) {
-            pf[2 * r] = *reinterpret_cast<const uint4*>(p.kc + (head + t) * kD + d0);
-            pf[2 * r + 1] = *reinterpret_cast<const uint4*>(p.vc + (head + t) * kD + d0);
-            pfs[r] = (uint32_t)p.ks[head + t] | ((uint32_t)p.vs[head + t] << 16);
-        }
-    }
-}
-
+// Attention of the G query heads of kv head h over context chunk c of layer
+// l (attention_int8_fused, :434-864): q|k|v from the QKV accumulators, RoPE,
+// the new token's K/V quantized and appended, chunk softmax and weighted
+// values; with several chunks the last one to finish merges the partials.
 template <int G>
-__device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4* cur,
-                          const uint32_t* curs, int l, int h, int c) {
+__device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[kPF],
+                          const uint32_t (&curs)[kAR], int l, int h, int c) {
     AttnShared& a = sh.a;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = ltid(), lane = tid & 63, wave = lwave();
     const int ctx = p.pos + 1;
     const int t0 = c * p.T;
     const int nt = min(p.T, ctx - t0);
     const int qd = p.Hq * kD, kvd = p.Hkv * kD;
     const float* rope = p.rope + (size_t)p.pos * kD;
     const size_t head = ((size_t)l * p.Hkv + h) * p.max_seq;
-    // RoPE on the G query heads (:460-481)
-    for (int i = tid; i < G * 64; i += kT) {
-        const int g = i >> 6, j = i & 63;
-        const float* qv = p.qkv + (size_t)(h * G + g) * kD;
-        const float x0 = ldc(qv + j), x1 = ldc(qv + j + 64);
-        const float cs = rope[j], sn = rope[64 + j];
-        a.qs[g][j] = __builtin_fmaf(x0, cs, -(x1 * sn));
-        a.qs[g][j + 64] = __builtin_fmaf(x0, sn, x1 * cs);
+    const LayerPtr Lw = layer(p, l);
+    const __amdgpu_buffer_rsrc_t racc =
+        rsrc(p.acc + (size_t)l * acc_off(p.H, p.F, p.Hq, p.Hkv).stride, (uint32_t)(qd + 2 * kvd) * 4);
+    // loads first: the q (and new k / v) accumulators, the rope row, the
+    // code record of the QKV stage
+    constexpr int kQ = (G * 64 + kT - 1) / kT;  // query pairs per thread
+    const __amdgpu_buffer_rsrc_t rr = rsrc(rope, kD * 4);
+    int qa[kQ][2];
+    float qc[kQ][2];
+#pragma unroll
+    for (int u = 0; u < kQ; ++u) {
+        const int i = tid + u * kT, g = (i >> 6) % G, j = i & 63;
+        const int row = (h * G + g) * kD;
+        qa[u][0] = ldc4i(racc, (uint32_t)(row + j) * 4);
+        qa[u][1] = ldc4i(racc, (uint32_t)(row + j + 64) * 4);
+        qc[u][0] = __int_as_float(ldc4i(rr, (uint32_t)j * 4));
+        qc[u][1] = __int_as_float(ldc4i(rr, (uint32_t)(j + 64) * 4));
+    }
+    const bool has_new = p.pos >= t0 && p.pos < t0 + nt;
+    const int krow = qd + (wave == 0 ? 0 : kvd) + h * kD;
+    const int ka0 = ldc4i(racc, (uint32_t)(krow + lane) * 4);
+    const int ka1 = ldc4i(racc, (uint32_t)(krow + lane + 64) * 4);
+    const float kc0 = __int_as_float(ldc4i(rr, (uint32_t)lane * 4));
+    const float ks0 = __int_as_float(ldc4i(rr, (uint32_t)(lane + 64) * 4));
+    float inv;
+    int cs;
+    read_rec(p, l, 0, inv, cs);
+    // RoPE on the G query heads (:460-481); chunk 0 also stores q as floats
+    {
+        const float sq = inv * Lw->sc[0];
+#pragma unroll
+        for (int u = 0; u < kQ; ++u) {
+            const int i = tid + u * kT;
+            if (i < G * 64) {
+                const int g = i >> 6, j = i & 63;
+                const size_t row = (size_t)(h * G + g) * kD;
+                const float x0 = gemv_y(qa[u][0], cs, sq);
+                const float x1 = gemv_y(qa[u][1], cs, sq);
+                if (c == 0) {
+                    stc(p.qkv + row + j, x0);
+                    stc(p.qkv + row + j + 64, x1);
+                }
+                const float cr = qc[u][0], sr = qc[u][1];
+                a.qs[g][j] = __builtin_fmaf(x0, cr, -(x1 * sr));
+                a.qs[g][j + 64] = __builtin_fmaf(x0, sr, x1 * cr);
+            }
+        }
     }
     // the new token: RoPE on k, quantize-append k and v (:482-533)
-    const bool has_new = p.pos >= t0 && p.pos < t0 + nt;
     if (has_new && wave < 2) {
-        const float* src = p.qkv + qd + (wave == 0 ? 0 : kvd) + (size_t)h * kD;
-        float x0 = ldc(src + lane), x1 = ldc(src + lane + 64);
+        const float sk = inv * Lw->sc[wave == 0 ? 1 : 2];
+        float x0 = gemv_y(ka0, cs, sk);
+        float x1 = gemv_y(ka1, cs, sk);
+        stc(p.qkv + krow + lane, x0);
+        stc(p.qkv + krow + lane + 64, x1);
         if (wave == 0) {
-            const float cs = rope[lane], sn = rope[64 + lane];
-            const float r0 = __builtin_fmaf(x0, cs, -(x1 * sn));
-            const float r1 = __builtin_fmaf(x0, sn, x1 * cs);
+            const float r0 = __builtin_fmaf(x0, kc0, -(x1 * ks0));
+            const float r1 = __builtin_fmaf(x0, ks0, x1 * kc0);
             x0 = r0;
             x1 = r1;
         }
@@ -638,14 +880,26 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4* cur,
     __syncthreads();
     if (!a.last) return;
     // merge (same formula as attn_combine_kernel): out = sum_c e^{m_c-M} o_c /
-    // sum_c e^{m_c-M} l_c. 1) every (chunk, head) statistic into LDS, loads
-    // issued together; 2) weights e^{m_c-M}, L per head; 3) o, a float4 of
-    // dims per thread, its chunks' loads issued 8 at a time.
+    // sum_c e^{m_c-M} l_c. The first kU chunks' o loads and every (chunk,
+    // head) statistic are issued together; the weights e^{m_c-M} and the
+    // denominators are formed in LDS while the o loads are in flight.
     const float* base = p.part + (size_t)h * p.C * G * stride;
     const __amdgpu_buffer_rsrc_t r = rsrc(base, (uint32_t)(p.C * G * stride) * 4);
     const int npairs = p.C * G;
     float* wts = &a.sc[0][0];  // [C][G] weights (the scores are no longer needed)
     float* lcs = wts + npairs;
+    constexpr int kSlots = G * kD / 4;                         // float4 slots of the G outputs
+    constexpr int kSplit = kT / kSlots > 0 ? kT / kSlots : 1;  // threads per slot
+    constexpr int kU = 8;
+    const int slot = tid % kSlots, part = tid / kSlots;
+    const int g_o = slot / (kD / 4), d4 = slot % (kD / 4);
+    const bool has_part = part < kSplit;
+    f4v ov[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {  // chunks past C read zeros (outside the resource)
+        const int cc = part + u * kSplit;
+        ov[u] = ldc16(r, (uint32_t)((cc * G + g_o) * stride + 4 + 4 * d4) * 4);
+    }
     for (int i0 = tid; i0 < npairs; i0 += 4 * kT) {
         f4v v[4];
 #pragma unroll
@@ -674,24 +928,31 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4* cur,
         if (lane == 0) a.mstat[g] = L;
     }
     __syncthreads();
-    constexpr int kSlots = G * kD / 4;          // float4 slots of the G outputs
-    constexpr int kSplit = kT / kSlots > 0 ? kT / kSlots : 1;  // threads per slot
-    const int slot = tid % kSlots, part = tid / kSlots;
     f4v acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (part < kSplit) {
-        const int g = slot / (kD / 4), d4 = slot % (kD / 4);
-        for (int c0 = part; c0 < p.C; c0 += 8 * kSplit) {
-            f4v v[8];
+    if (has_part) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kU; ++u) {
+            const int cc = part + u * kSplit;
+            if (cc < p.C) {
+                const float e = wts[cc * G + g_o];
+                acc4.x = __builtin_fmaf(e, ov[u].x, acc4.x);
+                acc4.y = __builtin_fmaf(e, ov[u].y, acc4.y);
+                acc4.z = __builtin_fmaf(e, ov[u].z, acc4.z);
+                acc4.w = __builtin_fmaf(e, ov[u].w, acc4.w);
+            }
+        }
+        for (int c0 = part + kU * kSplit; c0 < p.C; c0 += kU * kSplit) {
+            f4v v[kU];
+#pragma unroll
+            for (int u = 0; u < kU; ++u) {
                 const int cc = c0 + u * kSplit;
-                v[u] = ldc16(r, (uint32_t)((cc * G + g) * stride + 4 + 4 * d4) * 4);
+                v[u] = ldc16(r, (uint32_t)((cc * G + g_o) * stride + 4 + 4 * d4) * 4);
             }
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < kU; ++u) {
                 const int cc = c0 + u * kSplit;
                 if (cc < p.C) {
-                    const float e = wts[cc * G + g];
+                    const float e = wts[cc * G + g_o];
                     acc4.x = __builtin_fmaf(e, v[u].x, acc4.x);
                     acc4.y = __builtin_fmaf(e, v[u].y, acc4.y);
                     acc4.z = __builtin_fmaf(e, v[u].z, acc4.z);
@@ -701,7 +962,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4* cur,
         }
     }
     float* red = &a.ow[0][0][0];  // [kSplit][G*128]
-    if (part < kSplit) {
+    if (has_part) {
         red[part * G * kD + 4 * slot] = acc4.x;
         red[part * G * kD + 4 * slot + 1] = acc4.y;
         red[part * G * kD + 4 * slot + 2] = acc4.z;
@@ -734,191 +995,135 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
     }
 }
 
+// The head stage: the final hidden state x = h1 + down of the last layer
+// (stored as floats), then (with_head) the final RMSNorm, +-127 codes, the
+// int8 LM head over row blocks first, first+nwg, ... and the greedy argmax
+// (compute_logits :1660-1700, greedy :1745-1755): a partial per workgroup,
+// reduced by the last workgroup to arrive.
+__device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
+    Shared& s = sh.s;
+    const int tid = ltid(), lane = tid & 63, wave = lwave(), wg = blockIdx.x;
+    float best = -INFINITY;
+    int besti = INT_MAX;
+    if (first < n) {
+        const AccOff ao = acc_off(p.H, p.F, p.Hq, p.Hkv);
+        float4 nwr[kJ];
+        if (p.with_head) load_norm_w(nwr, p.final_norm, p.H);
+        float4 xv[kJ];
+        load_resid(xv, p, p.h1, p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H, p.L - 1, 3,
+                   layer(p, p.L - 1)->sc[6]);
+        float inv;
+        int cs;
+        store_slices(p.x, xv, p.H, 0, first, min(n, p.nwg));
+        if (!p.with_head) return;
+        norm_quant<127>(s, xv, nwr, p.final_norm != nullptr, p.H, p.eps, inv, cs);
+        const int HC = p.H / 16;
+        const int4* c4 = reinterpret_cast<const int4*>(s.codes);
+        for (int t = first; t < n; t += p.nwg) {
+            const uint4* wb = p.head + (size_t)t * HC * 64 + lane;
+            int acc = 0;
+            for (int c0 = wave; c0 < HC; c0 += 8 * kW) {
+                uint4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int c = c0 + u * kW;
+                    v[u] = c < HC ? wb[(size_t)c * 64] : make_uint4(0, 0, 0, 0);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int c = c0 + u * kW;
+                    if (c < HC) {
+                        const int4 a4 = c4[c];
+                        acc = sdot4(v[u].x, a4.x, acc);
+                        acc = sdot4(v[u].y, a4.y, acc);
+                        acc = sdot4(v[u].z, a4.z, acc);
+                        acc = sdot4(v[u].w, a4.w, acc);
+                    }
+                }
+            }
+            s.red_i[wave][lane] = acc;
+            __syncthreads();
+            if (wave == 0) {
+                int tot = 0;
+#pragma unroll
+                for (int w = 0; w < kW; ++w) tot += s.red_i[w][lane];
+                const int row = t * 64 + lane;
+                if (row < p.V) {
+                    const float val = (float)tot * (inv * p.head_scales[row]);
+                    p.logits[row] = val;
+                    am_combine(best, besti, val, row);
+                }
+            }
+            __syncthreads();
+        }
+    } else if (!p.with_head) {
+        return;
+    }
+    if (wave == 0) {
+        wave_argmax(best, besti);
+        if (lane == 0) {
+            stc(&p.am_part[wg].x, best);
+            stc(&p.am_part[wg].y, __int_as_float(besti));
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = __hip_atomic_fetch_add(p.sync + w_am(p.L, p.Hkv), 1u,
+                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s.flag = old == (unsigned)(p.nwg - 1);
+    }
+    __syncthreads();
+    if (s.flag && wave == 0) {
+        float v = -INFINITY;
+        int vi = INT_MAX;
+        for (int q = lane; q < p.nwg; q += 64)
+            am_combine(v, vi, ldc(&p.am_part[q].x), __float_as_int(ldc(&p.am_part[q].y)));
+        wave_argmax(v, vi);
+        if (lane == 0) {
+            p.io[2] = vi;
+            p.io[0] = vi;  // the next step's input when steps are chained
+            if (p.out_tokens) p.out_tokens[p.step] = vi;
+        }
+    }
+}
+
 // ---------------------------------------------------------------- kernel --
 
 template <int G>
 __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     __shared__ SharedAll sh;
     __shared__ int s_abort;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
     const int wg = blockIdx.x;
-    const int qd = p.Hq * kD, kvd = p.Hkv * kD;
-    const int KSH = p.H / 64, KSF = p.F / 64;
-    const int nstages = 5 * p.L + (p.with_head ? 1 : 0);
+    const int nstages = 5 * p.L + 1;
     unsigned gen = 0;
-
     int off = 0;  // first workgroup of the current stage
     for (int s = 0; s < nstages; ++s) {
         const int kind = kind_of(p, s);
         const int l = s / 5;
-        const int n = ntasks(p, s < 5 * p.L ? kind : S_HEAD);
+        const int n = ntasks(p, kind);
         const int first = (wg - off + p.nwg) % p.nwg;  // my first task index here
-        const bool have = first < n;
 
+        if (kind == S_HEAD) {
+            head_stage(sh, p, first, n);
+            if (p.trace && tid == 0) {
+                const uint64_t now = wall_clock64();
+                p.trace[((size_t)s * p.nwg + wg) * 2] = now;
+                p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = now;
+            }
+            return;
+        }
         if (kind == S_ATT) {
             for (int t = first; t < n; t += p.nwg) {
-                uint4 tile[2 * kAR];
+                uint4 tile[kPF];
                 uint32_t tiles[kAR];
                 load_att_tile(tile, tiles, p, l, t / p.C, t % p.C);
                 attn_task<G>(sh, p, tile, tiles, l, t / p.C, t % p.C);
                 __syncthreads();
             }
-        } else if (have || kind == S_HEAD) {
-            const DsLayer& Lw = p.layers[l < p.L ? l : 0];
-            const int slot = kind == S_QKV ? 0 : kind - 1;  // 0..3 for the TL1 stages
-            const uint4* W = kind == S_HEAD ? nullptr : Lw.mat[slot];
-            const int KS = slot == 3 ? KSF : KSH;
-            // the first weight tile is in flight while the input is normalized
-            uint4 tile[kPF];
-            if (kind != S_HEAD && have) load_tl1_tile(tile, W, first, KS);
-            // prologue: the stage input vector and the norm weights into LDS
-            // (all loads issued together), then norm + quantize
-            const float* nw = kind == S_HEAD ? p.final_norm : Lw.norm[slot];
-            int K = kind == S_DOWN ? p.F : p.H;
-            if (nw) load_ro(sh.s.ws, nw, K);
-            if (kind == S_QKV) {
-                if (l == 0) {  // embedding_lookup (:1294-1316) from the packed head
-                    const int tok = p.io[0];
-                    const float es = p.head_scales[tok];
-                    const uint8_t* hb = reinterpret_cast<const uint8_t*>(p.head);
-                    const size_t b = tok >> 6, r = tok & 63;
-                    for (int i = tid; i < p.H; i += kT) {
-                        const int8_t e =
-                            (int8_t)hb[((b * (p.H / 16) + (i >> 4)) * 64 + r) * 16 + (i & 15)];
-                        sh.s.xs[i] = (float)e * es;
-                    }
-                } else {
-                    load_vec(sh.s.xs, p.x, p.H);
-                }
-            } else if (kind == S_O) {
-                load_vec(sh.s.xs, p.attn, p.H);
-            } else if (kind == S_GU) {
-                load_vec(sh.s.xs, p.h1, p.H);
-            } else if (kind == S_DOWN) {
-                load_act(sh.s.xs, p.gu, p.F);
-            } else {  // S_HEAD
-                load_vec(sh.s.xs, p.x, p.H);
-            }
-            __syncthreads();
-            const float* nws = nw ? sh.s.ws : nullptr;
-            if (kind == S_HEAD) norm_quant<127>(sh, K, nws, p.eps);
-            else norm_quant<31>(sh, K, nws, p.eps);
-            const float inv = sh.s.inv_scale;
-            const int csum = sh.s.code_sum;
-
-            if (kind == S_HEAD) {
-                // int8 GEMV over row blocks wg, wg+nwg, ... with the greedy argmax
-                const int HC = p.H / 16;
-                const int4* c4 = reinterpret_cast<const int4*>(sh.s.codes);
-                float best = -INFINITY;
-                int besti = INT_MAX;
-                for (int t = first; t < n; t += p.nwg) {
-                    const uint4* wb = p.head + (size_t)t * HC * 64 + lane;
-                    int acc = 0;
-                    for (int c0 = wave; c0 < HC; c0 += 8 * kW) {
-                        uint4 v[8];
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            const int c = c0 + u * kW;
-                            v[u] = c < HC ? wb[(size_t)c * 64] : make_uint4(0, 0, 0, 0);
-                        }
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            const int c = c0 + u * kW;
-                            if (c < HC) {
-                                const int4 a4 = c4[c];
-                                acc = sdot4(v[u].x, a4.x, acc);
-                                acc = sdot4(v[u].y, a4.y, acc);
-                                acc = sdot4(v[u].z, a4.z, acc);
-                                acc = sdot4(v[u].w, a4.w, acc);
-                            }
-                        }
-                    }
-                    sh.s.red_i[wave][lane] = acc;
-                    __syncthreads();
-                    if (wave == 0) {
-                        int tot = 0;
-#pragma unroll
-                        for (int w = 0; w < kW; ++w) tot += sh.s.red_i[w][lane];
-                        const int row = t * 64 + lane;
-                        if (row < p.V) {
-                            const float val = (float)tot * (inv * p.head_scales[row]);
-                            p.logits[row] = val;
-                            am_combine(best, besti, val, row);
-                        }
-                    }
-                    __syncthreads();
-                }
-                // per-workgroup partial, then the last workgroup reduces (:1745-1755)
-                if (wave == 0) {
-                    wave_argmax(best, besti);
-                    if (lane == 0) {
-                        stc(&p.am_part[wg].x, best);
-                        stc(&p.am_part[wg].y, __int_as_float(besti));
-                    }
-                }
-                __builtin_amdgcn_s_waitcnt(0);
-                __syncthreads();
-                if (tid == 0) {
-                    const unsigned old =
-                        __hip_atomic_fetch_add(p.sync + w_am(p.L, p.Hkv), 1u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT);
-                    sh.s.flag = old == (unsigned)(p.nwg - 1);
-                }
-                __syncthreads();
-                if (sh.s.flag && wave == 0) {
-                    float v = -INFINITY;
-                    int vi = INT_MAX;
-                    for (int q = lane; q < p.nwg; q += 64)
-                        am_combine(v, vi, ldc(&p.am_part[q].x),
-                                   __float_as_int(ldc(&p.am_part[q].y)));
-                    wave_argmax(v, vi);
-                    if (lane == 0) {
-                        p.io[2] = vi;
-                        p.io[0] = vi;  // the next step's input when steps are chained
-                        if (p.out_tokens) p.out_tokens[p.step] = vi;
-                    }
-                }
-                if (p.trace && tid == 0) {
-                    const uint64_t now = wall_clock64();
-                    p.trace[((size_t)s * p.nwg + wg) * 2] = now;
-                    p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = now;
-                }
-                return;
-            }
-
-            // TL1 stages
-            for (int t = first; t < n; t += p.nwg) {
-                if (t != first) load_tl1_tile(tile, W, t, KS);
-                const int tot = tl1_rowblock(sh, tile, W, t, KS);
-                if (wave == 0) {
-                    const int row = t * 64 + lane;
-                    const int v = tot - csum;
-                    float sc;
-                    if (kind == S_QKV) sc = row < qd ? Lw.sc[0] : row < qd + kvd ? Lw.sc[1] : Lw.sc[2];
-                    else if (kind == S_O) sc = Lw.sc[3];
-                    else if (kind == S_GU) sc = row < p.F ? Lw.sc[4] : Lw.sc[5];
-                    else sc = Lw.sc[6];
-                    const float y = (float)v * (inv * sc);  // :1554, :118-126
-                    if (kind == S_QKV) stc(p.qkv + row, y);
-                    else if (kind == S_O) {
-                        // residual 1 (:1590); layer 0 reads the embedding WG 0 wrote
-                        stc(p.h1 + row, ldc(p.x + row) + y);
-                    } else if (kind == S_GU) stc(p.gu + row, y);
-                    else stc(p.x + row, ldc(p.h1 + row) + y);  // residual 2 (:1628)
-                }
-            }
-        }
-        // layer 0: workgroup 0 publishes the embedded token for the O residual
-        if (s == 0 && wg == 0) {
-            const int tok = p.io[0];
-            const float es = p.head_scales[tok];
-            const uint8_t* hb = reinterpret_cast<const uint8_t*>(p.head);
-            const size_t b = tok >> 6, r = tok & 63;
-            for (int i = tid; i < p.H; i += kT) {
-                const int8_t e = (int8_t)hb[((b * (p.H / 16) + (i >> 4)) * 64 + r) * 16 + (i & 15)];
-                stc(p.x + i, (float)e * es);
-            }
+        } else if (first < n) {
+            tl1_stage(sh, p, kind, l, first, n);
         }
         off = (off + n) % p.nwg;
         if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2] = wall_clock64();
@@ -929,8 +1134,26 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
 
 }  // namespace
 
-size_t ds_sync_words(int L, int Hkv) { return (size_t)(kNC + 2 + L * Hkv) * 64; }
+size_t ds_sync_words(int L, int Hkv) {
+    const size_t w = (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)L * 8;
+    return (w + 63) / 64 * 64;
+}
 size_t ds_error_word(int L, int Hkv) { return w_err(L, Hkv); }
+
+size_t ds_acc_words(int L, int H, int F, int Hq, int Hkv) {
+    return (size_t)L * acc_off(H, F, Hq, Hkv).stride;
+}
+
+void ds_plan_splits(DsParams& p) {
+    for (int slot = 0; slot < 4; ++slot) {
+        const int nb = gemv_rows(slot, p.H, p.F, p.Hq, p.Hkv) / 64;
+        const int KS = gemv_k(slot, p.H, p.F) / 64;
+        int S = nb > 0 ? p.nwg / nb : 1;
+        if (S > KS) S = KS;
+        if (S < 1) S = 1;
+        p.split[slot] = S;
+    }
+}
 
 int ds_grid_size() {
     int dev = 0;
@@ -978,6 +1201,11 @@ int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
         default:
             set_error("decode step: query heads per kv head must be 1, 2, 4 or 8");
             return TENZO_ERROR_UNSUPPORTED;
+    }
+    if (p.H % 64 || p.F % 64 || p.H > kJ * 4 * kT || p.F > kJ * 4 * kT) {
+        set_error("decode step: hidden and ffn sizes must be multiples of 64, at most %d",
+                  kJ * 4 * kT);
+        return TENZO_ERROR_UNSUPPORTED;
     }
     hipError_t e = hipLaunchCooperativeKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
     if (e != hipSuccess) return hip_fail(e, "hipLaunchCooperativeKernel(decode_step)");

@@ -101,7 +101,7 @@ struct tenzo_engine_opaque {
     int ds_nwg = 0;              // 0: not available on this device
     DsLayer* ds_layers = nullptr;  // device array [L]
     bool ds_layers_dirty = true;
-    unsigned* ds_sync = nullptr;
+    unsigned* ds_sync = nullptr;   // sync words, then the int32 GEMV accumulators
     float* ds_part = nullptr;
     float2* ds_am = nullptr;
     size_t ds_sync_bytes = 0;
@@ -360,6 +360,7 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.part = e->ds_part;
     p.am_part = e->ds_am;
     p.sync = e->ds_sync;
+    p.acc = reinterpret_cast<int*>(e->ds_sync + ds_sync_words(e->L, e->Hkv));
     p.io = e->io_dev;
     p.H = e->H;
     p.F = e->F;
@@ -371,6 +372,7 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.pos = pos;
     ds_chunking(pos + 1, e->Hkv, e->ds_nwg, &p.C, &p.T);
     p.nwg = e->ds_nwg;
+    ds_plan_splits(p);
     p.with_head = head ? 1 : 0;
     p.eps = e->eps;
     p.trace = e->ds_trace;
@@ -544,7 +546,8 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
             const int cseq = (int)ceil_div(e->max_seq, 1024);
             if (cseq > cmax) cmax = cseq;
             if (cmax < 1) cmax = 1;
-            e->ds_sync_bytes = ds_sync_words(e->L, Hkv) * 4;
+            e->ds_sync_bytes =
+                (ds_sync_words(e->L, Hkv) + ds_acc_words(e->L, e->H, e->F, Hq, Hkv)) * 4;
             ok = !alloc_t(e, &e->ds_layers, sizeof(DsLayer) * e->L) &&
                  !alloc_t(e, &e->ds_sync, e->ds_sync_bytes, true) &&
                  !alloc_t(e, &e->ds_part, (size_t)Hkv * cmax * G * kDsPartStride * 4) &&

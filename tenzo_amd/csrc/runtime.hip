@@ -70,7 +70,7 @@ void* Scratch::get(int slot, size_t bytes, hipStream_t stream) {
     }
     e = hipMemset(p, 0, want);
     if (e != hipSuccess) {
-        hipFree(p);
+        (void)hipFree(p);
         hip_fail(e, "scratch hipMemset");
         return nullptr;
     }

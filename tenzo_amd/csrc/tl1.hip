@@ -74,11 +74,15 @@ __device__ __forceinline__ float act_sumsq(const float* __restrict__ xm, int64_t
     if (MODE != 3) return block256_sumsq(xm, K, red);
     // same order as block256_sumsq, on the relu^2 * up values
     const int t = threadIdx.x;
-    float s = 0.0f;
-    for (int64_t i = t; i < K; i += 256) {
-        const float v = act_in<3>(xm, K, i);
-        s = __builtin_fmaf(v, v, s);
-    }
+    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int64_t i = 4 * t; i < K; i += 1024)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (i + k < K) {
+                const float v = act_in<3>(xm, K, i + k);
+                p[k] = __builtin_fmaf(v, v, p[k]);
+            }
+    float s = (p[0] + p[1]) + (p[2] + p[3]);
     s = wave_sum_tree(s);
     if ((t & 63) == 0) red[t >> 6] = s;
     __syncthreads();

@@ -122,10 +122,10 @@ def test_tl1_gemv_matches_golden_bit_exact():
 def test_sumsq_order_is_the_documented_tree():
     rng = np.random.default_rng(5)
     x = rng.standard_normal(6912).astype(np.float32)
-    p = np.zeros(256, np.float32)
-    for t in range(256):
+    p = np.zeros(1024, np.float32)
+    for t in range(1024):
         s = np.float32(0)
-        for v in x[t::256]:
+        for v in x[t::1024]:
             s = np.float32(np.float64(v) * np.float64(v) + np.float64(s))  # exact fma, rounded once
         p[t] = s
     while p.size > 1:
