@@ -180,9 +180,9 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
                 float s = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
-                s += __shfl_xor(s, 1, 64);
-                s += __shfl_xor(s, 2, 64);
-                s += __shfl_xor(s, 4, 64);
+                s += dpp_f<kDppXor1>(s);
+                s += dpp_f<kDppXor2>(s);
+                s += dpp_f<kDppHalfMirror>(s);
                 p[g] = s;
             }
             if (tl < nt) {

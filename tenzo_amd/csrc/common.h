@@ -60,25 +60,56 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // --------------------------------------------------------------- device ---
 
-// Sum over a wave with a butterfly in increasing lane distance: lane pairs
-// (0,1), (2,3), ... are added first, so the result is the balanced pairwise
-// tree over the 64 lanes in lane order, identical in every lane.
+// Cross-lane moves inside 16-lane rows (DPP): lane i receives lane
+// i^1, i^2 (quad permutations), 7-i within its half-row and 15-i within its
+// row. After the first two steps of a butterfly every lane of a quad holds the
+// same value, and after the third every lane of a half-row does, so the two
+// mirrors then act as the xor-4 and xor-8 partners.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Sum over a wave (all 64 lanes active) as the balanced pairwise tree over the
+// lanes in lane order: lane pairs (0,1), (2,3), ... first, then pairs of
+// pairs, ...; the four 16-lane row sums are combined as (r0+r1)+(r2+r3). The
+// result is identical in every lane. (Floating-point addition is commutative,
+// so which operand of a pair comes first does not change it.)
 __device__ __forceinline__ float wave_sum_tree(float v) {
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
+    v += dpp_f<kDppMirror>(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
 __device__ __forceinline__ int wave_sum_i32(int v) {
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
-    return v;
+    v += dpp_i<kDppXor1>(v);
+    v += dpp_i<kDppXor2>(v);
+    v += dpp_i<kDppHalfMirror>(v);
+    v += dpp_i<kDppMirror>(v);
+    return (__builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16)) +
+           (__builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
-    return v;
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kDppMirror>(v));
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Sum of squares of x[0..n) in the fixed order shared with the CPU oracle

@@ -24,12 +24,17 @@ struct DsParams {
     int8_t* vc;
     uint16_t* ks;               // [L][Hkv][max_seq] fp16
     uint16_t* vs;
+    // host-visible vectors of the last layer (x: the final hidden state)
     float* x;                   // [H] hidden state
     float* qkv;                 // [qd + 2 kvd]
     float* attn;                // [qd]
     float* h1;                  // [H]
     float* gu;                  // [2F]
     float* logits;              // [V]
+    // per-layer copies the kernel reads back (each written once per launch)
+    float* xs;                  // [L][H]  input of layer l
+    float* h1s;                 // [L][H]  x + o of layer l
+    float* attns;               // [L][qd] attention output of layer l
     float* part;                // [Hkv][C][G][kDsPartStride] attention partials
     float2* am_part;            // [nwg] argmax partials
     unsigned* sync;             // ds_sync_words() words, zero before each launch
@@ -51,6 +56,7 @@ struct DsParams {
 };
 
 constexpr int kDsThreads = 256;
+constexpr int kDsMaxChunk = 256;    // context tokens per attention task, at most
 constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
 constexpr int kDsCounters = 16;
 
@@ -59,6 +65,8 @@ constexpr int kDsCounters = 16;
 size_t ds_sync_words(int L, int Hkv);
 // int32 words of the accumulator region.
 size_t ds_acc_words(int L, int H, int F, int Hq, int Hkv);
+// floats of the per-layer vector region (xs, h1s, attns).
+size_t ds_vec_floats(int L, int H, int Hq);
 // K slices per row block for each GEMV stage (fills p.split from the shapes
 // and p.nwg).
 void ds_plan_splits(DsParams& p);
@@ -67,6 +75,9 @@ void ds_plan_splits(DsParams& p);
 int ds_grid_size();
 // Attention chunking (C chunks of T tokens per kv head) for context ctx.
 void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T);
+// Longest context the kernel's attention merge supports for G query heads per
+// kv head (its chunk statistics live in LDS).
+int ds_max_context(int G);
 // Launches one decode step (cooperative). The sync region must be zero.
 int launch_decode_step(const DsParams& p, int G, hipStream_t st);
 // Error word of the sync region (non-zero after an aborted step).

@@ -31,10 +31,16 @@
 // input, so each stage costs one memory round trip before its arithmetic.
 //
 // Synchronisation. Data produced inside the launch is written with
-// device-coherent stores / atomics and read with device-coherent loads (sc1:
-// served from the memory side, so no L2 write-back / invalidate fence is
-// needed); before arriving at a barrier every wave waits for its stores to be
-// acknowledged (s_waitcnt). The barrier is 16 counters on separate 256-byte
+// device-coherent stores / atomics (sc1: written through to the memory side);
+// before arriving at a barrier every wave waits for its stores to be
+// acknowledged (s_waitcnt). Every vector the stages read back (the per-layer
+// x, h1, attention outputs and GEMV accumulators) lives at its own address and
+// is written once per launch, before any workgroup reads it; the kernel
+// starts with an L2 invalidate (agent-scope acquire) in every workgroup, so an
+// XCD's L2 can hold no older copy of those lines and they are read with
+// ordinary cached loads: the first workgroup of an XCD to miss fetches a line
+// from memory and the other CUs of the XCD hit it in L2. Data rewritten within
+// a launch (the attention partials, the sync words) is read with sc1 loads. The barrier is 16 counters on separate 256-byte
 // lines polled together by one wave. The attention split-K merge is done by
 // the last workgroup to finish a kv head (a per-head arrival counter). Every
 // wait is bounded: on timeout a workgroup raises the error word and all
@@ -55,7 +61,7 @@ constexpr int kJ = 8;            // float4 groups per thread: vectors up to 8192
 constexpr int kNC = kDsCounters;
 constexpr int kD = 128;
 constexpr int kPS = kDsPartStride;  // partial record: m, l, -, -, o[128]
-constexpr int kTmax = 1024;      // attention tokens per task (LDS score buffer)
+constexpr int kTmax = kDsMaxChunk;  // attention tokens per task (LDS V tile)
 constexpr int kRT = kW * 8;      // attention tokens per round (8 per wave)
 constexpr int kAR = 4;           // attention rounds preloaded in registers
 constexpr unsigned kSpinLimit = 1u << 22;
@@ -117,6 +123,15 @@ __device__ __forceinline__ int ldc4i(__amdgpu_buffer_rsrc_t r, uint32_t byte_off
 __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
+__device__ __forceinline__ f4v ld16f(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ i4v ld16i(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(i4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ int ld4i(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0);
+}
 __device__ __forceinline__ uint32_t ld2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_amdgcn_raw_buffer_load_b16(r, byte_off, 0, 0);
 }
@@ -165,10 +180,14 @@ struct Shared {
     int flag;
 };
 
+constexpr int kTpad = kTmax + 64;  // weights past the chunk are zero up to here
+
 struct AttnShared {
     float qs[8][kD];
-    float sc[8][kTmax];
-    float ow[kW][8][kD];
+    float sc[8][kTpad];                                   // scores, then weights
+    int8_t vt[kTpad][kD] __attribute__((aligned(16)));    // the chunk's V codes
+    float vsc[kTmax];                                     // their fp16 scales
+    float ow[kT * 4];                                     // cross-wave partial sums
     float mstat[8], lstat[8];
     int8_t newk[kD] __attribute__((aligned(16)));
     int8_t newv[kD] __attribute__((aligned(16)));
@@ -237,7 +256,7 @@ __device__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
     return *s_abort == 0;
 }
 
-// ----------------------------------------------------------- prefetch -----
+// -------------------------------------------------------------- tiles ----
 
 // Loads kPF chunks per lane of K slice [c0, c1) of TL1 row block rb (KS
 // super-chunks of 64 columns per row block; wave w takes chunks c0+w, c0+w+4,
@@ -254,10 +273,10 @@ __device__ __forceinline__ void load_tl1_tile(uint4 (&pf)[kPF], const uint4* __r
 
 // Attention tile: the first kAR rounds of kRT tokens; lane (wave, l) holds 16
 // bytes of token r*kRT + wave*8 + l/8 at dims (l%8)*16 of K (pf[2r]) and V
-// (pf[2r+1]) and its two fp16 scales (pfs[r]). Tokens past the chunk read
+// (pf[2r+1]) and its fp16 K and V scales (pfs[2r], pfs[2r+1]). Tokens past the chunk read
 // zeros; the new token's slot is read but not used. Later rounds are read in
 // the loops that use them.
-__device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[kAR],
+__device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[2 * kAR],
                                               const DsParams& p, int l, int h, int c) {
     const int lane = ltid() & 63, wave = lwave();
     const int t0 = c * p.T;
@@ -273,7 +292,8 @@ __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[
         const int tl = r * kRT + wave * 8 + (lane >> 3);
         pf[2 * r] = ld16(rk, (uint32_t)(tl * kD + d0));
         pf[2 * r + 1] = ld16(rv, (uint32_t)(tl * kD + d0));
-        pfs[r] = ld2(rks, (uint32_t)tl * 2) | (ld2(rvs, (uint32_t)tl * 2) << 16);
+        pfs[2 * r] = ld2(rks, (uint32_t)tl * 2);
+        pfs[2 * r + 1] = ld2(rvs, (uint32_t)tl * 2);
     }
 }
 
@@ -307,12 +327,17 @@ __device__ __forceinline__ float gemv_y(int a, int csum, float invsc) {
 
 // The loaders below issue all kJ loads of a thread unconditionally (lanes past
 // K read zeros through the resource bounds) and leave zeros in v past K, so
-// no branch joins sit between the loads and their uses.
+// no branch joins sit between the loads and their uses. Each calls mid()
+// after issuing its loads and before using them: the stage's weight tile is
+// issued there, behind the input, so that waiting for the input (vector
+// memory operations complete in issue order) does not wait for the tile.
 
 // v = base + GEMV output (the residual adds :1590, :1628); the output's code
 // record is that of GEMV stage `slot` of layer l, w_scale its weight scale.
+template <class Mid>
 __device__ __forceinline__ void load_resid(float4 (&v)[kJ], const DsParams& p, const float* base,
-                                           const int* acc, int K, int l, int slot, float wsc) {
+                                           const int* acc, int K, int l, int slot, float wsc,
+                                           Mid&& mid) {
     const int t = ltid(), K4 = K >> 2;
     const __amdgpu_buffer_rsrc_t rb = rsrc(base, (uint32_t)K * 4);
     const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)K * 4);
@@ -320,12 +345,13 @@ __device__ __forceinline__ void load_resid(float4 (&v)[kJ], const DsParams& p, c
     i4v a[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
-        b[j] = ldc16(rb, (uint32_t)(t + kT * j) * 16);
-        a[j] = ldc16i(ra, (uint32_t)(t + kT * j) * 16);
+        b[j] = ld16f(rb, (uint32_t)(t + kT * j) * 16);
+        a[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16);
     }
     float inv;
     int csum;
     read_rec(p, l, slot, inv, csum);
+    mid();
     const float invsc = inv * wsc;
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
@@ -337,19 +363,22 @@ __device__ __forceinline__ void load_resid(float4 (&v)[kJ], const DsParams& p, c
     }
 }
 
-__device__ __forceinline__ void load_plain(float4 (&v)[kJ], const float* src, int K) {
+template <class Mid>
+__device__ __forceinline__ void load_plain(float4 (&v)[kJ], const float* src, int K, Mid&& mid) {
     const int t = ltid();
     const __amdgpu_buffer_rsrc_t r = rsrc(src, (uint32_t)K * 4);
     f4v b[kJ];
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) b[j] = ldc16(r, (uint32_t)(t + kT * j) * 16);
+    for (int j = 0; j < kJ; ++j) b[j] = ld16f(r, (uint32_t)(t + kT * j) * 16);
+    mid();
 #pragma unroll
     for (int j = 0; j < kJ; ++j) v[j] = make_float4(b[j].x, b[j].y, b[j].z, b[j].w);
 }
 
 // embedding_lookup (:1294-1316) of token io[0] from the packed int8 LM head
 // (lm_head.hip layout: [V/64][H/16][64 rows][16 bytes]).
-__device__ __forceinline__ void load_embed(float4 (&v)[kJ], const DsParams& p) {
+template <class Mid>
+__device__ __forceinline__ void load_embed(float4 (&v)[kJ], const DsParams& p, Mid&& mid) {
     const int t = ltid(), K4 = p.H >> 2;
     const int tok = p.io[0];
     const float es = p.head_scales[tok];
@@ -364,6 +393,7 @@ __device__ __forceinline__ void load_embed(float4 (&v)[kJ], const DsParams& p) {
         const int i = 4 * (t + kT * j);
         w[j] = __builtin_amdgcn_raw_buffer_load_b32(rr, (uint32_t)((i >> 4) * 1024 + (i & 15)), 0, 0);
     }
+    mid();
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
         const bool in = t + kT * j < K4;
@@ -389,20 +419,23 @@ __device__ __forceinline__ void store_slices(float* dst, const float4 (&v)[kJ], 
 
 // relu(gate)^2 * up (:1616-1620) from the gate|up accumulators; the gate and
 // up values are also stored as floats (slices as in store_slices).
+template <class Mid>
 __device__ __forceinline__ void load_act(float4 (&v)[kJ], const DsParams& p, const int* acc,
-                                         int l, float wg, float wu, int f, int m) {
+                                         int l, float wg, float wu, int f, int m, Mid&& mid) {
+    const bool last = l == p.L - 1;  // only the last layer's gate|up is stored
     const int t = ltid(), F = p.F, K4 = F >> 2;
     const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)F * 8);
     const __amdgpu_buffer_rsrc_t rg = rsrc(p.gu, (uint32_t)F * 8);
     i4v g[kJ], u[kJ];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
-        g[j] = ldc16i(ra, (uint32_t)(t + kT * j) * 16);
-        u[j] = ldc16i(ra, (uint32_t)(t + kT * j) * 16 + (uint32_t)F * 4);
+        g[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16);
+        u[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16 + (uint32_t)F * 4);
     }
     float inv;
     int csum;
     read_rec(p, l, 2, inv, csum);
+    mid();
     const float sg = inv * wg, su = inv * wu;
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
@@ -412,8 +445,8 @@ __device__ __forceinline__ void load_act(float4 (&v)[kJ], const DsParams& p, con
                                       gemv_y(g[j].z, csum, sg), gemv_y(g[j].w, csum, sg));
         const float4 uv = make_float4(gemv_y(u[j].x, csum, su), gemv_y(u[j].y, csum, su),
                                       gemv_y(u[j].z, csum, su), gemv_y(u[j].w, csum, su));
-        if (in && (q >> 4) % m == f) stc16(rg, (uint32_t)q * 16, gv);
-        if (in && (F / 64 + (q >> 4)) % m == f) stc16(rg, (uint32_t)q * 16 + (uint32_t)F * 4, uv);
+        if (last && in && (q >> 4) % m == f) stc16(rg, (uint32_t)q * 16, gv);
+        if (last && in && (F / 64 + (q >> 4)) % m == f) stc16(rg, (uint32_t)q * 16 + (uint32_t)F * 4, uv);
         float r;
         r = fmaxf(0.0f, gv.x);
         v[j].x = in ? (r * r) * uv.x : 0.0f;
@@ -574,30 +607,32 @@ __device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int
     const int S = p.split[slot];
     const int KS = K / 64, KSs = (KS + S - 1) / S;
     const uint4* W = Lw->mat[slot];
-    // read-only loads first (the first weight tile, the norm weights), then
-    // the stage input: one round trip for all of them
-    uint4 tile[kPF];
-    {
-        const int c0 = (first % S) * KSs;
-        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs));
-    }
+    // the norm weights and the stage input first, then the first task's
+    // weight tile (in flight during the normalization)
     float4 nwr[kJ];
     load_norm_w(nwr, Lw->norm[slot], K);
+    uint4 tile[kPF];
+    auto issue_tile = [&]() {
+        const int c0 = (first % S) * KSs;
+        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs));
+    };
     float4 xv[kJ];
     if (kind == S_QKV) {
         if (l == 0) {
-            load_embed(xv, p);
+            load_embed(xv, p, issue_tile);
         } else {
-            load_resid(xv, p, p.h1, accl - ao.stride + ao.down, K, l - 1, 3, layer(p, l - 1)->sc[6]);
+            load_resid(xv, p, p.h1s + (size_t)(l - 1) * p.H, accl - ao.stride + ao.down, K, l - 1,
+                       3, layer(p, l - 1)->sc[6], issue_tile);
         }
-        store_slices(p.x, xv, K, 0, first, m);
+        store_slices(p.xs + (size_t)l * p.H, xv, K, 0, first, m);
     } else if (kind == S_O) {
-        load_plain(xv, p.attn, K);
+        load_plain(xv, p.attns + (size_t)l * p.Hq * kD, K, issue_tile);
     } else if (kind == S_GU) {
-        load_resid(xv, p, p.x, accl + ao.o, K, l, 1, Lw->sc[3]);
-        store_slices(p.h1, xv, K, 0, first, m);
+        load_resid(xv, p, p.xs + (size_t)l * p.H, accl + ao.o, K, l, 1, Lw->sc[3], issue_tile);
+        store_slices(p.h1s + (size_t)l * p.H, xv, K, 0, first, m);
+        if (l == p.L - 1) store_slices(p.h1, xv, K, 0, first, m);
     } else {
-        load_act(xv, p, accl + ao.gu, l, Lw->sc[4], Lw->sc[5], first, m);
+        load_act(xv, p, accl + ao.gu, l, Lw->sc[4], Lw->sc[5], first, m, issue_tile);
     }
     float inv;
     int csum;
@@ -633,12 +668,21 @@ __device__ __forceinline__ void quant_kv(float x0, float x1, int8_t* codes, int 
     *s_out = amax * (1.0f / 127.0f);
 }
 
+// Byte j of w as a signed integer, converted to float (one SDWA convert).
+template <int J>
+__device__ __forceinline__ float sbyte(uint32_t w) {
+    return (float)(int8_t)(w >> (8 * J));
+}
+
 __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) f[4 * i + j] = (float)(int8_t)((w[i] >> (8 * j)) & 0xff);
+    for (int i = 0; i < 4; ++i) {
+        f[4 * i] = sbyte<0>(w[i]);
+        f[4 * i + 1] = sbyte<1>(w[i]);
+        f[4 * i + 2] = sbyte<2>(w[i]);
+        f[4 * i + 3] = sbyte<3>(w[i]);
+    }
 }
 
 // Attention of the G query heads of kv head h over context chunk c of layer
@@ -646,8 +690,7 @@ __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
 // the new token's K/V quantized and appended, chunk softmax and weighted
 // values; with several chunks the last one to finish merges the partials.
 template <int G>
-__device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[kPF],
-                          const uint32_t (&curs)[kAR], int l, int h, int c) {
+__device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c) {
     AttnShared& a = sh.a;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
     const int ctx = p.pos + 1;
@@ -669,20 +712,24 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
     for (int u = 0; u < kQ; ++u) {
         const int i = tid + u * kT, g = (i >> 6) % G, j = i & 63;
         const int row = (h * G + g) * kD;
-        qa[u][0] = ldc4i(racc, (uint32_t)(row + j) * 4);
-        qa[u][1] = ldc4i(racc, (uint32_t)(row + j + 64) * 4);
+        qa[u][0] = ld4i(racc, (uint32_t)(row + j) * 4);
+        qa[u][1] = ld4i(racc, (uint32_t)(row + j + 64) * 4);
         qc[u][0] = __int_as_float(ldc4i(rr, (uint32_t)j * 4));
         qc[u][1] = __int_as_float(ldc4i(rr, (uint32_t)(j + 64) * 4));
     }
     const bool has_new = p.pos >= t0 && p.pos < t0 + nt;
     const int krow = qd + (wave == 0 ? 0 : kvd) + h * kD;
-    const int ka0 = ldc4i(racc, (uint32_t)(krow + lane) * 4);
-    const int ka1 = ldc4i(racc, (uint32_t)(krow + lane + 64) * 4);
+    const int ka0 = ld4i(racc, (uint32_t)(krow + lane) * 4);
+    const int ka1 = ld4i(racc, (uint32_t)(krow + lane + 64) * 4);
     const float kc0 = __int_as_float(ldc4i(rr, (uint32_t)lane * 4));
     const float ks0 = __int_as_float(ldc4i(rr, (uint32_t)(lane + 64) * 4));
     float inv;
     int cs;
     read_rec(p, l, 0, inv, cs);
+    // then the chunk's K / V tile (in flight during the setup)
+    uint4 cur[kPF];
+    uint32_t curs[2 * kAR];
+    load_att_tile(cur, curs, p, l, h, c);
     // RoPE on the G query heads (:460-481); chunk 0 also stores q as floats
     {
         const float sq = inv * Lw->sc[0];
@@ -694,7 +741,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
                 const size_t row = (size_t)(h * G + g) * kD;
                 const float x0 = gemv_y(qa[u][0], cs, sq);
                 const float x1 = gemv_y(qa[u][1], cs, sq);
-                if (c == 0) {
+                if (c == 0 && l == p.L - 1) {
                     stc(p.qkv + row + j, x0);
                     stc(p.qkv + row + j + 64, x1);
                 }
@@ -709,8 +756,10 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
         const float sk = inv * Lw->sc[wave == 0 ? 1 : 2];
         float x0 = gemv_y(ka0, cs, sk);
         float x1 = gemv_y(ka1, cs, sk);
-        stc(p.qkv + krow + lane, x0);
-        stc(p.qkv + krow + lane + 64, x1);
+        if (l == p.L - 1) {
+            stc(p.qkv + krow + lane, x0);
+            stc(p.qkv + krow + lane + 64, x1);
+        }
         if (wave == 0) {
             const float r0 = __builtin_fmaf(x0, kc0, -(x1 * ks0));
             const float r1 = __builtin_fmaf(x0, ks0, x1 * kc0);
@@ -732,7 +781,8 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
     __syncthreads();
 
     const int sub = lane >> 3, d0 = (lane & 7) * 16;
-    // scores (:678-694)
+    // scores (:678-694); lane (wave, l) takes token r*kRT + wave*8 + l/8 and
+    // dims (l%8)*16.. of it, and stages that token's V codes and scale in LDS
     {
         float qr[G][16];
 #pragma unroll
@@ -743,37 +793,47 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
         for (int r = 0; r < rounds; ++r) {
             const int tl = r * kRT + wave * 8 + sub;
             const int t = t0 + tl;
-            float kf[16];
-            float skf = 0.0f;
-            if (tl < nt) {
-                uint4 kv;
-                if (t == p.pos) {
-                    kv = *reinterpret_cast<const uint4*>(a.newk + d0);
-                    skf = a.news[0];
-                } else if (r < kAR) {
-                    kv = cur[2 * r];
-                    skf = half_bits_to_float((uint16_t)(curs[r] & 0xffffu));
-                } else {
-                    kv = *reinterpret_cast<const uint4*>(p.kc + (head + t) * kD + d0);
-                    skf = half_bits_to_float(p.ks[head + t]);
-                }
-                unpack16(kv, kf);
+            uint4 kv, vv;
+            float skf, svf;
+            if (t == p.pos) {
+                kv = *reinterpret_cast<const uint4*>(a.newk + d0);
+                vv = *reinterpret_cast<const uint4*>(a.newv + d0);
+                skf = a.news[0];
+                svf = a.news[1];
+            } else if (r < kAR) {
+                kv = cur[2 * r];
+                vv = cur[2 * r + 1];
+                skf = half_bits_to_float((uint16_t)curs[2 * r]);
+                svf = half_bits_to_float((uint16_t)curs[2 * r + 1]);
             } else {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) kf[j] = 0.0f;
+                // past the preloaded rounds (long chunks): tokens past the
+                // chunk read zeros through the resource bounds
+                const size_t tok0 = head + t0;
+                const __amdgpu_buffer_rsrc_t rk = rsrc(p.kc + tok0 * kD, (uint32_t)nt * kD);
+                const __amdgpu_buffer_rsrc_t rv = rsrc(p.vc + tok0 * kD, (uint32_t)nt * kD);
+                const __amdgpu_buffer_rsrc_t rks = rsrc(p.ks + tok0, (uint32_t)nt * 2);
+                const __amdgpu_buffer_rsrc_t rvs = rsrc(p.vs + tok0, (uint32_t)nt * 2);
+                kv = ld16(rk, (uint32_t)(tl * kD + d0));
+                vv = ld16(rv, (uint32_t)(tl * kD + d0));
+                skf = half_bits_to_float((uint16_t)ld2(rks, (uint32_t)tl * 2));
+                svf = half_bits_to_float((uint16_t)ld2(rvs, (uint32_t)tl * 2));
             }
+            float kf[16];
+            unpack16(kv, kf);
             float pr[G];
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 float s = 0.0f;
 #pragma unroll
                 for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
-                s += __shfl_xor(s, 1, 64);
-                s += __shfl_xor(s, 2, 64);
-                s += __shfl_xor(s, 4, 64);
+                s += dpp_f<kDppXor1>(s);
+                s += dpp_f<kDppXor2>(s);
+                s += dpp_f<kDppHalfMirror>(s);
                 pr[g] = s;
             }
             if (tl < nt) {
+                *reinterpret_cast<uint4*>(&a.vt[tl][d0]) = vv;
+                if ((lane & 7) == 0) a.vsc[tl] = svf;
                 const float f = skf * kAttnScale;
 #pragma unroll
                 for (int g = 0; g < G; ++g)
@@ -782,7 +842,9 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
         }
     }
     __syncthreads();
-    // chunk softmax statistics (:824-830)
+    // chunk softmax statistics (:824-830); the weight kept for the values is
+    // e^{s-m} times the token's V scale (the product the multi-kernel path
+    // forms per token)
     for (int g = wave; g < G; g += kW) {
         float m = -1e30f;
         for (int i = lane; i < nt; i += 64) m = fmaxf(m, a.sc[g][i]);
@@ -790,9 +852,10 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
         float lsum = 0.0f;
         for (int i = lane; i < nt; i += 64) {
             const float e = expf(a.sc[g][i] - m);
-            a.sc[g][i] = e;
+            a.sc[g][i] = e * a.vsc[i];
             lsum += e;
         }
+        a.sc[g][nt + lane] = 0.0f;  // the value loop runs past nt by < 64
         lsum = wave_sum_tree(lsum);
         if (lane == 0) {
             a.mstat[g] = m;
@@ -800,71 +863,63 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
         }
     }
     __syncthreads();
-    // weighted values (:842-851)
-    float acc[G][16];
+    // weighted values (:842-851): lane l owns dims 4(l%32)..+3 of one head
+    // (G >= 2: head 2*(wave % (G/2)) + l/32; G = 1: head 0); the kNS wave
+    // (half-wave) sets that own the same outputs take every kNS-th token, and
+    // their sums are added in LDS in set order
+    constexpr int kWS = G >= 2 ? G / 2 : 1;          // waves per set of all heads
+    constexpr int kNS = G >= 2 ? kW / kWS : 2 * kW;  // token sets
+    static_assert(G <= 2 * kW, "at most 8 query heads per kv head");
+    constexpr int kVU = 8;  // tokens per step, their LDS reads issued together
+    static_assert(kVU * kNS <= kTpad - kTmax, "the zero padding covers one step");
+    const int dq = lane & 31, half = lane >> 5;
+    const int hd = G >= 2 ? (wave % kWS) * 2 + half : 0;
+    const int part = G >= 2 ? wave / kWS : wave * 2 + half;
+    float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tb = part; tb < nt; tb += kVU * kNS) {
+        uint32_t vb[kVU];
+        float wgt[kVU];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int u = 0; u < kVU; ++u) {
+            const int t = tb + u * kNS;  // past nt: weight 0, finite codes
+            vb[u] = *reinterpret_cast<const uint32_t*>(&a.vt[t][4 * dq]);
+            wgt[u] = a.sc[hd][t];
+        }
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
-    {
-        const int rounds = (nt + kRT - 1) / kRT;
-        for (int r = 0; r < rounds; ++r) {
-            const int tl = r * kRT + wave * 8 + sub;
-            const int t = t0 + tl;
-            if (tl < nt) {
-                uint4 vv;
-                float svf;
-                if (t == p.pos) {
-                    vv = *reinterpret_cast<const uint4*>(a.newv + d0);
-                    svf = a.news[1];
-                } else if (r < kAR) {
-                    vv = cur[2 * r + 1];
-                    svf = half_bits_to_float((uint16_t)(curs[r] >> 16));
-                } else {
-                    vv = *reinterpret_cast<const uint4*>(p.vc + (head + t) * kD + d0);
-                    svf = half_bits_to_float(p.vs[head + t]);
-                }
-                float vf[16];
-                unpack16(vv, vf);
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float wgt = a.sc[g][tl] * svf;
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
-                }
-            }
+        for (int u = 0; u < kVU; ++u) {
+            o[0] = __builtin_fmaf(sbyte<0>(vb[u]), wgt[u], o[0]);
+            o[1] = __builtin_fmaf(sbyte<1>(vb[u]), wgt[u], o[1]);
+            o[2] = __builtin_fmaf(sbyte<2>(vb[u]), wgt[u], o[2]);
+            o[3] = __builtin_fmaf(sbyte<3>(vb[u]), wgt[u], o[3]);
         }
     }
+    if (kNS > 1) {
+        float* ow = a.ow;  // [kNS][G][128]
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int k = 0; k < 4; ++k) ow[(part * G + hd) * kD + 4 * dq + k] = o[k];
+        __syncthreads();
+        if (part == 0) {
+            for (int q = 1; q < kNS; ++q)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            float v = acc[g][j];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            acc[g][j] = v;
+                for (int k = 0; k < 4; ++k) o[k] += ow[(q * G + hd) * kD + 4 * dq + k];
         }
-    if (lane < 8) {
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) a.ow[wave][g][d0 + j] = acc[g][j];
     }
-    __syncthreads();
     const int stride = kPS;
-    for (int i = tid; i < G * kD; i += kT) {
-        const int g = i >> 7, d = i & 127;
-        static_assert(kW == 4, "the wave reduction below sums 4 waves");
-        const float o = (a.ow[0][g][d] + a.ow[1][g][d]) + (a.ow[2][g][d] + a.ow[3][g][d]);
+    if (part == 0) {
+        const int d = 4 * dq;
         if (p.C == 1) {
-            stc(p.attn + (size_t)(h * G + g) * kD + d, o / a.lstat[g]);
+            const float L = a.lstat[hd];
+            const size_t off = (size_t)(h * G + hd) * kD + d;
+            const float4 r = make_float4(o[0] / L, o[1] / L, o[2] / L, o[3] / L);
+            stc16(rsrc(p.attns + (size_t)l * p.Hq * kD, (uint32_t)p.Hq * kD * 4),
+                  (uint32_t)off * 4, r);
+            if (l == p.L - 1) stc16(rsrc(p.attn, (uint32_t)p.Hq * kD * 4), (uint32_t)off * 4, r);
         } else {
-            float* pp = p.part + (((size_t)h * p.C + c) * G + g) * stride;
-            stc(pp + 4 + d, o);
-            if (d == 0) {
-                stc(pp, a.mstat[g]);
-                stc(pp + 1, a.lstat[g]);
+            float* pp = p.part + (((size_t)h * p.C + c) * G + hd) * stride;
+            stc16(rsrc(pp, stride * 4), (uint32_t)(4 + d) * 4, make_float4(o[0], o[1], o[2], o[3]));
+            if (dq == 0) {
+                stc(pp, a.mstat[hd]);
+                stc(pp + 1, a.lstat[hd]);
             }
         }
     }
@@ -886,18 +941,18 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
     const float* base = p.part + (size_t)h * p.C * G * stride;
     const __amdgpu_buffer_rsrc_t r = rsrc(base, (uint32_t)(p.C * G * stride) * 4);
     const int npairs = p.C * G;
-    float* wts = &a.sc[0][0];  // [C][G] weights (the scores are no longer needed)
+    float* wts = reinterpret_cast<float*>(&a.vt[0][0]);  // [C][G] weights (V tile no longer needed)
     float* lcs = wts + npairs;
     constexpr int kSlots = G * kD / 4;                         // float4 slots of the G outputs
     constexpr int kSplit = kT / kSlots > 0 ? kT / kSlots : 1;  // threads per slot
-    constexpr int kU = 8;
-    const int slot = tid % kSlots, part = tid / kSlots;
+    constexpr int kU = 16;
+    const int slot = tid % kSlots, mp = tid / kSlots;
     const int g_o = slot / (kD / 4), d4 = slot % (kD / 4);
-    const bool has_part = part < kSplit;
+    const bool has_part = mp < kSplit;
     f4v ov[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {  // chunks past C read zeros (outside the resource)
-        const int cc = part + u * kSplit;
+        const int cc = mp + u * kSplit;
         ov[u] = ldc16(r, (uint32_t)((cc * G + g_o) * stride + 4 + 4 * d4) * 4);
     }
     for (int i0 = tid; i0 < npairs; i0 += 4 * kT) {
@@ -932,7 +987,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
     if (has_part) {
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int cc = part + u * kSplit;
+            const int cc = mp + u * kSplit;
             if (cc < p.C) {
                 const float e = wts[cc * G + g_o];
                 acc4.x = __builtin_fmaf(e, ov[u].x, acc4.x);
@@ -941,7 +996,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
                 acc4.w = __builtin_fmaf(e, ov[u].w, acc4.w);
             }
         }
-        for (int c0 = part + kU * kSplit; c0 < p.C; c0 += kU * kSplit) {
+        for (int c0 = mp + kU * kSplit; c0 < p.C; c0 += kU * kSplit) {
             f4v v[kU];
 #pragma unroll
             for (int u = 0; u < kU; ++u) {
@@ -961,19 +1016,21 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, const uint4 (&cur)[k
             }
         }
     }
-    float* red = &a.ow[0][0][0];  // [kSplit][G*128]
+    float* red = a.ow;  // [kSplit][G*128]
     if (has_part) {
-        red[part * G * kD + 4 * slot] = acc4.x;
-        red[part * G * kD + 4 * slot + 1] = acc4.y;
-        red[part * G * kD + 4 * slot + 2] = acc4.z;
-        red[part * G * kD + 4 * slot + 3] = acc4.w;
+        red[mp * G * kD + 4 * slot] = acc4.x;
+        red[mp * G * kD + 4 * slot + 1] = acc4.y;
+        red[mp * G * kD + 4 * slot + 2] = acc4.z;
+        red[mp * G * kD + 4 * slot + 3] = acc4.w;
     }
     __syncthreads();
     for (int i = tid; i < G * kD; i += kT) {
         const int g = i >> 7, d = i & 127;
         float o = 0.0f;
         for (int q = 0; q < kSplit; ++q) o += red[q * G * kD + i];
-        stc(p.attn + (size_t)(h * G + g) * kD + d, o / a.mstat[g]);
+        const size_t off = (size_t)(h * G + g) * kD + d;
+        stc(p.attns + (size_t)l * p.Hq * kD + off, o / a.mstat[g]);
+        if (l == p.L - 1) stc(p.attn + off, o / a.mstat[g]);
     }
 }
 
@@ -1010,8 +1067,8 @@ __device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
         float4 nwr[kJ];
         if (p.with_head) load_norm_w(nwr, p.final_norm, p.H);
         float4 xv[kJ];
-        load_resid(xv, p, p.h1, p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H, p.L - 1, 3,
-                   layer(p, p.L - 1)->sc[6]);
+        load_resid(xv, p, p.h1s + (size_t)(p.L - 1) * p.H, p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H, p.L - 1, 3,
+                   layer(p, p.L - 1)->sc[6], [] {});
         float inv;
         int cs;
         store_slices(p.x, xv, p.H, 0, first, min(n, p.nwg));
@@ -1098,6 +1155,9 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     const int wg = blockIdx.x;
     const int nstages = 5 * p.L + 1;
     unsigned gen = 0;
+    // no line of this launch's per-layer vectors may survive in L2 from an
+    // earlier launch (they are read with cached loads after the first barrier)
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     int off = 0;  // first workgroup of the current stage
     for (int s = 0; s < nstages; ++s) {
         const int kind = kind_of(p, s);
@@ -1116,10 +1176,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
         }
         if (kind == S_ATT) {
             for (int t = first; t < n; t += p.nwg) {
-                uint4 tile[kPF];
-                uint32_t tiles[kAR];
-                load_att_tile(tile, tiles, p, l, t / p.C, t % p.C);
-                attn_task<G>(sh, p, tile, tiles, l, t / p.C, t % p.C);
+                attn_task<G>(sh, p, l, t / p.C, t % p.C);
                 __syncthreads();
             }
         } else if (first < n) {
@@ -1139,6 +1196,8 @@ size_t ds_sync_words(int L, int Hkv) {
     return (w + 63) / 64 * 64;
 }
 size_t ds_error_word(int L, int Hkv) { return w_err(L, Hkv); }
+
+size_t ds_vec_floats(int L, int H, int Hq) { return (size_t)L * (2 * H + Hq * kD); }
 
 size_t ds_acc_words(int L, int H, int F, int Hq, int Hkv) {
     return (size_t)L * acc_off(H, F, Hq, Hkv).stride;
@@ -1174,7 +1233,7 @@ int ds_grid_size() {
 }
 
 void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T) {
-    int c = (nwg * 3 / 4) / Hkv;  // leave room for the QKV tasks of the stage before
+    int c = (nwg * 3 / 4) / Hkv;
     if (c < 1) c = 1;
     if (c > ctx) c = ctx;
     int t = (ctx + c - 1) / c;
@@ -1185,10 +1244,11 @@ void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T) {
     c = (ctx + t - 1) / t;  // no empty chunks
     *C = c;
     *T = t;
-    // the merge keeps C x G chunk statistics (2 floats each) in the score
-    // buffer: C * G <= 8 * kTmax / 2 holds for every C chosen here
-    // (C <= max(3 nwg / 4, ctx / kTmax) with G <= 8)
 }
+
+// The merge keeps C x G chunk statistics (2 floats each) in the V tile's
+// LDS (kTmax * kD bytes).
+int ds_max_context(int G) { return kTmax * kD / 8 / G * kTmax; }
 
 int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
     void* args[] = {const_cast<DsParams*>(&p)};

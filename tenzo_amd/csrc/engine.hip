@@ -102,6 +102,7 @@ struct tenzo_engine_opaque {
     DsLayer* ds_layers = nullptr;  // device array [L]
     bool ds_layers_dirty = true;
     unsigned* ds_sync = nullptr;   // sync words, then the int32 GEMV accumulators
+    float* ds_vec = nullptr;       // per-layer x, h1, attention outputs
     float* ds_part = nullptr;
     float2* ds_am = nullptr;
     size_t ds_sync_bytes = 0;
@@ -314,7 +315,9 @@ int enqueue_step(tenzo_engine_t e, bool head, int T, int max_chunks) {
 
 // Whether the persistent kernel can run this model as loaded.
 bool ds_usable(tenzo_engine_t e) {
-    if (e->ds_nwg <= 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192) return false;
+    if (e->ds_nwg <= 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192 ||
+        e->max_seq > ds_max_context(e->Hq / e->Hkv))
+        return false;
     for (const DevLayer& d : e->layers)
         if (!d.mlp) return false;
     return true;
@@ -361,6 +364,9 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.am_part = e->ds_am;
     p.sync = e->ds_sync;
     p.acc = reinterpret_cast<int*>(e->ds_sync + ds_sync_words(e->L, e->Hkv));
+    p.xs = e->ds_vec;
+    p.h1s = p.xs + (size_t)e->L * e->H;
+    p.attns = p.h1s + (size_t)e->L * e->H;
     p.io = e->io_dev;
     p.H = e->H;
     p.F = e->F;
@@ -543,13 +549,14 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
         if (e->ds_nwg > 0) {
             const int G = Hq / Hkv;
             int cmax = (e->ds_nwg * 3 / 4) / Hkv;
-            const int cseq = (int)ceil_div(e->max_seq, 1024);
+            const int cseq = (int)ceil_div(e->max_seq, kDsMaxChunk);
             if (cseq > cmax) cmax = cseq;
             if (cmax < 1) cmax = 1;
             e->ds_sync_bytes =
                 (ds_sync_words(e->L, Hkv) + ds_acc_words(e->L, e->H, e->F, Hq, Hkv)) * 4;
             ok = !alloc_t(e, &e->ds_layers, sizeof(DsLayer) * e->L) &&
                  !alloc_t(e, &e->ds_sync, e->ds_sync_bytes, true) &&
+                 !alloc_t(e, &e->ds_vec, ds_vec_floats(e->L, e->H, Hq) * 4) &&
                  !alloc_t(e, &e->ds_part, (size_t)Hkv * cmax * G * kDsPartStride * 4) &&
                  !alloc_t(e, &e->ds_am, (size_t)e->ds_nwg * sizeof(float2));
         }
