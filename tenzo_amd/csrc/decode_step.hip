@@ -154,9 +154,10 @@ __host__ __device__ inline size_t w_am(int, int) { return (size_t)(kNC + 1) * 64
 __host__ __device__ inline size_t w_head(int l, int h, int Hkv) {
     return (size_t)(kNC + 2 + l * Hkv + h) * 64;
 }
-// (inv_scale, code_sum) of the activation codes of GEMV stage `slot` of layer l
+// (inv_scale, code_sum) of the activation codes of GEMV stage `slot` of layer
+// l, each on its own 128-byte line: written once per launch, read through L2
 __host__ __device__ inline size_t w_rec(int l, int slot, int L, int Hkv) {
-    return (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)(l * 4 + slot) * 2;
+    return (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)(l * 4 + slot) * 32;
 }
 
 // Accumulator region of one layer: q|k|v, o, gate|up, down (int32 each).
@@ -315,8 +316,8 @@ __device__ __forceinline__ void load_norm_w(float4 (&w)[kJ], const float* nw, in
 __device__ __forceinline__ void read_rec(const DsParams& p, int l, int slot, float& inv,
                                          int& csum) {
     const __amdgpu_buffer_rsrc_t r = rsrc(p.sync + w_rec(l, slot, p.L, p.Hkv), 8);
-    inv = __int_as_float(ldc4i(r, 0));
-    csum = ldc4i(r, 4);
+    inv = __int_as_float(ld4i(r, 0));
+    csum = ld4i(r, 4);
 }
 
 // Element of a GEMV output from its accumulator (TenzoEngine.cpp:1554,
@@ -410,10 +411,18 @@ __device__ __forceinline__ void store_slices(float* dst, const float4 (&v)[kJ], 
                                              int f, int m) {
     const int t = ltid(), K4 = K >> 2;
     const __amdgpu_buffer_rsrc_t r = rsrc(dst, (uint32_t)K * 4);
+    if (slice0 + K / 64 <= m) {  // every slice has a workgroup of its own: slice j is f's
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-        const int q = t + kT * j;
-        if (q < K4 && (slice0 + (q >> 4)) % m == f) stc16(r, (uint32_t)q * 16, v[j]);
+        for (int j = 0; j < kJ; ++j) {
+            const int q = t + kT * j;
+            if (q < K4 && slice0 + (q >> 4) == f) stc16(r, (uint32_t)q * 16, v[j]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kJ; ++j) {
+            const int q = t + kT * j;
+            if (q < K4 && (slice0 + (q >> 4)) % m == f) stc16(r, (uint32_t)q * 16, v[j]);
+        }
     }
 }
 
@@ -424,6 +433,7 @@ __device__ __forceinline__ void load_act(float4 (&v)[kJ], const DsParams& p, con
                                          int l, float wg, float wu, int f, int m, Mid&& mid) {
     const bool last = l == p.L - 1;  // only the last layer's gate|up is stored
     const int t = ltid(), F = p.F, K4 = F >> 2;
+    const bool own_one = 2 * F / 64 <= m;  // every slice has a workgroup of its own
     const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)F * 8);
     const __amdgpu_buffer_rsrc_t rg = rsrc(p.gu, (uint32_t)F * 8);
     i4v g[kJ], u[kJ];
@@ -445,8 +455,12 @@ __device__ __forceinline__ void load_act(float4 (&v)[kJ], const DsParams& p, con
                                       gemv_y(g[j].z, csum, sg), gemv_y(g[j].w, csum, sg));
         const float4 uv = make_float4(gemv_y(u[j].x, csum, su), gemv_y(u[j].y, csum, su),
                                       gemv_y(u[j].z, csum, su), gemv_y(u[j].w, csum, su));
-        if (last && in && (q >> 4) % m == f) stc16(rg, (uint32_t)q * 16, gv);
-        if (last && in && (F / 64 + (q >> 4)) % m == f) stc16(rg, (uint32_t)q * 16 + (uint32_t)F * 4, uv);
+        if (last) {
+            const int sg_ = q >> 4, su_ = F / 64 + (q >> 4);
+            if (in && (own_one ? sg_ == f : sg_ % m == f)) stc16(rg, (uint32_t)q * 16, gv);
+            if (in && (own_one ? su_ == f : su_ % m == f))
+                stc16(rg, (uint32_t)q * 16 + (uint32_t)F * 4, uv);
+        }
         float r;
         r = fmaxf(0.0f, gv.x);
         v[j].x = in ? (r * r) * uv.x : 0.0f;
@@ -684,6 +698,9 @@ __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
         f[4 * i + 3] = sbyte<3>(w[i]);
     }
 }
+
+template <int G>
+__device__ void attn_merge(AttnShared& a, const DsParams& p, int l, int h, int g);
 
 // Attention of the G query heads of kv head h over context chunk c of layer
 // l (attention_int8_fused, :434-864): q|k|v from the QKV accumulators, RoPE,
@@ -924,114 +941,122 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
         }
     }
     if (p.C == 1) return;
-    // the last chunk of this kv head to finish merges the partials
+    // The last M = min(G, C) chunks of this kv head to finish merge the
+    // partials, merger r taking query heads r, r+M, ...; each first waits
+    // until every chunk of the head has stored its partial.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    const int M = min(G, p.C);
+    unsigned* ctr = p.sync + w_head(l, h, p.Hkv);
     if (tid == 0) {
-        const unsigned old = __hip_atomic_fetch_add(p.sync + w_head(l, h, p.Hkv), 1u,
-                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        a.last = old == (unsigned)(p.C - 1);
+        const unsigned old =
+            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int r = (int)old - (p.C - M);
+        if (r >= 0) {
+            unsigned spins = 0;
+            while (ldcu(ctr) < (unsigned)p.C) {
+                if (++spins > kSpinLimit ||
+                    ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0)) {
+                    stcu(p.sync + w_err(p.L, p.Hkv), 1u);
+                    r = -1;
+                    break;
+                }
+            }
+        }
+        a.last = r;
     }
     __syncthreads();
-    if (!a.last) return;
-    // merge (same formula as attn_combine_kernel): out = sum_c e^{m_c-M} o_c /
-    // sum_c e^{m_c-M} l_c. The first kU chunks' o loads and every (chunk,
-    // head) statistic are issued together; the weights e^{m_c-M} and the
-    // denominators are formed in LDS while the o loads are in flight.
+    const int r = a.last;
+    for (int g = r; r >= 0 && g < G; g += M) attn_merge<G>(a, p, l, h, g);
+}
+
+// Merge of the C chunk partials of query head g of kv head h (same formula
+// as attn_combine_kernel): out = sum_c e^{m_c-M} o_c / sum_c e^{m_c-M} l_c.
+// Thread (cp, d4) = (tid / 32, tid % 32) sums dims 4 d4.. over the chunks
+// c = cp, cp + 8, ... in order, and the 8 sums are added in cp order. The
+// first kU chunks of each thread and every chunk statistic are loaded
+// together.
+template <int G>
+__device__ void attn_merge(AttnShared& a, const DsParams& p, int l, int h, int g) {
+    const int tid = ltid(), lane = tid & 63, wave = lwave();
+    const int stride = kPS;
     const float* base = p.part + (size_t)h * p.C * G * stride;
     const __amdgpu_buffer_rsrc_t r = rsrc(base, (uint32_t)(p.C * G * stride) * 4);
-    const int npairs = p.C * G;
-    float* wts = reinterpret_cast<float*>(&a.vt[0][0]);  // [C][G] weights (V tile no longer needed)
-    float* lcs = wts + npairs;
-    constexpr int kSlots = G * kD / 4;                         // float4 slots of the G outputs
-    constexpr int kSplit = kT / kSlots > 0 ? kT / kSlots : 1;  // threads per slot
-    constexpr int kU = 16;
-    const int slot = tid % kSlots, mp = tid / kSlots;
-    const int g_o = slot / (kD / 4), d4 = slot % (kD / 4);
-    const bool has_part = mp < kSplit;
+    float* wts = reinterpret_cast<float*>(&a.vt[0][0]);  // [C] weights (V tile no longer needed)
+    float* lcs = wts + p.C;
+    constexpr int kU = 8;
+    const int d4 = tid & 31, cp = tid >> 5;
     f4v ov[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {  // chunks past C read zeros (outside the resource)
-        const int cc = mp + u * kSplit;
-        ov[u] = ldc16(r, (uint32_t)((cc * G + g_o) * stride + 4 + 4 * d4) * 4);
+        const int c = cp + 8 * u;
+        ov[u] = ldc16(r, (uint32_t)((c * G + g) * stride + 4 + 4 * d4) * 4);
     }
-    for (int i0 = tid; i0 < npairs; i0 += 4 * kT) {
-        f4v v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) v[u] = ldc16(r, (uint32_t)(i0 + u * kT) * stride * 4);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + u * kT;
-            if (i < npairs) {
-                wts[i] = v[u].x;
-                lcs[i] = v[u].y;
-            }
-        }
+    for (int c = tid; c < p.C; c += kT) {
+        const f4v v = ldc16(r, (uint32_t)((c * G + g) * stride) * 4);
+        wts[c] = v.x;
+        lcs[c] = v.y;
     }
     __syncthreads();
-    for (int g = wave; g < G; g += kW) {  // one wave per head, lanes over chunks
-        float M = -1e30f;
-        for (int cc = lane; cc < p.C; cc += 64) M = fmaxf(M, wts[cc * G + g]);
-        M = wave_max(M);
+    if (wave == 0) {
+        float Mx = -1e30f;
+        for (int c = lane; c < p.C; c += 64) Mx = fmaxf(Mx, wts[c]);
+        Mx = wave_max(Mx);
         float L = 0.0f;
-        for (int cc = lane; cc < p.C; cc += 64) {
-            const float e = expf(wts[cc * G + g] - M);
-            wts[cc * G + g] = e;
-            L = __builtin_fmaf(e, lcs[cc * G + g], L);
+        for (int c = lane; c < p.C; c += 64) {
+            const float e = expf(wts[c] - Mx);
+            wts[c] = e;
+            L = __builtin_fmaf(e, lcs[c], L);
         }
         L = wave_sum_tree(L);
         if (lane == 0) a.mstat[g] = L;
     }
     __syncthreads();
     f4v acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (has_part) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+        const int c = cp + 8 * u;
+        if (c < p.C) {
+            const float e = wts[c];
+            acc4.x = __builtin_fmaf(e, ov[u].x, acc4.x);
+            acc4.y = __builtin_fmaf(e, ov[u].y, acc4.y);
+            acc4.z = __builtin_fmaf(e, ov[u].z, acc4.z);
+            acc4.w = __builtin_fmaf(e, ov[u].w, acc4.w);
+        }
+    }
+    for (int c0 = cp + 8 * kU; c0 < p.C; c0 += 8 * kU) {
+        f4v v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            v[u] = ldc16(r, (uint32_t)(((c0 + 8 * u) * G + g) * stride + 4 + 4 * d4) * 4);
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int cc = mp + u * kSplit;
-            if (cc < p.C) {
-                const float e = wts[cc * G + g_o];
-                acc4.x = __builtin_fmaf(e, ov[u].x, acc4.x);
-                acc4.y = __builtin_fmaf(e, ov[u].y, acc4.y);
-                acc4.z = __builtin_fmaf(e, ov[u].z, acc4.z);
-                acc4.w = __builtin_fmaf(e, ov[u].w, acc4.w);
-            }
-        }
-        for (int c0 = mp + kU * kSplit; c0 < p.C; c0 += kU * kSplit) {
-            f4v v[kU];
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int cc = c0 + u * kSplit;
-                v[u] = ldc16(r, (uint32_t)((cc * G + g_o) * stride + 4 + 4 * d4) * 4);
-            }
-#pragma unroll
-            for (int u = 0; u < kU; ++u) {
-                const int cc = c0 + u * kSplit;
-                if (cc < p.C) {
-                    const float e = wts[cc * G + g_o];
-                    acc4.x = __builtin_fmaf(e, v[u].x, acc4.x);
-                    acc4.y = __builtin_fmaf(e, v[u].y, acc4.y);
-                    acc4.z = __builtin_fmaf(e, v[u].z, acc4.z);
-                    acc4.w = __builtin_fmaf(e, v[u].w, acc4.w);
-                }
+            const int c = c0 + 8 * u;
+            if (c < p.C) {
+                const float e = wts[c];
+                acc4.x = __builtin_fmaf(e, v[u].x, acc4.x);
+                acc4.y = __builtin_fmaf(e, v[u].y, acc4.y);
+                acc4.z = __builtin_fmaf(e, v[u].z, acc4.z);
+                acc4.w = __builtin_fmaf(e, v[u].w, acc4.w);
             }
         }
     }
-    float* red = a.ow;  // [kSplit][G*128]
-    if (has_part) {
-        red[mp * G * kD + 4 * slot] = acc4.x;
-        red[mp * G * kD + 4 * slot + 1] = acc4.y;
-        red[mp * G * kD + 4 * slot + 2] = acc4.z;
-        red[mp * G * kD + 4 * slot + 3] = acc4.w;
+    float* red = a.ow;  // [8][128]
+    red[cp * kD + 4 * d4] = acc4.x;
+    red[cp * kD + 4 * d4 + 1] = acc4.y;
+    red[cp * kD + 4 * d4 + 2] = acc4.z;
+    red[cp * kD + 4 * d4 + 3] = acc4.w;
+    __syncthreads();
+    if (tid < kD) {
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) o += red[q * kD + tid];
+        const size_t off = (size_t)(h * G + g) * kD + tid;
+        const float y = o / a.mstat[g];
+        stc(p.attns + (size_t)l * p.Hq * kD + off, y);
+        if (l == p.L - 1) stc(p.attn + off, y);
     }
     __syncthreads();
-    for (int i = tid; i < G * kD; i += kT) {
-        const int g = i >> 7, d = i & 127;
-        float o = 0.0f;
-        for (int q = 0; q < kSplit; ++q) o += red[q * G * kD + i];
-        const size_t off = (size_t)(h * G + g) * kD + d;
-        stc(p.attns + (size_t)l * p.Hq * kD + off, o / a.mstat[g]);
-        if (l == p.L - 1) stc(p.attn + off, o / a.mstat[g]);
-    }
 }
 
 // ------------------------------------------------------------ LM head -----
@@ -1192,7 +1217,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
 }  // namespace
 
 size_t ds_sync_words(int L, int Hkv) {
-    const size_t w = (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)L * 8;
+    const size_t w = (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)L * 4 * 32;
     return (w + 63) / 64 * 64;
 }
 size_t ds_error_word(int L, int Hkv) { return w_err(L, Hkv); }
