@@ -943,10 +943,13 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
     if (p.C == 1) return;
     // The last M = min(G, C) chunks of this kv head to finish merge the
     // partials, merger r taking query heads r, r+M, ...; each first waits
-    // until every chunk of the head has stored its partial.
+    // until every chunk of the head has stored its partial. When there are
+    // more attention tasks than workgroups a workgroup runs several chunks in
+    // turn and must not wait for one of its own later chunks: then only the
+    // last chunk to finish merges (M = 1, nothing left to wait for).
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    const int M = min(G, p.C);
+    const int M = p.Hkv * p.C <= p.nwg ? min(G, p.C) : 1;
     unsigned* ctr = p.sync + w_head(l, h, p.Hkv);
     if (tid == 0) {
         const unsigned old =
