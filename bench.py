@@ -49,7 +49,30 @@ def parse():
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="engine execution mode (one persistent kernel per token, or one "
                          "kernel per stage replayed from a HIP graph / launched eagerly)")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: one calibration copy of PROBE_COPY_BYTES "
+                         "(a plain copy kernel of known size), then --steps chained decode "
+                         "steps; prints no JSON line")
     return ap.parse_args()
+
+
+PROBE_COPY_BYTES = 256 << 20
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "decode_step_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per decode_step_kernel launch as measured by rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration) and
+    recorded in profiles/decode_step_hbm_traffic.md, with the source it was
+    measured on; None if that file is absent."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
 
 
 # ---------------------------------------------------------------- synthetic
@@ -262,6 +285,19 @@ def main():
     e, host = build_model(torch, cfg, ctx)
     e.set_mode(args.mode)
     mode = e.mode
+    if args.pmc_probe:
+        src = torch.empty(PROBE_COPY_BYTES // 4, dtype=torch.int32, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # the calibration kernel: PROBE_COPY_BYTES read and written
+        torch.cuda.synchronize()
+        e.rewind(ctx)
+        e.decode(1, args.steps)
+        torch.cuda.synchronize()
+        e.close()
+        print(f"pmc probe: 1 copy of {PROBE_COPY_BYTES} bytes, {args.steps} decode steps at "
+              f"context {ctx}", flush=True)
+        return
 
     # warm up (also captures graphs / loads code), then the timed decode:
     # `steps` greedy tokens chained on the device from position ctx
@@ -298,7 +334,8 @@ def main():
     roofline = {"bound": "hbm", "kernel": dom_name,
                 "achieved": round(step_bytes / kern_s / 1e9, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(step_bytes / kern_s / 1e9 / PEAK_HBM_GBS, 4),
-                "traffic": None, "alg_bytes_per_launch": int(step_bytes),
+                "traffic": measured_traffic() if mode == "persistent" else None,
+                "alg_bytes_per_launch": int(step_bytes),
                 "mean_launch_us": round(kern_s * 1e6, 2)}
     rl_tl1 = tl1_roofline(torch, cfg, host)
     rl_head = head_roofline(torch, cfg, host)
