@@ -661,9 +661,14 @@ __device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int
         const int rb = t / S, c0 = (t % S) * KSs, c1 = min(KS, c0 + KSs);
         if (t != first) load_tl1_tile(tile, W, rb, KS, c0, c1);
         const int tot = tl1_rowblock(s, tile, W, rb, KS, c0, c1);
-        if (wave == 0)
-            __hip_atomic_fetch_add(out + rb * 64 + lane, tot, __ATOMIC_RELAXED,
+        if (wave == 0) {
+            if (S == 1)  // the row block's only contribution
+                __hip_atomic_store(out + rb * 64 + lane, tot, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
+            else
+                __hip_atomic_fetch_add(out + rb * 64 + lane, tot, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
 }
 
@@ -1104,26 +1109,25 @@ __device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
         norm_quant<127>(s, xv, nwr, p.final_norm != nullptr, p.H, p.eps, inv, cs);
         const int HC = p.H / 16;
         const int4* c4 = reinterpret_cast<const int4*>(s.codes);
+        constexpr int kHU = 16;  // 16-byte loads in flight per lane
         for (int t = first; t < n; t += p.nwg) {
-            const uint4* wb = p.head + (size_t)t * HC * 64 + lane;
+            // row block t: chunks of 16 columns x 64 rows, 1 KiB each (past HC: zeros)
+            const __amdgpu_buffer_rsrc_t rh =
+                rsrc(p.head + (size_t)t * HC * 64, (uint32_t)HC * 64 * 16);
             int acc = 0;
-            for (int c0 = wave; c0 < HC; c0 += 8 * kW) {
-                uint4 v[8];
+            for (int c0 = wave; c0 < HC; c0 += kHU * kW) {
+                uint4 v[kHU];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int c = c0 + u * kW;
-                    v[u] = c < HC ? wb[(size_t)c * 64] : make_uint4(0, 0, 0, 0);
-                }
+                for (int u = 0; u < kHU; ++u)
+                    v[u] = ld16(rh, (uint32_t)((c0 + u * kW) * 64 + lane) * 16);
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const int c = c0 + u * kW;
-                    if (c < HC) {
-                        const int4 a4 = c4[c];
-                        acc = sdot4(v[u].x, a4.x, acc);
-                        acc = sdot4(v[u].y, a4.y, acc);
-                        acc = sdot4(v[u].z, a4.z, acc);
-                        acc = sdot4(v[u].w, a4.w, acc);
-                    }
+                for (int u = 0; u < kHU; ++u) {
+                    const int c = min(c0 + u * kW, HC - 1);  // past HC the weights read 0
+                    const int4 a4 = c4[c];
+                    acc = sdot4(v[u].x, a4.x, acc);
+                    acc = sdot4(v[u].y, a4.y, acc);
+                    acc = sdot4(v[u].z, a4.z, acc);
+                    acc = sdot4(v[u].w, a4.w, acc);
                 }
             }
             s.red_i[wave][lane] = acc;
