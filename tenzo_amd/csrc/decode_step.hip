@@ -64,7 +64,7 @@ constexpr int kPS = kDsPartStride;  // partial record: m, l, -, -, o[128]
 constexpr int kTmax = kDsMaxChunk;  // attention tokens per task (LDS V tile)
 constexpr int kRT = kW * 8;      // attention tokens per round (8 per wave)
 constexpr int kAR = 4;           // attention rounds preloaded in registers
-constexpr unsigned kSpinLimit = 1u << 22;
+constexpr unsigned kSpinLimit = 1u << 18;  // ~0.3 s of polling; a barrier waits < 0.1 ms
 constexpr float kAttnScale = 0.08838834764831845f;  // 1/sqrt(128)
 
 // threadIdx.x behind an empty asm: values derived from it are recomputed in
@@ -257,6 +257,23 @@ __device__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
     return *s_abort == 0;
 }
 
+// Float4 groups of a K-element vector a wave holds: thread t owns groups
+// t + 256 j, so wave w's lanes cover groups [256 j + 64 w, 256 j + 64 w + 64);
+// the j with a group below K/4 (wave-uniform). Loads past that count would
+// only read zeros, so they are not issued at all.
+__device__ __forceinline__ int wave_groups(int K) {
+    const int K4 = K >> 2, w0 = lwave() * 64;
+    return K4 > w0 ? (K4 - w0 + kT - 1) / kT : 0;
+}
+
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] in [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // -------------------------------------------------------------- tiles ----
 
 // Loads kPF chunks per lane of K slice [c0, c1) of TL1 row block rb (KS
@@ -292,9 +309,11 @@ __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[
     for (int r = 0; r < kAR; ++r) {
         const int tl = r * kRT + wave * 8 + (lane >> 3);
         pf[2 * r] = ld16(rk, (uint32_t)(tl * kD + d0));
-        pf[2 * r + 1] = ld16(rv, (uint32_t)(tl * kD + d0));
         pfs[2 * r] = ld2(rks, (uint32_t)tl * 2);
+        pf[2 * r + 1] = ld16(rv, (uint32_t)(tl * kD + d0));
         pfs[2 * r + 1] = ld2(rvs, (uint32_t)tl * 2);
+        // keep the rounds in issue order: round r then waits only for its own 4 loads
+        __builtin_amdgcn_sched_barrier(0);
     }
 }
 
@@ -302,13 +321,14 @@ __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[
 __device__ __forceinline__ void load_norm_w(float4 (&w)[kJ], const float* nw, int K) {
     if (!nw) return;
     const __amdgpu_buffer_rsrc_t r = rsrc(nw, (uint32_t)K * 4);
-    const int t = ltid();
+    const int t = ltid(), Jw = wave_groups(K);
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-        const f4v v = __builtin_bit_cast(
-            f4v, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(t + kT * j) * 16, 0, 0));
-        w[j] = make_float4(v.x, v.y, v.z, v.w);
-    }
+    for (int j = 0; j < kJ; ++j)
+        if (j < Jw) {
+            const f4v v = __builtin_bit_cast(
+                f4v, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(t + kT * j) * 16, 0, 0));
+            w[j] = make_float4(v.x, v.y, v.z, v.w);
+        }
 }
 
 // ------------------------------------------------------------ prologue ----
@@ -326,82 +346,101 @@ __device__ __forceinline__ float gemv_y(int a, int csum, float invsc) {
     return (float)(a - csum) * invsc;
 }
 
-// The loaders below issue all kJ loads of a thread unconditionally (lanes past
-// K read zeros through the resource bounds) and leave zeros in v past K, so
-// no branch joins sit between the loads and their uses. Each calls mid()
-// after issuing its loads and before using them: the stage's weight tile is
-// issued there, behind the input, so that waiting for the input (vector
-// memory operations complete in issue order) does not wait for the tile.
+// A stage input is read in two steps. The issue_* functions start the loads
+// of the float4 groups the wave holds (wave_groups; lanes past K read zeros
+// through the resource bounds) into an InRaw; the caller then issues the
+// stage's weight tile and waits until only the tile is in flight (vector
+// memory operations complete in issue order), and the finish_* functions
+// build the input vector v (zeros past K). The issue and finish steps sit in
+// separate kind branches with the tile loads between them in common code, so
+// the tile's loads are pending on every path alike and waiting for the input
+// never waits for the tile.
+struct InRaw {
+    i4v x[kJ], y[kJ];  // raw 32-bit lanes of up to two K-vectors
+    int inv, csum;     // code record of the GEMV the input comes from
+};
 
-// v = base + GEMV output (the residual adds :1590, :1628); the output's code
-// record is that of GEMV stage `slot` of layer l, w_scale its weight scale.
-template <class Mid>
-__device__ __forceinline__ void load_resid(float4 (&v)[kJ], const DsParams& p, const float* base,
-                                           const int* acc, int K, int l, int slot, float wsc,
-                                           Mid&& mid) {
-    const int t = ltid(), K4 = K >> 2;
-    const __amdgpu_buffer_rsrc_t rb = rsrc(base, (uint32_t)K * 4);
-    const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)K * 4);
-    f4v b[kJ];
-    i4v a[kJ];
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-        b[j] = ld16f(rb, (uint32_t)(t + kT * j) * 16);
-        a[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16);
-    }
-    float inv;
-    int csum;
-    read_rec(p, l, slot, inv, csum);
-    mid();
-    const float invsc = inv * wsc;
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-        const bool in = t + kT * j < K4;
-        v[j].x = in ? b[j].x + gemv_y(a[j].x, csum, invsc) : 0.0f;
-        v[j].y = in ? b[j].y + gemv_y(a[j].y, csum, invsc) : 0.0f;
-        v[j].z = in ? b[j].z + gemv_y(a[j].z, csum, invsc) : 0.0f;
-        v[j].w = in ? b[j].w + gemv_y(a[j].w, csum, invsc) : 0.0f;
-    }
+__device__ __forceinline__ void issue_rec(InRaw& in, const DsParams& p, int l, int slot) {
+    const __amdgpu_buffer_rsrc_t r = rsrc(p.sync + w_rec(l, slot, p.L, p.Hkv), 8);
+    in.inv = ld4i(r, 0);
+    in.csum = ld4i(r, 4);
 }
 
-template <class Mid>
-__device__ __forceinline__ void load_plain(float4 (&v)[kJ], const float* src, int K, Mid&& mid) {
-    const int t = ltid();
-    const __amdgpu_buffer_rsrc_t r = rsrc(src, (uint32_t)K * 4);
-    f4v b[kJ];
+// x = a float vector, y = int32 accumulators (each K elements; y optional)
+__device__ __forceinline__ void issue_vec2(InRaw& in, const void* xs, const void* ys, int K) {
+    const int t = ltid(), Jw = wave_groups(K);
+    const __amdgpu_buffer_rsrc_t rx = rsrc(xs, (uint32_t)K * 4);
+    const __amdgpu_buffer_rsrc_t ry = rsrc(ys, ys ? (uint32_t)K * 4 : 0u);
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) b[j] = ld16f(r, (uint32_t)(t + kT * j) * 16);
-    mid();
+    for (int j = 0; j < kJ; ++j)
+        if (j < Jw) {
+            in.x[j] = ld16i(rx, (uint32_t)(t + kT * j) * 16);
+            if (ys) in.y[j] = ld16i(ry, (uint32_t)(t + kT * j) * 16);
+        }
+}
+
+// v = base + GEMV output (the residual adds :1590, :1628): x = base, y = the
+// accumulators; the record is that of the GEMV, w_scale its weight scale.
+__device__ __forceinline__ void finish_resid(float4 (&v)[kJ], const InRaw& in, int K, float wsc) {
+    const int t = ltid(), K4 = K >> 2, Jw = wave_groups(K);
+    const float invsc = __int_as_float(in.inv) * wsc;
+    const int cs = in.csum;
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) v[j] = make_float4(b[j].x, b[j].y, b[j].z, b[j].w);
+    for (int j = 0; j < kJ; ++j)
+        if (j < Jw) {
+            const bool ok = t + kT * j < K4;
+            v[j].x = ok ? __int_as_float(in.x[j].x) + gemv_y(in.y[j].x, cs, invsc) : 0.0f;
+            v[j].y = ok ? __int_as_float(in.x[j].y) + gemv_y(in.y[j].y, cs, invsc) : 0.0f;
+            v[j].z = ok ? __int_as_float(in.x[j].z) + gemv_y(in.y[j].z, cs, invsc) : 0.0f;
+            v[j].w = ok ? __int_as_float(in.x[j].w) + gemv_y(in.y[j].w, cs, invsc) : 0.0f;
+        } else {
+            v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+}
+
+__device__ __forceinline__ void finish_plain(float4 (&v)[kJ], const InRaw& in, int K) {
+    const int Jw = wave_groups(K);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        v[j] = j < Jw ? make_float4(__int_as_float(in.x[j].x), __int_as_float(in.x[j].y),
+                                    __int_as_float(in.x[j].z), __int_as_float(in.x[j].w))
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 // embedding_lookup (:1294-1316) of token io[0] from the packed int8 LM head
-// (lm_head.hip layout: [V/64][H/16][64 rows][16 bytes]).
-template <class Mid>
-__device__ __forceinline__ void load_embed(float4 (&v)[kJ], const DsParams& p, Mid&& mid) {
-    const int t = ltid(), K4 = p.H >> 2;
-    const int tok = p.io[0];
-    const float es = p.head_scales[tok];
+// (lm_head.hip layout: [V/64][H/16][64 rows][16 bytes]); x[j].x = 4 codes.
+__device__ __forceinline__ int embed_token(const DsParams& p) {
+    return __builtin_amdgcn_readfirstlane(p.io[0]);  // uniform: scalar descriptors
+}
+
+__device__ __forceinline__ void issue_embed(InRaw& in, const DsParams& p) {
+    const int t = ltid(), Jw = wave_groups(p.H);
+    const int tok = embed_token(p);
     const uint8_t* hb = reinterpret_cast<const uint8_t*>(p.head);
     const size_t b = tok >> 6, r = tok & 63;
     // row r of block b: 16 bytes every 1 KiB
     const __amdgpu_buffer_rsrc_t rr = rsrc(hb + (b * (p.H / 16) * 64 + r) * 16,
                                            (uint32_t)(p.H / 16) * 1024);
-    uint32_t w[kJ];
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < Jw) {
+            const int i = 4 * (t + kT * j);
+            in.x[j].x = (int)__builtin_amdgcn_raw_buffer_load_b32(
+                rr, (uint32_t)((i >> 4) * 1024 + (i & 15)), 0, 0);
+        }
+}
+
+__device__ __forceinline__ void finish_embed(float4 (&v)[kJ], const InRaw& in, const DsParams& p) {
+    const int t = ltid(), K4 = p.H >> 2, Jw = wave_groups(p.H);
+    const float es = p.head_scales[embed_token(p)];
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
-        const int i = 4 * (t + kT * j);
-        w[j] = __builtin_amdgcn_raw_buffer_load_b32(rr, (uint32_t)((i >> 4) * 1024 + (i & 15)), 0, 0);
-    }
-    mid();
-#pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-        const bool in = t + kT * j < K4;
-        v[j].x = in ? (float)(int8_t)(w[j] & 0xff) * es : 0.0f;
-        v[j].y = in ? (float)(int8_t)((w[j] >> 8) & 0xff) * es : 0.0f;
-        v[j].z = in ? (float)(int8_t)((w[j] >> 16) & 0xff) * es : 0.0f;
-        v[j].w = in ? (float)(int8_t)(w[j] >> 24) * es : 0.0f;
+        const bool ok = j < Jw && t + kT * j < K4;
+        const uint32_t w = (uint32_t)in.x[j].x;
+        v[j].x = ok ? (float)(int8_t)(w & 0xff) * es : 0.0f;
+        v[j].y = ok ? (float)(int8_t)((w >> 8) & 0xff) * es : 0.0f;
+        v[j].z = ok ? (float)(int8_t)((w >> 16) & 0xff) * es : 0.0f;
+        v[j].w = ok ? (float)(int8_t)(w >> 24) * es : 0.0f;
     }
 }
 
@@ -426,50 +465,58 @@ __device__ __forceinline__ void store_slices(float* dst, const float4 (&v)[kJ], 
     }
 }
 
-// relu(gate)^2 * up (:1616-1620) from the gate|up accumulators; the gate and
-// up values are also stored as floats (slices as in store_slices).
-template <class Mid>
-__device__ __forceinline__ void load_act(float4 (&v)[kJ], const DsParams& p, const int* acc,
-                                         int l, float wg, float wu, int f, int m, Mid&& mid) {
-    const bool last = l == p.L - 1;  // only the last layer's gate|up is stored
-    const int t = ltid(), F = p.F, K4 = F >> 2;
-    const bool own_one = 2 * F / 64 <= m;  // every slice has a workgroup of its own
+// relu(gate)^2 * up (:1616-1620) from the gate|up accumulators (x = gate,
+// y = up, record of the GU stage); the last layer's gate and up values are
+// also stored as floats (slices as in store_slices).
+__device__ __forceinline__ void issue_act(InRaw& in, const DsParams& p, const int* acc, int l) {
+    const int t = ltid(), F = p.F, Jw = wave_groups(F);
     const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)F * 8);
-    const __amdgpu_buffer_rsrc_t rg = rsrc(p.gu, (uint32_t)F * 8);
-    i4v g[kJ], u[kJ];
 #pragma unroll
-    for (int j = 0; j < kJ; ++j) {
-        g[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16);
-        u[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16 + (uint32_t)F * 4);
-    }
-    float inv;
-    int csum;
-    read_rec(p, l, 2, inv, csum);
-    mid();
+    for (int j = 0; j < kJ; ++j)
+        if (j < Jw) {
+            in.x[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16);
+            in.y[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16 + (uint32_t)F * 4);
+        }
+    issue_rec(in, p, l, 2);
+}
+
+__device__ __forceinline__ void finish_act(float4 (&v)[kJ], const InRaw& in, const DsParams& p,
+                                           int l, float wg, float wu, int f, int m) {
+    const bool last = l == p.L - 1;  // only the last layer's gate|up is stored
+    const int t = ltid(), F = p.F, K4 = F >> 2, Jw = wave_groups(F);
+    const bool own_one = 2 * F / 64 <= m;  // every slice has a workgroup of its own
+    const __amdgpu_buffer_rsrc_t rg = rsrc(p.gu, (uint32_t)F * 8);
+    const float inv = __int_as_float(in.inv);
+    const int csum = in.csum;
     const float sg = inv * wg, su = inv * wu;
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
+        if (j >= Jw) {
+            v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            continue;
+        }
         const int q = t + kT * j;
-        const bool in = q < K4;
-        const float4 gv = make_float4(gemv_y(g[j].x, csum, sg), gemv_y(g[j].y, csum, sg),
-                                      gemv_y(g[j].z, csum, sg), gemv_y(g[j].w, csum, sg));
-        const float4 uv = make_float4(gemv_y(u[j].x, csum, su), gemv_y(u[j].y, csum, su),
-                                      gemv_y(u[j].z, csum, su), gemv_y(u[j].w, csum, su));
+        const bool ok = q < K4;
+        const i4v g = in.x[j], u = in.y[j];
+        const float4 gv = make_float4(gemv_y(g.x, csum, sg), gemv_y(g.y, csum, sg),
+                                      gemv_y(g.z, csum, sg), gemv_y(g.w, csum, sg));
+        const float4 uv = make_float4(gemv_y(u.x, csum, su), gemv_y(u.y, csum, su),
+                                      gemv_y(u.z, csum, su), gemv_y(u.w, csum, su));
         if (last) {
             const int sg_ = q >> 4, su_ = F / 64 + (q >> 4);
-            if (in && (own_one ? sg_ == f : sg_ % m == f)) stc16(rg, (uint32_t)q * 16, gv);
-            if (in && (own_one ? su_ == f : su_ % m == f))
+            if (ok && (own_one ? sg_ == f : sg_ % m == f)) stc16(rg, (uint32_t)q * 16, gv);
+            if (ok && (own_one ? su_ == f : su_ % m == f))
                 stc16(rg, (uint32_t)q * 16 + (uint32_t)F * 4, uv);
         }
         float r;
         r = fmaxf(0.0f, gv.x);
-        v[j].x = in ? (r * r) * uv.x : 0.0f;
+        v[j].x = ok ? (r * r) * uv.x : 0.0f;
         r = fmaxf(0.0f, gv.y);
-        v[j].y = in ? (r * r) * uv.y : 0.0f;
+        v[j].y = ok ? (r * r) * uv.y : 0.0f;
         r = fmaxf(0.0f, gv.z);
-        v[j].z = in ? (r * r) * uv.z : 0.0f;
+        v[j].z = ok ? (r * r) * uv.z : 0.0f;
         r = fmaxf(0.0f, gv.w);
-        v[j].w = in ? (r * r) * uv.w : 0.0f;
+        v[j].w = ok ? (r * r) * uv.w : 0.0f;
     }
 }
 
@@ -490,7 +537,7 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
                                            bool has_w, int K, float eps, float& inv_out,
                                            int& csum_out) {
     const int t = ltid(), lane = t & 63, wave = lwave();
-    const int J = ((K >> 2) + kT - 1) / kT;  // groups in use (wave-uniform)
+    const int J = wave_groups(K);  // groups this wave holds
     float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
@@ -625,28 +672,43 @@ __device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int
     // weight tile (in flight during the normalization)
     float4 nwr[kJ];
     load_norm_w(nwr, Lw->norm[slot], K);
-    uint4 tile[kPF];
-    auto issue_tile = [&]() {
-        const int c0 = (first % S) * KSs;
-        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs));
-    };
-    float4 xv[kJ];
+    InRaw in;
     if (kind == S_QKV) {
         if (l == 0) {
-            load_embed(xv, p, issue_tile);
+            issue_embed(in, p);
         } else {
-            load_resid(xv, p, p.h1s + (size_t)(l - 1) * p.H, accl - ao.stride + ao.down, K, l - 1,
-                       3, layer(p, l - 1)->sc[6], issue_tile);
+            issue_vec2(in, p.h1s + (size_t)(l - 1) * p.H, accl - ao.stride + ao.down, K);
+            issue_rec(in, p, l - 1, 3);
         }
+    } else if (kind == S_O) {
+        issue_vec2(in, p.attns + (size_t)l * p.Hq * kD, nullptr, K);
+    } else if (kind == S_GU) {
+        issue_vec2(in, p.xs + (size_t)l * p.H, accl + ao.o, K);
+        issue_rec(in, p, l, 1);
+    } else {
+        issue_act(in, p, accl + ao.gu, l);
+    }
+    uint4 tile[kPF];
+    {
+        const int c0 = (first % S) * KSs;
+        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs));
+    }
+    wait_vm<kPF>();  // everything but the tile has arrived
+    float4 xv[kJ];
+    if (kind == S_QKV) {
+        if (l == 0)
+            finish_embed(xv, in, p);
+        else
+            finish_resid(xv, in, K, layer(p, l - 1)->sc[6]);
         store_slices(p.xs + (size_t)l * p.H, xv, K, 0, first, m);
     } else if (kind == S_O) {
-        load_plain(xv, p.attns + (size_t)l * p.Hq * kD, K, issue_tile);
+        finish_plain(xv, in, K);
     } else if (kind == S_GU) {
-        load_resid(xv, p, p.xs + (size_t)l * p.H, accl + ao.o, K, l, 1, Lw->sc[3], issue_tile);
+        finish_resid(xv, in, K, Lw->sc[3]);
         store_slices(p.h1s + (size_t)l * p.H, xv, K, 0, first, m);
         if (l == p.L - 1) store_slices(p.h1, xv, K, 0, first, m);
     } else {
-        load_act(xv, p, accl + ao.gu, l, Lw->sc[4], Lw->sc[5], first, m, issue_tile);
+        finish_act(xv, in, p, l, Lw->sc[4], Lw->sc[5], first, m);
     }
     float inv;
     int csum;
@@ -752,6 +814,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
     uint4 cur[kPF];
     uint32_t curs[2 * kAR];
     load_att_tile(cur, curs, p, l, h, c);
+    wait_vm<4 * kAR>();  // all but the tile
     // RoPE on the G query heads (:460-481); chunk 0 also stores q as floats
     {
         const float sq = inv * Lw->sc[0];
@@ -937,8 +1000,11 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
                   (uint32_t)off * 4, r);
             if (l == p.L - 1) stc16(rsrc(p.attn, (uint32_t)p.Hq * kD * 4), (uint32_t)off * 4, r);
         } else {
-            float* pp = p.part + (((size_t)h * p.C + c) * G + hd) * stride;
-            stc16(rsrc(pp, stride * 4), (uint32_t)(4 + d) * 4, make_float4(o[0], o[1], o[2], o[3]));
+            // the chunk's G records from a wave-uniform base (no per-lane descriptor)
+            float* pc = p.part + ((size_t)h * p.C + c) * G * stride;
+            float* pp = pc + hd * stride;
+            stc16(rsrc(pc, G * stride * 4), (uint32_t)(hd * stride + 4 + d) * 4,
+                  make_float4(o[0], o[1], o[2], o[3]));
             if (dq == 0) {
                 stc(pp, a.mstat[hd]);
                 stc(pp + 1, a.lstat[hd]);
@@ -1100,8 +1166,11 @@ __device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
         float4 nwr[kJ];
         if (p.with_head) load_norm_w(nwr, p.final_norm, p.H);
         float4 xv[kJ];
-        load_resid(xv, p, p.h1s + (size_t)(p.L - 1) * p.H, p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H, p.L - 1, 3,
-                   layer(p, p.L - 1)->sc[6], [] {});
+        InRaw in;
+        issue_vec2(in, p.h1s + (size_t)(p.L - 1) * p.H,
+                   p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H);
+        issue_rec(in, p, p.L - 1, 3);
+        finish_resid(xv, in, p.H, layer(p, p.L - 1)->sc[6]);
         float inv;
         int cs;
         store_slices(p.x, xv, p.H, 0, first, min(n, p.nwg));
