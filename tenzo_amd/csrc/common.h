@@ -65,9 +65,11 @@ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // row. After the first two steps of a butterfly every lane of a quad holds the
 // same value, and after the third every lane of a half-row does, so the two
 // mirrors then act as the xor-4 and xor-8 partners.
+// (mov_dpp leaves no old value to keep, so the compiler folds each move into
+// the add or max that uses it: one v_add_f32_dpp per butterfly step.)
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
-    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
 }
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {

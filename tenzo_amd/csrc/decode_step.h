@@ -59,6 +59,7 @@ constexpr int kDsThreads = 256;
 constexpr int kDsMaxChunk = 256;    // context tokens per attention task, at most
 constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
 constexpr int kDsCounters = 16;
+constexpr int kDsMaxLayers = 64;    // the layer table is staged in LDS
 
 // uint32 words of the sync region for L layers and Hkv kv heads (a multiple of
 // 64, so the accumulators can follow it in one allocation).

@@ -142,11 +142,38 @@ __device__ __forceinline__ void stc16(__amdgpu_buffer_rsrc_t r, uint32_t byte_of
 
 // ---------------------------------------------------------------- layout --
 
-// The per-layer descriptors are read-only for the whole launch: reading them
-// through the constant address space lets the compiler use scalar loads.
-typedef __attribute__((address_space(4))) const DsLayer* LayerPtr;
-__device__ __forceinline__ LayerPtr layer(const DsParams& p, int l) {
-    return (LayerPtr)(p.layers + l);
+// The per-layer descriptors are copied into LDS when the kernel starts (a
+// scalar load of layer l's entry would otherwise miss its cache at the layer's
+// first stage and stall every wave for an HBM round trip). Fields are read
+// from LDS at a uniform address and moved to scalar registers.
+__shared__ DsLayer s_layers[kDsMaxLayers];
+
+template <class T>
+__device__ __forceinline__ T* uni_ptr(T* q) {
+    const uint64_t v = reinterpret_cast<uint64_t>(q);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+struct LayerRef {
+    int l;
+    __device__ const uint4* mat(int slot) const { return uni_ptr(s_layers[l].mat[slot]); }
+    __device__ const float* norm(int slot) const { return uni_ptr(s_layers[l].norm[slot]); }
+    __device__ float sc(int i) const {
+        return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(s_layers[l].sc[i])));
+    }
+};
+__device__ __forceinline__ LayerRef layer(const DsParams&, int l) { return LayerRef{l}; }
+
+// Copies the layer table into LDS (all threads; a block barrier follows).
+__device__ __forceinline__ void stage_layers(const DsParams& p) {
+    static_assert(sizeof(DsLayer) % 4 == 0, "copied as words");
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(p.layers);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(s_layers);
+    const int words = p.L * (int)(sizeof(DsLayer) / 4);
+    for (int i = threadIdx.x; i < words; i += kT) dst[i] = src[i];
+    __syncthreads();
 }
 
 __host__ __device__ inline size_t w_err(int, int) { return (size_t)kNC * 64; }
@@ -593,27 +620,36 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
 
 // ---------------------------------------------------------------- GEMV ----
 
-__device__ __forceinline__ int dot64(const uint4 v, const int4* c4, int acc) {
-    // 64 columns of 2-bit codes (tl1.hip layout) against 64 int8 codes
-    const uint32_t M = 0x03030303u;
-    const int4 a0 = c4[0], a1 = c4[1], a2 = c4[2], a3 = c4[3];
-    acc = sdot4(v.x & M, a0.x, acc);
-    acc = sdot4((v.x >> 2) & M, a0.y, acc);
-    acc = sdot4((v.x >> 4) & M, a0.z, acc);
-    acc = sdot4((v.x >> 6) & M, a0.w, acc);
-    acc = sdot4(v.y & M, a1.x, acc);
-    acc = sdot4((v.y >> 2) & M, a1.y, acc);
-    acc = sdot4((v.y >> 4) & M, a1.z, acc);
-    acc = sdot4((v.y >> 6) & M, a1.w, acc);
-    acc = sdot4(v.z & M, a2.x, acc);
-    acc = sdot4((v.z >> 2) & M, a2.y, acc);
-    acc = sdot4((v.z >> 4) & M, a2.z, acc);
-    acc = sdot4((v.z >> 6) & M, a2.w, acc);
-    acc = sdot4(v.w & M, a3.x, acc);
-    acc = sdot4((v.w >> 2) & M, a3.y, acc);
-    acc = sdot4((v.w >> 4) & M, a3.z, acc);
-    acc = sdot4((v.w >> 6) & M, a3.w, acc);
-    return acc;
+// 64 columns of 2-bit codes u = w + 1 (tl1.hip layout: bits 2k..2k+1 of each
+// byte of word i hold the columns paired with activation word 4i + k) against
+// 64 int8 codes. Field k goes to accumulator k, masked in place rather than
+// shifted down, so acc[k] collects 4^k (k = 3: 32, from a one-bit shift)
+// times its exact sum; tl1_acc_total divides the factors out exactly. The
+// four independent chains keep v_dot4 from waiting on its own result.
+__device__ __forceinline__ void dot64(const uint4 v, const int4* c4, int (&acc)[4]) {
+    const uint32_t M0 = 0x03030303u, M1 = M0 << 2, M2 = M0 << 4, M3 = M0 << 5;
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    // all 16 fields first (independent of each other), then the products
+    uint32_t f[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        f[i][0] = w[i] & M0;
+        f[i][1] = w[i] & M1;
+        f[i][2] = w[i] & M2;
+        f[i][3] = (w[i] >> 1) & M3;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int4 a = c4[i];
+        acc[0] = sdot4(f[i][0], a.x, acc[0]);
+        acc[1] = sdot4(f[i][1], a.y, acc[1]);
+        acc[2] = sdot4(f[i][2], a.z, acc[2]);
+        acc[3] = sdot4(f[i][3], a.w, acc[3]);
+    }
+}
+
+__device__ __forceinline__ int tl1_acc_total(const int (&acc)[4]) {
+    return (acc[0] + (acc[1] >> 2)) + ((acc[2] >> 4) + (acc[3] >> 5));
 }
 
 // K slice [c0, c1) of one TL1 row block: returns the exact int32 sum
@@ -623,11 +659,11 @@ __device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
                                             int c1) {
     const int lane = ltid() & 63, wave = lwave();
     const int4* c4 = reinterpret_cast<const int4*>(s.codes);
-    int acc = 0;
+    int acc4[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < kPF; ++i) {
         const int c = c0 + wave + kW * i;
-        if (c < c1) acc = dot64(cur[i], c4 + c * 4, acc);
+        if (c < c1) dot64(cur[i], c4 + c * 4, acc4);
     }
     // K beyond the preloaded window: 8 loads in flight (past c1: zeros)
     const __amdgpu_buffer_rsrc_t r = rsrc(W + (size_t)rb * KS * 64, (uint32_t)c1 * 64 * 16);
@@ -638,9 +674,10 @@ __device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int c = cc + u * kW;
-            if (c < c1) acc = dot64(v[u], c4 + c * 4, acc);
+            if (c < c1) dot64(v[u], c4 + c * 4, acc4);
         }
     }
+    const int acc = tl1_acc_total(acc4);
     s.red_i[wave][lane] = acc;
     __syncthreads();
     int tot = 0;
@@ -659,7 +696,7 @@ __device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
 __device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int first, int n) {
     Shared& s = sh.s;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
-    const LayerPtr Lw = layer(p, l);
+    const LayerRef Lw = layer(p, l);
     const int slot = kind == S_QKV ? 0 : kind - 1;
     const int K = gemv_k(slot, p.H, p.F);
     const int m = min(n, p.nwg);
@@ -667,11 +704,10 @@ __device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int
     int* accl = p.acc + (size_t)l * ao.stride;
     const int S = p.split[slot];
     const int KS = K / 64, KSs = (KS + S - 1) / S;
-    const uint4* W = Lw->mat[slot];
-    // the norm weights and the stage input first, then the first task's
-    // weight tile (in flight during the normalization)
-    float4 nwr[kJ];
-    load_norm_w(nwr, Lw->norm[slot], K);
+    const uint4* W = Lw.mat(slot);
+    // the stage input and the norm weights first, then (once every wave has
+    // issued those, so no wave's input queues behind another's tile) the
+    // first task's weight tile, in flight during the normalization
     InRaw in;
     if (kind == S_QKV) {
         if (l == 0) {
@@ -688,6 +724,9 @@ __device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int
     } else {
         issue_act(in, p, accl + ao.gu, l);
     }
+    float4 nwr[kJ];
+    load_norm_w(nwr, Lw.norm(slot), K);
+    __builtin_amdgcn_s_barrier();
     uint4 tile[kPF];
     {
         const int c0 = (first % S) * KSs;
@@ -699,20 +738,20 @@ __device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int
         if (l == 0)
             finish_embed(xv, in, p);
         else
-            finish_resid(xv, in, K, layer(p, l - 1)->sc[6]);
+            finish_resid(xv, in, K, layer(p, l - 1).sc(6));
         store_slices(p.xs + (size_t)l * p.H, xv, K, 0, first, m);
     } else if (kind == S_O) {
         finish_plain(xv, in, K);
     } else if (kind == S_GU) {
-        finish_resid(xv, in, K, Lw->sc[3]);
+        finish_resid(xv, in, K, Lw.sc(3));
         store_slices(p.h1s + (size_t)l * p.H, xv, K, 0, first, m);
         if (l == p.L - 1) store_slices(p.h1, xv, K, 0, first, m);
     } else {
-        finish_act(xv, in, p, l, Lw->sc[4], Lw->sc[5], first, m);
+        finish_act(xv, in, p, l, Lw.sc(4), Lw.sc(5), first, m);
     }
     float inv;
     int csum;
-    norm_quant<31>(s, xv, nwr, Lw->norm[slot] != nullptr, K, p.eps, inv, csum);
+    norm_quant<31>(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps, inv, csum);
     if (first == 0 && tid == 0) {
         unsigned* r = p.sync + w_rec(l, slot, p.L, p.Hkv);
         stcu(r, __float_as_uint(inv));
@@ -783,7 +822,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
     const int qd = p.Hq * kD, kvd = p.Hkv * kD;
     const float* rope = p.rope + (size_t)p.pos * kD;
     const size_t head = ((size_t)l * p.Hkv + h) * p.max_seq;
-    const LayerPtr Lw = layer(p, l);
+    const LayerRef Lw = layer(p, l);
     const __amdgpu_buffer_rsrc_t racc =
         rsrc(p.acc + (size_t)l * acc_off(p.H, p.F, p.Hq, p.Hkv).stride, (uint32_t)(qd + 2 * kvd) * 4);
     // loads first: the q (and new k / v) accumulators, the rope row, the
@@ -810,14 +849,16 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
     float inv;
     int cs;
     read_rec(p, l, 0, inv, cs);
-    // then the chunk's K / V tile (in flight during the setup)
+    // then, once every wave has issued those, the chunk's K / V tile (in
+    // flight during the setup)
+    __builtin_amdgcn_s_barrier();
     uint4 cur[kPF];
     uint32_t curs[2 * kAR];
     load_att_tile(cur, curs, p, l, h, c);
     wait_vm<4 * kAR>();  // all but the tile
     // RoPE on the G query heads (:460-481); chunk 0 also stores q as floats
     {
-        const float sq = inv * Lw->sc[0];
+        const float sq = inv * Lw.sc(0);
 #pragma unroll
         for (int u = 0; u < kQ; ++u) {
             const int i = tid + u * kT;
@@ -838,7 +879,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
     }
     // the new token: RoPE on k, quantize-append k and v (:482-533)
     if (has_new && wave < 2) {
-        const float sk = inv * Lw->sc[wave == 0 ? 1 : 2];
+        const float sk = inv * Lw.sc(wave == 0 ? 1 : 2);
         float x0 = gemv_y(ka0, cs, sk);
         float x1 = gemv_y(ka1, cs, sk);
         if (l == p.L - 1) {
@@ -1170,7 +1211,7 @@ __device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
         issue_vec2(in, p.h1s + (size_t)(p.L - 1) * p.H,
                    p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H);
         issue_rec(in, p, p.L - 1, 3);
-        finish_resid(xv, in, p.H, layer(p, p.L - 1)->sc[6]);
+        finish_resid(xv, in, p.H, layer(p, p.L - 1).sc(6));
         float inv;
         int cs;
         store_slices(p.x, xv, p.H, 0, first, min(n, p.nwg));
@@ -1183,7 +1224,7 @@ __device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
             // row block t: chunks of 16 columns x 64 rows, 1 KiB each (past HC: zeros)
             const __amdgpu_buffer_rsrc_t rh =
                 rsrc(p.head + (size_t)t * HC * 64, (uint32_t)HC * 64 * 16);
-            int acc = 0;
+            int acc4[4] = {0, 0, 0, 0};  // independent chains (integer sums: exact in any order)
             for (int c0 = wave; c0 < HC; c0 += kHU * kW) {
                 uint4 v[kHU];
 #pragma unroll
@@ -1193,13 +1234,13 @@ __device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
                 for (int u = 0; u < kHU; ++u) {
                     const int c = min(c0 + u * kW, HC - 1);  // past HC the weights read 0
                     const int4 a4 = c4[c];
-                    acc = sdot4(v[u].x, a4.x, acc);
-                    acc = sdot4(v[u].y, a4.y, acc);
-                    acc = sdot4(v[u].z, a4.z, acc);
-                    acc = sdot4(v[u].w, a4.w, acc);
+                    acc4[0] = sdot4(v[u].x, a4.x, acc4[0]);
+                    acc4[1] = sdot4(v[u].y, a4.y, acc4[1]);
+                    acc4[2] = sdot4(v[u].z, a4.z, acc4[2]);
+                    acc4[3] = sdot4(v[u].w, a4.w, acc4[3]);
                 }
             }
-            s.red_i[wave][lane] = acc;
+            s.red_i[wave][lane] = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
             __syncthreads();
             if (wave == 0) {
                 int tot = 0;
@@ -1248,6 +1289,24 @@ __device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
 
 // ---------------------------------------------------------------- kernel --
 
+// Brings the norm weights of stage s (read by every workgroup, otherwise
+// from HBM at that stage's start) into L2 a stage early: one dword per
+// 128-byte line, lane l of wave w taking line 64 w + l (up to 8192 floats;
+// past the vector, or without a norm, the load reads nothing). The value is
+// only consumed after the next barrier, whose wait covers the load, so
+// nothing waits for it.
+__device__ __forceinline__ int touch_norm(const DsParams& p, int s) {
+    const int kind = s < 5 * p.L ? s % 5 : S_HEAD;
+    const int slot = kind == S_QKV ? 0 : kind - 1;
+    const bool gemv = kind != S_ATT && kind != S_HEAD;
+    const float* nw = kind == S_HEAD ? (p.with_head ? p.final_norm : nullptr)
+                      : gemv         ? layer(p, s / 5).norm(slot)
+                                     : nullptr;
+    const int K = gemv ? gemv_k(slot, p.H, p.F) : p.H;
+    const int line = lwave() * 64 + (ltid() & 63);
+    return ld4i(rsrc(nw, nw ? (uint32_t)K * 4 : 0u), (uint32_t)line * 128);
+}
+
 template <int G>
 __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     __shared__ SharedAll sh;
@@ -1259,14 +1318,18 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     // no line of this launch's per-layer vectors may survive in L2 from an
     // earlier launch (they are read with cached loads after the first barrier)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    stage_layers(p);
     int off = 0;  // first workgroup of the current stage
+    int sink = 0;
     for (int s = 0; s < nstages; ++s) {
         const int kind = kind_of(p, s);
         const int l = s / 5;
         const int n = ntasks(p, kind);
         const int first = (wg - off + p.nwg) % p.nwg;  // my first task index here
+        const int touched = s + 1 < nstages ? touch_norm(p, s + 1) : 0;
 
         if (kind == S_HEAD) {
+            if (p.nwg < 0) p.io[2] = sink;  // never true: keeps the prefetch loads
             head_stage(sh, p, first, n);
             if (p.trace && tid == 0) {
                 const uint64_t now = wall_clock64();
@@ -1287,6 +1350,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
         if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2] = wall_clock64();
         if (!grid_barrier(p, gen, &s_abort)) return;
         if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = wall_clock64();
+        sink ^= touched;  // after the barrier's wait: free
     }
 }
 
@@ -1362,6 +1426,10 @@ int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
         default:
             set_error("decode step: query heads per kv head must be 1, 2, 4 or 8");
             return TENZO_ERROR_UNSUPPORTED;
+    }
+    if (p.L > kDsMaxLayers) {
+        set_error("decode step: at most %d layers", kDsMaxLayers);
+        return TENZO_ERROR_UNSUPPORTED;
     }
     if (p.H % 64 || p.F % 64 || p.H > kJ * 4 * kT || p.F > kJ * 4 * kT) {
         set_error("decode step: hidden and ffn sizes must be multiples of 64, at most %d",

@@ -316,7 +316,7 @@ int enqueue_step(tenzo_engine_t e, bool head, int T, int max_chunks) {
 // Whether the persistent kernel can run this model as loaded.
 bool ds_usable(tenzo_engine_t e) {
     if (e->ds_nwg <= 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192 ||
-        e->max_seq > ds_max_context(e->Hq / e->Hkv))
+        e->L > kDsMaxLayers || e->max_seq > ds_max_context(e->Hq / e->Hkv))
         return false;
     for (const DevLayer& d : e->layers)
         if (!d.mlp) return false;
