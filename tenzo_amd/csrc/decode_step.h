@@ -74,6 +74,8 @@ void ds_plan_splits(DsParams& p);
 // Workgroup count the kernel runs with on the current device (a multiple of
 // kDsCounters, all co-resident), or 0 when cooperative launch is unavailable.
 int ds_grid_size();
+// Chunks per kv head the attention stage aims for (one task per workgroup).
+int ds_chunk_budget(int nwg, int Hkv);
 // Attention chunking (C chunks of T tokens per kv head) for context ctx.
 void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T);
 // Longest context the kernel's attention merge supports for G query heads per

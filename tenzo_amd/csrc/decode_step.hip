@@ -230,6 +230,10 @@ union SharedAll {
 
 // -------------------------------------------------------------- schedule --
 
+// Every stage function is inlined into the kernel: a real call would pass the
+// (uniform) pointers in vector registers, and each buffer load through them
+// would become a loop over lanes.
+
 // Rows of the GEMV of stage slot 0..3 (QKV, O, GU, DOWN) and its K.
 __host__ __device__ inline int gemv_rows(int slot, int H, int F, int Hq, int Hkv) {
     return slot == 0 ? (Hq + 2 * Hkv) * kD : slot == 2 ? 2 * F : H;
@@ -250,7 +254,7 @@ __device__ __forceinline__ int kind_of(const DsParams& p, int s) {
 
 // ------------------------------------------------------------- barrier ----
 
-__device__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
+__device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
     ++gen;
     __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are acknowledged
     __syncthreads();
@@ -693,7 +697,7 @@ __device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
 // task is `first` (< n): builds the stage input, stores the slices of it
 // later stages read, normalizes and quantizes it, publishes the code record
 // (task 0) and adds its tasks' K-slice sums into the accumulators.
-__device__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int first, int n) {
+__device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int first, int n) {
     Shared& s = sh.s;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
     const LayerRef Lw = layer(p, l);
@@ -806,14 +810,14 @@ __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
 }
 
 template <int G>
-__device__ void attn_merge(AttnShared& a, const DsParams& p, int l, int h, int g);
+__device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int l, int h, int g);
 
 // Attention of the G query heads of kv head h over context chunk c of layer
 // l (attention_int8_fused, :434-864): q|k|v from the QKV accumulators, RoPE,
 // the new token's K/V quantized and appended, chunk softmax and weighted
 // values; with several chunks the last one to finish merges the partials.
 template <int G>
-__device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c) {
+__device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c) {
     AttnShared& a = sh.a;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
     const int ctx = p.pos + 1;
@@ -1092,7 +1096,7 @@ __device__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c)
 // first kU chunks of each thread and every chunk statistic are loaded
 // together.
 template <int G>
-__device__ void attn_merge(AttnShared& a, const DsParams& p, int l, int h, int g) {
+__device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int l, int h, int g) {
     const int tid = ltid(), lane = tid & 63, wave = lwave();
     const int stride = kPS;
     const float* base = p.part + (size_t)h * p.C * G * stride;
@@ -1197,7 +1201,7 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
 // int8 LM head over row blocks first, first+nwg, ... and the greedy argmax
 // (compute_logits :1660-1700, greedy :1745-1755): a partial per workgroup,
 // reduced by the last workgroup to arrive.
-__device__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
+__device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int first, int n) {
     Shared& s = sh.s;
     const int tid = ltid(), lane = tid & 63, wave = lwave(), wg = blockIdx.x;
     float best = -INFINITY;
@@ -1397,8 +1401,10 @@ int ds_grid_size() {
     return n;
 }
 
+int ds_chunk_budget(int nwg, int Hkv) { return nwg / Hkv; }
+
 void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T) {
-    int c = (nwg * 3 / 4) / Hkv;
+    int c = ds_chunk_budget(nwg, Hkv);
     if (c < 1) c = 1;
     if (c > ctx) c = ctx;
     int t = (ctx + c - 1) / c;

@@ -548,7 +548,7 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
         e->ds_nwg = ds_grid_size();
         if (e->ds_nwg > 0) {
             const int G = Hq / Hkv;
-            int cmax = (e->ds_nwg * 3 / 4) / Hkv;
+            int cmax = ds_chunk_budget(e->ds_nwg, Hkv);
             const int cseq = (int)ceil_div(e->max_seq, kDsMaxChunk);
             if (cseq > cmax) cmax = cseq;
             if (cmax < 1) cmax = 1;
