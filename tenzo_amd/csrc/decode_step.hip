@@ -292,9 +292,15 @@ __device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, i
 // t + 256 j, so wave w's lanes cover groups [256 j + 64 w, 256 j + 64 w + 64);
 // the j with a group below K/4 (wave-uniform). Loads past that count would
 // only read zeros, so they are not issued at all.
+//
+// The count is made opaque at each call, so each loop compares it afresh
+// (s_cmp + s_cbranch per group) instead of carrying the outcome of every
+// j < J from an earlier loop as a lane mask rebuilt with vector instructions.
 __device__ __forceinline__ int wave_groups(int K) {
     const int K4 = K >> 2, w0 = lwave() * 64;
-    return K4 > w0 ? (K4 - w0 + kT - 1) / kT : 0;
+    int J = __builtin_amdgcn_readfirstlane(K4 > w0 ? (K4 - w0 + kT - 1) / kT : 0);
+    asm volatile("" : "+s"(J));
+    return J;
 }
 
 // s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
@@ -568,7 +574,7 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
                                            bool has_w, int K, float eps, float& inv_out,
                                            int& csum_out) {
     const int t = ltid(), lane = t & 63, wave = lwave();
-    const int J = wave_groups(K);  // groups this wave holds
+    int J = wave_groups(K);  // groups this wave holds (made opaque again per loop)
     float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
@@ -585,26 +591,40 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
     ss = (s.red_a[0] + s.red_a[1]) + (s.red_a[2] + s.red_a[3]);
     const float inv_rms = inv_rms_from_sumsq(ss, K, eps);
     float amax = QMAX == 31 ? 1e-6f : 1e-8f;
+    asm volatile("" : "+s"(J));
+    if (has_w) {  // (one branch for the stage, not one per group)
 #pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < J) {
-            float4 y = make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
-                                   __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
-            if (has_w) {
+        for (int j = 0; j < kJ; ++j)
+            if (j < J) {
+                float4 y = make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
+                                       __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
                 y.x = __fmul_rn(y.x, w[j].x);
                 y.y = __fmul_rn(y.y, w[j].y);
                 y.z = __fmul_rn(y.z, w[j].z);
                 y.w = __fmul_rn(y.w, w[j].w);
+                v[j] = y;
+                amax = fmaxf(amax,
+                             fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
             }
-            v[j] = y;
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < kJ; ++j)
+            if (j < J) {
+                const float4 y =
+                    make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
+                                __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
+                v[j] = y;
+                amax = fmaxf(amax,
+                             fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+            }
+    }
     amax = wave_max(amax);
     if (lane == 0) s.red_b[wave] = amax;
     __syncthreads();
     amax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
     const float scale = (float)QMAX / amax;
     int csum = 0;
+    asm volatile("" : "+s"(J));
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
         if (j < J) {
