@@ -557,11 +557,26 @@ __device__ __forceinline__ void finish_act(float4 (&v)[kJ], const InRaw& in, con
     }
 }
 
+// roundf(y * scale) (half away from zero), clamped to [-128, 127] for QMAX
+// 127. For |x| < 2^23, roundf(x) is the truncation of x + copysign(h, x) with
+// h = 0.5 - 2^-25 (the float just below 0.5): with n = floor(|x|), a fraction
+// below 0.5 leaves the sum below the float just under n + 1, and a fraction
+// of at least 0.5 brings it to n + 1 or above (n + 1 - 2^-25 rounds up, to
+// even, when n = 0). The conversion truncates, so a code costs a multiply, a
+// sign copy, an add and a convert.
 template <int QMAX>
 __device__ __forceinline__ int act_code(float y, float scale) {
-    float r = roundf(y * scale);
-    if (QMAX == 127) r = fminf(fmaxf(r, -128.0f), 127.0f);
-    return (int)r;
+    const float x = y * scale;
+    int r = (int)(x + __builtin_copysignf(0.49999997f, x));
+    if (QMAX == 127) r = min(max(r, -128), 127);
+    return r;
+}
+
+// Four codes (low bytes of c0..c3) packed into a word, c0 in the low byte.
+__device__ __forceinline__ uint32_t pack4(int c0, int c1, int c2, int c3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)c1, (uint32_t)c0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)c3, (uint32_t)c2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 // Normalizes v (K elements, zeros past K; rms_norm_raw :148-166 with weight w
@@ -630,9 +645,7 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
         if (j < J) {
             const int c0 = act_code<QMAX>(v[j].x, scale), c1 = act_code<QMAX>(v[j].y, scale);
             const int c2 = act_code<QMAX>(v[j].z, scale), c3 = act_code<QMAX>(v[j].w, scale);
-            *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) =
-                (uint32_t)(c0 & 0xff) | ((uint32_t)(c1 & 0xff) << 8) |
-                ((uint32_t)(c2 & 0xff) << 16) | ((uint32_t)(c3 & 0xff) << 24);
+            *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) = pack4(c0, c1, c2, c3);
             csum += (c0 + c1) + (c2 + c3);
         }
     csum = wave_sum_i32(csum);
