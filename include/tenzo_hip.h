@@ -74,6 +74,19 @@ TENZO_HIP_API int tenzo_hip_bitlinear_tl1(const int8_t* codes, const tenzo_hip_a
                                           int64_t N, int64_t K, float* y, int32_t* acc_out,
                                           void* stream);
 
+/* Multi-token TL1 contraction on int8 MFMA (prefill): the same results as M
+ * separate compute_from_lut calls (TenzoEngine.cpp:129-146), which
+ * prefill_token (TenzoEngine.cpp:1809-1819) makes one token at a time, from
+ * one pass over the packed weights: acc[m][n] and y[m][n] as in
+ * tenzo_hip_bitlinear_tl1, bit for bit. tile = 0 picks the workgroup shape;
+ * 100 * KW + 10 * RW + CT forces 64*RW rows x 32*CT tokens with KW K groups
+ * (142, 242, 442, 222, 422, 221, 421, 412, 411 or 811, with
+ * (N/64) % RW == 0). No scratch memory is used. */
+TENZO_HIP_API int tenzo_hip_bitlinear_tl1_batch(const int8_t* codes, const tenzo_hip_actq_t* q,
+                                                const void* w_packed, float w_scale, int64_t M,
+                                                int64_t N, int64_t K, float* y,
+                                                int32_t* acc_out, int tile, void* stream);
+
 /* executeBitLinearTL1(act, w, out, M, K, N, scale) (ROCmRuntime.h:20-28) on
  * device pointers: quantize each of the M activation rows then run the TL1
  * GEMV over the packed weights. */

@@ -194,4 +194,16 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
 
 __device__ __forceinline__ float i8_to_f32(int v) { return (float)v; }
 
+// Hand-off of split-K partials between workgroups. The partials are written
+// as device-scope atomics or device-coherent stores (both performed past the
+// XCD's L2 and read back with device-scope loads or atomics), so once this
+// wave's vector memory operations are acknowledged they are visible to every
+// workgroup, and a counter atomic issued after a block barrier can announce
+// them. __threadfence() would add a write-back and invalidation of the whole
+// L2 of the XCD (buffer_wbl2 / buffer_inv) to every arrival.
+__device__ __forceinline__ void partials_acked() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace tz

@@ -64,12 +64,11 @@ __device__ void argmax_finish(const ArgmaxWs& am, int nparts) {
     __shared__ int is_last;
     __shared__ float rv[4];
     __shared__ int ri[4];
-    __threadfence();
+    partials_acked();
     __syncthreads();
     if (threadIdx.x == 0) is_last = atomicAdd(am.counter, 1u) == (unsigned)(nparts - 1);
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     float v = -INFINITY;
     int i = INT_MAX;
     for (int p = threadIdx.x; p < nparts; p += 256) {
@@ -113,7 +112,8 @@ argmax_kernel(const float* __restrict__ logits, int64_t V, ArgmaxWs am) {
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; ++w) am_combine(rv[0], ri[0], rv[w], ri[w]);
-        am.part[blockIdx.x] = make_float2(rv[0], __int_as_float(ri[0]));
+        store_coherent(&am.part[blockIdx.x].x, rv[0]);
+        store_coherent(&am.part[blockIdx.x].y, __int_as_float(ri[0]));
     }
     argmax_finish(am, (int)gridDim.x);
 }
@@ -177,7 +177,10 @@ lm_head_i8_kernel(const uint4* __restrict__ w, const int32_t* __restrict__ codes
         if (am.out_idx) {
             int idx = (int)row;
             wave_argmax(val, idx);
-            if (lane == 0) am.part[b] = make_float2(val, __int_as_float(idx));
+            if (lane == 0) {
+                store_coherent(&am.part[b].x, val);
+                store_coherent(&am.part[b].y, __int_as_float(idx));
+            }
         }
     }
     if (am.out_idx) argmax_finish(am, (int)gridDim.x);

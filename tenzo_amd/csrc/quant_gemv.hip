@@ -218,13 +218,12 @@ gq_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
     }
     if (n < N)
         for (int bb = 0; bb < B && bb < BMAX; ++bb)
-            part[((int64_t)sp * B + bb) * N + n] = acc[bb];
-    __threadfence();
+            store_coherent(&part[((int64_t)sp * B + bb) * N + n], acc[bb]);
+    partials_acked();
     __syncthreads();
     if (threadIdx.x == 0) is_last = atomicAdd(&cnt[tile], 1u) == (unsigned)(splits - 1);
     __syncthreads();
     if (!is_last) return;
-    __threadfence();
     if (n < N) {
         for (int bb = 0; bb < B && bb < BMAX; ++bb) {
             float s = 0.0f;

@@ -43,5 +43,12 @@ int launch_tl1_gemv(const int8_t* codes, const tenzo_hip_actq_t* q, const void* 
                     const float* resid, int32_t* acc_out, hipStream_t st, int splits,
                     void* ws);
 int tl1_pick_splits(int64_t nb, int64_t KS, int64_t M);
+// The same contraction for M tokens at once on int8 MFMA (tl1_gemm.hip); the
+// arguments and results are those of launch_tl1_gemv. tile 0 picks the
+// workgroup shape, else 100 * K groups + 10 * row waves + 32-token tiles.
+int launch_tl1_mfma(const int8_t* codes, const tenzo_hip_actq_t* q, const void* w_packed,
+                    const RowScales& rs, int64_t M, int64_t N, int64_t K, float* y,
+                    const float* resid, int32_t* acc_out, hipStream_t st, int tile);
+void tl1_mfma_plan(int64_t M, int64_t N, int64_t KS, int* KW, int* RW, int* CT);
 
 }  // namespace tz

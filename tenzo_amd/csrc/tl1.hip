@@ -227,7 +227,7 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
         const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
         atomicAdd(&ws_acc[m * N + row], tot);
     }
-    __threadfence();
+    partials_acked();
     __syncthreads();
     if (threadIdx.x == 0) {
         const unsigned prev = atomicAdd(&ws_cnt[m * nb + b], 1u);
@@ -235,7 +235,6 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
     }
     __syncthreads();
     if (is_last && wave == 0) {
-        __threadfence();
         const int tot = atomicExch(&ws_acc[m * N + row], 0);
         tl1_finalize(tot, m, row, N, aq, rs, y, resid, acc_out);
         if (lane == 0) atomicExch(&ws_cnt[m * nb + b], 0u);

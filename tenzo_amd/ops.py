@@ -101,6 +101,21 @@ def bitlinear_tl1_into(codes: torch.Tensor, q: torch.Tensor, w_packed: torch.Ten
     return y
 
 
+def bitlinear_tl1_batch(codes: torch.Tensor, q: torch.Tensor, w_packed: torch.Tensor,
+                        w_scale: float, N: int, K: int, want_acc: bool = False,
+                        tile: int = 0, y: torch.Tensor | None = None):
+    """The TL1 contraction of all M token rows of codes at once on int8 MFMA
+    (prefill): the results of bitlinear_tl1, bit for bit."""
+    M = codes.shape[0]
+    if y is None:
+        y = torch.empty((M, N), dtype=torch.float32, device=codes.device)
+    acc = torch.empty((M, N), dtype=torch.int32, device=codes.device) if want_acc else None
+    _lib.check(_lib.load().tenzo_hip_bitlinear_tl1_batch(
+        _ptr(codes), _ptr(q), _ptr(w_packed), w_scale, M, N, K, _ptr(y), _ptr(acc), tile,
+        _stream()), "bitlinear_tl1_batch")
+    return y, acc
+
+
 def bitlinear_tl1_f32(x: torch.Tensor, w_packed: torch.Tensor, w_scale: float, N: int,
                       K: int) -> torch.Tensor:
     """executeBitLinearTL1(act, w, out, M, K, N, scale) on device tensors."""
