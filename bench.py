@@ -19,6 +19,7 @@ runs on), and the reference CPU path (oracle/_ref, compiled from the
 reference's own sources) timed on a bounded sample on the host cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--ctx 4096] [--no-cpu]
+    python bench.py --prefill N   # prompt prefill throughput instead (own JSON line)
 """
 from __future__ import annotations
 
@@ -49,6 +50,10 @@ def parse():
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="engine execution mode (one persistent kernel per token, or one "
                          "kernel per stage replayed from a HIP graph / launched eagerly)")
+    ap.add_argument("--prefill", type=int, default=0, metavar="N",
+                    help="instead of the decode benchmark: prefill an N-token prompt with "
+                         "tenzo_hip_engine_prefill (--steps timed prompts) beside the "
+                         "token-by-token tenzo_prefill_token rate; prints its own JSON line")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one calibration copy of PROBE_COPY_BYTES "
                          "(a plain copy kernel of known size), then --steps chained decode "
@@ -133,7 +138,8 @@ def build_model(torch, cfg, ctx):
             amax = x.abs().amax(dim=2).clamp_min(1e-8)
             c[l] = torch.clamp(torch.round(x * (127.0 / amax)[..., None]), -128, 127).to(torch.int8)
             s[l] = (amax * (1.0 / 127.0)).half()
-    e.set_kv_device(kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(), ctx)
+    if ctx > 0:
+        e.set_kv_device(kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(), ctx)
     e.set_rope_theta(cfg.theta)
     torch.cuda.synchronize()
     host.update(final_norm=final_norm, head=head, hs=hs, kc=kc, vc=vc, ks=ks, vs=vs)
@@ -268,6 +274,78 @@ def cpu_baseline(torch, cfg, host, ctx, seconds):
                       f"with its own flags, OpenMP {threads} threads)"}
 
 
+def mfma_roofline(torch, cfg, host, M):
+    """The int8 MFMA contraction as the batched prefill runs it: the four
+    projections of one layer at M rows (the whole pass), each replayed from a
+    graph and timed with HIP events. Algorithmic work = 2*M*N*K integer ops;
+    the dominant (largest) projection is reported against the 5.0 POP/s dense
+    int8 peak."""
+    from tenzo_amd import ops
+    H, F, qd, kvd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim
+    tl1, _, _ = host["layers"][0]
+    mats = {"qkv": (torch.cat([tl1["q"], tl1["k"], tl1["v"]]), qd + 2 * kvd, H),
+            "o": (tl1["o"], H, H), "gate_up": (torch.cat([tl1["gate"], tl1["up"]]), 2 * F, H),
+            "down": (tl1["down"], H, F)}
+    out = {}
+    for name, (w, n, k) in mats.items():
+        wp = ops.tl1_repack(w, n, k)
+        codes, q, _ = ops.rmsnorm_quant31(torch.randn(M, k, device="cuda"), None)
+        y = torch.empty((M, n), device="cuda")
+        t = graph_time(torch, lambda: ops.bitlinear_tl1_batch(codes, q, wp, 0.0159, n, k, y=y), 20)
+        out[name] = {"N": n, "K": k, "us": round(t * 1e6, 2),
+                     "tops": round(2.0 * M * n * k / t / 1e12, 1)}
+    return out
+
+
+def prefill_bench(torch, e, cfg, host, args):
+    n = args.prefill
+    if n > cfg.max_seq:
+        raise SystemExit(f"--prefill {n} exceeds the context ({cfg.max_seq})")
+    toks = np.random.default_rng(SEED).integers(0, cfg.vocab, n).astype(np.int32)
+    e.rewind(0)
+    e.prefill_batch(toks[:min(n, 64)])  # first use allocates the prefill buffers
+    for _ in range(max(args.warmup, 1)):
+        e.rewind(0)
+        e.prefill_batch(toks)
+    times = []
+    for _ in range(args.steps):
+        e.rewind(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e.prefill_batch(toks)  # streaming attention; returns after the device finished
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
+    # the reference's way: one prefill_token per prompt token (persistent kernel)
+    seq_n = min(n, 64)
+    e.rewind(0)
+    for t in toks[:4]:
+        e.prefill(int(t))
+    e.rewind(0)
+    t0 = time.perf_counter()
+    for t in toks[:seq_n]:
+        e.prefill(int(t))
+    seq_rate = seq_n / (time.perf_counter() - t0)
+    rows = min(n, 512)
+    roof = mfma_roofline(torch, cfg, host, rows)
+    dom = max(roof.values(), key=lambda r: r["N"] * r["K"])
+    out = {
+        "metric": "prefill_tokens_per_s", "value": round(n / dt, 1), "unit": "tok/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": f"BitNet-b1.58-2B-shaped prompt prefill, {n} tokens from "
+                               "position 0, batch 1 (tenzo_hip_engine_prefill)",
+                   "prompt_tokens": n, "rows_per_pass": 512},
+        "token_by_token_tok_s": round(seq_rate, 1),
+        "speedup_vs_token_by_token": round(n / dt / seq_rate, 1),
+        "roofline": {"bound": "mfma", "kernel": "tl1_mfma_kernel (gate|up projection)",
+                     "achieved": dom["tops"], "peak": 5000.0, "unit": "TOP/s",
+                     "frac": round(dom["tops"] / 5000.0, 4), "traffic": None,
+                     "rows": rows, "per_projection": roof},
+    }
+    print(json.dumps(out), flush=True)
+
+
 # ------------------------------------------------------------------- main
 
 def main():
@@ -281,8 +359,12 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU (the decode path has no CPU fallback)")
     cfg = synth.BITNET_2B
-    ctx = args.ctx
+    ctx = 0 if args.prefill else args.ctx
     e, host = build_model(torch, cfg, ctx)
+    if args.prefill:
+        prefill_bench(torch, e, cfg, host, args)
+        e.close()
+        return
     e.set_mode(args.mode)
     mode = e.mode
     if args.pmc_probe:

@@ -200,6 +200,19 @@ TENZO_HIP_API int tenzo_hip_execute_rmsnorm(const float* in, const float* w, flo
 
 /* ---- engine extensions (the engine itself is include/tenzo.h) ----------- */
 struct tenzo_engine_opaque;
+/* Prefills n prompt tokens (host array) at positions seq_len .. seq_len+n-1:
+ * the KV cache, the hidden state and seq_len end as after n calls of
+ * tenzo_prefill_token (TenzoEngine.cpp:1809-1819, C API :2187), which is how
+ * the reference prefills a prompt (main_inference.cpp:470-472). Each layer
+ * runs once per pass of up to 512 tokens: the TL1 projections as int8 MFMA
+ * contractions (tenzo_hip_bitlinear_tl1_batch), then every token's attention
+ * over its own prefix. exact != 0: the attention repeats a decode step's
+ * chunking and arithmetic per token, so everything equals the per-token
+ * kernels of the non-persistent modes bit for bit; exact == 0 (fast): one
+ * streaming pass per token with an online softmax, equal up to fp32 rounding
+ * of the softmax sums. */
+TENZO_HIP_API int tenzo_hip_engine_prefill(struct tenzo_engine_opaque* e, const int32_t* tokens,
+                                           int n, int exact);
 /* Copies a prefilled INT8 KV cache (codes [L][Hkv][seq_len][128], fp16 scales
  * [L][Hkv][seq_len]) into the engine and sets its sequence length; pointers
  * are device memory when is_device, else host. Mirrors writing the public

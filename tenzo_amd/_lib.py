@@ -56,6 +56,7 @@ SIGNATURES = {
     "tenzo_hip_engine_get_mode": (_I, [_P]),
     "tenzo_hip_engine_trace": (_I, [_P, _I]),
     "tenzo_hip_engine_decode": (_I, [_P, _I, _I, _P, _P]),
+    "tenzo_hip_engine_prefill": (_I, [_P, _P, _I, _I]),
     "tenzo_hip_engine_get_trace": (_I64, [_P, _P, _I64]),
     "tenzo_hip_engine_stream": (_P, [_P]),
     # include/tenzo.h

@@ -32,4 +32,31 @@ struct AttnLaunch {
 int attn_pick_chunk(int seq_len, int Hkv, int B);
 int launch_attn(const AttnLaunch& L, hipStream_t st);
 
+// Attention for n prompt tokens at positions pos0 .. pos0+n-1 over one INT8
+// cache: the k/v rows of all n tokens are RoPE'd, quantized and appended
+// first (as n decode steps would), then query i attends to positions
+// 0 .. pos0+i. exact: with the chunking and arithmetic of a decode step at
+// that position (chunk by chunk, then the decode merge), so every output
+// equals the one n sequential decode steps produce bit for bit; otherwise a
+// streaming pass per query (one wave, 64-token blocks, online softmax), equal
+// to within fp32 rounding of the softmax sums and far faster. q / k_new /
+// v_new are rows of row_stride elements (q at column 0, k and v where the
+// pointers say); out rows are out_stride apart.
+struct AttnPrefill {
+    const float* q = nullptr;
+    const float* k_new = nullptr;
+    const float* v_new = nullptr;
+    int64_t row_stride = 0;
+    int8_t* kc = nullptr;
+    int8_t* vc = nullptr;
+    uint16_t* ks = nullptr;
+    uint16_t* vs = nullptr;
+    const float* rope = nullptr;  // [max_seq][128]
+    int pos0 = 0, n = 0, Hq = 0, Hkv = 0, max_seq = 0;
+    float* out = nullptr;
+    int64_t out_stride = 0;
+    int exact = 0;
+};
+int launch_attn_prefill(const AttnPrefill& P, hipStream_t st);
+
 }  // namespace tz

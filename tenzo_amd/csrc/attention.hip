@@ -14,6 +14,8 @@
 // Lane mapping (both passes): a wave takes 8 tokens at a time; lane l reads
 // 16 bytes = dims (l%8)*16 .. +15 of token l/8, so one wave load is 1 KiB of
 // contiguous cache rows.
+#include <algorithm>
+
 #include "attention.h"
 #include "common.h"
 
@@ -21,6 +23,17 @@ namespace tz {
 
 constexpr int kD = 128;
 constexpr float kScaleFactor = 0.08838834764831845f;  // 1/sqrt(128)
+
+// Tokens per chunk for a context of seq_len: ~512 workgroups over the chip,
+// chunks of 32 .. kMaxChunk tokens.
+__host__ __device__ inline int pick_chunk(int seq_len, int Hkv, int B) {
+    const int target = (512 + Hkv * B - 1) / (Hkv * B);
+    int T = (seq_len + target - 1) / target;
+    T = (T + 31) / 32 * 32;
+    if (T < 32) T = 32;
+    if (T > kMaxChunk) T = kMaxChunk;
+    return T;
+}
 
 struct AttnArgs {
     const float* q;      // [B][Hq][128]
@@ -36,6 +49,14 @@ struct AttnArgs {
     int rope_indexed;
     int Hq, Hkv, max_seq, T;
     int64_t cache_batch_stride;  // elements between sequences' caches
+    int64_t q_stride;            // elements between the rows of q (per sequence / token)
+    int64_t kv_stride;           // elements between the rows of k_new / v_new
+    int64_t out_stride;          // elements between the rows of out
+    // Prefill: row b of q / out is the query of position pos + b over one
+    // cache whose k/v rows (through pos + b) are already appended; each query
+    // takes the chunk size decode would pick at its position (attn_pick_chunk).
+    int prefill;
+    int pos_n;  // streaming prefill: number of query rows
     float* out;          // [B][Hq][128] (used when nchunks == 1)
     float* part;         // [B][Hq][max_chunks][130] partials
     int max_chunks;
@@ -68,85 +89,28 @@ __device__ __forceinline__ void quant_kv_pair(float x0, float x1, int8_t* codes_
     *s_out = __fmul_rn(amax, 1.0f / 127.0f);
 }
 
+// One context chunk of the G query heads that share a kv head: scores of
+// tokens t0 .. t0+nt-1 against the rotated queries qs, the chunk's softmax
+// statistics, and the weighted values. On return (after a block barrier)
+// ow[w][g][:] hold the 4 waves' value sums and mstat / lstat the chunk's max
+// and exponent sum; the chunk partial of head g is then
+// o = (ow[0] + ow[1]) + (ow[2] + ow[3]). When has_new, position pos reads the
+// just-quantized row from newk / newv / news instead of the cache. Shared by
+// the decode chunk kernel and the prefill kernel, so both sum in one order.
 template <int G>
-__global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
-    __shared__ float qs[G][kD];
-    __shared__ float sc[G][kMaxChunk];
-    __shared__ float ow[4][G][kD];
-    __shared__ float mstat[G], lstat[G];
-    __shared__ __align__(16) int8_t newk[kD];
-    __shared__ __align__(16) int8_t newv[kD];
-    __shared__ float news[2];
-
-    const int c = blockIdx.x;
-    const int h = blockIdx.y;
-    const int b = blockIdx.z;
+__device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&sc)[G][kMaxChunk],
+                                              float (&ow)[4][G][kD], float* mstat, float* lstat,
+                                              const int8_t* __restrict__ kbase,
+                                              const int8_t* __restrict__ vbase,
+                                              const uint16_t* __restrict__ ksb,
+                                              const uint16_t* __restrict__ vsb, int t0, int nt,
+                                              bool has_new, int pos, const int8_t* newk,
+                                              const int8_t* newv, const float* news) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
-    const int seq_len = pos + 1;
-    const int t0 = c * a.T;
-    if (t0 >= seq_len) return;  // chunks past the context (fixed-size graph grids)
-    const int t1 = min(t0 + a.T, seq_len);
-    const int nt = t1 - t0;
-    const int nchunks = (seq_len + a.T - 1) / a.T;
-    const float* rope = a.rope + (a.rope_indexed ? (int64_t)pos * kD : 0);
-
-    // ---- RoPE on the G query heads (:460-481) ----
-    for (int i = tid; i < G * 64; i += 256) {
-        const int g = i >> 6, j = i & 63;
-        const int qh = h * G + g;
-        const float* qv = a.q + ((int64_t)b * a.Hq + qh) * kD;
-        const float x0 = qv[j], x1 = qv[j + 64];
-        const float cs = rope[j], sn = rope[64 + j];
-        const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
-        const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
-        qs[g][j] = r0;
-        qs[g][j + 64] = r1;
-        if (a.q_rot && c == 0) {
-            float* qr = a.q_rot + ((int64_t)b * a.Hq + qh) * kD;
-            qr[j] = r0;
-            qr[j + 64] = r1;
-        }
-    }
-    // ---- new token: RoPE on k, quantize-append k and v (:482-533) ----
-    const bool has_new = pos >= t0 && pos < t1;
-    const int64_t cache_head = (int64_t)b * a.cache_batch_stride + (int64_t)h * a.max_seq;
-    if (has_new && wave < 2) {
-        const float* src = (wave == 0 ? a.k_new : a.v_new) + ((int64_t)b * a.Hkv + h) * kD;
-        float x0 = src[lane], x1 = src[lane + 64];
-        if (wave == 0) {
-            const float cs = rope[lane], sn = rope[64 + lane];
-            const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
-            const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
-            x0 = r0;
-            x1 = r1;
-            if (a.k_rot) {
-                float* kr = a.k_rot + ((int64_t)b * a.Hkv + h) * kD;
-                kr[lane] = r0;
-                kr[lane + 64] = r1;
-            }
-        }
-        float s;
-        quant_kv_pair(x0, x1, wave == 0 ? newk : newv, lane, &s);
-        const uint16_t sh = float_to_half_bits(s);
-        int8_t* dst = (wave == 0 ? a.kc : a.vc) + (cache_head + pos) * kD;
-        dst[lane] = (wave == 0 ? newk : newv)[lane];
-        dst[lane + 64] = (wave == 0 ? newk : newv)[lane + 64];
-        if (lane == 0) {
-            (wave == 0 ? a.ks : a.vs)[cache_head + pos] = sh;
-            news[wave] = half_bits_to_float(sh);
-        }
-    }
-    __syncthreads();
-
     const int sub = lane >> 3;       // token within the wave's group of 8
     const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
-    const int8_t* kbase = a.kc + cache_head * kD;
-    const int8_t* vbase = a.vc + cache_head * kD;
-    const uint16_t* ksb = a.ks + cache_head;
-    const uint16_t* vsb = a.vs + cache_head;
 
     // ---- scores (:678-694) ----
     {
@@ -162,7 +126,7 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
             float skf = 0.0f;
             if (tl < nt) {
                 uint4 kv;
-                if (t == pos) {
+                if (has_new && t == pos) {
                     kv = *reinterpret_cast<const uint4*>(newk + d0);
                     skf = news[0];
                 } else {
@@ -226,7 +190,7 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
         if (tl < nt) {
             uint4 vv;
             float svf;
-            if (t == pos) {
+            if (has_new && t == pos) {
                 vv = *reinterpret_cast<const uint4*>(newv + d0);
                 svf = news[1];
             } else {
@@ -261,12 +225,94 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
             for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
     }
     __syncthreads();
+}
+
+template <int G>
+__global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
+    __shared__ float qs[G][kD];
+    __shared__ float sc[G][kMaxChunk];
+    __shared__ float ow[4][G][kD];
+    __shared__ float mstat[G], lstat[G];
+    __shared__ __align__(16) int8_t newk[kD];
+    __shared__ __align__(16) int8_t newv[kD];
+    __shared__ float news[2];
+
+    const int c = blockIdx.x;
+    const int h = blockIdx.y;
+    const int b = blockIdx.z;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + (a.prefill ? b : 0);
+    const int seq_len = pos + 1;
+    const int T = a.prefill ? pick_chunk(seq_len, a.Hkv, 1) : a.T;
+    const int t0 = c * T;
+    if (t0 >= seq_len) return;  // chunks past the context (fixed-size grids)
+    const int t1 = min(t0 + T, seq_len);
+    const int nt = t1 - t0;
+    const int nchunks = (seq_len + T - 1) / T;
+    const float* rope = a.rope + (a.rope_indexed ? (int64_t)pos * kD : 0);
+
+    // ---- RoPE on the G query heads (:460-481) ----
+    for (int i = tid; i < G * 64; i += 256) {
+        const int g = i >> 6, j = i & 63;
+        const int qh = h * G + g;
+        const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)qh * kD;
+        const float x0 = qv[j], x1 = qv[j + 64];
+        const float cs = rope[j], sn = rope[64 + j];
+        const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+        const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+        qs[g][j] = r0;
+        qs[g][j + 64] = r1;
+        if (a.q_rot && c == 0) {
+            float* qr = a.q_rot + ((int64_t)b * a.Hq + qh) * kD;
+            qr[j] = r0;
+            qr[j + 64] = r1;
+        }
+    }
+    // ---- new token: RoPE on k, quantize-append k and v (:482-533) ----
+    const bool has_new = !a.prefill && pos >= t0 && pos < t1;
+    const int64_t cache_head = (int64_t)b * a.cache_batch_stride + (int64_t)h * a.max_seq;
+    if (has_new && wave < 2) {
+        const float* src = (wave == 0 ? a.k_new : a.v_new) + (int64_t)b * a.kv_stride + (int64_t)h * kD;
+        float x0 = src[lane], x1 = src[lane + 64];
+        if (wave == 0) {
+            const float cs = rope[lane], sn = rope[64 + lane];
+            const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+            const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+            x0 = r0;
+            x1 = r1;
+            if (a.k_rot) {
+                float* kr = a.k_rot + ((int64_t)b * a.Hkv + h) * kD;
+                kr[lane] = r0;
+                kr[lane + 64] = r1;
+            }
+        }
+        float s;
+        quant_kv_pair(x0, x1, wave == 0 ? newk : newv, lane, &s);
+        const uint16_t sh = float_to_half_bits(s);
+        int8_t* dst = (wave == 0 ? a.kc : a.vc) + (cache_head + pos) * kD;
+        dst[lane] = (wave == 0 ? newk : newv)[lane];
+        dst[lane + 64] = (wave == 0 ? newk : newv)[lane + 64];
+        if (lane == 0) {
+            (wave == 0 ? a.ks : a.vs)[cache_head + pos] = sh;
+            news[wave] = half_bits_to_float(sh);
+        }
+    }
+    __syncthreads();
+
+    const int8_t* kbase = a.kc + cache_head * kD;
+    const int8_t* vbase = a.vc + cache_head * kD;
+    const uint16_t* ksb = a.ks + cache_head;
+    const uint16_t* vsb = a.vs + cache_head;
+    chunk_partial<G>(qs, sc, ow, mstat, lstat, kbase, vbase, ksb, vsb, t0, nt, has_new, pos, newk,
+                     newv, news);
     for (int i = tid; i < G * kD; i += 256) {
         const int g = i >> 7, d = i & 127;
         const float o = (ow[0][g][d] + ow[1][g][d]) + (ow[2][g][d] + ow[3][g][d]);
         const int qh = h * G + g;
         if (nchunks == 1) {
-            a.out[((int64_t)b * a.Hq + qh) * kD + d] = __fdiv_rn(o, lstat[g]);
+            a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, lstat[g]);
         } else {
             float* pp = a.part + (((int64_t)b * a.Hq + qh) * a.max_chunks + c) * kPartStride;
             pp[2 + d] = o;
@@ -281,8 +327,9 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
 // Merge of the chunk partials; one 128-thread block per (query head, sequence).
 __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-    const int pos = a.pos_dev ? *a.pos_dev : a.pos;
-    const int nchunks = (pos + 1 + a.T - 1) / a.T;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + (a.prefill ? b : 0);
+    const int T = a.prefill ? pick_chunk(pos + 1, a.Hkv, 1) : a.T;
+    const int nchunks = (pos + 1 + T - 1) / T;
     if (nchunks == 1) return;  // the chunk kernel wrote the output
     const float* pp = a.part + ((int64_t)b * a.Hq + qh) * a.max_chunks * kPartStride;
     float M = -1e30f;
@@ -293,18 +340,246 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
         L = __builtin_fmaf(e, pp[c * kPartStride + 1], L);
         o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
     }
-    a.out[((int64_t)b * a.Hq + qh) * kD + d] = __fdiv_rn(o, L);
+    a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, L);
 }
 
-int attn_pick_chunk(int seq_len, int Hkv, int B) {
-    // ~512 workgroups over the chip, chunks of 32..kMaxChunk tokens.
-    const int64_t target = ceil_div(512, (int64_t)Hkv * B);
-    int64_t T = ceil_div(seq_len, target);
-    T = ceil_div(T, 32) * 32;
-    if (T < 32) T = 32;
-    if (T > kMaxChunk) T = kMaxChunk;
-    return (int)T;
+// Prefill attention: one workgroup per (kv head, query row b) walks the
+// query's context chunks in order with chunk_partial (the decode chunk
+// kernel's arithmetic and chunk size at that position), keeps each chunk's
+// (m, l) in LDS and its value sums in the partial scratch (each value written
+// and read back by the same thread), then merges the chunks exactly as
+// attn_combine_kernel does. Dynamic LDS: m and l of G heads x max_chunks.
+template <int G>
+__global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
+    __shared__ float qs[G][kD];
+    __shared__ float sc[G][kMaxChunk];
+    __shared__ float ow[4][G][kD];
+    __shared__ float mstat[G], lstat[G];
+    extern __shared__ float cstat[];
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int pos = a.pos + b;
+    const int seq_len = pos + 1;
+    const int T = pick_chunk(seq_len, a.Hkv, 1);
+    const int nchunks = (seq_len + T - 1) / T;
+    const float* rope = a.rope + (int64_t)pos * kD;
+    for (int i = tid; i < G * 64; i += 256) {  // RoPE on the G query heads (:460-481)
+        const int g = i >> 6, j = i & 63;
+        const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)(h * G + g) * kD;
+        const float x0 = qv[j], x1 = qv[j + 64];
+        const float cs = rope[j], sn = rope[64 + j];
+        qs[g][j] = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+        qs[g][j + 64] = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+    }
+    __syncthreads();
+    const int64_t cache_head = (int64_t)h * a.max_seq;
+    float* mst = cstat;                       // [G][max_chunks]
+    float* lst = cstat + G * a.max_chunks;    // [G][max_chunks]
+    for (int c = 0; c < nchunks; ++c) {
+        const int t0 = c * T;
+        const int nt = min(t0 + T, seq_len) - t0;
+        chunk_partial<G>(qs, sc, ow, mstat, lstat, a.kc + cache_head * kD, a.vc + cache_head * kD,
+                         a.ks + cache_head, a.vs + cache_head, t0, nt, false, pos, nullptr,
+                         nullptr, nullptr);
+        for (int i = tid; i < G * kD; i += 256) {
+            const int g = i >> 7, d = i & 127;
+            const float o = (ow[0][g][d] + ow[1][g][d]) + (ow[2][g][d] + ow[3][g][d]);
+            const int qh = h * G + g;
+            if (nchunks == 1)
+                a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, lstat[g]);
+            else
+                a.part[(((int64_t)b * a.Hq + qh) * a.max_chunks + c) * kPartStride + 2 + d] = o;
+        }
+        if (tid < G) {
+            mst[tid * a.max_chunks + c] = mstat[tid];
+            lst[tid * a.max_chunks + c] = lstat[tid];
+        }
+        __syncthreads();  // ow, sc and the statistics are reused by the next chunk
+    }
+    if (nchunks == 1) return;
+    for (int i = tid; i < G * kD; i += 256) {  // attn_combine_kernel's merge
+        const int g = i >> 7, d = i & 127;
+        const int qh = h * G + g;
+        const float* pp = a.part + ((int64_t)b * a.Hq + qh) * a.max_chunks * kPartStride;
+        const float* mg = mst + g * a.max_chunks;
+        const float* lg = lst + g * a.max_chunks;
+        float M = -1e30f;
+        for (int c = 0; c < nchunks; ++c) M = fmaxf(M, mg[c]);
+        float L = 0.0f, o = 0.0f;
+        for (int c = 0; c < nchunks; ++c) {
+            const float e = expf(mg[c] - M);
+            L = __builtin_fmaf(e, lg[c], L);
+            o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
+        }
+        a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, L);
+    }
 }
+
+// Prefill attention, streaming form: one wave per (query row b, kv head h)
+// walks the query's causal prefix in blocks of 64 tokens with an online
+// softmax (running max m, sum l and value sums, rescaled when m grows). The
+// lane mapping is the decode kernel's: lane l holds dims (l%8)*16 .. +15 of
+// token l/8 of each group of 8, so one wave load is 1 KiB of cache rows and
+// the 8 lanes of a token finish its dot product with three DPP adds. The
+// scores, scales and exponentials are those of the decode kernel; only the
+// grouping of the softmax sums differs (fp32, well inside 1e-3). Four waves =
+// four consecutive queries of one kv head, whose K/V reads overlap in L1.
+template <int G>
+__global__ void __launch_bounds__(256) attn_prefill_stream_kernel(AttnArgs a) {
+    __shared__ float qs[4][G][kD];
+    const int h = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // the longest prefixes (last queries) are dispatched first
+    const int b = (gridDim.x - 1 - blockIdx.x) * 4 + wave;
+    const bool live = b < a.pos_n;
+    const int pos = a.pos + (live ? b : 0);
+    const float* rope = a.rope + (int64_t)pos * kD;
+    // RoPE on the G query heads of this wave's query (:460-481)
+    for (int i = lane; i < G * 64; i += 64) {
+        const int g = i >> 6, j = i & 63;
+        const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)(h * G + g) * kD;
+        const float x0 = live ? qv[j] : 0.0f, x1 = live ? qv[j + 64] : 0.0f;
+        const float cs = rope[j], sn = rope[64 + j];
+        qs[wave][g][j] = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+        qs[wave][g][j + 64] = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+    }
+    __syncthreads();
+    if (!live) return;
+    const int sub = lane >> 3, d0 = (lane & 7) * 16;
+    float qr[G][16];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) qr[g][j] = qs[wave][g][d0 + j];
+    const int64_t cache_head = (int64_t)h * a.max_seq;
+    const int8_t* kbase = a.kc + cache_head * kD;
+    const int8_t* vbase = a.vc + cache_head * kD;
+    const uint16_t* ksb = a.ks + cache_head;
+    const uint16_t* vsb = a.vs + cache_head;
+    float m[G], l[G], acc[G][16];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = -1e30f;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+    }
+    const int seq_len = pos + 1;
+    for (int t0 = 0; t0 < seq_len; t0 += 64) {
+        // scores of the block's 64 tokens: 8 groups of 8, this lane's token
+        // of group r is t0 + 8r + sub
+        float sc[8][G];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int t = t0 + 8 * r + sub;
+            const bool ok = t < seq_len;
+            float kf[16];
+            uint4 kv = make_uint4(0, 0, 0, 0);
+            if (ok) kv = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
+            unpack16(kv, kf);
+            const float f = ok ? __fmul_rn(half_bits_to_float(ksb[t]), kScaleFactor) : 0.0f;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
+                s += dpp_f<kDppXor1>(s);
+                s += dpp_f<kDppXor2>(s);
+                s += dpp_f<kDppHalfMirror>(s);
+                sc[r][g] = ok ? __fmul_rn(s, f) : -1e30f;
+            }
+        }
+        // online softmax: block max, rescale, exponentials
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float bm = sc[0][g];
+#pragma unroll
+            for (int r = 1; r < 8; ++r) bm = fmaxf(bm, sc[r][g]);
+            bm = wave_max(bm);
+            const float mn = fmaxf(m[g], bm);
+            const float corr = expf(m[g] - mn);
+            m[g] = mn;
+            float ls = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) {
+                const float e = sc[r][g] > -1e29f ? expf(sc[r][g] - mn) : 0.0f;
+                sc[r][g] = e;
+                ls += e;
+            }
+            // each token's exponential sits in its 8 lanes: sum one lane per token
+            ls = (lane & 7) == 0 ? ls : 0.0f;
+            l[g] = __builtin_fmaf(l[g], corr, wave_sum_tree(ls));
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[g][j] = __fmul_rn(acc[g][j], corr);
+        }
+        // weighted values of the block
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int t = t0 + 8 * r + sub;
+            if (t < seq_len) {
+                float vf[16];
+                unpack16(*reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0), vf);
+                const float sv = half_bits_to_float(vsb[t]);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float wgt = __fmul_rn(sc[r][g], sv);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
+                }
+            }
+        }
+    }
+    // reduce over the 8 token lanes that share dims, normalise, store
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float v = acc[g][j];
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            acc[g][j] = v;
+        }
+    if (lane < 8) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float* o = a.out + (int64_t)b * a.out_stride + (int64_t)(h * G + g) * kD + d0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) o[j] = __fdiv_rn(acc[g][j], l[g]);
+        }
+    }
+}
+
+// Prefill append: RoPE on k and the INT8 quantization of k and v for the
+// tokens at positions pos .. pos + n - 1, with the arithmetic of the decode
+// kernel's append (so the cache matches one decode step per token). Grid
+// (n, Hkv), 128 threads: wave 0 k, wave 1 v.
+__global__ void __launch_bounds__(128) attn_append_kernel(AttnArgs a) {
+    __shared__ __align__(16) int8_t codes[2][kD];
+    const int i = blockIdx.x, h = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int pos = a.pos + i;
+    const float* rope = a.rope + (int64_t)pos * kD;
+    const float* src = (wave == 0 ? a.k_new : a.v_new) + (int64_t)i * a.kv_stride + (int64_t)h * kD;
+    float x0 = src[lane], x1 = src[lane + 64];
+    if (wave == 0) {
+        const float cs = rope[lane], sn = rope[64 + lane];
+        const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+        const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+        x0 = r0;
+        x1 = r1;
+    }
+    float s;
+    quant_kv_pair(x0, x1, codes[wave], lane, &s);
+    const int64_t row = (int64_t)h * a.max_seq + pos;
+    int8_t* dst = (wave == 0 ? a.kc : a.vc) + row * kD;
+    dst[lane] = codes[wave][lane];
+    dst[lane + 64] = codes[wave][lane + 64];
+    if (lane == 0) (wave == 0 ? a.ks : a.vs)[row] = float_to_half_bits(s);
+}
+
+int attn_pick_chunk(int seq_len, int Hkv, int B) { return pick_chunk(seq_len, Hkv, B); }
 
 int launch_attn(const AttnLaunch& L, hipStream_t st) {
     const int G = L.Hq / L.Hkv;
@@ -325,6 +600,10 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
     a.max_seq = L.max_seq;
     a.T = L.T;
     a.cache_batch_stride = (int64_t)L.Hkv * L.max_seq;
+    a.q_stride = (int64_t)L.Hq * kD;
+    a.kv_stride = (int64_t)L.Hkv * kD;
+    a.out_stride = (int64_t)L.Hq * kD;
+    a.prefill = 0;
     a.out = L.out;
     a.max_chunks = L.max_chunks;
     a.q_rot = L.q_rot;
@@ -351,6 +630,86 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
         rc = launch_status("attn_combine_kernel");
     }
     return rc;
+}
+
+int attn_prefill_max_chunks(int pos0, int n, int Hkv) {
+    int mx = 1;
+    for (int i = 0; i < n; ++i) {
+        const int sl = pos0 + i + 1, T = pick_chunk(sl, Hkv, 1);
+        mx = std::max(mx, (sl + T - 1) / T);
+    }
+    return mx;
+}
+
+int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
+    const int G = P.Hq / P.Hkv;
+    AttnArgs a{};
+    a.q = P.q;
+    a.k_new = P.k_new;
+    a.v_new = P.v_new;
+    a.kc = P.kc;
+    a.vc = P.vc;
+    a.ks = P.ks;
+    a.vs = P.vs;
+    a.rope = P.rope;
+    a.pos = P.pos0;
+    a.rope_indexed = 1;
+    a.Hq = P.Hq;
+    a.Hkv = P.Hkv;
+    a.max_seq = P.max_seq;
+    a.cache_batch_stride = 0;
+    a.q_stride = P.row_stride;
+    a.kv_stride = P.row_stride;
+    a.out_stride = P.out_stride;
+    a.out = P.out;
+    a.prefill = 1;
+    hipLaunchKernelGGL(attn_append_kernel, dim3(P.n, P.Hkv), dim3(128), 0, st, a);
+    int rc = launch_status("attn_append_kernel");
+    if (rc) return rc;
+    if (!P.exact && (G == 1 || G == 2 || G == 4)) {
+        a.pos_n = P.n;
+        dim3 grid((unsigned)ceil_div(P.n, 4), P.Hkv);
+        switch (G) {
+            case 1: hipLaunchKernelGGL(attn_prefill_stream_kernel<1>, grid, dim3(256), 0, st, a); break;
+            case 2: hipLaunchKernelGGL(attn_prefill_stream_kernel<2>, grid, dim3(256), 0, st, a); break;
+            default: hipLaunchKernelGGL(attn_prefill_stream_kernel<4>, grid, dim3(256), 0, st, a); break;
+        }
+        return launch_status("attn_prefill_stream_kernel");
+    }
+    // exact form: queries in groups whose chunk partials fit ~64 MiB of scratch
+    const int mc = attn_prefill_max_chunks(P.pos0, P.n, P.Hkv);
+    const size_t per_query = (size_t)P.Hq * mc * kPartStride * 4;
+    const int qg_max = mc > 1 ? (int)std::max<size_t>(1, std::min<size_t>(P.n, (64u << 20) / per_query))
+                              : P.n;
+    const size_t lds = (size_t)2 * G * mc * 4;
+    if (lds > 64 * 1024) {
+        set_error("prefill attention: %d chunks per query exceed the LDS budget", mc);
+        return TENZO_ERROR_UNSUPPORTED;
+    }
+    for (int i0 = 0; i0 < P.n; i0 += qg_max) {
+        const int n = std::min(qg_max, P.n - i0);
+        a.pos = P.pos0 + i0;
+        a.q = P.q + (int64_t)i0 * P.row_stride;
+        a.out = P.out + (int64_t)i0 * P.out_stride;
+        a.max_chunks = mc;
+        a.part = nullptr;
+        if (mc > 1) {
+            a.part = (float*)Scratch::get(kScratchAttn, (size_t)n * per_query, st);
+            if (!a.part) return TENZO_ERROR_OUT_OF_MEMORY;
+        }
+        dim3 grid(P.Hkv, n);
+        switch (G) {
+            case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(256), lds, st, a); break;
+            case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(256), lds, st, a); break;
+            case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(256), lds, st, a); break;
+            case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(256), lds, st, a); break;
+            default:
+                set_error("attention: query heads per kv head must be 1, 2, 4 or 8 (got %d)", G);
+                return TENZO_ERROR_UNSUPPORTED;
+        }
+        if ((rc = launch_status("attn_prefill_kernel"))) return rc;
+    }
+    return TENZO_SUCCESS;
 }
 
 }  // namespace tz

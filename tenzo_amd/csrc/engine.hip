@@ -23,6 +23,7 @@
 // same stages as separate kernels, replayed from a captured HIP graph
 // (position and token read from device memory, one graph per attention chunk
 // size) or launched eagerly, remain selectable (tenzo_hip_engine_set_mode).
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <string>
@@ -109,6 +110,17 @@ struct tenzo_engine_opaque {
     int32_t* dec_out = nullptr;  // device tokens of tenzo_hip_engine_decode
     int dec_cap = 0;
     uint64_t* ds_trace = nullptr;  // step trace (tenzo_hip_engine_trace), null when off
+
+    // batched prefill (tenzo_hip_engine_prefill): rows of up to pf_cap tokens
+    int pf_cap = 0;
+    float* pf_x = nullptr;
+    float* pf_h1 = nullptr;
+    float* pf_qkv = nullptr;
+    float* pf_attn = nullptr;
+    float* pf_gu = nullptr;
+    int8_t* pf_codes = nullptr;
+    tenzo_hip_actq_t* pf_aq = nullptr;
+    int32_t* pf_tok = nullptr;
 
 };
 
@@ -311,6 +323,147 @@ int enqueue_step(tenzo_engine_t e, bool head, int T, int max_chunks) {
     for (int l = 0; l < e->L; ++l)
         if ((rc = enqueue_layer(e, l, T, max_chunks))) return rc;
     return head ? enqueue_head(e) : TENZO_SUCCESS;
+}
+
+// Tokens per batched-prefill pass: longer prompts go through in passes of
+// this many rows (every activation buffer holds that many rows).
+constexpr int kPrefillRows = 512;
+
+int prefill_buffers(tenzo_engine_t e) {
+    if (e->pf_cap) return TENZO_SUCCESS;
+    const size_t R = kPrefillRows;
+    const int64_t Kp = std::max(ceil_div(e->F, 64), ceil_div(e->H, 64)) * 64;
+    int rc;
+    if ((rc = alloc_t(e, &e->pf_x, R * e->H * 4)) || (rc = alloc_t(e, &e->pf_h1, R * e->H * 4)) ||
+        (rc = alloc_t(e, &e->pf_qkv, R * (e->qd + 2 * e->kvd) * 4)) ||
+        (rc = alloc_t(e, &e->pf_attn, R * e->qd * 4)) ||
+        (rc = alloc_t(e, &e->pf_gu, R * 2 * e->F * 4)) ||
+        (rc = alloc_t(e, &e->pf_codes, R * Kp, true)) ||
+        (rc = alloc_t(e, &e->pf_aq, R * sizeof(tenzo_hip_actq_t))) ||
+        (rc = alloc_t(e, &e->pf_tok, R * 4)))
+        return rc;
+    e->pf_cap = kPrefillRows;
+    return TENZO_SUCCESS;
+}
+
+// One layer for the m prompt tokens at positions pos0 .. pos0+m-1 (the m
+// forward_layer_raw calls of m prefill_token steps, TenzoEngine.cpp:1522-1632
+// and :1809-1819): the same stages as enqueue_layer with M = m rows, the TL1
+// contractions on int8 MFMA and the attention of every token over its own
+// prefix.
+int enqueue_prefill_layer(tenzo_engine_t e, int l, int pos0, int m, bool exact) {
+    const DevLayer& w = e->layers[l];
+    hipStream_t st = e->st;
+    const int64_t KpH = ceil_div(e->H, 64) * 64;
+    const int64_t nqkv = e->qd + 2 * e->kvd;
+    int rc;
+    if ((rc = launch_actquant(1, 31, e->pf_x, w.norm[0], e->eps, m, e->H, KpH, e->pf_codes,
+                              e->pf_aq, nullptr, st)))
+        return rc;
+    RowScales rs{};
+    rs.n = 3;
+    rs.end[0] = e->qd;
+    rs.end[1] = e->qd + e->kvd;
+    rs.end[2] = INT64_MAX;
+    rs.scale[0] = w.sc[0];
+    rs.scale[1] = w.sc[1];
+    rs.scale[2] = w.sc[2];
+    if ((rc = launch_tl1_mfma(e->pf_codes, e->pf_aq, w.qkv, rs, m, nqkv, e->H, e->pf_qkv,
+                              nullptr, nullptr, st, 0)))
+        return rc;
+    AttnPrefill a{};
+    a.q = e->pf_qkv;
+    a.k_new = e->pf_qkv + e->qd;
+    a.v_new = e->pf_qkv + e->qd + e->kvd;
+    a.row_stride = nqkv;
+    const size_t head_off = (size_t)l * e->Hkv * e->max_seq;
+    a.kc = e->kc + head_off * kD;
+    a.vc = e->vc + head_off * kD;
+    a.ks = e->ks + head_off;
+    a.vs = e->vs + head_off;
+    a.rope = e->rope;
+    a.pos0 = pos0;
+    a.n = m;
+    a.Hq = e->Hq;
+    a.Hkv = e->Hkv;
+    a.max_seq = e->max_seq;
+    a.out = e->pf_attn;
+    a.out_stride = e->qd;
+    a.exact = exact ? 1 : 0;
+    if ((rc = launch_attn_prefill(a, st))) return rc;
+    if ((rc = launch_actquant(1, 31, e->pf_attn, w.norm[1], e->eps, m, e->H, KpH, e->pf_codes,
+                              e->pf_aq, nullptr, st)))
+        return rc;
+    if ((rc = launch_tl1_mfma(e->pf_codes, e->pf_aq, w.o, RowScales::single(w.sc[3]), m, e->H,
+                              e->H, e->pf_h1, e->pf_x, nullptr, st, 0)))
+        return rc;
+    if (!w.mlp) {  // :1629-1631
+        const int64_t n = (int64_t)m * e->H;
+        hipLaunchKernelGGL(copy_kernel, dim3((unsigned)ceil_div(n, 256)), dim3(256), 0, st,
+                           e->pf_h1, e->pf_x, n);
+        return launch_status("copy_kernel");
+    }
+    if ((rc = launch_actquant(1, 31, e->pf_h1, w.norm[2], e->eps, m, e->H, KpH, e->pf_codes,
+                              e->pf_aq, nullptr, st)))
+        return rc;
+    RowScales gs{};
+    gs.n = 2;
+    gs.end[0] = e->F;
+    gs.end[1] = INT64_MAX;
+    gs.scale[0] = w.sc[4];
+    gs.scale[1] = w.sc[5];
+    if ((rc = launch_tl1_mfma(e->pf_codes, e->pf_aq, w.gu, gs, m, 2 * e->F, e->H, e->pf_gu,
+                              nullptr, nullptr, st, 0)))
+        return rc;
+    const int64_t KpF = ceil_div(e->F, 64) * 64;
+    if ((rc = launch_actquant(3, 31, e->pf_gu, w.norm[3], e->eps, m, e->F, KpF, e->pf_codes,
+                              e->pf_aq, nullptr, st)))
+        return rc;
+    return launch_tl1_mfma(e->pf_codes, e->pf_aq, w.down, RowScales::single(w.sc[6]), m, e->H,
+                           e->F, e->pf_x, e->pf_h1, nullptr, st, 0);
+}
+
+// n prompt tokens from position seq_len on, in passes of kPrefillRows; the
+// engine's x ends as the last token's hidden state, as after n prefill_token
+// calls (bit for bit when exact, else up to the streaming attention's
+// softmax rounding).
+int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
+    if (!ready(e, false)) return TENZO_ERROR_INVALID_ARGUMENT;
+    if (n <= 0 || !tokens) {
+        set_error("prefill: need n > 0 tokens (n=%d)", n);
+        return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    for (int i = 0; i < n; ++i)
+        if (tokens[i] < 0 || tokens[i] >= e->V) {
+            set_error("token %d outside [0, %d)", tokens[i], e->V);
+            return TENZO_ERROR_INVALID_ARGUMENT;
+        }
+    if ((int64_t)e->seq_len + n > e->max_seq) {
+        set_error("KV cache full (%d + %d positions > %d)", e->seq_len, n, e->max_seq);
+        return TENZO_ERROR_OUT_OF_MEMORY;
+    }
+    TZ_HIP(hipSetDevice(e->dev));
+    int rc;
+    if ((rc = prefill_buffers(e))) return rc;
+    int m = 0;
+    for (int i0 = 0; i0 < n; i0 += m) {
+        m = std::min(e->pf_cap, n - i0);
+        TZ_HIP(hipMemcpyAsync(e->pf_tok, tokens + i0, (size_t)m * 4, hipMemcpyHostToDevice, e->st));
+        rc = e->head_kind == 1 ? launch_embed_i8(e->head_i8, e->head_scales, e->pf_tok, e->V, e->H,
+                                                 e->pf_x, e->st, m)
+                               : launch_embed_f32(e->head_f32, e->pf_tok, e->V, e->H, e->pf_x,
+                                                  e->st, m);
+        if (rc) return rc;
+        for (int l = 0; l < e->L; ++l)
+            if ((rc = enqueue_prefill_layer(e, l, e->seq_len, m, exact))) return rc;
+        // the copy of the tokens and the next pass's buffers are reused
+        TZ_HIP(hipStreamSynchronize(e->st));
+        e->seq_len += m;
+    }
+    TZ_HIP(hipMemcpyAsync(e->x, e->pf_x + (int64_t)(m - 1) * e->H, (size_t)e->H * 4,
+                          hipMemcpyDeviceToDevice, e->st));
+    TZ_HIP(hipStreamSynchronize(e->st));
+    return TENZO_SUCCESS;
 }
 
 // Whether the persistent kernel can run this model as loaded.
@@ -704,6 +857,12 @@ TENZO_API tenzo_status_t tenzo_prefill_token(tenzo_engine_t e, int token) {
     if ((rc = ds_check(e))) return (tenzo_status_t)rc;
     e->seq_len += 1;  // :1816-1818
     return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_prefill(tenzo_engine_t e, const int32_t* tokens, int n,
+                                           int exact) {
+    if (!e) return TENZO_ERROR_INVALID_ARGUMENT;
+    return run_prefill(e, tokens, n, exact != 0);
 }
 
 TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,

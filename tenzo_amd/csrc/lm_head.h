@@ -33,12 +33,12 @@ int launch_lm_head_f32(const float* xn, const float* E, float* logits, int64_t V
                        hipStream_t st);
 int launch_argmax(const float* logits, int64_t V, const ArgmaxWs& am, hipStream_t st);
 // x = float(E[token]) * scales[token] from the packed int8 table; tokens
-// outside [0, V) give x = 0.
+// outside [0, V) give x = 0. n tokens (token_dev[0..n)) fill n rows of x.
 int launch_embed_i8(const void* w_packed, const float* scales, const int32_t* token_dev,
-                    int64_t V, int64_t H, float* x, hipStream_t st);
+                    int64_t V, int64_t H, float* x, hipStream_t st, int n = 1);
 // x = E[token] from a row-major fp32 table.
 int launch_embed_f32(const float* E, const int32_t* token_dev, int64_t V, int64_t H, float* x,
-                     hipStream_t st);
+                     hipStream_t st, int n = 1);
 // Repetition penalty of sample_top_k_top_p (TenzoEngine.cpp:1735-1743), in
 // place and in the order given (a token listed twice is penalised twice).
 int launch_rep_penalty(float* logits, int64_t V, const int32_t* tokens, int n, float penalty,

@@ -219,7 +219,8 @@ __global__ void embed_i8_kernel(const uint8_t* __restrict__ w, const float* __re
                                 float* __restrict__ x) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= H) return;
-    const int tok = *token_dev;
+    const int tok = token_dev[blockIdx.y];  // row blockIdx.y of x
+    x += (int64_t)blockIdx.y * H;
     if (tok < 0 || (int64_t)tok >= V) {
         x[i] = 0.0f;
         return;
@@ -233,7 +234,8 @@ __global__ void embed_f32_kernel(const float* __restrict__ E, const int32_t* __r
                                  int64_t V, int64_t H, float* __restrict__ x) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= H) return;
-    const int tok = *token_dev;
+    const int tok = token_dev[blockIdx.y];
+    x += (int64_t)blockIdx.y * H;
     x[i] = (tok < 0 || (int64_t)tok >= V) ? 0.0f : E[(int64_t)tok * H + i];
 }
 
@@ -304,16 +306,16 @@ int launch_argmax(const float* logits, int64_t V, const ArgmaxWs& am, hipStream_
 }
 
 int launch_embed_i8(const void* w_packed, const float* scales, const int32_t* token_dev,
-                    int64_t V, int64_t H, float* x, hipStream_t st) {
-    hipLaunchKernelGGL(embed_i8_kernel, dim3((unsigned)ceil_div(H, 256)), dim3(256), 0, st,
-                       (const uint8_t*)w_packed, scales, token_dev, V, H, x);
+                    int64_t V, int64_t H, float* x, hipStream_t st, int n) {
+    hipLaunchKernelGGL(embed_i8_kernel, dim3((unsigned)ceil_div(H, 256), (unsigned)n), dim3(256),
+                       0, st, (const uint8_t*)w_packed, scales, token_dev, V, H, x);
     return launch_status("embed_i8_kernel");
 }
 
 int launch_embed_f32(const float* E, const int32_t* token_dev, int64_t V, int64_t H, float* x,
-                     hipStream_t st) {
-    hipLaunchKernelGGL(embed_f32_kernel, dim3((unsigned)ceil_div(H, 256)), dim3(256), 0, st, E,
-                       token_dev, V, H, x);
+                     hipStream_t st, int n) {
+    hipLaunchKernelGGL(embed_f32_kernel, dim3((unsigned)ceil_div(H, 256), (unsigned)n), dim3(256),
+                       0, st, E, token_dev, V, H, x);
     return launch_status("embed_f32_kernel");
 }
 

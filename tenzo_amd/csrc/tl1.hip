@@ -137,6 +137,104 @@ actquant_kernel(const float* __restrict__ x, const float* __restrict__ w, float 
     }
 }
 
+// The same quantization with the row held in registers: thread t loads its
+// float4 groups t + 256 j (j < J) once, which is also the order of the
+// sum of squares above (p[k] accumulates element 4t + 1024 j + k over j), so
+// every result equals actquant_kernel's; the row is read from memory once
+// instead of three times. K % 4 == 0 and K <= 1024 J.
+template <int MODE, int QMAX, int J>
+__global__ void __launch_bounds__(256)
+actquant_reg_kernel(const float* __restrict__ x, const float* __restrict__ w, float eps,
+                    int64_t K, int64_t Kp, int8_t* __restrict__ codes,
+                    tenzo_hip_actq_t* __restrict__ q, float* __restrict__ y_out) {
+    __shared__ float redf[4];
+    __shared__ int redi[4];
+    const int t = threadIdx.x;
+    const int64_t m = blockIdx.x;
+    const float* xm = x + m * (MODE == 3 ? 2 * K : K);
+    float4 v[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int64_t i = 4 * t + 1024 * j;
+        v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (i < K) {
+            const float4 a = *reinterpret_cast<const float4*>(xm + i);
+            if (MODE == 3) {
+                const float4 u = *reinterpret_cast<const float4*>(xm + K + i);
+                const float r0 = fmaxf(0.0f, a.x), r1 = fmaxf(0.0f, a.y), r2 = fmaxf(0.0f, a.z),
+                            r3 = fmaxf(0.0f, a.w);
+                v[j] = make_float4(__fmul_rn(__fmul_rn(r0, r0), u.x), __fmul_rn(__fmul_rn(r1, r1), u.y),
+                                   __fmul_rn(__fmul_rn(r2, r2), u.z), __fmul_rn(__fmul_rn(r3, r3), u.w));
+            } else {
+                v[j] = a;
+            }
+        }
+    }
+    if (MODE >= 1) {
+        float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            if (4 * t + 1024 * j < K) {
+                p0 = __builtin_fmaf(v[j].x, v[j].x, p0);
+                p1 = __builtin_fmaf(v[j].y, v[j].y, p1);
+                p2 = __builtin_fmaf(v[j].z, v[j].z, p2);
+                p3 = __builtin_fmaf(v[j].w, v[j].w, p3);
+            }
+        }
+        float ss = (p0 + p1) + (p2 + p3);
+        ss = wave_sum_tree(ss);
+        if ((t & 63) == 0) redf[t >> 6] = ss;
+        __syncthreads();
+        ss = (redf[0] + redf[1]) + (redf[2] + redf[3]);
+        __syncthreads();
+        const float inv_rms = inv_rms_from_sumsq(ss, K, eps);
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int64_t i = 4 * t + 1024 * j;
+            if (i < K) {
+                v[j].x = norm_apply(v[j].x, inv_rms, w, i);
+                v[j].y = norm_apply(v[j].y, inv_rms, w, i + 1);
+                v[j].z = norm_apply(v[j].z, inv_rms, w, i + 2);
+                v[j].w = norm_apply(v[j].w, inv_rms, w, i + 3);
+                if (y_out) *reinterpret_cast<float4*>(y_out + m * K + i) = v[j];
+            }
+        }
+        if (MODE == 2) return;
+    }
+    float amax = QMAX == 31 ? 1e-6f : 1e-8f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
+                                 fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+    amax = block256_max(amax, redf);
+    const float scale_act = __fdiv_rn((float)QMAX, amax);
+    int csum = 0;
+    int8_t* cm = codes + m * Kp;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int64_t i = 4 * t + 1024 * j;
+        if (i >= Kp) continue;
+        int c[4] = {0, 0, 0, 0};
+        if (i < K) {
+            const float e[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                float r = roundf(__fmul_rn(e[k], scale_act));
+                if (QMAX == 127) r = fminf(fmaxf(r, -128.0f), 127.0f);
+                c[k] = (int)r;
+            }
+        }
+        csum += (c[0] + c[1]) + (c[2] + c[3]);
+        *reinterpret_cast<uint32_t*>(cm + i) = (uint32_t)(c[0] & 0xff) | ((uint32_t)(c[1] & 0xff) << 8) |
+                                              ((uint32_t)(c[2] & 0xff) << 16) | ((uint32_t)(c[3] & 0xff) << 24);
+    }
+    csum = block256_sum_i32(csum, redi);
+    if (t == 0) {
+        q[m].inv_scale = __fmul_rn(amax, 1.0f / (float)QMAX);
+        q[m].code_sum = csum;
+    }
+}
+
 // ------------------------------------------------------------------------
 // GEMV. Grid (row_blocks * splits, M); 256 threads = 4 waves. A block owns
 // one row block (lane = row) and a contiguous range of super-chunks, which
@@ -259,6 +357,19 @@ int launch_actquant(int mode, int qmax, const float* x, const float* norm_w, flo
                     int64_t M, int64_t K, int64_t Kp, int8_t* codes, tenzo_hip_actq_t* q,
                     float* y_out, hipStream_t st) {
     const dim3 grid((unsigned)M), blk(256);
+    if (K % 4 == 0 && K <= 16384) {
+        const int J = (int)ceil_div(K, 1024);
+#define AQR_CASE(MO, QM, JJ)                                                                  \
+    if (mode == MO && qmax == QM && J <= JJ) {                                                \
+        hipLaunchKernelGGL((actquant_reg_kernel<MO, QM, JJ>), grid, blk, 0, st, x, norm_w, eps, K, \
+                           Kp, codes, q, y_out);                                              \
+        return launch_status("actquant_reg_kernel");                                          \
+    }
+#define AQR_MODE(MO, QM) AQR_CASE(MO, QM, 2) AQR_CASE(MO, QM, 4) AQR_CASE(MO, QM, 8) AQR_CASE(MO, QM, 16)
+        AQR_MODE(0, 31) AQR_MODE(1, 31) AQR_MODE(3, 31) AQR_MODE(0, 127) AQR_MODE(1, 127)
+#undef AQR_MODE
+#undef AQR_CASE
+    }
 #define AQ_CASE(MO, QM)                                                                  \
     if (mode == MO && qmax == QM) {                                                      \
         hipLaunchKernelGGL((actquant_kernel<MO, QM>), grid, blk, 0, st, x, norm_w, eps, K, Kp, \

@@ -196,6 +196,13 @@ class Engine:
     def prefill(self, token: int):
         self._check(self.L.tenzo_prefill_token(self.h, int(token)), "tenzo_prefill_token")
 
+    def prefill_batch(self, tokens, exact: bool = False):
+        """All prompt tokens at once (tenzo_hip_engine_prefill): the state of
+        one prefill() per token (bit for bit when exact)."""
+        arr = np.ascontiguousarray(tokens, np.int32)
+        self._check(self.L.tenzo_hip_engine_prefill(self.h, _ptr(arr), int(arr.size),
+                                                    int(bool(exact))), "engine_prefill")
+
     def step(self, token: int, temperature: float = 0.0, penalty: float = 1.0,
              past=None, top_k: int = 40, top_p: float = 0.9) -> int:
         p = SamplingParams(temperature, top_p, top_k, penalty)

@@ -1,7 +1,9 @@
-"""Multi-token TL1 contraction on int8 MFMA (prefill) against the per-token
-GEMV and the CPU oracle: the int32 accumulators are exact, so the batched
-results equal the sequential per-token ones bit for bit (fp32 outputs are one
-multiply of them)."""
+"""Multi-token prefill: the TL1 contraction on int8 MFMA against the
+per-token GEMV and the CPU oracle (the int32 accumulators are exact, so the
+batched results equal the sequential per-token ones bit for bit: fp32 outputs
+are one multiply of them), and the engine's batched prefill against one
+prefill_token call per token (KV cache, hidden state and the following
+decode steps bit for bit: every stage runs the same arithmetic)."""
 import numpy as np
 import pytest
 
@@ -107,3 +109,126 @@ def test_batch_zero_and_extreme_codes(torch_dev):
         yo, acco, _ = oracle.tl1_gemv(x[m], w, N, 0.25)
         np.testing.assert_array_equal(ab[m].cpu().numpy(), acco)
         np.testing.assert_array_equal(yb[m].cpu().numpy(), yo)
+
+
+def _engine_pair(eng_mod, cfg, sm):
+    a, b = eng_mod.Engine(cfg), eng_mod.Engine(cfg)
+    for e in (a, b):
+        e.set_model(sm)
+        e.set_mode("eager")
+    return a, b
+
+
+@pytest.mark.parametrize("ctx,n", [(0, 1), (0, 5), (0, 40), (5, 23), (17, 30)])
+def test_engine_prefill_equals_token_by_token(torch_dev, ctx, n):
+    """exact=True: one pass of the batched pipeline equals n prefill_token
+    calls of the per-stage (eager) path bit for bit."""
+    from tenzo_amd import engine as eng_mod, synth
+    cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=3, ffn=1024,
+                             vocab=2048, max_seq=64, theta=10000.0)
+    sm = synth.make_model(cfg, seed=61 + n, ctx=ctx)
+    rng = np.random.default_rng(n)
+    toks = rng.integers(0, cfg.vocab, n).astype(np.int32)
+    print(f"engine prefill ctx={ctx} n={n}", flush=True)
+    a, b = _engine_pair(eng_mod, cfg, sm)
+    with a, b:
+        for t in toks:
+            a.prefill(int(t))
+        b.prefill_batch(toks, exact=True)
+        assert a.seq_len == b.seq_len == ctx + n
+        for x, y in zip(a.get_kv(ctx + n), b.get_kv(ctx + n)):
+            np.testing.assert_array_equal(x, y)
+        np.testing.assert_array_equal(a.buffer("x"), b.buffer("x"))
+        for t in (7, 11, 13):
+            assert a.step(t) == b.step(t)
+            np.testing.assert_array_equal(a.logits(), b.logits())
+
+
+def test_engine_prefill_longer_than_one_pass(torch_dev):
+    """600 tokens: two passes of the 512-row buffers, attention over up to 19
+    chunks per query, G = 4 query heads per kv head."""
+    from tenzo_amd import engine as eng_mod, synth
+    cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=2, ffn=512,
+                             vocab=1024, max_seq=640, theta=10000.0)
+    sm = synth.make_model(cfg, seed=71, ctx=0)
+    toks = np.random.default_rng(3).integers(0, cfg.vocab, 600).astype(np.int32)
+    a, b = _engine_pair(eng_mod, cfg, sm)
+    with a, b:
+        for t in toks:
+            a.prefill(int(t))
+        b.prefill_batch(toks, exact=True)
+        for x, y in zip(a.get_kv(600), b.get_kv(600)):
+            np.testing.assert_array_equal(x, y)
+        np.testing.assert_array_equal(a.buffer("x"), b.buffer("x"))
+        assert a.step(5) == b.step(5)
+        np.testing.assert_array_equal(a.logits(), b.logits())
+
+
+def test_engine_prefill_then_persistent_decode(torch_dev):
+    """A batched prefill followed by persistent-kernel decode steps gives the
+    tokens of token-by-token prefill + decode (fp32 logits to 1e-5: the
+    persistent kernel sums attention in its own order)."""
+    from tenzo_amd import engine as eng_mod, synth
+    cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=3, ffn=1024,
+                             vocab=2048, max_seq=64, theta=10000.0)
+    sm = synth.make_model(cfg, seed=83, ctx=0)
+    toks = np.arange(1, 20, dtype=np.int32) * 37 % cfg.vocab
+    with eng_mod.Engine(cfg) as a, eng_mod.Engine(cfg) as b:
+        a.set_model(sm)
+        b.set_model(sm)
+        for t in toks:
+            a.prefill(int(t))
+        b.prefill_batch(toks, exact=True)
+        ta, tb = a.decode(3, 6)[0], b.decode(3, 6)[0]
+        assert list(ta) == list(tb)
+        la, lb = a.logits(), b.logits()
+        assert np.abs(la - lb).max() <= 1e-5 * max(np.abs(la).max(), 1e-30)
+
+
+def test_engine_prefill_errors(torch_dev):
+    from tenzo_amd import engine as eng_mod, synth
+    cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=1, ffn=512,
+                             vocab=256, max_seq=16, theta=10000.0)
+    sm = synth.make_model(cfg, seed=5, ctx=0)
+    with eng_mod.Engine(cfg) as e:
+        e.set_model(sm)
+        with pytest.raises(RuntimeError, match="outside"):
+            e.prefill_batch(np.array([1, 256], np.int32))
+        with pytest.raises(RuntimeError, match="full"):
+            e.prefill_batch(np.zeros(17, np.int32))
+        assert e.seq_len == 0
+        e.prefill_batch(np.zeros(16, np.int32))
+        assert e.seq_len == 16
+
+
+@pytest.mark.parametrize("ctx,n,G", [(0, 40, 4), (17, 47, 4), (0, 600, 4), (3, 130, 1),
+                                     (0, 70, 2)])
+def test_engine_prefill_streaming_attention(torch_dev, ctx, n, G):
+    """The default (streaming attention) prefill against the exact one: the
+    attention differs only in how the softmax sums are grouped, so the hidden
+    state and the logits of the next step agree to 1e-4 and almost every KV
+    code is identical (a code can flip where a value sits on a rounding
+    boundary)."""
+    from tenzo_amd import engine as eng_mod, synth
+    cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=4 // G, n_layers=2, ffn=512,
+                             vocab=1024, max_seq=ctx + n + 8, theta=10000.0)
+    sm = synth.make_model(cfg, seed=97 + n, ctx=ctx)
+    toks = np.random.default_rng(n).integers(0, cfg.vocab, n).astype(np.int32)
+    print(f"streaming prefill ctx={ctx} n={n} G={G}", flush=True)
+    a, b = _engine_pair(eng_mod, cfg, sm)
+    with a, b:
+        a.prefill_batch(toks, exact=True)
+        b.prefill_batch(toks)
+        xa, xb = a.buffer("x"), b.buffer("x")
+        assert rel(xb, xa) < 1e-4
+        for u, v in zip(a.get_kv(ctx + n), b.get_kv(ctx + n)):
+            u, v = np.asarray(u, np.float64), np.asarray(v, np.float64)
+            assert (u != v).mean() < 0.01
+        ta, tb = a.step(5), b.step(5)
+        la, lb = a.logits(), b.logits()
+        assert rel(lb, la) < 1e-4
+        assert ta == tb
+
+
+def rel(a, b):
+    return np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30)
