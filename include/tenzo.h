@@ -18,8 +18,10 @@
  *     the reference's undefined behaviour;
  *   - tenzo_create_engine returns NULL when no GPU is usable or the config is
  *     unsupported (the reference never returns NULL);
- *   - sampling with temperature > 0 is not provided yet: generate_step returns
- *     -1 for it (greedy, temperature <= 0, is the supported mode).
+ *   - sampling with temperature > 0 runs on the device with the reference's
+ *     algorithm and draw (rand()/RAND_MAX from the process's libc); among
+ *     logits equal to the k-th largest the lowest indices are kept, where the
+ *     reference's heap keeps an insertion-order-dependent subset.
  */
 #ifndef TENZO_H
 #define TENZO_H

@@ -181,6 +181,16 @@ TENZO_HIP_API int tenzo_hip_lm_head_i8_codes(const int8_t* codes, const tenzo_hi
  * the first maximum, written to *out_idx (device int32). */
 TENZO_HIP_API int tenzo_hip_argmax(const float* logits, int64_t V, int32_t* out_idx,
                                    void* stream);
+/* Sampling branch of sample_top_k_top_p (TenzoEngine.cpp:1757-1806),
+ * temperature > 0, on logits that already carry the repetition penalty: top_k
+ * clamped to [1, 64], softmax at the temperature over the top-k, top-p
+ * cutoff, and the draw r in [0, 1] (the reference draws rand()/RAND_MAX; the
+ * engine passes that same value). The token goes to *out_token (device
+ * int32). Among logits equal to the k-th largest, the lowest indices are
+ * kept. V <= 262144. */
+TENZO_HIP_API int tenzo_hip_sample_top_k_top_p(const float* logits, int64_t V, int top_k,
+                                               float top_p, float temperature, float r,
+                                               int32_t* out_token, void* stream);
 /* embedding_lookup, int8 branch (TenzoEngine.cpp:1294-1316), reading the
  * table in the LM-head device layout: x = float(E[token]) * scales[token].
  * token is read from device memory (token_dev). */

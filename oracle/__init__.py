@@ -74,6 +74,7 @@ def lib() -> ctypes.CDLL:
             "orc_attention_step": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
             "orc_lm_head": (_F, [_P, _P, _P, _I64, _I64, _P, _P]),
             "orc_argmax": (_I, [_P, _I64]),
+            "orc_sample_top_k_top_p": (_I, [_P, _I64, _I, _F, _F, _F]),
             "orc_embed_i8": (None, [_P, _P, _I64, _I, _P]),
             "orc_q4_0": (None, [_P, _P, _P, _I, _I]),
             "orc_q8_0": (None, [_P, _P, _P, _I, _I]),
@@ -121,6 +122,7 @@ def ref() -> ctypes.CDLL:
             "ref_engine_get_kv": (None, [_P, _P, _P, _P, _P]),
             "ref_engine_seq_len": (_I, [_P]),
             "ref_engine_step": (_I, [_P, _I, _P]),
+            "ref_engine_sample": (_I, [_P, _P, _F, _F, _I, _F, _P, _I]),
             "ref_engine_prefill": (_I, [_P, _I]),
             "ref_engine_hidden": (None, [_P, _P]),
             "ref_num_threads": (_I, []),
@@ -273,6 +275,12 @@ def lm_head(xn, W, scales):
 def argmax(logits) -> int:
     logits = f32(logits)
     return int(lib().orc_argmax(_ptr(logits), logits.size))
+
+
+def sample_top_k_top_p(logits, top_k: int, top_p: float, temperature: float, r: float) -> int:
+    logits = f32(logits)
+    return int(lib().orc_sample_top_k_top_p(_ptr(logits), logits.size, int(top_k), float(top_p),
+                                            float(temperature), float(r)))
 
 
 def q4_0(a, w, K, N):

@@ -207,6 +207,21 @@ int ref_engine_buf(void* e, int which, float* out) {
     return static_cast<int>(b.size());
 }
 
+// sample_top_k_top_p (TenzoEngine.cpp:1722-1807) of the engine on the given
+// logits (copied into its logits scratch): the reference's own sampler,
+// drawing from the process's rand().
+int ref_engine_sample(void* e, const float* logits, float temperature, float top_p, int top_k,
+                      float penalty, const int* past, int past_len) {
+    auto* impl = static_cast<tenzo_engine_t>(e)->impl.get();
+    std::memcpy(impl->logits_scratch.data(), logits, impl->logits_scratch.size() * 4);
+    tenzo_sampling_params_t p = tenzo_default_sampling_params();
+    p.temperature = temperature;
+    p.top_p = top_p;
+    p.top_k = top_k;
+    p.repetition_penalty = penalty;
+    return impl->sample_top_k_top_p(&p, past, past_len);
+}
+
 int ref_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

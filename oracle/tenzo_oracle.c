@@ -387,6 +387,72 @@ int orc_argmax(const float* logits, int64_t V) {
     return (int)best;
 }
 
+/* sample_top_k_top_p (:1722-1807) for temperature > 0 after the penalty, with
+ * the uniform draw r passed in (the reference draws rand()/RAND_MAX there).
+ * Top-k by the reference's min-heap rule: the first k logits enter; a later
+ * logit replaces the heap's least (value, index) pair only when its value is
+ * strictly greater. Candidates then run in descending (value, index) order. */
+static int orc_pair_less(float a, int ia, float b, int ib) {
+    return a < b || (a == b && ia < ib);
+}
+
+int orc_sample_top_k_top_p(const float* logits, int64_t V, int top_k, float top_p,
+                           float temperature, float r) {
+    int k = top_k < 1 ? 1 : (top_k > 64 ? 64 : top_k);
+    float hv[64];
+    int hi[64];
+    int n = 0;
+    for (int64_t i = 0; i < V; ++i) {                          /* :1759-1767 */
+        const float l = logits[i];
+        if (n < k) {
+            hv[n] = l;
+            hi[n] = (int)i;
+            ++n;
+            continue;
+        }
+        int m = 0;                                             /* heap top: least pair */
+        for (int j = 1; j < n; ++j)
+            if (orc_pair_less(hv[j], hi[j], hv[m], hi[m])) m = j;
+        if (l > hv[m]) {
+            hv[m] = l;
+            hi[m] = (int)i;
+        }
+    }
+    /* descending (value, index): the heap popped least-first into candidates[n-1..0] */
+    for (int a = 0; a < n; ++a)
+        for (int b = a + 1; b < n; ++b)
+            if (orc_pair_less(hv[a], hi[a], hv[b], hi[b])) {
+                float tv = hv[a]; hv[a] = hv[b]; hv[b] = tv;
+                int ti = hi[a]; hi[a] = hi[b]; hi[b] = ti;
+            }
+    float probs[64];
+    const float max_l = hv[0];
+    float sum_exp = 0.0f;
+    for (int i = 0; i < n; ++i) {                              /* :1776-1782 */
+        probs[i] = expf((hv[i] - max_l) / temperature);
+        sum_exp += probs[i];
+    }
+    for (int i = 0; i < n; ++i) probs[i] /= sum_exp;
+    float cum_p = 0.0f;
+    int cutoff = n;
+    for (int i = 0; i < n; ++i) {                              /* :1784-1792 */
+        cum_p += probs[i];
+        if (cum_p >= top_p) {
+            cutoff = i + 1;
+            break;
+        }
+    }
+    float sub_sum = 0.0f;
+    for (int i = 0; i < cutoff; ++i) sub_sum += probs[i];
+    for (int i = 0; i < cutoff; ++i) probs[i] /= sub_sum;
+    float acc = 0.0f;
+    for (int i = 0; i < cutoff; ++i) {                         /* :1798-1804 */
+        acc += probs[i];
+        if (r <= acc) return hi[i];
+    }
+    return hi[0];
+}
+
 void orc_embed_i8(const int8_t* E, const float* scales, int64_t H, int token, float* x) {
     const int8_t* row = E + (int64_t)token * H;
     float s = scales[token];

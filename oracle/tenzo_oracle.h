@@ -40,6 +40,10 @@
  *   orc_decode_step                  compiled reference whole-engine step on small
  *                                    configs (logits 1e-3, greedy token equal)
  *   orc_argmax                       brute force (first maximum)
+ *   orc_sample_top_k_top_p           the compiled reference's own sampler on the
+ *                                    same logits and the same rand() draw (token
+ *                                    equal) + special cases (top_k 1 = argmax,
+ *                                    tiny temperature = argmax, top_p 1 keeps k)
  */
 #ifndef TENZO_ORACLE_H
 #define TENZO_ORACLE_H
@@ -112,6 +116,9 @@ void orc_attention_step(float* q, float* k, const float* v, int8_t* kc, int8_t* 
 float orc_lm_head(const float* xn, const int8_t* W, const float* scales, int64_t V,
                   int64_t H, float* logits, int8_t* codes);
 int orc_argmax(const float* logits, int64_t V);
+/* sample_top_k_top_p (:1722-1807), temperature > 0, with the draw r in [0, 1]. */
+int orc_sample_top_k_top_p(const float* logits, int64_t V, int top_k, float top_p,
+                           float temperature, float r);
 /* embedding_lookup int8 branch (:1294-1316). */
 void orc_embed_i8(const int8_t* E, const float* scales, int64_t H, int token, float* x);
 

@@ -40,6 +40,7 @@ SIGNATURES = {
     "tenzo_hip_i8_rows_repack": (_I, [_P, _P, _I64, _I64, _P]),
     "tenzo_hip_lm_head_i8": (_I, [_P, _P, _F, _P, _P, _P, _I64, _I64, _P]),
     "tenzo_hip_argmax": (_I, [_P, _I64, _P, _P]),
+    "tenzo_hip_sample_top_k_top_p": (_I, [_P, _I64, _I, _F, _F, _F, _P, _P]),
     "tenzo_hip_rmsnorm_quant127": (_I, [_P, _P, _I, _F, _I64, _I64, _P, _P, _P]),
     "tenzo_hip_lm_head_i8_codes": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     "tenzo_hip_embed_i8": (_I, [_P, _P, _P, _I64, _I64, _P, _P]),

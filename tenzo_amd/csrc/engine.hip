@@ -24,6 +24,7 @@
 // (position and token read from device memory, one graph per attention chunk
 // size) or launched eagerly, remain selectable (tenzo_hip_engine_set_mode).
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -88,6 +89,7 @@ struct tenzo_engine_opaque {
     void* gemv_ws = nullptr;
     float* attn_part = nullptr;
     void* am_ws = nullptr;
+    void* sample_ws = nullptr;   // top-k candidates of the sampler
     int32_t* io_dev = nullptr;   // [0] token, [1] position, [2] result token
     int32_t* io_host = nullptr;  // pinned mirror
     int32_t* pen_dev = nullptr;  // past tokens for the repetition penalty
@@ -689,6 +691,7 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
          !alloc_t(e, &e->aq, 256) && !alloc_t(e, &e->gemv_ws, ws, true) &&
          !alloc_t(e, &e->attn_part, parts) &&
          !alloc_t(e, &e->am_ws, argmax_ws_bytes(e->V), true) &&
+         !alloc_t(e, &e->sample_ws, sample_ws_bytes(e->V)) &&
          !alloc_t(e, &e->io_dev, 256, true) &&
          !alloc_t(e, &e->rope, (size_t)e->max_seq * kD * 4);
     if (ok) {
@@ -869,10 +872,13 @@ TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,
                                   const tenzo_sampling_params_t* params, const int* past,
                                   int past_len) {
     if (!e) return -1;
+    // sample_top_k_top_p's defaults (:1728-1731)
     const float temperature = params ? params->temperature : 0.7f;
+    const float top_p = params ? params->top_p : 0.9f;
+    const int top_k = params ? params->top_k : 40;
     const float penalty = params ? params->repetition_penalty : 1.15f;
-    if (temperature > 0.0f) {
-        set_error("generate_step: sampling with temperature > 0 is not provided (greedy only)");
+    if (temperature > 0.0f && e->V > 262144) {
+        set_error("generate_step: sampling supports vocabularies up to 262144");
         return -1;
     }
     if (run_step(e, cur_token, true)) return -1;
@@ -896,7 +902,14 @@ TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,
         if (hipMemcpyAsync(e->pen_dev, past, (size_t)past_len * 4, hipMemcpyHostToDevice, st) !=
                 hipSuccess ||
             launch_rep_penalty(e->logits, e->V, e->pen_dev, past_len, penalty, st) ||
-            launch_argmax(e->logits, e->V, am, st))
+            (temperature <= 0.0f && launch_argmax(e->logits, e->V, am, st)))
+            return -1;
+    }
+    if (temperature > 0.0f) {
+        // the draw of :1797, from the process's rand() as in the reference
+        const float r = static_cast<float>(rand()) / static_cast<float>(RAND_MAX);
+        if (launch_sample(e->logits, e->V, top_k, top_p, temperature, r, e->sample_ws,
+                          e->io_dev + 2, e->st))
             return -1;
     }
     if (hipMemcpyAsync(e->io_host + 2, e->io_dev + 2, 4, hipMemcpyDeviceToHost, e->st) !=

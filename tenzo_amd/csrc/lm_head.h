@@ -41,6 +41,13 @@ int launch_embed_f32(const float* E, const int32_t* token_dev, int64_t V, int64_
                      hipStream_t st, int n = 1);
 // Repetition penalty of sample_top_k_top_p (TenzoEngine.cpp:1735-1743), in
 // place and in the order given (a token listed twice is penalised twice).
+// sample_top_k_top_p (TenzoEngine.cpp:1722-1807) for temperature > 0 with the
+// draw r: the token goes to *out_token (device). ws: sample_ws_bytes(V).
+constexpr int kSampleSlice = 2048;  // logits per first-stage workgroup
+constexpr int kSampleK = 64;        // the reference clamps top_k to [1, 64]
+size_t sample_ws_bytes(int64_t V);
+int launch_sample(const float* logits, int64_t V, int top_k, float top_p, float temperature,
+                  float r, void* ws, int32_t* out_token, hipStream_t st);
 int launch_rep_penalty(float* logits, int64_t V, const int32_t* tokens, int n, float penalty,
                        hipStream_t st);
 

@@ -252,6 +252,124 @@ __global__ void rep_penalty_kernel(float* __restrict__ logits, int64_t V,
     }
 }
 
+// ------------------------------------------------------------- sampling --
+// sample_top_k_top_p (:1722-1807) for temperature > 0: the top-k (k <= 64)
+// logits, a softmax at the temperature over them, the top-p cutoff and one
+// draw r in [0, 1]. Stage 1: each workgroup sorts a slice of kSampleSlice
+// logits in LDS (bitonic, order "a before b" = larger value, or equal value
+// and lower index) and keeps its first 64; stage 2: one workgroup sorts the
+// slices' candidates the same way, takes the first k, orders them as the
+// reference's heap hands them out (descending (value, index)), and one lane
+// replays the reference's probability, cutoff and draw loops in its order.
+
+template <int N, int THREADS>
+__device__ __forceinline__ void bitonic_sort_desc(float* v, int* idx) {
+    for (int size = 2; size <= N; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int t = threadIdx.x; t < N / 2; t += THREADS) {
+                const int lo = 2 * t - (t & (stride - 1));
+                const int hi = lo + stride;
+                const bool up = (lo & size) == 0;  // this run sorts "before" first
+                const float a = v[lo], b = v[hi];
+                const int ia = idx[lo], ib = idx[hi];
+                const bool b_first = b > a || (b == a && ib < ia);
+                if (b_first == up) {
+                    v[lo] = b;
+                    v[hi] = a;
+                    idx[lo] = ib;
+                    idx[hi] = ia;
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) sample_slice_kernel(const float* __restrict__ logits,
+                                                           int64_t V, float2* __restrict__ cand) {
+    __shared__ float v[kSampleSlice];
+    __shared__ int idx[kSampleSlice];
+    const int64_t base = (int64_t)blockIdx.x * kSampleSlice;
+    for (int t = threadIdx.x; t < kSampleSlice; t += 256) {
+        const int64_t i = base + t;
+        v[t] = i < V ? logits[i] : -INFINITY;
+        idx[t] = i < V ? (int)i : INT_MAX;
+    }
+    __syncthreads();
+    bitonic_sort_desc<kSampleSlice, 256>(v, idx);
+    if (threadIdx.x < kSampleK)
+        cand[(int64_t)blockIdx.x * kSampleK + threadIdx.x] =
+            make_float2(v[threadIdx.x], __int_as_float(idx[threadIdx.x]));
+}
+
+__global__ void __launch_bounds__(1024)
+sample_pick_kernel(const float2* __restrict__ cand, int nslices, int k, float top_p,
+                   float temperature, float r, int32_t* __restrict__ out) {
+    __shared__ float v[kSampleSlice * 4];
+    __shared__ int idx[kSampleSlice * 4];
+    const int n = nslices * kSampleK;
+    for (int t = threadIdx.x; t < kSampleSlice * 4; t += 1024) {
+        const float2 c = t < n ? cand[t] : make_float2(-INFINITY, __int_as_float(INT_MAX));
+        v[t] = c.x;
+        idx[t] = __float_as_int(c.y);
+    }
+    __syncthreads();
+    bitonic_sort_desc<kSampleSlice * 4, 1024>(v, idx);
+    if (threadIdx.x != 0) return;
+    // candidates as the heap hands them out: descending (value, index) (:1769-1774)
+    float cv[kSampleK];
+    int ci[kSampleK];
+    int m = 0;
+    for (int j = 0; j < k; ++j)
+        if (idx[j] != INT_MAX) {
+            cv[m] = v[j];
+            ci[m] = idx[j];
+            ++m;
+        }
+    for (int a = 1; a < m; ++a) {  // equal values: higher index first
+        const float x = cv[a];
+        const int xi = ci[a];
+        int b = a - 1;
+        while (b >= 0 && cv[b] == x && ci[b] < xi) {
+            cv[b + 1] = cv[b];
+            ci[b + 1] = ci[b];
+            --b;
+        }
+        cv[b + 1] = x;
+        ci[b + 1] = xi;
+    }
+    float probs[kSampleK];
+    const float max_l = cv[0];
+    float sum_exp = 0.0f;
+    for (int i = 0; i < m; ++i) {  // :1776-1782
+        probs[i] = expf((cv[i] - max_l) / temperature);
+        sum_exp += probs[i];
+    }
+    for (int i = 0; i < m; ++i) probs[i] /= sum_exp;
+    float cum_p = 0.0f;
+    int cutoff = m;
+    for (int i = 0; i < m; ++i) {  // :1784-1792
+        cum_p += probs[i];
+        if (cum_p >= top_p) {
+            cutoff = i + 1;
+            break;
+        }
+    }
+    float sub_sum = 0.0f;
+    for (int i = 0; i < cutoff; ++i) sub_sum += probs[i];
+    for (int i = 0; i < cutoff; ++i) probs[i] /= sub_sum;
+    float acc = 0.0f;
+    int pick = ci[0];
+    for (int i = 0; i < cutoff; ++i) {  // :1798-1804
+        acc += probs[i];
+        if (r <= acc) {
+            pick = ci[i];
+            break;
+        }
+    }
+    *out = pick;
+}
+
 // -------------------------------------------------------------------- host --
 
 static int64_t head_blocks(int64_t V) { return ceil_div(V, 64); }
@@ -317,6 +435,25 @@ int launch_embed_f32(const float* E, const int32_t* token_dev, int64_t V, int64_
     hipLaunchKernelGGL(embed_f32_kernel, dim3((unsigned)ceil_div(H, 256), (unsigned)n), dim3(256),
                        0, st, E, token_dev, V, H, x);
     return launch_status("embed_f32_kernel");
+}
+
+size_t sample_ws_bytes(int64_t V) { return (size_t)ceil_div(V, kSampleSlice) * kSampleK * 8; }
+
+int launch_sample(const float* logits, int64_t V, int top_k, float top_p, float temperature,
+                  float r, void* ws, int32_t* out_token, hipStream_t st) {
+    const int64_t nslices = ceil_div(V, kSampleSlice);
+    if (nslices * kSampleK > kSampleSlice * 4) {
+        set_error("sampler: vocab %lld above %d", (long long)V, kSampleSlice * kSampleSlice * 4 / kSampleK);
+        return TENZO_ERROR_UNSUPPORTED;
+    }
+    const int k = top_k < 1 ? 1 : (top_k > kSampleK ? kSampleK : top_k);  // :1731
+    hipLaunchKernelGGL(sample_slice_kernel, dim3((unsigned)nslices), dim3(256), 0, st, logits, V,
+                       (float2*)ws);
+    int rc = launch_status("sample_slice_kernel");
+    if (rc) return rc;
+    hipLaunchKernelGGL(sample_pick_kernel, dim3(1), dim3(1024), 0, st, (const float2*)ws,
+                       (int)nslices, k, top_p, temperature, r, out_token);
+    return launch_status("sample_pick_kernel");
 }
 
 int launch_rep_penalty(float* logits, int64_t V, const int32_t* tokens, int n, float penalty,
@@ -396,6 +533,18 @@ TENZO_HIP_API int tenzo_hip_argmax(const float* logits, int64_t V, int32_t* out_
     void* ws = Scratch::get(kScratchHead, argmax_ws_bytes(V), st);
     if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
     return launch_argmax(logits, V, argmax_ws_at(ws, V, out_idx), st);
+}
+
+TENZO_HIP_API int tenzo_hip_sample_top_k_top_p(const float* logits, int64_t V, int top_k,
+                                               float top_p, float temperature, float r,
+                                               int32_t* out_token, void* stream) {
+    TZ_CHECK(logits && out_token && V > 0, "sample_top_k_top_p: bad arguments");
+    TZ_CHECK(temperature > 0.0f, "sample_top_k_top_p: temperature must be > 0 (got %g)",
+             (double)temperature);
+    hipStream_t st = (hipStream_t)stream;
+    void* ws = Scratch::get(kScratchTmp, sample_ws_bytes(V), st);
+    if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+    return launch_sample(logits, V, top_k, top_p, temperature, r, ws, out_token, st);
 }
 
 TENZO_HIP_API int tenzo_hip_embed_i8(const void* w_packed, const float* scales,

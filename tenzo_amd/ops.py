@@ -253,6 +253,16 @@ def argmax(logits: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def sample_top_k_top_p(logits: torch.Tensor, top_k: int, top_p: float, temperature: float,
+                       r: float) -> int:
+    """sample_top_k_top_p's sampling branch on device logits with the draw r."""
+    out = torch.empty(1, dtype=torch.int32, device=logits.device)
+    _lib.check(_lib.load().tenzo_hip_sample_top_k_top_p(
+        _ptr(logits), logits.numel(), int(top_k), float(top_p), float(temperature), float(r),
+        _ptr(out), _stream()), "sample_top_k_top_p")
+    return int(out.item())
+
+
 def embed_i8(w_packed, scales, token: torch.Tensor, V: int, H: int) -> torch.Tensor:
     x = torch.empty(H, dtype=torch.float32, device=w_packed.device)
     _lib.check(_lib.load().tenzo_hip_embed_i8(_ptr(w_packed), _ptr(scales), _ptr(token), V, H,

@@ -457,3 +457,55 @@ def test_decode_stages_against_live_reference():
     lg, _, _ = oracle.lm_head(xn, sm.embed, sm.embed_scales)
     np.testing.assert_allclose(lg, logits_ref, rtol=1e-5, atol=1e-6)
     R.ref_engine_destroy(e)
+
+
+def _libc():
+    import ctypes
+    libc = ctypes.CDLL("libc.so.6")
+    libc.rand.restype = ctypes.c_int
+    libc.srand.argtypes = [ctypes.c_uint]
+    return libc
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="compiled reference not built")
+def test_sampler_matches_compiled_reference():
+    """orc_sample_top_k_top_p against the reference's own sample_top_k_top_p
+    (TenzoEngine.cpp:1722-1807) on the same logits and the same rand() draw:
+    the reference draws r = rand()/RAND_MAX from the process's libc, so the
+    test seeds libc, lets the reference sample, reseeds and hands the oracle
+    the same r."""
+    import ctypes
+    R = oracle.ref()
+    libc = _libc()
+    V = 4096
+    e = R.ref_engine_create(128, 1, 1, 1, 64, V, 8)
+    try:
+        rng = np.random.default_rng(7)
+        cases = [(40, 0.9, 0.7), (1, 0.9, 0.7), (64, 1.0, 1.3), (10, 0.5, 0.2), (64, 0.99, 5.0),
+                 (3, 0.1, 1.0), (200, 0.95, 0.8), (0, 0.9, 0.7)]
+        for trial in range(240):
+            k, p, T = cases[trial % len(cases)]
+            logits = (rng.standard_normal(V) * rng.uniform(0.5, 8.0)).astype(np.float32)
+            seed = 1000 + trial
+            libc.srand(seed)
+            t_ref = R.ref_engine_sample(e, logits.ctypes.data_as(ctypes.c_void_p), T, p, k, 1.0,
+                                        None, 0)
+            libc.srand(seed)
+            r = np.float32(libc.rand()) / np.float32(2147483647)
+            t_orc = oracle.sample_top_k_top_p(logits, k, p, T, float(r))
+            assert t_orc == t_ref, (trial, k, p, T)
+    finally:
+        R.ref_engine_destroy(e)
+
+
+def test_sampler_special_cases():
+    rng = np.random.default_rng(3)
+    logits = rng.standard_normal(1000).astype(np.float32)
+    top = int(np.argmax(logits))
+    for r in (0.0, 0.5, 1.0):
+        assert oracle.sample_top_k_top_p(logits, 1, 0.9, 0.7, r) == top      # k = 1
+        assert oracle.sample_top_k_top_p(logits, 40, 0.9, 1e-4, r) == top    # T -> 0
+    # top_p = 1 keeps all k: with r = 1 the last candidate (the k-th largest) is drawn
+    order = np.argsort(-logits)
+    assert oracle.sample_top_k_top_p(logits, 5, 1.0, 1e6, 1.0) in set(order[:5].tolist())
+    assert oracle.sample_top_k_top_p(logits, 5, 1.0, 1.0, 0.0) == top
