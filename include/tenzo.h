@@ -21,7 +21,12 @@
  *   - sampling with temperature > 0 runs on the device with the reference's
  *     algorithm and draw (rand()/RAND_MAX from the process's libc); among
  *     logits equal to the k-th largest the lowest indices are kept, where the
- *     reference's heap keeps an insertion-order-dependent subset.
+ *     reference's heap keeps an insertion-order-dependent subset;
+ *   - tenzo_load_model takes the projection shapes from the config (the
+ *     reference hard-codes BitNet-2B's 2560/640 there) and returns
+ *     TENZO_ERROR_MODEL_PARSE when weights.bin is smaller than the fp32
+ *     embedding table (the reference reads past the end); otherwise it
+ *     follows the reference's offsets, scales and fallbacks.
  */
 #ifndef TENZO_H
 #define TENZO_H

@@ -56,6 +56,14 @@ TENZO_HIP_API size_t tenzo_hip_tl1_packed_bytes(int64_t N, int64_t K);
 TENZO_HIP_API int tenzo_hip_tl1_repack(const uint8_t* w_tl1, void* w_packed, int64_t N,
                                        int64_t K, void* stream);
 
+/* The device layout straight from the raw 2-bit layout the model loader
+ * reads (pack_ternary_weights_raw's input, TenzoEngine.cpp:1842-1884: byte
+ * (r/4, c) of [N/4][K] holds row r, column c at bits 2(r%4) as w+1): the same
+ * bytes as tenzo_hip_tl1_repack of the TL1 blocks that function produces.
+ * N % 64 == 0. */
+TENZO_HIP_API int tenzo_hip_tl1_repack_raw(const uint8_t* raw, void* w_packed, int64_t N,
+                                           int64_t K, void* stream);
+
 /* Activation quantization of build_lut (TenzoEngine.cpp:22-62) for M tokens
  * of K values: codes[m][k] = round(x * 31/absmax), written with a row stride
  * of ceil(K/64)*64 (zero padded); q[m] = {absmax/31, sum of codes}. When
@@ -181,6 +189,12 @@ TENZO_HIP_API int tenzo_hip_lm_head_i8_codes(const int8_t* codes, const tenzo_hi
  * the first maximum, written to *out_idx (device int32). */
 TENZO_HIP_API int tenzo_hip_argmax(const float* logits, int64_t V, int32_t* out_idx,
                                    void* stream);
+/* The model loader's int8 LM-head quantization (load_model_from_files,
+ * TenzoEngine.cpp:1925-1941) of V fp32 rows of H, as the reference is built
+ * (-ffast-math): scales[v] = amax * (1/127) (amax floored at 1e-8), codes =
+ * clamp(round(x * (127/amax)), -127, 127), row-major [V][H] int8. */
+TENZO_HIP_API int tenzo_hip_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes,
+                                          float* scales, void* stream);
 /* Sampling branch of sample_top_k_top_p (TenzoEngine.cpp:1757-1806),
  * temperature > 0, on logits that already carry the repetition penalty: top_k
  * clamped to [1, 64], softmax at the temperature over the top-k, top-p
@@ -207,6 +221,16 @@ TENZO_HIP_API int tenzo_hip_execute_bitlinear_tl1(const float* act, const uint8_
                                                   float scale);
 TENZO_HIP_API int tenzo_hip_execute_rmsnorm(const float* in, const float* w, float* out,
                                             size_t dim, float eps);
+
+/* HOST function: the byte offsets of the weights.bin tensors and the
+ * projection scales that load_model_from_files (TenzoEngine.cpp:1943-1959)
+ * reads from a model.mlir text: an index constant whose next non-blank line
+ * is a memref.view of it, an f32 constant whose next non-blank line passes it
+ * as the third operand of "tenzo.bitlinear_elut". Up to max_views / max_scales
+ * values are written; *n_views / *n_scales receive the counts found. */
+TENZO_HIP_API int tenzo_hip_parse_model_mlir(const char* text, uint64_t* views, int max_views,
+                                             float* scales, int max_scales, int* n_views,
+                                             int* n_scales);
 
 /* ---- engine extensions (the engine itself is include/tenzo.h) ----------- */
 struct tenzo_engine_opaque;

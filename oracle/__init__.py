@@ -75,6 +75,7 @@ def lib() -> ctypes.CDLL:
             "orc_lm_head": (_F, [_P, _P, _P, _I64, _I64, _P, _P]),
             "orc_argmax": (_I, [_P, _I64]),
             "orc_sample_top_k_top_p": (_I, [_P, _I64, _I, _F, _F, _F]),
+            "orc_quant_rows_i8": (None, [_P, _I64, _I64, _P, _P]),
             "orc_embed_i8": (None, [_P, _P, _I64, _I, _P]),
             "orc_q4_0": (None, [_P, _P, _P, _I, _I]),
             "orc_q8_0": (None, [_P, _P, _P, _I, _I]),
@@ -123,6 +124,9 @@ def ref() -> ctypes.CDLL:
             "ref_engine_seq_len": (_I, [_P]),
             "ref_engine_step": (_I, [_P, _I, _P]),
             "ref_engine_sample": (_I, [_P, _P, _F, _F, _I, _F, _P, _I]),
+            "ref_engine_load": (_I, [_P, ctypes.c_char_p, ctypes.c_char_p]),
+            "ref_engine_layer_data": (ctypes.c_long, [_P, _I, _I, _P, _P]),
+            "ref_engine_head_data": (None, [_P, _P, _P, _P]),
             "ref_engine_prefill": (_I, [_P, _I]),
             "ref_engine_hidden": (None, [_P, _P]),
             "ref_num_threads": (_I, []),
@@ -275,6 +279,15 @@ def lm_head(xn, W, scales):
 def argmax(logits) -> int:
     logits = f32(logits)
     return int(lib().orc_argmax(_ptr(logits), logits.size))
+
+
+def quant_rows_i8(E):
+    E = f32(E)
+    V, H = E.shape
+    codes = np.empty((V, H), np.int8)
+    scales = np.empty(V, np.float32)
+    lib().orc_quant_rows_i8(_ptr(E), V, H, _ptr(codes), _ptr(scales))
+    return codes, scales
 
 
 def sample_top_k_top_p(logits, top_k: int, top_p: float, temperature: float, r: float) -> int:

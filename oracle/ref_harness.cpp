@@ -222,6 +222,44 @@ int ref_engine_sample(void* e, const float* logits, float temperature, float top
     return impl->sample_top_k_top_p(&p, past, past_len);
 }
 
+// load_model_from_files (TenzoEngine.cpp:1887-2078) through the C API.
+int ref_engine_load(void* e, const char* weights, const char* mlir) {
+    return tenzo_load_model(static_cast<tenzo_engine_t>(e), weights, mlir);
+}
+
+// What the loader put in layer l: which 0..6 = q, k, v, out, gate, up, down
+// TL1 bytes (returns the byte count and writes the scale), 7..10 = in_norm,
+// attn_sub_norm, post_norm, ffn_sub_norm (returns the float count).
+long ref_engine_layer_data(void* e, int l, int which, void* out, float* scale) {
+    auto& lw = static_cast<tenzo_engine_t>(e)->impl->layers[l];
+    const std::vector<int8_t>* w[7] = {&lw.q_w, &lw.k_w, &lw.v_w, &lw.out_w,
+                                       &lw.gate_w, &lw.up_w, &lw.down_w};
+    const float sc[7] = {lw.q_scale, lw.k_scale, lw.v_scale, lw.out_scale,
+                         lw.gate_scale, lw.up_scale, lw.down_scale};
+    const std::vector<float>* nv[4] = {&lw.in_norm, &lw.attn_sub_norm, &lw.post_norm,
+                                       &lw.ffn_sub_norm};
+    if (which >= 0 && which < 7) {
+        if (out) std::memcpy(out, w[which]->data(), w[which]->size());
+        if (scale) *scale = sc[which];
+        return (long)w[which]->size();
+    }
+    if (which >= 7 && which < 11) {
+        const std::vector<float>& v = *nv[which - 7];
+        if (out) std::memcpy(out, v.data(), v.size() * 4);
+        return (long)v.size();
+    }
+    return -1;
+}
+
+// The loader's int8 LM head (codes [V][H], scales [V]) and final norm [H].
+void ref_engine_head_data(void* e, int8_t* codes, float* scales, float* final_norm) {
+    auto* impl = static_cast<tenzo_engine_t>(e)->impl.get();
+    if (codes) std::memcpy(codes, impl->embed_w_i8.data(), impl->embed_w_i8.size());
+    if (scales) std::memcpy(scales, impl->embed_scales.data(), impl->embed_scales.size() * 4);
+    if (final_norm)
+        std::memcpy(final_norm, impl->final_norm_w.data(), impl->final_norm_w.size() * 4);
+}
+
 int ref_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

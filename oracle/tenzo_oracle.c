@@ -387,6 +387,27 @@ int orc_argmax(const float* logits, int64_t V) {
     return (int)best;
 }
 
+/* The loader's LM-head quantization (:1925-1941) as the reference is built
+ * (-ffast-math): per row amax (floor 1e-8), stored scale = amax * (1/127) (the
+ * divide by the constant folded into a multiply), codes = clamp(round(x *
+ * (127 / amax)), -127, 127) (1 / (amax * (1/127)) re-associated to 127 /
+ * amax; x * (1 / scale) differs at exact .5 ties). */
+void orc_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes, float* scales) {
+    for (int64_t v = 0; v < V; ++v) {
+        const float* row = E + v * H;
+        float amax = 1e-8f;
+        for (int64_t i = 0; i < H; ++i) amax = fmaxf(amax, fabsf(row[i]));
+        const float scale = amax * (1.0f / 127.0f);
+        scales[v] = scale;
+        const float inv_s = 127.0f / amax;
+        for (int64_t i = 0; i < H; ++i) {
+            float c = roundf(row[i] * inv_s);
+            c = c < -127.0f ? -127.0f : (c > 127.0f ? 127.0f : c);
+            codes[v * H + i] = (int8_t)c;
+        }
+    }
+}
+
 /* sample_top_k_top_p (:1722-1807) for temperature > 0 after the penalty, with
  * the uniform draw r passed in (the reference draws rand()/RAND_MAX there).
  * Top-k by the reference's min-heap rule: the first k logits enter; a later

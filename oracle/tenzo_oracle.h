@@ -40,6 +40,9 @@
  *   orc_decode_step                  compiled reference whole-engine step on small
  *                                    configs (logits 1e-3, greedy token equal)
  *   orc_argmax                       brute force (first maximum)
+ *   orc_quant_rows_i8                the compiled reference's loader output (its
+ *                                    int8 LM head and row scales, bit-exact) on
+ *                                    synthetic model files
  *   orc_sample_top_k_top_p           the compiled reference's own sampler on the
  *                                    same logits and the same rand() draw (token
  *                                    equal) + special cases (top_k 1 = argmax,
@@ -116,6 +119,8 @@ void orc_attention_step(float* q, float* k, const float* v, int8_t* kc, int8_t* 
 float orc_lm_head(const float* xn, const int8_t* W, const float* scales, int64_t V,
                   int64_t H, float* logits, int8_t* codes);
 int orc_argmax(const float* logits, int64_t V);
+/* load_model_from_files' LM-head quantization (:1925-1941), row-major [V][H]. */
+void orc_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes, float* scales);
 /* sample_top_k_top_p (:1722-1807), temperature > 0, with the draw r in [0, 1]. */
 int orc_sample_top_k_top_p(const float* logits, int64_t V, int top_k, float top_p,
                            float temperature, float r);

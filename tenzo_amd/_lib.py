@@ -24,6 +24,7 @@ SIGNATURES = {
     "tenzo_hip_release_scratch": (_I, []),
     "tenzo_hip_tl1_packed_bytes": (_SZ, [_I64, _I64]),
     "tenzo_hip_tl1_repack": (_I, [_P, _P, _I64, _I64, _P]),
+    "tenzo_hip_tl1_repack_raw": (_I, [_P, _P, _I64, _I64, _P]),
     "tenzo_hip_rmsnorm_quant31": (_I, [_P, _P, _I, _F, _I64, _I64, _P, _P, _P, _P]),
     "tenzo_hip_bitlinear_tl1": (_I, [_P, _P, _P, _F, _I64, _I64, _I64, _P, _P, _P]),
     "tenzo_hip_bitlinear_tl1_f32": (_I, [_P, _P, _F, _I64, _I64, _I64, _P, _P]),
@@ -41,6 +42,8 @@ SIGNATURES = {
     "tenzo_hip_lm_head_i8": (_I, [_P, _P, _F, _P, _P, _P, _I64, _I64, _P]),
     "tenzo_hip_argmax": (_I, [_P, _I64, _P, _P]),
     "tenzo_hip_sample_top_k_top_p": (_I, [_P, _I64, _I, _F, _F, _F, _P, _P]),
+    "tenzo_hip_quant_rows_i8": (_I, [_P, _I64, _I64, _P, _P, _P]),
+    "tenzo_hip_parse_model_mlir": (_I, [_S, _P, _I, _P, _I, _P, _P]),
     "tenzo_hip_rmsnorm_quant127": (_I, [_P, _P, _I, _F, _I64, _I64, _P, _P, _P]),
     "tenzo_hip_lm_head_i8_codes": (_I, [_P, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     "tenzo_hip_embed_i8": (_I, [_P, _P, _P, _I64, _I64, _P, _P]),

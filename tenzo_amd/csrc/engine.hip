@@ -34,7 +34,13 @@
 #include "common.h"
 #include "decode_step.h"
 #include "lm_head.h"
+#include "model_file.h"
 #include "tl1.h"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 using namespace tz;
 
@@ -325,6 +331,180 @@ int enqueue_step(tenzo_engine_t e, bool head, int T, int max_chunks) {
     for (int l = 0; l < e->L; ++l)
         if ((rc = enqueue_layer(e, l, T, max_chunks))) return rc;
     return head ? enqueue_head(e) : TENZO_SUCCESS;
+}
+
+// ---- tenzo_load_model (load_model_from_files, TenzoEngine.cpp:1887-2078) ----
+
+// weights.bin mapped read-only for the duration of a load.
+struct MappedFile {
+    const uint8_t* p = nullptr;
+    size_t n = 0;
+    int fd = -1;
+    ~MappedFile() {
+        if (p && n) munmap(const_cast<uint8_t*>(p), n);
+        if (fd >= 0) close(fd);
+    }
+    bool open_ro(const char* path) {
+        fd = ::open(path, O_RDONLY);
+        if (fd < 0) return false;
+        struct stat st {};
+        if (fstat(fd, &st) != 0) return false;
+        n = (size_t)st.st_size;
+        if (n == 0) return true;
+        void* m = mmap(nullptr, n, PROT_READ, MAP_PRIVATE, fd, 0);
+        if (m == MAP_FAILED) return false;
+        p = static_cast<const uint8_t*>(m);
+        return true;
+    }
+};
+
+// The next tensor's offset: the next memref view of the MLIR, else the
+// running sequential offset (get_offset, :1991-2001); the running offset
+// advances by the tensor's size either way.
+struct OffsetCursor {
+    const std::vector<uint64_t>& views;
+    size_t v = 1;  // view 0 is the embedding table
+    uint64_t seq;
+    uint64_t next(uint64_t bytes) {
+        const uint64_t off = v < views.size() ? views[v++] : seq;
+        seq += bytes;
+        return off;
+    }
+};
+
+// A ternary projection of N rows x K columns from the raw [N/4][K] bytes at
+// off into rows row0.. of a device matrix; past the end of the file the
+// projection is all zeros (raw byte 0x55, as safe_pack_ternary's 0x55 TL1
+// fill, :1975-1983).
+int load_raw_projection(tenzo_engine_t e, const MappedFile& f, uint64_t off, int64_t N,
+                        int64_t K, void* dst, int64_t row0, uint8_t* staging) {
+    const size_t bytes = (size_t)N * (size_t)(K / 4);
+    if (off + bytes <= f.n) {
+        TZ_HIP(hipMemcpy(staging, f.p + off, bytes, hipMemcpyHostToDevice));
+    } else {
+        TZ_HIP(hipMemsetAsync(staging, 0x55, bytes, e->st));
+    }
+    char* out = (char*)dst + (size_t)(row0 / 64) * ceil_div(K, 64) * 1024;
+    int rc = launch_tl1_repack_raw(staging, out, N, K, e->st);
+    if (rc) return rc;
+    TZ_HIP(hipStreamSynchronize(e->st));
+    return TENZO_SUCCESS;
+}
+
+// An fp32 vector of n at off (norm weights); past the end of the file ones
+// (safe_slice_f32, :1966-1973).
+int load_vec(tenzo_engine_t e, const MappedFile& f, uint64_t off, int64_t n, float** dst) {
+    std::vector<float> v((size_t)n, 1.0f);
+    if (off + (uint64_t)n * 4 <= f.n) std::memcpy(v.data(), f.p + off, (size_t)n * 4);
+    return upload_vec(e, v.data(), n, dst);
+}
+
+int load_model_files(tenzo_engine_t e, const char* weights_path, const char* mlir_path) {
+    std::string text;
+    {
+        FILE* mf = std::fopen(mlir_path, "rb");
+        if (!mf) {
+            set_error("load_model: cannot open %s", mlir_path);
+            return TENZO_ERROR_IO;
+        }
+        char buf[1 << 16];
+        size_t got;
+        while ((got = std::fread(buf, 1, sizeof(buf), mf)) > 0) text.append(buf, got);
+        std::fclose(mf);
+    }
+    MappedFile f;
+    if (!f.open_ro(weights_path)) {
+        set_error("load_model: cannot open %s", weights_path);
+        return TENZO_ERROR_IO;
+    }
+    const int64_t H = e->H, F = e->F, V = e->V, qd = e->qd, kvd = e->kvd;
+    const uint64_t embed_bytes = (uint64_t)V * H * 4;
+    if (f.n < embed_bytes) {  // the reference reads the table without a bound (:1913)
+        set_error("load_model: %s holds %zu bytes, less than the %dx%d fp32 embedding table",
+                  weights_path, f.n, (int)V, (int)H);
+        return TENZO_ERROR_MODEL_PARSE;
+    }
+    ModelFileIndex ix;
+    parse_model_mlir(text.data(), text.size(), &ix);
+
+    // staging for the largest raw projection
+    const size_t stage_bytes = (size_t)std::max({qd * (H / 4), kvd * (H / 4), H * (qd / 4),
+                                                  F * (H / 4), H * (F / 4)});
+    uint8_t* staging = nullptr;
+    TZ_HIP(hipMalloc(&staging, stage_bytes));
+    OffsetCursor oc{ix.views, 1, embed_bytes};
+    size_t si = 0;
+    auto scale = [&]() { return si < ix.scales.size() ? ix.scales[si++] : 1.0f; };  // :2003-2008
+    const int64_t KSH = ceil_div(H, 64), KSF = ceil_div(F, 64), KSQ = ceil_div(qd, 64);
+    int rc = TENZO_SUCCESS;
+    for (int l = 0; l < e->L && !rc; ++l) {
+        DevLayer& d = e->layers[l];
+        if (!d.qkv) rc = alloc_tracked(e, &d.qkv, (size_t)((qd + 2 * kvd) / 64) * KSH * 1024, false);
+        if (!rc && !d.o) rc = alloc_tracked(e, &d.o, (size_t)(H / 64) * KSQ * 1024, false);
+        if (!rc && !d.gu) rc = alloc_tracked(e, &d.gu, (size_t)(2 * F / 64) * KSH * 1024, false);
+        if (!rc && !d.down) rc = alloc_tracked(e, &d.down, (size_t)(H / 64) * KSF * 1024, false);
+        if (rc) break;
+        // the order of :2010-2070: in_norm, q, k, v, attn_sub_norm, out, post_norm, gate,
+        // up, ffn_sub_norm, down
+        if (!rc) rc = load_vec(e, f, oc.next(H * 4), H, &d.norm[0]);
+        if (!rc) rc = load_raw_projection(e, f, oc.next(qd * (H / 4)), qd, H, d.qkv, 0, staging);
+        d.sc[0] = scale();
+        if (!rc) rc = load_raw_projection(e, f, oc.next(kvd * (H / 4)), kvd, H, d.qkv, qd, staging);
+        d.sc[1] = scale();
+        if (!rc)
+            rc = load_raw_projection(e, f, oc.next(kvd * (H / 4)), kvd, H, d.qkv, qd + kvd,
+                                     staging);
+        d.sc[2] = scale();
+        if (!rc) rc = load_vec(e, f, oc.next(H * 4), H, &d.norm[1]);
+        if (!rc) rc = load_raw_projection(e, f, oc.next(H * (qd / 4)), H, qd, d.o, 0, staging);
+        d.sc[3] = scale();
+        if (!rc) rc = load_vec(e, f, oc.next(H * 4), H, &d.norm[2]);
+        if (!rc) rc = load_raw_projection(e, f, oc.next(F * (H / 4)), F, H, d.gu, 0, staging);
+        d.sc[4] = scale();
+        if (!rc) rc = load_raw_projection(e, f, oc.next(F * (H / 4)), F, H, d.gu, F, staging);
+        d.sc[5] = scale();
+        if (!rc) rc = load_vec(e, f, oc.next(F * 4), F, &d.norm[3]);
+        if (!rc) rc = load_raw_projection(e, f, oc.next(H * (F / 4)), H, F, d.down, 0, staging);
+        d.sc[6] = scale();
+        d.mlp = true;
+        d.set = !rc;
+    }
+    (void)hipFree(staging);
+    if (rc) return rc;
+    // final norm: the next view, else the running offset (:2073-2075)
+    const uint64_t foff = oc.v < ix.views.size() ? ix.views[oc.v] : oc.seq;
+    if ((rc = load_vec(e, f, foff, H, &e->final_norm))) return rc;
+
+    // int8 LM head / tied embedding from the fp32 table at offset 0 (:1925-1941),
+    // quantized on the device in chunks of rows
+    if (!e->head_i8 &&
+        (rc = alloc_tracked(e, &e->head_i8, tenzo_hip_i8_packed_bytes(V, H), false)))
+        return rc;
+    if (!e->head_scales && (rc = alloc_t(e, &e->head_scales, (size_t)V * 4))) return rc;
+    int8_t* codes = nullptr;
+    float* rows = nullptr;
+    const int64_t chunk = std::max<int64_t>(1, std::min<int64_t>(V, (256 << 20) / (H * 4)));
+    bool ok = hipMalloc(&codes, (size_t)V * H) == hipSuccess &&
+              hipMalloc(&rows, (size_t)chunk * H * 4) == hipSuccess;
+    for (int64_t v0 = 0; ok && v0 < V; v0 += chunk) {
+        const int64_t n = std::min(chunk, V - v0);
+        ok = hipMemcpy(rows, f.p + (size_t)v0 * H * 4, (size_t)n * H * 4, hipMemcpyHostToDevice) ==
+                 hipSuccess &&
+             launch_quant_rows_i8(rows, n, H, codes + v0 * H, e->head_scales + v0, e->st) == 0 &&
+             hipStreamSynchronize(e->st) == hipSuccess;
+    }
+    ok = ok && launch_i8_repack(codes, e->head_i8, V, H, e->st) == 0 &&
+         hipStreamSynchronize(e->st) == hipSuccess;
+    if (rows) (void)hipFree(rows);
+    if (codes) (void)hipFree(codes);
+    if (!ok) {
+        set_error("load_model: uploading the LM head failed");
+        return TENZO_ERROR_OUT_OF_MEMORY;
+    }
+    e->head_kind = 1;
+    e->ds_layers_dirty = true;
+    drop_graphs(e);
+    return TENZO_SUCCESS;
 }
 
 // Tokens per batched-prefill pass: longer prompts go through in passes of
@@ -844,9 +1024,8 @@ TENZO_API tenzo_status_t tenzo_set_lm_head_f32(tenzo_engine_t e, const float* w,
 TENZO_API tenzo_status_t tenzo_load_model(tenzo_engine_t e, const char* weights_path,
                                           const char* mlir_path) {
     if (!e || !weights_path || !mlir_path) return TENZO_ERROR_INVALID_ARGUMENT;
-    set_error("tenzo_load_model: the weights.bin/model.mlir loader is not provided; install "
-              "weights with tenzo_set_layer_weights and tenzo_set_lm_head_i8");
-    return TENZO_ERROR_UNSUPPORTED;
+    if (hipSetDevice(e->dev) != hipSuccess) return TENZO_ERROR_UNSUPPORTED;
+    return (tenzo_status_t)load_model_files(e, weights_path, mlir_path);
 }
 
 TENZO_API tenzo_status_t tenzo_prefill_token(tenzo_engine_t e, int token) {

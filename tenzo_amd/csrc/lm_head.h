@@ -41,6 +41,9 @@ int launch_embed_f32(const float* E, const int32_t* token_dev, int64_t V, int64_
                      hipStream_t st, int n = 1);
 // Repetition penalty of sample_top_k_top_p (TenzoEngine.cpp:1735-1743), in
 // place and in the order given (a token listed twice is penalised twice).
+// The model loader's LM-head quantization of V fp32 rows of H (TenzoEngine.cpp:1925-1941).
+int launch_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes, float* scales,
+                         hipStream_t st);
 // sample_top_k_top_p (TenzoEngine.cpp:1722-1807) for temperature > 0 with the
 // draw r: the token goes to *out_token (device). ws: sample_ws_bytes(V).
 constexpr int kSampleSlice = 2048;  // logits per first-stage workgroup

@@ -252,6 +252,38 @@ __global__ void rep_penalty_kernel(float* __restrict__ logits, int64_t V,
     }
 }
 
+// --------------------------------------------------------- table loading --
+// The loader's LM-head quantization (load_model_from_files,
+// TenzoEngine.cpp:1925-1941) as the reference is built (-ffast-math): per row
+// amax (floor 1e-8), stored scale = amax * (1/127) (the divide by the
+// constant folded into a multiply), codes = clamp(round(x * (127 / amax)),
+// -127, 127) (1 / (amax * (1/127)) re-associated; x * (1 / scale) differs at
+// exact .5 ties). One block per row.
+__global__ void __launch_bounds__(256) quant_rows_i8_kernel(const float* __restrict__ E,
+                                                            int64_t H, int8_t* __restrict__ codes,
+                                                            float* __restrict__ scales) {
+    __shared__ float red[4];
+    const int64_t v = blockIdx.x;
+    const float* row = E + v * H;
+    float amax = 1e-8f;
+    for (int64_t i = threadIdx.x; i < H; i += 256) amax = fmaxf(amax, fabsf(row[i]));
+    amax = block256_max(amax, red);
+    const float scale = __fmul_rn(amax, 1.0f / 127.0f);
+    const float inv_s = 127.0f / amax;
+    for (int64_t i = threadIdx.x; i < H; i += 256) {
+        const float c = fminf(fmaxf(roundf(__fmul_rn(row[i], inv_s)), -127.0f), 127.0f);
+        codes[v * H + i] = (int8_t)c;
+    }
+    if (threadIdx.x == 0) scales[v] = scale;
+}
+
+int launch_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes, float* scales,
+                         hipStream_t st) {
+    hipLaunchKernelGGL(quant_rows_i8_kernel, dim3((unsigned)V), dim3(256), 0, st, E, H, codes,
+                       scales);
+    return launch_status("quant_rows_i8_kernel");
+}
+
 // ------------------------------------------------------------- sampling --
 // sample_top_k_top_p (:1722-1807) for temperature > 0: the top-k (k <= 64)
 // logits, a softmax at the temperature over them, the top-p cutoff and one
@@ -533,6 +565,13 @@ TENZO_HIP_API int tenzo_hip_argmax(const float* logits, int64_t V, int32_t* out_
     void* ws = Scratch::get(kScratchHead, argmax_ws_bytes(V), st);
     if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
     return launch_argmax(logits, V, argmax_ws_at(ws, V, out_idx), st);
+}
+
+TENZO_HIP_API int tenzo_hip_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes,
+                                          float* scales, void* stream) {
+    TZ_CHECK(E && codes && scales && V > 0 && H > 0 && V <= INT32_MAX,
+             "quant_rows_i8: bad arguments");
+    return launch_quant_rows_i8(E, V, H, codes, scales, (hipStream_t)stream);
 }
 
 TENZO_HIP_API int tenzo_hip_sample_top_k_top_p(const float* logits, int64_t V, int top_k,

@@ -22,6 +22,9 @@ struct RowScales {
 
 int launch_tl1_repack(const uint8_t* w_tl1, void* w_packed, int64_t N, int64_t K,
                       hipStream_t st);
+// From the loader's raw [N/4][K] 2-bit layout (pack_ternary_weights_raw's input).
+int launch_tl1_repack_raw(const uint8_t* raw, void* w_packed, int64_t N, int64_t K,
+                          hipStream_t st);
 // mode 0: codes of x; 1: codes of rms_norm_raw(x, norm_w); 3: x is gate|up
 // ([M][2K]) and the row is relu(gate)^2 * up before the norm. qmax 31 (TL1
 // activations) or 127 (LM head). Codes are written with row stride Kp.

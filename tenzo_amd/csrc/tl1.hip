@@ -50,6 +50,32 @@ __global__ void tl1_repack_kernel(const uint8_t* __restrict__ src, uint32_t* __r
     dst[idx] = out;
 }
 
+// The same device layout straight from the raw 2-bit layout the model
+// loader reads (pack_ternary_weights_raw, TenzoEngine.cpp:1842-1884): byte
+// (r/4, c) of a [N/4][K] array holds row r's column c at bits 2(r%4), as
+// w + 1. Columns past K are padded with u = 1.
+__global__ void tl1_repack_raw_kernel(const uint8_t* __restrict__ raw, uint32_t* __restrict__ dst,
+                                      int64_t nb, int64_t K, int64_t KS) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= nb * KS * 256) return;
+    const int q = (int)(idx & 3);
+    const int r = (int)((idx >> 2) & 63);
+    const int64_t bs = idx >> 8;
+    const int64_t s = bs % KS;
+    const int64_t b = bs / KS;
+    const int64_t row = b * 64 + r;
+    const uint8_t* src = raw + (row >> 2) * K;
+    const int shift = 2 * (int)(row & 3);
+    uint32_t out = 0;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+        const int64_t col = s * 64 + q * 16 + c;
+        const uint32_t u = col < K ? (uint32_t)((src[col] >> shift) & 3) : 1u;
+        out |= u << (8 * (c & 3) + 2 * (c >> 2));
+    }
+    dst[idx] = out;
+}
+
 // ------------------------------------------------------------------------
 // Activation quantization, one 256-thread block per token.
 //   QMAX 31  : build_lut (:28-42): amax floor 1e-6, code = round(v * (31/amax)),
@@ -420,6 +446,15 @@ int launch_tl1_gemv(const int8_t* codes, const tenzo_hip_actq_t* q, const void* 
     return launch_status("tl1_gemv_kernel");
 }
 
+int launch_tl1_repack_raw(const uint8_t* raw, void* w_packed, int64_t N, int64_t K,
+                          hipStream_t st) {
+    const int64_t nb = N / 64, KS = ceil_div(K, 64);
+    const int64_t total = nb * KS * 256;
+    hipLaunchKernelGGL(tl1_repack_raw_kernel, dim3((unsigned)ceil_div(total, 256)), dim3(256), 0,
+                       st, raw, (uint32_t*)w_packed, nb, K, KS);
+    return launch_status("tl1_repack_raw_kernel");
+}
+
 int launch_tl1_repack(const uint8_t* w_tl1, void* w_packed, int64_t N, int64_t K,
                       hipStream_t st) {
     const int64_t nb = N / 64, kh = K / 2, KS = ceil_div(K, 64);
@@ -480,6 +515,14 @@ TENZO_HIP_API int tenzo_hip_tl1_repack(const uint8_t* w_tl1, void* w_packed, int
              "tl1_repack: need N %% 64 == 0 and K %% 2 == 0 (N=%lld K=%lld)", (long long)N,
              (long long)K);
     return launch_tl1_repack(w_tl1, w_packed, N, K, (hipStream_t)stream);
+}
+
+TENZO_HIP_API int tenzo_hip_tl1_repack_raw(const uint8_t* raw, void* w_packed, int64_t N,
+                                           int64_t K, void* stream) {
+    TZ_CHECK(raw && w_packed, "tl1_repack_raw: null pointer");
+    TZ_CHECK(N > 0 && K > 0 && N % 64 == 0,
+             "tl1_repack_raw: need N %% 64 == 0 (N=%lld K=%lld)", (long long)N, (long long)K);
+    return launch_tl1_repack_raw(raw, w_packed, N, K, (hipStream_t)stream);
 }
 
 TENZO_HIP_API int tenzo_hip_rmsnorm_quant31(const float* x, const float* norm_w, int do_norm,

@@ -137,6 +137,12 @@ class Engine:
             self.set_kv_from(sm)
         self.set_rope_theta(c.theta)
 
+    def load_model(self, weights_path: str, mlir_path: str):
+        """tenzo_load_model: weights.bin + model.mlir as the reference's exporter
+        writes them."""
+        self._check(self.L.tenzo_load_model(self.h, weights_path.encode(), mlir_path.encode()),
+                    "tenzo_load_model")
+
     def set_kv_from(self, sm: synth.SynthModel):
         n = sm.ctx
         kc = np.ascontiguousarray(sm.kc[:, :, :n])
