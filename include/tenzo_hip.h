@@ -125,6 +125,26 @@ TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
                                              float* out, float* q_rot, float* k_rot,
                                              void* stream);
 
+/* ---- Ternary KV-cache decode attention ----------------------------------- */
+
+/* One decode step of FusedKVCache::forward_attention_raw in the ternary modes
+ * (TenzoEngine.cpp:534-648 append, :695-805 scores, :852-885 values):
+ * mode 1 = "tl1_fused", 2 = "popcount_fused". Arguments as
+ * tenzo_hip_attn_int8_decode, with cache rows of 32 bytes per (kv head, token)
+ * kb / vb [B][Hkv][max_seq][32] and fp32 scales ks / vs [B][Hkv][max_seq]:
+ *   V rows and mode-1 K rows: byte i = dims 4i..4i+3 as 2-bit fields w + 1
+ *   (w in {-1, 0, 1}, bit 2j for dim 4i + j; a field 3 reads as 0);
+ *   mode-2 K rows: uint64 {kp0, kp1, kn0, kn1} sign bitplanes (bit d of
+ *   kp0 / kn0: dim d above / below the row's threshold; kp1 / kn1 dims 64..127),
+ *   the layout of the reference's PopcountBitplanes (TenzoEngine.h:87-89).
+ * The new row is thresholded at half its mean |x| with scale = mean |x| over
+ * the dims above it (reductions in the order of the reference build). */
+TENZO_HIP_API int tenzo_hip_attn_tern_decode(int mode, const float* q, const float* k_new,
+                                             const float* v_new, uint8_t* kb, uint8_t* vb,
+                                             float* ks, float* vs, const float* rope_cs, int B,
+                                             int Hq, int Hkv, int max_seq, int pos, float* out,
+                                             float* q_rot, float* k_rot, void* stream);
+
 /* HOST function: fills cs[pos - pos0][0..127] = cos/sin table rows for
  * positions pos0 .. pos0+n_pos-1 with the reference's RoPE angles
  * (TenzoEngine.cpp:465-469; theta is 10000 there and a parameter here). */
@@ -247,16 +267,18 @@ struct tenzo_engine_opaque;
  * of the softmax sums. */
 TENZO_HIP_API int tenzo_hip_engine_prefill(struct tenzo_engine_opaque* e, const int32_t* tokens,
                                            int n, int exact);
-/* Copies a prefilled INT8 KV cache (codes [L][Hkv][seq_len][128], fp16 scales
- * [L][Hkv][seq_len]) into the engine and sets its sequence length; pointers
- * are device memory when is_device, else host. Mirrors writing the public
- * FusedKVCache state (TenzoEngine.h:60-115). */
-TENZO_HIP_API int tenzo_hip_engine_set_kv(struct tenzo_engine_opaque* e, const int8_t* kc,
-                                          const int8_t* vc, const uint16_t* ks,
-                                          const uint16_t* vs, int seq_len, int is_device);
+/* Copies a prefilled KV cache into the engine and sets its sequence length;
+ * pointers are device memory when is_device, else host. Layout by kv_mode:
+ * int8_fused codes [L][Hkv][seq_len][128] int8 and fp16 scales [L][Hkv][seq_len];
+ * tl1_fused / popcount_fused rows [L][Hkv][seq_len][32] bytes (the layouts of
+ * tenzo_hip_attn_tern_decode) and fp32 scales [L][Hkv][seq_len]. Mirrors
+ * writing the public FusedKVCache state (TenzoEngine.h:60-115). */
+TENZO_HIP_API int tenzo_hip_engine_set_kv(struct tenzo_engine_opaque* e, const void* kc,
+                                          const void* vc, const void* ks, const void* vs,
+                                          int seq_len, int is_device);
 /* Reads back the cache (same layout, seq_len positions). */
-TENZO_HIP_API int tenzo_hip_engine_get_kv(struct tenzo_engine_opaque* e, int8_t* kc,
-                                          int8_t* vc, uint16_t* ks, uint16_t* vs, int seq_len);
+TENZO_HIP_API int tenzo_hip_engine_get_kv(struct tenzo_engine_opaque* e, void* kc, void* vc,
+                                          void* ks, void* vs, int seq_len);
 /* Rewinds the sequence to seq_len <= the current length (positions past it
  * are overwritten by the next steps), e.g. to roll back rejected tokens or to
  * decode repeatedly at one position. No reference counterpart (the reference

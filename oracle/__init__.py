@@ -84,6 +84,12 @@ def lib() -> ctypes.CDLL:
             "orc_quantize_q8_0": (None, [_P, _I, _P]),
             "orc_q4_0_q8act": (None, [_P, _P, _P, _I, _I]),
             "orc_decode_step": (_I, [_P, _I, _I, _P, _P, _P]),
+            "orc_tern_stats": (None, [_P, _I, _P, _P]),
+            "orc_tern_pack": (None, [_P, _I, _F, _P]),
+            "orc_tern_bitplanes": (None, [_P, _F, _P]),
+            "orc_attn_tern": (None, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+            "orc_attention_step_tern": (None, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                               _P, _P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -111,6 +117,10 @@ def ref() -> ctypes.CDLL:
             "ref_rms_norm": (None, [_P, _P, _P, _I, _F]),
             "ref_pack_raw": (None, [_P, _I64, _I64, _P]),
             "ref_attention_int8": (None, [_I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
+            "ref_attention_tern": (None, [_I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
+            "ref_engine_create_mode": (_P, [_I, _I, _I, _I, _I, _I, _I, _I]),
+            "ref_engine_get_kv_tern": (None, [_P, _I, _P, _P, _P, _P]),
+            "ref_engine_set_kv_tern": (None, [_P, _I, _P, _P, _P, _P, _I]),
             "ref_q4_0": (None, [_P, _P, _P, _I, _I]),
             "ref_q8_0": (None, [_P, _P, _P, _I, _I]),
             "ref_gptq": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
@@ -265,6 +275,56 @@ def attention_step(q, k, v, kc, vc, ks, vs, Hq, Hkv, max_seq, pos, rope_cs, f16_
     return out, q, k
 
 
+# ternary KV modes: 1 = tl1_fused, 2 = popcount_fused
+KV_MODES = {"int8_fused": 0, "tl1_fused": 1, "popcount_fused": 2}
+
+
+def tern_stats(x):
+    """(threshold, scale) of one KV / query row (TenzoEngine.cpp:544-565)."""
+    x = f32(x)
+    th = ctypes.c_float()
+    s = ctypes.c_float()
+    lib().orc_tern_stats(_ptr(x), x.size, ctypes.byref(th), ctypes.byref(s))
+    return np.float32(th.value), np.float32(s.value)
+
+
+def tern_pack(x, th) -> np.ndarray:
+    x = f32(x)
+    out = np.empty(x.size // 4, np.uint8)
+    lib().orc_tern_pack(_ptr(x), x.size, float(th), _ptr(out))
+    return out
+
+
+def tern_bitplanes(x, th) -> np.ndarray:
+    x = f32(x)
+    out = np.empty(4, np.uint64)
+    lib().orc_tern_bitplanes(_ptr(x), float(th), _ptr(out))
+    return out
+
+
+def attn_tern(mode: int, q, kb, vb, ks, vs, Hq, Hkv, max_seq, seq_len) -> np.ndarray:
+    q = f32(q)
+    kb = np.ascontiguousarray(kb, np.uint8)
+    vb = np.ascontiguousarray(vb, np.uint8)
+    out = np.zeros(Hq * 128, np.float32)
+    lib().orc_attn_tern(mode, _ptr(q), _ptr(kb), _ptr(vb), _ptr(f32(ks)), _ptr(f32(vs)), Hq,
+                        Hkv, max_seq, seq_len, _ptr(out))
+    return out
+
+
+def attention_step_tern(mode: int, q, k, v, kb, vb, ks, vs, Hq, Hkv, max_seq, pos, rope_cs):
+    """forward_attention_raw in a ternary mode: mutates the given cache arrays in place."""
+    q = f32(q).copy()
+    k = f32(k).copy()
+    v = f32(v)
+    out = np.zeros(Hq * 128, np.float32)
+    for a in (kb, vb, ks, vs):
+        assert a.flags["C_CONTIGUOUS"]
+    lib().orc_attention_step_tern(mode, _ptr(q), _ptr(k), _ptr(v), _ptr(kb), _ptr(vb), _ptr(ks),
+                                  _ptr(vs), Hq, Hkv, max_seq, pos, _ptr(f32(rope_cs)), _ptr(out))
+    return out, q, k
+
+
 def lm_head(xn, W, scales):
     xn = f32(xn)
     W = np.ascontiguousarray(W, np.int8)
@@ -385,6 +445,7 @@ class Model(ctypes.Structure):
         ("final_norm", _P),
         ("embed", _P), ("embed_scales", _P),
         ("kc", _P), ("vc", _P), ("ks", _P), ("vs", _P),
+        ("kv_mode", _I),
     ]
 
 
@@ -394,7 +455,9 @@ class OracleModel:
     The KV arrays are owned here and updated in place by each step.
     """
 
-    def __init__(self, sm, f16_kv_scales: bool = True):
+    def __init__(self, sm, f16_kv_scales: bool = True, kv_mode: int = 0, kv=None):
+        """kv_mode 1 / 2 (tl1_fused / popcount_fused) take kv = (kb, vb, ks, vs):
+        [L][Hkv][max_seq][32] uint8 rows and [L][Hkv][max_seq] fp32 scales."""
         self.sm = sm
         c = sm.cfg
         self._keep = []
@@ -420,11 +483,16 @@ class OracleModel:
         m.final_norm = _ptr(sm.final_norm)
         m.embed = _ptr(sm.embed)
         m.embed_scales = _ptr(sm.embed_scales)
-        self.kc = sm.kc.copy()
-        self.vc = sm.vc.copy()
-        self.ks = sm.ks.copy()
-        self.vs = sm.vs.copy()
+        if kv_mode == 0:
+            self.kc = sm.kc.copy()
+            self.vc = sm.vc.copy()
+            self.ks = sm.ks.copy()
+            self.vs = sm.vs.copy()
+        else:
+            self.kc, self.vc, self.ks, self.vs = (np.ascontiguousarray(a).copy() for a in kv)
+            assert self.kc.dtype == np.uint8 and self.kc.shape[-1] == 32
         m.kc, m.vc, m.ks, m.vs = _ptr(self.kc), _ptr(self.vc), _ptr(self.ks), _ptr(self.vs)
+        m.kv_mode = kv_mode
         self.m = m
 
     def step(self, token: int, pos: int, theta: float):

@@ -87,6 +87,30 @@ void ref_attention_int8(int Hq, int Hkv, int max_seq, int pos,
     std::memcpy(vs, c.int8_v_scales.data(), n_sc * 4);
 }
 
+// The ternary KV modes (TenzoEngine.cpp:534-648, :695-885): mode 1 tl1_fused,
+// 2 popcount_fused. kb / vb [Hkv][max_seq][32] bytes (popcount K: the
+// PopcountBitplanes structs), ks / vs fp32; updated in place.
+void ref_attention_tern(int mode, int Hq, int Hkv, int max_seq, int pos, float* q, float* k,
+                        float* v, uint8_t* kb, uint8_t* vb, float* ks, float* vs, float* out) {
+    FusedKVCache c(1, Hq, Hkv, 128, max_seq, mode == 1 ? "tl1_fused" : "popcount_fused");
+    const size_t n_b = static_cast<size_t>(Hkv) * max_seq * 32;
+    const size_t n_sc = static_cast<size_t>(Hkv) * max_seq * 4;
+    uint8_t* ck = mode == 1 ? c.tl1_k.data() : reinterpret_cast<uint8_t*>(c.popcount_k.data());
+    uint8_t* cv = mode == 1 ? c.tl1_v.data() : c.popcount_v.data();
+    float* cks = mode == 1 ? c.tl1_k_scales.data() : c.popcount_k_scales.data();
+    float* cvs = mode == 1 ? c.tl1_v_scales.data() : c.popcount_v_scales.data();
+    std::memcpy(ck, kb, n_b);
+    std::memcpy(cv, vb, n_b);
+    std::memcpy(cks, ks, n_sc);
+    std::memcpy(cvs, vs, n_sc);
+    c.cur_seq_len = pos;
+    c.forward_attention_raw(0, q, k, v, out);
+    std::memcpy(kb, ck, n_b);
+    std::memcpy(vb, cv, n_b);
+    std::memcpy(ks, cks, n_sc);
+    std::memcpy(vs, cvs, n_sc);
+}
+
 // Quantized GEMV free functions (TenzoEngine.cpp:1022-1175).
 void ref_q4_0(const float* a, const uint8_t* w, float* y, int K, int N) {
     tenzo::compute_linear_gguf_q4_0(a, w, y, K, N);
@@ -104,6 +128,22 @@ void ref_awq(const float* a, const uint32_t* qw, const float* s, const uint32_t*
 }
 
 // ---- Whole engine (TenzoEngine.cpp:1215-1838) through the reference's C API ----
+
+// kv_mode is borrowed by the engine and re-read every layer, hence literals.
+void* ref_engine_create_mode(int H, int Hq, int Hkv, int L, int F, int V, int max_seq, int mode) {
+    tenzo_config_t cfg = tenzo_default_config();
+    cfg.hidden_size = H;
+    cfg.num_q_heads = Hq;
+    cfg.num_kv_heads = Hkv;
+    cfg.head_dim = 128;
+    cfg.num_layers = L;
+    cfg.ffn_dim = F;
+    cfg.vocab_size = V;
+    cfg.max_seq_len = max_seq;
+    cfg.kv_mode = mode == 1 ? "tl1_fused" : mode == 2 ? "popcount_fused" : "int8_fused";
+    cfg.device = "cpu";
+    return tenzo_create_engine(&cfg);
+}
 
 void* ref_engine_create(int H, int Hq, int Hkv, int L, int F, int V, int max_seq) {
     tenzo_config_t cfg = tenzo_default_config();
@@ -152,6 +192,40 @@ void ref_engine_get_kv(void* e, int8_t* kc, int8_t* vc, float* ks, float* vs) {
     std::memcpy(vc, c.int8_v.data(), c.int8_v.size());
     std::memcpy(ks, c.int8_k_scales.data(), c.int8_k_scales.size() * 4);
     std::memcpy(vs, c.int8_v_scales.data(), c.int8_v_scales.size() * 4);
+}
+
+// Writes the ternary caches (full [L][Hkv][max_seq] layout) and the length.
+void ref_engine_set_kv_tern(void* e, int mode, const uint8_t* kb, const uint8_t* vb,
+                            const float* ks, const float* vs, int seq_len) {
+    FusedKVCache& c = static_cast<tenzo_engine_t>(e)->impl->kv_cache;
+    if (mode == 1) {
+        std::memcpy(c.tl1_k.data(), kb, c.tl1_k.size());
+        std::memcpy(c.tl1_v.data(), vb, c.tl1_v.size());
+        std::memcpy(c.tl1_k_scales.data(), ks, c.tl1_k_scales.size() * 4);
+        std::memcpy(c.tl1_v_scales.data(), vs, c.tl1_v_scales.size() * 4);
+    } else {
+        std::memcpy(c.popcount_k.data(), kb, c.popcount_k.size() * 32);
+        std::memcpy(c.popcount_v.data(), vb, c.popcount_v.size());
+        std::memcpy(c.popcount_k_scales.data(), ks, c.popcount_k_scales.size() * 4);
+        std::memcpy(c.popcount_v_scales.data(), vs, c.popcount_v_scales.size() * 4);
+    }
+    c.cur_seq_len = seq_len;
+}
+
+// The ternary caches of an engine created with mode 1 / 2 (rows of 32 bytes).
+void ref_engine_get_kv_tern(void* e, int mode, uint8_t* kb, uint8_t* vb, float* ks, float* vs) {
+    FusedKVCache& c = static_cast<tenzo_engine_t>(e)->impl->kv_cache;
+    if (mode == 1) {
+        std::memcpy(kb, c.tl1_k.data(), c.tl1_k.size());
+        std::memcpy(vb, c.tl1_v.data(), c.tl1_v.size());
+        std::memcpy(ks, c.tl1_k_scales.data(), c.tl1_k_scales.size() * 4);
+        std::memcpy(vs, c.tl1_v_scales.data(), c.tl1_v_scales.size() * 4);
+    } else {
+        std::memcpy(kb, c.popcount_k.data(), c.popcount_k.size() * 32);
+        std::memcpy(vb, c.popcount_v.data(), c.popcount_v.size());
+        std::memcpy(ks, c.popcount_k_scales.data(), c.popcount_k_scales.size() * 4);
+        std::memcpy(vs, c.popcount_v_scales.data(), c.popcount_v_scales.size() * 4);
+    }
 }
 
 int ref_engine_seq_len(void* e) { return tenzo_get_seq_len(static_cast<tenzo_engine_t>(e)); }

@@ -349,6 +349,169 @@ void orc_attention_step(float* q, float* k, const float* v, int8_t* kc, int8_t* 
 }
 
 /* ------------------------------------------------------------------------- */
+/* Ternary KV modes: tl1_fused (2-bit K and V, :534-587 append, :695-763 and  */
+/* :852-885 attention) and popcount_fused (K as sign bitplanes, 2-bit V,       */
+/* :588-648 append, :764-805 and :852-885 attention). Cache rows are 32 bytes  */
+/* per (kv head, token): tl1 K / every V byte i holds dims 4i..4i+3 as 2-bit   */
+/* fields (w + 1) from bit 0; popcount K is uint64 {kp0, kp1, kn0, kn1} (bit d */
+/* of kp0 / kn0: dim d > th / < -th; kp1 / kn1: dims 64..127). Scales fp32.    */
+/* ------------------------------------------------------------------------- */
+
+/* Sum of |x[i]| (over the i with |x[i]| > th when masked) in the order the
+ * reference build evaluates it (-O3 -mavx2 -ffast-math): eight lanes i mod 8,
+ * each summed in index order, then ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)). */
+static float tern_abs_sum(const float* x, int d, int masked, float th, int* cnt) {
+    float l[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int c = 0;
+    for (int i = 0; i < d; ++i) {
+        const float a = fabsf(x[i]);
+        if (!masked || a > th) {
+            l[i & 7] += a;
+            ++c;
+        }
+    }
+    if (cnt) *cnt = c;
+    const float a0 = l[0] + l[4], a1 = l[1] + l[5], a2 = l[2] + l[6], a3 = l[3] + l[7];
+    return (a0 + a2) + (a1 + a3);
+}
+
+/* :544-565: mean |x|, threshold 0.5 mean, scale = mean of the |x| above it
+ * (mean + 1e-6 when none is). */
+void orc_tern_stats(const float* x, int d, float* th, float* s) {
+    const float mean = tern_abs_sum(x, d, 0, 0.0f, NULL) / (float)d;
+    const float t = 0.5f * mean;
+    int cnt = 0;
+    const float nz = tern_abs_sum(x, d, 1, t, &cnt);
+    *th = t;
+    *s = cnt > 0 ? nz / (float)cnt : mean + 1e-6f;
+}
+
+static int tern_code(float v, float th) { return v > th ? 1 : (v < -th ? -1 : 0); }
+
+/* :567-582: four dims per byte, field (w + 1) at bit 2j for dim 4i + j. */
+void orc_tern_pack(const float* x, int d, float th, uint8_t* out) {
+    for (int i = 0; i < d; i += 4) {
+        unsigned b = 0;
+        for (int j = 0; j < 4; ++j) b |= (unsigned)(tern_code(x[i + j], th) + 1) << (2 * j);
+        out[i / 4] = (uint8_t)b;
+    }
+}
+
+/* :622-633: {kp0, kp1, kn0, kn1} for a 128-dim row. */
+void orc_tern_bitplanes(const float* x, float th, uint64_t* out) {
+    uint64_t p0 = 0, p1 = 0, n0 = 0, n1 = 0;
+    for (int i = 0; i < 64; ++i) {
+        if (x[i] > th) p0 |= 1ull << i;
+        else if (x[i] < -th) n0 |= 1ull << i;
+        if (x[64 + i] > th) p1 |= 1ull << i;
+        else if (x[64 + i] < -th) n1 |= 1ull << i;
+    }
+    out[0] = p0; out[1] = p1; out[2] = n0; out[3] = n1;
+}
+
+/* The 2-bit field decode of the reference's LUT_W0 / LUT_W1 (:697-698):
+ * 0 -> -1, 1 -> 0, 2 -> +1, 3 -> 0. */
+static int tern_field(unsigned f) { return f == 3 ? 0 : (int)f - 1; }
+
+void orc_attn_tern(int mode, const float* q, const uint8_t* kb, const uint8_t* vb,
+                   const float* ks, const float* vs, int Hq, int Hkv, int max_seq,
+                   int seq_len, float* out) {
+    const int D = 128;
+    const int gqa = Hq / Hkv;                                 /* :659 */
+    const float scale_factor = 1.0f / sqrtf((float)D);        /* :660 */
+    if (seq_len <= 0 || Hkv <= 0) return;
+    float* scores = (float*)malloc((size_t)seq_len * 4);
+    for (int qh = 0; qh < Hq; ++qh) {
+        const int kvh = qh / gqa;
+        const float* qv = q + qh * D;
+        const uint8_t* kbase = kb + (size_t)kvh * max_seq * 32;
+        const uint8_t* vbase = vb + (size_t)kvh * max_seq * 32;
+        const float* ksb = ks + (size_t)kvh * max_seq;
+        const float* vsb = vs + (size_t)kvh * max_seq;
+        float max_score = -1e30f;
+        if (mode == 1) {
+            /* :700-714 as built: s_q = max|q| * (1/127) (1 when q = 0), codes
+             * round(q * (127 / max|q|)) (1/s_q re-associated) */
+            float max_q = 0.0f;
+            for (int d = 0; d < D; ++d) max_q = fmaxf(max_q, fabsf(qv[d]));
+            const float s_q = max_q > 0.0f ? max_q * (1.0f / 127.0f) : 1.0f;
+            const float inv = max_q > 0.0f ? 127.0f / max_q : 1.0f;
+            int qi[128];
+            for (int d = 0; d < D; ++d) qi[d] = (int)roundf(qv[d] * inv);
+            const float q_eff = s_q * scale_factor;
+            for (int t = 0; t < seq_len; ++t) {               /* :720-760 */
+                const uint8_t* kr = kbase + (size_t)t * 32;
+                int32_t isum = 0;
+                for (int d = 0; d < D; ++d)
+                    isum += qi[d] * tern_field((kr[d / 4] >> (2 * (d % 4))) & 3u);
+                const float dot = (float)isum * (q_eff * ksb[t]);
+                scores[t] = dot;
+                if (dot > max_score) max_score = dot;
+            }
+        } else {
+            /* :766-791: q's own threshold, scale and bitplanes */
+            float th_q, s_q;
+            orc_tern_stats(qv, D, &th_q, &s_q);
+            uint64_t qp[4];
+            orc_tern_bitplanes(qv, th_q, qp);
+            const float q_eff = s_q * scale_factor;
+            for (int t = 0; t < seq_len; ++t) {               /* :793-804 */
+                uint64_t kp[4];
+                memcpy(kp, kbase + (size_t)t * 32, 32);
+                const int pm = __builtin_popcountll(qp[0] & kp[0]) + __builtin_popcountll(qp[1] & kp[1]) +
+                               __builtin_popcountll(qp[2] & kp[2]) + __builtin_popcountll(qp[3] & kp[3]);
+                const int nm = __builtin_popcountll(qp[0] & kp[2]) + __builtin_popcountll(qp[1] & kp[3]) +
+                               __builtin_popcountll(qp[2] & kp[0]) + __builtin_popcountll(qp[3] & kp[1]);
+                const float dot = (float)(pm - nm) * (q_eff * ksb[t]);
+                scores[t] = dot;
+                if (dot > max_score) max_score = dot;
+            }
+        }
+        float sum = 0.0f;                                     /* :824-830 */
+        for (int t = 0; t < seq_len; ++t) {
+            scores[t] = expf(scores[t] - max_score);
+            sum += scores[t];
+        }
+        const float inv_sum = 1.0f / sum;
+        for (int t = 0; t < seq_len; ++t) scores[t] *= inv_sum;
+        float acc[128] = {0};                                 /* :852-885 */
+        for (int t = 0; t < seq_len; ++t) {
+            const uint8_t* vr = vbase + (size_t)t * 32;
+            const float wsc = scores[t] * vsb[t];
+            for (int d = 0; d < D; ++d)
+                acc[d] = fmaf((float)tern_field((vr[d / 4] >> (2 * (d % 4))) & 3u), wsc, acc[d]);
+        }
+        memcpy(out + qh * D, acc, sizeof(acc));
+    }
+    free(scores);
+}
+
+void orc_attention_step_tern(int mode, float* q, float* k, const float* v, uint8_t* kb,
+                             uint8_t* vb, float* ks, float* vs, int Hq, int Hkv, int max_seq,
+                             int pos, const float* rope_cs, float* out) {
+    const int D = 128;
+    orc_rope_apply(q, Hq, D, rope_cs);                        /* :458-481 */
+    orc_rope_apply(k, Hkv, D, rope_cs);                       /* :482-504 */
+    for (int h = 0; h < Hkv; ++h) {                           /* :534-648 */
+        const size_t row = (size_t)h * max_seq + pos;
+        float th_k, s_k, th_v, s_v;
+        orc_tern_stats(k + h * D, D, &th_k, &s_k);
+        orc_tern_stats(v + h * D, D, &th_v, &s_v);
+        ks[row] = s_k;
+        vs[row] = s_v;
+        if (mode == 1) {
+            orc_tern_pack(k + h * D, D, th_k, kb + row * 32);
+        } else {
+            uint64_t planes[4];
+            orc_tern_bitplanes(k + h * D, th_k, planes);
+            memcpy(kb + row * 32, planes, 32);
+        }
+        orc_tern_pack(v + h * D, D, th_v, vb + row * 32);
+    }
+    orc_attn_tern(mode, q, kb, vb, ks, vs, Hq, Hkv, max_seq, pos + 1, out);
+}
+
+/* ------------------------------------------------------------------------- */
 /* LM head (:1634-1720), argmax (:1745-1755), embedding (:1294-1316)          */
 /* ------------------------------------------------------------------------- */
 
@@ -664,10 +827,16 @@ int orc_decode_step(const orc_model_t* m, int token, int pos, const float* rope_
         orc_tl1_gemv_i32(m->v_w[l], codes, kvd, H, acc);
         for (int i = 0; i < kvd; ++i) v[i] = (float)acc[i] * (inv * sc[2]);
         /* :1578 */
-        orc_attention_step(q, k, v, m->kc + cache_off * D, m->vc + cache_off * D,
-                           m->ks + cache_off, m->vs + cache_off, m->n_q_heads,
-                           m->n_kv_heads, m->max_seq, pos, rope_cs, m->f16_kv_scales,
-                           attn);
+        if (m->kv_mode == 0)
+            orc_attention_step(q, k, v, m->kc + cache_off * D, m->vc + cache_off * D,
+                               m->ks + cache_off, m->vs + cache_off, m->n_q_heads,
+                               m->n_kv_heads, m->max_seq, pos, rope_cs, m->f16_kv_scales,
+                               attn);
+        else
+            orc_attention_step_tern(m->kv_mode, q, k, v, (uint8_t*)m->kc + cache_off * 32,
+                                    (uint8_t*)m->vc + cache_off * 32, m->ks + cache_off,
+                                    m->vs + cache_off, m->n_q_heads, m->n_kv_heads,
+                                    m->max_seq, pos, rope_cs, attn);
         /* :1582-1590 */
         orc_rms_norm(attn, m->attn_sub_norm[l], nx, H, eps);
         inv = orc_quant31(nx, H, codes);

@@ -116,6 +116,18 @@ void orc_attention_step(float* q, float* k, const float* v, int8_t* kc, int8_t* 
 
 /* ---- int8 LM head (compute_logits, :1634-1720), input already normalized ---- */
 /* Returns s_x; codes optional. */
+/* ---- ternary KV modes (tl1_fused = 1, popcount_fused = 2; :534-648, :695-885) ---- */
+void orc_tern_stats(const float* x, int d, float* th, float* s);
+void orc_tern_pack(const float* x, int d, float th, uint8_t* out);
+void orc_tern_bitplanes(const float* x, float th, uint64_t* out);
+/* kb / vb [Hkv][max_seq][32] bytes, ks / vs [Hkv][max_seq] fp32 */
+void orc_attn_tern(int mode, const float* q, const uint8_t* kb, const uint8_t* vb,
+                   const float* ks, const float* vs, int Hq, int Hkv, int max_seq,
+                   int seq_len, float* out);
+void orc_attention_step_tern(int mode, float* q, float* k, const float* v, uint8_t* kb,
+                             uint8_t* vb, float* ks, float* vs, int Hq, int Hkv, int max_seq,
+                             int pos, const float* rope_cs, float* out);
+
 float orc_lm_head(const float* xn, const int8_t* W, const float* scales, int64_t V,
                   int64_t H, float* logits, int8_t* codes);
 int orc_argmax(const float* logits, int64_t V);
@@ -153,8 +165,10 @@ typedef struct {
     const float* final_norm;
     const int8_t* embed;  /* [vocab][hidden] int8, tied LM head */
     const float* embed_scales;
-    /* KV cache state, [n_layers][n_kv_heads][max_seq][128] / [..][max_seq] */
+    /* KV cache state, [n_layers][n_kv_heads][max_seq][128] / [..][max_seq];
+     * kv_mode 1 / 2: rows of 32 bytes (see orc_attn_tern), fp32 scales */
     int8_t* kc; int8_t* vc; float* ks; float* vs;
+    int kv_mode;          /* 0 int8_fused, 1 tl1_fused, 2 popcount_fused */
 } orc_model_t;
 
 /* Runs one token through all layers at position pos (appending to the cache),

@@ -32,6 +32,8 @@ SIGNATURES = {
     "tenzo_hip_rmsnorm": (_I, [_P, _P, _P, _I64, _F, _P]),
     "tenzo_hip_attn_int8_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                                         _P, _P, _P, _P]),
+    "tenzo_hip_attn_tern_decode": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                        _I, _P, _P, _P, _P]),
     "tenzo_hip_rope_table": (None, [_F, _I, _I, _I, _P]),
     "tenzo_hip_gemv_q4_0": (_I, [_P, _I, _P, _P, _I, _I, _I, _P]),
     "tenzo_hip_gemv_q4_0_q8_0": (_I, [_P, _P, _P, _I, _I, _I, _P]),

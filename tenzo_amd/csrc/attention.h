@@ -32,6 +32,37 @@ struct AttnLaunch {
 int attn_pick_chunk(int seq_len, int Hkv, int B);
 int launch_attn(const AttnLaunch& L, hipStream_t st);
 
+// Merge of the chunk partials [B][Hq][max_chunks][130] of a decode step at
+// position pos (pos_dev when non-null) with chunks of T tokens into out.
+int launch_attn_combine(const float* part, float* out, int B, int Hq, int Hkv, int T,
+                        int max_chunks, const int* pos_dev, int pos, hipStream_t st);
+
+// Decode attention over a ternary KV cache (attention_tern.hip): mode 1
+// tl1_fused, 2 popcount_fused; rows of 32 bytes per (kv head, token) in kb / vb
+// ([B][Hkv][max_seq][32]) and fp32 scales ks / vs ([B][Hkv][max_seq]).
+struct AttnTernLaunch {
+    int mode = 0;
+    const float* q = nullptr;
+    const float* k_new = nullptr;
+    const float* v_new = nullptr;
+    uint8_t* kb = nullptr;
+    uint8_t* vb = nullptr;
+    float* ks = nullptr;
+    float* vs = nullptr;
+    const float* rope = nullptr;
+    const int* pos_dev = nullptr;
+    int pos = 0;
+    int rope_indexed = 0;
+    int B = 1, Hq = 0, Hkv = 0, max_seq = 0;
+    int T = 64;
+    int max_chunks = 1;
+    float* out = nullptr;
+    float* part = nullptr;
+    float* q_rot = nullptr;
+    float* k_rot = nullptr;
+};
+int launch_attn_tern(const AttnTernLaunch& L, hipStream_t st);
+
 // Attention for n prompt tokens at positions pos0 .. pos0+n-1 over one INT8
 // cache: the k/v rows of all n tokens are RoPE'd, quantized and appended
 // first (as n decode steps would), then query i attends to positions

@@ -632,6 +632,22 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
     return rc;
 }
 
+int launch_attn_combine(const float* part, float* out, int B, int Hq, int Hkv, int T,
+                        int max_chunks, const int* pos_dev, int pos, hipStream_t st) {
+    AttnArgs a{};
+    a.part = const_cast<float*>(part);
+    a.out = out;
+    a.Hq = Hq;
+    a.Hkv = Hkv;
+    a.T = T;
+    a.max_chunks = max_chunks;
+    a.pos_dev = pos_dev;
+    a.pos = pos;
+    a.out_stride = (int64_t)Hq * kD;
+    hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, B), dim3(128), 0, st, a);
+    return launch_status("attn_combine_kernel");
+}
+
 int attn_prefill_max_chunks(int pos0, int n, int Hkv) {
     int mx = 1;
     for (int i = 0; i < n; ++i) {

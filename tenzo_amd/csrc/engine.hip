@@ -78,6 +78,11 @@ struct tenzo_engine_opaque {
     float* head_scales = nullptr;
     float* head_f32 = nullptr;
 
+    // KV cache: kv_kind 0 int8_fused (rows of 128 int8 codes, fp16 scales),
+    // 1 tl1_fused / 2 popcount_fused (rows of 32 bytes, fp32 scales)
+    int kv_kind = 0;
+    int kv_row = 128;  // bytes per (layer, kv head, token) row
+    int kv_sb = 2;     // bytes per scale
     int8_t* kc = nullptr;
     int8_t* vc = nullptr;
     uint16_t* ks = nullptr;
@@ -251,28 +256,52 @@ int enqueue_layer(tenzo_engine_t e, int l, int T, int max_chunks) {
     if ((rc = launch_tl1_gemv(e->codes, e->aq, w.qkv, rs, 1, e->qd + 2 * e->kvd, e->H, e->qkv,
                               nullptr, nullptr, st, 0, e->gemv_ws)))
         return rc;
-    // 4: RoPE, INT8 append at the device-held position, attention
-    AttnLaunch a{};
-    a.q = e->qkv;
-    a.k_new = e->qkv + e->qd;
-    a.v_new = e->qkv + e->qd + e->kvd;
-    const size_t head_off = (size_t)l * e->Hkv * e->max_seq;
-    a.kc = e->kc + head_off * kD;
-    a.vc = e->vc + head_off * kD;
-    a.ks = e->ks + head_off;
-    a.vs = e->vs + head_off;
-    a.rope = e->rope;
-    a.rope_indexed = 1;
-    a.pos_dev = e->io_dev + 1;
-    a.B = 1;
-    a.Hq = e->Hq;
-    a.Hkv = e->Hkv;
-    a.max_seq = e->max_seq;
-    a.T = T;
-    a.max_chunks = max_chunks;
-    a.out = e->attn;
-    a.part = e->attn_part;
-    if ((rc = launch_attn(a, st))) return rc;
+    // 4: RoPE, KV append at the device-held position, attention
+    if (e->kv_kind != 0) {
+        const size_t rows = (size_t)l * e->Hkv * e->max_seq;
+        AttnTernLaunch t{};
+        t.mode = e->kv_kind;
+        t.q = e->qkv;
+        t.k_new = e->qkv + e->qd;
+        t.v_new = e->qkv + e->qd + e->kvd;
+        t.kb = reinterpret_cast<uint8_t*>(e->kc) + rows * 32;
+        t.vb = reinterpret_cast<uint8_t*>(e->vc) + rows * 32;
+        t.ks = reinterpret_cast<float*>(e->ks) + rows;
+        t.vs = reinterpret_cast<float*>(e->vs) + rows;
+        t.rope = e->rope;
+        t.rope_indexed = 1;
+        t.pos_dev = e->io_dev + 1;
+        t.Hq = e->Hq;
+        t.Hkv = e->Hkv;
+        t.max_seq = e->max_seq;
+        t.T = T;
+        t.max_chunks = max_chunks;
+        t.out = e->attn;
+        t.part = e->attn_part;
+        if ((rc = launch_attn_tern(t, st))) return rc;
+    } else {
+        AttnLaunch a{};
+        a.q = e->qkv;
+        a.k_new = e->qkv + e->qd;
+        a.v_new = e->qkv + e->qd + e->kvd;
+        const size_t head_off = (size_t)l * e->Hkv * e->max_seq;
+        a.kc = e->kc + head_off * kD;
+        a.vc = e->vc + head_off * kD;
+        a.ks = e->ks + head_off;
+        a.vs = e->vs + head_off;
+        a.rope = e->rope;
+        a.rope_indexed = 1;
+        a.pos_dev = e->io_dev + 1;
+        a.B = 1;
+        a.Hq = e->Hq;
+        a.Hkv = e->Hkv;
+        a.max_seq = e->max_seq;
+        a.T = T;
+        a.max_chunks = max_chunks;
+        a.out = e->attn;
+        a.part = e->attn_part;
+        if ((rc = launch_attn(a, st))) return rc;
+    }
     // 5-7: attn sub-norm, O projection, residual 1
     if ((rc = launch_actquant(1, 31, e->attn, w.norm[1], e->eps, 1, e->H, KpH, e->codes, e->aq,
                               nullptr, st)))
@@ -609,6 +638,8 @@ int enqueue_prefill_layer(tenzo_engine_t e, int l, int pos0, int m, bool exact) 
 // engine's x ends as the last token's hidden state, as after n prefill_token
 // calls (bit for bit when exact, else up to the streaming attention's
 // softmax rounding).
+int run_step(tenzo_engine_t e, int token, bool head);
+
 int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
     if (!ready(e, false)) return TENZO_ERROR_INVALID_ARGUMENT;
     if (n <= 0 || !tokens) {
@@ -626,6 +657,16 @@ int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
     }
     TZ_HIP(hipSetDevice(e->dev));
     int rc;
+    if (e->kv_kind != 0) {
+        // the batched pass appends INT8 rows; a ternary cache is filled by
+        // decode steps without the LM head (tenzo_prefill_token per token)
+        for (int i = 0; i < n; ++i) {
+            if ((rc = run_step(e, tokens[i], false))) return rc;
+            TZ_HIP(hipStreamSynchronize(e->st));
+            e->seq_len += 1;
+        }
+        return TENZO_SUCCESS;
+    }
     if ((rc = prefill_buffers(e))) return rc;
     int m = 0;
     for (int i0 = 0; i0 < n; i0 += m) {
@@ -650,7 +691,7 @@ int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
 
 // Whether the persistent kernel can run this model as loaded.
 bool ds_usable(tenzo_engine_t e) {
-    if (e->ds_nwg <= 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192 ||
+    if (e->ds_nwg <= 0 || e->kv_kind != 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192 ||
         e->L > kDsMaxLayers || e->max_seq > ds_max_context(e->Hq / e->Hkv))
         return false;
     for (const DevLayer& d : e->layers)
@@ -820,8 +861,10 @@ TENZO_API void tenzo_destroy_engine(tenzo_engine_t e);
 TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     tenzo_config_t c = config ? *config : tenzo_default_config();
     const std::string kv = c.kv_mode ? c.kv_mode : "int8_fused";
-    if (kv != "int8_fused") {
-        set_error("kv_mode \"%s\" is not provided on the GPU (int8_fused only)", kv.c_str());
+    const int kv_kind = kv == "int8_fused" ? 0 : kv == "tl1_fused" ? 1 : kv == "popcount_fused" ? 2 : -1;
+    if (kv_kind < 0) {
+        set_error("kv_mode \"%s\" is not provided on the GPU (int8_fused, tl1_fused, "
+                  "popcount_fused)", kv.c_str());
         return nullptr;
     }
     const int H = c.hidden_size, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
@@ -841,6 +884,9 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     auto* e = new tenzo_engine_opaque();
     e->cfg = c;
     e->kv_mode = kv;
+    e->kv_kind = kv_kind;
+    e->kv_row = kv_kind == 0 ? kD : 32;
+    e->kv_sb = kv_kind == 0 ? 2 : 4;
     e->device = c.device ? c.device : "rocm";
     e->cfg.kv_mode = e->kv_mode.c_str();
     e->cfg.device = e->device.c_str();
@@ -861,8 +907,9 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     const int64_t Fp = ceil_div(e->F, 64) * 64;
     const size_t ws = tl1_ws_bytes(1, 2 * e->F > e->qd + 2 * e->kvd ? 2 * e->F
                                                                     : e->qd + 2 * e->kvd);
-    ok = ok && !alloc_t(e, &e->kc, cache * kD, true) && !alloc_t(e, &e->vc, cache * kD, true) &&
-         !alloc_t(e, &e->ks, cache * 2, true) && !alloc_t(e, &e->vs, cache * 2, true) &&
+    const size_t row = (size_t)e->kv_row, sb = (size_t)e->kv_sb;
+    ok = ok && !alloc_t(e, &e->kc, cache * row, true) && !alloc_t(e, &e->vc, cache * row, true) &&
+         !alloc_t(e, &e->ks, cache * sb, true) && !alloc_t(e, &e->vs, cache * sb, true) &&
          !alloc_t(e, &e->x, (size_t)H * 4) && !alloc_t(e, &e->qkv, (size_t)(e->qd + 2 * e->kvd) * 4) &&
          !alloc_t(e, &e->attn, (size_t)e->qd * 4) && !alloc_t(e, &e->h1, (size_t)H * 4) &&
          !alloc_t(e, &e->gu, (size_t)2 * e->F * 4) && !alloc_t(e, &e->xn, (size_t)H * 4) &&
@@ -1176,8 +1223,8 @@ TENZO_HIP_API int tenzo_hip_engine_decode(tenzo_engine_t e, int token, int n, in
     return TENZO_SUCCESS;
 }
 
-TENZO_HIP_API int tenzo_hip_engine_set_kv(tenzo_engine_t e, const int8_t* kc, const int8_t* vc,
-                                          const uint16_t* ks, const uint16_t* vs, int seq_len,
+TENZO_HIP_API int tenzo_hip_engine_set_kv(tenzo_engine_t e, const void* kc, const void* vc,
+                                          const void* ks, const void* vs, int seq_len,
                                           int is_device) {
     TZ_CHECK(e && kc && vc && ks && vs, "engine_set_kv: null pointer");
     TZ_CHECK(seq_len >= 0 && seq_len <= e->max_seq, "engine_set_kv: seq_len %d outside [0, %d]",
@@ -1186,35 +1233,37 @@ TENZO_HIP_API int tenzo_hip_engine_set_kv(tenzo_engine_t e, const int8_t* kc, co
     if (seq_len > 0) {
         const hipMemcpyKind k = is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
         const size_t rows = (size_t)e->L * e->Hkv;
-        TZ_HIP(hipMemcpy2DAsync(e->kc, (size_t)e->max_seq * kD, kc, (size_t)seq_len * kD,
-                                (size_t)seq_len * kD, rows, k, e->st));
-        TZ_HIP(hipMemcpy2DAsync(e->vc, (size_t)e->max_seq * kD, vc, (size_t)seq_len * kD,
-                                (size_t)seq_len * kD, rows, k, e->st));
-        TZ_HIP(hipMemcpy2DAsync(e->ks, (size_t)e->max_seq * 2, ks, (size_t)seq_len * 2,
-                                (size_t)seq_len * 2, rows, k, e->st));
-        TZ_HIP(hipMemcpy2DAsync(e->vs, (size_t)e->max_seq * 2, vs, (size_t)seq_len * 2,
-                                (size_t)seq_len * 2, rows, k, e->st));
+        const size_t R = (size_t)e->kv_row, S = (size_t)e->kv_sb;
+        TZ_HIP(hipMemcpy2DAsync(e->kc, R * e->max_seq, kc, R * seq_len,
+                                R * seq_len, rows, k, e->st));
+        TZ_HIP(hipMemcpy2DAsync(e->vc, R * e->max_seq, vc, R * seq_len,
+                                R * seq_len, rows, k, e->st));
+        TZ_HIP(hipMemcpy2DAsync(e->ks, S * e->max_seq, ks, S * seq_len,
+                                S * seq_len, rows, k, e->st));
+        TZ_HIP(hipMemcpy2DAsync(e->vs, S * e->max_seq, vs, S * seq_len,
+                                S * seq_len, rows, k, e->st));
         TZ_HIP(hipStreamSynchronize(e->st));
     }
     e->seq_len = seq_len;
     return TENZO_SUCCESS;
 }
 
-TENZO_HIP_API int tenzo_hip_engine_get_kv(tenzo_engine_t e, int8_t* kc, int8_t* vc, uint16_t* ks,
-                                          uint16_t* vs, int seq_len) {
+TENZO_HIP_API int tenzo_hip_engine_get_kv(tenzo_engine_t e, void* kc, void* vc, void* ks,
+                                          void* vs, int seq_len) {
     TZ_CHECK(e && kc && vc && ks && vs, "engine_get_kv: null pointer");
     TZ_CHECK(seq_len > 0 && seq_len <= e->max_seq, "engine_get_kv: bad seq_len %d", seq_len);
     TZ_HIP(hipSetDevice(e->dev));
     const size_t rows = (size_t)e->L * e->Hkv;
+    const size_t R = (size_t)e->kv_row, S = (size_t)e->kv_sb;
     TZ_HIP(hipStreamSynchronize(e->st));
-    TZ_HIP(hipMemcpy2D(kc, (size_t)seq_len * kD, e->kc, (size_t)e->max_seq * kD,
-                       (size_t)seq_len * kD, rows, hipMemcpyDeviceToHost));
-    TZ_HIP(hipMemcpy2D(vc, (size_t)seq_len * kD, e->vc, (size_t)e->max_seq * kD,
-                       (size_t)seq_len * kD, rows, hipMemcpyDeviceToHost));
-    TZ_HIP(hipMemcpy2D(ks, (size_t)seq_len * 2, e->ks, (size_t)e->max_seq * 2,
-                       (size_t)seq_len * 2, rows, hipMemcpyDeviceToHost));
-    TZ_HIP(hipMemcpy2D(vs, (size_t)seq_len * 2, e->vs, (size_t)e->max_seq * 2,
-                       (size_t)seq_len * 2, rows, hipMemcpyDeviceToHost));
+    TZ_HIP(hipMemcpy2D(kc, R * seq_len, e->kc, R * e->max_seq,
+                       R * seq_len, rows, hipMemcpyDeviceToHost));
+    TZ_HIP(hipMemcpy2D(vc, R * seq_len, e->vc, R * e->max_seq,
+                       R * seq_len, rows, hipMemcpyDeviceToHost));
+    TZ_HIP(hipMemcpy2D(ks, S * seq_len, e->ks, S * e->max_seq,
+                       S * seq_len, rows, hipMemcpyDeviceToHost));
+    TZ_HIP(hipMemcpy2D(vs, S * seq_len, e->vs, S * e->max_seq,
+                       S * seq_len, rows, hipMemcpyDeviceToHost));
     return TENZO_SUCCESS;
 }
 

@@ -82,9 +82,14 @@ def _ptr(a):
 class Engine:
     """One device-resident decode engine."""
 
-    def __init__(self, cfg: synth.DecodeConfig | Config):
+    def __init__(self, cfg: synth.DecodeConfig | Config, kv_mode: str | None = None):
+        """kv_mode: "int8_fused" (default), "tl1_fused" or "popcount_fused"."""
         self.L = lib()
         self.cfg = cfg if isinstance(cfg, Config) else config_from(cfg)
+        if kv_mode is not None:
+            self._kv_mode = kv_mode.encode()  # the config borrows the string
+            self.cfg.kv_mode = self._kv_mode
+        self.kv_mode = (self.cfg.kv_mode or b"int8_fused").decode()
         self.h = self.L.tenzo_create_engine(ctypes.byref(self.cfg))
         if not self.h:
             raise RuntimeError("tenzo_create_engine failed: " +
@@ -145,6 +150,13 @@ class Engine:
 
     def set_kv_from(self, sm: synth.SynthModel):
         n = sm.ctx
+        if self.kv_mode != "int8_fused":
+            if n:
+                raise ValueError("the synthetic model's cache is INT8; use set_kv for "
+                                 f"{self.kv_mode}")
+            self.set_kv(np.zeros(1, np.uint8), np.zeros(1, np.uint8), np.zeros(1, np.float32),
+                        np.zeros(1, np.float32), 0)
+            return
         kc = np.ascontiguousarray(sm.kc[:, :, :n])
         vc = np.ascontiguousarray(sm.vc[:, :, :n])
         ks = np.ascontiguousarray(sm.ks[:, :, :n].astype(np.float16)).view(np.uint16)
@@ -152,7 +164,8 @@ class Engine:
         self.set_kv(kc, vc, ks, vs, n)
 
     def set_kv(self, kc, vc, ks, vs, seq_len: int):
-        """Host arrays [L][Hkv][seq_len][128] int8 and [L][Hkv][seq_len] fp16 bits."""
+        """Host arrays [L][Hkv][seq_len][128] int8 and [L][Hkv][seq_len] fp16 bits
+        (int8_fused), or [L][Hkv][seq_len][32] uint8 and fp32 (ternary modes)."""
         self._check(self.L.tenzo_hip_engine_set_kv(self.h, _ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs),
                                                    seq_len, 0), "engine_set_kv")
 
@@ -161,8 +174,18 @@ class Engine:
                                                    seq_len, 1), "engine_set_kv")
 
     def get_kv(self, seq_len: int):
+        """int8_fused: codes [L][Hkv][n][128] int8 and fp32 (from fp16) scales;
+        ternary modes: rows [L][Hkv][n][32] uint8 and fp32 scales."""
         c = self.cfg
         shape = (c.num_layers, c.num_kv_heads, seq_len)
+        if self.kv_mode != "int8_fused":
+            kb = np.empty(shape + (32,), np.uint8)
+            vb = np.empty_like(kb)
+            ks = np.empty(shape, np.float32)
+            vs = np.empty_like(ks)
+            self._check(self.L.tenzo_hip_engine_get_kv(self.h, _ptr(kb), _ptr(vb), _ptr(ks),
+                                                       _ptr(vs), seq_len), "engine_get_kv")
+            return kb, vb, ks, vs
         kc = np.empty(shape + (128,), np.int8)
         vc = np.empty_like(kc)
         ks = np.empty(shape, np.uint16)

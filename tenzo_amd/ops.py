@@ -164,6 +164,30 @@ def attn_int8_decode(q, k_new, v_new, kc, vc, ks, vs, rope_cs, pos: int, want_ro
     return (out, q_rot, k_rot) if want_rot else out
 
 
+KV_TERN_MODES = {"tl1_fused": 1, "popcount_fused": 2}
+
+
+def attn_tern_decode(mode, q, k_new, v_new, kb, vb, ks, vs, rope_cs, pos: int, want_rot=False):
+    """forward_attention_raw in a ternary KV mode ("tl1_fused" / "popcount_fused",
+    or 1 / 2) for B sequences at position pos.
+
+    kb/vb [B][Hkv][max_seq][32] uint8 rows and ks/vs [B][Hkv][max_seq] fp32
+    (updated in place at pos); the rest as attn_int8_decode."""
+    mode = KV_TERN_MODES.get(mode, mode)
+    B, Hkv, max_seq, R = kb.shape
+    assert R == 32 and kb.dtype == torch.uint8 and ks.dtype == torch.float32
+    D = 128
+    Hq = q.numel() // (B * D)
+    out = torch.empty((B, Hq * D), dtype=torch.float32, device=q.device)
+    q_rot = torch.empty_like(out) if want_rot else None
+    k_rot = torch.empty((B, Hkv * D), dtype=torch.float32, device=q.device) if want_rot else None
+    _lib.check(_lib.load().tenzo_hip_attn_tern_decode(
+        int(mode), _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(kb), _ptr(vb), _ptr(ks), _ptr(vs),
+        _ptr(rope_cs), B, Hq, Hkv, max_seq, pos, _ptr(out), _ptr(q_rot), _ptr(k_rot), _stream()),
+        "attn_tern_decode")
+    return (out, q_rot, k_rot) if want_rot else out
+
+
 # -------------------------------------------------------- quantized GEMV ---
 
 def gemv_q4_0(act: torch.Tensor, w: torch.Tensor, K: int, N: int) -> torch.Tensor:

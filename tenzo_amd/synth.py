@@ -165,3 +165,31 @@ def make_model(cfg: DecodeConfig, seed: int = 2, ctx: int = 0) -> SynthModel:
             arr_c[:, :, :ctx] = c
             arr_s[:, :, :ctx] = f16_round(s)
     return SynthModel(cfg, layers, final_norm, embed, embed_scales, kc, vc, ks, vs, ctx)
+
+
+def tern_kv(cfg: DecodeConfig, mode: int, ctx: int, seed: int = 3):
+    """Random ternary KV cache content for ``ctx`` tokens (mode 1 tl1_fused,
+    2 popcount_fused): rows [L][Hkv][max_seq][32] uint8 and fp32 scales
+    [L][Hkv][max_seq]. Each dim is -1 / 0 / +1 with probabilities 0.345 /
+    0.31 / 0.345 (a Gaussian row thresholded at half its mean |x|); scales
+    around the mean |x| above that threshold."""
+    rng = np.random.default_rng(seed)
+    shape = (cfg.n_layers, cfg.n_kv_heads, cfg.max_seq)
+    rows = {}
+    for name in ("k", "v"):
+        w = rng.choice(np.array([-1, 0, 1], np.int8), size=shape[:2] + (ctx, HEAD_DIM),
+                       p=[0.345, 0.31, 0.345])
+        if name == "k" and mode == 2:
+            pos, neg = w > 0, w < 0
+            planes = [np.packbits(m[..., h * 64:(h + 1) * 64], axis=-1, bitorder="little")
+                      for m in (pos, neg) for h in (0, 1)]
+            packed = np.concatenate(planes, axis=-1)  # kp0 | kp1 | kn0 | kn1
+        else:
+            f = (w + 1).astype(np.uint8).reshape(shape[:2] + (ctx, HEAD_DIM // 4, 4))
+            packed = f[..., 0] | (f[..., 1] << 2) | (f[..., 2] << 4) | (f[..., 3] << 6)
+        full = np.zeros(shape + (32,), np.uint8)
+        full[:, :, :ctx] = packed
+        sc = np.zeros(shape, np.float32)
+        sc[:, :, :ctx] = rng.uniform(0.9, 1.5, size=shape[:2] + (ctx,)).astype(np.float32)
+        rows[name] = (full, sc)
+    return rows["k"][0], rows["v"][0], rows["k"][1], rows["v"][1]

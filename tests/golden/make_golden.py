@@ -199,6 +199,78 @@ def decode_fixture():
     save("decode_tiny", **arrays)
 
 
+TERN_ATT = dict(Hq=8, Hkv=2, max_seq=96, pos=70)
+
+
+def attention_tern_fixture():
+    """FusedKVCache::forward_attention_raw in the ternary modes (1 tl1_fused,
+    2 popcount_fused): the compiled reference on a random cache."""
+    Hq, Hkv, S, pos = TERN_ATT["Hq"], TERN_ATT["Hkv"], TERN_ATT["max_seq"], TERN_ATT["pos"]
+    cfg = synth.DecodeConfig(hidden=Hq * 128, n_q_heads=Hq, n_kv_heads=Hkv, n_layers=1, ffn=64,
+                             vocab=64, max_seq=S, theta=10000.0)
+    R = oracle.ref()
+    out = {}
+    for mode in (1, 2):
+        kb, vb, ks, vs = (a[0] for a in synth.tern_kv(cfg, mode, pos, seed=20 + mode))
+        rng = np.random.default_rng(30 + mode)
+        q = rng.standard_normal(Hq * 128).astype(np.float32)
+        k = (2 * rng.standard_normal(Hkv * 128)).astype(np.float32)
+        v = rng.standard_normal(Hkv * 128).astype(np.float32)
+        res = np.zeros(Hq * 128, np.float32)
+        rk, rv, rks, rvs = kb.copy(), vb.copy(), ks.copy(), vs.copy()
+        R.ref_attention_tern(mode, Hq, Hkv, S, pos, P(q.copy()), P(k.copy()), P(v), P(rk), P(rv),
+                             P(rks), P(rvs), P(res))
+        out.update({f"m{mode}_{n}": a for n, a in dict(
+            q=q, k=k, v=v, kb=kb, vb=vb, ks=ks, vs=vs, out=res, kb_out=rk[:, :pos + 1],
+            vb_out=rv[:, :pos + 1], ks_out=rks[:, :pos + 1], vs_out=rvs[:, :pos + 1]).items()})
+    save("attention_tern", **out)
+
+
+def run_ref_engine_tern(sm, mode, tokens):
+    """Greedy steps of the compiled reference engine with kv_mode tl1_fused (1) /
+    popcount_fused (2), from an empty cache."""
+    R = oracle.ref()
+    c = sm.cfg
+    e = R.ref_engine_create_mode(c.hidden, c.n_q_heads, c.n_kv_heads, c.n_layers, c.ffn, c.vocab,
+                                 c.max_seq, mode)
+    keep = [layer_struct(sm, l) for l in range(c.n_layers)]
+    for l, w in enumerate(keep):
+        assert R.ref_engine_set_layer(e, l, ctypes.byref(w)) == 0
+    assert R.ref_engine_set_head(e, P(sm.embed), P(sm.embed_scales), P(sm.final_norm), c.vocab,
+                                 c.hidden) == 0
+    logits, hidden, out_tok = [], [], []
+    for t in tokens:
+        lg = np.empty(c.vocab, np.float32)
+        tok = R.ref_engine_step(e, int(t), P(lg))
+        h = np.empty(c.hidden, np.float32)
+        R.ref_engine_hidden(e, P(h))
+        logits.append(lg)
+        hidden.append(h)
+        out_tok.append(tok)
+    shape = (c.n_layers, c.n_kv_heads, c.max_seq)
+    kb, vb = np.empty(shape + (32,), np.uint8), np.empty(shape + (32,), np.uint8)
+    ks, vs = np.empty(shape, np.float32), np.empty(shape, np.float32)
+    R.ref_engine_get_kv_tern(e, mode, P(kb), P(vb), P(ks), P(vs))
+    R.ref_engine_destroy(e)
+    n = len(tokens)
+    return (np.array(out_tok), np.stack(logits), np.stack(hidden),
+            (kb[:, :, :n], vb[:, :, :n], ks[:, :, :n], vs[:, :, :n]))
+
+
+def decode_tern_fixture():
+    """The decode_tiny model run by the reference engine in each ternary mode."""
+    z = np.load(os.path.join(OUT, "decode_tiny.npz"))
+    sm = load_tiny_model(z)
+    tokens = np.array([7, 300, 42, 5, 99, 11, 250, 3], np.int64)
+    out = {"tokens": tokens}
+    for mode in (1, 2):
+        tok, logits, hidden, (kb, vb, ks, vs) = run_ref_engine_tern(sm, mode, tokens)
+        out.update({f"m{mode}_out_tokens": tok, f"m{mode}_logits": logits,
+                    f"m{mode}_hidden": hidden, f"m{mode}_kb": kb, f"m{mode}_vb": vb,
+                    f"m{mode}_ks": ks, f"m{mode}_vs": vs})
+    save("decode_tern", **out)
+
+
 def load_tiny_model(z) -> synth.SynthModel:
     """Rebuilds the decode fixture's model from its stored arrays."""
     layers = []
@@ -221,3 +293,5 @@ if __name__ == "__main__":
     attention_fixture()
     quant_gemv_fixture()
     decode_fixture()
+    attention_tern_fixture()
+    decode_tern_fixture()
