@@ -50,6 +50,10 @@ def parse():
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="engine execution mode (one persistent kernel per token, or one "
                          "kernel per stage replayed from a HIP graph / launched eagerly)")
+    ap.add_argument("--kv-mode", default="int8_fused",
+                    choices=["int8_fused", "tl1_fused", "popcount_fused"],
+                    help="KV cache mode; the ternary modes print their own JSON line (decode on "
+                         "the graph path and the ternary attention kernel's roofline)")
     ap.add_argument("--prefill", type=int, default=0, metavar="N",
                     help="instead of the decode benchmark: prefill an N-token prompt with "
                          "tenzo_hip_engine_prefill (--steps timed prompts) beside the "
@@ -89,12 +93,28 @@ def tl1_random_dev(torch, n_bytes, gen):
     return (nib[0] | (nib[1] << 4)).contiguous()
 
 
-def build_model(torch, cfg, ctx):
+def tern_rows_dev(torch, shape, planes, gen):
+    """Random ternary cache rows (P(-1) = P(+1) = 0.345, P(0) = 0.31) packed on
+    the GPU: 2-bit fields (w + 1) four to a byte, or sign bitplanes
+    {kp0, kp1, kn0, kn1} when planes."""
+    u = torch.rand(shape + (128,), device="cuda", generator=gen)
+    w = (u > 0.345).to(torch.int16) + (u > 0.655).to(torch.int16) - 1
+    if planes:
+        bit = (2 ** torch.arange(8, device="cuda", dtype=torch.int16))
+        pos = ((w > 0).to(torch.int16).reshape(shape + (16, 8)) * bit).sum(-1)
+        neg = ((w < 0).to(torch.int16).reshape(shape + (16, 8)) * bit).sum(-1)
+        return torch.cat([pos, neg], dim=-1).to(torch.uint8).contiguous()
+    f = (w + 1).reshape(shape + (32, 4))
+    return (f[..., 0] | (f[..., 1] << 2) | (f[..., 2] << 4) | (f[..., 3] << 6)).to(
+        torch.uint8).contiguous()
+
+
+def build_model(torch, cfg, ctx, kv_mode="int8_fused"):
     from tenzo_amd import engine, synth
     gen = torch.Generator(device="cuda")
     gen.manual_seed(SEED)
     rng = np.random.default_rng(SEED)
-    e = engine.Engine(cfg)
+    e = engine.Engine(cfg, kv_mode=kv_mode)
     host = {"layers": []}
     for l in range(cfg.n_layers):
         tl1 = {p: tl1_random_dev(torch, n * k // 4, gen)
@@ -126,8 +146,19 @@ def build_model(torch, cfg, ctx):
         hs[r0:r0 + E.shape[0]] = s
     e._check(e.L.tenzo_set_lm_head_i8(e.h, head.data_ptr(), hs.data_ptr(), V, H),
              "set_lm_head_i8")
-    # INT8 KV cache: ctx tokens of N(0,1) per (layer, kv head), quantized per token
     L, Hkv = cfg.n_layers, cfg.n_kv_heads
+    if kv_mode != "int8_fused":
+        kb = tern_rows_dev(torch, (L, Hkv, ctx), kv_mode == "popcount_fused", gen)
+        vb = tern_rows_dev(torch, (L, Hkv, ctx), False, gen)
+        ks = torch.rand((L, Hkv, ctx), device="cuda", generator=gen) * 0.6 + 0.9
+        vs = torch.rand((L, Hkv, ctx), device="cuda", generator=gen) * 0.6 + 0.9
+        if ctx > 0:
+            e.set_kv_device(kb.data_ptr(), vb.data_ptr(), ks.data_ptr(), vs.data_ptr(), ctx)
+        e.set_rope_theta(cfg.theta)
+        torch.cuda.synchronize()
+        host.update(final_norm=final_norm, head=head, hs=hs, kc=kb, vc=vb, ks=ks, vs=vs)
+        return e, host
+    # INT8 KV cache: ctx tokens of N(0,1) per (layer, kv head), quantized per token
     kc = torch.empty((L, Hkv, ctx, 128), dtype=torch.int8, device="cuda")
     vc = torch.empty_like(kc)
     ks = torch.empty((L, Hkv, ctx), dtype=torch.float16, device="cuda")
@@ -352,6 +383,83 @@ def prefill_bench(torch, e, cfg, host, args):
     print(json.dumps(out), flush=True)
 
 
+TERN_ROW_BYTES = 32 + 32 + 4 + 4  # K row, V row, two fp32 scales per (kv head, token)
+
+
+def tern_bench(torch, e, cfg, host, args):
+    """Decode with a ternary KV cache (graph path: the persistent kernel is
+    INT8-only) and the ternary attention op at one layer's shape."""
+    from tenzo_amd import ops
+    ctx, mode = args.ctx, args.kv_mode
+    tok = 1
+    e.rewind(ctx)
+    e.decode(tok, max(args.warmup, 1))
+    e.rewind(ctx)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e.decode(tok, args.steps)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    # the attention op over layer 0's cache at position ctx (one kv append +
+    # attention + chunk merge per call), replayed from a graph
+    Hq, Hkv = cfg.n_q_heads, cfg.n_kv_heads
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 1)
+    S = ctx + 1
+    kb = torch.zeros((1, Hkv, S, 32), dtype=torch.uint8, device="cuda")
+    vb = torch.zeros_like(kb)
+    ks = torch.zeros((1, Hkv, S), dtype=torch.float32, device="cuda")
+    vs = torch.zeros_like(ks)
+    kb[0, :, :ctx] = host["kc"][0]
+    vb[0, :, :ctx] = host["vc"][0]
+    ks[0, :, :ctx] = host["ks"][0]
+    vs[0, :, :ctx] = host["vs"][0]
+    q = torch.randn((1, Hq * 128), device="cuda", generator=gen)
+    k = torch.randn((1, Hkv * 128), device="cuda", generator=gen)
+    v = torch.randn((1, Hkv * 128), device="cuda", generator=gen)
+    cs = ops.rope_table(cfg.theta, ctx, 1)[0].cuda()
+    att_s = graph_time(torch, lambda: ops.attn_tern_decode(mode, q, k, v, kb, vb, ks, vs, cs,
+                                                           ctx), 200)
+    att_bytes = Hkv * S * TERN_ROW_BYTES + (2 * Hq + 2 * Hkv) * 128 * 4
+    gbs = att_bytes / att_s / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+        if oracle.ref_available():
+            P = oracle._ptr
+            m = 1 if mode == "tl1_fused" else 2
+            hk = [t.cpu().numpy()[0].copy() for t in (kb, vb, ks, vs)]
+            qh, kh, vh = (t.cpu().numpy()[0] for t in (q, k, v))
+            out = np.zeros(Hq * 128, np.float32)
+            R = oracle.ref()
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or n < 3:
+                R.ref_attention_tern(m, Hq, Hkv, S, ctx, P(qh.copy()), P(kh.copy()), P(vh),
+                                     *(P(a) for a in hk), P(out))
+                n += 1
+            cpu = {"value": round(n / (time.perf_counter() - t0), 2), "unit": "attention calls/s",
+                   "cores": R.ref_num_threads(), "kind": "reference",
+                   "sample": f"FusedKVCache::forward_attention_raw ({mode}), one layer, "
+                             f"Hq {Hq} Hkv {Hkv}, position {ctx}, {n} calls"}
+    out = {
+        "metric": f"decode tok/s BitNet-2B-shape bs=1 ctx {ctx}, {mode} KV",
+        "value": round(args.steps / dt, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "ternary KV (int32 dot, fp32 softmax)", "data": "synthetic",
+        "config": {"workload": f"BitNet-b1.58-2B-shaped greedy decode step, batch 1, context "
+                               f"{ctx}, {mode} KV cache (graph path)", "engine_mode": e.mode},
+        "roofline": {"bound": "hbm", "kernel": "attn_tern_chunk_kernel + attn_combine_kernel",
+                     "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
+                     "alg_bytes_per_launch": int(att_bytes),
+                     "mean_launch_us": round(att_s * 1e6, 2)},
+        "gpu_attention_calls_per_s": round(1.0 / att_s, 1),
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 # ------------------------------------------------------------------- main
 
 def main():
@@ -366,7 +474,15 @@ def main():
         raise SystemExit("bench.py needs a GPU (the decode path has no CPU fallback)")
     cfg = synth.BITNET_2B
     ctx = 0 if args.prefill else args.ctx
-    e, host = build_model(torch, cfg, ctx)
+    tern = args.kv_mode != "int8_fused"
+    if tern and args.prefill:
+        raise SystemExit("--prefill runs the int8_fused cache")
+    e, host = build_model(torch, cfg, ctx, args.kv_mode)
+    if tern:
+        e.set_mode("graph")
+        tern_bench(torch, e, cfg, host, args)
+        e.close()
+        return
     if args.prefill:
         prefill_bench(torch, e, cfg, host, args)
         e.close()

@@ -324,21 +324,52 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     }
 }
 
-// Merge of the chunk partials; one 128-thread block per (query head, sequence).
+// Merge of the chunk partials; one 128-thread block per (query head, sequence):
+//   M = max_c m_c,  L = sum_c e^{m_c - M} l_c,  o = sum_c e^{m_c - M} o_c,
+// summed in chunk order with one fma per term. The chunks' (m, l) are staged
+// in LDS by the whole block and each thread's o_c loads are issued kMergeU at
+// a time, so the loop waits for memory once per kMergeU chunks instead of once
+// per chunk; the arithmetic (and so the result) is that of the plain loop.
+constexpr int kMergeLds = 1024;  // chunks staged in LDS (contexts of 32K at 32-token chunks)
+constexpr int kMergeU = 16;
+
 __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
+    __shared__ float ms[kMergeLds], ls[kMergeLds];
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + (a.prefill ? b : 0);
     const int T = a.prefill ? pick_chunk(pos + 1, a.Hkv, 1) : a.T;
     const int nchunks = (pos + 1 + T - 1) / T;
     if (nchunks == 1) return;  // the chunk kernel wrote the output
     const float* pp = a.part + ((int64_t)b * a.Hq + qh) * a.max_chunks * kPartStride;
-    float M = -1e30f;
-    for (int c = 0; c < nchunks; ++c) M = fmaxf(M, pp[c * kPartStride]);
-    float L = 0.0f, o = 0.0f;
-    for (int c = 0; c < nchunks; ++c) {
-        const float e = expf(pp[c * kPartStride] - M);
-        L = __builtin_fmaf(e, pp[c * kPartStride + 1], L);
-        o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
+    float M = -1e30f, L = 0.0f, o = 0.0f;
+    if (nchunks > kMergeLds) {
+        for (int c = 0; c < nchunks; ++c) M = fmaxf(M, pp[c * kPartStride]);
+        for (int c = 0; c < nchunks; ++c) {
+            const float e = expf(pp[c * kPartStride] - M);
+            L = __builtin_fmaf(e, pp[c * kPartStride + 1], L);
+            o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
+        }
+    } else {
+        for (int c = d; c < nchunks; c += 128) {
+            ms[c] = pp[c * kPartStride];
+            ls[c] = pp[c * kPartStride + 1];
+        }
+        __syncthreads();
+        for (int c = 0; c < nchunks; ++c) M = fmaxf(M, ms[c]);
+        for (int c0 = 0; c0 < nchunks; c0 += kMergeU) {
+            float ov[kMergeU];
+#pragma unroll
+            for (int u = 0; u < kMergeU; ++u)
+                ov[u] = c0 + u < nchunks ? pp[(c0 + u) * kPartStride + 2 + d] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < kMergeU; ++u) {
+                if (c0 + u < nchunks) {
+                    const float e = expf(ms[c0 + u] - M);
+                    L = __builtin_fmaf(e, ls[c0 + u], L);
+                    o = __builtin_fmaf(e, ov[u], o);
+                }
+            }
+        }
     }
     a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, L);
 }
