@@ -40,6 +40,16 @@
  *   orc_decode_step                  compiled reference whole-engine step on small
  *                                    configs (logits 1e-3, greedy token equal)
  *   orc_argmax                       brute force (first maximum)
+ *   orc_tern_stats, orc_tern_pack,
+ *   orc_tern_bitplanes,
+ *   orc_attention_step_tern          compiled reference (bit-exact rows and scales,
+ *                                    outputs 1e-5; fixture and live) + special rows
+ *                                    (zero, constant magnitude, one spike) + a check
+ *                                    that index-order sums give other scales
+ *                                    (tests/test_kv_tern.py)
+ *   orc_attn_tern                    closed forms: seq_len 1 (out = w_v s_v, fields
+ *                                    3 read 0) and two tokens (out = tanh(score/2)
+ *                                    with a brute-force integer dot)
  *   orc_quant_rows_i8                the compiled reference's loader output (its
  *                                    int8 LM head and row scales, bit-exact) on
  *                                    synthetic model files

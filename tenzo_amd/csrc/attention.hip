@@ -327,14 +327,15 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
 // Merge of the chunk partials; one 128-thread block per (query head, sequence):
 //   M = max_c m_c,  L = sum_c e^{m_c - M} l_c,  o = sum_c e^{m_c - M} o_c,
 // summed in chunk order with one fma per term. The chunks' (m, l) are staged
-// in LDS by the whole block and each thread's o_c loads are issued kMergeU at
-// a time, so the loop waits for memory once per kMergeU chunks instead of once
-// per chunk; the arithmetic (and so the result) is that of the plain loop.
+// in LDS by the whole block, each chunk's weight e^{m_c - M} is evaluated once
+// into LDS, and each thread's o_c loads are issued kMergeU at a time, so the
+// loop waits for memory once per kMergeU chunks instead of once per chunk; the
+// arithmetic (and so the result) is that of the plain loop.
 constexpr int kMergeLds = 1024;  // chunks staged in LDS (contexts of 32K at 32-token chunks)
-constexpr int kMergeU = 16;
+constexpr int kMergeU = 32;
 
 __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
-    __shared__ float ms[kMergeLds], ls[kMergeLds];
+    __shared__ float ms[kMergeLds], ls[kMergeLds], es[kMergeLds];
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + (a.prefill ? b : 0);
     const int T = a.prefill ? pick_chunk(pos + 1, a.Hkv, 1) : a.T;
@@ -356,6 +357,10 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
         }
         __syncthreads();
         for (int c = 0; c < nchunks; ++c) M = fmaxf(M, ms[c]);
+        // each chunk's weight e^{m_c - M} once per block (the same expf the
+        // plain loop evaluates in every thread)
+        for (int c = d; c < nchunks; c += 128) es[c] = expf(ms[c] - M);
+        __syncthreads();
         for (int c0 = 0; c0 < nchunks; c0 += kMergeU) {
             float ov[kMergeU];
 #pragma unroll
@@ -364,7 +369,7 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
 #pragma unroll
             for (int u = 0; u < kMergeU; ++u) {
                 if (c0 + u < nchunks) {
-                    const float e = expf(ms[c0 + u] - M);
+                    const float e = es[c0 + u];
                     L = __builtin_fmaf(e, ls[c0 + u], L);
                     o = __builtin_fmaf(e, ov[u], o);
                 }
