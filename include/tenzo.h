@@ -7,10 +7,10 @@
  * (src/main_inference.cpp, examples/basic_inference.cpp) link against this
  * library unchanged. Differences, by design:
  *   - the decode step runs on the GPU whatever `device` says (this library
- *     has no CPU path); `kv_mode` is "int8_fused" (or NULL), "tl1_fused" or
- *     "popcount_fused" (the reference's fp32 fallback for other strings and
- *     its paged mode are not provided: create returns NULL); the ternary
- *     modes run the graph path and fill the cache token by token in
+ *     has no CPU path); `kv_mode` is "int8_fused" (or NULL), "tl1_fused",
+ *     "popcount_fused" or "paged_int8" (the reference's fp32 fallback for
+ *     other strings is not provided: create returns NULL); the modes other
+ *     than int8_fused run the graph path and fill the cache token by token in
  *     tenzo_hip_engine_prefill;
  *   - weights are copied to device memory when they are set, so the caller may
  *     free its copies afterwards (the reference keeps non-owning pointers to
@@ -74,7 +74,7 @@ typedef struct {
     int ffn_dim;         /* 6912 */
     int vocab_size;      /* 128256 */
     int max_seq_len;     /* 8192 */
-    const char* kv_mode; /* "int8_fused", "tl1_fused", "popcount_fused" */
+    const char* kv_mode; /* "int8_fused", "tl1_fused", "popcount_fused", "paged_int8" */
     const char* device;  /* ignored: always the GPU */
 } tenzo_config_t;
 

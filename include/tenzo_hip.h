@@ -145,6 +145,23 @@ TENZO_HIP_API int tenzo_hip_attn_tern_decode(int mode, const float* q, const flo
                                              int Hq, int Hkv, int max_seq, int pos, float* out,
                                              float* q_rot, float* k_rot, void* stream);
 
+/* ---- paged_int8 decode attention ----------------------------------------- */
+
+/* One decode step of PagedKVCache::forward_attention_raw (TenzoEngine.cpp:269-445)
+ * for one layer of a block pool: codes pk / pv [blocks][n_layers][Hkv][16][128]
+ * int8, fp32 scales pks / pvs [blocks][n_layers][Hkv][16]; block_table[t / 16]
+ * is the physical block of token t and must already hold the block of pos (the
+ * reference allocates it on reaching a new block, :318-324). q / k_new / v_new
+ * as tenzo_hip_attn_int8_decode (batch 1); the new row is quantized like
+ * int8_fused with an fp32 scale; softmax 1 / (sum + 1e-8); tokens with weight
+ * below 1e-7 add no value. */
+TENZO_HIP_API int tenzo_hip_attn_paged_int8_decode(const float* q, const float* k_new,
+                                                   const float* v_new, int8_t* pk, int8_t* pv,
+                                                   float* pks, float* pvs,
+                                                   const int32_t* block_table, int n_layers,
+                                                   int layer, const float* rope_cs, int Hq,
+                                                   int Hkv, int pos, float* out, void* stream);
+
 /* HOST function: fills cs[pos - pos0][0..127] = cos/sin table rows for
  * positions pos0 .. pos0+n_pos-1 with the reference's RoPE angles
  * (TenzoEngine.cpp:465-469; theta is 10000 there and a parameter here). */
@@ -271,7 +288,9 @@ TENZO_HIP_API int tenzo_hip_engine_prefill(struct tenzo_engine_opaque* e, const 
  * pointers are device memory when is_device, else host. Layout by kv_mode:
  * int8_fused codes [L][Hkv][seq_len][128] int8 and fp16 scales [L][Hkv][seq_len];
  * tl1_fused / popcount_fused rows [L][Hkv][seq_len][32] bytes (the layouts of
- * tenzo_hip_attn_tern_decode) and fp32 scales [L][Hkv][seq_len]. Mirrors
+ * tenzo_hip_attn_tern_decode) and fp32 scales [L][Hkv][seq_len]; paged_int8 the
+ * int8_fused codes with fp32 scales, scattered into fresh blocks (the block
+ * manager is reset first) and gathered back in block-table order. Mirrors
  * writing the public FusedKVCache state (TenzoEngine.h:60-115). */
 TENZO_HIP_API int tenzo_hip_engine_set_kv(struct tenzo_engine_opaque* e, const void* kc,
                                           const void* vc, const void* ks, const void* vs,
@@ -284,6 +303,10 @@ TENZO_HIP_API int tenzo_hip_engine_get_kv(struct tenzo_engine_opaque* e, void* k
  * decode repeatedly at one position. No reference counterpart (the reference
  * only resets to 0, TenzoEngine.cpp:1249-1255). */
 TENZO_HIP_API int tenzo_hip_engine_set_seq_len(struct tenzo_engine_opaque* e, int seq_len);
+/* paged_int8 engines: copies up to cap entries of the sequence's block table
+ * (PagedKVCache::block_table, TenzoEngine.h:160) and returns its length. */
+TENZO_HIP_API int tenzo_hip_engine_block_table(struct tenzo_engine_opaque* e, int32_t* out,
+                                               int cap);
 /* RoPE theta (the reference hard-codes 10000; BitNet-2B uses 500000). */
 TENZO_HIP_API int tenzo_hip_engine_set_rope_theta(struct tenzo_engine_opaque* e, float theta);
 /* Copies the last step's logits (vocab fp32) to host memory. */

@@ -88,6 +88,8 @@ def lib() -> ctypes.CDLL:
             "orc_tern_pack": (None, [_P, _I, _F, _P]),
             "orc_tern_bitplanes": (None, [_P, _F, _P]),
             "orc_attn_tern": (None, [_I, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+            "orc_attention_step_paged": (None, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                                _I, _P, _P]),
             "orc_attention_step_tern": (None, [_I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                                _P, _P]),
         }
@@ -121,6 +123,9 @@ def ref() -> ctypes.CDLL:
             "ref_engine_create_mode": (_P, [_I, _I, _I, _I, _I, _I, _I, _I]),
             "ref_engine_get_kv_tern": (None, [_P, _I, _P, _P, _P, _P]),
             "ref_engine_set_kv_tern": (None, [_P, _I, _P, _P, _P, _P, _I]),
+            "ref_attention_paged": (_I, [_I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         _I, _P]),
+            "ref_engine_get_kv_paged": (_I, [_P, _P, _P, _P, _P, _P]),
             "ref_q4_0": (None, [_P, _P, _P, _I, _I]),
             "ref_q8_0": (None, [_P, _P, _P, _I, _I]),
             "ref_gptq": (None, [_P, _P, _P, _P, _P, _I, _I, _I]),
@@ -325,6 +330,26 @@ def attention_step_tern(mode: int, q, k, v, kb, vb, ks, vs, Hq, Hkv, max_seq, po
     return out, q, k
 
 
+PAGE = 16  # tokens per block of the paged_int8 cache (PagedKVCache::BLOCK_SIZE)
+
+
+def attention_step_paged(q, k, v, pk, pv, pks, pvs, block_table, n_layers, layer, Hq, Hkv, pos,
+                         rope_cs):
+    """PagedKVCache::forward_attention_raw for one layer; pools [blocks][n_layers][Hkv][16][128]
+    int8 and [blocks][n_layers][Hkv][16] fp32 are updated in place."""
+    q = f32(q).copy()
+    k = f32(k).copy()
+    v = f32(v)
+    bt = np.ascontiguousarray(block_table, np.int32)
+    out = np.zeros(Hq * 128, np.float32)
+    for a in (pk, pv, pks, pvs):
+        assert a.flags["C_CONTIGUOUS"]
+    lib().orc_attention_step_paged(_ptr(q), _ptr(k), _ptr(v), _ptr(pk), _ptr(pv), _ptr(pks),
+                                   _ptr(pvs), _ptr(bt), n_layers, layer, Hq, Hkv, pos,
+                                   _ptr(f32(rope_cs)), _ptr(out))
+    return out, q, k
+
+
 def lm_head(xn, W, scales):
     xn = f32(xn)
     W = np.ascontiguousarray(W, np.int8)
@@ -445,7 +470,7 @@ class Model(ctypes.Structure):
         ("final_norm", _P),
         ("embed", _P), ("embed_scales", _P),
         ("kc", _P), ("vc", _P), ("ks", _P), ("vs", _P),
-        ("kv_mode", _I),
+        ("kv_mode", _I), ("block_table", _P),
     ]
 
 
@@ -483,7 +508,11 @@ class OracleModel:
         m.final_norm = _ptr(sm.final_norm)
         m.embed = _ptr(sm.embed)
         m.embed_scales = _ptr(sm.embed_scales)
-        if kv_mode == 0:
+        if kv_mode == 3:  # kv = (pk, pv, pks, pvs, block_table)
+            self.kc, self.vc, self.ks, self.vs = (np.ascontiguousarray(a).copy() for a in kv[:4])
+            self.block_table = np.ascontiguousarray(kv[4], np.int32).copy()
+            m.block_table = _ptr(self.block_table)
+        elif kv_mode == 0:
             self.kc = sm.kc.copy()
             self.vc = sm.vc.copy()
             self.ks = sm.ks.copy()

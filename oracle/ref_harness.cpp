@@ -111,6 +111,46 @@ void ref_attention_tern(int mode, int Hq, int Hkv, int max_seq, int pos, float* 
     std::memcpy(vs, cvs, n_sc);
 }
 
+// PagedKVCache::forward_attention_raw (TenzoEngine.cpp:269-445) on caller-held
+// pools ([total_blocks][n_layers][Hkv][16][128] codes, fp32 scales) and block
+// table (n_bt entries, their blocks taken out of the free list); the call may
+// allocate one block. Pools and table are copied back; returns the table size.
+int ref_attention_paged(int Hq, int Hkv, int n_layers, int layer, int total_blocks, int pos,
+                        float* q, float* k, float* v, int8_t* pk, int8_t* pv, float* pks,
+                        float* pvs, int32_t* block_table, int n_bt, float* out) {
+    tenzo::PagedKVCache c(n_layers, Hq, Hkv, 128, total_blocks);
+    std::memcpy(c.paged_k_pool.data(), pk, c.paged_k_pool.size());
+    std::memcpy(c.paged_v_pool.data(), pv, c.paged_v_pool.size());
+    std::memcpy(c.paged_k_scales.data(), pks, c.paged_k_scales.size() * 4);
+    std::memcpy(c.paged_v_scales.data(), pvs, c.paged_v_scales.size() * 4);
+    c.block_table.assign(block_table, block_table + n_bt);
+    for (int i = 0; i < n_bt; ++i) {
+        auto& f = c.block_mgr.free_blocks;
+        for (size_t j = 0; j < f.size(); ++j)
+            if (f[j] == block_table[i]) { f.erase(f.begin() + j); break; }
+    }
+    c.cur_seq_len = pos;
+    c.forward_attention_raw(layer, q, k, v, out);
+    std::memcpy(pk, c.paged_k_pool.data(), c.paged_k_pool.size());
+    std::memcpy(pv, c.paged_v_pool.data(), c.paged_v_pool.size());
+    std::memcpy(pks, c.paged_k_scales.data(), c.paged_k_scales.size() * 4);
+    std::memcpy(pvs, c.paged_v_scales.data(), c.paged_v_scales.size() * 4);
+    for (size_t i = 0; i < c.block_table.size(); ++i) block_table[i] = c.block_table[i];
+    return (int)c.block_table.size();
+}
+
+// The paged pools and block table of an engine created with kv_mode paged_int8.
+int ref_engine_get_kv_paged(void* e, int8_t* pk, int8_t* pv, float* pks, float* pvs,
+                            int32_t* block_table) {
+    tenzo::PagedKVCache& c = static_cast<tenzo_engine_t>(e)->impl->paged_kv_cache;
+    std::memcpy(pk, c.paged_k_pool.data(), c.paged_k_pool.size());
+    std::memcpy(pv, c.paged_v_pool.data(), c.paged_v_pool.size());
+    std::memcpy(pks, c.paged_k_scales.data(), c.paged_k_scales.size() * 4);
+    std::memcpy(pvs, c.paged_v_scales.data(), c.paged_v_scales.size() * 4);
+    for (size_t i = 0; i < c.block_table.size(); ++i) block_table[i] = c.block_table[i];
+    return (int)c.block_table.size();
+}
+
 // Quantized GEMV free functions (TenzoEngine.cpp:1022-1175).
 void ref_q4_0(const float* a, const uint8_t* w, float* y, int K, int N) {
     tenzo::compute_linear_gguf_q4_0(a, w, y, K, N);
@@ -140,7 +180,8 @@ void* ref_engine_create_mode(int H, int Hq, int Hkv, int L, int F, int V, int ma
     cfg.ffn_dim = F;
     cfg.vocab_size = V;
     cfg.max_seq_len = max_seq;
-    cfg.kv_mode = mode == 1 ? "tl1_fused" : mode == 2 ? "popcount_fused" : "int8_fused";
+    cfg.kv_mode = mode == 1 ? "tl1_fused" : mode == 2 ? "popcount_fused"
+                : mode == 3 ? "paged_int8" : "int8_fused";
     cfg.device = "cpu";
     return tenzo_create_engine(&cfg);
 }

@@ -512,6 +512,72 @@ void orc_attention_step_tern(int mode, float* q, float* k, const float* v, uint8
 }
 
 /* ------------------------------------------------------------------------- */
+/* paged_int8 (PagedKVCache, :218-445): pools [blocks][L][Hkv][16][128] int8,  */
+/* fp32 scales [blocks][L][Hkv][16], a block table per sequence.               */
+/* ------------------------------------------------------------------------- */
+
+static size_t paged_row(int blk, int n_layers, int layer, int Hkv, int h) {
+    return ((size_t)blk * n_layers + layer) * Hkv + h;  /* then x 16 slots */
+}
+
+void orc_attention_step_paged(float* q, float* k, const float* v, int8_t* pk, int8_t* pv,
+                              float* pks, float* pvs, const int32_t* block_table, int n_layers,
+                              int layer, int Hq, int Hkv, int pos, const float* rope_cs,
+                              float* out) {
+    const int D = 128, BS = 16;
+    orc_rope_apply(q, Hq, D, rope_cs);                        /* :271-292 */
+    orc_rope_apply(k, Hkv, D, rope_cs);                       /* :294-315 */
+    const int lb = pos / BS, slot = pos % BS;                 /* :318-326 */
+    const int phys = block_table[lb];
+    for (int h = 0; h < Hkv; ++h) {                           /* :328-352: the int8_fused quantizer */
+        const size_t r = paged_row(phys, n_layers, layer, Hkv, h) * BS + slot;
+        pks[r] = orc_kv_quant(k + h * D, D, pk + r * D);
+        pvs[r] = orc_kv_quant(v + h * D, D, pv + r * D);
+    }
+    const int total = pos + 1;                                /* :355-445 */
+    const int gqa = Hq / Hkv;
+    const float qk_scale = 1.0f / sqrtf((float)D);
+    float* scores = (float*)malloc((size_t)total * 4);
+    for (int qh = 0; qh < Hq; ++qh) {
+        const int kvh = qh / gqa;
+        const float* qv = q + qh * D;
+        float max_score = -1e30f;
+        for (int t = 0; t < total; ++t) {                     /* :366-393 */
+            const size_t r = paged_row(block_table[t / BS], n_layers, layer, Hkv, kvh) * BS + t % BS;
+            const int8_t* kr = pk + r * D;
+            float a0[8] = {0}, a1[8] = {0};
+            for (int d = 0; d < D; d += 16)
+                for (int j = 0; j < 8; ++j) {
+                    a0[j] = fmaf(qv[d + j], (float)kr[d + j], a0[j]);
+                    a1[j] = fmaf(qv[d + 8 + j], (float)kr[d + 8 + j], a1[j]);
+                }
+            float dot = 0.0f;
+            for (int j = 0; j < 8; ++j) dot += a0[j] + a1[j];
+            const float score = dot * pks[r] * qk_scale;
+            scores[t] = score;
+            if (score > max_score) max_score = score;
+        }
+        float sum = 0.0f;                                     /* :396-405 */
+        for (int t = 0; t < total; ++t) {
+            scores[t] = expf(scores[t] - max_score);
+            sum += scores[t];
+        }
+        const float inv_sum = 1.0f / (sum + 1e-8f);
+        for (int t = 0; t < total; ++t) scores[t] *= inv_sum;
+        float* o = out + qh * D;                              /* :408-443 */
+        memset(o, 0, D * sizeof(float));
+        for (int t = 0; t < total; ++t) {
+            const float alpha = scores[t];
+            if (alpha < 1e-7f) continue;
+            const size_t r = paged_row(block_table[t / BS], n_layers, layer, Hkv, kvh) * BS + t % BS;
+            const float w = alpha * pvs[r];
+            for (int d = 0; d < D; ++d) o[d] = fmaf(w, (float)pv[r * D + d], o[d]);
+        }
+    }
+    free(scores);
+}
+
+/* ------------------------------------------------------------------------- */
 /* LM head (:1634-1720), argmax (:1745-1755), embedding (:1294-1316)          */
 /* ------------------------------------------------------------------------- */
 
@@ -827,7 +893,11 @@ int orc_decode_step(const orc_model_t* m, int token, int pos, const float* rope_
         orc_tl1_gemv_i32(m->v_w[l], codes, kvd, H, acc);
         for (int i = 0; i < kvd; ++i) v[i] = (float)acc[i] * (inv * sc[2]);
         /* :1578 */
-        if (m->kv_mode == 0)
+        if (m->kv_mode == 3)
+            orc_attention_step_paged(q, k, v, m->kc, m->vc, m->ks, m->vs, m->block_table,
+                                     m->n_layers, l, m->n_q_heads, m->n_kv_heads, pos, rope_cs,
+                                     attn);
+        else if (m->kv_mode == 0)
             orc_attention_step(q, k, v, m->kc + cache_off * D, m->vc + cache_off * D,
                                m->ks + cache_off, m->vs + cache_off, m->n_q_heads,
                                m->n_kv_heads, m->max_seq, pos, rope_cs, m->f16_kv_scales,

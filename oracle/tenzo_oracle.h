@@ -50,6 +50,8 @@
  *   orc_attn_tern                    closed forms: seq_len 1 (out = w_v s_v, fields
  *                                    3 read 0) and two tokens (out = tanh(score/2)
  *                                    with a brute-force integer dot)
+ *   orc_attention_step_paged         compiled reference (bit-exact pool rows and
+ *                                    scales, outputs 1e-5, permuted block tables)
  *   orc_quant_rows_i8                the compiled reference's loader output (its
  *                                    int8 LM head and row scales, bit-exact) on
  *                                    synthetic model files
@@ -138,6 +140,12 @@ void orc_attention_step_tern(int mode, float* q, float* k, const float* v, uint8
                              uint8_t* vb, float* ks, float* vs, int Hq, int Hkv, int max_seq,
                              int pos, const float* rope_cs, float* out);
 
+/* ---- paged_int8 (PagedKVCache::forward_attention_raw :269-445), one layer ---- */
+void orc_attention_step_paged(float* q, float* k, const float* v, int8_t* pk, int8_t* pv,
+                              float* pks, float* pvs, const int32_t* block_table, int n_layers,
+                              int layer, int Hq, int Hkv, int pos, const float* rope_cs,
+                              float* out);
+
 float orc_lm_head(const float* xn, const int8_t* W, const float* scales, int64_t V,
                   int64_t H, float* logits, int8_t* codes);
 int orc_argmax(const float* logits, int64_t V);
@@ -178,7 +186,10 @@ typedef struct {
     /* KV cache state, [n_layers][n_kv_heads][max_seq][128] / [..][max_seq];
      * kv_mode 1 / 2: rows of 32 bytes (see orc_attn_tern), fp32 scales */
     int8_t* kc; int8_t* vc; float* ks; float* vs;
-    int kv_mode;          /* 0 int8_fused, 1 tl1_fused, 2 popcount_fused */
+    int kv_mode;          /* 0 int8_fused, 1 tl1_fused, 2 popcount_fused, 3 paged_int8 */
+    /* paged_int8: kc / vc are the pools [blocks][n_layers][Hkv][16][128], ks / vs
+     * their fp32 scales, block_table maps logical to physical blocks */
+    const int32_t* block_table;
 } orc_model_t;
 
 /* Runs one token through all layers at position pos (appending to the cache),

@@ -63,6 +63,33 @@ struct AttnTernLaunch {
 };
 int launch_attn_tern(const AttnTernLaunch& L, hipStream_t st);
 
+// paged_int8 decode attention (attention_paged.hip) over one layer of block
+// pools pk / pv [blocks][n_layers][Hkv][16][128] int8 with fp32 scales pks / pvs
+// [blocks][n_layers][Hkv][16]; block_table[t / 16] is the physical block of
+// token t (the block of pos included). ws: paged_ws_bytes bytes, or null for
+// the library scratch. Batch 1.
+struct AttnPagedLaunch {
+    const float* q = nullptr;
+    const float* k_new = nullptr;
+    const float* v_new = nullptr;
+    int8_t* pk = nullptr;
+    int8_t* pv = nullptr;
+    float* pks = nullptr;
+    float* pvs = nullptr;
+    const int32_t* block_table = nullptr;
+    const float* rope = nullptr;
+    const int* pos_dev = nullptr;
+    int pos = 0;
+    int rope_indexed = 0;
+    int n_layers = 1, layer = 0, Hq = 0, Hkv = 0;
+    int T = 64;
+    int max_chunks = 1;
+    float* ws = nullptr;
+    float* out = nullptr;
+};
+size_t paged_ws_bytes(int Hq, int max_chunks, int T);
+int launch_attn_paged(const AttnPagedLaunch& L, hipStream_t st);
+
 // Attention for n prompt tokens at positions pos0 .. pos0+n-1 over one INT8
 // cache: the k/v rows of all n tokens are RoPE'd, quantized and appended
 // first (as n decode steps would), then query i attends to positions

@@ -83,6 +83,13 @@ struct tenzo_engine_opaque {
     int kv_kind = 0;
     int kv_row = 128;  // bytes per (layer, kv head, token) row
     int kv_sb = 2;     // bytes per scale
+    // paged_int8 (kv_kind 3): kc / vc / ks / vs are block pools
+    // [blocks][L][Hkv][16][...]; the block manager mirrors PagedBlockManager
+    // (TenzoEngine.h:120-152: free list filled high to low, taken from the back)
+    int pg_blocks = 0;
+    std::vector<int32_t> pg_free, pg_table;
+    int32_t* pg_bt = nullptr;  // device copy of pg_table
+    float* pg_ws = nullptr;    // scores, chunk maxima and chunk sums
     int8_t* kc = nullptr;
     int8_t* vc = nullptr;
     uint16_t* ks = nullptr;
@@ -257,7 +264,29 @@ int enqueue_layer(tenzo_engine_t e, int l, int T, int max_chunks) {
                               nullptr, nullptr, st, 0, e->gemv_ws)))
         return rc;
     // 4: RoPE, KV append at the device-held position, attention
-    if (e->kv_kind != 0) {
+    if (e->kv_kind == 3) {
+        AttnPagedLaunch p{};
+        p.q = e->qkv;
+        p.k_new = e->qkv + e->qd;
+        p.v_new = e->qkv + e->qd + e->kvd;
+        p.pk = e->kc;
+        p.pv = e->vc;
+        p.pks = reinterpret_cast<float*>(e->ks);
+        p.pvs = reinterpret_cast<float*>(e->vs);
+        p.block_table = e->pg_bt;
+        p.rope = e->rope;
+        p.rope_indexed = 1;
+        p.pos_dev = e->io_dev + 1;
+        p.n_layers = e->L;
+        p.layer = l;
+        p.Hq = e->Hq;
+        p.Hkv = e->Hkv;
+        p.T = T;
+        p.max_chunks = max_chunks;
+        p.ws = e->pg_ws;
+        p.out = e->attn;
+        if ((rc = launch_attn_paged(p, st))) return rc;
+    } else if (e->kv_kind != 0) {
         const size_t rows = (size_t)l * e->Hkv * e->max_seq;
         AttnTernLaunch t{};
         t.mode = e->kv_kind;
@@ -640,6 +669,34 @@ int enqueue_prefill_layer(tenzo_engine_t e, int l, int pos0, int m, bool exact) 
 // softmax rounding).
 int run_step(tenzo_engine_t e, int token, bool head);
 
+// PagedBlockManager::reset (TenzoEngine.h:127-133) and the table's reset.
+void pg_reset(tenzo_engine_t e) {
+    e->pg_free.clear();
+    for (int i = e->pg_blocks - 1; i >= 0; --i) e->pg_free.push_back(i);
+    e->pg_table.clear();
+}
+
+// Blocks for the first n tokens, allocated as PagedKVCache does on reaching a
+// new block (:318-324: the last free block); the new entries are copied to
+// the device table before anything reads them.
+int pg_ensure(tenzo_engine_t e, int n) {
+    const size_t had = e->pg_table.size();
+    while ((int)e->pg_table.size() * 16 < n) {
+        if (e->pg_free.empty()) {
+            set_error("paged KV: no free block for %d tokens", n);
+            return TENZO_ERROR_OUT_OF_MEMORY;
+        }
+        e->pg_table.push_back(e->pg_free.back());
+        e->pg_free.pop_back();
+    }
+    if (e->pg_table.size() > had) {
+        TZ_HIP(hipMemcpyAsync(e->pg_bt + had, e->pg_table.data() + had,
+                              (e->pg_table.size() - had) * 4, hipMemcpyHostToDevice, e->st));
+        TZ_HIP(hipStreamSynchronize(e->st));
+    }
+    return TENZO_SUCCESS;
+}
+
 int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
     if (!ready(e, false)) return TENZO_ERROR_INVALID_ARGUMENT;
     if (n <= 0 || !tokens) {
@@ -788,6 +845,10 @@ int run_step(tenzo_engine_t e, int token, bool head) {
     TZ_HIP(hipSetDevice(e->dev));
     const int pos = e->seq_len;
     const int T = attn_pick_chunk(pos + 1, e->Hkv, 1);
+    if (e->kv_kind == 3) {
+        const int prc = pg_ensure(e, pos + 1);
+        if (prc) return prc;
+    }
     e->io_host[0] = token;
     e->io_host[1] = pos;
     TZ_HIP(hipMemcpyAsync(e->io_dev, e->io_host, 8, hipMemcpyHostToDevice, e->st));
@@ -861,10 +922,11 @@ TENZO_API void tenzo_destroy_engine(tenzo_engine_t e);
 TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     tenzo_config_t c = config ? *config : tenzo_default_config();
     const std::string kv = c.kv_mode ? c.kv_mode : "int8_fused";
-    const int kv_kind = kv == "int8_fused" ? 0 : kv == "tl1_fused" ? 1 : kv == "popcount_fused" ? 2 : -1;
+    const int kv_kind = kv == "int8_fused" ? 0 : kv == "tl1_fused" ? 1 : kv == "popcount_fused" ? 2
+                        : kv == "paged_int8" ? 3 : -1;
     if (kv_kind < 0) {
         set_error("kv_mode \"%s\" is not provided on the GPU (int8_fused, tl1_fused, "
-                  "popcount_fused)", kv.c_str());
+                  "popcount_fused, paged_int8)", kv.c_str());
         return nullptr;
     }
     const int H = c.hidden_size, Hq = c.num_q_heads, Hkv = c.num_kv_heads;
@@ -885,7 +947,7 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     e->cfg = c;
     e->kv_mode = kv;
     e->kv_kind = kv_kind;
-    e->kv_row = kv_kind == 0 ? kD : 32;
+    e->kv_row = kv_kind == 0 || kv_kind == 3 ? kD : 32;
     e->kv_sb = kv_kind == 0 ? 2 : 4;
     e->device = c.device ? c.device : "rocm";
     e->cfg.kv_mode = e->kv_mode.c_str();
@@ -901,7 +963,9 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     e->kvd = Hkv * kD;
     e->layers.resize(e->L);
     bool ok = hipGetDevice(&e->dev) == hipSuccess && hipStreamCreate(&e->st) == hipSuccess;
-    const size_t cache = (size_t)e->L * Hkv * e->max_seq;
+    // paged_int8: the reference sizes its pool at ceil(max_seq / 16) blocks (:1218)
+    e->pg_blocks = kv_kind == 3 ? (int)ceil_div(e->max_seq, 16) : 0;
+    const size_t cache = (size_t)e->L * Hkv * (kv_kind == 3 ? (size_t)e->pg_blocks * 16 : e->max_seq);
     const int Tmin = 32;
     const size_t parts = (size_t)Hq * ceil_div(e->max_seq, Tmin) * kPartStride * 4;
     const int64_t Fp = ceil_div(e->F, 64) * 64;
@@ -921,6 +985,12 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
          !alloc_t(e, &e->sample_ws, sample_ws_bytes(e->V)) &&
          !alloc_t(e, &e->io_dev, 256, true) &&
          !alloc_t(e, &e->rope, (size_t)e->max_seq * kD * 4);
+    if (ok && kv_kind == 3) {
+        const int mc = (int)ceil_div(e->max_seq, 32);
+        ok = !alloc_t(e, &e->pg_bt, (size_t)e->pg_blocks * 4, true) &&
+             !alloc_t(e, &e->pg_ws, (size_t)Hq * ((size_t)e->max_seq + 256 + (size_t)mc * (kD + 1)) * 4);
+        pg_reset(e);
+    }
     if (ok) {
         void* h = nullptr;
         ok = hipHostMalloc(&h, 256, hipHostMallocDefault) == hipSuccess;
@@ -966,7 +1036,10 @@ TENZO_API void tenzo_destroy_engine(tenzo_engine_t e) {
 
 TENZO_API void tenzo_reset(tenzo_engine_t e) {
     // TenzoEngine.cpp:1249-1255 / :213-215: only the sequence length
-    if (e) e->seq_len = 0;
+    if (e) {
+        e->seq_len = 0;
+        if (e->kv_kind == 3) pg_reset(e);  // PagedKVCache::reset (:246-250)
+    }
 }
 
 TENZO_API int tenzo_get_seq_len(tenzo_engine_t e) { return e ? e->seq_len : 0; }
@@ -1159,6 +1232,10 @@ TENZO_HIP_API int tenzo_hip_engine_decode(tenzo_engine_t e, int token, int n, in
     TZ_CHECK(e->seq_len + n <= e->max_seq, "engine_decode: %d steps from position %d exceed "
              "max_seq %d", n, e->seq_len, e->max_seq);
     TZ_HIP(hipSetDevice(e->dev));
+    if (e->kv_kind == 3) {
+        const int prc = pg_ensure(e, e->seq_len + n);
+        if (prc) return prc;
+    }
     if (n > e->dec_cap) {
         if (e->dec_out) {
             TZ_HIP(hipStreamSynchronize(e->st));
@@ -1230,6 +1307,28 @@ TENZO_HIP_API int tenzo_hip_engine_set_kv(tenzo_engine_t e, const void* kc, cons
     TZ_CHECK(seq_len >= 0 && seq_len <= e->max_seq, "engine_set_kv: seq_len %d outside [0, %d]",
              seq_len, e->max_seq);
     TZ_HIP(hipSetDevice(e->dev));
+    if (e->kv_kind == 3) {  // logical rows scattered into fresh blocks
+        TZ_HIP(hipStreamSynchronize(e->st));
+        pg_reset(e);
+        const int prc = pg_ensure(e, seq_len);
+        if (prc) return prc;
+        const hipMemcpyKind k = is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+        for (int b = 0; b * 16 < seq_len; ++b) {
+            const size_t cnt = (size_t)std::min(16, seq_len - b * 16);
+            for (int l = 0; l < e->L; ++l)
+                for (int h = 0; h < e->Hkv; ++h) {
+                    const size_t dr = (((size_t)e->pg_table[b] * e->L + l) * e->Hkv + h) * 16;
+                    const size_t sr = ((size_t)l * e->Hkv + h) * seq_len + (size_t)b * 16;
+                    TZ_HIP(hipMemcpyAsync(e->kc + dr * kD, (const int8_t*)kc + sr * kD, cnt * kD, k, e->st));
+                    TZ_HIP(hipMemcpyAsync(e->vc + dr * kD, (const int8_t*)vc + sr * kD, cnt * kD, k, e->st));
+                    TZ_HIP(hipMemcpyAsync((float*)e->ks + dr, (const float*)ks + sr, cnt * 4, k, e->st));
+                    TZ_HIP(hipMemcpyAsync((float*)e->vs + dr, (const float*)vs + sr, cnt * 4, k, e->st));
+                }
+        }
+        TZ_HIP(hipStreamSynchronize(e->st));
+        e->seq_len = seq_len;
+        return TENZO_SUCCESS;
+    }
     if (seq_len > 0) {
         const hipMemcpyKind k = is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
         const size_t rows = (size_t)e->L * e->Hkv;
@@ -1253,6 +1352,24 @@ TENZO_HIP_API int tenzo_hip_engine_get_kv(tenzo_engine_t e, void* kc, void* vc, 
     TZ_CHECK(e && kc && vc && ks && vs, "engine_get_kv: null pointer");
     TZ_CHECK(seq_len > 0 && seq_len <= e->max_seq, "engine_get_kv: bad seq_len %d", seq_len);
     TZ_HIP(hipSetDevice(e->dev));
+    if (e->kv_kind == 3) {  // gathered from the blocks in table order
+        TZ_CHECK((int)e->pg_table.size() * 16 >= seq_len, "engine_get_kv: %d tokens but %d "
+                 "blocks", seq_len, (int)e->pg_table.size());
+        TZ_HIP(hipStreamSynchronize(e->st));
+        for (int b = 0; b * 16 < seq_len; ++b) {
+            const size_t cnt = (size_t)std::min(16, seq_len - b * 16);
+            for (int l = 0; l < e->L; ++l)
+                for (int h = 0; h < e->Hkv; ++h) {
+                    const size_t sr = (((size_t)e->pg_table[b] * e->L + l) * e->Hkv + h) * 16;
+                    const size_t dr = ((size_t)l * e->Hkv + h) * seq_len + (size_t)b * 16;
+                    TZ_HIP(hipMemcpy((int8_t*)kc + dr * kD, e->kc + sr * kD, cnt * kD, hipMemcpyDeviceToHost));
+                    TZ_HIP(hipMemcpy((int8_t*)vc + dr * kD, e->vc + sr * kD, cnt * kD, hipMemcpyDeviceToHost));
+                    TZ_HIP(hipMemcpy((float*)ks + dr, (float*)e->ks + sr, cnt * 4, hipMemcpyDeviceToHost));
+                    TZ_HIP(hipMemcpy((float*)vs + dr, (float*)e->vs + sr, cnt * 4, hipMemcpyDeviceToHost));
+                }
+        }
+        return TENZO_SUCCESS;
+    }
     const size_t rows = (size_t)e->L * e->Hkv;
     const size_t R = (size_t)e->kv_row, S = (size_t)e->kv_sb;
     TZ_HIP(hipStreamSynchronize(e->st));
@@ -1265,6 +1382,14 @@ TENZO_HIP_API int tenzo_hip_engine_get_kv(tenzo_engine_t e, void* kc, void* vc, 
     TZ_HIP(hipMemcpy2D(vs, S * seq_len, e->vs, S * e->max_seq,
                        S * seq_len, rows, hipMemcpyDeviceToHost));
     return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_block_table(tenzo_engine_t e, int32_t* out, int cap) {
+    TZ_CHECK(e && (out || cap == 0), "engine_block_table: null pointer");
+    TZ_CHECK(e->kv_kind == 3, "engine_block_table: kv_mode is not paged_int8");
+    const int n = (int)e->pg_table.size();
+    for (int i = 0; i < n && i < cap; ++i) out[i] = e->pg_table[i];
+    return n;
 }
 
 TENZO_HIP_API int tenzo_hip_engine_set_seq_len(tenzo_engine_t e, int seq_len) {

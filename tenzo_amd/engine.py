@@ -150,6 +150,11 @@ class Engine:
 
     def set_kv_from(self, sm: synth.SynthModel):
         n = sm.ctx
+        if self.kv_mode == "paged_int8":
+            self.set_kv(np.ascontiguousarray(sm.kc[:, :, :n]), np.ascontiguousarray(sm.vc[:, :, :n]),
+                        np.ascontiguousarray(sm.ks[:, :, :n]), np.ascontiguousarray(sm.vs[:, :, :n]),
+                        n)
+            return
         if self.kv_mode != "int8_fused":
             if n:
                 raise ValueError("the synthetic model's cache is INT8; use set_kv for "
@@ -178,6 +183,14 @@ class Engine:
         ternary modes: rows [L][Hkv][n][32] uint8 and fp32 scales."""
         c = self.cfg
         shape = (c.num_layers, c.num_kv_heads, seq_len)
+        if self.kv_mode == "paged_int8":
+            kc = np.empty(shape + (128,), np.int8)
+            vc = np.empty_like(kc)
+            ks = np.empty(shape, np.float32)
+            vs = np.empty_like(ks)
+            self._check(self.L.tenzo_hip_engine_get_kv(self.h, _ptr(kc), _ptr(vc), _ptr(ks),
+                                                       _ptr(vs), seq_len), "engine_get_kv")
+            return kc, vc, ks, vs
         if self.kv_mode != "int8_fused":
             kb = np.empty(shape + (32,), np.uint8)
             vb = np.empty_like(kb)
@@ -193,6 +206,14 @@ class Engine:
         self._check(self.L.tenzo_hip_engine_get_kv(self.h, _ptr(kc), _ptr(vc), _ptr(ks), _ptr(vs),
                                                    seq_len), "engine_get_kv")
         return kc, vc, ks.view(np.float16).astype(np.float32), vs.view(np.float16).astype(np.float32)
+
+    def block_table(self) -> np.ndarray:
+        """The paged_int8 sequence's block table (logical -> physical block)."""
+        n = self.L.tenzo_hip_engine_block_table(self.h, None, 0)
+        out = np.zeros(max(n, 1), np.int32)
+        self._check(min(0, self.L.tenzo_hip_engine_block_table(self.h, _ptr(out), n)),
+                    "engine_block_table")
+        return out[:n]
 
     def set_rope_theta(self, theta: float):
         self._check(self.L.tenzo_hip_engine_set_rope_theta(self.h, theta), "set_rope_theta")

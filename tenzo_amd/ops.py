@@ -188,6 +188,24 @@ def attn_tern_decode(mode, q, k_new, v_new, kb, vb, ks, vs, rope_cs, pos: int, w
     return (out, q_rot, k_rot) if want_rot else out
 
 
+def attn_paged_int8_decode(q, k_new, v_new, pk, pv, pks, pvs, block_table, layer: int, rope_cs,
+                           pos: int):
+    """PagedKVCache::forward_attention_raw for one layer at position pos (batch 1).
+
+    pk/pv [blocks][n_layers][Hkv][16][128] int8 and pks/pvs [blocks][n_layers][Hkv][16]
+    fp32 (updated in place at pos); block_table int32 covering position pos."""
+    nb, n_layers, Hkv, page, D = pk.shape
+    assert page == 16 and pk.dtype == torch.int8 and pks.dtype == torch.float32
+    assert block_table.dtype == torch.int32 and block_table.numel() * 16 > pos
+    Hq = q.numel() // D
+    out = torch.empty((1, Hq * D), dtype=torch.float32, device=q.device)
+    _lib.check(_lib.load().tenzo_hip_attn_paged_int8_decode(
+        _ptr(q), _ptr(k_new), _ptr(v_new), _ptr(pk), _ptr(pv), _ptr(pks), _ptr(pvs),
+        _ptr(block_table), n_layers, layer, _ptr(rope_cs), Hq, Hkv, pos, _ptr(out), _stream()),
+        "attn_paged_int8_decode")
+    return out
+
+
 # -------------------------------------------------------- quantized GEMV ---
 
 def gemv_q4_0(act: torch.Tensor, w: torch.Tensor, K: int, N: int) -> torch.Tensor:

@@ -193,3 +193,26 @@ def tern_kv(cfg: DecodeConfig, mode: int, ctx: int, seed: int = 3):
         sc[:, :, :ctx] = rng.uniform(0.9, 1.5, size=shape[:2] + (ctx,)).astype(np.float32)
         rows[name] = (full, sc)
     return rows["k"][0], rows["v"][0], rows["k"][1], rows["v"][1]
+
+
+PAGE = 16  # tokens per block of the paged_int8 cache
+
+
+def paged_kv(cfg: DecodeConfig, ctx: int, block_table, seed: int = 4):
+    """Random paged_int8 pools for ``ctx`` tokens placed through ``block_table``:
+    codes [blocks][L][Hkv][16][128] int8 (per-token quantized N(0,1) rows) and
+    fp32 scales [blocks][L][Hkv][16], blocks = ceil(max_seq / 16)."""
+    rng = np.random.default_rng(seed)
+    nb = (cfg.max_seq + PAGE - 1) // PAGE
+    L, Hkv = cfg.n_layers, cfg.n_kv_heads
+    pools = []
+    for _ in range(2):
+        codes = np.zeros((nb, L, Hkv, PAGE, HEAD_DIM), np.int8)
+        scales = np.ones((nb, L, Hkv, PAGE), np.float32)
+        if ctx:
+            c, sc = kv_quantize(rng.standard_normal((L, Hkv, ctx, HEAD_DIM)).astype(np.float32))
+            for t in range(ctx):
+                codes[block_table[t // PAGE], :, :, t % PAGE] = c[:, :, t]
+                scales[block_table[t // PAGE], :, :, t % PAGE] = sc[:, :, t]
+        pools += [codes, scales]
+    return pools[0], pools[2], pools[1], pools[3]

@@ -271,6 +271,77 @@ def decode_tern_fixture():
     save("decode_tern", **out)
 
 
+PAGED_ATT = dict(Hq=8, Hkv=2, n_layers=2, layer=1, max_seq=320, pos=96)
+
+
+def attention_paged_fixture():
+    """PagedKVCache::forward_attention_raw on a permuted block table, position
+    96 (the reference allocates the block of the new token), plus a peaked-q
+    case whose softmax has weights below the 1e-7 cut-off."""
+    c = PAGED_ATT
+    cfg = synth.DecodeConfig(hidden=c["Hq"] * 128, n_q_heads=c["Hq"], n_kv_heads=c["Hkv"],
+                             n_layers=c["n_layers"], ffn=64, vocab=64, max_seq=c["max_seq"],
+                             theta=10000.0)
+    nb = (c["max_seq"] + 15) // 16
+    rng = np.random.default_rng(40)
+    perm = rng.permutation(nb).astype(np.int32)
+    pk, pv, pks, pvs = synth.paged_kv(cfg, c["pos"], perm, seed=41)
+    R = oracle.ref()
+    out = {"perm": perm}
+    for name, qscale in (("", 1.0), ("peak_", 40.0)):
+        q = (qscale * rng.standard_normal(c["Hq"] * 128)).astype(np.float32)
+        k = (2 * rng.standard_normal(c["Hkv"] * 128)).astype(np.float32)
+        v = rng.standard_normal(c["Hkv"] * 128).astype(np.float32)
+        rc = [a.copy() for a in (pk, pv, pks, pvs)]
+        bt = perm.copy()
+        res = np.zeros(c["Hq"] * 128, np.float32)
+        n = R.ref_attention_paged(c["Hq"], c["Hkv"], c["n_layers"], c["layer"], nb, c["pos"],
+                                  P(q.copy()), P(k.copy()), P(v), *(P(a) for a in rc), P(bt),
+                                  c["pos"] // 16, P(res))
+        out.update({name + "q": q, name + "k": k, name + "v": v, name + "out": res,
+                    name + "block_table": bt[:n], name + "pk_out": rc[0], name + "pv_out": rc[1],
+                    name + "pks_out": rc[2], name + "pvs_out": rc[3]})
+    out.update(pk=pk, pv=pv, pks=pks, pvs=pvs)
+    save("attention_paged", **out)
+
+
+def decode_paged_fixture():
+    """The decode_tiny model run by the reference engine with kv_mode paged_int8
+    from an empty cache (its block manager allocates as the steps go)."""
+    z = np.load(os.path.join(OUT, "decode_tiny.npz"))
+    sm = load_tiny_model(z)
+    c = sm.cfg
+    tokens = np.array([7, 300, 42, 5, 99, 11, 250, 3, 17, 64, 128, 255, 1, 2, 3, 4, 5, 6],
+                      np.int64)
+    R = oracle.ref()
+    e = R.ref_engine_create_mode(c.hidden, c.n_q_heads, c.n_kv_heads, c.n_layers, c.ffn, c.vocab,
+                                 32, 3)
+    keep = [layer_struct(sm, l) for l in range(c.n_layers)]
+    for l, w in enumerate(keep):
+        assert R.ref_engine_set_layer(e, l, ctypes.byref(w)) == 0
+    assert R.ref_engine_set_head(e, P(sm.embed), P(sm.embed_scales), P(sm.final_norm), c.vocab,
+                                 c.hidden) == 0
+    logits, hidden, out_tok = [], [], []
+    for t in tokens:
+        lg = np.empty(c.vocab, np.float32)
+        out_tok.append(R.ref_engine_step(e, int(t), P(lg)))
+        h = np.empty(c.hidden, np.float32)
+        R.ref_engine_hidden(e, P(h))
+        logits.append(lg)
+        hidden.append(h)
+    nb = 2
+    pk = np.empty((nb, c.n_layers, c.n_kv_heads, 16, 128), np.int8)
+    pv = np.empty_like(pk)
+    pks = np.empty((nb, c.n_layers, c.n_kv_heads, 16), np.float32)
+    pvs = np.empty_like(pks)
+    bt = np.zeros(nb, np.int32)
+    n = R.ref_engine_get_kv_paged(e, P(pk), P(pv), P(pks), P(pvs), P(bt))
+    R.ref_engine_destroy(e)
+    save("decode_paged", tokens=tokens, out_tokens=np.array(out_tok), logits=np.stack(logits),
+         hidden=np.stack(hidden), pk=pk, pv=pv, pks=pks, pvs=pvs, block_table=bt[:n],
+         max_seq=np.int64(32))
+
+
 def load_tiny_model(z) -> synth.SynthModel:
     """Rebuilds the decode fixture's model from its stored arrays."""
     layers = []
@@ -295,3 +366,5 @@ if __name__ == "__main__":
     decode_fixture()
     attention_tern_fixture()
     decode_tern_fixture()
+    attention_paged_fixture()
+    decode_paged_fixture()

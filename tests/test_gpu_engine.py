@@ -290,7 +290,7 @@ def test_engine_error_paths(eng_mod):
         assert b"full" in L.tenzo_hip_last_error()
         assert L.tenzo_set_layer_weights(None, 0, None) == -1
     bad = eng_mod.config_from(cfg)
-    for mode in (b"paged_int8", b"fp32"):  # not provided on the GPU
+    for mode in (b"fp32", b"int4_fused"):  # not provided on the GPU
         bad.kv_mode = mode
         assert not L.tenzo_create_engine(ctypes.byref(bad))
         assert b"kv_mode" in L.tenzo_hip_last_error()
