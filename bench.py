@@ -51,7 +51,7 @@ def parse():
                     help="engine execution mode (one persistent kernel per token, or one "
                          "kernel per stage replayed from a HIP graph / launched eagerly)")
     ap.add_argument("--kv-mode", default="int8_fused",
-                    choices=["int8_fused", "tl1_fused", "popcount_fused"],
+                    choices=["int8_fused", "tl1_fused", "popcount_fused", "paged_int8"],
                     help="KV cache mode; the ternary modes print their own JSON line (decode on "
                          "the graph path and the ternary attention kernel's roofline)")
     ap.add_argument("--prefill", type=int, default=0, metavar="N",
@@ -147,7 +147,7 @@ def build_model(torch, cfg, ctx, kv_mode="int8_fused"):
     e._check(e.L.tenzo_set_lm_head_i8(e.h, head.data_ptr(), hs.data_ptr(), V, H),
              "set_lm_head_i8")
     L, Hkv = cfg.n_layers, cfg.n_kv_heads
-    if kv_mode != "int8_fused":
+    if kv_mode in ("tl1_fused", "popcount_fused"):
         kb = tern_rows_dev(torch, (L, Hkv, ctx), kv_mode == "popcount_fused", gen)
         vb = tern_rows_dev(torch, (L, Hkv, ctx), False, gen)
         ks = torch.rand((L, Hkv, ctx), device="cuda", generator=gen) * 0.6 + 0.9
@@ -161,14 +161,16 @@ def build_model(torch, cfg, ctx, kv_mode="int8_fused"):
     # INT8 KV cache: ctx tokens of N(0,1) per (layer, kv head), quantized per token
     kc = torch.empty((L, Hkv, ctx, 128), dtype=torch.int8, device="cuda")
     vc = torch.empty_like(kc)
-    ks = torch.empty((L, Hkv, ctx), dtype=torch.float16, device="cuda")
+    # fp16 scales (BASELINE); paged_int8 keeps the reference's fp32
+    sdt = torch.float32 if kv_mode == "paged_int8" else torch.float16
+    ks = torch.empty((L, Hkv, ctx), dtype=sdt, device="cuda")
     vs = torch.empty_like(ks)
     for c, s in ((kc, ks), (vc, vs)):
         for l in range(L):
             x = torch.randn((Hkv, ctx, 128), device="cuda", generator=gen)
             amax = x.abs().amax(dim=2).clamp_min(1e-8)
             c[l] = torch.clamp(torch.round(x * (127.0 / amax)[..., None]), -128, 127).to(torch.int8)
-            s[l] = (amax * (1.0 / 127.0)).half()
+            s[l] = (amax * (1.0 / 127.0)).to(sdt)
     if ctx > 0:
         e.set_kv_device(kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(), ctx)
     e.set_rope_theta(cfg.theta)
@@ -384,6 +386,7 @@ def prefill_bench(torch, e, cfg, host, args):
 
 
 TERN_ROW_BYTES = 32 + 32 + 4 + 4  # K row, V row, two fp32 scales per (kv head, token)
+PAGED_ROW_BYTES = 128 + 128 + 4 + 4
 
 
 def tern_bench(torch, e, cfg, host, args):
@@ -406,24 +409,60 @@ def tern_bench(torch, e, cfg, host, args):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(SEED + 1)
     S = ctx + 1
-    kb = torch.zeros((1, Hkv, S, 32), dtype=torch.uint8, device="cuda")
-    vb = torch.zeros_like(kb)
-    ks = torch.zeros((1, Hkv, S), dtype=torch.float32, device="cuda")
-    vs = torch.zeros_like(ks)
-    kb[0, :, :ctx] = host["kc"][0]
-    vb[0, :, :ctx] = host["vc"][0]
-    ks[0, :, :ctx] = host["ks"][0]
-    vs[0, :, :ctx] = host["vs"][0]
+    if mode != "paged_int8":
+        kb = torch.zeros((1, Hkv, S, 32), dtype=torch.uint8, device="cuda")
+        vb = torch.zeros_like(kb)
+        ks = torch.zeros((1, Hkv, S), dtype=torch.float32, device="cuda")
+        vs = torch.zeros_like(ks)
+        kb[0, :, :ctx] = host["kc"][0]
+        vb[0, :, :ctx] = host["vc"][0]
+        ks[0, :, :ctx] = host["ks"][0]
+        vs[0, :, :ctx] = host["vs"][0]
     q = torch.randn((1, Hq * 128), device="cuda", generator=gen)
     k = torch.randn((1, Hkv * 128), device="cuda", generator=gen)
     v = torch.randn((1, Hkv * 128), device="cuda", generator=gen)
     cs = ops.rope_table(cfg.theta, ctx, 1)[0].cuda()
-    att_s = graph_time(torch, lambda: ops.attn_tern_decode(mode, q, k, v, kb, vb, ks, vs, cs,
-                                                           ctx), 200)
-    att_bytes = Hkv * S * TERN_ROW_BYTES + (2 * Hq + 2 * Hkv) * 128 * 4
+    if mode == "paged_int8":
+        # layer 0's cache in blocks 0, 1, ... (the engine's allocation order)
+        nb = (S + 15) // 16
+
+        def pool(x, width):
+            full = torch.zeros((Hkv, nb * 16) + width, dtype=x.dtype, device="cuda")
+            full[:, :ctx] = x[0]
+            return full.reshape((Hkv, nb, 16) + width).transpose(0, 1).unsqueeze(1).contiguous()
+        pk, pv = pool(host["kc"], (128,)), pool(host["vc"], (128,))
+        pks, pvs = pool(host["ks"], ()), pool(host["vs"], ())
+        bt = torch.arange(nb, dtype=torch.int32, device="cuda")
+        kernel = "paged_scores + softmax + values + sum kernels"
+        att_s = graph_time(torch, lambda: ops.attn_paged_int8_decode(q, k, v, pk, pv, pks, pvs, bt,
+                                                                     0, cs, ctx), 200)
+        att_bytes = Hkv * S * PAGED_ROW_BYTES + (2 * Hq + 2 * Hkv) * 128 * 4
+    else:
+        kernel = "attn_tern_chunk_kernel + attn_combine_kernel"
+        att_s = graph_time(torch, lambda: ops.attn_tern_decode(mode, q, k, v, kb, vb, ks, vs, cs,
+                                                               ctx), 200)
+        att_bytes = Hkv * S * TERN_ROW_BYTES + (2 * Hq + 2 * Hkv) * 128 * 4
     gbs = att_bytes / att_s / 1e9
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and mode == "paged_int8":
+        import oracle
+        if oracle.ref_available():
+            P = oracle._ptr
+            hp = [t.cpu().numpy().copy() for t in (pk, pv, pks, pvs)]
+            btn = bt.cpu().numpy().copy()
+            qh, kh, vh = (t.cpu().numpy()[0] for t in (q, k, v))
+            out = np.zeros(Hq * 128, np.float32)
+            R = oracle.ref()
+            n, t0 = 0, time.perf_counter()
+            while time.perf_counter() - t0 < min(args.cpu_seconds, 10.0) or n < 3:
+                R.ref_attention_paged(Hq, Hkv, 1, 0, nb, ctx, P(qh.copy()), P(kh.copy()), P(vh),
+                                      *(P(a) for a in hp), P(btn.copy()), (ctx + 15) // 16, P(out))
+                n += 1
+            cpu = {"value": round(n / (time.perf_counter() - t0), 2), "unit": "attention calls/s",
+                   "cores": 1, "kind": "reference",
+                   "sample": f"PagedKVCache::forward_attention_raw, one layer, Hq {Hq} Hkv {Hkv}, "
+                             f"position {ctx}, {n} calls (single-threaded in the reference)"}
+    elif not args.no_cpu:
         import oracle
         if oracle.ref_available():
             P = oracle._ptr
@@ -446,10 +485,11 @@ def tern_bench(torch, e, cfg, host, args):
         "value": round(args.steps / dt, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(dt / args.steps * 1e3, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "ternary KV (int32 dot, fp32 softmax)", "data": "synthetic",
+        "dtype": ("int8 KV, fp32 scales" if mode == "paged_int8" else
+                  "ternary KV (int32 dot, fp32 softmax)"), "data": "synthetic",
         "config": {"workload": f"BitNet-b1.58-2B-shaped greedy decode step, batch 1, context "
                                f"{ctx}, {mode} KV cache (graph path)", "engine_mode": e.mode},
-        "roofline": {"bound": "hbm", "kernel": "attn_tern_chunk_kernel + attn_combine_kernel",
+        "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
                      "alg_bytes_per_launch": int(att_bytes),
