@@ -183,11 +183,18 @@ __global__ void __launch_bounds__(256) paged_softmax_kernel(PagedArgs a) {
     float M = -1e30f;
     for (int c = 0; c < nchunks; ++c) M = fmaxf(M, cm[c]);
     float* s = a.scores + (int64_t)qh * a.score_stride;
+    // thread tid takes t = tid, tid + 256, ... in order; a read-only pass sums
+    // the exponentials (its loads issued kU at a time), a second pass writes
+    // the normalized weights (the same expf of the same score)
+    constexpr int kU = 8;
     float l = 0.0f;
-    for (int t = tid; t < seq_len; t += 256) {
-        const float e = expf(s[t] - M);
-        s[t] = e;
-        l += e;
+    for (int t0 = tid; t0 < seq_len; t0 += 256 * kU) {
+        float v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = t0 + 256 * u < seq_len ? s[t0 + 256 * u] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            if (t0 + 256 * u < seq_len) l += expf(v[u] - M);
     }
     l = wave_sum_tree(l);
     if (lane == 0) red[wave] = l;
@@ -195,7 +202,14 @@ __global__ void __launch_bounds__(256) paged_softmax_kernel(PagedArgs a) {
     if (tid == 0) stat = __fdiv_rn(1.0f, ((red[0] + red[1]) + (red[2] + red[3])) + 1e-8f);
     __syncthreads();
     const float inv = stat;
-    for (int t = tid; t < seq_len; t += 256) s[t] = __fmul_rn(s[t], inv);
+    for (int t0 = tid; t0 < seq_len; t0 += 256 * kU) {
+        float v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u) v[u] = t0 + 256 * u < seq_len ? s[t0 + 256 * u] : 0.0f;
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            if (t0 + 256 * u < seq_len) s[t0 + 256 * u] = __fmul_rn(expf(v[u] - M), inv);
+    }
 }
 
 // Weighted values of one chunk (:408-443): thread (d4, p) owns dims 4 d4 .. +3
