@@ -160,3 +160,36 @@ def test_engine_paged_reference_goldens(eng_mod):
             assert (g != r).mean() < 0.01 and np.abs(g - r).max() <= 1
         e.reset()
         assert e.seq_len == 0 and len(e.block_table()) == 0
+
+
+@pytest.mark.parametrize("kv_mode", ["paged_int8", "tl1_fused", "popcount_fused"])
+def test_engine_kv_modes_chained_decode_and_prefill(eng_mod, kv_mode):
+    """Chained decode on the device (tenzo_hip_engine_decode) equals one step
+    at a time, and the batched prefill entry point equals tenzo_prefill_token
+    per token, across a block boundary; reset frees the sequence."""
+    sm = synth.make_model(CFG, seed=73, ctx=0)
+    toks = [3, 77, 1000, 5, 42, 9, 600, 11, 12, 13, 14, 15, 16, 17]
+    with eng_mod.Engine(CFG, kv_mode=kv_mode) as a, eng_mod.Engine(CFG, kv_mode=kv_mode) as b:
+        for e in (a, b):
+            e.set_model(sm)
+        a.prefill_batch(toks)
+        for t in toks:
+            b.prefill(t)
+        assert a.seq_len == b.seq_len == len(toks)
+        got, _ = a.decode(7, 6)
+        ref = []
+        tok = 7
+        for _ in range(6):
+            tok = b.step(tok)
+            ref.append(tok)
+        assert list(got) == ref
+        np.testing.assert_array_equal(a.logits(), b.logits())
+        n = len(toks) + 6
+        for x, y in zip(a.get_kv(n), b.get_kv(n)):
+            np.testing.assert_array_equal(x, y)
+        if kv_mode == "paged_int8":
+            np.testing.assert_array_equal(a.block_table(), np.arange(2))
+            a.reset()
+            assert len(a.block_table()) == 0
+            a.prefill_batch(toks[:3])
+            np.testing.assert_array_equal(a.block_table(), [0])
