@@ -328,11 +328,12 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
 //   M = max_c m_c,  L = sum_c e^{m_c - M} l_c,  o = sum_c e^{m_c - M} o_c,
 // summed in chunk order with one fma per term. The chunks' (m, l) are staged
 // in LDS by the whole block, each chunk's weight e^{m_c - M} is evaluated once
-// into LDS, and each thread's o_c loads are issued kMergeU at a time, so the
-// loop waits for memory once per kMergeU chunks instead of once per chunk; the
-// arithmetic (and so the result) is that of the plain loop.
+// into LDS, and each thread's o_c loads are issued kMergeU at a time (the first
+// batch together with the statistics' loads), so the loop waits for memory
+// once per kMergeU chunks instead of once per chunk; the arithmetic (and so
+// the result) is that of the plain loop.
 constexpr int kMergeLds = 1024;  // chunks staged in LDS (contexts of 32K at 32-token chunks)
-constexpr int kMergeU = 32;
+constexpr int kMergeU = 64;
 
 __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
     __shared__ float ms[kMergeLds], ls[kMergeLds], es[kMergeLds];
@@ -351,6 +352,12 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
             o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
         }
     } else {
+        // the first kMergeU value loads go out before the statistics are
+        // staged (they do not depend on M), so both share one wait
+        float ov[kMergeU];
+#pragma unroll
+        for (int u = 0; u < kMergeU; ++u)
+            ov[u] = u < nchunks ? pp[u * kPartStride + 2 + d] : 0.0f;
         for (int c = d; c < nchunks; c += 128) {
             ms[c] = pp[c * kPartStride];
             ls[c] = pp[c * kPartStride + 1];
@@ -362,10 +369,11 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
         for (int c = d; c < nchunks; c += 128) es[c] = expf(ms[c] - M);
         __syncthreads();
         for (int c0 = 0; c0 < nchunks; c0 += kMergeU) {
-            float ov[kMergeU];
+            if (c0 > 0) {
 #pragma unroll
-            for (int u = 0; u < kMergeU; ++u)
-                ov[u] = c0 + u < nchunks ? pp[(c0 + u) * kPartStride + 2 + d] : 0.0f;
+                for (int u = 0; u < kMergeU; ++u)
+                    ov[u] = c0 + u < nchunks ? pp[(c0 + u) * kPartStride + 2 + d] : 0.0f;
+            }
 #pragma unroll
             for (int u = 0; u < kMergeU; ++u) {
                 if (c0 + u < nchunks) {
