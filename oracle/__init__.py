@@ -66,6 +66,8 @@ def lib() -> ctypes.CDLL:
             "orc_tl1_gemv_i32": (None, [_P, _P, _I64, _I64, _P]),
             "orc_tl1_gemv": (_F, [_P, _P, _I64, _I64, _F, _P, _P]),
             "orc_sumsq": (_F, [_P, _I64]),
+            "orc_rsqrt_est": (_F, [_F]),
+            "orc_inv_rms": (_F, [_F, _I64, _F]),
             "orc_rms_norm": (None, [_P, _P, _P, _I64, _F]),
             "orc_kv_quant": (_F, [_P, _I, _P]),
             "orc_rope_table": (None, [_F, _I, _I, _P]),
@@ -222,6 +224,14 @@ def tl1_gemv(x: np.ndarray, w: np.ndarray, N: int, w_scale: float):
 def sumsq(x: np.ndarray) -> np.float32:
     x = f32(x)
     return np.float32(lib().orc_sumsq(_ptr(x), x.size))
+
+
+def rsqrt_est(a: float) -> np.float32:
+    return np.float32(lib().orc_rsqrt_est(float(a)))
+
+
+def inv_rms(ss: float, dim: int, eps: float = 1e-5) -> np.float32:
+    return np.float32(lib().orc_inv_rms(float(ss), int(dim), float(eps)))
 
 
 def rms_norm(x: np.ndarray, w: np.ndarray | None, eps: float = 1e-5) -> np.ndarray:

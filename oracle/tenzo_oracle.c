@@ -215,23 +215,51 @@ float orc_tl1_gemv(const float* x, const uint8_t* w, int64_t N, int64_t K, float
 /* RMSNorm (:148-166)                                                         */
 /* ------------------------------------------------------------------------- */
 
+/* The reference build (-O3 -mavx2 -mfma -ffast-math) vectorises rms_norm_raw's
+ * "omp simd reduction(+:sum_sq)" loop into one 8-lane accumulator: lane j is an
+ * FMA chain over x[j], x[j+8], ... in index order; the n % 8 tail elements are
+ * then added to lane 0 one at a time, and the lanes are summed as
+ * ((l0+l4)+(l2+l6)) + ((l1+l5)+(l3+l7)) (vextractf128 / vmovhlps / vshufps). */
 float orc_sumsq(const float* x, int64_t n) {
-    float p[1024];
-    for (int t = 0; t < 1024; ++t) {
-        float s = 0.0f;
-        for (int64_t i = t; i < n; i += 1024) s = fmaf(x[i], x[i], s);
-        p[t] = s;
-    }
-    for (int w = 512; w >= 1; w >>= 1)       /* balanced pairwise tree */
-        for (int t = 0; t < w; ++t) p[t] = p[2 * t] + p[2 * t + 1];
-    return p[0];
+    float l[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    const int64_t n8 = n / 8 * 8;
+    for (int64_t i = 0; i < n8; i += 8)
+        for (int j = 0; j < 8; ++j) l[j] = fmaf(x[i + j], x[i + j], l[j]);
+    for (int64_t i = n8; i < n; ++i) l[0] = fmaf(x[i], x[i], l[0]);
+    return ((l[0] + l[4]) + (l[2] + l[6])) + ((l[1] + l[5]) + (l[3] + l[7]));
 }
 
+/* x86 RSQRTSS of the host the reference was built and its goldens written on:
+ * indexed by the exponent's parity and the top 10 mantissa bits (a in [0.5, 2)),
+ * the estimate's exponent moving by half the input's (gen_rsqrt_est.c). */
+static const uint32_t kRsqrtEst[2048] = {
+#include "rsqrt_est_table.inc"
+};
+
+float orc_rsqrt_est(float a) {
+    uint32_t b;
+    memcpy(&b, &a, 4);
+    const int32_t e = (int32_t)(b >> 23), odd = e & 1, e0 = odd ? 127 : 126;
+    const uint32_t t = kRsqrtEst[odd * 1024 + ((b >> 13) & 1023u)];
+    const uint32_t r = (uint32_t)((int32_t)t - ((e - e0) / 2) * (1 << 23));
+    float f;
+    memcpy(&f, &r, 4);
+    return f;
+}
+
+/* inv_rms of :154 as built: 1/std::sqrt(a) becomes the estimate y0 = rsqrtss(a)
+ * and one Newton step, evaluated as (y0 * -0.5f) * fmaf(a * y0, y0, -3.0f); the
+ * mean is a true division (vdivss). */
+float orc_inv_rms(float ss, int64_t dim, float eps) {
+    const float a = ss / (float)dim + eps;
+    const float y0 = orc_rsqrt_est(a);
+    return (y0 * -0.5f) * fmaf(a * y0, y0, -3.0f);
+}
+
+/* :155-165 as built: the weighted product is reassociated to (x * w) * inv_rms. */
 void orc_rms_norm(const float* x, const float* w, float* y, int64_t dim, float eps) {
-    float ss = orc_sumsq(x, dim);
-    float inv_rms = 1.0f / sqrtf(ss / (float)dim + eps);    /* :154 */
-    for (int64_t i = 0; i < dim; ++i)                       /* :155-165 */
-        y[i] = w ? (x[i] * inv_rms) * w[i] : x[i] * inv_rms;
+    const float inv_rms = orc_inv_rms(orc_sumsq(x, dim), dim, eps);
+    for (int64_t i = 0; i < dim; ++i) y[i] = w ? (x[i] * w[i]) * inv_rms : x[i] * inv_rms;
 }
 
 /* ------------------------------------------------------------------------- */

@@ -18,9 +18,13 @@
  *                                    bytes and scale) + closed form
  *   orc_tl1_gemv_i32 / orc_tl1_gemv  closed form sum_k W[n,k]*a_k (dense brute
  *                                    force) + compiled-reference goldens (bit-exact)
- *   orc_rms_norm                     fp64 brute force (1e-6 rel) + compiled
- *                                    reference (1e-6 rel; its summation order is
- *                                    compiler-defined under -ffast-math)
+ *   orc_sumsq, orc_inv_rms,
+ *   orc_rms_norm                     compiled reference (bit-exact at dims 1..8200,
+ *                                    live and fixture) + fp64 brute force (1e-6)
+ *                                    + the eight-chain order against an exact
+ *                                    rational restatement on small rows
+ *   orc_rsqrt_est                    the host's RSQRTSS over every positive normal
+ *                                    float (Intel hosts) + exponent scaling
  *   orc_kv_quant                     compiled-reference goldens (bit-exact codes)
  *                                    + special cases (all-zero, single spike)
  *   orc_rope_table, orc_rope_apply   compiled reference (bit-exact rotated q/k) +
@@ -95,12 +99,16 @@ void orc_tl1_gemv_i32(const uint8_t* w, const int8_t* codes, int64_t N, int64_t 
 float orc_tl1_gemv(const float* x, const uint8_t* w, int64_t N, int64_t K, float w_scale,
                    float* y, int32_t* acc);
 
-/* ---- RMSNorm (rms_norm_raw, :148-166) ---- */
-/* Sum of squares in a fixed order: 1024 strided partials p[t] = fma-accumulated
- * x[t], x[t+1024], ..., then a balanced pairwise tree over p[0..1023]. (The
- * reference's order is compiler-chosen under -ffast-math; this one is pinned to
- * it at 2e-6 and is the order every GPU kernel of this repo uses.) */
+/* ---- RMSNorm (rms_norm_raw, :148-166, as the reference build evaluates it) ---- */
+/* Sum of squares: eight FMA chains (chain j over x[j], x[j+8], ...), the n % 8
+ * tail added to chain 0, then ((c0+c4)+(c2+c6)) + ((c1+c5)+(c3+c7)). */
 float orc_sumsq(const float* x, int64_t n);
+/* RSQRTSS estimate of the reference's build host (table, exact for every
+ * positive normal a). */
+float orc_rsqrt_est(float a);
+/* inv_rms = (y0 * -0.5) * fma(a * y0, y0, -3), a = ss / dim + eps, y0 = est(a). */
+float orc_inv_rms(float ss, int64_t dim, float eps);
+/* y = (x * w) * inv_rms, or x * inv_rms without weights. */
 void orc_rms_norm(const float* x, const float* w, float* y, int64_t dim, float eps);
 
 /* ---- INT8 KV cache (FusedKVCache, TenzoEngine.h:60-115, .cpp:506-533) ---- */

@@ -114,31 +114,6 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
-// Sum of squares of x[0..n) in the fixed order shared with the CPU oracle
-// (orc_sumsq): 1024 strided partials p[m] = fma-accumulated x[m], x[m+1024],
-// ...; then a balanced pairwise tree over p[0..1023] in index order. Thread t
-// of 256 owns p[4t..4t+3] (and adds them as the tree's first two levels); the
-// butterfly over the wave and the 4-wave sum are the remaining levels. Must be
-// called by all threads of a 256-thread block; `red` is 4 floats of LDS.
-__device__ __forceinline__ float block256_sumsq(const float* __restrict__ x, int64_t n,
-                                                float* red) {
-    const int t = threadIdx.x;
-    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
-    for (int64_t i = 4 * t; i < n; i += 1024) {
-        p0 = __builtin_fmaf(x[i], x[i], p0);
-        if (i + 1 < n) p1 = __builtin_fmaf(x[i + 1], x[i + 1], p1);
-        if (i + 2 < n) p2 = __builtin_fmaf(x[i + 2], x[i + 2], p2);
-        if (i + 3 < n) p3 = __builtin_fmaf(x[i + 3], x[i + 3], p3);
-    }
-    float s = (p0 + p1) + (p2 + p3);
-    s = wave_sum_tree(s);
-    if ((t & 63) == 0) red[t >> 6] = s;
-    __syncthreads();
-    float r = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return r;
-}
-
 // Block-wide max / integer sum for 256 threads (order-independent).
 __device__ __forceinline__ float block256_max(float v, float* red) {
     v = wave_max(v);
@@ -165,18 +140,105 @@ __device__ __forceinline__ int block256_sum_i32(int v, int* red) {
 // are correctly rounded (__fsqrt_rn is not: without
 // OCML_BASIC_ROUNDED_OPERATIONS it maps to the native approximation).
 
-// inv_rms of rms_norm_raw (TenzoEngine.cpp:154): 1 / sqrt(ss/dim + eps), each
-// operation correctly rounded.
-__device__ __forceinline__ float inv_rms_from_sumsq(float ss, int64_t dim, float eps) {
-    const float mean = ss / (float)dim;
-    return 1.0f / sqrtf(mean + eps);
+// ---- rms_norm_raw (TenzoEngine.cpp:148-166) as the reference build evaluates it ----
+//
+// The reference is compiled with -O3 -mavx2 -mfma -ffast-math, under which
+//  * the "omp simd reduction(+:sum_sq)" loop is one 8-lane FMA accumulator:
+//    chain j runs over x[j], x[j+8], ... in index order, the n % 8 tail is
+//    added to chain 0, and the chains are summed as
+//    ((c0+c4)+(c2+c6)) + ((c1+c5)+(c3+c7));
+//  * 1.0f / std::sqrt(a) is the RSQRTSS estimate y0 refined by one Newton
+//    step, (y0 * -0.5f) * fma(a * y0, y0, -3.0f), with a = ss / dim + eps;
+//  * the weighted product x * inv_rms * w is reassociated to (x * w) * inv_rms.
+// The activation codes that follow a norm depend on every one of these
+// roundings, so the kernels reproduce them exactly.
+
+// RSQRTSS of the host the reference was built on, for a in [0.5, 2): entry
+// 1024 * (exponent parity) + top 10 mantissa bits (gen_rsqrt_est.c).
+constexpr int kRsqrtEstWords = 2048;
+__device__ static const uint32_t kRsqrtEstTab[kRsqrtEstWords] = {
+#include "rsqrt_est_table.inc"
+};
+
+// The estimate for a positive normal a; tab is kRsqrtEstTab or a copy of it
+// (in LDS). Its exponent moves by half the input's, exactly.
+__device__ __forceinline__ float rsqrt_est(float a, const uint32_t* tab) {
+    const uint32_t b = __float_as_uint(a);
+    const int e = (int)(b >> 23), odd = e & 1, e0 = odd ? 127 : 126;
+    const uint32_t t = tab[odd * 1024 + ((b >> 13) & 1023u)];
+    return __uint_as_float((uint32_t)((int)t - ((e - e0) / 2) * (1 << 23)));
 }
 
-// y = x * inv_rms * w evaluated left to right (TenzoEngine.cpp:158).
+// inv_rms of :154 from the sum of squares.
+__device__ __forceinline__ float inv_rms_ref(float ss, int64_t dim, float eps,
+                                             const uint32_t* tab) {
+    const float a = __fadd_rn(__fdiv_rn(ss, (float)dim), eps);
+    const float y0 = rsqrt_est(a, tab);
+    return __fmul_rn(__fmul_rn(y0, -0.5f), __builtin_fmaf(__fmul_rn(a, y0), y0, -3.0f));
+}
+
+// y = (x * w) * inv_rms, or x * inv_rms without weights (:155-165 as built).
 __device__ __forceinline__ float norm_apply(float x, float inv_rms, const float* __restrict__ w,
                                             int64_t i) {
-    float v = __fmul_rn(x, inv_rms);
-    return w ? __fmul_rn(v, w[i]) : v;
+    return w ? __fmul_rn(__fmul_rn(x, w[i]), inv_rms) : __fmul_rn(x, inv_rms);
+}
+
+// Chain layout of a row in LDS: element i at ct[(i % 8) * ld + i / 8], so
+// chain j is row j. ld >= ceil(n / 8) is a multiple of 4 and 4 mod 32 words,
+// so the eight rows start in distinct banks.
+__host__ __device__ inline int chain_ld(int64_t n) {
+    const int c = (int)((n + 7) / 8);
+    return (c + 27) / 32 * 32 + 4;
+}
+__device__ __forceinline__ int chain_pos(int64_t i, int ld) {
+    return (int)(i & 7) * ld + (int)(i >> 3);
+}
+
+// Sum of squares of the n-element row in chain layout, in the reference
+// build's order; called by a whole wave (lane l runs chain l % 8, so every
+// lane's loads hit an address another lane of its row-group also reads), the
+// result is returned in every lane.
+__device__ __forceinline__ float chain_sumsq(const float* ct, int ld, int64_t n) {
+    const int j = threadIdx.x & 7;
+    const int n8 = (int)(n >> 3), nq = n8 >> 2;
+    const float4* row = reinterpret_cast<const float4*>(ct + j * ld);
+    float s = 0.0f;
+    if (nq >= 4) {
+        // four float4s per step, the next four loaded while these are summed
+        float4 a0 = row[0], a1 = row[1], a2 = row[2], a3 = row[3];
+        for (int q = 0; q + 4 <= nq; q += 4) {
+            const int nx = min(q + 4, nq - 4);  // (a repeat of the last four at the end)
+            const float4 b0 = row[nx], b1 = row[nx + 1], b2 = row[nx + 2], b3 = row[nx + 3];
+            const float4 a[4] = {a0, a1, a2, a3};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                s = __builtin_fmaf(a[u].x, a[u].x, s);
+                s = __builtin_fmaf(a[u].y, a[u].y, s);
+                s = __builtin_fmaf(a[u].z, a[u].z, s);
+                s = __builtin_fmaf(a[u].w, a[u].w, s);
+            }
+            a0 = b0;
+            a1 = b1;
+            a2 = b2;
+            a3 = b3;
+        }
+    }
+    for (int q = nq & ~3; q < nq; ++q) {
+        const float4 a = row[q];
+        s = __builtin_fmaf(a.x, a.x, s);
+        s = __builtin_fmaf(a.y, a.y, s);
+        s = __builtin_fmaf(a.z, a.z, s);
+        s = __builtin_fmaf(a.w, a.w, s);
+    }
+    for (int k = nq * 4; k < n8; ++k) s = __builtin_fmaf(ct[j * ld + k], ct[j * ld + k], s);
+    if (j == 0)
+        for (int t = 0; t < (int)(n & 7); ++t) {
+            const float v = ct[t * ld + n8];
+            s = __builtin_fmaf(v, v, s);
+        }
+    const float c0 = lane_f(s, 0), c1 = lane_f(s, 1), c2 = lane_f(s, 2), c3 = lane_f(s, 3);
+    const float c4 = lane_f(s, 4), c5 = lane_f(s, 5), c6 = lane_f(s, 6), c7 = lane_f(s, 7);
+    return ((c0 + c4) + (c2 + c6)) + ((c1 + c5) + (c3 + c7));
 }
 
 // Signed 8-bit dot of 4 lanes + accumulator (v_dot4_i32_i8).

@@ -20,8 +20,8 @@
 // (the GEMV's own rounding steps) using the (inv_scale, code_sum) record the
 // producing stage published, and adds the residual. Each stage input is built
 // in registers (thread t owns float4 groups t, t+256, ...), normalized and
-// quantized there: the RMSNorm sum of squares follows the fixed 1024-partial
-// order of the CPU oracle, which is exactly this ownership. Vectors later
+// quantized there; the RMSNorm sum of squares runs over a copy in LDS in the
+// reference build's order (eight FMA chains, common.h). Vectors later
 // stages need as floats (x, h1, q|k|v, gate|up) are stored by the workgroups
 // of the stage that builds them, 64-element slices spread over those
 // workgroups.
@@ -147,6 +147,8 @@ __device__ __forceinline__ void stc16(__amdgpu_buffer_rsrc_t r, uint32_t byte_of
 // first stage and stall every wave for an HBM round trip). Fields are read
 // from LDS at a uniform address and moved to scalar registers.
 __shared__ DsLayer s_layers[kDsMaxLayers];
+// The RSQRTSS estimate table of inv_rms_ref, staged with the layer table.
+__shared__ uint32_t s_rsq[kRsqrtEstWords];
 
 template <class T>
 __device__ __forceinline__ T* uni_ptr(T* q) {
@@ -166,13 +168,15 @@ struct LayerRef {
 };
 __device__ __forceinline__ LayerRef layer(const DsParams&, int l) { return LayerRef{l}; }
 
-// Copies the layer table into LDS (all threads; a block barrier follows).
+// Copies the layer table and the RSQRTSS table into LDS (all threads; a block
+// barrier follows).
 __device__ __forceinline__ void stage_layers(const DsParams& p) {
     static_assert(sizeof(DsLayer) % 4 == 0, "copied as words");
     const uint32_t* src = reinterpret_cast<const uint32_t*>(p.layers);
     uint32_t* dst = reinterpret_cast<uint32_t*>(s_layers);
     const int words = p.L * (int)(sizeof(DsLayer) / 4);
     for (int i = threadIdx.x; i < words; i += kT) dst[i] = src[i];
+    for (int i = threadIdx.x; i < kRsqrtEstWords; i += kT) s_rsq[i] = kRsqrtEstTab[i];
     __syncthreads();
 }
 
@@ -200,8 +204,11 @@ __host__ __device__ inline AccOff acc_off(int H, int F, int Hq, int Hkv) {
     return a;
 }
 
+constexpr int kChainLd = (kJ * 4 * kT / 8 + 27) / 32 * 32 + 4;  // chain_ld of the longest row
+
 struct Shared {
     int8_t codes[8192] __attribute__((aligned(16)));
+    float chain[8 * kChainLd] __attribute__((aligned(16)));  // the row being normalized
     int red_i[kW][64];
     float red_a[kW], red_b[kW];
     int red_c[kW];
@@ -580,71 +587,68 @@ __device__ __forceinline__ uint32_t pack4(int c0, int c1, int c2, int c3) {
 }
 
 // Normalizes v (K elements, zeros past K; rms_norm_raw :148-166 with weight w
-// when has_w) and quantizes it into s.codes (QMAX 31: build_lut :28-42; QMAX 127:
-// compute_logits :1666-1678). The sum of squares is taken in the fixed order
-// of the CPU oracle (orc_sumsq): thread t's chains p0..p3 over its groups are
-// the partials 4t..4t+3, then the balanced tree in index order.
+// when has_w, in the reference build's arithmetic: see common.h) and quantizes
+// it into s.codes (QMAX 31: build_lut :28-42; QMAX 127: compute_logits
+// :1666-1678). The row goes to LDS in chain layout and wave 0 sums its squares
+// in the reference build's order; meanwhile every wave forms the weighted
+// products p = x * w and their largest magnitude. Rounding is monotonic and
+// inv_rms > 0, so the absmax of the normalized row, max |p * inv_rms|, is
+// max |p| * inv_rms rounded once: that reduction overlaps the chains.
 template <int QMAX>
 __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const float4 (&w)[kJ],
                                            bool has_w, int K, float eps, float& inv_out,
                                            int& csum_out) {
     const int t = ltid(), lane = t & 63, wave = lwave();
     int J = wave_groups(K);  // groups this wave holds (made opaque again per loop)
-    float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+    const int ld = chain_ld(K);
+    float pmax = 0.0f;
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
         if (j < J) {
-            p0 = __builtin_fmaf(v[j].x, v[j].x, p0);
-            p1 = __builtin_fmaf(v[j].y, v[j].y, p1);
-            p2 = __builtin_fmaf(v[j].z, v[j].z, p2);
-            p3 = __builtin_fmaf(v[j].w, v[j].w, p3);
+            const int i = 4 * (t + kT * j);
+            s.chain[chain_pos(i, ld)] = v[j].x;
+            s.chain[chain_pos(i + 1, ld)] = v[j].y;
+            s.chain[chain_pos(i + 2, ld)] = v[j].z;
+            s.chain[chain_pos(i + 3, ld)] = v[j].w;
         }
-    float ss = wave_sum_tree((p0 + p1) + (p2 + p3));
-    if (lane == 0) s.red_a[wave] = ss;
-    __syncthreads();
-    static_assert(kW == 4, "the cross-wave sums below are for 4 waves");
-    ss = (s.red_a[0] + s.red_a[1]) + (s.red_a[2] + s.red_a[3]);
-    const float inv_rms = inv_rms_from_sumsq(ss, K, eps);
-    float amax = QMAX == 31 ? 1e-6f : 1e-8f;
     asm volatile("" : "+s"(J));
     if (has_w) {  // (one branch for the stage, not one per group)
 #pragma unroll
         for (int j = 0; j < kJ; ++j)
             if (j < J) {
-                float4 y = make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
-                                       __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
-                y.x = __fmul_rn(y.x, w[j].x);
-                y.y = __fmul_rn(y.y, w[j].y);
-                y.z = __fmul_rn(y.z, w[j].z);
-                y.w = __fmul_rn(y.w, w[j].w);
-                v[j] = y;
-                amax = fmaxf(amax,
-                             fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+                v[j] = make_float4(__fmul_rn(v[j].x, w[j].x), __fmul_rn(v[j].y, w[j].y),
+                                   __fmul_rn(v[j].z, w[j].z), __fmul_rn(v[j].w, w[j].w));
+                pmax = fmaxf(pmax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
+                                         fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
             }
     } else {
 #pragma unroll
         for (int j = 0; j < kJ; ++j)
-            if (j < J) {
-                const float4 y =
-                    make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
-                                __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
-                v[j] = y;
-                amax = fmaxf(amax,
-                             fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
-            }
+            if (j < J)
+                pmax = fmaxf(pmax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
+                                         fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
     }
-    amax = wave_max(amax);
-    if (lane == 0) s.red_b[wave] = amax;
+    pmax = wave_max(pmax);
+    if (lane == 0) s.red_b[wave] = pmax;
     __syncthreads();
-    amax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
+    if (wave == 0) {
+        const float inv = inv_rms_ref(chain_sumsq(s.chain, ld, K), K, eps, s_rsq);
+        if (lane == 0) s.red_a[0] = inv;
+    }
+    __syncthreads();
+    const float inv_rms = s.red_a[0];
+    pmax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
+    const float amax = fmaxf(QMAX == 31 ? 1e-6f : 1e-8f, __fmul_rn(pmax, inv_rms));
     const float scale = (float)QMAX / amax;
     int csum = 0;
     asm volatile("" : "+s"(J));
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
         if (j < J) {
-            const int c0 = act_code<QMAX>(v[j].x, scale), c1 = act_code<QMAX>(v[j].y, scale);
-            const int c2 = act_code<QMAX>(v[j].z, scale), c3 = act_code<QMAX>(v[j].w, scale);
+            const float4 y = make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
+                                         __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
+            const int c0 = act_code<QMAX>(y.x, scale), c1 = act_code<QMAX>(y.y, scale);
+            const int c2 = act_code<QMAX>(y.z, scale), c3 = act_code<QMAX>(y.w, scale);
             *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) = pack4(c0, c1, c2, c3);
             csum += (c0 + c1) + (c2 + c3);
         }

@@ -95,26 +95,47 @@ __device__ __forceinline__ float act_in(const float* __restrict__ xm, int64_t K,
     return xm[i];
 }
 
+// Rows up to this length are staged in LDS (chain layout) for the sum of
+// squares; longer rows (the operator entry points accept any length) run the
+// same chains from memory.
+constexpr int64_t kChainMaxK = 16128;  // 8 * chain_ld(K) floats fit in 64 KiB
+
+// inv_rms of rms_norm_raw for row xm (act_in values), in the reference build's
+// arithmetic. ct: dynamic LDS of 8 * chain_ld(K) floats when K <= kChainMaxK.
+// All 256 threads call it; the row is in ct (chain layout) afterwards.
 template <int MODE>
-__device__ __forceinline__ float act_sumsq(const float* __restrict__ xm, int64_t K, float* red) {
-    if (MODE != 3) return block256_sumsq(xm, K, red);
-    // same order as block256_sumsq, on the relu^2 * up values
+__device__ __forceinline__ float act_inv_rms(const float* __restrict__ xm, int64_t K, float eps,
+                                             float* ct, float* s_inv) {
     const int t = threadIdx.x;
-    float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int64_t i = 4 * t; i < K; i += 1024)
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-            if (i + k < K) {
-                const float v = act_in<3>(xm, K, i + k);
-                p[k] = __builtin_fmaf(v, v, p[k]);
+    if (K <= kChainMaxK) {
+        const int ld = chain_ld(K);
+        for (int64_t i = t; i < K; i += 256) ct[chain_pos(i, ld)] = act_in<MODE>(xm, K, i);
+        __syncthreads();
+        if (t < 64) {
+            const float ss = chain_sumsq(ct, ld, K);
+            if (t == 0) *s_inv = inv_rms_ref(ss, K, eps, kRsqrtEstTab);
+        }
+    } else if (t < 64) {
+        // chain j = t % 8 over elements j, j + 8, ... from memory
+        const int j = t & 7;
+        const int64_t n8 = K >> 3;
+        float s = 0.0f;
+        for (int64_t k = 0; k < n8; ++k) {
+            const float v = act_in<MODE>(xm, K, 8 * k + j);
+            s = __builtin_fmaf(v, v, s);
+        }
+        if (j == 0)
+            for (int64_t i = 8 * n8; i < K; ++i) {
+                const float v = act_in<MODE>(xm, K, i);
+                s = __builtin_fmaf(v, v, s);
             }
-    float s = (p[0] + p[1]) + (p[2] + p[3]);
-    s = wave_sum_tree(s);
-    if ((t & 63) == 0) red[t >> 6] = s;
+        const float c0 = lane_f(s, 0), c1 = lane_f(s, 1), c2 = lane_f(s, 2), c3 = lane_f(s, 3);
+        const float c4 = lane_f(s, 4), c5 = lane_f(s, 5), c6 = lane_f(s, 6), c7 = lane_f(s, 7);
+        const float ss = ((c0 + c4) + (c2 + c6)) + ((c1 + c5) + (c3 + c7));
+        if (t == 0) *s_inv = inv_rms_ref(ss, K, eps, kRsqrtEstTab);
+    }
     __syncthreads();
-    float r = (red[0] + red[1]) + (red[2] + red[3]);
-    __syncthreads();
-    return r;
+    return *s_inv;
 }
 
 template <int MODE, int QMAX>
@@ -122,13 +143,15 @@ __global__ void __launch_bounds__(256)
 actquant_kernel(const float* __restrict__ x, const float* __restrict__ w, float eps, int64_t K,
                 int64_t Kp, int8_t* __restrict__ codes, tenzo_hip_actq_t* __restrict__ q,
                 float* __restrict__ y_out) {
+    extern __shared__ float ct[];  // chain layout of the row (MODE >= 1, K <= kChainMaxK)
     __shared__ float redf[4];
     __shared__ int redi[4];
+    __shared__ float s_inv;
     const int t = threadIdx.x;
     const int64_t m = blockIdx.x;
     const float* xm = x + m * (MODE == 3 ? 2 * K : K);
     float inv_rms = 1.0f;
-    if (MODE >= 1) inv_rms = inv_rms_from_sumsq(act_sumsq<MODE>(xm, K, redf), K, eps);
+    if (MODE >= 1) inv_rms = act_inv_rms<MODE>(xm, K, eps, ct, &s_inv);
     if (MODE == 2) {
         for (int64_t i = t; i < K; i += 256) y_out[m * K + i] = norm_apply(xm[i], inv_rms, w, i);
         return;
@@ -161,6 +184,11 @@ actquant_kernel(const float* __restrict__ x, const float* __restrict__ w, float 
         q[m].inv_scale = __fmul_rn(amax, 1.0f / (float)QMAX);
         q[m].code_sum = csum;
     }
+}
+
+// Dynamic LDS of actquant_kernel for a row of K.
+static size_t actquant_lds(int mode, int64_t K) {
+    return mode >= 1 && K <= kChainMaxK ? (size_t)8 * chain_ld(K) * 4 : 0;
 }
 
 // The same quantization with the row held in registers: thread t loads its
@@ -197,23 +225,29 @@ actquant_reg_kernel(const float* __restrict__ x, const float* __restrict__ w, fl
         }
     }
     if (MODE >= 1) {
-        float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+        // the row into LDS in chain layout; wave 0 sums its squares in the
+        // reference build's order
+        constexpr int LD = (1024 * J / 8 + 27) / 32 * 32 + 4;  // chain_ld(1024 J)
+        __shared__ float ct[8 * LD];
+        __shared__ float s_inv;
+        const int ld = chain_ld(K);
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            if (4 * t + 1024 * j < K) {
-                p0 = __builtin_fmaf(v[j].x, v[j].x, p0);
-                p1 = __builtin_fmaf(v[j].y, v[j].y, p1);
-                p2 = __builtin_fmaf(v[j].z, v[j].z, p2);
-                p3 = __builtin_fmaf(v[j].w, v[j].w, p3);
+            const int64_t i = 4 * t + 1024 * j;
+            if (i < K) {
+                ct[chain_pos(i, ld)] = v[j].x;
+                ct[chain_pos(i + 1, ld)] = v[j].y;
+                ct[chain_pos(i + 2, ld)] = v[j].z;
+                ct[chain_pos(i + 3, ld)] = v[j].w;
             }
         }
-        float ss = (p0 + p1) + (p2 + p3);
-        ss = wave_sum_tree(ss);
-        if ((t & 63) == 0) redf[t >> 6] = ss;
         __syncthreads();
-        ss = (redf[0] + redf[1]) + (redf[2] + redf[3]);
+        if (t < 64) {
+            const float ss = chain_sumsq(ct, ld, K);
+            if (t == 0) s_inv = inv_rms_ref(ss, K, eps, kRsqrtEstTab);
+        }
         __syncthreads();
-        const float inv_rms = inv_rms_from_sumsq(ss, K, eps);
+        const float inv_rms = s_inv;
 #pragma unroll
         for (int j = 0; j < J; ++j) {
             const int64_t i = 4 * t + 1024 * j;
@@ -398,8 +432,8 @@ int launch_actquant(int mode, int qmax, const float* x, const float* norm_w, flo
     }
 #define AQ_CASE(MO, QM)                                                                  \
     if (mode == MO && qmax == QM) {                                                      \
-        hipLaunchKernelGGL((actquant_kernel<MO, QM>), grid, blk, 0, st, x, norm_w, eps, K, Kp, \
-                           codes, q, y_out);                                             \
+        hipLaunchKernelGGL((actquant_kernel<MO, QM>), grid, blk, actquant_lds(MO, K), st, x,  \
+                           norm_w, eps, K, Kp, codes, q, y_out);                         \
         return launch_status("actquant_kernel");                                         \
     }
     AQ_CASE(0, 31) AQ_CASE(1, 31) AQ_CASE(3, 31) AQ_CASE(0, 127) AQ_CASE(1, 127)
@@ -410,7 +444,8 @@ int launch_actquant(int mode, int qmax, const float* x, const float* norm_w, flo
 
 int launch_rmsnorm(const float* x, const float* w, float* y, int64_t dim, float eps,
                    hipStream_t st) {
-    hipLaunchKernelGGL((actquant_kernel<2, 31>), dim3(1), dim3(256), 0, st, x, w, eps, dim, dim,
+    hipLaunchKernelGGL((actquant_kernel<2, 31>), dim3(1), dim3(256), actquant_lds(2, dim), st, x,
+                       w, eps, dim, dim,
                        (int8_t*)nullptr, (tenzo_hip_actq_t*)nullptr, y);
     return launch_status("rmsnorm");
 }

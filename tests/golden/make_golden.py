@@ -68,11 +68,16 @@ def pack_raw_fixture():
     save("tl1_pack_raw", tern=tern, raw=raw, N=np.int64(N), K=np.int64(K), packed=out.view(np.uint8))
 
 
+RMS_DIMS = (2560, 6912, 64, 1, 7, 13, 100, 4100)
+
+
 def rmsnorm_fixture():
+    """rms_norm_raw as the reference build computes it, with and without weights;
+    inputs over several magnitudes (the RSQRTSS estimate's input spans binades)."""
     R = oracle.ref()
     rng = np.random.default_rng(103)
     out = {}
-    for dim in (2560, 6912, 64):
+    for dim in RMS_DIMS:
         x = (rng.standard_normal(dim) * 3).astype(np.float32)
         w = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
         y = np.empty(dim, np.float32)
@@ -358,6 +363,11 @@ def load_tiny_model(z) -> synth.SynthModel:
 
 if __name__ == "__main__":
     oracle.build(ref=True)
+    only = sys.argv[1:]
+    if only:  # e.g. python tests/golden/make_golden.py rmsnorm_fixture
+        for name in only:
+            globals()[name]()
+        sys.exit(0)
     tl1_fixture()
     pack_raw_fixture()
     rmsnorm_fixture()

@@ -83,14 +83,16 @@ def test_rmsnorm_quant31_bit_exact(torch_dev):
     from tenzo_amd import ops
     torch = torch_dev
     rng = np.random.default_rng(4)
-    for K in (2560, 6912, 100):
+    # 16384: the longest row the register path holds; 16390, 20001: rows past
+    # the LDS chain layout (chains read from memory); 101: K % 4 != 0
+    for K in (2560, 6912, 100, 101, 16384, 16390, 20001):
         print(f"rmsnorm_quant31 K={K}", flush=True)
         x = (rng.standard_normal(K) * 3).astype(np.float32)
         w = (1 + 0.1 * rng.standard_normal(K)).astype(np.float32)
         codes, q, y = ops.rmsnorm_quant31(to_dev(torch, x), to_dev(torch, w), want_y=True)
         y = y.cpu().numpy()[0]
         yo = oracle.rms_norm(x, w)
-        np.testing.assert_array_equal(y, yo)  # same summation order as the oracle
+        np.testing.assert_array_equal(y, yo)  # the reference build's arithmetic, as the oracle
         co, invo = oracle.quant31(yo)
         np.testing.assert_array_equal(codes.cpu().numpy()[0, :K], co)
         assert not codes.cpu().numpy()[0, K:].any()
@@ -102,10 +104,14 @@ def test_rmsnorm_quant31_bit_exact(torch_dev):
 def test_rmsnorm_against_reference_goldens(torch_dev):
     from tenzo_amd import ops
     torch = torch_dev
+    from tests.golden.make_golden import RMS_DIMS
     z = np.load(os.path.join(GOLD, "rmsnorm.npz"))
-    for dim in (2560, 6912, 64):
+    for dim in RMS_DIMS:
+        print(f"rmsnorm golden dim={dim}", flush=True)
         y = ops.rmsnorm(to_dev(torch, z[f"x{dim}"]), to_dev(torch, z[f"w{dim}"])).cpu().numpy()
-        np.testing.assert_allclose(y, z[f"y{dim}"], rtol=2e-6, atol=0)
+        np.testing.assert_array_equal(y, z[f"y{dim}"])
+        y0 = ops.rmsnorm(to_dev(torch, z[f"x{dim}"]), None).cpu().numpy()
+        np.testing.assert_array_equal(y0, z[f"ynow{dim}"])
 
 
 def test_host_pointer_shims(torch_dev):

@@ -119,30 +119,114 @@ def test_tl1_gemv_matches_golden_bit_exact():
 
 # ---------------------------------------------------------------- RMSNorm --
 
-def test_sumsq_order_is_the_documented_tree():
-    rng = np.random.default_rng(5)
-    x = rng.standard_normal(6912).astype(np.float32)
-    p = np.zeros(1024, np.float32)
-    for t in range(1024):
+def _rn32(q):
+    """A rational rounded to the nearest float32 (ties to even), exactly."""
+    from fractions import Fraction
+    import math
+    if q == 0:
+        return np.float32(0)
+    e = math.frexp(float(q))[1]            # 2^(e-1) <= |q| < 2^e, up to a rounding of q
+    m = round(q * Fraction(2) ** (24 - e))  # Fraction rounding: half to even
+    return np.float32(float(m) * 2.0 ** (e - 24))
+
+
+def _eight_chain_sumsq(x):
+    """rms_norm_raw's sum of squares as the reference build orders it, each FMA
+    rounded once from its exact value."""
+    from fractions import Fraction
+    n = x.size
+    lanes = [Fraction(0)] * 8
+    for i in range(n // 8 * 8):
+        j = i % 8
+        lanes[j] = Fraction(float(_rn32(lanes[j] + Fraction(float(x[i])) ** 2)))
+    for i in range(n // 8 * 8, n):
+        lanes[0] = Fraction(float(_rn32(lanes[0] + Fraction(float(x[i])) ** 2)))
+    c = [np.float32(v) for v in lanes]
+    return ((c[0] + c[4]) + (c[2] + c[6])) + ((c[1] + c[5]) + (c[3] + c[7]))
+
+
+@pytest.mark.parametrize("n", [1, 5, 8, 13, 64, 100, 2560, 6912])
+def test_sumsq_is_the_eight_chain_order(n):
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * rng.choice([1e-3, 1.0, 50.0], size=n)).astype(np.float32)
+    assert oracle.sumsq(x) == _eight_chain_sumsq(x)
+    # a different order (one chain, index order) rounds differently somewhere
+    if n >= 2560:
         s = np.float32(0)
-        for v in x[t::1024]:
-            s = np.float32(np.float64(v) * np.float64(v) + np.float64(s))  # exact fma, rounded once
-        p[t] = s
-    while p.size > 1:
-        p = (p[0::2] + p[1::2]).astype(np.float32)
-    assert oracle.sumsq(x) == p[0]
+        for v in x:
+            s = _rn32(Fraction_of(s) + Fraction_of(v) ** 2)
+        assert oracle.sumsq(x) != s
+
+
+def Fraction_of(v):
+    from fractions import Fraction
+    return Fraction(float(v))
+
+
+def test_rsqrt_estimate_table():
+    """The RSQRTSS table: the library's and the oracle's copies are one table,
+    the lookup scales exactly with the exponent, the estimate is within the
+    ISA's 1.5 * 2^-12 bound, and the Newton-refined inv_rms is within 2^-21 of
+    1/sqrt. On an Intel host the table reproduces this CPU's RSQRTSS over every
+    positive normal float (gen_rsqrt_est.c check)."""
+    import subprocess
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    a = open(os.path.join(root, "tenzo_amd", "csrc", "rsqrt_est_table.inc")).read()
+    b = open(os.path.join(root, "oracle", "rsqrt_est_table.inc")).read()
+    assert a == b and len(a.split(",")) == 2049
+    rng = np.random.default_rng(7)
+    for v in np.concatenate([rng.uniform(1e-5, 1e4, 2000), 2.0 ** np.arange(-20, 20)]):
+        v = np.float32(v)
+        y0 = oracle.rsqrt_est(v)
+        assert abs(float(y0) * np.sqrt(float(v)) - 1) <= 1.5 * 2 ** -12
+        assert oracle.rsqrt_est(np.float32(v * 4)) == y0 / 2
+    for ss, dim in ((1.0, 1), (2560.0, 2560), (123.456, 6912), (1e-3, 64)):
+        inv = oracle.inv_rms(ss, dim)
+        exact = 1 / np.sqrt(np.float64(np.float32(np.float32(ss) / np.float32(dim)) +
+                                        np.float32(1e-5)))
+        assert abs(inv / exact - 1) < 2 ** -21
+    if "GenuineIntel" not in open("/proc/cpuinfo").read():
+        pytest.skip("the table is the RSQRTSS of an Intel host; this host's estimate differs")
+    exe = os.path.join("/tmp", f"gen_rsqrt_est_{os.getpid()}")
+    subprocess.run(["gcc", "-O2", "-msse", os.path.join(root, "tenzo_amd", "csrc", "gen_rsqrt_est.c"),
+                    "-o", exe], check=True)
+    try:
+        r = subprocess.run([exe, "check"], input=b, capture_output=True, text=True, timeout=120)
+    finally:
+        os.unlink(exe)
+    assert r.returncode == 0 and r.stdout.strip() == "0", r.stdout + r.stderr
 
 
 def test_rms_norm_matches_golden_and_fp64():
+    """Bit-exact against the compiled reference's rms_norm_raw (fixture), and
+    within 1e-6 of the fp64 formula."""
+    from tests.golden.make_golden import RMS_DIMS
     z = gold("rmsnorm")
-    for dim in (2560, 6912, 64):
+    for dim in RMS_DIMS:
         x, w = z[f"x{dim}"], z[f"w{dim}"]
         y = oracle.rms_norm(x, w)
-        np.testing.assert_allclose(y, z[f"y{dim}"], rtol=2e-6, atol=0)
-        np.testing.assert_allclose(oracle.rms_norm(x, None), z[f"ynow{dim}"], rtol=2e-6)
+        np.testing.assert_array_equal(y, z[f"y{dim}"])
+        np.testing.assert_array_equal(oracle.rms_norm(x, None), z[f"ynow{dim}"])
         x64 = x.astype(np.float64)
         exact = x64 / np.sqrt((x64 * x64).mean() + 1e-5) * w
-        np.testing.assert_allclose(y, exact, rtol=2e-6)
+        np.testing.assert_allclose(y, exact, rtol=1e-6)
+
+
+@pytest.mark.ref
+def test_rms_norm_bit_exact_against_live_reference():
+    R = oracle.ref()
+    P = oracle._ptr
+    rng = np.random.default_rng(11)
+    dims = list(range(1, 70)) + [255, 1000, 2560, 4096, 6912, 8192, 8200, 16384]
+    for dim in dims:
+        for scale in (1e-4, 1.0, 40.0):
+            x = (rng.standard_normal(dim) * scale).astype(np.float32)
+            w = (1 + 0.1 * rng.standard_normal(dim)).astype(np.float32)
+            for ww in (w, None):
+                y = np.empty(dim, np.float32)
+                R.ref_rms_norm(P(x), None if ww is None else P(ww), P(y), dim, np.float32(1e-5))
+                np.testing.assert_array_equal(oracle.rms_norm(x, ww), y,
+                                              err_msg=f"dim {dim} scale {scale}")
 
 
 # ---------------------------------------------------------------- KV / RoPE
@@ -373,8 +457,8 @@ STAGES = ["x", "norm_x", "q", "k", "v", "attn_out", "attn_sub", "out", "h1", "po
 def test_decode_stages_against_live_reference():
     """Teacher-forced: every stage of forward_layer_raw is fed the reference's
     own input for that stage and must reproduce the reference's output -
-    bit-exact for everything downstream of integer codes, 2e-6 for the norms
-    (summation order) and 1e-5 for attention (fp32 reduction order)."""
+    bit-exact for the norms and everything downstream of integer codes, and
+    1e-5 for attention (fp32 reduction order)."""
     import ctypes
     from tests.golden.make_golden import layer_struct
     R = oracle.ref()
@@ -414,7 +498,7 @@ def test_decode_stages_against_live_reference():
         x = buf(0)[:H].copy()
         R.ref_engine_layer(e, l)
         r = {n: buf(i) for i, n in enumerate(STAGES)}
-        np.testing.assert_allclose(oracle.rms_norm(x, lw.in_norm), r["norm_x"][:H], rtol=2e-6)
+        np.testing.assert_array_equal(oracle.rms_norm(x, lw.in_norm), r["norm_x"][:H])
         q = lin("q", lw, r["norm_x"][:H], qd, H)
         k = lin("k", lw, r["norm_x"][:H], kvd, H)
         v = lin("v", lw, r["norm_x"][:H], kvd, H)
@@ -424,20 +508,20 @@ def test_decode_stages_against_live_reference():
         np.testing.assert_array_equal(q_rot, r["q"][:qd])
         np.testing.assert_array_equal(k_rot, r["k"][:kvd])
         np.testing.assert_allclose(attn, r["attn_out"][:qd], rtol=1e-5, atol=1e-6)
-        np.testing.assert_allclose(oracle.rms_norm(r["attn_out"][:H], lw.attn_sub_norm),
-                                   r["attn_sub"][:H], rtol=2e-6)
+        np.testing.assert_array_equal(oracle.rms_norm(r["attn_out"][:H], lw.attn_sub_norm),
+                                      r["attn_sub"][:H])
         np.testing.assert_array_equal(lin("o", lw, r["attn_sub"][:H], H, H), r["out"][:H])
         np.testing.assert_array_equal((x + r["out"][:H]).astype(np.float32), r["h1"][:H])
-        np.testing.assert_allclose(oracle.rms_norm(r["h1"][:H], lw.post_norm), r["post_norm"][:H],
-                                   rtol=2e-6)
+        np.testing.assert_array_equal(oracle.rms_norm(r["h1"][:H], lw.post_norm),
+                                      r["post_norm"][:H])
         g = lin("gate", lw, r["post_norm"][:H], F, H)
         u = lin("up", lw, r["post_norm"][:H], F, H)
         np.testing.assert_array_equal(g, r["gate"][:F])
         np.testing.assert_array_equal(u, r["up"][:F])
         relu = np.maximum(g, np.float32(0))
         np.testing.assert_array_equal(((relu * relu) * u).astype(np.float32), r["act"][:F])
-        np.testing.assert_allclose(oracle.rms_norm(r["act"][:F], lw.ffn_sub_norm),
-                                   r["ffn_norm"][:F], rtol=2e-6)
+        np.testing.assert_array_equal(oracle.rms_norm(r["act"][:F], lw.ffn_sub_norm),
+                                      r["ffn_norm"][:F])
         np.testing.assert_array_equal(lin("down", lw, r["ffn_norm"][:F], H, F), r["down"][:H])
         np.testing.assert_array_equal((r["h1"][:H] + r["down"][:H]).astype(np.float32),
                                       buf(0)[:H])
