@@ -317,11 +317,21 @@ TENZO_HIP_API int tenzo_hip_engine_get_logits(struct tenzo_engine_opaque* e, flo
  * out in floats. */
 TENZO_HIP_API int tenzo_hip_engine_get_buffer(struct tenzo_engine_opaque* e, const char* name,
                                               float* out, int64_t n);
+/* Per-layer state of the last step when it ran the persistent kernel (mode 2),
+ * for layer-by-layer checks against a CPU restatement of forward_layer_raw
+ * (TenzoEngine.cpp:1522-1632); no reference counterpart. which: 0 the layer's
+ * input x, 1 h1 = x + out projection, 2 the attention output (fp32, H / qd
+ * floats); the int32 TL1 sums sum_k (w_k + 1) a_k (the activation codes' sum
+ * is not yet subtracted) of 3 q|k|v, 4 the out projection, 5 gate|up, 6 down.
+ * n is the capacity of out in 4-byte words. */
+TENZO_HIP_API int tenzo_hip_engine_get_layer_state(struct tenzo_engine_opaque* e, int layer,
+                                                   int which, void* out, int64_t n);
 /* How a decode step is executed (no reference counterpart; the results are
  * the same up to fp32 reduction order in attention):
  *   2 (default) one persistent cooperative kernel per token, stages separated
  *     by in-kernel barriers (needs cooperative launch, an int8 LM head, MLP
- *     weights in every layer, hidden and ffn <= 8192; otherwise mode 1 runs);
+ *     weights in every layer, hidden and ffn multiples of 64 and <= 8192;
+ *     otherwise mode 1 runs);
  *   1 one kernel per stage, replayed from a captured HIP graph;
  *   0 one kernel per stage, launched eagerly. */
 TENZO_HIP_API int tenzo_hip_engine_set_mode(struct tenzo_engine_opaque* e, int mode);

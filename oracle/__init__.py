@@ -76,6 +76,7 @@ def lib() -> ctypes.CDLL:
             "orc_attention_step": (None, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
             "orc_lm_head": (_F, [_P, _P, _P, _I64, _I64, _P, _P]),
             "orc_argmax": (_I, [_P, _I64]),
+            "orc_rep_penalty": (None, [_P, _I64, _P, _I, _F]),
             "orc_sample_top_k_top_p": (_I, [_P, _I64, _I, _F, _F, _F]),
             "orc_quant_rows_i8": (None, [_P, _I64, _I64, _P, _P]),
             "orc_embed_i8": (None, [_P, _P, _I64, _I, _P]),
@@ -374,6 +375,13 @@ def lm_head(xn, W, scales):
 def argmax(logits) -> int:
     logits = f32(logits)
     return int(lib().orc_argmax(_ptr(logits), logits.size))
+
+
+def rep_penalty(logits, tokens, penalty: float) -> np.ndarray:
+    out = f32(logits).copy()
+    t = np.ascontiguousarray(tokens, np.int32)
+    lib().orc_rep_penalty(_ptr(out), out.size, _ptr(t), int(t.size), float(penalty))
+    return out
 
 
 def quant_rows_i8(E):

@@ -665,6 +665,22 @@ void orc_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes, floa
     }
 }
 
+/* The repetition penalty of sample_top_k_top_p (:1735-1743): applied in place,
+ * once per occurrence, only when penalty != 1. As built (-ffast-math) the
+ * division is hoisted: inv = 1 / penalty once, positive logits times inv,
+ * the others times penalty. */
+void orc_rep_penalty(float* logits, int64_t V, const int32_t* tokens, int n, float penalty) {
+    if (penalty == 1.0f || !tokens || n <= 0) return;
+    const float inv = 1.0f / penalty;
+    for (int k = 0; k < n; ++k) {
+        const int32_t t = tokens[k];
+        if (t >= 0 && t < V) {
+            const float l = logits[t];
+            logits[t] = l > 0.0f ? l * inv : l * penalty;
+        }
+    }
+}
+
 /* sample_top_k_top_p (:1722-1807) for temperature > 0 after the penalty, with
  * the uniform draw r passed in (the reference draws rand()/RAND_MAX there).
  * Top-k by the reference's min-heap rule: the first k logits enter; a later

@@ -36,14 +36,21 @@
  *   orc_q4_0, orc_q8_0, orc_gptq,
  *   orc_awq                          fp64 brute force of each dequant formula +
  *                                    compiled-reference goldens (layout conventions)
- *   orc_q4_0_q8act, orc_quantize_q8_0  no reference counterpart: closed form
- *                                    (fp64 brute force of the block formula); the
- *                                    Q8_0 quantizer follows llama.cpp's published
- *                                    quantize_row_q8_0 and is "parity unpinned"
- *                                    against any reference output
+ *   orc_q4_0_q8act                   no reference counterpart: closed form (fp64
+ *                                    brute force of the block formula)
+ *   orc_quantize_q8_0                llama.cpp's published quantize_row_q8_0 (no
+ *                                    reference counterpart), pinned by the
+ *                                    properties its arithmetic fixes: amax -> +-127,
+ *                                    |q| <= 127, zero block -> d = 0, fp16 scale of
+ *                                    amax/127, half-step reconstruction bound, exact
+ *                                    half-steps away from zero
  *   orc_decode_step                  compiled reference whole-engine step on small
  *                                    configs (logits 1e-3, greedy token equal)
  *   orc_argmax                       brute force (first maximum)
+ *   orc_rep_penalty                  the compiled reference's sampler (its logits
+ *                                    after the penalty, bit-exact) with repeated,
+ *                                    negative, zero and out-of-range tokens + a
+ *                                    check that a true division rounds differently
  *   orc_tern_stats, orc_tern_pack,
  *   orc_tern_bitplanes,
  *   orc_attention_step_tern          compiled reference (bit-exact rows and scales,
@@ -157,6 +164,9 @@ void orc_attention_step_paged(float* q, float* k, const float* v, int8_t* pk, in
 float orc_lm_head(const float* xn, const int8_t* W, const float* scales, int64_t V,
                   int64_t H, float* logits, int8_t* codes);
 int orc_argmax(const float* logits, int64_t V);
+/* Repetition penalty in place (:1735-1743 as built: positive logits times
+ * 1/penalty, others times penalty; per occurrence; skipped at penalty 1). */
+void orc_rep_penalty(float* logits, int64_t V, const int32_t* tokens, int n, float penalty);
 /* load_model_from_files' LM-head quantization (:1925-1941), row-major [V][H]. */
 void orc_quant_rows_i8(const float* E, int64_t V, int64_t H, int8_t* codes, float* scales);
 /* sample_top_k_top_p (:1722-1807), temperature > 0, with the draw r in [0, 1]. */

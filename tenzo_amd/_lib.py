@@ -60,6 +60,7 @@ SIGNATURES = {
     "tenzo_hip_engine_set_rope_theta": (_I, [_P, _F]),
     "tenzo_hip_engine_get_logits": (_I, [_P, _P]),
     "tenzo_hip_engine_get_buffer": (_I, [_P, _S, _P, _I64]),
+    "tenzo_hip_engine_get_layer_state": (_I, [_P, _I, _I, _P, _I64]),
     "tenzo_hip_engine_use_graph": (_I, [_P, _I]),
     "tenzo_hip_engine_set_mode": (_I, [_P, _I]),
     "tenzo_hip_engine_get_mode": (_I, [_P]),

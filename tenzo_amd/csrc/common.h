@@ -250,7 +250,12 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }
 
+// fp16 of an fp32 value that was rounded on its own. The empty asm keeps the
+// compiler from fusing the conversion with the operation that produced f:
+// v_fma_mixlo_f16 would round a product once, straight to fp16, which differs
+// from fp16(fp32(a * b)) where fp32(a * b) sits on an fp16 rounding tie.
 __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    asm volatile("" : "+v"(f));
     return __half_as_ushort(__float2half_rn(f));
 }
 

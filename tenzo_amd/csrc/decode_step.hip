@@ -1480,6 +1480,17 @@ int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
         return TENZO_ERROR_UNSUPPORTED;
     }
     hipError_t e = hipLaunchCooperativeKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
+    if (e == hipErrorIllegalState || e == hipErrorNotSupported) {
+        // The runtime refuses a cooperative launch while another process holds
+        // the device's cooperative-launch resources. The kernel needs no more
+        // than all nwg workgroups resident, which an ordinary launch of this
+        // grid gives on an idle device (one workgroup per CU; ds_grid_size
+        // checked the occupancy); every wait in it is bounded, so a grid that
+        // is not fully resident ends the step with the error word instead of
+        // hanging.
+        (void)hipGetLastError();
+        e = hipLaunchKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
+    }
     if (e != hipSuccess) return hip_fail(e, "hipLaunchCooperativeKernel(decode_step)");
     return TENZO_SUCCESS;
 }

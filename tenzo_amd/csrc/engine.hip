@@ -130,6 +130,7 @@ struct tenzo_engine_opaque {
     int32_t* dec_out = nullptr;  // device tokens of tenzo_hip_engine_decode
     int dec_cap = 0;
     uint64_t* ds_trace = nullptr;  // step trace (tenzo_hip_engine_trace), null when off
+    bool ds_state_valid = false;   // the last step ran the persistent kernel
 
     // batched prefill (tenzo_hip_engine_prefill): rows of up to pf_cap tokens
     int pf_cap = 0;
@@ -749,7 +750,8 @@ int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
 // Whether the persistent kernel can run this model as loaded.
 bool ds_usable(tenzo_engine_t e) {
     if (e->ds_nwg <= 0 || e->kv_kind != 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192 ||
-        e->L > kDsMaxLayers || e->max_seq > ds_max_context(e->Hq / e->Hkv))
+        e->H % 64 || e->F % 64 || e->L > kDsMaxLayers ||
+        e->max_seq > ds_max_context(e->Hq / e->Hkv))
         return false;
     for (const DevLayer& d : e->layers)
         if (!d.mlp) return false;
@@ -818,7 +820,9 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.out_tokens = out_tokens;
     p.step = step;
     TZ_HIP(hipMemsetAsync(e->ds_sync, 0, e->ds_sync_bytes, e->st));
-    return launch_decode_step(p, e->Hq / e->Hkv, e->st);
+    rc = launch_decode_step(p, e->Hq / e->Hkv, e->st);
+    e->ds_state_valid = rc == TENZO_SUCCESS;
+    return rc;
 }
 
 // After a persistent step: the kernel's error word (non-zero when a wait
@@ -854,6 +858,7 @@ int run_step(tenzo_engine_t e, int token, bool head) {
     TZ_HIP(hipMemcpyAsync(e->io_dev, e->io_host, 8, hipMemcpyHostToDevice, e->st));
     int rc;
     e->io_host[3] = 0;
+    e->ds_state_valid = false;
     if (e->mode == 2 && ds_usable(e)) {
         if ((rc = run_persistent(e, head, pos))) return rc;
         TZ_HIP(hipMemcpyAsync(e->io_host + 3, e->ds_sync + ds_error_word(e->L, e->Hkv), 4,
@@ -1442,6 +1447,41 @@ TENZO_HIP_API int tenzo_hip_engine_get_buffer(tenzo_engine_t e, const char* name
     }
     set_error("engine_get_buffer: unknown buffer \"%s\"", name);
     return TENZO_ERROR_INVALID_ARGUMENT;
+}
+
+TENZO_HIP_API int tenzo_hip_engine_get_layer_state(tenzo_engine_t e, int layer, int which,
+                                                   void* out, int64_t n) {
+    TZ_CHECK(e && out, "engine_get_layer_state: null pointer");
+    TZ_CHECK(layer >= 0 && layer < e->L, "engine_get_layer_state: layer %d out of range", layer);
+    TZ_CHECK(e->ds_state_valid,
+             "engine_get_layer_state: the last step did not run the persistent kernel");
+    const int* acc = reinterpret_cast<const int*>(e->ds_sync + ds_sync_words(e->L, e->Hkv));
+    const int64_t qkv = e->qd + 2 * (int64_t)e->kvd;
+    const int64_t stride = qkv + 2 * (int64_t)e->H + 2 * (int64_t)e->F;  // q|k|v, o, gate|up, down
+    const int* al = acc + layer * stride;
+    const float* xs = e->ds_vec;
+    const float* h1s = xs + (size_t)e->L * e->H;
+    const float* attns = h1s + (size_t)e->L * e->H;
+    const void* src = nullptr;
+    int64_t len = 0;
+    switch (which) {
+        case 0: src = xs + (size_t)layer * e->H; len = e->H; break;
+        case 1: src = h1s + (size_t)layer * e->H; len = e->H; break;
+        case 2: src = attns + (size_t)layer * e->qd; len = e->qd; break;
+        case 3: src = al; len = qkv; break;
+        case 4: src = al + qkv; len = e->H; break;
+        case 5: src = al + qkv + e->H; len = 2 * (int64_t)e->F; break;
+        case 6: src = al + qkv + e->H + 2 * (int64_t)e->F; len = e->H; break;
+        default:
+            set_error("engine_get_layer_state: unknown buffer %d", which);
+            return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    TZ_CHECK(n >= len, "engine_get_layer_state: buffer %d needs %lld words", which,
+             (long long)len);
+    TZ_HIP(hipSetDevice(e->dev));
+    TZ_HIP(hipStreamSynchronize(e->st));
+    TZ_HIP(hipMemcpy(out, src, (size_t)len * 4, hipMemcpyDeviceToHost));
+    return TENZO_SUCCESS;
 }
 
 TENZO_HIP_API int tenzo_hip_engine_use_graph(tenzo_engine_t e, int on) {

@@ -240,14 +240,17 @@ __global__ void embed_f32_kernel(const float* __restrict__ E, const int32_t* __r
 }
 
 // :1735-1743, sequential so that repeated tokens compound as in the reference.
+// The reference build (-ffast-math) hoists the division out of the loop: it
+// computes 1 / penalty once (vdivss) and multiplies each positive logit by it.
 __global__ void rep_penalty_kernel(float* __restrict__ logits, int64_t V,
                                    const int32_t* __restrict__ tokens, int n, float penalty) {
     if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const float inv = __fdiv_rn(1.0f, penalty);
     for (int k = 0; k < n; ++k) {
         const int t = tokens[k];
         if (t >= 0 && (int64_t)t < V) {
             const float l = logits[t];
-            logits[t] = l > 0.0f ? __fdiv_rn(l, penalty) : __fmul_rn(l, penalty);
+            logits[t] = l > 0.0f ? __fmul_rn(l, inv) : __fmul_rn(l, penalty);
         }
     }
 }

@@ -289,6 +289,25 @@ class Engine:
                  "logits": c.vocab_size}
         return out[:sizes[name]].copy()
 
+    LAYER_STATE = {"x": (0, np.float32), "h1": (1, np.float32), "attn_out": (2, np.float32),
+                   "acc_qkv": (3, np.int32), "acc_o": (4, np.int32), "acc_gu": (5, np.int32),
+                   "acc_down": (6, np.int32)}
+
+    def layer_state(self, layer: int, name: str) -> np.ndarray:
+        """Layer `layer`'s state from the last persistent step: its input "x",
+        "h1", "attn_out" (fp32), or the int32 TL1 sums sum_k (w_k + 1) a_k
+        "acc_qkv", "acc_o", "acc_gu", "acc_down" (tenzo_hip_engine_get_layer_state)."""
+        which, dt = self.LAYER_STATE[name]
+        c = self.cfg
+        n = max(2 * c.ffn_dim, c.hidden_size + 2 * c.num_kv_heads * 128,
+                c.num_q_heads * 128 + 2 * c.num_kv_heads * 128)
+        out = np.empty(n, dt)
+        self._check(self.L.tenzo_hip_engine_get_layer_state(self.h, int(layer), which, _ptr(out), n),
+                    f"get_layer_state({name})")
+        q, kv, H, F = c.num_q_heads * 128, c.num_kv_heads * 128, c.hidden_size, c.ffn_dim
+        size = {0: H, 1: H, 2: q, 3: q + 2 * kv, 4: H, 5: 2 * F, 6: H}[which]
+        return out[:size].copy()
+
     def trace(self, on: bool = True):
         """Record per-stage barrier timestamps of the persistent kernel."""
         self._check(self.L.tenzo_hip_engine_trace(self.h, int(bool(on))), "engine_trace")

@@ -65,3 +65,32 @@ def test_default_config_matches_reference_defaults():
             cfg.ffn_dim, cfg.vocab_size, cfg.max_seq_len) == (2560, 20, 5, 128, 30, 6912,
                                                               128256, 8192)
     assert cfg.kv_mode == b"int8_fused"
+
+
+REFERENCE = "/root/reference"
+
+
+def test_reference_callers_link_against_the_library(tmp_path):
+    """The reference's own SDK callers (examples/basic_inference.cpp and the
+    CLI src/main_inference.cpp, which also needs its CPU profiler source)
+    compile against include/ (tenzo.hpp, tenzo.h) and link against
+    libtenzo_hip.so unchanged; every engine symbol they import is ours.
+    Link only, nothing is run. Skipped where the reference checkout is absent."""
+    import pytest
+    import subprocess
+    if not os.path.isdir(os.path.join(REFERENCE, "examples")):
+        pytest.skip("reference checkout not present")
+    lib = os.path.join(ROOT, "tenzo_amd")
+    for name, srcs in (("basic_inference", ["examples/basic_inference.cpp"]),
+                       ("main_inference", ["src/main_inference.cpp",
+                                           "src/runtime/MicroarchProfiler.cpp"])):
+        exe = str(tmp_path / name)
+        subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(ROOT, "include"),
+                        "-I", os.path.join(REFERENCE, "src")] +
+                       [os.path.join(REFERENCE, s) for s in srcs] +
+                       ["-L", lib, "-ltenzo_hip", "-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib",
+                        "-o", exe], check=True, timeout=300)
+        undef = subprocess.run(["nm", "-D", "--undefined-only", exe], capture_output=True,
+                               text=True, check=True).stdout
+        imported = {ln.split()[-1] for ln in undef.splitlines() if " tenzo_" in ln}
+        assert imported and imported <= declared_symbols(), imported - declared_symbols()

@@ -235,21 +235,24 @@ def test_engine_prefill_then_decode_equals_steps(eng_mod):
 
 
 def test_engine_repetition_penalty(eng_mod):
+    """The penalty of sample_top_k_top_p (:1735-1743) as the reference build
+    evaluates it (oracle.rep_penalty, pinned to the compiled reference):
+    repeated tokens compound, both signs of logit, out-of-range tokens skipped."""
     sm = synth.make_model(CFG, seed=47, ctx=3)
     with eng_mod.Engine(CFG) as e:
         e.set_model(sm)
         e.step(11)
         base = e.logits()
-        e.reset()
-        e.set_kv_from(sm)
-        best = int(np.argmax(base))
-        past = [best, best, 4]
-        tok = e.step(11, penalty=1.3, past=past)
-        pen = base.copy()
-        for t in past:  # TenzoEngine.cpp:1735-1743, applied per occurrence
-            pen[t] = pen[t] / np.float32(1.3) if pen[t] > 0 else pen[t] * np.float32(1.3)
-        np.testing.assert_array_equal(e.logits(), pen)
-        assert tok == oracle.argmax(pen)
+        order = np.argsort(base)
+        for pen, past in ((1.3, [int(order[-1])] * 2 + [4]),
+                          (0.7, [int(order[0]), int(order[-1]), int(order[-2]), int(order[-2])]),
+                          (1.15, list(order[-40:]) + list(order[:40]) + [-3, CFG.vocab + 2])):
+            e.reset()
+            e.set_kv_from(sm)
+            tok = e.step(11, penalty=pen, past=past)
+            ref = oracle.rep_penalty(base, past, pen)
+            np.testing.assert_array_equal(e.logits(), ref)
+            assert tok == oracle.argmax(ref)
 
 
 def test_engine_f32_lm_head(eng_mod):

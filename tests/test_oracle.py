@@ -391,6 +391,48 @@ def test_quant_gemv_match_golden_and_fp64():
         np.testing.assert_allclose(y, a.astype(np.float64) @ Wd, rtol=1e-4, atol=1e-5)
 
 
+def test_quantize_q8_0_properties():
+    """orc_quantize_q8_0 (llama.cpp's quantize_row_q8_0: d = amax/127 stored as
+    fp16, q = roundf(x * (1/d))) pinned by what its arithmetic fixes, not by a
+    second copy of the formula: the block's largest |x| maps to +-127, every
+    |q| <= 127, a zero block gives d = 0 and zero codes, the scale is the fp16
+    rounding of amax/127, every element is reconstructed within half a step,
+    exact half-steps round away from zero (a power-of-two scale makes x * (1/d)
+    exact), and the sign of each code follows x."""
+    rng = np.random.default_rng(29)
+    K = 32 * 64
+    x = (rng.standard_normal(K) * rng.choice([1e-3, 1.0, 30.0], size=K)).astype(np.float32)
+    x[32:64] = 0.0                                           # a zero block
+    x[64:96] = rng.choice([-1.0, 1.0], 32).astype(np.float32) * np.float32(2.5)  # constant |x|
+    # block 3: scale 2^-3 exactly (amax = 127/8), elements at exact half-steps
+    half = (np.arange(32) % 20 + 0.5).astype(np.float32) * np.float32(0.125)
+    half *= np.where(np.arange(32) % 2, -1, 1).astype(np.float32)
+    half[0] = np.float32(127 / 8)
+    x[96:128] = half
+    out = oracle.quantize_q8_0(x).reshape(K // 32, 34)
+    d16 = out[:, :2].copy().view(np.float16)[:, 0]
+    q = out[:, 2:].view(np.int8).astype(np.int64)
+    xb = x.reshape(K // 32, 32)
+    amax = np.abs(xb).max(axis=1)
+    # scale: fp16 of the fp32 amax/127 (a nearest rounding of the exact ratio)
+    d32 = (amax / np.float32(127)).astype(np.float32)
+    np.testing.assert_array_equal(d16, d32.astype(np.float16))
+    assert np.all(np.abs(q) <= 127)
+    for b in range(K // 32):
+        if amax[b] == 0:
+            assert d16[b] == 0 and not q[b].any()
+            continue
+        j = int(np.argmax(np.abs(xb[b])))
+        assert q[b, j] == (127 if xb[b, j] > 0 else -127)
+        assert np.all(np.sign(q[b]) * np.sign(xb[b]) >= 0)
+        err = np.abs(xb[b].astype(np.float64) - q[b] * np.float64(d32[b]))
+        assert np.all(err <= 0.5 * np.float64(d32[b]) * (1 + 1e-5))
+    # exact half-steps: away from zero
+    k = np.floor(np.abs(half[1:].astype(np.float64)) / 0.125)
+    np.testing.assert_array_equal(np.abs(q[3, 1:]), k + 1)
+    np.testing.assert_array_equal(q[2], np.sign(x[64:96]).astype(np.int64) * 127)
+
+
 def test_q4_0_q8act_closed_form():
     rng = np.random.default_rng(19)
     K, N = 256, 32
@@ -580,6 +622,43 @@ def test_sampler_matches_compiled_reference():
             assert t_orc == t_ref, (trial, k, p, T)
     finally:
         R.ref_engine_destroy(e)
+
+
+@pytest.mark.ref
+def test_rep_penalty_matches_compiled_reference():
+    """orc_rep_penalty against the penalty loop of the reference's own
+    sample_top_k_top_p (:1735-1743) as built: its logits scratch after the
+    call, bit for bit, with repeated tokens (the penalty compounds), negative,
+    zero and out-of-range tokens. The build multiplies positive logits by a
+    hoisted 1/penalty; a true division rounds differently on some of them, so
+    the test tells the two apart."""
+    import ctypes
+    R = oracle.ref()
+    V = 4096
+    e = R.ref_engine_create(128, 1, 1, 1, 64, V, 8)
+    differs = 0
+    try:
+        rng = np.random.default_rng(17)
+        for trial, pen in enumerate([1.3, 0.7, 1.15, 1.1, 2.0, 0.9, 1.05, 3.7] * 6):
+            logits = (rng.standard_normal(V) * rng.uniform(0.5, 8.0)).astype(np.float32)
+            logits[rng.integers(0, V, 20)] = 0.0
+            past = rng.integers(0, V, size=int(rng.integers(1, 200))).astype(np.int32)
+            past = np.concatenate([past, past[:10], [-1, V, V + 5]]).astype(np.int32)
+            t_ref = R.ref_engine_sample(e, logits.ctypes.data_as(ctypes.c_void_p), 0.0, 0.9, 40,
+                                        pen, past.ctypes.data_as(ctypes.c_void_p), past.size)
+            after = np.empty(V, np.float32)
+            R.ref_engine_buf(e, 15, after.ctypes.data_as(ctypes.c_void_p))
+            mine = oracle.rep_penalty(logits, past, pen)
+            np.testing.assert_array_equal(mine, after, err_msg=f"trial {trial} penalty {pen}")
+            assert t_ref == oracle.argmax(mine)
+            div = logits.copy()
+            for t in past:
+                if 0 <= t < V:
+                    div[t] = div[t] / np.float32(pen) if div[t] > 0 else div[t] * np.float32(pen)
+            differs += int((div != mine).any())
+    finally:
+        R.ref_engine_destroy(e)
+    assert differs > 0  # a true division would have failed this test
 
 
 def test_sampler_special_cases():
