@@ -194,52 +194,56 @@ __device__ __forceinline__ int chain_pos(int64_t i, int ld) {
     return (int)(i & 7) * ld + (int)(i >> 3);
 }
 
-// Sum of squares of the n-element row in chain layout, in the reference
-// build's order; called by a whole wave (lane l runs chain l % 8, so every
-// lane's loads hit an address another lane of its row-group also reads), the
-// result is returned in every lane.
-__device__ __forceinline__ float chain_sumsq(const float* ct, int ld, int64_t n) {
+// Sum of squares of the n-element row in chain layout (ct, ld), in the
+// reference build's order (orc_sumsq), by one wave: lanes 0..7 run chains
+// 0..7, one FMA per term. A wave issues about one VALU instruction per 4
+// cycles whether or not it depends on the previous one, so the chains cost
+// about n / 8 FMA issues plus one LDS wait per block of 64 terms. The n % 8
+// tail is added to chain 0; the result is returned in every lane of the wave.
+__device__ __forceinline__ float chain_sumsq_wave(const float* ct, int ld, int64_t n) {
     const int j = threadIdx.x & 7;
-    const int n8 = (int)(n >> 3), nq = n8 >> 2;
-    const float4* row = reinterpret_cast<const float4*>(ct + j * ld);
+    const int n8 = (int)(n >> 3), nq = n8 >> 2;  // whole float4s of a chain
+    constexpr int kB = 16;                        // float4s per block
     float s = 0.0f;
-    if (nq >= 4) {
-        // four float4s per step, the next four loaded while these are summed
-        float4 a0 = row[0], a1 = row[1], a2 = row[2], a3 = row[3];
-        for (int q = 0; q + 4 <= nq; q += 4) {
-            const int nx = min(q + 4, nq - 4);  // (a repeat of the last four at the end)
-            const float4 b0 = row[nx], b1 = row[nx + 1], b2 = row[nx + 2], b3 = row[nx + 3];
-            const float4 a[4] = {a0, a1, a2, a3};
+    // only lanes 0..7 run: an LDS read then returns 8 x 16 bytes instead of
+    // 64 x 16. (Measured on the MI355X for rows of 2560 / 6912: blocks of 16
+    // float4 read together, then their 64 FMAs, beat blocks of 4 or 8 and
+    // explicitly double-buffered blocks, which the compiler turns back into
+    // a wait per block plus register copies.)
+    if ((threadIdx.x & 63) < 8) {
+        const float4* row = reinterpret_cast<const float4*>(ct + j * ld);
+        int q = 0;
+        for (; q + kB <= nq; q += kB) {
+            float4 v[kB];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                s = __builtin_fmaf(a[u].x, a[u].x, s);
-                s = __builtin_fmaf(a[u].y, a[u].y, s);
-                s = __builtin_fmaf(a[u].z, a[u].z, s);
-                s = __builtin_fmaf(a[u].w, a[u].w, s);
+            for (int u = 0; u < kB; ++u) v[u] = row[q + u];
+#pragma unroll
+            for (int u = 0; u < kB; ++u) {
+                s = __builtin_fmaf(v[u].x, v[u].x, s);
+                s = __builtin_fmaf(v[u].y, v[u].y, s);
+                s = __builtin_fmaf(v[u].z, v[u].z, s);
+                s = __builtin_fmaf(v[u].w, v[u].w, s);
             }
-            a0 = b0;
-            a1 = b1;
-            a2 = b2;
-            a3 = b3;
         }
-    }
-    for (int q = nq & ~3; q < nq; ++q) {
-        const float4 a = row[q];
-        s = __builtin_fmaf(a.x, a.x, s);
-        s = __builtin_fmaf(a.y, a.y, s);
-        s = __builtin_fmaf(a.z, a.z, s);
-        s = __builtin_fmaf(a.w, a.w, s);
-    }
-    for (int k = nq * 4; k < n8; ++k) s = __builtin_fmaf(ct[j * ld + k], ct[j * ld + k], s);
-    if (j == 0)
-        for (int t = 0; t < (int)(n & 7); ++t) {
-            const float v = ct[t * ld + n8];
-            s = __builtin_fmaf(v, v, s);
+        for (; q < nq; ++q) {
+            const float4 v = row[q];
+            s = __builtin_fmaf(v.x, v.x, s);
+            s = __builtin_fmaf(v.y, v.y, s);
+            s = __builtin_fmaf(v.z, v.z, s);
+            s = __builtin_fmaf(v.w, v.w, s);
         }
+        for (int k = nq * 4; k < n8; ++k) s = __builtin_fmaf(ct[j * ld + k], ct[j * ld + k], s);
+        if (j == 0)
+            for (int64_t t = (int64_t)n8 * 8; t < n; ++t) {
+                const float v = ct[(int)(t & 7) * ld + n8];
+                s = __builtin_fmaf(v, v, s);
+            }
+    }
     const float c0 = lane_f(s, 0), c1 = lane_f(s, 1), c2 = lane_f(s, 2), c3 = lane_f(s, 3);
     const float c4 = lane_f(s, 4), c5 = lane_f(s, 5), c6 = lane_f(s, 6), c7 = lane_f(s, 7);
     return ((c0 + c4) + (c2 + c6)) + ((c1 + c5) + (c3 + c7));
 }
+
 
 // Signed 8-bit dot of 4 lanes + accumulator (v_dot4_i32_i8).
 __device__ __forceinline__ int sdot4(uint32_t a, int32_t b, int c) {

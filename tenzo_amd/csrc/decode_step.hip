@@ -590,8 +590,9 @@ __device__ __forceinline__ uint32_t pack4(int c0, int c1, int c2, int c3) {
 // when has_w, in the reference build's arithmetic: see common.h) and quantizes
 // it into s.codes (QMAX 31: build_lut :28-42; QMAX 127: compute_logits
 // :1666-1678). The row goes to LDS in chain layout and wave 0 sums its squares
-// in the reference build's order; meanwhile every wave forms the weighted
-// products p = x * w and their largest magnitude. Rounding is monotonic and
+// in the reference build's order (chain_sumsq_wave); before that every wave
+// forms the weighted products p = x * w and their largest magnitude.
+// Rounding is monotonic and
 // inv_rms > 0, so the absmax of the normalized row, max |p * inv_rms|, is
 // max |p| * inv_rms rounded once: that reduction overlaps the chains.
 template <int QMAX>
@@ -632,7 +633,7 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
     if (lane == 0) s.red_b[wave] = pmax;
     __syncthreads();
     if (wave == 0) {
-        const float inv = inv_rms_ref(chain_sumsq(s.chain, ld, K), K, eps, s_rsq);
+        const float inv = inv_rms_ref(chain_sumsq_wave(s.chain, ld, K), K, eps, s_rsq);
         if (lane == 0) s.red_a[0] = inv;
     }
     __syncthreads();

@@ -101,8 +101,9 @@ __device__ __forceinline__ float act_in(const float* __restrict__ xm, int64_t K,
 constexpr int64_t kChainMaxK = 16128;  // 8 * chain_ld(K) floats fit in 64 KiB
 
 // inv_rms of rms_norm_raw for row xm (act_in values), in the reference build's
-// arithmetic. ct: dynamic LDS of 8 * chain_ld(K) floats when K <= kChainMaxK.
-// All 256 threads call it; the row is in ct (chain layout) afterwards.
+// arithmetic. ct: dynamic LDS of 8 * chain_ld(K) floats when K <= kChainMaxK;
+// s_inv: a float of LDS. All 256 threads call it; the row is in ct (chain
+// layout) afterwards.
 template <int MODE>
 __device__ __forceinline__ float act_inv_rms(const float* __restrict__ xm, int64_t K, float eps,
                                              float* ct, float* s_inv) {
@@ -112,7 +113,7 @@ __device__ __forceinline__ float act_inv_rms(const float* __restrict__ xm, int64
         for (int64_t i = t; i < K; i += 256) ct[chain_pos(i, ld)] = act_in<MODE>(xm, K, i);
         __syncthreads();
         if (t < 64) {
-            const float ss = chain_sumsq(ct, ld, K);
+            const float ss = chain_sumsq_wave(ct, ld, K);
             if (t == 0) *s_inv = inv_rms_ref(ss, K, eps, kRsqrtEstTab);
         }
     } else if (t < 64) {
@@ -243,7 +244,7 @@ actquant_reg_kernel(const float* __restrict__ x, const float* __restrict__ w, fl
         }
         __syncthreads();
         if (t < 64) {
-            const float ss = chain_sumsq(ct, ld, K);
+            const float ss = chain_sumsq_wave(ct, ld, K);
             if (t == 0) s_inv = inv_rms_ref(ss, K, eps, kRsqrtEstTab);
         }
         __syncthreads();
