@@ -586,23 +586,64 @@ __device__ __forceinline__ uint32_t pack4(int c0, int c1, int c2, int c3) {
     return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
-// Normalizes v (K elements, zeros past K; rms_norm_raw :148-166 with weight w
-// when has_w, in the reference build's arithmetic: see common.h) and quantizes
-// it into s.codes (QMAX 31: build_lut :28-42; QMAX 127: compute_logits
-// :1666-1678). The row goes to LDS in chain layout and wave 0 sums its squares
-// in the reference build's order (chain_sumsq_wave); before that every wave
-// forms the weighted products p = x * w and their largest magnitude.
-// Rounding is monotonic and
-// inv_rms > 0, so the absmax of the normalized row, max |p * inv_rms|, is
-// max |p| * inv_rms rounded once: that reduction overlaps the chains.
+// Codes of the weighted products p (K elements, zeros past K) for the RMS
+// scale inv_rms into s.codes: amax = max(floor, pmax * inv_rms), code =
+// round(p * inv_rms * (QMAX / amax)) (QMAX 31: build_lut :28-42; QMAX 127:
+// compute_logits :1666-1678); returns this thread's code sum.
 template <int QMAX>
-__device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const float4 (&w)[kJ],
-                                           bool has_w, int K, float eps, float& inv_out,
-                                           int& csum_out) {
-    const int t = ltid(), lane = t & 63, wave = lwave();
-    int J = wave_groups(K);  // groups this wave holds (made opaque again per loop)
-    const int ld = chain_ld(K);
+__device__ __forceinline__ int quant_codes(Shared& s, const float4 (&p)[kJ], int K, float inv_rms,
+                                           float amax) {
+    const int t = ltid();
+    int J = wave_groups(K);
+    const float scale = (float)QMAX / amax;
+    int csum = 0;
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < J) {
+            const float4 y = make_float4(__fmul_rn(p[j].x, inv_rms), __fmul_rn(p[j].y, inv_rms),
+                                         __fmul_rn(p[j].z, inv_rms), __fmul_rn(p[j].w, inv_rms));
+            const int c0 = act_code<QMAX>(y.x, scale), c1 = act_code<QMAX>(y.y, scale);
+            const int c2 = act_code<QMAX>(y.z, scale), c3 = act_code<QMAX>(y.w, scale);
+            *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) = pack4(c0, c1, c2, c3);
+            csum += (c0 + c1) + (c2 + c3);
+        }
+    return csum;
+}
+
+// The products p = x * w (w only when has_w; p = x otherwise) and the
+// largest |p| of this thread.
+__device__ __forceinline__ float weigh(float4 (&p)[kJ], const float4 (&v)[kJ], const float4 (&w)[kJ],
+                                      bool has_w, int K) {
+    int J = wave_groups(K);
     float pmax = 0.0f;
+    if (has_w) {  // (one branch for the stage, not one per group)
+#pragma unroll
+        for (int j = 0; j < kJ; ++j)
+            if (j < J)
+                p[j] = make_float4(__fmul_rn(v[j].x, w[j].x), __fmul_rn(v[j].y, w[j].y),
+                                   __fmul_rn(v[j].z, w[j].z), __fmul_rn(v[j].w, w[j].w));
+    } else {
+#pragma unroll
+        for (int j = 0; j < kJ; ++j)
+            if (j < J) p[j] = v[j];
+    }
+    asm volatile("" : "+s"(J));
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < J)
+            pmax = fmaxf(pmax, fmaxf(fmaxf(fabsf(p[j].x), fabsf(p[j].y)),
+                                     fmaxf(fabsf(p[j].z), fabsf(p[j].w))));
+    return pmax;
+}
+
+// The exact RMS scale of x (rms_norm_raw :148-166 in the reference build's
+// arithmetic, common.h): the row goes to LDS in chain layout and wave 0 sums
+// its squares in the reference build's order. Ends with the result in every
+// thread (two block barriers).
+__device__ __forceinline__ float exact_inv_rms(Shared& s, const float4 (&v)[kJ], int K, float eps) {
+    const int t = ltid(), wave = lwave();
+    int J = wave_groups(K);
+    const int ld = chain_ld(K);
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
         if (j < J) {
@@ -612,52 +653,109 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
             s.chain[chain_pos(i + 2, ld)] = v[j].z;
             s.chain[chain_pos(i + 3, ld)] = v[j].w;
         }
-    asm volatile("" : "+s"(J));
-    if (has_w) {  // (one branch for the stage, not one per group)
-#pragma unroll
-        for (int j = 0; j < kJ; ++j)
-            if (j < J) {
-                v[j] = make_float4(__fmul_rn(v[j].x, w[j].x), __fmul_rn(v[j].y, w[j].y),
-                                   __fmul_rn(v[j].z, w[j].z), __fmul_rn(v[j].w, w[j].w));
-                pmax = fmaxf(pmax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
-                                         fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
-            }
-    } else {
-#pragma unroll
-        for (int j = 0; j < kJ; ++j)
-            if (j < J)
-                pmax = fmaxf(pmax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)),
-                                         fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
-    }
-    pmax = wave_max(pmax);
-    if (lane == 0) s.red_b[wave] = pmax;
     __syncthreads();
     if (wave == 0) {
         const float inv = inv_rms_ref(chain_sumsq_wave(s.chain, ld, K), K, eps, s_rsq);
-        if (lane == 0) s.red_a[0] = inv;
+        if ((t & 63) == 0) s.red_a[0] = inv;
     }
     __syncthreads();
-    const float inv_rms = s.red_a[0];
+    return s.red_a[0];
+}
+
+// Normalizes v (K elements, zeros past K; rms_norm_raw :148-166 with weight w
+// when has_w) and quantizes it into s.codes, returning the code record
+// (inv_scale = amax / QMAX and the code sum). Rounding is monotonic and
+// inv_rms > 0, so the absmax of the normalized row, max |p * inv_rms|, is
+// max |p| * inv_rms rounded once.
+template <int QMAX>
+__device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const float4 (&w)[kJ],
+                                           bool has_w, int K, float eps, float& inv_out,
+                                           int& csum_out) {
+    const int lane = ltid() & 63, wave = lwave();
+    float4 p[kJ];
+    float pmax = wave_max(weigh(p, v, w, has_w, K));
+    if (lane == 0) s.red_b[wave] = pmax;
+    const float inv_rms = exact_inv_rms(s, v, K, eps);  // (its barriers publish red_b)
     pmax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
     const float amax = fmaxf(QMAX == 31 ? 1e-6f : 1e-8f, __fmul_rn(pmax, inv_rms));
-    const float scale = (float)QMAX / amax;
-    int csum = 0;
-    asm volatile("" : "+s"(J));
-#pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < J) {
-            const float4 y = make_float4(__fmul_rn(v[j].x, inv_rms), __fmul_rn(v[j].y, inv_rms),
-                                         __fmul_rn(v[j].z, inv_rms), __fmul_rn(v[j].w, inv_rms));
-            const int c0 = act_code<QMAX>(y.x, scale), c1 = act_code<QMAX>(y.y, scale);
-            const int c2 = act_code<QMAX>(y.z, scale), c3 = act_code<QMAX>(y.w, scale);
-            *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) = pack4(c0, c1, c2, c3);
-            csum += (c0 + c1) + (c2 + c3);
-        }
-    csum = wave_sum_i32(csum);
+    int csum = wave_sum_i32(quant_codes<QMAX>(s, p, K, inv_rms, amax));
     if (lane == 0) s.red_c[wave] = csum;
     __syncthreads();
     csum_out = (s.red_c[0] + s.red_c[1]) + (s.red_c[2] + s.red_c[3]);
     inv_out = amax * (1.0f / (float)QMAX);
+}
+
+// The ±31 codes of norm_quant<31> for a workgroup that needs only the codes
+// (the record comes from another workgroup), without waiting for the
+// sequential sum of squares in the common case.
+//
+// With any positive scale r in place of inv_rms, act_code's product is
+// z_i = fl(p_i r) * fl(31 / fl(pmax r)) = t_i (1 + e), t_i = 31 p_i / pmax,
+// |e| <= 3.01u (u = 2^-24; three roundings, the division correctly rounded),
+// as long as nothing over- or underflows and pmax r stays above the floor
+// 1e-6. The code is a nondecreasing function of z_i (for a given sign) that
+// steps within 2u |z| + 1.5u of each half-integer (the roundings of z and of
+// z + 0.49999997, each within half an ulp). So the codes for r = an estimate
+// of inv_rms (from a sum of squares in any order) and for r = inv_rms itself
+// can differ only where the computed fl(z_i) lies within 9.1u |z_i| + 1.5u
+// of a half-integer; the test below uses 16u |z_i| + 32u. Elements that close
+// are rare; if the row has one, or the estimate is not safely above the
+// floor or not finite, the codes are recomputed with the exact inv_rms.
+// Either way s.codes ends up holding exactly norm_quant<31>'s codes. (A
+// subnormal p_i r gives |z_i| < 2^-100 for both scales: code 0 either way.)
+__device__ __forceinline__ void norm_quant_codes31(Shared& s, float4 (&v)[kJ],
+                                                   const float4 (&w)[kJ], bool has_w, int K,
+                                                   float eps) {
+    const int t = ltid(), lane = t & 63, wave = lwave();
+    float4 p[kJ];
+    float pmax = wave_max(weigh(p, v, w, has_w, K));
+    float ss = 0.0f;
+    int J = wave_groups(K);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < J) {
+            ss = __builtin_fmaf(v[j].x, v[j].x, ss);
+            ss = __builtin_fmaf(v[j].y, v[j].y, ss);
+            ss = __builtin_fmaf(v[j].z, v[j].z, ss);
+            ss = __builtin_fmaf(v[j].w, v[j].w, ss);
+        }
+    ss = wave_sum_tree(ss);
+    if (lane == 0) {
+        s.red_b[wave] = pmax;
+        s.red_a[wave] = ss;
+    }
+    __syncthreads();
+    pmax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
+    ss = (s.red_a[0] + s.red_a[1]) + (s.red_a[2] + s.red_a[3]);
+    const float r = inv_rms_ref(ss, K, eps, s_rsq);
+    const float amax = __fmul_rn(pmax, r);
+    // estimate within 1e-3 of inv_rms (any summation order of K <= 16384
+    // squares), so amax >= 2e-6 keeps the exact amax above the floor
+    bool near = !(amax >= 2e-6f && amax <= 3.0e38f && ss <= 3.0e38f);
+    const float scale = 31.0f / amax;
+    asm volatile("" : "+s"(J));
+#pragma unroll
+    for (int j = 0; j < kJ; ++j)
+        if (j < J) {
+            const float ys[4] = {__fmul_rn(p[j].x, r), __fmul_rn(p[j].y, r),
+                                 __fmul_rn(p[j].z, r), __fmul_rn(p[j].w, r)};
+            int c[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                c[e] = act_code<31>(ys[e], scale);
+                const float a = fabsf(__fmul_rn(ys[e], scale));
+                near |= fabsf((a - floorf(a)) - 0.5f) <= __builtin_fmaf(a, 0x1p-20f, 0x1p-19f);
+            }
+            *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) = pack4(c[0], c[1], c[2], c[3]);
+        }
+    const bool wnear = __any(near);
+    if (lane == 0) s.red_c[wave] = wnear ? 1 : 0;
+    __syncthreads();
+    if ((s.red_c[0] | s.red_c[1] | s.red_c[2] | s.red_c[3]) != 0) {
+        const float inv_rms = exact_inv_rms(s, v, K, eps);
+        (void)quant_codes<31>(s, p, K, inv_rms, fmaxf(1e-6f, __fmul_rn(pmax, inv_rms)));
+        __syncthreads();
+    }
 }
 
 // ---------------------------------------------------------------- GEMV ----
@@ -731,10 +829,20 @@ __device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
     return tot;
 }
 
+// Whether the workgroup whose first task is `first` publishes the code record
+// of a GEMV stage of n tasks: the first workgroup without a task when there is
+// one (it computes nothing else, so the exact sum of squares, the one
+// sequential step of the stage, runs beside the other workgroups' dot
+// products), else the workgroup of task 0.
+__device__ __forceinline__ bool rec_writer(const DsParams& p, int first, int n) {
+    return n < p.nwg ? first == n : first == 0;
+}
+
 // One GEMV stage (QKV, O, GU or DOWN) of layer l for a workgroup whose first
-// task is `first` (< n): builds the stage input, stores the slices of it
-// later stages read, normalizes and quantizes it, publishes the code record
-// (task 0) and adds its tasks' K-slice sums into the accumulators.
+// task is `first` (< n, or the record writer): builds the stage input, stores
+// the slices of it later stages read, quantizes its normalization (exactly,
+// with the record, in the record writer; the codes alone elsewhere) and adds
+// its tasks' K-slice sums into the accumulators.
 __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int first, int n) {
     Shared& s = sh.s;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
@@ -769,12 +877,15 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     float4 nwr[kJ];
     load_norm_w(nwr, Lw.norm(slot), K);
     __builtin_amdgcn_s_barrier();
+    const bool tasks = first < n, rec = rec_writer(p, first, n);
     uint4 tile[kPF];
-    {
+    if (tasks) {
         const int c0 = (first % S) * KSs;
         load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs));
+        wait_vm<kPF>();  // everything but the tile has arrived
+    } else {
+        wait_vm<0>();
     }
-    wait_vm<kPF>();  // everything but the tile has arrived
     float4 xv[kJ];
     if (kind == S_QKV) {
         if (l == 0)
@@ -791,13 +902,17 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     } else {
         finish_act(xv, in, p, l, Lw.sc(4), Lw.sc(5), first, m);
     }
-    float inv;
-    int csum;
-    norm_quant<31>(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps, inv, csum);
-    if (first == 0 && tid == 0) {
-        unsigned* r = p.sync + w_rec(l, slot, p.L, p.Hkv);
-        stcu(r, __float_as_uint(inv));
-        stcu(r + 1, (unsigned)csum);
+    if (rec) {
+        float inv;
+        int csum;
+        norm_quant<31>(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps, inv, csum);
+        if (tid == 0) {
+            unsigned* r = p.sync + w_rec(l, slot, p.L, p.Hkv);
+            stcu(r, __float_as_uint(inv));
+            stcu(r + 1, (unsigned)csum);
+        }
+    } else {
+        norm_quant_codes31(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps);
     }
     int* out = accl + (slot == 0 ? 0 : slot == 1 ? ao.o : slot == 2 ? ao.gu : ao.down);
     for (int t = first; t < n; t += p.nwg) {
@@ -1385,7 +1500,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
                 attn_task<G>(sh, p, l, t / p.C, t % p.C);
                 __syncthreads();
             }
-        } else if (first < n) {
+        } else if (first < n || rec_writer(p, first, n)) {
             tl1_stage(sh, p, kind, l, first, n);
         }
         off = (off + n) % p.nwg;

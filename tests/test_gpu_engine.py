@@ -297,3 +297,47 @@ def test_engine_error_paths(eng_mod):
         bad.kv_mode = mode
         assert not L.tenzo_create_engine(ctypes.byref(bad))
         assert b"kv_mode" in L.tenzo_hip_last_error()
+
+
+@pytest.mark.parametrize("ffn", [1024, 8192])
+def test_persistent_codes_at_rounding_ties(eng_mod, ffn):
+    """Workgroups with GEMV tasks take their +-31 codes from an estimate of the
+    RMS scale and recompute them with the exact one when an element lies
+    within the estimate's error bound of a rounding tie. Here the embedding row
+    of the token holds the values -62..62, each in many places, the first
+    layer's input norm is 1, and so every odd value becomes z = 31 e / 62 = a
+    half-integer: the exact path decides every one. The first layer's q|k|v
+    sums, and every later stage, must still be bit-exact. ffn 8192 gives the
+    gate|up stage 256 tasks, one per workgroup: then the workgroup of task 0
+    computes the record itself."""
+    cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=2, ffn=ffn,
+                             vocab=1000, max_seq=16, theta=10000.0)
+    sm = synth.make_model(cfg, seed=7, ctx=3)
+    tok = 21
+    sm.embed[tok] = (np.arange(cfg.hidden) % 125 - 62).astype(np.int8)
+    sm.layers[0].in_norm[:] = 1.0
+    print(f"persistent ties ffn={ffn}", flush=True)
+    with eng_mod.Engine(cfg) as e:
+        e.set_model(sm)
+        assert e.mode == "persistent"
+        e.step(tok)
+        H, F, qd, kvd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim
+        x = e.layer_state(0, "x")
+        y = oracle.rms_norm(x, sm.layers[0].in_norm)
+        z = np.abs(y * (np.float32(31) / np.abs(y).max()))
+        assert (np.abs(z - np.floor(z) - 0.5) < 1e-5).sum() > cfg.hidden // 3  # at ties
+        for l in range(cfg.n_layers):
+            lw = sm.layers[l]
+            checks = (("acc_qkv", oracle.rms_norm(e.layer_state(l, "x"), lw.in_norm),
+                       [("q", qd), ("k", kvd), ("v", kvd)], H),
+                      ("acc_o", oracle.rms_norm(e.layer_state(l, "attn_out"), lw.attn_sub_norm),
+                       [("o", H)], qd),
+                      ("acc_gu", oracle.rms_norm(e.layer_state(l, "h1"), lw.post_norm),
+                       [("gate", F), ("up", F)], H))
+            for name, inp, mats, K in checks:
+                c, _ = oracle.quant31(inp)
+                acc, off = e.layer_state(l, name), 0
+                for m, rows in mats:
+                    ref = oracle.tl1_gemv_i32(lw.tl1[m], c, rows, K) + np.int32(c.astype(np.int64).sum())
+                    np.testing.assert_array_equal(acc[off:off + rows], ref, err_msg=f"layer {l} {m}")
+                    off += rows
