@@ -322,12 +322,13 @@ __device__ __forceinline__ void wait_vm() {
 
 // Loads kPF chunks per lane of K slice [c0, c1) of TL1 row block rb (KS
 // super-chunks of 64 columns per row block; wave w takes chunks c0+w, c0+w+4,
-// ...). Chunks past c1 read zeros.
+// ...). Chunks past c1 read zeros, and so does every chunk when !live (the
+// loads are issued all the same, with nothing to read).
 __device__ __forceinline__ void load_tl1_tile(uint4 (&pf)[kPF], const uint4* __restrict__ W,
-                                              int rb, int KS, int c0, int c1) {
+                                              int rb, int KS, int c0, int c1, bool live = true) {
     const int lane = ltid() & 63, wave = lwave();
     const __amdgpu_buffer_rsrc_t r =
-        rsrc(W + (size_t)rb * KS * 64, (uint32_t)c1 * 64 * 16);
+        rsrc(W + (size_t)rb * KS * 64, live ? (uint32_t)c1 * 64 * 16 : 0u);
 #pragma unroll
     for (int i = 0; i < kPF; ++i)
         pf[i] = ld16(r, (uint32_t)((c0 + wave + kW * i) * 64 + lane) * 16);
@@ -363,16 +364,14 @@ __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[
 
 // Norm weights (thread t: float4 groups t + 256 j; zeros past K) into registers.
 __device__ __forceinline__ void load_norm_w(float4 (&w)[kJ], const float* nw, int K) {
-    if (!nw) return;
-    const __amdgpu_buffer_rsrc_t r = rsrc(nw, (uint32_t)K * 4);
-    const int t = ltid(), Jw = wave_groups(K);
+    const __amdgpu_buffer_rsrc_t r = rsrc(nw, nw ? (uint32_t)K * 4 : 0u);
+    const int t = ltid();
 #pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < Jw) {
-            const f4v v = __builtin_bit_cast(
-                f4v, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(t + kT * j) * 16, 0, 0));
-            w[j] = make_float4(v.x, v.y, v.z, v.w);
-        }
+    for (int j = 0; j < kJ; ++j) {
+        const f4v v = __builtin_bit_cast(
+            f4v, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(t + kT * j) * 16, 0, 0));
+        w[j] = make_float4(v.x, v.y, v.z, v.w);
+    }
 }
 
 // ------------------------------------------------------------ prologue ----
@@ -391,8 +390,10 @@ __device__ __forceinline__ float gemv_y(int a, int csum, float invsc) {
 }
 
 // A stage input is read in two steps. The issue_* functions start the loads
-// of the float4 groups the wave holds (wave_groups; lanes past K read zeros
-// through the resource bounds) into an InRaw; the caller then issues the
+// of all kJ float4 groups of the thread into an InRaw (groups past K read
+// zeros through the resource bounds; none of these loads sits in a branch: a
+// load under a condition joins a phi whose register copy waits for every
+// outstanding load, the weight tile's included); the caller then issues the
 // stage's weight tile and waits until only the tile is in flight (vector
 // memory operations complete in issue order), and the finish_* functions
 // build the input vector v (zeros past K). The issue and finish steps sit in
@@ -410,17 +411,45 @@ __device__ __forceinline__ void issue_rec(InRaw& in, const DsParams& p, int l, i
     in.csum = ld4i(r, 4);
 }
 
+// Where a GEMV stage's input comes from: x = a float vector (or the gate
+// half of the gate|up accumulators, or for layer 0 the token's row of the
+// packed int8 embedding, 16 bytes every 1 KiB), y = the int32 accumulators
+// added to it (or the up half), rec = the code record of the GEMV they come
+// from. Absent parts (null) read zeros.
+struct InSrc {
+    const void* x;
+    uint32_t xbytes;
+    bool emb;
+    const void* y;
+    uint32_t ybytes;
+    const unsigned* rec;
+};
+
+__device__ __forceinline__ void issue_in(InRaw& in, const InSrc& src) {
+    const int t = ltid();
+    const __amdgpu_buffer_rsrc_t rx = rsrc(src.x, src.xbytes);
+    const __amdgpu_buffer_rsrc_t ry = rsrc(src.y, src.y ? src.ybytes : 0u);
+    const __amdgpu_buffer_rsrc_t rr = rsrc(src.rec, src.rec ? 8u : 0u);
+#pragma unroll
+    for (int j = 0; j < kJ; ++j) {
+        const uint32_t q = (uint32_t)(t + kT * j);
+        in.x[j] = ld16i(rx, src.emb ? (q >> 2) * 1024u : q * 16u);
+        in.y[j] = ld16i(ry, q * 16u);
+    }
+    in.inv = ld4i(rr, 0);
+    in.csum = ld4i(rr, 4);
+}
+
 // x = a float vector, y = int32 accumulators (each K elements; y optional)
 __device__ __forceinline__ void issue_vec2(InRaw& in, const void* xs, const void* ys, int K) {
-    const int t = ltid(), Jw = wave_groups(K);
+    const int t = ltid();
     const __amdgpu_buffer_rsrc_t rx = rsrc(xs, (uint32_t)K * 4);
     const __amdgpu_buffer_rsrc_t ry = rsrc(ys, ys ? (uint32_t)K * 4 : 0u);
 #pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < Jw) {
-            in.x[j] = ld16i(rx, (uint32_t)(t + kT * j) * 16);
-            if (ys) in.y[j] = ld16i(ry, (uint32_t)(t + kT * j) * 16);
-        }
+    for (int j = 0; j < kJ; ++j) {
+        in.x[j] = ld16i(rx, (uint32_t)(t + kT * j) * 16);
+        in.y[j] = ld16i(ry, (uint32_t)(t + kT * j) * 16);
+    }
 }
 
 // v = base + GEMV output (the residual adds :1590, :1628): x = base, y = the
@@ -457,21 +486,11 @@ __device__ __forceinline__ int embed_token(const DsParams& p) {
     return __builtin_amdgcn_readfirstlane(p.io[0]);  // uniform: scalar descriptors
 }
 
-__device__ __forceinline__ void issue_embed(InRaw& in, const DsParams& p) {
-    const int t = ltid(), Jw = wave_groups(p.H);
-    const int tok = embed_token(p);
+// Row `tok` of the packed int8 LM head (lm_head.hip layout: [V/64][H/16][64
+// rows][16 bytes]): 16 bytes every 1 KiB from here.
+__device__ __forceinline__ const void* embed_row(const DsParams& p, int tok) {
     const uint8_t* hb = reinterpret_cast<const uint8_t*>(p.head);
-    const size_t b = tok >> 6, r = tok & 63;
-    // row r of block b: 16 bytes every 1 KiB
-    const __amdgpu_buffer_rsrc_t rr = rsrc(hb + (b * (p.H / 16) * 64 + r) * 16,
-                                           (uint32_t)(p.H / 16) * 1024);
-#pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < Jw) {
-            const int i = 4 * (t + kT * j);
-            in.x[j].x = (int)__builtin_amdgcn_raw_buffer_load_b32(
-                rr, (uint32_t)((i >> 4) * 1024 + (i & 15)), 0, 0);
-        }
+    return hb + ((size_t)(tok >> 6) * (p.H / 16) * 64 + (tok & 63)) * 16;
 }
 
 __device__ __forceinline__ void finish_embed(float4 (&v)[kJ], const InRaw& in, const DsParams& p) {
@@ -480,7 +499,9 @@ __device__ __forceinline__ void finish_embed(float4 (&v)[kJ], const InRaw& in, c
 #pragma unroll
     for (int j = 0; j < kJ; ++j) {
         const bool ok = j < Jw && t + kT * j < K4;
-        const uint32_t w = (uint32_t)in.x[j].x;
+        // the thread's 4 bytes are word t % 4 of the 16 read
+        const i4v x = in.x[j];
+        const uint32_t w = (uint32_t)((t & 2) ? ((t & 1) ? x.w : x.z) : ((t & 1) ? x.y : x.x));
         v[j].x = ok ? (float)(int8_t)(w & 0xff) * es : 0.0f;
         v[j].y = ok ? (float)(int8_t)((w >> 8) & 0xff) * es : 0.0f;
         v[j].z = ok ? (float)(int8_t)((w >> 16) & 0xff) * es : 0.0f;
@@ -512,18 +533,6 @@ __device__ __forceinline__ void store_slices(float* dst, const float4 (&v)[kJ], 
 // relu(gate)^2 * up (:1616-1620) from the gate|up accumulators (x = gate,
 // y = up, record of the GU stage); the last layer's gate and up values are
 // also stored as floats (slices as in store_slices).
-__device__ __forceinline__ void issue_act(InRaw& in, const DsParams& p, const int* acc, int l) {
-    const int t = ltid(), F = p.F, Jw = wave_groups(F);
-    const __amdgpu_buffer_rsrc_t ra = rsrc(acc, (uint32_t)F * 8);
-#pragma unroll
-    for (int j = 0; j < kJ; ++j)
-        if (j < Jw) {
-            in.x[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16);
-            in.y[j] = ld16i(ra, (uint32_t)(t + kT * j) * 16 + (uint32_t)F * 4);
-        }
-    issue_rec(in, p, l, 2);
-}
-
 __device__ __forceinline__ void finish_act(float4 (&v)[kJ], const InRaw& in, const DsParams& p,
                                            int l, float wg, float wu, int f, int m) {
     const bool last = l == p.L - 1;  // only the last layer's gate|up is stored
@@ -858,34 +867,42 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     // the stage input and the norm weights first, then (once every wave has
     // issued those, so no wave's input queues behind another's tile) the
     // first task's weight tile, in flight during the normalization
-    InRaw in;
+    // (the sources are chosen per kind; the loads themselves are one
+    // straight sequence, none under a condition: see InRaw)
+    InSrc src{nullptr, (uint32_t)K * 4, false, nullptr, (uint32_t)K * 4, nullptr};
     if (kind == S_QKV) {
         if (l == 0) {
-            issue_embed(in, p);
+            src.x = embed_row(p, embed_token(p));
+            src.xbytes = (uint32_t)(p.H / 16) * 1024;
+            src.emb = true;
         } else {
-            issue_vec2(in, p.h1s + (size_t)(l - 1) * p.H, accl - ao.stride + ao.down, K);
-            issue_rec(in, p, l - 1, 3);
+            src.x = p.h1s + (size_t)(l - 1) * p.H;
+            src.y = accl - ao.stride + ao.down;
+            src.rec = p.sync + w_rec(l - 1, 3, p.L, p.Hkv);
         }
     } else if (kind == S_O) {
-        issue_vec2(in, p.attns + (size_t)l * p.Hq * kD, nullptr, K);
+        src.x = p.attns + (size_t)l * p.Hq * kD;
     } else if (kind == S_GU) {
-        issue_vec2(in, p.xs + (size_t)l * p.H, accl + ao.o, K);
-        issue_rec(in, p, l, 1);
+        src.x = p.xs + (size_t)l * p.H;
+        src.y = accl + ao.o;
+        src.rec = p.sync + w_rec(l, 1, p.L, p.Hkv);
     } else {
-        issue_act(in, p, accl + ao.gu, l);
+        src.x = accl + ao.gu;
+        src.y = accl + ao.gu + p.F;
+        src.rec = p.sync + w_rec(l, 2, p.L, p.Hkv);
     }
+    InRaw in;
+    issue_in(in, src);
     float4 nwr[kJ];
     load_norm_w(nwr, Lw.norm(slot), K);
     __builtin_amdgcn_s_barrier();
     const bool tasks = first < n, rec = rec_writer(p, first, n);
     uint4 tile[kPF];
-    if (tasks) {
+    {  // (the record writer issues the same loads with nothing to read)
         const int c0 = (first % S) * KSs;
-        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs));
-        wait_vm<kPF>();  // everything but the tile has arrived
-    } else {
-        wait_vm<0>();
+        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs), tasks);
     }
+    wait_vm<kPF>();  // everything but the tile has arrived
     float4 xv[kJ];
     if (kind == S_QKV) {
         if (l == 0)
