@@ -194,44 +194,49 @@ __device__ __forceinline__ int chain_pos(int64_t i, int ld) {
     return (int)(i & 7) * ld + (int)(i >> 3);
 }
 
+// FMAs of the squares of B float4 of a chain row into s, in order; the B
+// LDS reads are issued together, ahead of the FMAs.
+template <int B>
+__device__ __forceinline__ void chain_block(const float4* row, float& s) {
+    float4 v[B];
+#pragma unroll
+    for (int u = 0; u < B; ++u) v[u] = row[u];
+#pragma unroll
+    for (int u = 0; u < B; ++u) {
+        s = __builtin_fmaf(v[u].x, v[u].x, s);
+        s = __builtin_fmaf(v[u].y, v[u].y, s);
+        s = __builtin_fmaf(v[u].z, v[u].z, s);
+        s = __builtin_fmaf(v[u].w, v[u].w, s);
+    }
+}
+
 // Sum of squares of the n-element row in chain layout (ct, ld), in the
 // reference build's order (orc_sumsq), by one wave: lanes 0..7 run chains
-// 0..7, one FMA per term. A wave issues about one VALU instruction per 4
-// cycles whether or not it depends on the previous one, so the chains cost
-// about n / 8 FMA issues plus one LDS wait per block of 64 terms. The n % 8
-// tail is added to chain 0; the result is returned in every lane of the wave.
+// 0..7, one FMA per term. The chains are bound by the latency of dependent
+// FMAs (about 8 cycles each on the MI355X: 1.07 us for n = 2560, 2.88 us for
+// 6912, measured), so the LDS reads only have to stay out of their way: a
+// block of 16 float4 per lane is read before its 64 FMAs (one LDS wait per
+// block), and what is left of a row goes in blocks of 8 and 4 rather than
+// one float4 (one wait) at a time. Only lanes 0..7 read: an LDS read then
+// returns 8 x 16 bytes instead of 64 x 16. The n % 8 tail is added to chain
+// 0; the result is returned in every lane of the wave.
 __device__ __forceinline__ float chain_sumsq_wave(const float* ct, int ld, int64_t n) {
     const int j = threadIdx.x & 7;
     const int n8 = (int)(n >> 3), nq = n8 >> 2;  // whole float4s of a chain
-    constexpr int kB = 16;                        // float4s per block
     float s = 0.0f;
-    // only lanes 0..7 run: an LDS read then returns 8 x 16 bytes instead of
-    // 64 x 16. (Measured on the MI355X for rows of 2560 / 6912: blocks of 16
-    // float4 read together, then their 64 FMAs, beat blocks of 4 or 8 and
-    // explicitly double-buffered blocks, which the compiler turns back into
-    // a wait per block plus register copies.)
     if ((threadIdx.x & 63) < 8) {
         const float4* row = reinterpret_cast<const float4*>(ct + j * ld);
         int q = 0;
-        for (; q + kB <= nq; q += kB) {
-            float4 v[kB];
-#pragma unroll
-            for (int u = 0; u < kB; ++u) v[u] = row[q + u];
-#pragma unroll
-            for (int u = 0; u < kB; ++u) {
-                s = __builtin_fmaf(v[u].x, v[u].x, s);
-                s = __builtin_fmaf(v[u].y, v[u].y, s);
-                s = __builtin_fmaf(v[u].z, v[u].z, s);
-                s = __builtin_fmaf(v[u].w, v[u].w, s);
-            }
+        for (; q + 16 <= nq; q += 16) chain_block<16>(row + q, s);
+        if (q + 8 <= nq) {
+            chain_block<8>(row + q, s);
+            q += 8;
         }
-        for (; q < nq; ++q) {
-            const float4 v = row[q];
-            s = __builtin_fmaf(v.x, v.x, s);
-            s = __builtin_fmaf(v.y, v.y, s);
-            s = __builtin_fmaf(v.z, v.z, s);
-            s = __builtin_fmaf(v.w, v.w, s);
+        if (q + 4 <= nq) {
+            chain_block<4>(row + q, s);
+            q += 4;
         }
+        for (; q < nq; ++q) chain_block<1>(row + q, s);
         for (int k = nq * 4; k < n8; ++k) s = __builtin_fmaf(ct[j * ld + k], ct[j * ld + k], s);
         if (j == 0)
             for (int64_t t = (int64_t)n8 * 8; t < n; ++t) {
@@ -243,7 +248,6 @@ __device__ __forceinline__ float chain_sumsq_wave(const float* ct, int ld, int64
     const float c4 = lane_f(s, 4), c5 = lane_f(s, 5), c6 = lane_f(s, 6), c7 = lane_f(s, 7);
     return ((c0 + c4) + (c2 + c6)) + ((c1 + c5) + (c3 + c7));
 }
-
 
 // Signed 8-bit dot of 4 lanes + accumulator (v_dot4_i32_i8).
 __device__ __forceinline__ int sdot4(uint32_t a, int32_t b, int c) {
