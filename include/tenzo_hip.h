@@ -125,6 +125,22 @@ TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
                                              float* out, float* q_rot, float* k_rot,
                                              void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tenzo_hip_attn_int8_decode, same arguments and results,
+ * with its chunk partials in a fixed 8 MiB array of device memory per device
+ * that comes with the library's code object instead of the library scratch;
+ * it calls no allocator. Calls whose partials exceed the array
+ * (B * Hq * chunks * 520 bytes: e.g. B 1 up to ~200k tokens of context, B 16
+ * up to 8k) return TENZO_ERROR_INVALID_ARGUMENT. Every call on a device
+ * shares that device's array: calls that overlap on one device race. */
+TENZO_HIP_API int tenzo_hip_attn_int8_decode_noalloc(const float* q, const float* k_new,
+                                                     const float* v_new, int8_t* kc, int8_t* vc,
+                                                     uint16_t* ks, uint16_t* vs,
+                                                     const float* rope_cs, int B, int Hq, int Hkv,
+                                                     int max_seq, int pos, float* out,
+                                                     float* q_rot, float* k_rot, void* stream);
+
 /* ---- Ternary KV-cache decode attention ----------------------------------- */
 
 /* One decode step of FusedKVCache::forward_attention_raw in the ternary modes

@@ -32,6 +32,8 @@ SIGNATURES = {
     "tenzo_hip_rmsnorm": (_I, [_P, _P, _P, _I64, _F, _P]),
     "tenzo_hip_attn_int8_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                                         _P, _P, _P, _P]),
+    "tenzo_hip_attn_int8_decode_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
+                                                _I, _P, _P, _P, _P]),
     "tenzo_hip_attn_tern_decode": (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I,
                                         _I, _P, _P, _P, _P]),
     "tenzo_hip_attn_paged_int8_decode": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _P, _I,

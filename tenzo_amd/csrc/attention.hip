@@ -15,6 +15,7 @@
 // 16 bytes = dims (l%8)*16 .. +15 of token l/8, so one wave load is 1 KiB of
 // contiguous cache rows.
 #include <algorithm>
+#include <mutex>
 
 #include "attention.h"
 #include "common.h"
@@ -776,6 +777,53 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
 
 using namespace tz;
 
+namespace tz {
+namespace {
+
+// The chunk partials of tenzo_hip_attn_int8_decode_noalloc (kPartStride
+// floats per sequence, query head and chunk): a fixed array in device memory,
+// one copy per device, loaded with the code object and held until the
+// process ends, so the entry point allocates nothing. In host code `scratch`
+// only names the variable: its device address comes from
+// hipGetSymbolAddress, per device.
+constexpr size_t kNoAllocPartFloats = (size_t)2 << 20;  // 8 MiB
+static __device__ __align__(256) float scratch[kNoAllocPartFloats];
+
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+float* g_noalloc_part[kNoAllocMaxDevices];  // device address of `scratch`, per device
+
+// The current device's copy of `scratch` (looked up on the first call on a
+// device, with that device current), or null with the error set.
+float* noalloc_part() {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        hip_fail(e, "attn_int8_decode_noalloc: hipGetDevice");
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kNoAllocMaxDevices) {
+        set_error("attn_int8_decode_noalloc: device %d beyond the %d supported", dev,
+                  kNoAllocMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_part[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                     "attn_int8_decode_noalloc: hipGetSymbolAddress(scratch)");
+            return nullptr;
+        }
+        g_noalloc_part[dev] = static_cast<float*>(ptr);
+    }
+    return g_noalloc_part[dev];
+}
+
+}  // namespace
+}  // namespace tz
+
 extern "C" {
 
 TENZO_HIP_API void tenzo_hip_rope_table(float theta, int head_dim, int pos0, int n_pos,
@@ -797,12 +845,12 @@ TENZO_HIP_API void tenzo_hip_rope_table(float theta, int head_dim, int pos0, int
     }
 }
 
-TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
-                                             const float* v_new, int8_t* kc, int8_t* vc,
-                                             uint16_t* ks, uint16_t* vs, const float* rope_cs,
-                                             int B, int Hq, int Hkv, int max_seq, int pos,
-                                             float* out, float* q_rot, float* k_rot,
-                                             void* stream) {
+// Checks the arguments of the int8 decode entry points and fills L.
+static int attn_int8_args(tz::AttnLaunch& L, const float* q, const float* k_new,
+                          const float* v_new, int8_t* kc, int8_t* vc, uint16_t* ks, uint16_t* vs,
+                          const float* rope_cs, int B, int Hq, int Hkv, int max_seq, int pos,
+                          float* out, float* q_rot, float* k_rot) {
+    using namespace tz;
     TZ_CHECK(q && k_new && v_new && kc && vc && ks && vs && rope_cs && out,
              "attn_int8_decode: null pointer");
     TZ_CHECK(B > 0 && B <= 65535 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0,
@@ -810,7 +858,6 @@ TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
     TZ_CHECK(pos >= 0 && pos < max_seq, "attn_int8_decode: pos %d outside [0, %d)", pos,
              max_seq);
     TZ_CHECK(q_rot != q && k_rot != k_new, "attn_int8_decode: q_rot/k_rot must not alias q/k");
-    AttnLaunch L{};
     L.q = q;
     L.k_new = k_new;
     L.v_new = v_new;
@@ -829,6 +876,42 @@ TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
     L.out = out;
     L.q_rot = q_rot;
     L.k_rot = k_rot;
+    return TENZO_SUCCESS;
+}
+
+TENZO_HIP_API int tenzo_hip_attn_int8_decode(const float* q, const float* k_new,
+                                             const float* v_new, int8_t* kc, int8_t* vc,
+                                             uint16_t* ks, uint16_t* vs, const float* rope_cs,
+                                             int B, int Hq, int Hkv, int max_seq, int pos,
+                                             float* out, float* q_rot, float* k_rot,
+                                             void* stream) {
+    tz::AttnLaunch L{};
+    const int rc = attn_int8_args(L, q, k_new, v_new, kc, vc, ks, vs, rope_cs, B, Hq, Hkv,
+                                  max_seq, pos, out, q_rot, k_rot);
+    if (rc) return rc;
+    return tz::launch_attn(L, (hipStream_t)stream);
+}
+
+TENZO_HIP_API int tenzo_hip_attn_int8_decode_noalloc(const float* q, const float* k_new,
+                                                     const float* v_new, int8_t* kc, int8_t* vc,
+                                                     uint16_t* ks, uint16_t* vs,
+                                                     const float* rope_cs, int B, int Hq, int Hkv,
+                                                     int max_seq, int pos, float* out,
+                                                     float* q_rot, float* k_rot, void* stream) {
+    using namespace tz;
+    AttnLaunch L{};
+    const int rc = attn_int8_args(L, q, k_new, v_new, kc, vc, ks, vs, rope_cs, B, Hq, Hkv,
+                                  max_seq, pos, out, q_rot, k_rot);
+    if (rc) return rc;
+    if (L.max_chunks > 1) {  // (one chunk writes the output directly: no partials)
+        const size_t need = (size_t)B * Hq * L.max_chunks * kPartStride;
+        TZ_CHECK(need <= kNoAllocPartFloats,
+                 "attn_int8_decode_noalloc: %zu bytes of chunk partials (B=%d Hq=%d, %d chunks) "
+                 "exceed its fixed %zu-byte array; use tenzo_hip_attn_int8_decode",
+                 need * 4, B, Hq, L.max_chunks, kNoAllocPartFloats * 4);
+        L.part = noalloc_part();
+        if (!L.part) return TENZO_ERROR_UNSUPPORTED;
+    }
     return launch_attn(L, (hipStream_t)stream);
 }
 
