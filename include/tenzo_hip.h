@@ -192,6 +192,10 @@ TENZO_HIP_API void tenzo_hip_rope_table(float theta, int head_dim, int pos0, int
 /* compute_linear_gguf_q4_0 (:1022-1075): w [N][K/32] blocks of 18 bytes. */
 TENZO_HIP_API int tenzo_hip_gemv_q4_0(const void* act, int act_dtype, const uint8_t* w,
                                       float* y, int K, int N, int B, void* stream);
+/* compute_linear_gguf_q8_0 (:1078-1114): w [N][K/32] blocks of 34 bytes
+ * (fp16 d, 32 int8 codes), 2-byte aligned. */
+TENZO_HIP_API int tenzo_hip_gemv_q8_0(const void* act, int act_dtype, const uint8_t* w,
+                                      float* y, int K, int N, int B, void* stream);
 /* Q4_0 weights x Q8_0 activations (no reference counterpart: the reference
  * has only fp32 activations for Q4_0): qa = B rows of K/32 blocks of 34 bytes. */
 TENZO_HIP_API int tenzo_hip_gemv_q4_0_q8_0(const uint8_t* qa, const uint8_t* w, float* y,

@@ -757,6 +757,13 @@ void orc_embed_i8(const int8_t* E, const float* scales, int64_t H, int token, fl
 /* Quantized GEMVs (:1022-1175)                                               */
 /* ------------------------------------------------------------------------- */
 
+/* tmp[0] + ... + tmp[7] of the reference's Q4_0 / Q8_0 loops (:1072, :1112) as
+ * its build evaluates it (-O3 -ffast-math; the generated code of
+ * oracle/_ref): adjacent pairs, then the pairs of pairs. */
+static float orc_lanes8_sum(const float* t) {
+    return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
 /* :1022-1075. Eight fp32 lanes: lane j takes block elements j, 8+j, 16+j, 24+j;
  * elements 0..15 are the low nibbles of qs[0..15], 16..31 the high nibbles. */
 void orc_q4_0(const float* a, const uint8_t* w, float* y, int K, int N) {
@@ -782,9 +789,7 @@ void orc_q4_0(const float* a, const uint8_t* w, float* y, int K, int N) {
                 acc[j] = fmaf(bd, d, acc[j]);
             }
         }
-        float s = acc[0];
-        for (int j = 1; j < 8; ++j) s += acc[j];
-        y[n] = s;
+        y[n] = orc_lanes8_sum(acc);
     }
 }
 
@@ -803,9 +808,7 @@ void orc_q8_0(const float* a, const uint8_t* w, float* y, int K, int N) {
                 for (int j = 0; j < 8; ++j)
                     acc[j] = fmaf(a[b * 32 + i * 8 + j] * (float)qs[i * 8 + j], d, acc[j]);
         }
-        float s = acc[0];
-        for (int j = 1; j < 8; ++j) s += acc[j];
-        y[n] = s;
+        y[n] = orc_lanes8_sum(acc);
     }
 }
 

@@ -41,6 +41,7 @@ SIGNATURES = {
     "tenzo_hip_engine_block_table": (_I, [_P, _P, _I]),
     "tenzo_hip_rope_table": (None, [_F, _I, _I, _I, _P]),
     "tenzo_hip_gemv_q4_0": (_I, [_P, _I, _P, _P, _I, _I, _I, _P]),
+    "tenzo_hip_gemv_q8_0": (_I, [_P, _I, _P, _P, _I, _I, _I, _P]),
     "tenzo_hip_gemv_q4_0_q8_0": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "tenzo_hip_gemv_gptq": (_I, [_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
     "tenzo_hip_gemv_awq": (_I, [_P, _I, _P, _P, _I, _P, _P, _I, _I, _I, _I, _P]),

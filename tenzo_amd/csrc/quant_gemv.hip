@@ -1,5 +1,5 @@
-// 4-bit quantized GEMVs on gfx950: GGUF Q4_0 (fp32/fp16 or Q8_0
-// activations), GPTQ and AWQ (reference src/runtime/TenzoEngine.cpp:1022-1175).
+// Quantized GEMVs on gfx950: GGUF Q4_0 (fp32/fp16 or Q8_0 activations), GGUF
+// Q8_0, GPTQ and AWQ (reference src/runtime/TenzoEngine.cpp:1022-1175).
 #include "common.h"
 
 namespace tz {
@@ -83,6 +83,89 @@ q4_0_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __
                     dw[4] = hp[8];
                     const float d = half_bits_to_float((uint16_t)(dw[0] & 0xffffu));
                     acc = __builtin_fmaf(q4_block_dot(dw, 0, a_s + bb * 32), d, acc);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+}
+
+// ------------------------------------------------------------------------
+// Q8_0 weights (compute_linear_gguf_q8_0, TenzoEngine.cpp:1078-1114): rows of
+// K/32 blocks of 34 bytes (fp16 d, then 32 int8 codes), y_n = sum_b d_b *
+// sum_j a_j q_j. Eight blocks are 272 bytes = 17 x 16, so whenever a row's
+// group of 8 blocks starts 16-byte aligned (row stride 34 K/32: K % 256 == 0)
+// a lane reads the group with seventeen 16-byte loads; other blocks are read
+// as halfwords. LPR lanes share a row; the activation row is staged in LDS as
+// fp32. A code becomes a float in one conversion of its sign-extended byte.
+// ------------------------------------------------------------------------
+
+__device__ __forceinline__ float sbyte_at(const uint32_t* dw, int o) {
+    return (float)(int)(int8_t)(dw[o >> 2] >> (8 * (o & 3)));
+}
+
+// sum_j a_j q_j of the block whose fp16 scale sits at byte `off` of dw
+__device__ __forceinline__ float q8_block_dot(const uint32_t* dw, int off, const float* a) {
+    const float4* a4 = reinterpret_cast<const float4*>(a);
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const float4 av = a4[j];
+        s = __builtin_fmaf(av.x, sbyte_at(dw, off + 2 + 4 * j), s);
+        s = __builtin_fmaf(av.y, sbyte_at(dw, off + 3 + 4 * j), s);
+        s = __builtin_fmaf(av.z, sbyte_at(dw, off + 4 + 4 * j), s);
+        s = __builtin_fmaf(av.w, sbyte_at(dw, off + 5 + 4 * j), s);
+    }
+    return s;
+}
+
+template <typename TA, int LPR>
+__global__ void __launch_bounds__(256)
+q8_0_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __restrict__ y,
+            int K, int N) {
+    extern __shared__ float a_s[];
+    const int b = blockIdx.y;
+    for (int i = threadIdx.x; i < K; i += 256) a_s[i] = to_f32<TA>(act[(int64_t)b * K + i]);
+    __syncthreads();
+    constexpr int RPB = 256 / LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    const int nbk = K / 32;
+    const int ngroups = (nbk + 7) / 8;
+    float acc = 0.0f;
+    if (row < N) {
+        const uint8_t* rowp = w + (int64_t)row * nbk * 34;
+        for (int g = sub; g < ngroups; g += LPR) {
+            const int b0 = g * 8;
+            if (b0 + 8 <= nbk && (((uintptr_t)(rowp + b0 * 34)) & 15) == 0) {
+                uint32_t dw[68];
+                const uint4* p = reinterpret_cast<const uint4*>(rowp + b0 * 34);
+#pragma unroll
+                for (int i = 0; i < 17; ++i) {
+                    const uint4 v = p[i];
+                    dw[4 * i] = v.x;
+                    dw[4 * i + 1] = v.y;
+                    dw[4 * i + 2] = v.z;
+                    dw[4 * i + 3] = v.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t dbits = (dw[(34 * i) >> 2] >> (8 * ((34 * i) & 3))) & 0xffffu;
+                    const float d = half_bits_to_float((uint16_t)dbits);
+                    acc = __builtin_fmaf(q8_block_dot(dw, 34 * i, a_s + (b0 + i) * 32), d, acc);
+                }
+            } else {
+                for (int bb = b0; bb < nbk && bb < b0 + 8; ++bb) {
+                    // 34 bytes, 2-byte aligned: assembled from halfwords
+                    const uint16_t* hp = reinterpret_cast<const uint16_t*>(rowp + bb * 34);
+                    uint32_t dw[9];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) dw[i] = hp[2 * i] | ((uint32_t)hp[2 * i + 1] << 16);
+                    dw[8] = hp[16];
+                    const float d = half_bits_to_float((uint16_t)(dw[0] & 0xffffu));
+                    acc = __builtin_fmaf(q8_block_dot(dw, 0, a_s + bb * 32), d, acc);
                 }
             }
         }
@@ -264,6 +347,24 @@ static int launch_q4_0(const TA* act, const uint8_t* w, float* y, int K, int N, 
     return launch_status("q4_0_kernel");
 }
 
+template <typename TA>
+static int launch_q8_0(const TA* act, const uint8_t* w, float* y, int K, int N, int B,
+                       hipStream_t st) {
+    const int nbk = K / 32;
+    const int lpr = pick_lpr((nbk + 7) / 8);
+    const size_t smem = (size_t)K * 4;
+    dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
+#define Q80_CASE(L)                                                                   \
+    case L:                                                                           \
+        hipLaunchKernelGGL((q8_0_kernel<TA, L>), grid, dim3(256), smem, st, act, w, y, K, N); \
+        break;
+    switch (lpr) {
+        Q80_CASE(1) Q80_CASE(2) Q80_CASE(4) Q80_CASE(8) Q80_CASE(16) Q80_CASE(32) Q80_CASE(64)
+    }
+#undef Q80_CASE
+    return launch_status("q8_0_kernel");
+}
+
 template <bool AWQ, typename TA, typename TS>
 static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
                      const uint32_t* qzeros, float* y, int K, int N, int group, int B,
@@ -340,6 +441,19 @@ TENZO_HIP_API int tenzo_hip_gemv_q4_0(const void* act, int act_dtype, const uint
     hipStream_t st = (hipStream_t)stream;
     if (act_dtype == 0) return launch_q4_0((const float*)act, w, y, K, N, B, st);
     return launch_q4_0((const uint16_t*)act, w, y, K, N, B, st);
+}
+
+TENZO_HIP_API int tenzo_hip_gemv_q8_0(const void* act, int act_dtype, const uint8_t* w,
+                                      float* y, int K, int N, int B, void* stream) {
+    TZ_CHECK(act && w && y, "gemv_q8_0: null pointer");
+    TZ_CHECK(K > 0 && K % 32 == 0 && N > 0 && B > 0 && B <= 65535,
+             "gemv_q8_0: need K %% 32 == 0 (K=%d)", K);
+    TZ_CHECK(K <= 16384, "gemv_q8_0: K=%d above the LDS staging limit 16384", K);
+    TZ_CHECK(((uintptr_t)w & 1) == 0, "gemv_q8_0: weights must be 2-byte aligned");
+    TZ_CHECK(act_dtype == 0 || act_dtype == 1, "gemv_q8_0: act_dtype must be 0 or 1");
+    hipStream_t st = (hipStream_t)stream;
+    if (act_dtype == 0) return launch_q8_0((const float*)act, w, y, K, N, B, st);
+    return launch_q8_0((const uint16_t*)act, w, y, K, N, B, st);
 }
 
 TENZO_HIP_API int tenzo_hip_gemv_q4_0_q8_0(const uint8_t* qa, const uint8_t* w, float* y,

@@ -217,6 +217,17 @@ def gemv_q4_0(act: torch.Tensor, w: torch.Tensor, K: int, N: int) -> torch.Tenso
     return y
 
 
+def gemv_q8_0(act: torch.Tensor, w: torch.Tensor, K: int, N: int) -> torch.Tensor:
+    """compute_linear_gguf_q8_0 for B activation rows (fp32 or fp16) of K:
+    w = N rows of K/32 blocks of 34 bytes. Returns [B][N] fp32."""
+    a = act.reshape(-1, K).contiguous()
+    B = a.shape[0]
+    y = torch.empty((B, N), dtype=torch.float32, device=act.device)
+    _lib.check(_lib.load().tenzo_hip_gemv_q8_0(_ptr(a), _dtype_code(a), _ptr(w), _ptr(y), K, N,
+                                               B, _stream()), "gemv_q8_0")
+    return y
+
+
 def gemv_q4_0_q8_0(qa: torch.Tensor, w: torch.Tensor, K: int, N: int) -> torch.Tensor:
     B = qa.numel() // (K // 32 * 34)
     y = torch.empty((B, N), dtype=torch.float32, device=qa.device)

@@ -1,9 +1,16 @@
-"""GGUF Q4_0 (fp16 / fp32 / Q8_0 activations), GPTQ and AWQ GEMVs on the GPU
-against the CPU oracle and the compiled-reference goldens, at the benchmark
-shapes (Q4_0 11008x4096; GPTQ/AWQ K=4096 N=14336 group 128, batch 1 and 8).
-These are fp32 reductions in a different order from the reference, so the
-bar is 1e-3 relative to the largest |y| of the call (outputs near zero are
-sums of cancelling terms)."""
+"""GGUF Q4_0 (fp16 / fp32 / Q8_0 activations), GGUF Q8_0, GPTQ and AWQ GEMVs on
+the GPU against the CPU oracle (bit-exact with the compiled reference for the
+GGUF formats) and the compiled-reference goldens, at the benchmark shapes (Q4_0
+and Q8_0 11008x4096; GPTQ/AWQ K=4096 N=14336 group 128, batch 1 and 8).
+
+These are fp32 reductions in another order than the reference's, so each
+output is held to the forward-error bound of fp32 summation, which no order
+can exceed: with the terms t_k = a_k w_k (w dequantized exactly),
+|y - sum t| <= gamma_n sum |t_k| for any order with n roundings on the
+longest path (gamma_n = n u / (1 - n u), u = 2^-24), so two orders differ by
+at most 2 gamma_n sum |t_k|, taken with n = K + 8. The run prints how much of
+that bound is used, and the north star's 1e-3 (relative to the largest |y|
+of the call) is checked as well."""
 import os
 
 import numpy as np
@@ -30,18 +37,39 @@ def dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-def close(y, ref):
+U = 2.0 ** -24
+
+
+def close(y, ref, a=None, W=None):
+    """y vs ref (both [..., N]); with the activations a [.., K] and the
+    dequantized weights W [N][K], also the summation bound above."""
     y = np.asarray(y, np.float64)
     ref = np.asarray(ref, np.float64)
-    err = np.abs(y - ref).max() / np.abs(ref).max()
-    print(f"  max err / max|y| = {err:.2e}", flush=True)
-    assert err < RTOL
+    err = np.abs(y - ref)
+    rel = err.max() / np.abs(ref).max()
+    msg = f"  max err / max|y| = {rel:.2e}"
+    if W is not None:
+        K = W.shape[1]
+        n = K + 8
+        gamma = n * U / (1 - n * U)
+        mag = np.abs(np.asarray(a, np.float64)) @ np.abs(W).T  # sum_k |a_k w_nk|
+        tol = 2 * gamma * mag
+        used = (err / np.maximum(tol, 1e-300)).max()
+        msg += f", of the summation bound: {used:.2e}"
+        assert (err <= tol).all(), msg
+    print(msg, flush=True)
+    assert rel < RTOL
 
 
-def make_q4(rng, N, K):
+def q4_dense(q, d):
+    return (q.astype(np.float64) - 8) * np.repeat(d.astype(np.float64), 32, axis=1)
+
+
+def make_q4(rng, N, K, dense=False):
     q = rng.integers(0, 16, size=(N, K), dtype=np.uint8)
     d = np.abs(rng.normal(0, 0.01, size=(N, K // 32))).astype(np.float16)
-    return formats.q4_0_pack(q, d)
+    w = formats.q4_0_pack(q, d)
+    return (w, q4_dense(q, d)) if dense else w
 
 
 @pytest.mark.parametrize("N,K", [(64, 32), (100, 256), (11008, 4096), (257, 4128)])
@@ -50,13 +78,37 @@ def test_q4_0_fp16_and_fp32_activations(torch_dev, N, K):
     torch = torch_dev
     print(f"q4_0 N={N} K={K}", flush=True)
     rng = np.random.default_rng(N + K)
-    w = make_q4(rng, N, K)
+    w, W = make_q4(rng, N, K, dense=True)
     a16 = rng.standard_normal(K).astype(np.float16)
-    ref = oracle.q4_0(a16.astype(np.float32), w, K, N)
+    a = a16.astype(np.float32)
+    ref = oracle.q4_0(a, w, K, N)
     y = ops.gemv_q4_0(dev(torch, a16), dev(torch, w), K, N).cpu().numpy()[0]
-    close(y, ref)
-    y32 = ops.gemv_q4_0(dev(torch, a16.astype(np.float32)), dev(torch, w), K, N).cpu().numpy()[0]
-    close(y32, ref)
+    close(y, ref, a, W)
+    y32 = ops.gemv_q4_0(dev(torch, a), dev(torch, w), K, N).cpu().numpy()[0]
+    close(y32, ref, a, W)
+
+
+@pytest.mark.parametrize("N,K,B", [(64, 32, 1), (100, 288, 2), (11008, 4096, 1),
+                                   (11008, 4096, 8), (257, 4128, 1)])
+def test_q8_0_weights(torch_dev, N, K, B):
+    """compute_linear_gguf_q8_0 (TenzoEngine.cpp:1078-1114). K = 288 and 4128
+    leave rows that are not 16-byte aligned or a partial group of 8 blocks
+    (the halfword path); 4096 takes the 16-byte loads."""
+    from tenzo_amd import ops
+    torch = torch_dev
+    print(f"q8_0 N={N} K={K} B={B}", flush=True)
+    rng = np.random.default_rng(3 * N + K + B)
+    q = rng.integers(-127, 128, size=(N, K)).astype(np.int8)
+    d = np.abs(rng.normal(0, 0.01, size=(N, K // 32))).astype(np.float16)
+    w = formats.q8_0_pack(q, d)
+    W = q.astype(np.float64) * np.repeat(d.astype(np.float64), 32, axis=1)
+    a16 = rng.standard_normal((B, K)).astype(np.float16)
+    a = a16.astype(np.float32)
+    ref = np.stack([oracle.q8_0(a[b], w, K, N) for b in range(B)])
+    y = ops.gemv_q8_0(dev(torch, a16), dev(torch, w), K, N).cpu().numpy()
+    close(y, ref, a, W)
+    y32 = ops.gemv_q8_0(dev(torch, a), dev(torch, w), K, N).cpu().numpy()
+    np.testing.assert_array_equal(y32, y)  # the same fp32 activations either way
 
 
 @pytest.mark.parametrize("N,K", [(64, 32), (11008, 4096)])
@@ -79,6 +131,7 @@ def test_quant_gemv_reference_goldens(torch_dev):
     K, N, G = (int(v) for v in z["dims"])
     a = dev(torch, z["a"])
     close(ops.gemv_q4_0(a, dev(torch, z["q4_w"]), K, N).cpu().numpy()[0], z["q4_y"])
+    close(ops.gemv_q8_0(a, dev(torch, z["q8_w"]), K, N).cpu().numpy()[0], z["q8_y"])
     sc = dev(torch, z["scales"])
     for kind, fn in (("gptq", ops.gemv_gptq), ("awq", ops.gemv_awq)):
         y = fn(a, dev(torch, z[f"{kind}_qweight"]), sc, dev(torch, z[f"{kind}_qzeros"]), K, N,
@@ -104,13 +157,23 @@ def test_gptq_awq_benchmark_shape(torch_dev, kind, B):
     y = fn(dev(torch, a), dev(torch, qw), dev(torch, scales16), dev(torch, qz), K, N,
            G).cpu().numpy()
     ofn = oracle.gptq if kind == "gptq" else oracle.awq
+    W = gq_dense(q, zeros, scales16, G, kind)
     for b in range(B):
         ref = ofn(a[b].astype(np.float32), qw, scales16.astype(np.float32), qz, K, N, G)
-        close(y[b], ref)
+        close(y[b], ref, a[b].astype(np.float32), W)
     # batch rows are independent: row b of the batched call equals a batch-1 call
     y1 = fn(dev(torch, a[-1:]), dev(torch, qw), dev(torch, scales16), dev(torch, qz), K, N,
             G).cpu().numpy()
     np.testing.assert_array_equal(y1[0], y[-1])
+
+
+def gq_dense(q, zeros, scales, G, kind):
+    """[N][K] weights of GPTQ (zero = nibble + 1, :1117-1143) or AWQ (zero =
+    nibble, :1146-1175) from the unpacked q [K][N], zeros and scales [K/G][N]."""
+    z = zeros.astype(np.float64) + (1 if kind == "gptq" else 0)
+    s = scales.astype(np.float64)
+    return ((q.astype(np.float64) - np.repeat(z, G, axis=0)[:q.shape[0]]) *
+            np.repeat(s, G, axis=0)[:q.shape[0]]).T
 
 
 def test_gptq_fp32_scales_and_ragged_groups(torch_dev):
@@ -125,8 +188,8 @@ def test_gptq_fp32_scales_and_ragged_groups(torch_dev):
     qw, qz = formats.gptq_pack(q, zeros)
     y = ops.gemv_gptq(dev(torch, a), dev(torch, qw), dev(torch, scales), dev(torch, qz), K, N,
                       G).cpu().numpy()[0]
-    close(y, oracle.gptq(a, qw, scales, qz, K, N, G))
+    close(y, oracle.gptq(a, qw, scales, qz, K, N, G), a, gq_dense(q, zeros, scales, G, "gptq"))
     qw, qz = formats.awq_pack(q, zeros)
     y = ops.gemv_awq(dev(torch, a), dev(torch, qw), dev(torch, scales), dev(torch, qz), K, N,
                      G).cpu().numpy()[0]
-    close(y, oracle.awq(a, qw, scales, qz, K, N, G))
+    close(y, oracle.awq(a, qw, scales, qz, K, N, G), a, gq_dense(q, zeros, scales, G, "awq"))

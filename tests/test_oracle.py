@@ -362,10 +362,10 @@ def test_quant_gemv_match_golden_and_fp64():
     K, N, G = (int(v) for v in z["dims"])
     a = z["a"]
     y = oracle.q4_0(a, z["q4_w"], K, N)
-    np.testing.assert_allclose(y, z["q4_y"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(y, z["q4_y"])  # the compiled reference's own output
     np.testing.assert_allclose(y, dequant_q4_0(z["q4_w"], K, N) @ a, rtol=1e-4, atol=1e-5)
     y = oracle.q8_0(a, z["q8_w"], K, N)
-    np.testing.assert_allclose(y, z["q8_y"], rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(y, z["q8_y"])
     blk = z["q8_w"].reshape(N, K // 32, 34)
     d = blk[:, :, :2].copy().view(np.float16).astype(np.float64)[:, :, 0]
     W8 = (blk[:, :, 2:].view(np.int8).astype(np.float64) * d[:, :, None]).reshape(N, K)
@@ -591,6 +591,29 @@ def _libc():
     libc.rand.restype = ctypes.c_int
     libc.srand.argtypes = [ctypes.c_uint]
     return libc
+
+
+@pytest.mark.skipif(not oracle.ref_available(), reason="compiled reference not built")
+def test_gguf_gemvs_match_compiled_reference():
+    """orc_q4_0 / orc_q8_0 bit for bit against the reference's own
+    compute_linear_gguf_q4_0 / _q8_0 (TenzoEngine.cpp:1022-1114, built with its
+    flags) on shapes of several row and block counts, including the BASELINE
+    config-3 K."""
+    import ctypes
+    from tenzo_amd import formats
+    R = oracle.ref()
+    P = lambda x: x.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+    rng = np.random.default_rng(23)
+    for K, N in ((32, 5), (288, 33), (4096, 96)):
+        a = rng.standard_normal(K).astype(np.float32)
+        d = np.abs(rng.normal(0, 0.02, size=(N, K // 32))).astype(np.float16)
+        w4 = formats.q4_0_pack(rng.integers(0, 16, size=(N, K), dtype=np.uint8), d)
+        w8 = formats.q8_0_pack(rng.integers(-127, 128, size=(N, K)).astype(np.int8), d)
+        y = np.empty(N, np.float32)
+        R.ref_q4_0(P(a), P(w4), P(y), K, N)
+        np.testing.assert_array_equal(oracle.q4_0(a, w4, K, N), y, err_msg=f"q4_0 {K}x{N}")
+        R.ref_q8_0(P(a), P(w8), P(y), K, N)
+        np.testing.assert_array_equal(oracle.q8_0(a, w8, K, N), y, err_msg=f"q8_0 {K}x{N}")
 
 
 @pytest.mark.skipif(not oracle.ref_available(), reason="compiled reference not built")
