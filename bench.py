@@ -47,6 +47,11 @@ def parse():
     ap.add_argument("--ctx", type=int, default=4096)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config kernel leg (BASELINE configs 1, 3, 4, 5)")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="run only the per-config kernel leg (for profiling it)")
+    ap.add_argument("--cpu-configs-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="engine execution mode (one persistent kernel per token, or one "
                          "kernel per stage replayed from a HIP graph / launched eagerly)")
@@ -502,8 +507,252 @@ def tern_bench(torch, e, cfg, host, args):
 
 # ------------------------------------------------------------------- main
 
+# ------------------------------------------------------------ configs leg
+#
+# BASELINE.json's other configs, each timed as a kernel on its own: configs 1
+# (one TL1 GEMV 6912x2560), 3 (Q4_0 11008x4096 with fp16 and Q8_0 activations,
+# and the reference's Q8_0-weight GEMV at the same shape), 4 (GPTQ / AWQ
+# K 4096 x N 14336, group 128, batch 1 and 8) and 5 (INT8-KV decode attention,
+# 20 q / 5 kv heads, batch 1 and 16, context 1k / 8k / 32k). The weights (or
+# caches) are rotated over enough distinct copies that a pass reads >= 1 GiB,
+# so the reads come from HBM rather than the 256 MB last-level cache; every
+# call of a pass is captured into one HIP graph and the graph replayed between
+# two HIP events. Algorithmic bytes per call: the packed weights (scales,
+# zeros) or the cache rows and scales read, plus activations and outputs.
+# The compiled reference's function for each (oracle/_ref) is timed beside it
+# in a child process on the host cores.
+
+GIB = 1 << 30
+
+
+def _copies(nbytes, floor=GIB):
+    return max(2, -(-floor // nbytes))
+
+
+def _per_call(torch, calls, reps=3):
+    return graph_time(torch, lambda: [c() for c in calls], reps) / len(calls)
+
+
+def _entry(alg, t, copies):
+    gbs = alg / t / 1e9
+    return {"alg_bytes": int(alg), "mean_us": round(t * 1e6, 2), "achieved_gbs": round(gbs, 1),
+            "frac": round(gbs / PEAK_HBM_GBS, 4), "copies": int(copies)}
+
+
+def _gguf_dev(torch, gen, copies, N, K, bpb):
+    """copies x N rows of K/32 GGUF blocks of bpb bytes: random codes, fp16
+    scales |N(0, 0.01)|."""
+    nbk = K // 32
+    w = torch.randint(0, 256, (copies, N, nbk, bpb), dtype=torch.uint8, device="cuda",
+                      generator=gen)
+    d = (torch.randn((copies, N, nbk), device="cuda", generator=gen).abs() * 0.01).half()
+    w[..., :2] = d.view(torch.uint8).view(copies, N, nbk, 2)
+    return w
+
+
+def configs_bench(torch):
+    from tenzo_amd import _lib, ops
+    L = _lib.load()
+    P, S = ops._ptr, ops._stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 7)
+    out = {}
+    # config 1: one TL1 GEMV, 6912 x 2560
+    N, K = 6912, 2560
+    nb = ops.tl1_packed_bytes(N, K)
+    c = _copies(nb)
+    W = tl1_random_dev(torch, c * nb, gen).view(c, nb)
+    codes, q, _ = ops.rmsnorm_quant31(torch.randn(K, device="cuda", generator=gen))
+    y = torch.empty(N, device="cuda")
+    t = _per_call(torch, [lambda i=i: ops.bitlinear_tl1_into(codes, q, W[i], 0.0159, N, K, y)
+                          for i in range(c)])
+    out["c1_tl1_6912x2560"] = _entry(N * K // 4 + K + N * 4, t, c)
+    del W
+    # config 3: Q4_0 (fp16 and Q8_0 activations) and Q8_0 weights, 11008 x 4096
+    N, K = 11008, 4096
+    nbk = K // 32
+    y = torch.empty(N, device="cuda")
+    a16 = torch.randn(K, device="cuda", generator=gen).half()
+    c = _copies(N * nbk * 18)
+    W = _gguf_dev(torch, gen, c, N, K, 18)
+    t = _per_call(torch, [lambda i=i: L.tenzo_hip_gemv_q4_0(P(a16), 1, P(W[i]), P(y), K, N, 1,
+                                                            S()) for i in range(c)])
+    out["c3_q4_0_fp16act"] = _entry(N * nbk * 18 + K * 2 + N * 4, t, c)
+    qa = _gguf_dev(torch, gen, 1, 1, K, 34)[0, 0]
+    t = _per_call(torch, [lambda i=i: L.tenzo_hip_gemv_q4_0_q8_0(P(qa), P(W[i]), P(y), K, N, 1,
+                                                                 S()) for i in range(c)])
+    out["c3_q4_0_q8_0act"] = _entry(N * nbk * 18 + nbk * 34 + N * 4, t, c)
+    del W
+    c = _copies(N * nbk * 34)
+    W = _gguf_dev(torch, gen, c, N, K, 34)
+    t = _per_call(torch, [lambda i=i: L.tenzo_hip_gemv_q8_0(P(a16), 1, P(W[i]), P(y), K, N, 1,
+                                                            S()) for i in range(c)])
+    out["c3_q8_0_weights"] = _entry(N * nbk * 34 + K * 2 + N * 4, t, c)
+    del W
+    # config 4: GPTQ / AWQ, K 4096 x N 14336, group 128, fp16 scales
+    K, N, G = 4096, 14336, 128
+    wbytes = K // 8 * N * 4 + K // G * N * 2 + K // G // 8 * N * 4
+    c = _copies(wbytes)
+    qw = torch.randint(-2**31, 2**31 - 1, (c, K // 8, N), dtype=torch.int32, device="cuda",
+                       generator=gen)
+    sc = (torch.randn((c, K // G, N), device="cuda", generator=gen).abs() * 0.01).half()
+    qz = torch.randint(-2**31, 2**31 - 1, (c, K // G // 8, N), dtype=torch.int32, device="cuda",
+                       generator=gen)
+    for kind in ("gptq", "awq"):
+        fn = getattr(L, f"tenzo_hip_gemv_{kind}")
+        for B in (1, 8):
+            a = torch.randn((B, K), device="cuda", generator=gen).half()
+            yb = torch.empty((B, N), device="cuda")
+            t = _per_call(torch, [lambda i=i: fn(P(a), 1, P(qw[i]), P(sc[i]), 1, P(qz[i]), P(yb),
+                                                 K, N, G, B, S()) for i in range(c)])
+            out[f"c4_{kind}_b{B}"] = _entry(wbytes + B * K * 2 + B * N * 4, t, c)
+    del qw, sc, qz
+    # config 5: INT8-KV decode attention, 20 / 5 heads of 128
+    Hq, Hkv = 20, 5
+    cs = ops.rope_table(500000.0, 0, 1)[0].cuda()
+    for B in (1, 16):
+        for ctx in (1024, 8192, 32768):
+            per = B * Hkv * ctx * (2 * 128 + 2 * 2)  # K and V codes + fp16 scales read
+            c = _copies(per)
+            kc = torch.randint(-127, 128, (c, B, Hkv, ctx, 128), dtype=torch.int8,
+                               device="cuda", generator=gen)
+            vc = torch.randint(-127, 128, (c, B, Hkv, ctx, 128), dtype=torch.int8,
+                               device="cuda", generator=gen)
+            ks = (torch.rand((c, B, Hkv, ctx), device="cuda", generator=gen) * 0.03 + 0.01).half()
+            vs = (torch.rand((c, B, Hkv, ctx), device="cuda", generator=gen) * 0.03 + 0.01).half()
+            qv = torch.randn((B, Hq * 128), device="cuda", generator=gen).half().float()
+            kv = torch.randn((B, Hkv * 128), device="cuda", generator=gen)
+            o = torch.empty((B, Hq * 128), device="cuda")
+            pos = ctx - 1
+            t = _per_call(torch, [lambda i=i: L.tenzo_hip_attn_int8_decode(
+                P(qv), P(kv), P(kv), P(kc[i]), P(vc[i]), P(ks[i]), P(vs[i]), P(cs), B, Hq, Hkv,
+                ctx, pos, P(o), None, None, S()) for i in range(c)])
+            out[f"c5_attn_b{B}_ctx{ctx // 1024}k"] = _entry(per + B * (Hq + 2 * Hkv) * 512, t, c)
+            del kc, vc, ks, vs
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_configs(seconds=1.0):
+    """The compiled reference's functions for the same configs on the host (run
+    in a child process: no GPU). Each is timed for about `seconds` (at least
+    two calls after one warm-up) over copies of the weights totalling >= 256 MB
+    where one copy would fit in the host's caches."""
+    import oracle
+    from tenzo_amd import formats
+    if not oracle.ref_available():
+        return {}
+    R = oracle.ref()
+    Pp = oracle._ptr
+    rng = np.random.default_rng(SEED + 7)
+    res = {}
+
+    def clock(name, calls, alg):
+        calls[0]()
+        n, t0 = 0, time.perf_counter()
+        while n < 2 or (time.perf_counter() - t0 < seconds and n < 10000):
+            calls[n % len(calls)]()
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        res[name] = {"us": round(dt * 1e6, 1), "gbs": round(alg / dt / 1e9, 2)}
+
+    N, K = 6912, 2560
+    c = _copies(N * K // 2, 256 << 20)
+    W = rng.integers(-128, 128, size=(c, N * K // 2), dtype=np.int8)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = np.empty(N, np.float32)
+    clock("c1_tl1_6912x2560", [lambda i=i: R.ref_tl1_gemv(Pp(x), Pp(W[i]), K, N, 0.0159, Pp(y))
+                               for i in range(c)], N * K // 4 + K * 4 + N * 4)
+    del W
+    N, K = 11008, 4096
+    nbk = K // 32
+    a = rng.standard_normal(K).astype(np.float16).astype(np.float32)
+    y = np.empty(N, np.float32)
+    for name, bpb, fn in (("c3_q4_0_fp16act", 18, R.ref_q4_0), ("c3_q8_0_weights", 34, R.ref_q8_0)):
+        w = rng.integers(0, 256, size=(N * nbk, bpb), dtype=np.uint8)
+        w[:, :2] = (np.abs(rng.normal(0, 0.01, N * nbk)).astype(np.float16)
+                    .view(np.uint8).reshape(-1, 2))
+        clock(name, [lambda w=w: fn(Pp(a), Pp(w), Pp(y), K, N)], N * nbk * bpb + K * 4 + N * 4)
+    K, N, G = 4096, 14336, 128
+    qw = rng.integers(0, 2**32, size=(K // 8, N), dtype=np.uint32)
+    sc = np.abs(rng.normal(0, 0.01, size=(K // G, N))).astype(np.float16).astype(np.float32)
+    qz = rng.integers(0, 2**32, size=(K // G // 8 + 1, N), dtype=np.uint32)
+    y = np.empty(N, np.float32)
+    wbytes = K // 8 * N * 4 + K // G * N * 4 + K // G // 8 * N * 4
+    for kind in ("gptq", "awq"):
+        fn = getattr(R, f"ref_{kind}")
+        for B in (1, 8):
+            A = rng.standard_normal((B, K)).astype(np.float16).astype(np.float32)
+            clock(f"c4_{kind}_b{B}",
+                  [lambda: [fn(Pp(A[b]), Pp(qw), Pp(sc), Pp(qz), Pp(y), K, N, G)
+                            for b in range(B)]], B * (wbytes + K * 4 + N * 4))
+    Hq, Hkv = 20, 5
+    for B in (1, 16):
+        for ctx in (1024, 8192, 32768):
+            ms = ctx + 1
+            kc = rng.integers(-127, 128, size=(B, Hkv, ms, 128), dtype=np.int8)
+            ks = rng.uniform(0.01, 0.04, size=(B, Hkv, ms)).astype(np.float32)
+            q = rng.standard_normal((B, Hq * 128)).astype(np.float32)
+            k = rng.standard_normal((B, Hkv * 128)).astype(np.float32)
+            reps = max(2, min(20, int(2e8 // (B * Hkv * ctx * 260))))
+            dt = R.ref_attention_int8_time(B, Hq, Hkv, ms, ctx - 1, Pp(kc), Pp(kc), Pp(ks), Pp(ks),
+                                           Pp(q), Pp(k), Pp(k), reps)
+            alg = B * Hkv * ctx * (2 * 128 + 2 * 4)
+            res[f"c5_attn_b{B}_ctx{ctx // 1024}k"] = {"us": round(dt * 1e6, 1),
+                                                      "gbs": round(alg / dt / 1e9, 2)}
+            del kc
+    return res
+
+
+def host_cpu():
+    """CPU model, sockets and physical cores of the host (lscpu), the OpenMP
+    threads and placement the reference legs run with."""
+    info = {}
+    try:
+        import subprocess
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        kv = dict(l.split(":", 1) for l in txt.splitlines() if ":" in l)
+        kv = {k.strip(): v.strip() for k, v in kv.items()}
+        info = {"model": kv.get("Model name"), "sockets": kv.get("Socket(s)"),
+                "cores_per_socket": kv.get("Core(s) per socket"),
+                "threads_per_core": kv.get("Thread(s) per core"), "cpus": kv.get("CPU(s)")}
+    except (OSError, ValueError):
+        pass
+    info["cpus_usable"] = len(os.sched_getaffinity(0))
+    info["omp"] = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OMP_PLACES",
+                                                    "OMP_PROC_BIND")}
+    return info
+
+
+def run_cpu_configs(seconds):
+    """cpu_configs in a child process (OpenMP placed on cores, spread), its
+    JSON line parsed."""
+    import subprocess
+    env = dict(os.environ, OMP_PLACES="cores", OMP_PROC_BIND="spread")
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-configs-child",
+                        "--cpu-seconds", str(seconds)], capture_output=True, text=True,
+                       env=env, timeout=900)
+    lines = [l for l in r.stdout.splitlines() if l.startswith("{")]
+    if r.returncode != 0 or not lines:
+        return {"error": f"child exited {r.returncode}: {r.stderr[-300:]}"}
+    return json.loads(lines[-1])
+
+
+def merge_configs(gpu, cpu):
+    for name, e in gpu.items():
+        ref = cpu.get(name) if isinstance(cpu, dict) else None
+        e["cpu_ref_us"] = ref["us"] if ref else None
+        e["cpu_ref_gbs"] = ref["gbs"] if ref else None
+    return gpu
+
+
 def main():
     args = parse()
+    if args.cpu_configs_child:  # the child of run_cpu_configs: host only, no GPU
+        out = {"host": host_cpu()}
+        out.update(cpu_configs(min(args.cpu_seconds, 2.0)))
+        print(json.dumps(out), flush=True)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not implemented)"}))
@@ -513,6 +762,9 @@ def main():
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU (the decode path has no CPU fallback)")
     cfg = synth.BITNET_2B
+    if args.configs_only:
+        print(json.dumps({"configs": configs_bench(torch)}), flush=True)
+        return
     ctx = 0 if args.prefill else args.ctx
     tern = args.kv_mode != "int8_fused"
     if tern and args.prefill:
@@ -584,6 +836,21 @@ def main():
     rl_tl1 = tl1_roofline(torch, cfg, host)
     rl_head = head_roofline(torch, cfg, host)
     cpu = None if args.no_cpu else cpu_baseline(torch, cfg, host, ctx, args.cpu_seconds)
+    if cpu is not None:
+        cpu["host"] = host_cpu()
+        cpu["gbs"] = round(step_bytes * cpu["value"] / 1e9, 2) if cpu.get("value") else None
+    configs = None
+    if not args.no_configs:
+        e.close()
+        e = None
+        torch.cuda.empty_cache()
+        gpu_cfg = configs_bench(torch)
+        host_cfg = {} if args.no_cpu else run_cpu_configs(args.cpu_seconds)
+        configs = merge_configs(gpu_cfg, host_cfg)
+        if isinstance(host_cfg, dict) and "host" in host_cfg:
+            configs["cpu_host"] = host_cfg["host"]
+        elif isinstance(host_cfg, dict) and "error" in host_cfg:
+            configs["cpu_error"] = host_cfg["error"]
 
     out = {
         "metric": "decode tok/s BitNet-2B-shape bs=1 ctx 4k; GEMV+attn HBM GB/s % of peak",
@@ -605,8 +872,10 @@ def main():
                           "lm_head_i8": {k: (round(v, 2) if isinstance(v, float) else v)
                                          for k, v in rl_head.items()}},
         "cpu_baseline": cpu,
+        "configs": configs,
     }
-    e.close()
+    if e is not None:
+        e.close()
     print(json.dumps(out), flush=True)
 
 

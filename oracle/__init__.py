@@ -148,6 +148,8 @@ def ref() -> ctypes.CDLL:
             "ref_engine_prefill": (_I, [_P, _I]),
             "ref_engine_hidden": (None, [_P, _P]),
             "ref_num_threads": (_I, []),
+            "ref_attention_int8_time": (ctypes.c_double, [_I, _I, _I, _I, _I, _P, _P, _P, _P,
+                                                          _P, _P, _P, _I]),
             "ref_engine_embed": (None, [_P, _I]),
             "ref_engine_layer": (None, [_P, _I]),
             "ref_engine_finish": (None, [_P]),

@@ -9,6 +9,7 @@
 // rms_norm_raw, pack_ternary_weights_raw) callable from here.
 #include "runtime/TenzoEngine.cpp"
 
+#include <chrono>
 #include <cstdint>
 #include <cstring>
 #include <vector>
@@ -85,6 +86,44 @@ void ref_attention_int8(int Hq, int Hkv, int max_seq, int pos,
     std::memcpy(vc, c.int8_v.data(), n_el);
     std::memcpy(ks, c.int8_k_scales.data(), n_sc * 4);
     std::memcpy(vs, c.int8_v_scales.data(), n_sc * 4);
+}
+
+// Timing of the same call without the copies: one cache of `batch` sequences
+// ([batch][Hkv][max_seq] rows) filled once from the arrays, then `reps` rounds
+// of forward_attention_raw at position pos for every sequence (the reference
+// serves a batch as one call per sequence). Returns the mean seconds per round.
+double ref_attention_int8_time(int batch, int Hq, int Hkv, int max_seq, int pos,
+                               const int8_t* kc, const int8_t* vc, const float* ks,
+                               const float* vs, const float* q, const float* k, const float* v,
+                               int reps) {
+    const size_t n_el = static_cast<size_t>(Hkv) * max_seq * 128;
+    const size_t n_sc = static_cast<size_t>(Hkv) * max_seq;
+    std::vector<FusedKVCache*> cs;
+    for (int b = 0; b < batch; ++b) {
+        FusedKVCache* c = new FusedKVCache(1, Hq, Hkv, 128, max_seq, "int8_fused");
+        std::memcpy(c->int8_k.data(), kc + b * n_el, n_el);
+        std::memcpy(c->int8_v.data(), vc + b * n_el, n_el);
+        std::memcpy(c->int8_k_scales.data(), ks + b * n_sc, n_sc * 4);
+        std::memcpy(c->int8_v_scales.data(), vs + b * n_sc, n_sc * 4);
+        cs.push_back(c);
+    }
+    std::vector<float> qq(Hq * 128), kk(Hkv * 128), vv(Hkv * 128), out(Hq * 128);
+    double total = 0.0;
+    for (int r = 0; r <= reps; ++r) {  // round 0 warms up
+        const auto t0 = std::chrono::steady_clock::now();
+        for (int b = 0; b < batch; ++b) {
+            std::memcpy(qq.data(), q + (size_t)b * Hq * 128, qq.size() * 4);  // RoPE is in place
+            std::memcpy(kk.data(), k + (size_t)b * Hkv * 128, kk.size() * 4);
+            std::memcpy(vv.data(), v + (size_t)b * Hkv * 128, vv.size() * 4);
+            cs[b]->cur_seq_len = pos;
+            cs[b]->forward_attention_raw(0, qq.data(), kk.data(), vv.data(), out.data());
+        }
+        const double dt =
+            std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        if (r > 0) total += dt;
+    }
+    for (FusedKVCache* c : cs) delete c;
+    return total / reps;
 }
 
 // The ternary KV modes (TenzoEngine.cpp:534-648, :695-885): mode 1 tl1_fused,
