@@ -175,6 +175,100 @@ q8_0_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __
     if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
 }
 
+// Q4_0 with fp16 activations on the packed fp16 dot (v_dot2_f32_f16): the
+// activations are staged in LDS as pairs (a_j, a_16+j) of each block, the
+// two elements that share a weight byte; a byte becomes the pair of weights
+// (lo - 8, hi - 8) in fp16 with a byte permute, an and-or that forms the fp16
+// numbers 1024 + q (exponent of 1024, q in the low mantissa bits) and one
+// packed subtraction of 1032, all exact; each pair then costs one dot step
+// with fp32 accumulation (the products of fp16 operands are exact in fp32).
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float q4_block_h2(const uint32_t* dw, int off, const uint32_t* apb) {
+    const uint4* ap4 = reinterpret_cast<const uint4*>(apb);
+    const h2v bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+    // the two masks in VGPRs, so the and-or is one v_and_or_b32 (a VOP3 op on
+    // gfx9 takes no literal and at most one scalar operand)
+    uint32_t lo4 = 0x000f000fu, one024 = 0x64006400u;
+    asm volatile("" : "+v"(lo4), "+v"(one024));
+    float s = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+        const int o = off + 2 + 4 * m;  // the 4 code bytes of elements 4m..4m+3 (and +16)
+        const uint32_t c = (o & 3) == 0 ? dw[o >> 2]
+                                        : __builtin_amdgcn_alignbyte(dw[(o >> 2) + 1], dw[o >> 2], o & 3);
+        const uint32_t hi = c >> 4;
+        const uint4 A = ap4[m];
+        const uint32_t a[4] = {A.x, A.y, A.z, A.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // bytes [lo nibble of byte k, 0, hi nibble of byte k, 0] as 1024 + q, fp16 pair
+            const uint32_t sel = (uint32_t)k | 0x0c00u | ((uint32_t)(4 + k) << 16) | 0x0c000000u;
+            const uint32_t z = (__builtin_amdgcn_perm(hi, c, sel) & lo4) | one024;
+            const h2v wq = __builtin_bit_cast(h2v, z) + bias;
+            s = __builtin_amdgcn_fdot2(wq, __builtin_bit_cast(h2v, a[k]), s, false);
+        }
+    }
+    return s;
+}
+
+template <int LPR>
+__global__ void __launch_bounds__(256)
+q4_0_f16_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w,
+                float* __restrict__ y, int K, int N) {
+    extern __shared__ uint32_t ap[];  // K/2 words: block b, j < 16: (a_32b+j, a_32b+16+j)
+    const int b = blockIdx.y;
+    const uint16_t* ab = act + (int64_t)b * K;
+    for (int i = threadIdx.x; i < K / 2; i += 256) {
+        const int blk = i >> 4, j = i & 15;
+        ap[i] = (uint32_t)ab[blk * 32 + j] | ((uint32_t)ab[blk * 32 + 16 + j] << 16);
+    }
+    __syncthreads();
+    constexpr int RPB = 256 / LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    const int nbk = K / 32;
+    const int ngroups = (nbk + 7) / 8;
+    float acc = 0.0f;
+    if (row < N) {
+        const uint8_t* rowp = w + (int64_t)row * nbk * 18;
+        for (int g = sub; g < ngroups; g += LPR) {
+            const int b0 = g * 8;
+            if (b0 + 8 <= nbk && (((uintptr_t)(rowp + b0 * 18)) & 15) == 0) {
+                uint32_t dw[36];
+                const uint4* p = reinterpret_cast<const uint4*>(rowp + b0 * 18);
+#pragma unroll
+                for (int i = 0; i < 9; ++i) {
+                    const uint4 v = p[i];
+                    dw[4 * i] = v.x;
+                    dw[4 * i + 1] = v.y;
+                    dw[4 * i + 2] = v.z;
+                    dw[4 * i + 3] = v.w;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t dbits = (dw[(18 * i) >> 2] >> (8 * ((18 * i) & 3))) & 0xffffu;
+                    const float d = half_bits_to_float((uint16_t)dbits);
+                    acc = __builtin_fmaf(q4_block_h2(dw, 18 * i, ap + (b0 + i) * 16), d, acc);
+                }
+            } else {
+                for (int bb = b0; bb < nbk && bb < b0 + 8; ++bb) {
+                    const uint16_t* hp = reinterpret_cast<const uint16_t*>(rowp + bb * 18);
+                    uint32_t dw[5];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) dw[i] = hp[2 * i] | ((uint32_t)hp[2 * i + 1] << 16);
+                    dw[4] = hp[8];
+                    const float d = half_bits_to_float((uint16_t)(dw[0] & 0xffffu));
+                    acc = __builtin_fmaf(q4_block_h2(dw, 0, ap + bb * 16), d, acc);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+}
+
 // Q4_0 weights x Q8_0 activations: per block the exact int32 dot
 // sum_j (q_j - 8) qa_j = dot4(q, qa) - 8 * sum_j qa_j, then an fp32 FMA with
 // d_w * d_a. Activations staged in LDS as codes + fp32 scales + code sums.
@@ -440,7 +534,21 @@ TENZO_HIP_API int tenzo_hip_gemv_q4_0(const void* act, int act_dtype, const uint
     TZ_CHECK(act_dtype == 0 || act_dtype == 1, "gemv_q4_0: act_dtype must be 0 or 1");
     hipStream_t st = (hipStream_t)stream;
     if (act_dtype == 0) return launch_q4_0((const float*)act, w, y, K, N, B, st);
-    return launch_q4_0((const uint16_t*)act, w, y, K, N, B, st);
+    // fp16 activations: the packed fp16 dot kernel
+    const int nbk = K / 32;
+    const int lpr = pick_lpr((nbk + 7) / 8);
+    const size_t smem = (size_t)K * 2;
+    dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
+    const uint16_t* a16 = (const uint16_t*)act;
+#define Q4H_CASE(L)                                                                        \
+    case L:                                                                                \
+        hipLaunchKernelGGL((q4_0_f16_kernel<L>), grid, dim3(256), smem, st, a16, w, y, K, N); \
+        break;
+    switch (lpr) {
+        Q4H_CASE(1) Q4H_CASE(2) Q4H_CASE(4) Q4H_CASE(8) Q4H_CASE(16) Q4H_CASE(32) Q4H_CASE(64)
+    }
+#undef Q4H_CASE
+    return launch_status("q4_0_f16_kernel");
 }
 
 TENZO_HIP_API int tenzo_hip_gemv_q8_0(const void* act, int act_dtype, const uint8_t* w,
