@@ -1,5 +1,7 @@
 // Quantized GEMVs on gfx950: GGUF Q4_0 (fp32/fp16 or Q8_0 activations), GGUF
 // Q8_0, GPTQ and AWQ (reference src/runtime/TenzoEngine.cpp:1022-1175).
+#include <type_traits>
+
 #include "common.h"
 
 namespace tz {
@@ -413,6 +415,144 @@ gq_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
     if (threadIdx.x == 0) atomicExch(&cnt[tile], 0u);
 }
 
+// GPTQ / AWQ with fp16 activations on the packed fp16 dot: per group, the
+// nibble pairs of a qweight word become exact fp16 pairs (q - z) (a byte
+// permute, an and-or forming 1024 + q, one packed subtraction of 1024 + z)
+// and meet the activation pairs of the same two k in one v_dot2_f32_f16 step
+// (exact products, fp32 accumulation); the group's sum is then scaled once,
+// y += s * sum_k a_k (q_k - z). The activations are staged in LDS as pairs
+// in the order of the nibble pairs: (k, k+1), (k+2, k+3), ... for GPTQ and,
+// for AWQ's nibble order {0,2,4,6,1,3,5,7}, (k, k+2), (k+4, k+6), (k+1, k+3),
+// (k+5, k+7). Split-K and the partial sums as gq_kernel.
+template <bool AWQ, typename TS, int BMAX>
+__global__ void __launch_bounds__(256)
+gq_h2_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qweight,
+             const TS* __restrict__ scales, const uint32_t* __restrict__ qzeros,
+             float* __restrict__ y, int K, int N, int group, int B, int KC, int splits,
+             float* __restrict__ part, uint32_t* __restrict__ cnt) {
+    extern __shared__ uint4 ap2v[];  // [BMAX][KC/2] fp16 pairs, 16-byte aligned
+    uint32_t* ap2 = reinterpret_cast<uint32_t*>(ap2v);
+    __shared__ int is_last;
+    constexpr int kQ = 16;  // k-octets whose qweight words are loaded together
+    const int tile = blockIdx.x;
+    const int sp = blockIdx.y;
+    const int k0 = sp * KC;
+    const int k1 = min(K, k0 + KC);
+    const int nk = k1 - k0;
+    const int KP = KC / 2;
+    // rows B..BMAX-1 are staged as zeros and computed like the others (their
+    // sums are not stored), so the row loops have no branch
+    for (int i = threadIdx.x; i < BMAX * (nk / 2); i += 256) {
+        const int bb = i / (nk / 2), pi = i - bb * (nk / 2);  // pair pi of the split
+        if (bb >= B) {
+            ap2[bb * KP + pi] = 0u;
+            continue;
+        }
+        const int oct = pi >> 2, j = pi & 3;
+        int ka, kb;  // the two k of pair j of the octet
+        if (AWQ) {
+            ka = (j & 1) * 4 + (j >> 1);
+            kb = ka + 2;
+        } else {
+            ka = 2 * j;
+            kb = ka + 1;
+        }
+        const uint16_t* ab = act + (int64_t)bb * K + k0 + oct * 8;
+        ap2[bb * KP + pi] = (uint32_t)ab[ka] | ((uint32_t)ab[kb] << 16);
+    }
+    __syncthreads();
+    const int n = tile * 256 + threadIdx.x;
+    float acc[BMAX];
+#pragma unroll
+    for (int bb = 0; bb < BMAX; ++bb) acc[bb] = 0.0f;
+    uint32_t lo4 = 0x000f000fu, one024 = 0x64006400u;  // VGPR operands of v_and_or_b32
+    asm volatile("" : "+v"(lo4), "+v"(one024));
+    if (n < N) {
+        for (int g0 = k0; g0 < k1; g0 += group) {
+            const int g = g0 / group;
+            const float s = to_f32<TS>(scales[(int64_t)g * N + n]);
+            int z;
+            if (AWQ) {
+                z = (int)((qzeros[(int64_t)g * (N / 8) + n / 8] >> (4 * (n % 8))) & 15u);
+            } else {
+                z = (int)((qzeros[(int64_t)(g / 8) * N + n] >> (4 * (g % 8))) & 15u) + 1;
+            }
+            const _Float16 bz = (_Float16)(-1024.0f - (float)z);
+            const h2v bias = {bz, bz};
+            float gs[BMAX];
+#pragma unroll
+            for (int bb = 0; bb < BMAX; ++bb) gs[bb] = 0.0f;
+            const int gend = min(k1, g0 + group);
+            for (int kc = g0; kc < gend; kc += 8 * kQ) {
+              // the chunk's qweight words first (kQ loads in flight; rows past
+              // K are clamped, read and not used), then their dot steps
+              uint32_t qv[kQ];
+#pragma unroll
+              for (int u = 0; u < kQ; ++u)
+                  qv[u] = qweight[(int64_t)min(kc / 8 + u, K / 8 - 1) * N + n];
+              // every octet of the chunk is computed (a use under a condition
+              // would let the compiler move its load down to it): octets past
+              // the group get zero weights and read pairs inside the split
+#pragma unroll
+              for (int u = 0; u < kQ; ++u) {
+                const int k = kc + 8 * u;
+                const bool live = k < gend;
+                const uint32_t qw = qv[u];
+                const uint32_t hi = qw >> 4;
+                h2v wq[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t sel =
+                        (uint32_t)i | 0x0c00u | ((uint32_t)(4 + i) << 16) | 0x0c000000u;
+                    const uint32_t zz = (__builtin_amdgcn_perm(hi, qw, sel) & lo4) | one024;
+                    const h2v wd = __builtin_bit_cast(h2v, zz) + bias;
+                    wq[i] = live ? wd : h2v{(_Float16)0.0f, (_Float16)0.0f};
+                }
+                const int pk = live ? (k - k0) / 2 : 0;  // first pair of the octet
+#pragma unroll
+                for (int bb = 0; bb < BMAX; ++bb) {
+                    // (KP and pk are multiples of 4: 16-byte LDS reads)
+                    const uint4 A = ap2v[(bb * KP + pk) >> 2];
+                    gs[bb] = __builtin_amdgcn_fdot2(wq[0], __builtin_bit_cast(h2v, A.x), gs[bb],
+                                                    false);
+                    gs[bb] = __builtin_amdgcn_fdot2(wq[1], __builtin_bit_cast(h2v, A.y), gs[bb],
+                                                    false);
+                    gs[bb] = __builtin_amdgcn_fdot2(wq[2], __builtin_bit_cast(h2v, A.z), gs[bb],
+                                                    false);
+                    gs[bb] = __builtin_amdgcn_fdot2(wq[3], __builtin_bit_cast(h2v, A.w), gs[bb],
+                                                    false);
+                }
+              }
+            }
+#pragma unroll
+            for (int bb = 0; bb < BMAX; ++bb) acc[bb] = __builtin_fmaf(gs[bb], s, acc[bb]);
+        }
+    }
+    if (splits == 1) {
+        if (n < N)
+            for (int bb = 0; bb < B && bb < BMAX; ++bb) y[(int64_t)bb * N + n] = acc[bb];
+        return;
+    }
+    if (n < N)
+        for (int bb = 0; bb < B && bb < BMAX; ++bb)
+            store_coherent(&part[((int64_t)sp * B + bb) * N + n], acc[bb]);
+    partials_acked();
+    __syncthreads();
+    if (threadIdx.x == 0) is_last = atomicAdd(&cnt[tile], 1u) == (unsigned)(splits - 1);
+    __syncthreads();
+    if (!is_last) return;
+    if (n < N) {
+        for (int bb = 0; bb < B && bb < BMAX; ++bb) {
+            float sum = 0.0f;
+            for (int q = 0; q < splits; ++q)
+                sum += __hip_atomic_load(&part[((int64_t)q * B + bb) * N + n], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            y[(int64_t)bb * N + n] = sum;
+        }
+    }
+    if (threadIdx.x == 0) atomicExch(&cnt[tile], 0u);
+}
+
 // ------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------
@@ -492,10 +632,19 @@ static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
     dim3 grid((unsigned)tiles, (unsigned)splits);
 #define GQ_CASE(BM)                                                                          \
     if (B <= BM) {                                                                           \
-        hipLaunchKernelGGL((gq_kernel<AWQ, TA, TS, BM>), grid, dim3(256), smem, st, act,      \
-                           qweight, scales, qzeros, y, K, N, group, B, KC, splits, part, cnt); \
+        if (kF16)                                                                            \
+            hipLaunchKernelGGL((gq_h2_kernel<AWQ, TS, BM>), grid, dim3(256),                 \
+                               (size_t)BM * KC * 2, st,                                      \
+                               (const uint16_t*)act, qweight, scales, qzeros, y, K, N, group, \
+                               B, KC, splits, part, cnt);                                    \
+        else                                                                                 \
+            hipLaunchKernelGGL((gq_kernel<AWQ, TA, TS, BM>), grid, dim3(256), smem, st, act,  \
+                               qweight, scales, qzeros, y, K, N, group, B, KC, splits, part,  \
+                               cnt);                                                         \
         return launch_status(AWQ ? "awq_kernel" : "gptq_kernel");                            \
     }
+    // fp16 activations take the packed fp16 dot (the pairs need whole k-octets: K % 8 == 0)
+    constexpr bool kF16 = std::is_same<TA, uint16_t>::value;
     GQ_CASE(1) GQ_CASE(2) GQ_CASE(4) GQ_CASE(8)
 #undef GQ_CASE
     set_error("gptq/awq: batch %d > 8 not supported", B);
