@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--configs-only", action="store_true",
                     help="run only the per-config kernel leg (for profiling it)")
     ap.add_argument("--cpu-configs-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--stage-trace", action="store_true",
+                    help="print only the persistent kernel's per-stage trace (JSON line)")
     ap.add_argument("--mode", default="persistent", choices=["persistent", "graph", "eager"],
                     help="engine execution mode (one persistent kernel per token, or one "
                          "kernel per stage replayed from a HIP graph / launched eagerly)")
@@ -507,6 +509,57 @@ def tern_bench(torch, e, cfg, host, args):
 
 # ------------------------------------------------------------------- main
 
+# --------------------------------------------------------- stage trace
+
+STAGE_NAMES = ("QKV", "ATT", "O", "GU", "DOWN")
+
+
+def stage_trace(e, cfg, ctx, runs=8):
+    """Per-stage timing of the persistent kernel from its barrier trace
+    (tenzo_hip_engine_trace: every workgroup stamps the 100 MHz wall clock
+    when it reaches and when it leaves each grid barrier). For each stage:
+    "work" = last arrival at its barrier - first departure from the previous
+    one, "barrier" = first departure - last arrival, medians over `runs`
+    steps at position ctx (the first two are dropped), averaged over layers
+    1..L-1; with the stage's algorithmic bytes and GB/s."""
+    e.trace(True)
+    tok = 1
+    traces = []
+    for _ in range(runs):
+        e.rewind(ctx)
+        tok = e.step(tok)
+        traces.append(e.get_trace().astype(np.int64))
+    e.trace(False)
+    t = np.array(traces[2:])  # [R][stages][nwg][2] ticks of 10 ns
+    S = t.shape[1]
+    work = np.zeros(S)
+    bar = np.zeros(S)
+    for s_ in range(S):
+        arr, lv = t[:, s_, :, 0], t[:, s_, :, 1]
+        if s_:
+            work[s_] = np.median((arr.max(axis=1) - t[:, s_ - 1, :, 1].min(axis=1)) * 0.01)
+        bar[s_] = np.median((lv.min(axis=1) - arr.max(axis=1)) * 0.01)
+    H, F, qd, kvd = cfg.hidden, cfg.ffn, cfg.q_dim, cfg.kv_dim
+    sb = {"QKV": (qd + 2 * kvd) * H // 4, "ATT": cfg.n_kv_heads * (ctx + 1) * (2 * 128 + 4),
+          "O": H * qd // 4, "GU": 2 * F * H // 4, "DOWN": H * F // 4}
+    L = cfg.n_layers
+    out = {}
+    for k, name in enumerate(STAGE_NAMES):
+        idx = [5 * l + k for l in range(1, L)]
+        w, b = float(np.mean(work[idx])), float(np.mean(bar[idx]))
+        out[name] = {"work_us": round(w, 2), "barrier_us": round(b, 2), "bytes": sb[name],
+                     "gbs_work_and_barrier": round(sb[name] / ((w + b) * 1e-6) / 1e9, 1)}
+    out["HEAD"] = {"work_us": round(float(work[S - 1]), 2),
+                   "bytes": cfg.vocab * H + cfg.vocab * 4,
+                   "gbs": round((cfg.vocab * H + cfg.vocab * 4) / (work[S - 1] * 1e-6) / 1e9, 1)}
+    layer = sum(out[n]["work_us"] + out[n]["barrier_us"] for n in STAGE_NAMES)
+    out["layer_us"] = round(layer, 2)
+    out["step_us"] = round(float(np.median((t[:, S - 1, :, 0].max(axis=1) -
+                                            t[:, 0, :, 1].min(axis=1)) * 0.01)), 1)
+    out["barriers_per_step"] = 5 * L
+    return out
+
+
 # ------------------------------------------------------------ configs leg
 #
 # BASELINE.json's other configs, each timed as a kernel on its own: configs 1
@@ -781,6 +834,12 @@ def main():
         return
     e.set_mode(args.mode)
     mode = e.mode
+    if args.stage_trace:
+        print(json.dumps({"stage_trace": stage_trace(e, cfg, ctx),
+                          "config": {"workload": "BitNet-2B decode step", "context": ctx}}),
+              flush=True)
+        e.close()
+        return
     if args.pmc_probe:
         src = torch.empty(PROBE_COPY_BYTES // 4, dtype=torch.int32, device="cuda").fill_(1)
         dst = torch.empty_like(src)
@@ -833,6 +892,17 @@ def main():
                 "traffic": measured_traffic() if mode == "persistent" else None,
                 "alg_bytes_per_launch": int(step_bytes),
                 "mean_launch_us": round(kern_s * 1e6, 2)}
+    # the metric's GEMV + attention share: TL1 weights and KV cache bytes over
+    # the step's kernel time less the LM-head stage (from the stage trace)
+    st = stage_trace(e, cfg, ctx) if mode == "persistent" else None
+    sb = cfg.step_bytes(ctx + 1 + args.steps // 2)
+    ga_bytes = sb["tl1"] + sb["kv"]
+    gemv_attn = None
+    if st is not None:
+        ga_s = kern_s - st["HEAD"]["work_us"] * 1e-6
+        gemv_attn = {"bytes": int(ga_bytes), "time_us": round(ga_s * 1e6, 1),
+                     "gbs": round(ga_bytes / ga_s / 1e9, 1),
+                     "frac": round(ga_bytes / ga_s / 1e9 / PEAK_HBM_GBS, 4)}
     rl_tl1 = tl1_roofline(torch, cfg, host)
     rl_head = head_roofline(torch, cfg, host)
     cpu = None if args.no_cpu else cpu_baseline(torch, cfg, host, ctx, args.cpu_seconds)
@@ -866,6 +936,8 @@ def main():
         "step_hbm_bytes": step_bytes, "step_gbs": round(step_gbs, 1),
         "step_frac_of_peak": round(step_gbs / PEAK_HBM_GBS, 4),
         "roofline": roofline,
+        "gemv_attn": gemv_attn,
+        "stages": st,
         "api_generate_step_tok_s": round(api_tok_s, 2),
         "stage_kernels": {"tl1_gemv": {k: (round(v, 2) if isinstance(v, float) else v)
                                        for k, v in rl_tl1.items()},
