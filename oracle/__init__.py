@@ -9,8 +9,9 @@ Two libraries, both loaded with ctypes:
   from the reference checkout by ``Makefile`` (target ``ref``). Optional: it
   exists only where it was built.
 
-Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
-leg may import this package, and only to check or time the CPU path. The
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU baseline
+legs (the reference engine step and the per-config reference functions) may
+import this package, and only to check or time the CPU path. The
 product (``tenzo_amd``) never imports it.
 """
 from __future__ import annotations

@@ -2,7 +2,7 @@
  * tenzo_oracle.h - CPU restatement of Tenzo's quantized decode hot path.
  *
  * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and bench.py's
- * cpu_baseline leg may load this library, and only as the checker. The product
+ * CPU baseline legs may load this library, and only as the checker. The product
  * (tenzo_amd/, libtenzo_hip.so) never calls it.
  *
  * Every function restates one reference function (file:line into the reference
@@ -33,9 +33,12 @@
  *                                    dequantized cache (1e-3) + compiled reference
  *                                    + ctx=1 special case
  *   orc_lm_head                      closed-form int32 dot + compiled reference
- *   orc_q4_0, orc_q8_0, orc_gptq,
- *   orc_awq                          fp64 brute force of each dequant formula +
- *                                    compiled-reference goldens (layout conventions)
+ *   orc_q4_0, orc_q8_0               compiled reference (bit-exact: the lane chains
+ *                                    and their pairwise sum, live at three shapes
+ *                                    and the goldens) + fp64 brute force
+ *   orc_gptq, orc_awq                fp64 brute force of each dequant formula +
+ *                                    compiled-reference goldens (layout conventions;
+ *                                    the build's vectorised order is not restated)
  *   orc_q4_0_q8act                   no reference counterpart: closed form (fp64
  *                                    brute force of the block formula)
  *   orc_quantize_q8_0                llama.cpp's published quantize_row_q8_0 (no
