@@ -243,6 +243,83 @@ __global__ void copy_kernel(const float* __restrict__ src, float* __restrict__ d
     if (i < n) dst[i] = src[i];
 }
 
+// Paged pools <-> the contiguous export layout [L][Hkv][seq][128] through the block
+// table: export row (l*Hkv + h)*seq + t is pool row ((table[t/16]*L + l)*Hkv + h)*16 +
+// t%16 (PagedKVCache's block layout, TenzoEngine.cpp:308-322). One thread per 16-byte
+// piece of a K and a V row; the piece-0 thread also moves the row's two scales.
+__global__ void kv_page_copy_kernel(int8_t* __restrict__ pk, int8_t* __restrict__ pv,
+                                    float* __restrict__ pks, float* __restrict__ pvs,
+                                    int8_t* __restrict__ xk, int8_t* __restrict__ xv,
+                                    float* __restrict__ xks, float* __restrict__ xvs,
+                                    const int32_t* __restrict__ table, int lh_rows, int seq,
+                                    int to_pool) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (int64_t)lh_rows * seq * 8) return;
+    const int64_t r = i >> 3;
+    const int piece = (int)(i & 7);
+    const int t = (int)(r % seq);
+    const int64_t lh = r / seq;
+    const int64_t p = ((int64_t)table[t >> 4] * lh_rows + lh) * 16 + (t & 15);
+    uint4* pk4 = (uint4*)(pk + p * kD) + piece;
+    uint4* pv4 = (uint4*)(pv + p * kD) + piece;
+    uint4* xk4 = (uint4*)(xk + r * kD) + piece;
+    uint4* xv4 = (uint4*)(xv + r * kD) + piece;
+    if (to_pool) {
+        *pk4 = *xk4;
+        *pv4 = *xv4;
+        if (piece == 0) pks[p] = xks[r], pvs[p] = xvs[r];
+    } else {
+        *xk4 = *pk4;
+        *xv4 = *pv4;
+        if (piece == 0) xks[r] = pks[p], xvs[r] = pvs[p];
+    }
+}
+
+// Moves seq_len tokens of every (layer, kv head) between the paged pools and the
+// contiguous layout through one staging buffer: the four arrays in one copy each and
+// one table-driven kernel, instead of four copies per 16-token block per row.
+int pg_transfer(tenzo_engine_t e, int8_t* kc, int8_t* vc, float* ks, float* vs, int seq_len,
+                hipMemcpyKind kind, bool to_pool) {
+    const int lh = e->L * e->Hkv;
+    const size_t rows = (size_t)lh * seq_len;
+    void* stage = nullptr;
+    if (hipMalloc(&stage, rows * (2 * kD + 8)) != hipSuccess) {
+        set_error("paged KV transfer: cannot allocate %zu bytes of staging",
+                  rows * (2 * kD + 8));
+        return TENZO_ERROR_OUT_OF_MEMORY;
+    }
+    int8_t* xk = (int8_t*)stage;
+    int8_t* xv = xk + rows * kD;
+    float* xks = (float*)(xv + rows * kD);
+    float* xvs = xks + rows;
+    hipError_t err = hipSuccess;
+    auto copy = [&](void* d, const void* s, size_t n) {
+        if (err == hipSuccess) err = hipMemcpyAsync(d, s, n, kind, e->st);
+    };
+    if (to_pool) {
+        copy(xk, kc, rows * kD), copy(xv, vc, rows * kD);
+        copy(xks, ks, rows * 4), copy(xvs, vs, rows * 4);
+    }
+    if (err == hipSuccess) {
+        hipLaunchKernelGGL(kv_page_copy_kernel, dim3((unsigned)ceil_div((int64_t)rows * 8, 256)),
+                           dim3(256), 0, e->st, e->kc, e->vc, (float*)e->ks, (float*)e->vs, xk,
+                           xv, xks, xvs, e->pg_bt, lh, seq_len, (int)to_pool);
+        err = hipGetLastError();
+    }
+    if (!to_pool) {
+        copy(kc, xk, rows * kD), copy(vc, xv, rows * kD);
+        copy(ks, xks, rows * 4), copy(vs, xvs, rows * 4);
+    }
+    const hipError_t serr = hipStreamSynchronize(e->st);
+    (void)hipFree(stage);
+    if (err == hipSuccess) err = serr;
+    if (err != hipSuccess) {
+        set_error("paged KV transfer: %s", hipGetErrorString(err));
+        return TENZO_ERROR_UNSUPPORTED;
+    }
+    return TENZO_SUCCESS;
+}
+
 // One layer (forward_layer_raw, TenzoEngine.cpp:1522-1632).
 int enqueue_layer(tenzo_engine_t e, int l, int T, int max_chunks) {
     const DevLayer& w = e->layers[l];
@@ -1317,20 +1394,12 @@ TENZO_HIP_API int tenzo_hip_engine_set_kv(tenzo_engine_t e, const void* kc, cons
         pg_reset(e);
         const int prc = pg_ensure(e, seq_len);
         if (prc) return prc;
-        const hipMemcpyKind k = is_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
-        for (int b = 0; b * 16 < seq_len; ++b) {
-            const size_t cnt = (size_t)std::min(16, seq_len - b * 16);
-            for (int l = 0; l < e->L; ++l)
-                for (int h = 0; h < e->Hkv; ++h) {
-                    const size_t dr = (((size_t)e->pg_table[b] * e->L + l) * e->Hkv + h) * 16;
-                    const size_t sr = ((size_t)l * e->Hkv + h) * seq_len + (size_t)b * 16;
-                    TZ_HIP(hipMemcpyAsync(e->kc + dr * kD, (const int8_t*)kc + sr * kD, cnt * kD, k, e->st));
-                    TZ_HIP(hipMemcpyAsync(e->vc + dr * kD, (const int8_t*)vc + sr * kD, cnt * kD, k, e->st));
-                    TZ_HIP(hipMemcpyAsync((float*)e->ks + dr, (const float*)ks + sr, cnt * 4, k, e->st));
-                    TZ_HIP(hipMemcpyAsync((float*)e->vs + dr, (const float*)vs + sr, cnt * 4, k, e->st));
-                }
+        if (seq_len > 0) {
+            const int trc = pg_transfer(e, (int8_t*)kc, (int8_t*)vc, (float*)ks, (float*)vs,
+                                        seq_len, is_device ? hipMemcpyDeviceToDevice
+                                                           : hipMemcpyHostToDevice, true);
+            if (trc) return trc;
         }
-        TZ_HIP(hipStreamSynchronize(e->st));
         e->seq_len = seq_len;
         return TENZO_SUCCESS;
     }
@@ -1361,19 +1430,8 @@ TENZO_HIP_API int tenzo_hip_engine_get_kv(tenzo_engine_t e, void* kc, void* vc, 
         TZ_CHECK((int)e->pg_table.size() * 16 >= seq_len, "engine_get_kv: %d tokens but %d "
                  "blocks", seq_len, (int)e->pg_table.size());
         TZ_HIP(hipStreamSynchronize(e->st));
-        for (int b = 0; b * 16 < seq_len; ++b) {
-            const size_t cnt = (size_t)std::min(16, seq_len - b * 16);
-            for (int l = 0; l < e->L; ++l)
-                for (int h = 0; h < e->Hkv; ++h) {
-                    const size_t sr = (((size_t)e->pg_table[b] * e->L + l) * e->Hkv + h) * 16;
-                    const size_t dr = ((size_t)l * e->Hkv + h) * seq_len + (size_t)b * 16;
-                    TZ_HIP(hipMemcpy((int8_t*)kc + dr * kD, e->kc + sr * kD, cnt * kD, hipMemcpyDeviceToHost));
-                    TZ_HIP(hipMemcpy((int8_t*)vc + dr * kD, e->vc + sr * kD, cnt * kD, hipMemcpyDeviceToHost));
-                    TZ_HIP(hipMemcpy((float*)ks + dr, (float*)e->ks + sr, cnt * 4, hipMemcpyDeviceToHost));
-                    TZ_HIP(hipMemcpy((float*)vs + dr, (float*)e->vs + sr, cnt * 4, hipMemcpyDeviceToHost));
-                }
-        }
-        return TENZO_SUCCESS;
+        return pg_transfer(e, (int8_t*)kc, (int8_t*)vc, (float*)ks, (float*)vs, seq_len,
+                           hipMemcpyDeviceToHost, false);
     }
     const size_t rows = (size_t)e->L * e->Hkv;
     const size_t R = (size_t)e->kv_row, S = (size_t)e->kv_sb;

@@ -83,7 +83,7 @@ class Engine:
     """One device-resident decode engine."""
 
     def __init__(self, cfg: synth.DecodeConfig | Config, kv_mode: str | None = None):
-        """kv_mode: "int8_fused" (default), "tl1_fused" or "popcount_fused"."""
+        """kv_mode: "int8_fused" (default), "tl1_fused", "popcount_fused" or "paged_int8"."""
         self.L = lib()
         self.cfg = cfg if isinstance(cfg, Config) else config_from(cfg)
         if kv_mode is not None:

@@ -193,3 +193,36 @@ def test_engine_kv_modes_chained_decode_and_prefill(eng_mod, kv_mode):
             assert len(a.block_table()) == 0
             a.prefill_batch(toks[:3])
             np.testing.assert_array_equal(a.block_table(), [0])
+
+
+def test_engine_paged_kv_round_trip(eng_mod, torch_dev):
+    """set_kv / get_kv move every (layer, kv head) row through the block table in one
+    staging pass: 30 layers x 5 kv heads at a ragged length (1000 tokens, a partial last
+    block) from host buffers, then a shorter cache (333 tokens) from device buffers,
+    read back bit for bit."""
+    torch = torch_dev
+    cfg = synth.DecodeConfig(hidden=640, n_q_heads=5, n_kv_heads=5, n_layers=30, ffn=64,
+                             vocab=256, max_seq=1024)
+    rng = np.random.default_rng(5)
+    n = 1000
+    shape = (cfg.n_layers, cfg.n_kv_heads, n)
+    kc = rng.integers(-128, 128, shape + (128,), dtype=np.int8)
+    vc = rng.integers(-128, 128, shape + (128,), dtype=np.int8)
+    ks = rng.random(shape, dtype=np.float32)
+    vs = rng.random(shape, dtype=np.float32)
+    with eng_mod.Engine(cfg, kv_mode="paged_int8") as e:
+        print("paged set_kv host n=1000", flush=True)
+        e.set_kv(kc, vc, ks, vs, n)
+        assert e.seq_len == n
+        np.testing.assert_array_equal(e.block_table(), np.arange((n + 15) // 16))
+        for got, want in zip(e.get_kv(n), (kc, vc, ks, vs)):
+            np.testing.assert_array_equal(got, want)
+        m = 333
+        src = [np.ascontiguousarray(a[:, :, ::-1][:, :, :m]) for a in (kc, vc, ks, vs)]
+        dev = [torch.from_numpy(a).cuda() for a in src]
+        print("paged set_kv device n=333", flush=True)
+        e.set_kv_device(*(t.data_ptr() for t in dev), m)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(e.block_table(), np.arange((m + 15) // 16))
+        for got, want in zip(e.get_kv(m), src):
+            np.testing.assert_array_equal(got, want)
