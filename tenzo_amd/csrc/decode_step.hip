@@ -212,6 +212,7 @@ struct Shared {
     int red_i[kW][64];
     float red_a[kW], red_b[kW];
     int red_c[kW];
+    int red_s[kW];
     int flag;
 };
 
@@ -601,14 +602,14 @@ __device__ __forceinline__ uint32_t pack4(int c0, int c1, int c2, int c3) {
 // compute_logits :1666-1678); returns this thread's code sum.
 template <int QMAX>
 __device__ __forceinline__ int quant_codes(Shared& s, const float4 (&p)[kJ], int K, float inv_rms,
-                                           float amax) {
+                                           float amax, int q_lo = 0, int q_hi = 1 << 30) {
     const int t = ltid();
     int J = wave_groups(K);
     const float scale = (float)QMAX / amax;
     int csum = 0;
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
-        if (j < J) {
+        if (j < J && t + kT * j >= q_lo && t + kT * j < q_hi) {
             const float4 y = make_float4(__fmul_rn(p[j].x, inv_rms), __fmul_rn(p[j].y, inv_rms),
                                          __fmul_rn(p[j].z, inv_rms), __fmul_rn(p[j].w, inv_rms));
             const int c0 = act_code<QMAX>(y.x, scale), c1 = act_code<QMAX>(y.y, scale);
@@ -694,9 +695,27 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
     inv_out = amax * (1.0f / (float)QMAX);
 }
 
+// The inv_scale half of norm_quant<31>'s record alone (the code sum is added
+// up by the workgroups that compute the codes): the exact RMS scale and the
+// absmax, no codes.
+__device__ __forceinline__ float norm_record_inv31(Shared& s, float4 (&v)[kJ],
+                                                  const float4 (&w)[kJ], bool has_w, int K,
+                                                  float eps) {
+    const int lane = ltid() & 63, wave = lwave();
+    float4 p[kJ];
+    float pmax = wave_max(weigh(p, v, w, has_w, K));
+    if (lane == 0) s.red_b[wave] = pmax;
+    const float inv_rms = exact_inv_rms(s, v, K, eps);  // (its barriers publish red_b)
+    pmax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
+    return fmaxf(1e-6f, __fmul_rn(pmax, inv_rms)) * (1.0f / 31.0f);
+}
+
 // The ±31 codes of norm_quant<31> for a workgroup that needs only the codes
 // (the record comes from another workgroup), without waiting for the
-// sequential sum of squares in the common case.
+// sequential sum of squares in the common case. Only the float4 groups
+// [q_lo, q_hi) get codes (the columns the workgroup's tasks read); the
+// absmax and the estimate still cover the whole row. Returns the sum of the
+// codes written (in every thread).
 //
 // With any positive scale r in place of inv_rms, act_code's product is
 // z_i = fl(p_i r) * fl(31 / fl(pmax r)) = t_i (1 + e), t_i = 31 p_i / pmax,
@@ -712,9 +731,9 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
 // floor or not finite, the codes are recomputed with the exact inv_rms.
 // Either way s.codes ends up holding exactly norm_quant<31>'s codes. (A
 // subnormal p_i r gives |z_i| < 2^-100 for both scales: code 0 either way.)
-__device__ __forceinline__ void norm_quant_codes31(Shared& s, float4 (&v)[kJ],
-                                                   const float4 (&w)[kJ], bool has_w, int K,
-                                                   float eps) {
+__device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
+                                                  const float4 (&w)[kJ], bool has_w, int K,
+                                                  float eps, int q_lo, int q_hi) {
     const int t = ltid(), lane = t & 63, wave = lwave();
     float4 p[kJ];
     float pmax = wave_max(weigh(p, v, w, has_w, K));
@@ -743,9 +762,10 @@ __device__ __forceinline__ void norm_quant_codes31(Shared& s, float4 (&v)[kJ],
     bool near = !(amax >= 2e-6f && amax <= 3.0e38f && ss <= 3.0e38f);
     const float scale = 31.0f / amax;
     asm volatile("" : "+s"(J));
+    int csum = 0;
 #pragma unroll
     for (int j = 0; j < kJ; ++j)
-        if (j < J) {
+        if (j < J && t + kT * j >= q_lo && t + kT * j < q_hi) {
             const float ys[4] = {__fmul_rn(p[j].x, r), __fmul_rn(p[j].y, r),
                                  __fmul_rn(p[j].z, r), __fmul_rn(p[j].w, r)};
             int c[4];
@@ -756,15 +776,23 @@ __device__ __forceinline__ void norm_quant_codes31(Shared& s, float4 (&v)[kJ],
                 near |= fabsf((a - floorf(a)) - 0.5f) <= __builtin_fmaf(a, 0x1p-20f, 0x1p-19f);
             }
             *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) = pack4(c[0], c[1], c[2], c[3]);
+            csum += (c[0] + c[1]) + (c[2] + c[3]);
         }
     const bool wnear = __any(near);
-    if (lane == 0) s.red_c[wave] = wnear ? 1 : 0;
+    csum = wave_sum_i32(csum);
+    if (lane == 0) {
+        s.red_c[wave] = wnear ? 1 : 0;
+        s.red_s[wave] = csum;
+    }
     __syncthreads();
     if ((s.red_c[0] | s.red_c[1] | s.red_c[2] | s.red_c[3]) != 0) {
         const float inv_rms = exact_inv_rms(s, v, K, eps);
-        (void)quant_codes<31>(s, p, K, inv_rms, fmaxf(1e-6f, __fmul_rn(pmax, inv_rms)));
+        csum = wave_sum_i32(quant_codes<31>(s, p, K, inv_rms,
+                                            fmaxf(1e-6f, __fmul_rn(pmax, inv_rms)), q_lo, q_hi));
+        if (lane == 0) s.red_s[wave] = csum;
         __syncthreads();
     }
+    return (s.red_s[0] + s.red_s[1]) + (s.red_s[2] + s.red_s[3]);
 }
 
 // ---------------------------------------------------------------- GEMV ----
@@ -919,17 +947,30 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     } else {
         finish_act(xv, in, p, l, Lw.sc(4), Lw.sc(5), first, m);
     }
-    if (rec) {
+    // With fewer tasks than workgroups, every workgroup has at most one task
+    // and the record writer none: the writer publishes inv_scale alone, each
+    // task quantizes only the K slice it reads, and the tasks of row block 0
+    // (one per slice) add their slices' code sums into the record.
+    const bool single = n < p.nwg;
+    unsigned* recw = p.sync + w_rec(l, slot, p.L, p.Hkv);
+    if (rec && single) {
+        const float inv = norm_record_inv31(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps);
+        if (tid == 0) stcu(recw, __float_as_uint(inv));
+    } else if (rec) {
         float inv;
         int csum;
         norm_quant<31>(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps, inv, csum);
         if (tid == 0) {
-            unsigned* r = p.sync + w_rec(l, slot, p.L, p.Hkv);
-            stcu(r, __float_as_uint(inv));
-            stcu(r + 1, (unsigned)csum);
+            stcu(recw, __float_as_uint(inv));
+            stcu(recw + 1, (unsigned)csum);
         }
     } else {
-        norm_quant_codes31(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps);
+        const int c0 = (first % S) * KSs, c1 = min(KS, c0 + KSs);
+        const int csum = norm_quant_codes31(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps,
+                                            single ? c0 * 16 : 0, single ? c1 * 16 : K / 4);
+        if (single && first < S && tid == 0)
+            __hip_atomic_fetch_add(reinterpret_cast<int*>(recw + 1), csum, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
     }
     int* out = accl + (slot == 0 ? 0 : slot == 1 ? ao.o : slot == 2 ? ao.gu : ao.down);
     for (int t = first; t < n; t += p.nwg) {
