@@ -55,7 +55,7 @@ struct DsParams {
     uint64_t* trace;
 };
 
-constexpr int kDsThreads = 256;
+constexpr int kDsThreads = 512;
 constexpr int kDsMaxChunk = 256;    // context tokens per attention task, at most
 constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
 constexpr int kDsCounters = 16;

@@ -19,7 +19,7 @@
 // them applies the epilogue y = float(acc - code_sum) * (inv_scale * w_scale)
 // (the GEMV's own rounding steps) using the (inv_scale, code_sum) record the
 // producing stage published, and adds the residual. Each stage input is built
-// in registers (thread t owns float4 groups t, t+256, ...), normalized and
+// in registers (thread t owns float4 groups t, t+kT, ...), normalized and
 // quantized there; the RMSNorm sum of squares runs over a copy in LDS in the
 // reference build's order (eight FMA chains, common.h). Vectors later
 // stages need as floats (x, h1, q|k|v, gate|up) are stored by the workgroups
@@ -54,16 +54,18 @@
 namespace tz {
 namespace {
 
-constexpr int kT = kDsThreads;   // 256 threads = 4 waves
-constexpr int kW = kT / 64;
-constexpr int kPF = 10;          // tile uint4 per lane preloaded
-constexpr int kJ = 8;            // float4 groups per thread: vectors up to 8192
+constexpr int kT = kDsThreads;   // threads per workgroup
+constexpr int kW = kT / 64;      // waves per workgroup
+constexpr int kPF = 40 / kW;     // tile uint4 per lane preloaded (a 2560-wide row block)
+constexpr int kJ = 8192 / (4 * kT);  // float4 groups per thread: vectors up to 8192
 constexpr int kNC = kDsCounters;
 constexpr int kD = 128;
 constexpr int kPS = kDsPartStride;  // partial record: m, l, -, -, o[128]
 constexpr int kTmax = kDsMaxChunk;  // attention tokens per task (LDS V tile)
 constexpr int kRT = kW * 8;      // attention tokens per round (8 per wave)
-constexpr int kAR = 4;           // attention rounds preloaded in registers
+constexpr int kAR = kW >= 8 ? 2 : 4;  // attention rounds preloaded in registers
+static_assert(2 * kAR <= kPF, "the attention tile uses the GEMV tile's registers");
+static_assert(kW == 4 || kW == 8, "4 or 8 waves per workgroup");
 constexpr unsigned kSpinLimit = 1u << 18;  // ~0.3 s of polling; a barrier waits < 0.1 ms
 constexpr float kAttnScale = 0.08838834764831845f;  // 1/sqrt(128)
 
@@ -297,7 +299,7 @@ __device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, i
 }
 
 // Float4 groups of a K-element vector a wave holds: thread t owns groups
-// t + 256 j, so wave w's lanes cover groups [256 j + 64 w, 256 j + 64 w + 64);
+// t + kT j, so wave w's lanes cover groups [kT j + 64 w, kT j + 64 w + 64);
 // the j with a group below K/4 (wave-uniform). Loads past that count would
 // only read zeros, so they are not issued at all.
 //
@@ -317,6 +319,34 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt has 6 bits");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Cross-wave combinations of per-wave values in LDS (lane 0 of each wave
+// wrote r[wave]); the orders are fixed, and only integer sums, maxima and the
+// scale estimate use them.
+__device__ __forceinline__ float red_max(const float* r) {
+    float m = r[0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) m = fmaxf(m, r[w]);
+    return m;
+}
+__device__ __forceinline__ float red_sum(const float* r) {
+    float a = r[0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) a += r[w];
+    return a;
+}
+__device__ __forceinline__ int red_sum(const int* r) {
+    int a = r[0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) a += r[w];
+    return a;
+}
+__device__ __forceinline__ int red_or(const int* r) {
+    int a = r[0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) a |= r[w];
+    return a;
 }
 
 // -------------------------------------------------------------- tiles ----
@@ -363,7 +393,7 @@ __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[
     }
 }
 
-// Norm weights (thread t: float4 groups t + 256 j; zeros past K) into registers.
+// Norm weights (thread t: float4 groups t + kT j; zeros past K) into registers.
 __device__ __forceinline__ void load_norm_w(float4 (&w)[kJ], const float* nw, int K) {
     const __amdgpu_buffer_rsrc_t r = rsrc(nw, nw ? (uint32_t)K * 4 : 0u);
     const int t = ltid();
@@ -686,12 +716,12 @@ __device__ __forceinline__ void norm_quant(Shared& s, float4 (&v)[kJ], const flo
     float pmax = wave_max(weigh(p, v, w, has_w, K));
     if (lane == 0) s.red_b[wave] = pmax;
     const float inv_rms = exact_inv_rms(s, v, K, eps);  // (its barriers publish red_b)
-    pmax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
+    pmax = red_max(s.red_b);
     const float amax = fmaxf(QMAX == 31 ? 1e-6f : 1e-8f, __fmul_rn(pmax, inv_rms));
     int csum = wave_sum_i32(quant_codes<QMAX>(s, p, K, inv_rms, amax));
     if (lane == 0) s.red_c[wave] = csum;
     __syncthreads();
-    csum_out = (s.red_c[0] + s.red_c[1]) + (s.red_c[2] + s.red_c[3]);
+    csum_out = red_sum(s.red_c);
     inv_out = amax * (1.0f / (float)QMAX);
 }
 
@@ -706,7 +736,7 @@ __device__ __forceinline__ float norm_record_inv31(Shared& s, float4 (&v)[kJ],
     float pmax = wave_max(weigh(p, v, w, has_w, K));
     if (lane == 0) s.red_b[wave] = pmax;
     const float inv_rms = exact_inv_rms(s, v, K, eps);  // (its barriers publish red_b)
-    pmax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
+    pmax = red_max(s.red_b);
     return fmaxf(1e-6f, __fmul_rn(pmax, inv_rms)) * (1.0f / 31.0f);
 }
 
@@ -753,8 +783,8 @@ __device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
         s.red_a[wave] = ss;
     }
     __syncthreads();
-    pmax = fmaxf(fmaxf(s.red_b[0], s.red_b[1]), fmaxf(s.red_b[2], s.red_b[3]));
-    ss = (s.red_a[0] + s.red_a[1]) + (s.red_a[2] + s.red_a[3]);
+    pmax = red_max(s.red_b);
+    ss = red_sum(s.red_a);
     const float r = inv_rms_ref(ss, K, eps, s_rsq);
     const float amax = __fmul_rn(pmax, r);
     // estimate within 1e-3 of inv_rms (any summation order of K <= 16384
@@ -785,14 +815,14 @@ __device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
         s.red_s[wave] = csum;
     }
     __syncthreads();
-    if ((s.red_c[0] | s.red_c[1] | s.red_c[2] | s.red_c[3]) != 0) {
+    if (red_or(s.red_c) != 0) {
         const float inv_rms = exact_inv_rms(s, v, K, eps);
         csum = wave_sum_i32(quant_codes<31>(s, p, K, inv_rms,
                                             fmaxf(1e-6f, __fmul_rn(pmax, inv_rms)), q_lo, q_hi));
         if (lane == 0) s.red_s[wave] = csum;
         __syncthreads();
     }
-    return (s.red_s[0] + s.red_s[1]) + (s.red_s[2] + s.red_s[3]);
+    return red_sum(s.red_s);
 }
 
 // ---------------------------------------------------------------- GEMV ----
@@ -1211,7 +1241,7 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
     constexpr int kWS = G >= 2 ? G / 2 : 1;          // waves per set of all heads
     constexpr int kNS = G >= 2 ? kW / kWS : 2 * kW;  // token sets
     static_assert(G <= 2 * kW, "at most 8 query heads per kv head");
-    constexpr int kVU = 8;  // tokens per step, their LDS reads issued together
+    constexpr int kVU = 8 * kNS <= kTpad - kTmax ? 8 : (kTpad - kTmax) / kNS;  // tokens per step
     static_assert(kVU * kNS <= kTpad - kTmax, "the zero padding covers one step");
     const int dq = lane & 31, half = lane >> 5;
     const int hd = G >= 2 ? (wave % kWS) * 2 + half : 0;
@@ -1303,7 +1333,7 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
 // Merge of the C chunk partials of query head g of kv head h (same formula
 // as attn_combine_kernel): out = sum_c e^{m_c-M} o_c / sum_c e^{m_c-M} l_c.
 // Thread (cp, d4) = (tid / 32, tid % 32) sums dims 4 d4.. over the chunks
-// c = cp, cp + 8, ... in order, and the 8 sums are added in cp order. The
+// c = cp, cp + kT/32, ... in order, and the kT/32 sums are added in cp order. The
 // first kU chunks of each thread and every chunk statistic are loaded
 // together.
 template <int G>
@@ -1315,11 +1345,12 @@ __device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int
     float* wts = reinterpret_cast<float*>(&a.vt[0][0]);  // [C] weights (V tile no longer needed)
     float* lcs = wts + p.C;
     constexpr int kU = 8;
+    constexpr int kCP = kT / 32;  // chunk sets: thread (cp, d4) takes chunks cp, cp + kCP, ...
     const int d4 = tid & 31, cp = tid >> 5;
     f4v ov[kU];
 #pragma unroll
     for (int u = 0; u < kU; ++u) {  // chunks past C read zeros (outside the resource)
-        const int c = cp + 8 * u;
+        const int c = cp + kCP * u;
         ov[u] = ldc16(r, (uint32_t)((c * G + g) * stride + 4 + 4 * d4) * 4);
     }
     for (int c = tid; c < p.C; c += kT) {
@@ -1345,7 +1376,7 @@ __device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int
     f4v acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
-        const int c = cp + 8 * u;
+        const int c = cp + kCP * u;
         if (c < p.C) {
             const float e = wts[c];
             acc4.x = __builtin_fmaf(e, ov[u].x, acc4.x);
@@ -1354,14 +1385,14 @@ __device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int
             acc4.w = __builtin_fmaf(e, ov[u].w, acc4.w);
         }
     }
-    for (int c0 = cp + 8 * kU; c0 < p.C; c0 += 8 * kU) {
+    for (int c0 = cp + kCP * kU; c0 < p.C; c0 += kCP * kU) {
         f4v v[kU];
 #pragma unroll
         for (int u = 0; u < kU; ++u)
-            v[u] = ldc16(r, (uint32_t)(((c0 + 8 * u) * G + g) * stride + 4 + 4 * d4) * 4);
+            v[u] = ldc16(r, (uint32_t)(((c0 + kCP * u) * G + g) * stride + 4 + 4 * d4) * 4);
 #pragma unroll
         for (int u = 0; u < kU; ++u) {
-            const int c = c0 + 8 * u;
+            const int c = c0 + kCP * u;
             if (c < p.C) {
                 const float e = wts[c];
                 acc4.x = __builtin_fmaf(e, v[u].x, acc4.x);
@@ -1371,7 +1402,7 @@ __device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int
             }
         }
     }
-    float* red = a.ow;  // [8][128]
+    float* red = a.ow;  // [kCP][128]
     red[cp * kD + 4 * d4] = acc4.x;
     red[cp * kD + 4 * d4 + 1] = acc4.y;
     red[cp * kD + 4 * d4 + 2] = acc4.z;
@@ -1380,7 +1411,7 @@ __device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int
     if (tid < kD) {
         float o = 0.0f;
 #pragma unroll
-        for (int q = 0; q < 8; ++q) o += red[q * kD + tid];
+        for (int q = 0; q < kCP; ++q) o += red[q * kD + tid];
         const size_t off = (size_t)(h * G + g) * kD + tid;
         const float y = o / a.mstat[g];
         stc(p.attns + (size_t)l * p.Hq * kD + off, y);
