@@ -397,8 +397,9 @@ PAGED_ROW_BYTES = 128 + 128 + 4 + 4
 
 
 def tern_bench(torch, e, cfg, host, args):
-    """Decode with a ternary KV cache (graph path: the persistent kernel is
-    INT8-only) and the ternary attention op at one layer's shape."""
+    """Decode with a ternary or paged KV cache (ternary: graph path; paged:
+    the engine mode asked for, persistent by default) and the mode's attention
+    op at one layer's shape."""
     from tenzo_amd import ops
     ctx, mode = args.ctx, args.kv_mode
     tok = 1
@@ -495,7 +496,8 @@ def tern_bench(torch, e, cfg, host, args):
         "dtype": ("int8 KV, fp32 scales" if mode == "paged_int8" else
                   "ternary KV (int32 dot, fp32 softmax)"), "data": "synthetic",
         "config": {"workload": f"BitNet-b1.58-2B-shaped greedy decode step, batch 1, context "
-                               f"{ctx}, {mode} KV cache (graph path)", "engine_mode": e.mode},
+                               f"{ctx}, {mode} KV cache ({e.mode} engine mode)",
+                   "engine_mode": e.mode},
         "roofline": {"bound": "hbm", "kernel": kernel,
                      "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None,
@@ -824,7 +826,9 @@ def main():
         raise SystemExit("--prefill runs the int8_fused cache")
     e, host = build_model(torch, cfg, ctx, args.kv_mode)
     if tern:
-        e.set_mode("graph")
+        # the persistent kernel runs paged_int8 (and int8_fused); the ternary
+        # modes run on the graph path
+        e.set_mode(args.mode if args.kv_mode == "paged_int8" else "graph")
         tern_bench(torch, e, cfg, host, args)
         e.close()
         return

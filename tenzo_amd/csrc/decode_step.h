@@ -20,10 +20,16 @@ struct DsParams {
     const uint4* head;          // packed int8 LM head (lm_head.hip layout)
     const float* head_scales;
     const float* rope;          // [max_seq][128] cos | sin
-    int8_t* kc;                 // [L][Hkv][max_seq][128]
+    int8_t* kc;                 // [L][Hkv][max_seq][128] (paged: the code pools)
     int8_t* vc;
-    uint16_t* ks;               // [L][Hkv][max_seq] fp16
+    uint16_t* ks;               // [L][Hkv][max_seq] fp16 (unused when paged)
     uint16_t* vs;
+    // paged_int8 (block_table non-null): pools of 16-token blocks, codes
+    // kc/vc [blocks][L][Hkv][16][128] and fp32 scales pks/pvs [blocks][L][Hkv][16];
+    // block_table[t / 16] is the pool block of token t
+    const int32_t* block_table;
+    float* pks;
+    float* pvs;
     // host-visible vectors of the last layer (x: the final hidden state)
     float* x;                   // [H] hidden state
     float* qkv;                 // [qd + 2 kvd]
@@ -60,6 +66,7 @@ constexpr int kDsMaxChunk = 256;    // context tokens per attention task, at mos
 constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
 constexpr int kDsCounters = 16;
 constexpr int kDsMaxLayers = 64;    // the layer table is staged in LDS
+constexpr int kDsMaxBlocks = 1024;  // paged: the block table is staged in LDS (16384 tokens)
 
 // uint32 words of the sync region for L layers and Hkv kv heads (a multiple of
 // 64, so the accumulators can follow it in one allocation).

@@ -172,6 +172,23 @@ __device__ __forceinline__ LayerRef layer(const DsParams&, int l) { return Layer
 
 // Copies the layer table and the RSQRTSS table into LDS (all threads; a block
 // barrier follows).
+// paged_int8: the sequence's block table (blocks 0 .. pos / 16), copied into
+// LDS at the start of the kernel, and the pool row of token t of (l, h):
+// ((block_table[t / 16] * L + l) * Hkv + h) * 16 + t % 16 (PagedKVCache's
+// layout, TenzoEngine.cpp:320-321).
+__shared__ int32_t s_bt[kDsMaxBlocks];
+__device__ __forceinline__ void stage_blocks(const DsParams& p) {
+    for (int i = threadIdx.x; i <= p.pos / 16; i += kT) s_bt[i] = p.block_table[i];
+}
+__device__ __forceinline__ uint32_t page_row(const DsParams& p, int l, int h, int t) {
+    return ((uint32_t)s_bt[t >> 4] * (uint32_t)(p.L * p.Hkv) + (uint32_t)(l * p.Hkv + h)) * 16u +
+           (uint32_t)(t & 15);
+}
+// Rows of the pools (a multiple of 16 per layer and kv head).
+__device__ __forceinline__ uint32_t pool_rows(const DsParams& p) {
+    return (uint32_t)((p.max_seq + 15) / 16) * (uint32_t)(p.L * p.Hkv) * 16u;
+}
+
 __device__ __forceinline__ void stage_layers(const DsParams& p) {
     static_assert(sizeof(DsLayer) % 4 == 0, "copied as words");
     const uint32_t* src = reinterpret_cast<const uint32_t*>(p.layers);
@@ -191,6 +208,12 @@ __host__ __device__ inline size_t w_head(int l, int h, int Hkv) {
 // l, each on its own 128-byte line: written once per launch, read through L2
 __host__ __device__ inline size_t w_rec(int l, int slot, int L, int Hkv) {
     return (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)(l * 4 + slot) * 32;
+}
+
+// paged_int8: counter of the chunks of kv head h of layer l that have
+// published their softmax statistics (one line each, after the records)
+__host__ __device__ inline size_t w_stat(int l, int h, int L, int Hkv) {
+    return (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)L * 4 * 32 + (size_t)(l * Hkv + h) * 64;
 }
 
 // Accumulator region of one layer: q|k|v, o, gate|up, down (int32 each).
@@ -370,17 +393,38 @@ __device__ __forceinline__ void load_tl1_tile(uint4 (&pf)[kPF], const uint4* __r
 // (pf[2r+1]) and its fp16 K and V scales (pfs[2r], pfs[2r+1]). Tokens past the chunk read
 // zeros; the new token's slot is read but not used. Later rounds are read in
 // the loops that use them.
+template <bool PAGED>
 __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[2 * kAR],
                                               const DsParams& p, int l, int h, int c) {
     const int lane = ltid() & 63, wave = lwave();
     const int t0 = c * p.T;
     const int nt = min(p.T, p.pos + 1 - t0);
+    const int d0 = (lane & 7) * 16;
+    if (PAGED) {
+        // each lane's token through the block table (tokens past the chunk read
+        // the context's last token: finite values nothing uses)
+        const uint32_t rows = pool_rows(p);
+        const __amdgpu_buffer_rsrc_t rk = rsrc(p.kc, rows * kD);
+        const __amdgpu_buffer_rsrc_t rv = rsrc(p.vc, rows * kD);
+        const __amdgpu_buffer_rsrc_t rks = rsrc(p.pks, rows * 4);
+        const __amdgpu_buffer_rsrc_t rvs = rsrc(p.pvs, rows * 4);
+#pragma unroll
+        for (int r = 0; r < kAR; ++r) {
+            const int tl = r * kRT + wave * 8 + (lane >> 3);
+            const uint32_t row = page_row(p, l, h, min(t0 + tl, p.pos));
+            pf[2 * r] = ld16(rk, row * kD + d0);
+            pfs[2 * r] = (uint32_t)ld4i(rks, row * 4);
+            pf[2 * r + 1] = ld16(rv, row * kD + d0);
+            pfs[2 * r + 1] = (uint32_t)ld4i(rvs, row * 4);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return;
+    }
     const size_t tok0 = ((size_t)l * p.Hkv + h) * p.max_seq + t0;
     const __amdgpu_buffer_rsrc_t rk = rsrc(p.kc + tok0 * kD, (uint32_t)nt * kD);
     const __amdgpu_buffer_rsrc_t rv = rsrc(p.vc + tok0 * kD, (uint32_t)nt * kD);
     const __amdgpu_buffer_rsrc_t rks = rsrc(p.ks + tok0, (uint32_t)nt * 2);
     const __amdgpu_buffer_rsrc_t rvs = rsrc(p.vs + tok0, (uint32_t)nt * 2);
-    const int d0 = (lane & 7) * 16;
 #pragma unroll
     for (int r = 0; r < kAR; ++r) {
         const int tl = r * kRT + wave * 8 + (lane >> 3);
@@ -1052,12 +1096,105 @@ __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
 
 template <int G>
 __device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int l, int h, int g);
+template <int G>
+__device__ __forceinline__ void attn_merge_sum(AttnShared& a, const DsParams& p, int l, int h,
+                                               int g);
+
+// paged_int8 softmax (:395-405) for chunk c of kv head h, whose raw scores
+// s_t are in a.sc: the chunk's (max m_c, sum l_c of e^{s_t - m_c}) per query
+// head go into its partial records; once all C chunks of the head have
+// published theirs (a counter per (layer, kv head), every chunk task of the
+// stage being resident), every chunk forms M = max m_c and
+// L = sum_c l_c e^{m_c - M} in the same order, and turns its scores into the
+// value weights p_t s_v[t], p_t = e^{s_t - M} / (L + 1e-8), 0 where p_t < 1e-7
+// (:412-414). L equals the reference's sum of e^{s_t - M} up to rounding.
+// Returns false when a wait timed out (the error word is set).
+template <int G>
+__device__ __forceinline__ bool paged_weights(AttnShared& a, const DsParams& p, int l, int h,
+                                              int c, int nt) {
+    const int tid = ltid(), lane = tid & 63, wave = lwave();
+    const int stride = kPS;
+    for (int g = wave; g < G; g += kW) {
+        float m = -1e30f;
+        for (int i = lane; i < nt; i += 64) m = fmaxf(m, a.sc[g][i]);
+        m = wave_max(m);
+        float lsum = 0.0f;
+        for (int i = lane; i < nt; i += 64) lsum += expf(a.sc[g][i] - m);
+        lsum = wave_sum_tree(lsum);
+        if (lane == 0) {
+            a.mstat[g] = m;
+            a.lstat[g] = lsum;
+        }
+    }
+    __syncthreads();
+    const float* rec = p.part + (size_t)h * p.C * G * stride;  // [C][G][stride]
+    if (p.C > 1) {
+        if (tid < G) {
+            float* pp = p.part + (((size_t)h * p.C + c) * G + tid) * stride;
+            stc(pp, a.mstat[tid]);
+            stc(pp + 1, a.lstat[tid]);
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) {
+            unsigned* ctr = p.sync + w_stat(l, h, p.L, p.Hkv);
+            __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            int ok = 1;
+            unsigned spins = 0;
+            while (ldcu(ctr) < (unsigned)p.C) {
+                if (++spins > kSpinLimit ||
+                    ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0)) {
+                    stcu(p.sync + w_err(p.L, p.Hkv), 1u);
+                    ok = 0;
+                    break;
+                }
+            }
+            a.last = ok;
+        }
+        __syncthreads();
+        if (a.last == 0) return false;
+        for (int g = wave; g < G; g += kW) {
+            float M = -1e30f;
+            for (int q = lane; q < p.C; q += 64) M = fmaxf(M, ldc(rec + ((size_t)q * G + g) * stride));
+            M = wave_max(M);
+            float L = 0.0f;
+            for (int q = lane; q < p.C; q += 64) {
+                const float* pr = rec + ((size_t)q * G + g) * stride;
+                L = __builtin_fmaf(ldc(pr + 1), expf(ldc(pr) - M), L);
+            }
+            L = wave_sum_tree(L);
+            if (lane == 0) {
+                a.mstat[g] = M;
+                a.lstat[g] = __fdiv_rn(1.0f, L + 1e-8f);
+            }
+        }
+    } else {
+        if (tid < G) a.lstat[tid] = __fdiv_rn(1.0f, a.lstat[tid] + 1e-8f);
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += kW) {
+        const float M = a.mstat[g], inv = a.lstat[g];
+        for (int i = lane; i < nt; i += 64) {
+            const float pw = __fmul_rn(expf(a.sc[g][i] - M), inv);
+            a.sc[g][i] = pw < 1e-7f ? 0.0f : __fmul_rn(pw, a.vsc[i]);
+        }
+        a.sc[g][nt + lane] = 0.0f;  // the value loop runs past nt by < 64
+    }
+    __syncthreads();
+    return true;
+}
 
 // Attention of the G query heads of kv head h over context chunk c of layer
 // l (attention_int8_fused, :434-864): q|k|v from the QKV accumulators, RoPE,
 // the new token's K/V quantized and appended, chunk softmax and weighted
 // values; with several chunks the last one to finish merges the partials.
-template <int G>
+// PAGED (paged_int8, PagedKVCache::forward_attention_raw :248-445): rows
+// through the block table, fp32 scales, and the softmax normalized over the
+// whole context before the values, so that weights below 1e-7 are skipped as
+// the reference does: each chunk publishes its (max, sum of exponentials),
+// waits until every chunk of its kv head has, and forms the normalized
+// weights from the combined statistics; the partials are then plain sums.
+template <int G, bool PAGED>
 __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c) {
     AttnShared& a = sh.a;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
@@ -1099,7 +1236,7 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
     __builtin_amdgcn_s_barrier();
     uint4 cur[kPF];
     uint32_t curs[2 * kAR];
-    load_att_tile(cur, curs, p, l, h, c);
+    load_att_tile<PAGED>(cur, curs, p, l, h, c);
     wait_vm<4 * kAR>();  // all but the tile
     // RoPE on the G query heads (:460-481); chunk 0 also stores q as floats
     {
@@ -1140,13 +1277,19 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
         float s;
         int8_t* nb = wave == 0 ? a.newk : a.newv;
         quant_kv(x0, x1, nb, lane, &s);
-        const uint16_t sh16 = float_to_half_bits(s);
-        int8_t* dst = (wave == 0 ? p.kc : p.vc) + (head + p.pos) * kD;
+        const size_t row = PAGED ? (size_t)page_row(p, l, h, p.pos) : head + p.pos;
+        int8_t* dst = (wave == 0 ? p.kc : p.vc) + row * kD;
         dst[lane] = nb[lane];
         dst[lane + 64] = nb[lane + 64];
         if (lane == 0) {
-            (wave == 0 ? p.ks : p.vs)[head + p.pos] = sh16;
-            a.news[wave] = half_bits_to_float(sh16);
+            if (PAGED) {  // fp32 scales (:342-345)
+                (wave == 0 ? p.pks : p.pvs)[row] = s;
+                a.news[wave] = s;
+            } else {
+                const uint16_t sh16 = float_to_half_bits(s);
+                (wave == 0 ? p.ks : p.vs)[row] = sh16;
+                a.news[wave] = half_bits_to_float(sh16);
+            }
         }
     }
     __syncthreads();
@@ -1174,8 +1317,18 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
             } else if (r < kAR) {
                 kv = cur[2 * r];
                 vv = cur[2 * r + 1];
-                skf = half_bits_to_float((uint16_t)curs[2 * r]);
-                svf = half_bits_to_float((uint16_t)curs[2 * r + 1]);
+                skf = PAGED ? __uint_as_float(curs[2 * r]) : half_bits_to_float((uint16_t)curs[2 * r]);
+                svf = PAGED ? __uint_as_float(curs[2 * r + 1])
+                            : half_bits_to_float((uint16_t)curs[2 * r + 1]);
+            } else if (PAGED) {
+                // past the preloaded rounds: rows through the block table
+                // (tokens past the chunk read the context's last token)
+                const uint32_t rows = pool_rows(p);
+                const uint32_t row = page_row(p, l, h, min(t, p.pos));
+                kv = ld16(rsrc(p.kc, rows * kD), row * kD + d0);
+                vv = ld16(rsrc(p.vc, rows * kD), row * kD + d0);
+                skf = __int_as_float(ld4i(rsrc(p.pks, rows * 4), row * 4));
+                svf = __int_as_float(ld4i(rsrc(p.pvs, rows * 4), row * 4));
             } else {
                 // past the preloaded rounds (long chunks): tokens past the
                 // chunk read zeros through the resource bounds
@@ -1208,11 +1361,16 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
                 const float f = skf * kAttnScale;
 #pragma unroll
                 for (int g = 0; g < G; ++g)
-                    if ((lane & 7) == (g & 7)) a.sc[g][tl] = pr[g] * f;
+                    if ((lane & 7) == (g & 7))  // paged: (dot * s_k) * qk_scale (:391)
+                        a.sc[g][tl] = PAGED ? __fmul_rn(__fmul_rn(pr[g], skf), kAttnScale)
+                                            : pr[g] * f;
             }
         }
     }
     __syncthreads();
+    if (PAGED) {
+        if (!paged_weights<G>(a, p, l, h, c, nt)) return;
+    } else {
     // chunk softmax statistics (:824-830); the weight kept for the values is
     // e^{s-m} times the token's V scale (the product the multi-kernel path
     // forms per token)
@@ -1234,6 +1392,7 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
         }
     }
     __syncthreads();
+    }
     // weighted values (:842-851): lane l owns dims 4(l%32)..+3 of one head
     // (G >= 2: head 2*(wave % (G/2)) + l/32; G = 1: head 0); the kNS wave
     // (half-wave) sets that own the same outputs take every kNS-th token, and
@@ -1281,7 +1440,8 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
         if (p.C == 1) {
             const float L = a.lstat[hd];
             const size_t off = (size_t)(h * G + hd) * kD + d;
-            const float4 r = make_float4(o[0] / L, o[1] / L, o[2] / L, o[3] / L);
+            const float4 r = PAGED ? make_float4(o[0], o[1], o[2], o[3])  // normalized weights
+                                   : make_float4(o[0] / L, o[1] / L, o[2] / L, o[3] / L);
             stc16(rsrc(p.attns + (size_t)l * p.Hq * kD, (uint32_t)p.Hq * kD * 4),
                   (uint32_t)off * 4, r);
             if (l == p.L - 1) stc16(rsrc(p.attn, (uint32_t)p.Hq * kD * 4), (uint32_t)off * 4, r);
@@ -1291,7 +1451,7 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
             float* pp = pc + hd * stride;
             stc16(rsrc(pc, G * stride * 4), (uint32_t)(hd * stride + 4 + d) * 4,
                   make_float4(o[0], o[1], o[2], o[3]));
-            if (dq == 0) {
+            if (!PAGED && dq == 0) {  // (paged: the statistics are stored already)
                 stc(pp, a.mstat[hd]);
                 stc(pp + 1, a.lstat[hd]);
             }
@@ -1327,7 +1487,12 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
     }
     __syncthreads();
     const int r = a.last;
-    for (int g = r; r >= 0 && g < G; g += M) attn_merge<G>(a, p, l, h, g);
+    for (int g = r; r >= 0 && g < G; g += M) {
+        if (PAGED)
+            attn_merge_sum<G>(a, p, l, h, g);
+        else
+            attn_merge<G>(a, p, l, h, g);
+    }
 }
 
 // Merge of the C chunk partials of query head g of kv head h (same formula
@@ -1420,6 +1585,47 @@ __device__ __forceinline__ void attn_merge(AttnShared& a, const DsParams& p, int
     __syncthreads();
 }
 
+// paged_int8: out = the sum of the C chunk sums of query head g (their weights
+// are normalized already; paged_sum_kernel's sum in another order). Thread
+// (cp, d4) sums dims 4 d4.. over the chunks cp, cp + kT/32, ... and the kT/32
+// sums are added in cp order.
+template <int G>
+__device__ __forceinline__ void attn_merge_sum(AttnShared& a, const DsParams& p, int l, int h,
+                                               int g) {
+    const int tid = ltid();
+    const int stride = kPS;
+    const float* base = p.part + (size_t)h * p.C * G * stride;
+    const __amdgpu_buffer_rsrc_t r = rsrc(base, (uint32_t)(p.C * G * stride) * 4);
+    constexpr int kU = 8;
+    constexpr int kCP = kT / 32;
+    const int d4 = tid & 31, cp = tid >> 5;
+    f4v acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = cp; c0 < p.C; c0 += kCP * kU) {
+        f4v v[kU];
+#pragma unroll
+        for (int u = 0; u < kU; ++u)  // chunks past C read zeros (outside the resource)
+            v[u] = ldc16(r, (uint32_t)(((c0 + kCP * u) * G + g) * stride + 4 + 4 * d4) * 4);
+#pragma unroll
+        for (int u = 0; u < kU; ++u)
+            if (c0 + kCP * u < p.C) acc4 += v[u];
+    }
+    float* red = a.ow;  // [kCP][128]
+    red[cp * kD + 4 * d4] = acc4.x;
+    red[cp * kD + 4 * d4 + 1] = acc4.y;
+    red[cp * kD + 4 * d4 + 2] = acc4.z;
+    red[cp * kD + 4 * d4 + 3] = acc4.w;
+    __syncthreads();
+    if (tid < kD) {
+        float o = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kCP; ++q) o += red[q * kD + tid];
+        const size_t off = (size_t)(h * G + g) * kD + tid;
+        stc(p.attns + (size_t)l * p.Hq * kD + off, o);
+        if (l == p.L - 1) stc(p.attn + off, o);
+    }
+    __syncthreads();
+}
+
 // ------------------------------------------------------------ LM head -----
 
 __device__ __forceinline__ void am_combine(float& v, int& i, float ov, int oi) {
@@ -1465,7 +1671,7 @@ __device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int
         norm_quant<127>(s, xv, nwr, p.final_norm != nullptr, p.H, p.eps, inv, cs);
         const int HC = p.H / 16;
         const int4* c4 = reinterpret_cast<const int4*>(s.codes);
-        constexpr int kHU = 16;  // 16-byte loads in flight per lane
+        constexpr int kHU = 8;  // 16-byte loads in flight per lane (x 8 waves)
         for (int t = first; t < n; t += p.nwg) {
             // row block t: chunks of 16 columns x 64 rows, 1 KiB each (past HC: zeros)
             const __amdgpu_buffer_rsrc_t rh =
@@ -1553,7 +1759,7 @@ __device__ __forceinline__ int touch_norm(const DsParams& p, int s) {
     return ld4i(rsrc(nw, nw ? (uint32_t)K * 4 : 0u), (uint32_t)line * 128);
 }
 
-template <int G>
+template <int G, bool PAGED>
 __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     __shared__ SharedAll sh;
     __shared__ int s_abort;
@@ -1564,6 +1770,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     // no line of this launch's per-layer vectors may survive in L2 from an
     // earlier launch (they are read with cached loads after the first barrier)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (PAGED) stage_blocks(p);  // (stage_layers' block barrier covers it)
     stage_layers(p);
     int off = 0;  // first workgroup of the current stage
     int sink = 0;
@@ -1586,7 +1793,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
         }
         if (kind == S_ATT) {
             for (int t = first; t < n; t += p.nwg) {
-                attn_task<G>(sh, p, l, t / p.C, t % p.C);
+                attn_task<G, PAGED>(sh, p, l, t / p.C, t % p.C);
                 __syncthreads();
             }
         } else if (first < n || rec_writer(p, first, n)) {
@@ -1603,7 +1810,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
 }  // namespace
 
 size_t ds_sync_words(int L, int Hkv) {
-    const size_t w = (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)L * 4 * 32;
+    const size_t w = (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)L * 4 * 32 + (size_t)L * Hkv * 64;
     return (w + 63) / 64 * 64;
 }
 size_t ds_error_word(int L, int Hkv) { return w_err(L, Hkv); }
@@ -1635,7 +1842,7 @@ int ds_grid_size() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_kernel<4>, kT, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_kernel<4, false>, kT, 0) !=
             hipSuccess ||
         per_cu < 1)
         return 0;
@@ -1666,17 +1873,30 @@ int ds_max_context(int G) { return kTmax * kD / 8 / G * kTmax; }
 int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
     void* args[] = {const_cast<DsParams*>(&p)};
     void* fn = nullptr;
-    switch (G) {
-        case 1: fn = (void*)decode_step_kernel<1>; break;
-        case 2: fn = (void*)decode_step_kernel<2>; break;
-        case 4: fn = (void*)decode_step_kernel<4>; break;
-        case 8: fn = (void*)decode_step_kernel<8>; break;
+    const bool paged = p.block_table != nullptr;
+    switch (G * 2 + (paged ? 1 : 0)) {
+        case 2: fn = (void*)decode_step_kernel<1, false>; break;
+        case 3: fn = (void*)decode_step_kernel<1, true>; break;
+        case 4: fn = (void*)decode_step_kernel<2, false>; break;
+        case 5: fn = (void*)decode_step_kernel<2, true>; break;
+        case 8: fn = (void*)decode_step_kernel<4, false>; break;
+        case 9: fn = (void*)decode_step_kernel<4, true>; break;
+        case 16: fn = (void*)decode_step_kernel<8, false>; break;
+        case 17: fn = (void*)decode_step_kernel<8, true>; break;
         default:
             set_error("decode step: query heads per kv head must be 1, 2, 4 or 8");
             return TENZO_ERROR_UNSUPPORTED;
     }
     if (p.L > kDsMaxLayers) {
         set_error("decode step: at most %d layers", kDsMaxLayers);
+        return TENZO_ERROR_UNSUPPORTED;
+    }
+    // paged: the block table fits in LDS, and every chunk task of the
+    // attention stage is resident (their softmax waits for all of them)
+    if (paged && (p.pos / 16 >= kDsMaxBlocks || p.C * p.Hkv > p.nwg ||
+                  (size_t)(p.max_seq + 15) / 16 * 16 * p.L * p.Hkv * kD >= (1ull << 32))) {
+        set_error("decode step (paged): context %d needs %d attention tasks for %d workgroups",
+                  p.pos + 1, p.C * p.Hkv, p.nwg);
         return TENZO_ERROR_UNSUPPORTED;
     }
     if (p.H % 64 || p.F % 64 || p.H > kJ * 4 * kT || p.F > kJ * 4 * kT) {

@@ -826,10 +826,19 @@ int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
 
 // Whether the persistent kernel can run this model as loaded.
 bool ds_usable(tenzo_engine_t e) {
-    if (e->ds_nwg <= 0 || e->kv_kind != 0 || e->head_kind != 1 || e->H > 8192 || e->F > 8192 ||
-        e->H % 64 || e->F % 64 || e->L > kDsMaxLayers ||
+    if (e->ds_nwg <= 0 || (e->kv_kind != 0 && e->kv_kind != 3) || e->head_kind != 1 ||
+        e->H > 8192 || e->F > 8192 || e->H % 64 || e->F % 64 || e->L > kDsMaxLayers ||
         e->max_seq > ds_max_context(e->Hq / e->Hkv))
         return false;
+    if (e->kv_kind == 3) {
+        // paged: the block table in LDS, every attention chunk task resident
+        // (chunks of at most kDsMaxChunk tokens, ds_chunk_budget of them per
+        // kv head), the pools addressable with 32-bit offsets
+        if (e->max_seq > kDsMaxBlocks * 16 ||
+            e->max_seq > kDsMaxChunk * ds_chunk_budget(e->ds_nwg, e->Hkv) ||
+            (size_t)e->pg_blocks * 16 * e->L * e->Hkv * kD >= (1ull << 32))
+            return false;
+    }
     for (const DevLayer& d : e->layers)
         if (!d.mlp) return false;
     return true;
@@ -864,8 +873,14 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.rope = e->rope;
     p.kc = e->kc;
     p.vc = e->vc;
-    p.ks = e->ks;
-    p.vs = e->vs;
+    if (e->kv_kind == 3) {
+        p.block_table = e->pg_bt;
+        p.pks = (float*)e->ks;
+        p.pvs = (float*)e->vs;
+    } else {
+        p.ks = (uint16_t*)e->ks;
+        p.vs = (uint16_t*)e->vs;
+    }
     p.x = e->x;
     p.qkv = e->qkv;
     p.attn = e->attn;

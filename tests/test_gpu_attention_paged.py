@@ -108,15 +108,21 @@ def eng_mod(torch_dev):
 # six chained steps as for int8_fused (each step's last-bit attention differences
 # can move an activation code by one, ~1e-3 of the logits, so longer chains are
 # not held to 1e-3); context 14 crosses into a new block at the third step
-@pytest.mark.parametrize("mode,ctx", [("graph", 9), ("eager", 14), ("graph", 600), ("graph", 14)])
+@pytest.mark.parametrize("mode,ctx", [("graph", 9), ("eager", 14), ("graph", 600), ("graph", 14),
+                                      ("persistent", 0), ("persistent", 14),
+                                      ("persistent", 600), ("persistent", 2039)])
 def test_engine_paged_matches_oracle(eng_mod, mode, ctx):
-    sm = synth.make_model(CFG, seed=71, ctx=ctx)
-    om = oracle.OracleModel(sm, kv_mode=3, kv=to_pools(sm, CFG))
-    with eng_mod.Engine(CFG, kv_mode="paged_int8") as e:
+    """Graph, eager and persistent (one launch per token: statistics of every
+    chunk of a kv head combined in-kernel before the values) engines against
+    the oracle's paged step; the persistent cases cover one chunk (first
+    token), short chunks and 8-token chunks spread over 128 blocks."""
+    cfg = CFG if ctx < 1000 else synth.DecodeConfig(**{**CFG.__dict__, "max_seq": 2048})
+    sm = synth.make_model(cfg, seed=71, ctx=ctx)
+    om = oracle.OracleModel(sm, kv_mode=3, kv=to_pools(sm, cfg))
+    with eng_mod.Engine(cfg, kv_mode="paged_int8") as e:
         e.set_model(sm)
-        e.set_mode("persistent")  # the persistent kernel is int8_fused only
-        assert e.mode == "graph"
         e.set_mode(mode)
+        assert e.mode == mode
         tok = 5
         for i in range(6):
             print(f"step {i} mode={mode} ctx={ctx}", flush=True)
@@ -172,6 +178,7 @@ def test_engine_kv_modes_chained_decode_and_prefill(eng_mod, kv_mode):
     with eng_mod.Engine(CFG, kv_mode=kv_mode) as a, eng_mod.Engine(CFG, kv_mode=kv_mode) as b:
         for e in (a, b):
             e.set_model(sm)
+            e.set_mode("graph")  # the batched prefill's own arithmetic (not the persistent kernel's)
         a.prefill_batch(toks)
         for t in toks:
             b.prefill(t)
