@@ -397,9 +397,8 @@ PAGED_ROW_BYTES = 128 + 128 + 4 + 4
 
 
 def tern_bench(torch, e, cfg, host, args):
-    """Decode with a ternary or paged KV cache (ternary: graph path; paged:
-    the engine mode asked for, persistent by default) and the mode's attention
-    op at one layer's shape."""
+    """Decode with a ternary or paged KV cache (the engine mode asked for,
+    persistent by default) and the mode's attention op at one layer's shape."""
     from tenzo_amd import ops
     ctx, mode = args.ctx, args.kv_mode
     tok = 1
@@ -826,9 +825,7 @@ def main():
         raise SystemExit("--prefill runs the int8_fused cache")
     e, host = build_model(torch, cfg, ctx, args.kv_mode)
     if tern:
-        # the persistent kernel runs paged_int8 (and int8_fused); the ternary
-        # modes run on the graph path
-        e.set_mode(args.mode if args.kv_mode == "paged_int8" else "graph")
+        e.set_mode(args.mode)  # the persistent kernel runs every KV mode
         tern_bench(torch, e, cfg, host, args)
         e.close()
         return

@@ -23,14 +23,14 @@
 // heads of the kv head, chunk partials (m, l, o) merged by attn_combine_kernel.
 #include "attention.h"
 #include "common.h"
+#include "tern_kv.h"
 
 namespace tz {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kRowW = 8;    // dwords per cache row
+constexpr int kRowW = kTernRowW;  // dwords per cache row
 constexpr int kParts = 8;   // token sets of the value pass (32 threads each)
-constexpr float kScaleFactor = 0.08838834764831845f;  // 1/sqrt(128)
 
 struct TernArgs {
     const float* q;
@@ -50,63 +50,6 @@ struct TernArgs {
     float* q_rot;
     float* k_rot;
 };
-
-// Sum over the 128 dims of x of |x_d| (masked: only the |x_d| > th) in the
-// order the reference build evaluates its loops (-O3 -mavx2 -ffast-math,
-// :544-561): eight partial sums over dims j, j+8, ..., j+120 in index order,
-// then (l0+l4, l1+l5, l2+l6, l3+l7), (a0+a2, a1+a3), b0+b1 -- the xor
-// butterfly over lanes 4, 2, 1 of lanes 0..7. Called by a whole wave; the
-// result is returned in every lane. Adding 0 for a masked dim leaves a
-// partial sum unchanged, as the build's masked vector add does.
-__device__ __forceinline__ float tern_abs_sum(const float* x, int lane, bool masked, float th) {
-    float l = 0.0f;
-    if (lane < 8) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const float a = fabsf(x[lane + 8 * i]);
-            l += (!masked || a > th) ? a : 0.0f;
-        }
-    }
-    l += __shfl_xor(l, 4, 64);
-    l += __shfl_xor(l, 2, 64);
-    l += __shfl_xor(l, 1, 64);
-    return __shfl(l, 0, 64);
-}
-
-// Threshold and scale of a 128-dim row (:544-565).
-__device__ __forceinline__ void tern_stats(const float* x, int lane, float* th_out, float* s_out) {
-    const float mean = tern_abs_sum(x, lane, false, 0.0f) * (1.0f / 128.0f);
-    const float th = 0.5f * mean;
-    const float nz = tern_abs_sum(x, lane, true, th);
-    const int cnt = __popcll(__ballot(fabsf(x[lane]) > th)) +
-                    __popcll(__ballot(fabsf(x[lane + 64]) > th));
-    *th_out = th;
-    *s_out = cnt > 0 ? __fdiv_rn(nz, (float)cnt) : mean + 1e-6f;
-}
-
-__device__ __forceinline__ uint32_t tern_field(float v, float th) {
-    return v > th ? 2u : (v < -th ? 0u : 1u);
-}
-
-// Dword w (dims 16w .. 16w+15) of a 2-bit row (:567-582).
-__device__ __forceinline__ uint32_t tern_word(const float* x, int w, float th) {
-    uint32_t r = 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) r |= tern_field(x[16 * w + i], th) << (2 * i);
-    return r;
-}
-
-// Dword w of the row's sign bitplanes {kp0, kp1, kn0, kn1} (:622-633).
-__device__ __forceinline__ uint32_t plane_word(const float* x, int lane, float th) {
-    const uint64_t p0 = __ballot(x[lane] > th), p1 = __ballot(x[lane + 64] > th);
-    const uint64_t n0 = __ballot(x[lane] < -th), n1 = __ballot(x[lane + 64] < -th);
-    const int w = lane & 7;
-    const uint64_t v = w < 2 ? p0 : (w < 4 ? p1 : (w < 6 ? n0 : n1));
-    return (uint32_t)(w & 1 ? v >> 32 : v);
-}
-
-// A field 3 decodes as 0: clear bit 1 of every field whose bit 0 is set.
-__device__ __forceinline__ uint32_t canon_fields(uint32_t w) { return w & ~((w & 0x55555555u) << 1); }
 
 template <int MODE, int G>
 __global__ void __launch_bounds__(256) attn_tern_chunk_kernel(TernArgs a) {
@@ -179,39 +122,12 @@ __global__ void __launch_bounds__(256) attn_tern_chunk_kernel(TernArgs a) {
     const int jobs = G + (has_new ? 2 : 0);
     for (int j = wave; j < jobs; j += 4) {
         if (j < G) {
-            const float* q = qs[j];
-            if (MODE == 1) {
-                // as built: s_q = max|q| * (1/127), codes round(q * (127 / max|q|))
-                const float x0 = q[lane], x1 = q[lane + 64];
-                const float mx = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
-                const float s_q = mx > 0.0f ? __fmul_rn(mx, 1.0f / 127.0f) : 1.0f;
-                const float inv = mx > 0.0f ? __fdiv_rn(127.0f, mx) : 1.0f;
-                const int c0 = (int)roundf(__fmul_rn(x0, inv));
-                const int c1 = (int)roundf(__fmul_rn(x1, inv));
-                int8_t* qb = reinterpret_cast<int8_t*>(qw[j]);
-                const int d0 = lane, d1 = lane + 64;
-                qb[4 * (8 * (d0 & 3) + (d0 >> 4)) + ((d0 & 15) >> 2)] = (int8_t)c0;
-                qb[4 * (8 * (d1 & 3) + (d1 >> 4)) + ((d1 & 15) >> 2)] = (int8_t)c1;
-                const int sum = wave_sum_i32(c0 + c1);
-                if (lane == 0) {
-                    qsum[j] = sum;
-                    qeff[j] = __fmul_rn(s_q, kScaleFactor);
-                }
-            } else {
-                float th, s;
-                tern_stats(q, lane, &th, &s);
-                const uint32_t w = plane_word(q, lane, th);
-                if (lane < kRowW) qw[j][lane] = w;
-                if (lane == 0) qeff[j] = __fmul_rn(s, kScaleFactor);
-            }
+            tern_query<MODE>(qs[j], lane, qw[j], &qsum[j], &qeff[j]);
         } else {
             const int kv = j - G;  // 0: k, 1: v
-            const float* x = xn[kv];
-            float th, s;
-            tern_stats(x, lane, &th, &s);
-            uint32_t w = (MODE == 2 && kv == 0) ? plane_word(x, lane, th) : 0u;
+            float s;
+            const uint32_t w = tern_row<MODE>(xn[kv], kv, lane, &s);
             if (lane < kRowW) {
-                if (!(MODE == 2 && kv == 0)) w = tern_word(x, lane, th);
                 nrow[kv][lane] = w;
                 uint32_t* dst = reinterpret_cast<uint32_t*>((kv == 0 ? a.kb : a.vb) +
                                                             (head + pos) * 32);
@@ -248,44 +164,10 @@ __global__ void __launch_bounds__(256) attn_tern_chunk_kernel(TernArgs a) {
             skf = a.ks[head + t];
             vsc[tid] = a.vs[head + t];
         }
-        if (MODE == 1) {
-            uint32_t m0[kRowW], m1[kRowW], m2[kRowW], m3[kRowW];
+        float scv[G];
+        tern_scores<G, MODE>(kr, qw, qsum, qeff, skf, scv);
 #pragma unroll
-            for (int w = 0; w < kRowW; ++w) {
-                const uint32_t f = canon_fields(kr[w]);
-                m0[w] = f & 0x03030303u;         // field 0 of each byte
-                m1[w] = f & 0x0C0C0C0Cu;         // 4 x field 1
-                m2[w] = f & 0x30303030u;         // 16 x field 2
-                m3[w] = (f >> 2) & 0x30303030u;  // 16 x field 3
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const int* Q = reinterpret_cast<const int*>(qw[g]);
-                int a0 = 0, a1 = 0, a2 = 0;
-#pragma unroll
-                for (int w = 0; w < kRowW; ++w) {
-                    a0 = sdot4(m0[w], Q[w], a0);
-                    a1 = sdot4(m1[w], Q[8 + w], a1);
-                    a2 = sdot4(m2[w], Q[16 + w], a2);
-                    a2 = sdot4(m3[w], Q[24 + w], a2);
-                }
-                // sum_d q_d (field_d - 1): the scaled sums are exact multiples
-                const int dot = a0 + (a1 >> 2) + (a2 >> 4) - qsum[g];
-                sc[g][tid] = __fmul_rn((float)dot, __fmul_rn(qeff[g], skf));
-            }
-        } else {
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const uint32_t* Q = qw[g];
-                int pm = 0, nm = 0;
-#pragma unroll
-                for (int i = 0; i < kRowW; ++i) {
-                    pm += __popc(Q[i] & kr[i]);
-                    nm += __popc(Q[i] & kr[i ^ 4]);
-                }
-                sc[g][tid] = __fmul_rn((float)(pm - nm), __fmul_rn(qeff[g], skf));
-            }
-        }
+        for (int g = 0; g < G; ++g) sc[g][tid] = scv[g];
     }
     __syncthreads();
 
@@ -319,10 +201,8 @@ __global__ void __launch_bounds__(256) attn_tern_chunk_kernel(TernArgs a) {
         const int word = bi >> 2, sh = 8 * (bi & 3);
         for (int t = p; t < nt; t += kParts) {
             const uint32_t* row = reinterpret_cast<const uint32_t*>(vt[t]);
-            const uint32_t f = canon_fields((row[word] >> sh) & 0xffu);
             float w[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) w[k] = (float)((int)((f >> (2 * k)) & 3u) - 1);
+            tern_value4(row[word] >> sh, w);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 const float wt = sc[g][t];

@@ -28,8 +28,10 @@ struct DsParams {
     // kc/vc [blocks][L][Hkv][16][128] and fp32 scales pks/pvs [blocks][L][Hkv][16];
     // block_table[t / 16] is the pool block of token t
     const int32_t* block_table;
-    float* pks;
+    float* pks;                 // fp32 scales: paged pools, or [L][Hkv][max_seq] (ternary)
     float* pvs;
+    int kv_mode;                // 0 int8_fused, 1 tl1_fused, 2 popcount_fused, 3 paged_int8
+                                // (ternary: kc / vc hold 32-byte rows [L][Hkv][max_seq][32])
     // host-visible vectors of the last layer (x: the final hidden state)
     float* x;                   // [H] hidden state
     float* qkv;                 // [qd + 2 kvd]

@@ -50,6 +50,7 @@
 // multi-kernel path (tl1.hip, attention.hip, lm_head.hip).
 #include "attention.h"
 #include "decode_step.h"
+#include "tern_kv.h"
 
 namespace tz {
 namespace {
@@ -254,6 +255,14 @@ struct AttnShared {
     int8_t newv[kD] __attribute__((aligned(16)));
     float news[2];
     int last;
+    // ternary modes: the new token's rotated k and its v, the query codes and
+    // the appended rows (tern_kv.h)
+    float xn[2][kD];
+    uint32_t qw[8][32];
+    int qsum[8];
+    float qeff[8];
+    uint32_t nrow[2][kTernRowW];
+    float nsc[2];
 };
 
 union SharedAll {
@@ -1194,8 +1203,9 @@ __device__ __forceinline__ bool paged_weights(AttnShared& a, const DsParams& p, 
 // the reference does: each chunk publishes its (max, sum of exponentials),
 // waits until every chunk of its kv head has, and forms the normalized
 // weights from the combined statistics; the partials are then plain sums.
-template <int G, bool PAGED>
+template <int G, int KVM>
 __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c) {
+    constexpr bool PAGED = KVM == 3, TERN = KVM == 1 || KVM == 2;
     AttnShared& a = sh.a;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
     const int ctx = p.pos + 1;
@@ -1236,8 +1246,26 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
     __builtin_amdgcn_s_barrier();
     uint4 cur[kPF];
     uint32_t curs[2 * kAR];
-    load_att_tile<PAGED>(cur, curs, p, l, h, c);
-    wait_vm<4 * kAR>();  // all but the tile
+    static_assert(kPF >= 4 && 2 * kAR >= 2, "a ternary K|V row pair fits the tile registers");
+    if constexpr (TERN) {
+        // thread tid: the 32-byte K and V rows and fp32 scales of token t0 + tid
+        // (past the head's rows: zeros)
+        const __amdgpu_buffer_rsrc_t rk = rsrc(p.kc + head * 32, (uint32_t)p.max_seq * 32);
+        const __amdgpu_buffer_rsrc_t rv = rsrc(p.vc + head * 32, (uint32_t)p.max_seq * 32);
+        const __amdgpu_buffer_rsrc_t rks = rsrc(p.pks + head, (uint32_t)p.max_seq * 4);
+        const __amdgpu_buffer_rsrc_t rvs = rsrc(p.pvs + head, (uint32_t)p.max_seq * 4);
+        const uint32_t tt = (uint32_t)min(t0 + tid, p.max_seq);
+        cur[0] = ld16(rk, tt * 32);
+        cur[1] = ld16(rk, tt * 32 + 16);
+        cur[2] = ld16(rv, tt * 32);
+        cur[3] = ld16(rv, tt * 32 + 16);
+        curs[0] = (uint32_t)ld4i(rks, tt * 4);
+        curs[1] = (uint32_t)ld4i(rvs, tt * 4);
+        wait_vm<6>();  // all but the rows
+    } else {
+        load_att_tile<PAGED>(cur, curs, p, l, h, c);
+        wait_vm<4 * kAR>();  // all but the tile
+    }
     // RoPE on the G query heads (:460-481); chunk 0 also stores q as floats
     {
         const float sq = inv * Lw.sc(0);
@@ -1260,7 +1288,24 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
         }
     }
     // the new token: RoPE on k, quantize-append k and v (:482-533)
-    if (has_new && wave < 2) {
+    if (TERN && has_new && wave < 2) {
+        // ternary: rotated k and raw v to LDS; their rows are formed below
+        const float sk = inv * Lw.sc(wave == 0 ? 1 : 2);
+        float x0 = gemv_y(ka0, cs, sk);
+        float x1 = gemv_y(ka1, cs, sk);
+        if (l == p.L - 1) {
+            stc(p.qkv + krow + lane, x0);
+            stc(p.qkv + krow + lane + 64, x1);
+        }
+        if (wave == 0) {
+            const float r0 = __builtin_fmaf(x0, kc0, -(x1 * ks0));
+            const float r1 = __builtin_fmaf(x0, ks0, x1 * kc0);
+            x0 = r0;
+            x1 = r1;
+        }
+        a.xn[wave][lane] = x0;
+        a.xn[wave][lane + 64] = x1;
+    } else if (!TERN && has_new && wave < 2) {
         const float sk = inv * Lw.sc(wave == 0 ? 1 : 2);
         float x0 = gemv_y(ka0, cs, sk);
         float x1 = gemv_y(ka1, cs, sk);
@@ -1294,6 +1339,55 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
     }
     __syncthreads();
 
+    if constexpr (TERN) {
+        // query codes of the G heads and the new token's rows (:534-648,
+        // :700-714, :766-791), one wave per job
+        const int jobs = G + (has_new ? 2 : 0);
+        for (int j = wave; j < jobs; j += kW) {
+            if (j < G) {
+                tern_query<KVM>(a.qs[j], lane, a.qw[j], &a.qsum[j], &a.qeff[j]);
+            } else {
+                const int kv = j - G;  // 0: k, 1: v
+                float sr;
+                const uint32_t w = tern_row<KVM>(a.xn[kv], kv, lane, &sr);
+                if (lane < kTernRowW) {
+                    a.nrow[kv][lane] = w;
+                    reinterpret_cast<uint32_t*>((kv == 0 ? p.kc : p.vc) + (head + p.pos) * 32)[lane] = w;
+                }
+                if (lane == 0) {
+                    (kv == 0 ? p.pks : p.pvs)[head + p.pos] = sr;
+                    a.nsc[kv] = sr;
+                }
+            }
+        }
+        __syncthreads();
+        // scores (:720-760 / :793-804): thread tid takes token t0 + tid and
+        // stages its V row and scale in LDS
+        if (tid < nt) {
+            const int t = t0 + tid;
+            uint32_t kr[kTernRowW];
+            uint4 v0 = cur[2], v1 = cur[3];
+            float skf = __uint_as_float(curs[0]), svf = __uint_as_float(curs[1]);
+            if (t == p.pos) {
+#pragma unroll
+                for (int i = 0; i < kTernRowW; ++i) kr[i] = a.nrow[0][i];
+                v0 = make_uint4(a.nrow[1][0], a.nrow[1][1], a.nrow[1][2], a.nrow[1][3]);
+                v1 = make_uint4(a.nrow[1][4], a.nrow[1][5], a.nrow[1][6], a.nrow[1][7]);
+                skf = a.nsc[0];
+                svf = a.nsc[1];
+            } else {
+                kr[0] = cur[0].x; kr[1] = cur[0].y; kr[2] = cur[0].z; kr[3] = cur[0].w;
+                kr[4] = cur[1].x; kr[5] = cur[1].y; kr[6] = cur[1].z; kr[7] = cur[1].w;
+            }
+            reinterpret_cast<uint4*>(&a.vt[tid][0])[0] = v0;
+            reinterpret_cast<uint4*>(&a.vt[tid][0])[1] = v1;
+            a.vsc[tid] = svf;
+            float scv[G];
+            tern_scores<G, KVM>(kr, a.qw, a.qsum, a.qeff, skf, scv);
+#pragma unroll
+            for (int g = 0; g < G; ++g) a.sc[g][tid] = scv[g];
+        }
+    } else {
     const int sub = lane >> 3, d0 = (lane & 7) * 16;
     // scores (:678-694); lane (wave, l) takes token r*kRT + wave*8 + l/8 and
     // dims (l%8)*16.. of it, and stages that token's V codes and scale in LDS
@@ -1367,6 +1461,7 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
             }
         }
     }
+    }
     __syncthreads();
     if (PAGED) {
         if (!paged_weights<G>(a, p, l, h, c, nt)) return;
@@ -1397,15 +1492,28 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
     // (G >= 2: head 2*(wave % (G/2)) + l/32; G = 1: head 0); the kNS wave
     // (half-wave) sets that own the same outputs take every kNS-th token, and
     // their sums are added in LDS in set order
+    // (ternary: thread (byte dq, head hd, token set part) of kT/32/G sets
+    // decodes byte dq of each V row, dims 4 dq..4 dq+3, :852-885)
     constexpr int kWS = G >= 2 ? G / 2 : 1;          // waves per set of all heads
-    constexpr int kNS = G >= 2 ? kW / kWS : 2 * kW;  // token sets
+    constexpr int kNS = TERN ? kT / 32 / G : G >= 2 ? kW / kWS : 2 * kW;  // token sets
     static_assert(G <= 2 * kW, "at most 8 query heads per kv head");
     constexpr int kVU = 8 * kNS <= kTpad - kTmax ? 8 : (kTpad - kTmax) / kNS;  // tokens per step
     static_assert(kVU * kNS <= kTpad - kTmax, "the zero padding covers one step");
-    const int dq = lane & 31, half = lane >> 5;
-    const int hd = G >= 2 ? (wave % kWS) * 2 + half : 0;
-    const int part = G >= 2 ? wave / kWS : wave * 2 + half;
+    const int dq = TERN ? tid & 31 : lane & 31, half = lane >> 5;
+    const int hd = TERN ? (tid >> 5) % G : G >= 2 ? (wave % kWS) * 2 + half : 0;
+    const int part = TERN ? (tid >> 5) / G : G >= 2 ? wave / kWS : wave * 2 + half;
     float o[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (TERN) {
+        const int word = dq >> 2, sh = 8 * (dq & 3);
+        for (int t = part; t < nt; t += kNS) {
+            const uint32_t* row = reinterpret_cast<const uint32_t*>(&a.vt[t][0]);
+            float w[4];
+            tern_value4(row[word] >> sh, w);
+            const float wt = a.sc[hd][t];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = __builtin_fmaf(w[k], wt, o[k]);
+        }
+    } else
     for (int tb = part; tb < nt; tb += kVU * kNS) {
         uint32_t vb[kVU];
         float wgt[kVU];
@@ -1759,7 +1867,7 @@ __device__ __forceinline__ int touch_norm(const DsParams& p, int s) {
     return ld4i(rsrc(nw, nw ? (uint32_t)K * 4 : 0u), (uint32_t)line * 128);
 }
 
-template <int G, bool PAGED>
+template <int G, int KVM>
 __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     __shared__ SharedAll sh;
     __shared__ int s_abort;
@@ -1770,7 +1878,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     // no line of this launch's per-layer vectors may survive in L2 from an
     // earlier launch (they are read with cached loads after the first barrier)
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (PAGED) stage_blocks(p);  // (stage_layers' block barrier covers it)
+    if (KVM == 3) stage_blocks(p);  // (stage_layers' block barrier covers it)
     stage_layers(p);
     int off = 0;  // first workgroup of the current stage
     int sink = 0;
@@ -1793,7 +1901,7 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
         }
         if (kind == S_ATT) {
             for (int t = first; t < n; t += p.nwg) {
-                attn_task<G, PAGED>(sh, p, l, t / p.C, t % p.C);
+                attn_task<G, KVM>(sh, p, l, t / p.C, t % p.C);
                 __syncthreads();
             }
         } else if (first < n || rec_writer(p, first, n)) {
@@ -1842,7 +1950,7 @@ int ds_grid_size() {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_kernel<4, false>, kT, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_step_kernel<4, 0>, kT, 0) !=
             hipSuccess ||
         per_cu < 1)
         return 0;
@@ -1873,16 +1981,19 @@ int ds_max_context(int G) { return kTmax * kD / 8 / G * kTmax; }
 int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
     void* args[] = {const_cast<DsParams*>(&p)};
     void* fn = nullptr;
-    const bool paged = p.block_table != nullptr;
-    switch (G * 2 + (paged ? 1 : 0)) {
-        case 2: fn = (void*)decode_step_kernel<1, false>; break;
-        case 3: fn = (void*)decode_step_kernel<1, true>; break;
-        case 4: fn = (void*)decode_step_kernel<2, false>; break;
-        case 5: fn = (void*)decode_step_kernel<2, true>; break;
-        case 8: fn = (void*)decode_step_kernel<4, false>; break;
-        case 9: fn = (void*)decode_step_kernel<4, true>; break;
-        case 16: fn = (void*)decode_step_kernel<8, false>; break;
-        case 17: fn = (void*)decode_step_kernel<8, true>; break;
+    const bool paged = p.kv_mode == 3;
+    if (p.kv_mode < 0 || p.kv_mode > 3 || (paged != (p.block_table != nullptr))) {
+        set_error("decode step: kv mode %d", p.kv_mode);
+        return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    switch (G * 4 + p.kv_mode) {
+#define TZ_DS_CASE(g, m) \
+        case g * 4 + m: fn = (void*)decode_step_kernel<g, m>; break;
+        TZ_DS_CASE(1, 0) TZ_DS_CASE(1, 1) TZ_DS_CASE(1, 2) TZ_DS_CASE(1, 3)
+        TZ_DS_CASE(2, 0) TZ_DS_CASE(2, 1) TZ_DS_CASE(2, 2) TZ_DS_CASE(2, 3)
+        TZ_DS_CASE(4, 0) TZ_DS_CASE(4, 1) TZ_DS_CASE(4, 2) TZ_DS_CASE(4, 3)
+        TZ_DS_CASE(8, 0) TZ_DS_CASE(8, 1) TZ_DS_CASE(8, 2) TZ_DS_CASE(8, 3)
+#undef TZ_DS_CASE
         default:
             set_error("decode step: query heads per kv head must be 1, 2, 4 or 8");
             return TENZO_ERROR_UNSUPPORTED;

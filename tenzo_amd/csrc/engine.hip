@@ -826,7 +826,7 @@ int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
 
 // Whether the persistent kernel can run this model as loaded.
 bool ds_usable(tenzo_engine_t e) {
-    if (e->ds_nwg <= 0 || (e->kv_kind != 0 && e->kv_kind != 3) || e->head_kind != 1 ||
+    if (e->ds_nwg <= 0 || e->kv_kind < 0 || e->kv_kind > 3 || e->head_kind != 1 ||
         e->H > 8192 || e->F > 8192 || e->H % 64 || e->F % 64 || e->L > kDsMaxLayers ||
         e->max_seq > ds_max_context(e->Hq / e->Hkv))
         return false;
@@ -873,8 +873,9 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.rope = e->rope;
     p.kc = e->kc;
     p.vc = e->vc;
-    if (e->kv_kind == 3) {
-        p.block_table = e->pg_bt;
+    p.kv_mode = e->kv_kind;
+    if (e->kv_kind != 0) {  // fp32 scales (paged pools or ternary rows)
+        p.block_table = e->kv_kind == 3 ? e->pg_bt : nullptr;
         p.pks = (float*)e->ks;
         p.pvs = (float*)e->vs;
     } else {

@@ -147,7 +147,10 @@ def _cfg(L):
 @pytest.mark.parametrize("kv_mode,mode,ctx,L", [
     ("tl1_fused", "graph", 9, 3), ("tl1_fused", "eager", 9, 3), ("tl1_fused", "graph", 600, 3),
     ("popcount_fused", "graph", 9, 3), ("popcount_fused", "eager", 9, 3),
-    ("popcount_fused", "graph", 600, 1)])
+    ("popcount_fused", "graph", 600, 1),
+    ("tl1_fused", "persistent", 0, 3), ("tl1_fused", "persistent", 9, 3),
+    ("tl1_fused", "persistent", 600, 3), ("popcount_fused", "persistent", 9, 3),
+    ("popcount_fused", "persistent", 600, 1)])
 def test_engine_tern_matches_oracle(eng_mod, kv_mode, mode, ctx, L):
     km = 1 if kv_mode == "tl1_fused" else 2
     cfg = _cfg(L)
@@ -157,9 +160,8 @@ def test_engine_tern_matches_oracle(eng_mod, kv_mode, mode, ctx, L):
     with eng_mod.Engine(cfg, kv_mode=kv_mode) as e:
         e.set_model(sm, kv=False)
         e.set_kv(*(np.ascontiguousarray(a[:, :, :ctx]) for a in kv), ctx)
-        e.set_mode("persistent")  # the persistent kernel is int8_fused only
-        assert e.mode == "graph"
         e.set_mode(mode)
+        assert e.mode == mode
         tok = 5
         for i in range(6):
             print(f"step {i} kv_mode={kv_mode} mode={mode} ctx={ctx} L={L}", flush=True)
@@ -176,8 +178,9 @@ def test_engine_tern_matches_oracle(eng_mod, kv_mode, mode, ctx, L):
         assert rel(ks[:, :, ctx:], om.ks[:, :, ctx:ctx + 6]) < 1e-3
 
 
+@pytest.mark.parametrize("mode", ["persistent", "graph"])
 @pytest.mark.parametrize("kv_mode", ["tl1_fused", "popcount_fused"])
-def test_engine_tern_layer_local(eng_mod, kv_mode):
+def test_engine_tern_layer_local(eng_mod, kv_mode, mode):
     """Three layers at context 600, one step: layer 0 appends exactly the
     oracle's rows (its input is the embedding), and the last layer's
     attention equals the oracle's from the engine's own q|k|v (rows bit-exact,
@@ -190,6 +193,8 @@ def test_engine_tern_layer_local(eng_mod, kv_mode):
     with eng_mod.Engine(cfg, kv_mode=kv_mode) as e:
         e.set_model(sm, kv=False)
         e.set_kv(*(np.ascontiguousarray(a[:, :, :ctx]) for a in kv), ctx)
+        e.set_mode(mode)
+        assert e.mode == mode
         e.step(5)
         om.step(5, ctx, cfg.theta)
         got = e.get_kv(ctx + 1)
@@ -236,6 +241,7 @@ def test_engine_tern_prefill_equals_steps(eng_mod, kv_mode):
     with eng_mod.Engine(cfg, kv_mode=kv_mode) as a, eng_mod.Engine(cfg, kv_mode=kv_mode) as b:
         for e in (a, b):
             e.set_model(sm)
+            e.set_mode("graph")  # the batched prefill's own arithmetic (not the persistent kernel's)
         a.prefill_batch(toks[:-1])
         for t in toks[:-1]:
             b.prefill(t)
