@@ -65,6 +65,9 @@ def parse():
                     help="instead of the decode benchmark: prefill an N-token prompt with "
                          "tenzo_hip_engine_prefill (--steps timed prompts) beside the "
                          "token-by-token tenzo_prefill_token rate; prints its own JSON line")
+    ap.add_argument("--tl1-methods", action="store_true",
+                    help="time the masked-v_dot4 TL1 GEMV against the reference's table "
+                         "method at 6912x2560 and 65536x8192, print one JSON line, exit")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="for rocprofv3 --pmc runs: one calibration copy of PROBE_COPY_BYTES "
                          "(a plain copy kernel of known size), then --steps chained decode "
@@ -604,6 +607,30 @@ def _gguf_dev(torch, gen, copies, N, K, bpb):
     return w
 
 
+def tl1_methods(torch):
+    """The masked-v_dot4 TL1 GEMV against the reference's table method (LDS
+    tables per activation pair, v_perm lookups) on the same weights: config
+    1's 6912 x 2560 (latency-bound: a wave sees about one 64-column chunk)
+    and 65536 x 8192 (134 MB: each wave loops over 32 chunks)."""
+    from tenzo_amd import ops
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(SEED + 9)
+    out = {}
+    for N, K in ((6912, 2560), (65536, 8192)):
+        nb = ops.tl1_packed_bytes(N, K)
+        c = _copies(nb)
+        W = tl1_random_dev(torch, c * nb, gen).view(c, nb)
+        codes, q, _ = ops.rmsnorm_quant31(torch.randn(K, device="cuda", generator=gen))
+        y = torch.empty(N, device="cuda")
+        alg = N * K // 4 + K + N * 4
+        for name, fn in (("v_dot4", lambda i: ops.bitlinear_tl1_into(codes, q, W[i], 0.0159, N, K, y)),
+                         ("table", lambda i: ops.bitlinear_tl1_lut(codes, q, W[i], 0.0159, N, K, y=y))):
+            t = _per_call(torch, [lambda i=i: fn(i) for i in range(c)])
+            out[f"tl1_{N}x{K}_{name}"] = _entry(alg, t, c)
+        del W
+    return out
+
+
 def configs_bench(torch):
     from tenzo_amd import _lib, ops
     L = _lib.load()
@@ -621,6 +648,11 @@ def configs_bench(torch):
     t = _per_call(torch, [lambda i=i: ops.bitlinear_tl1_into(codes, q, W[i], 0.0159, N, K, y)
                           for i in range(c)])
     out["c1_tl1_6912x2560"] = _entry(N * K // 4 + K + N * 4, t, c)
+    # the same GEMV by the reference's table method (LDS tables per activation
+    # pair, v_perm lookups): the measurement behind the masked-v_dot4 choice
+    t = _per_call(torch, [lambda i=i: ops.bitlinear_tl1_lut(codes, q, W[i], 0.0159, N, K, y=y)
+                          for i in range(c)])
+    out["c1_tl1_6912x2560_table_method"] = _entry(N * K // 4 + K + N * 4, t, c)
     del W
     # config 3: Q4_0 (fp16 and Q8_0 activations) and Q8_0 weights, 11008 x 4096
     N, K = 11008, 4096
@@ -818,6 +850,9 @@ def main():
     cfg = synth.BITNET_2B
     if args.configs_only:
         print(json.dumps({"configs": configs_bench(torch)}), flush=True)
+        return
+    if args.tl1_methods:
+        print(json.dumps({"tl1_methods": tl1_methods(torch)}), flush=True)
         return
     ctx = 0 if args.prefill else args.ctx
     tern = args.kv_mode != "int8_fused"

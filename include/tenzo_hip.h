@@ -82,6 +82,17 @@ TENZO_HIP_API int tenzo_hip_bitlinear_tl1(const int8_t* codes, const tenzo_hip_a
                                           int64_t N, int64_t K, float* y, int32_t* acc_out,
                                           void* stream);
 
+/* The same product as tenzo_hip_bitlinear_tl1 by the reference's own table
+ * method (build_lut and compute_single_block, TenzoEngine.cpp:22-127): a
+ * 16-entry table per activation pair in LDS, looked up with each 4-bit pair of
+ * weight codes. Same arguments and bit-identical results; it is there to
+ * measure the table method against the masked-v_dot4 kernel, not used by the
+ * engine. K needs at most 64 KiB of tables per workgroup. */
+TENZO_HIP_API int tenzo_hip_bitlinear_tl1_lut(const int8_t* codes, const tenzo_hip_actq_t* q,
+                                              const void* w_packed, float w_scale, int64_t M,
+                                              int64_t N, int64_t K, float* y, int32_t* acc_out,
+                                              void* stream);
+
 /* Multi-token TL1 contraction on int8 MFMA (prefill): the same results as M
  * separate compute_from_lut calls (TenzoEngine.cpp:129-146), which
  * prefill_token (TenzoEngine.cpp:1809-1819) makes one token at a time, from

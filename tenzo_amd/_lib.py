@@ -27,6 +27,7 @@ SIGNATURES = {
     "tenzo_hip_tl1_repack_raw": (_I, [_P, _P, _I64, _I64, _P]),
     "tenzo_hip_rmsnorm_quant31": (_I, [_P, _P, _I, _F, _I64, _I64, _P, _P, _P, _P]),
     "tenzo_hip_bitlinear_tl1": (_I, [_P, _P, _P, _F, _I64, _I64, _I64, _P, _P, _P]),
+    "tenzo_hip_bitlinear_tl1_lut": (_I, [_P, _P, _P, _F, _I64, _I64, _I64, _P, _P, _P]),
     "tenzo_hip_bitlinear_tl1_f32": (_I, [_P, _P, _F, _I64, _I64, _I64, _P, _P]),
     "tenzo_hip_bitlinear_tl1_batch": (_I, [_P, _P, _P, _F, _I64, _I64, _I64, _P, _P, _I, _P]),
     "tenzo_hip_rmsnorm": (_I, [_P, _P, _P, _I64, _F, _P]),

@@ -401,6 +401,104 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
 }
 
 // ------------------------------------------------------------------------
+// The same GEMV by the reference's own method (build_lut :22-62,
+// compute_single_block :64-127): a 16-entry int8 table per activation pair
+// (entry u0 | u1 << 2 = (u0 - 1) a0 + (u1 - 1) a1), staged in LDS, looked up
+// with each 4-bit pair of weight codes. It reads the same packed weights as
+// tl1_gemv_kernel, whose 4-bit nibbles pair the columns (16i + b, 16i + 4 + b)
+// (low nibble of byte b of dword i) and (16i + 8 + b, 16i + 12 + b) (high
+// nibble) of a super-chunk; the lookup is two byte permutes (v_perm, the
+// pshufb of the reference) and a select. The tables hold the reference's
+// values (w in {-1, 0, +1}), so the sum is sum w a directly; tl1_finalize
+// takes sum (w + 1) a - code_sum, hence the code sum added back before it.
+// The int32 sums are exact, so the
+// results equal tl1_gemv_kernel's bit for bit; the kernel exists to measure
+// the table method against the masked v_dot4 one (same grid, same splits).
+// ------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(256)
+tl1_lut_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
+                    const tenzo_hip_actq_t* __restrict__ aq, int64_t N, int64_t KS, int splits,
+                    RowScales rs, float* y, int32_t* __restrict__ acc_out,
+                    int32_t* __restrict__ ws_acc, uint32_t* __restrict__ ws_cnt) {
+    extern __shared__ uint4 lut[];  // [(s1 - s0) * 32 pairs] tables of 16 bytes
+    __shared__ int red[4][64];
+    __shared__ int is_last;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t nb = N >> 6;
+    const int64_t b = blockIdx.x / splits;
+    const int sp = (int)(blockIdx.x - b * splits);
+    const int64_t m = blockIdx.y;
+    const int64_t per = (KS + splits - 1) / splits;
+    const int64_t s0 = sp * per;
+    const int64_t s1 = s0 + per < KS ? s0 + per : KS;
+    const int8_t* cm = codes + m * KS * 64;
+    // the tables of the block's super-chunks
+    for (int64_t q = threadIdx.x; q < (s1 - s0) * 32; q += 256) {
+        const int64_t sc = s0 + q / 32;
+        const int i = (int)(q % 32) / 8, bb = (int)(q % 8) / 2, hh = (int)(q % 2);
+        const int64_t c0 = sc * 64 + 16 * i + 8 * hh + bb;
+        const int a0 = cm[c0], a1 = cm[c0 + 4];
+        uint32_t t[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int u1 = 0; u1 < 3; ++u1)
+#pragma unroll
+            for (int u0 = 0; u0 < 3; ++u0) {
+                const int idx = u0 | (u1 << 2);
+                const int v = min(max((u0 - 1) * a0 + (u1 - 1) * a1, -128), 127);
+                t[idx >> 2] |= (uint32_t)(v & 0xff) << (8 * (idx & 3));
+            }
+        lut[q] = make_uint4(t[0], t[1], t[2], t[3]);
+    }
+    __syncthreads();
+    const uint4* wb = w + b * KS * 64 + lane;
+    int acc = 0;
+    for (int64_t s = s0 + wave; s < s1; s += 4) {
+        const uint4 v = wb[s * 64];
+        const uint32_t ws[4] = {v.x, v.y, v.z, v.w};
+        const uint4* tb = lut + (s - s0) * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {  // nibble k: byte k / 2, half k % 2
+                const uint4 tab = tb[i * 8 + k];  // the same address in every lane
+                const uint32_t nib = (ws[i] >> (4 * k)) & 15u;
+                const uint32_t sel = nib & 7u;
+                const uint32_t lo = __builtin_amdgcn_perm(tab.y, tab.x, sel);
+                const uint32_t hi = __builtin_amdgcn_perm(tab.w, tab.z, sel);
+                acc += (int)(int8_t)((nib & 8u) ? hi : lo);
+            }
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    const int64_t row = b * 64 + lane;
+    if (splits == 1) {
+        if (wave == 0) {
+            const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+            tl1_finalize(tot + aq[m].code_sum, m, row, N, aq, rs, y, nullptr, acc_out);
+        }
+        return;
+    }
+    if (wave == 0) {
+        const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+        atomicAdd(&ws_acc[m * N + row], tot);
+    }
+    partials_acked();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = atomicAdd(&ws_cnt[m * nb + b], 1u);
+        is_last = prev == (unsigned)(splits - 1);
+    }
+    __syncthreads();
+    if (is_last && wave == 0) {
+        const int tot = atomicExch(&ws_acc[m * N + row], 0);
+        tl1_finalize(tot + aq[m].code_sum, m, row, N, aq, rs, y, nullptr, acc_out);
+        if (lane == 0) atomicExch(&ws_cnt[m * nb + b], 0u);
+    }
+}
+
+// ------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------
 
@@ -580,6 +678,35 @@ TENZO_HIP_API int tenzo_hip_bitlinear_tl1(const int8_t* codes, const tenzo_hip_a
     RowScales rs = RowScales::single(w_scale);
     return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, nullptr, acc_out,
                            (hipStream_t)stream, 0, nullptr);
+}
+
+TENZO_HIP_API int tenzo_hip_bitlinear_tl1_lut(const int8_t* codes, const tenzo_hip_actq_t* q,
+                                              const void* w_packed, float w_scale, int64_t M,
+                                              int64_t N, int64_t K, float* y, int32_t* acc_out,
+                                              void* stream) {
+    TZ_CHECK(codes && q && w_packed && y, "bitlinear_tl1_lut: null pointer");
+    TZ_CHECK(M > 0 && M <= 65535 && N > 0 && N % 64 == 0 && K > 0,
+             "bitlinear_tl1_lut: need N %% 64 == 0 (N=%lld)", (long long)N);
+    hipStream_t st = (hipStream_t)stream;
+    const int64_t nb = N / 64, KS = ceil_div(K, 64);
+    int splits = tl1_pick_splits(nb, KS, M);
+    if (splits > KS) splits = (int)KS;
+    const int64_t per = ceil_div(KS, splits);
+    const size_t lds = (size_t)per * 32 * 16;
+    TZ_CHECK(lds <= 64 * 1024, "bitlinear_tl1_lut: K=%lld needs %zu bytes of tables", (long long)K,
+             lds);
+    int32_t* ws_acc = nullptr;
+    uint32_t* ws_cnt = nullptr;
+    if (splits > 1) {
+        void* ws = Scratch::get(kScratchGemvAcc, tl1_ws_bytes(M, N), st);
+        if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
+        ws_acc = (int32_t*)ws;
+        ws_cnt = (uint32_t*)((char*)ws + (size_t)M * N * 4);
+    }
+    hipLaunchKernelGGL(tl1_lut_gemv_kernel, dim3((unsigned)(nb * splits), (unsigned)M), dim3(256),
+                       lds, st, (const uint4*)w_packed, codes, q, N, KS, splits,
+                       RowScales::single(w_scale), y, acc_out, ws_acc, ws_cnt);
+    return launch_status("tl1_lut_gemv_kernel");
 }
 
 TENZO_HIP_API int tenzo_hip_bitlinear_tl1_f32(const float* x, const void* w_packed,

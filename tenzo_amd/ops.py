@@ -91,6 +91,22 @@ def bitlinear_tl1(codes: torch.Tensor, q: torch.Tensor, w_packed: torch.Tensor, 
     return y, acc
 
 
+def bitlinear_tl1_lut(codes: torch.Tensor, q: torch.Tensor, w_packed: torch.Tensor,
+                      w_scale: float, N: int, K: int, want_acc: bool = False,
+                      y: torch.Tensor | None = None):
+    """bitlinear_tl1 by the reference's table method (a 16-entry table per
+    activation pair in LDS, looked up per 4-bit weight pair): the same bits;
+    kept to measure the two methods against each other."""
+    M = codes.shape[0]
+    if y is None:
+        y = torch.empty((M, N), dtype=torch.float32, device=codes.device)
+    acc = torch.empty((M, N), dtype=torch.int32, device=codes.device) if want_acc else None
+    _lib.check(_lib.load().tenzo_hip_bitlinear_tl1_lut(
+        _ptr(codes), _ptr(q), _ptr(w_packed), w_scale, M, N, K, _ptr(y), _ptr(acc), _stream()),
+        "bitlinear_tl1_lut")
+    return y, acc
+
+
 def bitlinear_tl1_into(codes: torch.Tensor, q: torch.Tensor, w_packed: torch.Tensor,
                        w_scale: float, N: int, K: int, y: torch.Tensor) -> torch.Tensor:
     """bitlinear_tl1 writing into a caller-owned y (no allocation per call)."""

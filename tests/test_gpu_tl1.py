@@ -133,3 +133,26 @@ def test_host_pointer_shims(torch_dev):
     np.testing.assert_array_equal(yn, oracle.rms_norm(xn, wn))
     # bad arguments are rejected, not run
     assert L.tenzo_hip_execute_bitlinear_tl1(P(x), P(w), P(y), 2, K, 100, 0.5) == 0
+
+
+@pytest.mark.parametrize("N,K,M", [(64, 2, 1), (128, 130, 1), (6912, 2560, 1), (2560, 6912, 1),
+                                   (256, 640, 3)])
+def test_tl1_lut_gemv_equals_dot4_gemv(torch_dev, N, K, M):
+    """The table-method kernel (the reference's build_lut / pshufb lookup on
+    the GPU) gives the masked-v_dot4 kernel's int32 sums and outputs bit for
+    bit, and the oracle's."""
+    from tenzo_amd import ops
+    torch = torch_dev
+    print(f"tl1 lut N={N} K={K} M={M}", flush=True)
+    rng = np.random.default_rng(N + 3 * K + M)
+    w = formats.tl1_random(N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    wp = ops.tl1_repack(to_dev(torch, w), N, K)
+    codes, q, _ = ops.rmsnorm_quant31(to_dev(torch, x), None)
+    y, acc = ops.bitlinear_tl1(codes, q, wp, 0.0159, N, K, want_acc=True)
+    yl, accl = ops.bitlinear_tl1_lut(codes, q, wp, 0.0159, N, K, want_acc=True)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(accl.cpu().numpy(), acc.cpu().numpy())
+    np.testing.assert_array_equal(yl.cpu().numpy().view(np.uint32), y.cpu().numpy().view(np.uint32))
+    yo, acco, _ = oracle.tl1_gemv(x[0], w, N, 0.0159)
+    np.testing.assert_array_equal(accl.cpu().numpy()[0], acco)
