@@ -503,9 +503,12 @@ tl1_lut_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ code
 // ------------------------------------------------------------------------
 
 int tl1_pick_splits(int64_t nb, int64_t KS, int64_t M) {
-    // Aim at ~4 blocks per CU of the 256, with at least one super-chunk per
-    // wave of every block.
-    int64_t want = ceil_div(1024, nb * M);
+    // Aim at about one block per CU of the 256, with at least one super-chunk
+    // per wave of every block: each further K split adds the partials'
+    // atomics and the last block's read-back, memory round trips in series
+    // (6912 x 2560: 7.14 us with 10 splits, 5.43 with 3; 2560 x 6912: 9.37 us
+    // with 26, 5.84 with 7).
+    int64_t want = ceil_div(256, nb * M);
     int64_t cap = KS / 4 > 0 ? KS / 4 : 1;
     if (want > cap) want = cap;
     if (want < 1) want = 1;
