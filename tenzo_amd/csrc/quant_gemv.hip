@@ -553,6 +553,116 @@ gq_h2_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qwei
     if (threadIdx.x == 0) atomicExch(&cnt[tile], 0u);
 }
 
+// GPTQ / AWQ with fp16 activations, batch 4..16, on fp16 MFMA
+// (v_mfma_f32_16x16x16_f16): D[m][n] += sum_k A[m][k] (q - z)[k][n] over
+// 16-k steps, the batch rows as M (padded to 16 with zeros) and 16 output
+// columns per wave as N. Each lane builds its B operand, column n = lane % 16
+// at k = 4 (lane / 16) .. +3 of the step, from half a qweight word: the same
+// exact fp16 (q - z) as gq_h2_kernel (byte permute, and-or forming 1024 + q,
+// one packed subtraction of 1024 + z). A group's group / 16 steps go into a
+// fresh accumulator that is scaled once, y += s * sum. The activations are staged
+// in LDS with each k-octet in the qweight word's nibble order (AWQ:
+// k = {0,2,4,6,1,3,5,7}), rows padded by 8 bytes so the 16 rows of an A
+// operand read fall in different banks. A workgroup owns 32 columns: waves
+// (tile, half) = (w % 2, w / 2) take 16 columns and one half of K, and the
+// halves are added in LDS. Each lane keeps the 32 qweight words of 512 k in
+// flight. Products are exact and summed in fp32 (the MFMA's own order).
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef float f4m __attribute__((ext_vector_type(4)));
+constexpr int kGqChunk = 512;  // k per load batch (32 words per lane)
+
+template <bool AWQ, typename TS, int NG>  // NG = group / 16 steps per group
+__global__ void __launch_bounds__(256)
+gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qweight,
+               const TS* __restrict__ scales, const uint32_t* __restrict__ qzeros,
+               float* __restrict__ y, int K, int N, int B) {
+    constexpr int kSteps = kGqChunk / 16, kGroups = kSteps / NG;  // per chunk
+    extern __shared__ uint2 a_lds[];  // [B][K + 4] fp16, 8-byte aligned rows
+    uint16_t* ah = reinterpret_cast<uint16_t*>(a_lds);
+    __shared__ f4m red[2][64];
+    const int KP = K + 4;
+    // one k-octet (16 bytes) per thread and load, permuted in registers for AWQ
+    const int K8 = K >> 3;
+    for (int m = 0; m < B; ++m) {
+        const uint4* src = reinterpret_cast<const uint4*>(act + (int64_t)m * K);
+        uint2* dst = reinterpret_cast<uint2*>(ah + m * KP);
+#pragma unroll 2
+        for (int o = threadIdx.x; o < K8; o += 256) {
+            uint4 v = src[o];
+            if (AWQ)  // halves (0,1)(2,3)(4,5)(6,7) -> (0,2)(4,6)(1,3)(5,7)
+                v = uint4{(v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16),
+                          (v.x >> 16) | (v.y & 0xffff0000u), (v.z >> 16) | (v.w & 0xffff0000u)};
+            dst[2 * o] = uint2{v.x, v.y};
+            dst[2 * o + 1] = uint2{v.z, v.w};
+        }
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tile = wave & 1, half = wave >> 1;
+    const int col = lane & 15, kq = lane >> 4;
+    const int n = blockIdx.x * 32 + tile * 16 + col;
+    const int nn = min(n, N - 1);  // columns past N read the last one, not stored
+    const int m = lane & 15;       // A operand row
+    const bool arow = m < B;
+    const uint16_t* arp = ah + min(m, B - 1) * KP + 4 * kq;
+    const int kh = K / 2, ka = half * kh, kb = ka + kh;
+    const uint32_t sh = 16u * (uint32_t)(kq & 1);
+    uint32_t lo4 = 0x000f000fu, one024 = 0x64006400u;  // VGPR operands of v_and_or_b32
+    asm volatile("" : "+v"(lo4), "+v"(one024));
+    f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int kc = ka; kc < kb; kc += kGqChunk) {
+        // this lane's 32 words of the chunk (k-octets kc/8 + 2j + kq/2) and the
+        // chunk's group scales and zeros, all in flight together
+        uint32_t qv[kSteps];
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j)
+            qv[j] = qweight[(int64_t)(kc / 8 + 2 * j + (kq >> 1)) * N + nn];
+        float sc[kGroups];
+        uint32_t zw[kGroups];
+#pragma unroll
+        for (int gi = 0; gi < kGroups; ++gi) {
+            const int g = kc / (16 * NG) + gi;
+            sc[gi] = to_f32<TS>(scales[(int64_t)g * N + nn]);
+            zw[gi] = AWQ ? qzeros[(int64_t)g * (N / 8) + nn / 8] : qzeros[(int64_t)(g / 8) * N + nn];
+        }
+#pragma unroll
+        for (int gi = 0; gi < kGroups; ++gi) {
+            const int g = kc / (16 * NG) + gi;
+            const int z = AWQ ? (int)((zw[gi] >> (4 * (nn % 8))) & 15u)
+                              : (int)((zw[gi] >> (4 * (g % 8))) & 15u) + 1;
+            const _Float16 bz = (_Float16)(-1024.0f - (float)z);
+            const h2v bias = {bz, bz};
+            f4m cg = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int jj = 0; jj < NG; ++jj) {
+                const int j = gi * NG + jj;
+                const uint32_t x = qv[j] >> sh, hx = x >> 4;
+                const uint32_t z0 = (__builtin_amdgcn_perm(hx, x, 0x0c040c00u) & lo4) | one024;
+                const uint32_t z1 = (__builtin_amdgcn_perm(hx, x, 0x0c050c01u) & lo4) | one024;
+                const h2v w0 = __builtin_bit_cast(h2v, z0) + bias;
+                const h2v w1 = __builtin_bit_cast(h2v, z1) + bias;
+                const h4v b = {w0.x, w0.y, w1.x, w1.y};
+                h4v a = *reinterpret_cast<const h4v*>(arp + kc + 16 * j);
+                if (!arow)
+                    a = h4v{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+                cg = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, cg, 0, 0, 0);
+            }
+            acc += cg * sc[gi];
+        }
+    }
+    if (half == 1) red[tile][lane] = acc;
+    __syncthreads();
+    if (half == 0 && n < N) {
+        const f4m o = acc + red[tile][lane];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = 4 * kq + i;  // D: lane holds rows 4 (lane / 16) .. +3 of column n
+            if (row < B) y[(int64_t)row * N + n] = o[i];
+        }
+    }
+}
+
 // ------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------
@@ -645,9 +755,29 @@ static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
     }
     // fp16 activations take the packed fp16 dot (the pairs need whole k-octets: K % 8 == 0)
     constexpr bool kF16 = std::is_same<TA, uint16_t>::value;
+    // and from batch 4 on, fp16 MFMA (K in whole 512-k chunks per half, groups of 16-k steps
+    // dividing them, the staged activations within LDS)
+    if (kF16 && B >= 4 && B <= 16 && K % (2 * kGqChunk) == 0 && group % 16 == 0 &&
+        ((uintptr_t)act & 15) == 0 &&
+        kGqChunk % group == 0 && (size_t)B * (K + 4) * 2 <= 160 * 1024 - 2048) {
+        const dim3 grid((unsigned)ceil_div(N, 32));
+        const size_t lds = (size_t)B * (K + 4) * 2;
+        switch (group / 16) {
+#define GQM_CASE(NG)                                                                          \
+            case NG:                                                                          \
+                hipLaunchKernelGGL((gq_mfma_kernel<AWQ, TS, NG>), grid, dim3(256), lds, st,    \
+                                   (const uint16_t*)act, qweight, scales, qzeros, y, K, N, B); \
+                return launch_status(AWQ ? "awq_mfma_kernel" : "gptq_mfma_kernel");
+            GQM_CASE(2) GQM_CASE(4) GQM_CASE(8) GQM_CASE(16) GQM_CASE(32)
+#undef GQM_CASE
+            default: break;  // other group sizes: the packed fp16 dot below
+        }
+    }
     GQ_CASE(1) GQ_CASE(2) GQ_CASE(4) GQ_CASE(8)
 #undef GQ_CASE
-    set_error("gptq/awq: batch %d > 8 not supported", B);
+    set_error("gptq/awq: batch %d > 8 needs the MFMA path (16-byte aligned fp16 activations, "
+              "K %% 1024 == 0, group 32..512 dividing 512, B (K + 4) fp16 within 158 KiB of LDS)",
+              B);
     return TENZO_ERROR_UNSUPPORTED;
 }
 
@@ -740,8 +870,8 @@ TENZO_HIP_API int tenzo_hip_gemv_gptq(const void* act, int act_dtype, const uint
                                       const uint32_t* qzeros, float* y, int K, int N,
                                       int group, int B, void* stream) {
     TZ_CHECK(act && qweight && scales && qzeros && y, "gemv_gptq: null pointer");
-    TZ_CHECK(K > 0 && K % 8 == 0 && N > 0 && group > 0 && group % 8 == 0 && B >= 1 && B <= 8,
-             "gemv_gptq: need K %% 8 == 0, group %% 8 == 0, 1 <= B <= 8");
+    TZ_CHECK(K > 0 && K % 8 == 0 && N > 0 && group > 0 && group % 8 == 0 && B >= 1 && B <= 16,
+             "gemv_gptq: need K %% 8 == 0, group %% 8 == 0, 1 <= B <= 16");
     TZ_CHECK((act_dtype == 0 || act_dtype == 1) && (scale_dtype == 0 || scale_dtype == 1),
              "gemv_gptq: dtype codes must be 0 (fp32) or 1 (fp16)");
     return dispatch_gq<false>(act, act_dtype, qweight, scales, scale_dtype, qzeros, y, K, N,
@@ -754,8 +884,8 @@ TENZO_HIP_API int tenzo_hip_gemv_awq(const void* act, int act_dtype, const uint3
                                      int B, void* stream) {
     TZ_CHECK(act && qweight && scales && qzeros && y, "gemv_awq: null pointer");
     TZ_CHECK(K > 0 && K % 8 == 0 && N > 0 && N % 8 == 0 && group > 0 && group % 8 == 0 &&
-                 B >= 1 && B <= 8,
-             "gemv_awq: need K %% 8 == 0, N %% 8 == 0, group %% 8 == 0, 1 <= B <= 8");
+                 B >= 1 && B <= 16,
+             "gemv_awq: need K %% 8 == 0, N %% 8 == 0, group %% 8 == 0, 1 <= B <= 16");
     TZ_CHECK((act_dtype == 0 || act_dtype == 1) && (scale_dtype == 0 || scale_dtype == 1),
              "gemv_awq: dtype codes must be 0 (fp32) or 1 (fp16)");
     return dispatch_gq<true>(act, act_dtype, qweight, scales, scale_dtype, qzeros, y, K, N,

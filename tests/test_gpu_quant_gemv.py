@@ -161,10 +161,42 @@ def test_gptq_awq_benchmark_shape(torch_dev, kind, B):
     for b in range(B):
         ref = ofn(a[b].astype(np.float32), qw, scales16.astype(np.float32), qz, K, N, G)
         close(y[b], ref, a[b].astype(np.float32), W)
-    # batch rows are independent: row b of the batched call equals a batch-1 call
-    y1 = fn(dev(torch, a[-1:]), dev(torch, qw), dev(torch, scales16), dev(torch, qz), K, N,
+    # batch rows are independent: the last rows of the batched call equal a call on those
+    # rows alone (batch 4 and up runs on MFMA, whose rows do not mix; batch 1 on the dot)
+    t = 4 if B >= 4 else 1
+    yt = fn(dev(torch, a[-t:]), dev(torch, qw), dev(torch, scales16), dev(torch, qz), K, N,
             G).cpu().numpy()
-    np.testing.assert_array_equal(y1[0], y[-1])
+    np.testing.assert_array_equal(yt, y[-t:])
+
+
+@pytest.mark.parametrize("kind", ["gptq", "awq"])
+@pytest.mark.parametrize("B,K,N,G,f32s", [(4, 1024, 1000, 32, False), (5, 2048, 264, 64, True),
+                                          (16, 4096, 96, 256, False), (9, 1024, 40, 512, False),
+                                          (12, 2048, 520, 128, True)])
+def test_gptq_awq_mfma_shapes(torch_dev, kind, B, K, N, G, f32s):
+    """Batch 4-16 with fp16 activations runs on fp16 MFMA: ragged N (a partly used 32-column
+    tile), batches that fill 4..16 of the 16 MFMA rows, every group size from 32 to 512
+    (2..32 MFMA steps per group), fp16 and fp32 scales."""
+    from tenzo_amd import ops
+    torch = torch_dev
+    print(f"{kind} mfma B={B} K={K} N={N} G={G} f32s={f32s}", flush=True)
+    rng = np.random.default_rng(B * 7 + K + N + G)
+    q = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
+    zeros = rng.integers(0, 16, size=(K // G, N), dtype=np.uint8)
+    scales = synth.f16_round(np.abs(rng.normal(0, 0.01, size=(K // G, N))))
+    scales = scales.astype(np.float32 if f32s else np.float16)
+    pack = formats.gptq_pack if kind == "gptq" else formats.awq_pack
+    qw, qz = pack(q, zeros)
+    a = rng.standard_normal((B, K)).astype(np.float16)
+    fn = ops.gemv_gptq if kind == "gptq" else ops.gemv_awq
+    y = fn(dev(torch, a), dev(torch, qw), dev(torch, scales), dev(torch, qz), K, N,
+           G).cpu().numpy()
+    assert y.shape == (B, N)
+    ofn = oracle.gptq if kind == "gptq" else oracle.awq
+    W = gq_dense(q, zeros, scales, G, kind)
+    for b in range(B):
+        ref = ofn(a[b].astype(np.float32), qw, scales.astype(np.float32), qz, K, N, G)
+        close(y[b], ref, a[b].astype(np.float32), W)
 
 
 def gq_dense(q, zeros, scales, G, kind):
