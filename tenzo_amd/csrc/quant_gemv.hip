@@ -564,30 +564,59 @@ gq_h2_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qwei
 // in LDS with each k-octet in the qweight word's nibble order (AWQ:
 // k = {0,2,4,6,1,3,5,7}), rows padded by 8 bytes so the 16 rows of an A
 // operand read fall in different banks. A workgroup owns 32 columns: waves
-// (tile, half) = (w % 2, w / 2) take 16 columns and one half of K, and the
-// halves are added in LDS. Each lane keeps the 32 qweight words of 512 k in
-// flight. Products are exact and summed in fp32 (the MFMA's own order).
+// (tile, part) = (w % 2, w / 2) take 16 columns and one of 4, 2 or 1 parts of
+// K (whole 512-k chunks each), and the parts are added in LDS in part order.
+// Each lane keeps the 32 qweight words of a chunk in flight, the first
+// chunk's issued before the activations are staged. Products are exact and
+// summed in fp32 (the MFMA's own order).
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef float f4m __attribute__((ext_vector_type(4)));
 constexpr int kGqChunk = 512;  // k per load batch (32 words per lane)
+constexpr int kGqParts = 4;    // most k parts per workgroup (2 waves each)
+constexpr size_t kGqLds = 160 * 1024 - 8192;  // staged activations, beside the part sums
+constexpr int kGqLR = 8;  // gq_v4_kernel: lanes per row of a workgroup's columns
 
 template <bool AWQ, typename TS, int NG>  // NG = group / 16 steps per group
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
 gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qweight,
                const TS* __restrict__ scales, const uint32_t* __restrict__ qzeros,
                float* __restrict__ y, int K, int N, int B) {
     constexpr int kSteps = kGqChunk / 16, kGroups = kSteps / NG;  // per chunk
     extern __shared__ uint2 a_lds[];  // [B][K + 4] fp16, 8-byte aligned rows
     uint16_t* ah = reinterpret_cast<uint16_t*>(a_lds);
-    __shared__ f4m red[2][64];
+    __shared__ f4m red[kGqParts - 1][2][64];
     const int KP = K + 4;
-    // one k-octet (16 bytes) per thread and load, permuted in registers for AWQ
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int parts = (int)blockDim.x >> 7;  // k parts: waves (tile, part) = (w % 2, w / 2)
+    const int tile = wave & 1, part = wave >> 1;
+    const int col = lane & 15, kq = lane >> 4;
+    const int n = blockIdx.x * 32 + tile * 16 + col;
+    const int nn = min(n, N - 1);  // columns past N read the last one, not stored
+    const int kp = K / parts, ka = part * kp, kb = ka + kp;
+    // this lane's 32 words of a chunk (k-octets kc/8 + 2j + kq/2) and the chunk's group
+    // scales and zeros, all in flight together; the first chunk's before the staging
+    uint32_t qv[kSteps];
+    float sc[kGroups];
+    uint32_t zw[kGroups];
+    auto load_chunk = [&](int kc) {
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j)
+            qv[j] = qweight[(int64_t)(kc / 8 + 2 * j + (kq >> 1)) * N + nn];
+#pragma unroll
+        for (int gi = 0; gi < kGroups; ++gi) {
+            const int g = kc / (16 * NG) + gi;
+            sc[gi] = to_f32<TS>(scales[(int64_t)g * N + nn]);
+            zw[gi] = AWQ ? qzeros[(int64_t)g * (N / 8) + nn / 8] : qzeros[(int64_t)(g / 8) * N + nn];
+        }
+    };
+    load_chunk(ka);
+    // activations: one k-octet (16 bytes) per thread and load, permuted in registers for AWQ
     const int K8 = K >> 3;
     for (int m = 0; m < B; ++m) {
         const uint4* src = reinterpret_cast<const uint4*>(act + (int64_t)m * K);
         uint2* dst = reinterpret_cast<uint2*>(ah + m * KP);
-#pragma unroll 2
-        for (int o = threadIdx.x; o < K8; o += 256) {
+        for (int o = threadIdx.x; o < K8; o += blockDim.x) {
             uint4 v = src[o];
             if (AWQ)  // halves (0,1)(2,3)(4,5)(6,7) -> (0,2)(4,6)(1,3)(5,7)
                 v = uint4{(v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16),
@@ -597,35 +626,14 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
         }
     }
     __syncthreads();
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int tile = wave & 1, half = wave >> 1;
-    const int col = lane & 15, kq = lane >> 4;
-    const int n = blockIdx.x * 32 + tile * 16 + col;
-    const int nn = min(n, N - 1);  // columns past N read the last one, not stored
-    const int m = lane & 15;       // A operand row
+    const int m = lane & 15;  // A operand row
     const bool arow = m < B;
     const uint16_t* arp = ah + min(m, B - 1) * KP + 4 * kq;
-    const int kh = K / 2, ka = half * kh, kb = ka + kh;
     const uint32_t sh = 16u * (uint32_t)(kq & 1);
     uint32_t lo4 = 0x000f000fu, one024 = 0x64006400u;  // VGPR operands of v_and_or_b32
     asm volatile("" : "+v"(lo4), "+v"(one024));
     f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int kc = ka; kc < kb; kc += kGqChunk) {
-        // this lane's 32 words of the chunk (k-octets kc/8 + 2j + kq/2) and the
-        // chunk's group scales and zeros, all in flight together
-        uint32_t qv[kSteps];
-#pragma unroll
-        for (int j = 0; j < kSteps; ++j)
-            qv[j] = qweight[(int64_t)(kc / 8 + 2 * j + (kq >> 1)) * N + nn];
-        float sc[kGroups];
-        uint32_t zw[kGroups];
-#pragma unroll
-        for (int gi = 0; gi < kGroups; ++gi) {
-            const int g = kc / (16 * NG) + gi;
-            sc[gi] = to_f32<TS>(scales[(int64_t)g * N + nn]);
-            zw[gi] = AWQ ? qzeros[(int64_t)g * (N / 8) + nn / 8] : qzeros[(int64_t)(g / 8) * N + nn];
-        }
 #pragma unroll
         for (int gi = 0; gi < kGroups; ++gi) {
             const int g = kc / (16 * NG) + gi;
@@ -650,16 +658,233 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
             }
             acc += cg * sc[gi];
         }
+        if (kc + kGqChunk < kb) load_chunk(kc + kGqChunk);
     }
-    if (half == 1) red[tile][lane] = acc;
+    // the parts' sums added in part order
+    if (part > 0) red[part - 1][tile][lane] = acc;
     __syncthreads();
-    if (half == 0 && n < N) {
-        const f4m o = acc + red[tile][lane];
+    if (part == 0 && n < N) {
+        f4m o = acc;
+        for (int p = 1; p < parts; ++p) o += red[p - 1][tile][lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = 4 * kq + i;  // D: lane holds rows 4 (lane / 16) .. +3 of column n
             if (row < B) y[(int64_t)row * N + n] = o[i];
         }
+    }
+}
+
+// GPTQ / AWQ at batch 1..4 with 128-bit weight loads: a lane owns 4 adjacent
+// columns (one 16-byte load of a qweight row = their 4 words of one k-octet),
+// LR lanes cover a workgroup's 4 LR columns and the kGqT / LR lane groups
+// ("k-groups") take consecutive K ranges of SPL segments of 64 k (8 octets,
+// 8 loads; the last k-groups have fewer or none when K is not a multiple of
+// their total). The next segment's words, scales and zeros are in flight while a
+// segment is computed, the first segment's before the activations are staged.
+// Per segment and column the group's scale applies once:
+// y += s * sum_k a_k (q_k - z).
+//
+// fp16 activations: nibbles e and e + 4 of a word become one exact fp16 pair
+// (q - z) with a shift, an and-or forming 1024 + q and one packed
+// subtraction of 1024 + z, and meet the activations of the same two k in
+// v_dot2_f32_f16 (exact products, fp32 accumulation). The staged octet holds
+// those activation pairs: GPTQ (k, k+4) for k < 4; AWQ, whose nibble e holds
+// k = {0,2,4,6,1,3,5,7}[e], (0,1)(2,3)(4,5)(6,7) -- the octet as it is.
+// fp32 activations: (float)q - z per nibble in fp32 FMAs, the octet staged in
+// nibble order. One octet of LDS padding after each k-group's range keeps
+// the k-groups of a wave on different banks. The k-groups' sums are added in
+// LDS in k-group order (each output written once, by one workgroup).
+constexpr int kGqT = 512;  // threads of gq_v4_kernel
+template <typename TA>
+struct GqAct;  // activations of one k-octet
+template <>
+struct GqAct<uint16_t> {
+    static constexpr int kU4 = 1;  // 16-byte units per octet
+};
+template <>
+struct GqAct<float> {
+    static constexpr int kU4 = 2;
+};
+
+template <bool AWQ, typename TA, typename TS, int BM, int LR, int GS>  // GS: groups per segment
+__global__ void __launch_bounds__(kGqT)
+gq_v4_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
+             const TS* __restrict__ scales, const uint32_t* __restrict__ qzeros,
+             float* __restrict__ y, int K, int N, int group, int B, int SPL) {
+    constexpr int KG = kGqT / LR, CW = 4 * LR, kU = GqAct<TA>::kU4;
+    constexpr int kOs = 8 / GS;  // octets per group inside a segment
+    constexpr int kSW = sizeof(TS) == 2 ? 2 : 4, kZW = AWQ ? 1 : 4;
+    extern __shared__ uint4 av_s[];  // [B][K/8 + KG] octets of kU x 16 bytes
+    __shared__ float red[KG][BM][CW];
+    const int tid = threadIdx.x, cq = tid % LR, kg = tid / LR;
+    const int n0 = blockIdx.x * CW + 4 * cq;
+    const int nc = min(n0, N - 4);  // lanes past N read the last 4 columns, not stored
+    const int K8 = K >> 3, rs = K8 + KG;  // LDS row stride in octets
+    const int ob = kg * SPL * 8;          // the k-group's first octet
+    const int nseg = max(0, min(SPL, (K8 - ob) >> 3));  // its segments (the last k-groups may
+                                                        // have fewer or none)
+    // one segment's words, with its groups' scales and zeros raw (fp16 scales as 2 words,
+    // fp32 as 4; GPTQ zeros as the 4 columns' words, AWQ as the one word holding them)
+    struct Seg {
+        uint4 q[8];
+        uint32_t s[GS][kSW];
+        uint32_t z[GS][kZW];
+    };
+    auto load_seg = [&](Seg& d, int seg) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            d.q[u] = *reinterpret_cast<const uint4*>(qweight + (int64_t)(ob + seg * 8 + u) * N + nc);
+#pragma unroll
+        for (int gi = 0; gi < GS; ++gi) {
+            const int g = ((ob + seg * 8) * 8) / group + gi;
+            if (kSW == 2) {
+                const uint2 v = *reinterpret_cast<const uint2*>(scales + (int64_t)g * N + nc);
+                d.s[gi][0] = v.x;
+                d.s[gi][kSW - 1] = v.y;
+            } else {
+                const uint4 v = *reinterpret_cast<const uint4*>(scales + (int64_t)g * N + nc);
+                d.s[gi][0] = v.x;
+                d.s[gi][1 % kSW] = v.y;
+                d.s[gi][2 % kSW] = v.z;
+                d.s[gi][kSW - 1] = v.w;
+            }
+            if (AWQ) {
+                d.z[gi][0] = qzeros[(int64_t)g * (N / 8) + nc / 8];
+            } else {
+                const uint4 v = *reinterpret_cast<const uint4*>(qzeros + (int64_t)(g / 8) * N + nc);
+                d.z[gi][0] = v.x;
+                d.z[gi][1 % kZW] = v.y;
+                d.z[gi][2 % kZW] = v.z;
+                d.z[gi][kZW - 1] = v.w;
+            }
+        }
+    };
+    Seg sa, sb;
+    if (nseg > 0) load_seg(sa, 0);
+    {  // activations: one 16-byte unit per thread and load
+        const int units = K8 * kU, orng = SPL * 8;
+        for (int b = 0; b < B; ++b) {
+            const uint4* src = reinterpret_cast<const uint4*>(act + (int64_t)b * K);
+            for (int i = tid; i < units; i += kGqT) {
+                const int o = i / kU, h = i - o * kU;
+                uint4 v = src[i];
+                if (kU == 1) {
+                    if (!AWQ)  // fp16 halves (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
+                        v = uint4{(v.x & 0xffffu) | (v.z << 16), (v.x >> 16) | (v.z & 0xffff0000u),
+                                  (v.y & 0xffffu) | (v.w << 16), (v.y >> 16) | (v.w & 0xffff0000u)};
+                } else if (AWQ) {  // fp32 units (0..3)(4..7) -> (0,2,4,6)(1,3,5,7)
+                    const uint4 w = src[i ^ 1];
+                    const uint4 lo = h ? w : v, hi = h ? v : w;
+                    v = h ? uint4{lo.y, lo.w, hi.y, hi.w} : uint4{lo.x, lo.z, hi.x, hi.z};
+                }
+                av_s[(b * rs + o + o / orng) * kU + h] = v;
+            }
+        }
+    }
+    __syncthreads();
+    uint32_t lo4 = 0x000f000fu, one024 = 0x64006400u;  // VGPR operands of v_and_or_b32
+    asm volatile("" : "+v"(lo4), "+v"(one024));
+    float acc[BM][4];
+#pragma unroll
+    for (int b = 0; b < BM; ++b)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[b][c] = 0.0f;
+    auto compute_seg = [&](const Seg& d, int seg) {
+#pragma unroll
+        for (int gi = 0; gi < GS; ++gi) {
+            const int g = ((ob + seg * 8) * 8) / group + gi;
+            float sc[4], zf[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                if (kSW == 2)
+                    sc[c] = half_bits_to_float((uint16_t)(d.s[gi][(c >> 1) % kSW] >> (16 * (c & 1))));
+                else
+                    sc[c] = __builtin_bit_cast(float, d.s[gi][c % kSW]);
+                if (AWQ)
+                    zf[c] = (float)((d.z[gi][0] >> (4 * (nc % 8 + c))) & 15u);
+                else
+                    zf[c] = (float)(((d.z[gi][c % kZW] >> (4 * (g % 8))) & 15u) + 1);
+            }
+            float gs[BM][4];
+#pragma unroll
+            for (int b = 0; b < BM; ++b)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) gs[b][c] = 0.0f;
+#pragma unroll
+            for (int uu = 0; uu < kOs; ++uu) {
+                const int u = gi * kOs + uu;  // octet of the segment
+                const int o = ob + seg * 8 + u;
+                const uint32_t qw4[4] = {d.q[u].x, d.q[u].y, d.q[u].z, d.q[u].w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    if (kU == 1) {
+                        const _Float16 bz = (_Float16)(-1024.0f - zf[c]);
+                        const h2v bias = {bz, bz};
+                        h2v wd[4];  // nibbles (i, i + 4)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const uint32_t zz = ((qw4[c] >> (4 * i)) & lo4) | one024;
+                            wd[i] = __builtin_bit_cast(h2v, zz) + bias;
+                        }
+#pragma unroll
+                        for (int b = 0; b < BM; ++b) {
+                            if (b >= B) break;
+                            const uint4 A = av_s[b * rs + o + kg];
+                            float t = gs[b][c];
+                            t = __builtin_amdgcn_fdot2(wd[0], __builtin_bit_cast(h2v, A.x), t, false);
+                            t = __builtin_amdgcn_fdot2(wd[1], __builtin_bit_cast(h2v, A.y), t, false);
+                            t = __builtin_amdgcn_fdot2(wd[2], __builtin_bit_cast(h2v, A.z), t, false);
+                            t = __builtin_amdgcn_fdot2(wd[3], __builtin_bit_cast(h2v, A.w), t, false);
+                            gs[b][c] = t;
+                        }
+                    } else {
+                        const uint32_t ev = qw4[c] & 0x0f0f0f0fu, od = (qw4[c] >> 4) & 0x0f0f0f0fu;
+                        float wf[8];  // nibble e = position e of the staged octet
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            wf[2 * i] = (float)((ev >> (8 * i)) & 0xffu) - zf[c];
+                            wf[2 * i + 1] = (float)((od >> (8 * i)) & 0xffu) - zf[c];
+                        }
+#pragma unroll
+                        for (int b = 0; b < BM; ++b) {
+                            if (b >= B) break;
+                            const uint4 A0 = av_s[(b * rs + o + kg) * 2];
+                            const uint4 A1 = av_s[(b * rs + o + kg) * 2 + 1];
+                            const uint32_t aw[8] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w};
+                            float t = gs[b][c];
+#pragma unroll
+                            for (int e = 0; e < 8; ++e)
+                                t = __builtin_fmaf(__builtin_bit_cast(float, aw[e]), wf[e], t);
+                            gs[b][c] = t;
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int b = 0; b < BM; ++b)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) acc[b][c] = __builtin_fmaf(gs[b][c], sc[c], acc[b][c]);
+        }
+    };
+    for (int seg = 0; seg < nseg; seg += 2) {
+        if (seg + 1 < nseg) load_seg(sb, seg + 1);
+        compute_seg(sa, seg);
+        if (seg + 1 >= nseg) break;
+        if (seg + 2 < nseg) load_seg(sa, seg + 2);
+        compute_seg(sb, seg + 1);
+    }
+#pragma unroll
+    for (int b = 0; b < BM; ++b)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) red[kg][b][4 * cq + c] = acc[b][c];
+    __syncthreads();
+    for (int t = tid; t < B * CW; t += kGqT) {
+        const int b = t / CW, col = t - b * CW;
+        const int n = blockIdx.x * CW + col;
+        if (n >= N) continue;
+        float sum = 0.0f;
+        for (int q = 0; q < KG; ++q) sum += red[q][b][col];
+        y[(int64_t)b * N + n] = sum;
     }
 }
 
@@ -713,6 +938,51 @@ template <bool AWQ, typename TA, typename TS>
 static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
                      const uint32_t* qzeros, float* y, int K, int N, int group, int B,
                      hipStream_t st) {
+    constexpr bool kF16 = std::is_same<TA, uint16_t>::value;
+    // fp16 activations from batch 4 on: fp16 MFMA (K in whole 512-k chunks per part, groups of 16-k steps
+    // dividing them, the staged activations within LDS)
+    if (kF16 && B >= 4 && B <= 16 && K % kGqChunk == 0 && group % 16 == 0 &&
+        kGqChunk % group == 0 && ((uintptr_t)act & 15) == 0 &&
+        (size_t)B * (K + 4) * 2 <= kGqLds) {
+        int parts = kGqParts;  // K split into 4, 2 or 1 parts of whole chunks
+        while (K % (parts * kGqChunk) != 0) parts /= 2;
+        const dim3 grid((unsigned)ceil_div(N, 32)), block((unsigned)(128 * parts));
+        const size_t lds = (size_t)B * (K + 4) * 2;
+        switch (group / 16) {
+#define GQM_CASE(NG)                                                                          \
+            case NG:                                                                          \
+                hipLaunchKernelGGL((gq_mfma_kernel<AWQ, TS, NG>), grid, block, lds, st,        \
+                                   (const uint16_t*)act, qweight, scales, qzeros, y, K, N, B); \
+                return launch_status(AWQ ? "awq_mfma_kernel" : "gptq_mfma_kernel");
+            GQM_CASE(2) GQM_CASE(4) GQM_CASE(8) GQM_CASE(16) GQM_CASE(32)
+#undef GQM_CASE
+            default: break;  // other group sizes: the packed fp16 dot below
+        }
+    }
+    // batch 1..4: 128-bit weight loads, 4 columns per lane (N % 4 == 0, aligned operands,
+    // K in whole 64-k segments, groups of 32 or a multiple of 64)
+    {
+        constexpr int LR = kGqLR, KG = kGqT / LR;
+        const size_t lds = (size_t)B * (K / 8 + KG) * 16 * (kF16 ? 1 : 2);
+        const bool aligned = ((uintptr_t)act & 15) == 0 && ((uintptr_t)qweight & 15) == 0 &&
+                             ((uintptr_t)scales & (sizeof(TS) == 2 ? 7 : 15)) == 0 &&
+                             ((uintptr_t)qzeros & (AWQ ? 3 : 15)) == 0;
+        if (B <= 4 && N % 4 == 0 && K % 64 == 0 && (group == 32 || group % 64 == 0) &&
+            aligned && lds <= 64 * 1024) {
+            const int SPL = (int)ceil_div(K / 64, KG);
+            const dim3 grid((unsigned)ceil_div(N, 4 * LR));
+#define GQV_CASE(BM, GS)                                                                      \
+            if (B <= BM && (GS == 2) == (group == 32)) {                                      \
+                hipLaunchKernelGGL((gq_v4_kernel<AWQ, TA, TS, BM, LR, GS>), grid, dim3(kGqT),  \
+                                   lds, st, act, qweight, scales, qzeros, y, K, N, group, B,   \
+                                   SPL);                                                      \
+                return launch_status(AWQ ? "awq_v4_kernel" : "gptq_v4_kernel");               \
+            }
+            GQV_CASE(1, 1) GQV_CASE(1, 2) GQV_CASE(2, 1) GQV_CASE(2, 2) GQV_CASE(4, 1)
+            GQV_CASE(4, 2)
+#undef GQV_CASE
+        }
+    }
     const int tiles = (int)ceil_div(N, 256);
     // split K (in whole groups) until there are ~1024 blocks
     const int ngroups = (int)ceil_div(K, group);
@@ -753,30 +1023,12 @@ static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
                                cnt);                                                         \
         return launch_status(AWQ ? "awq_kernel" : "gptq_kernel");                            \
     }
-    // fp16 activations take the packed fp16 dot (the pairs need whole k-octets: K % 8 == 0)
-    constexpr bool kF16 = std::is_same<TA, uint16_t>::value;
-    // and from batch 4 on, fp16 MFMA (K in whole 512-k chunks per half, groups of 16-k steps
-    // dividing them, the staged activations within LDS)
-    if (kF16 && B >= 4 && B <= 16 && K % (2 * kGqChunk) == 0 && group % 16 == 0 &&
-        ((uintptr_t)act & 15) == 0 &&
-        kGqChunk % group == 0 && (size_t)B * (K + 4) * 2 <= 160 * 1024 - 2048) {
-        const dim3 grid((unsigned)ceil_div(N, 32));
-        const size_t lds = (size_t)B * (K + 4) * 2;
-        switch (group / 16) {
-#define GQM_CASE(NG)                                                                          \
-            case NG:                                                                          \
-                hipLaunchKernelGGL((gq_mfma_kernel<AWQ, TS, NG>), grid, dim3(256), lds, st,    \
-                                   (const uint16_t*)act, qweight, scales, qzeros, y, K, N, B); \
-                return launch_status(AWQ ? "awq_mfma_kernel" : "gptq_mfma_kernel");
-            GQM_CASE(2) GQM_CASE(4) GQM_CASE(8) GQM_CASE(16) GQM_CASE(32)
-#undef GQM_CASE
-            default: break;  // other group sizes: the packed fp16 dot below
-        }
-    }
+    // otherwise the packed fp16 dot (fp16 activations; the pairs need whole k-octets:
+    // K % 8 == 0) or fp32 FMAs, 32-bit weight loads, split K
     GQ_CASE(1) GQ_CASE(2) GQ_CASE(4) GQ_CASE(8)
 #undef GQ_CASE
     set_error("gptq/awq: batch %d > 8 needs the MFMA path (16-byte aligned fp16 activations, "
-              "K %% 1024 == 0, group 32..512 dividing 512, B (K + 4) fp16 within 158 KiB of LDS)",
+              "K %% 512 == 0, group 32..512 dividing 512, B (K + 4) fp16 within 152 KiB of LDS)",
               B);
     return TENZO_ERROR_UNSUPPORTED;
 }

@@ -171,12 +171,13 @@ def test_gptq_awq_benchmark_shape(torch_dev, kind, B):
 
 @pytest.mark.parametrize("kind", ["gptq", "awq"])
 @pytest.mark.parametrize("B,K,N,G,f32s", [(4, 1024, 1000, 32, False), (5, 2048, 264, 64, True),
-                                          (16, 4096, 96, 256, False), (9, 1024, 40, 512, False),
-                                          (12, 2048, 520, 128, True)])
+                                          (16, 4096, 96, 256, False), (9, 1536, 40, 512, False),
+                                          (12, 2048, 520, 128, True), (6, 512, 72, 64, False)])
 def test_gptq_awq_mfma_shapes(torch_dev, kind, B, K, N, G, f32s):
     """Batch 4-16 with fp16 activations runs on fp16 MFMA: ragged N (a partly used 32-column
     tile), batches that fill 4..16 of the 16 MFMA rows, every group size from 32 to 512
-    (2..32 MFMA steps per group), fp16 and fp32 scales."""
+    (2..32 MFMA steps per group), fp16 and fp32 scales, K in 4, 2 and 1 parts per workgroup
+    with one to three 512-k chunks per part."""
     from tenzo_amd import ops
     torch = torch_dev
     print(f"{kind} mfma B={B} K={K} N={N} G={G} f32s={f32s}", flush=True)
@@ -197,6 +198,45 @@ def test_gptq_awq_mfma_shapes(torch_dev, kind, B, K, N, G, f32s):
     for b in range(B):
         ref = ofn(a[b].astype(np.float32), qw, scales.astype(np.float32), qz, K, N, G)
         close(y[b], ref, a[b].astype(np.float32), W)
+
+
+@pytest.mark.parametrize("kind", ["gptq", "awq"])
+@pytest.mark.parametrize("B,K,N,G,f16a,f32s", [(1, 2048, 40, 32, True, False),
+                                               (2, 6144, 1000, 64, False, True),
+                                               (3, 4096, 520, 256, True, True),
+                                               (4, 2048, 264, 128, False, False),
+                                               (1, 4096, 8, 512, False, False),
+                                               (2, 8192, 96, 1024, True, False),
+                                               (4, 4096, 72, 1024, True, False),
+                                               (1, 10240, 64, 128, True, False),
+                                               (3, 3072, 128, 32, False, True)])
+def test_gptq_awq_wide_load_shapes(torch_dev, kind, B, K, N, G, f16a, f32s):
+    """Batch 1-4 on 128-bit weight loads (4 columns per lane): fp16 and fp32 activations and
+    scales, groups of 32 (two per 64-k segment) up to 1024 (spanning several k-groups), one to
+    three segments per k-group (K = 6144, 8192: two; 10240: three, the last k-group one),
+    k-groups left without a segment (K = 2048, 3072), N not a multiple of the workgroup's 32
+    columns, and batch 4 with fp16 activations where the MFMA path does not apply (group
+    1024)."""
+    from tenzo_amd import ops
+    torch = torch_dev
+    print(f"{kind} wide B={B} K={K} N={N} G={G} f16a={f16a} f32s={f32s}", flush=True)
+    rng = np.random.default_rng(B * 13 + K + N + G)
+    q = rng.integers(0, 16, size=(K, N), dtype=np.uint8)
+    zeros = rng.integers(0, 16, size=(K // G, N), dtype=np.uint8)
+    scales = synth.f16_round(np.abs(rng.normal(0, 0.01, size=(K // G, N))))
+    scales = scales.astype(np.float32 if f32s else np.float16)
+    pack = formats.gptq_pack if kind == "gptq" else formats.awq_pack
+    qw, qz = pack(q, zeros)
+    a = rng.standard_normal((B, K)).astype(np.float16 if f16a else np.float32)
+    fn = ops.gemv_gptq if kind == "gptq" else ops.gemv_awq
+    y = fn(dev(torch, a), dev(torch, qw), dev(torch, scales), dev(torch, qz), K, N,
+           G).cpu().numpy()
+    assert y.shape == (B, N)
+    ofn = oracle.gptq if kind == "gptq" else oracle.awq
+    W = gq_dense(q, zeros, scales, G, kind)
+    for b in range(B):
+        a32 = a[b].astype(np.float32)
+        close(y[b], ofn(a32, qw, scales.astype(np.float32), qz, K, N, G), a32, W)
 
 
 def gq_dense(q, zeros, scales, G, kind):
