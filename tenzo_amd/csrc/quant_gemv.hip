@@ -694,7 +694,8 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
 // nibble order. One octet of LDS padding after each k-group's range keeps
 // the k-groups of a wave on different banks. The k-groups' sums are added in
 // LDS in k-group order (each output written once, by one workgroup).
-constexpr int kGqT = 512;  // threads of gq_v4_kernel
+constexpr int kGqT = 512;    // threads of gq_v4_kernel
+constexpr int kGqStg = 8;    // 16-byte activation units staged per thread
 template <typename TA>
 struct GqAct;  // activations of one k-octet
 template <>
@@ -730,10 +731,7 @@ gq_v4_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
         uint32_t s[GS][kSW];
         uint32_t z[GS][kZW];
     };
-    auto load_seg = [&](Seg& d, int seg) {
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            d.q[u] = *reinterpret_cast<const uint4*>(qweight + (int64_t)(ob + seg * 8 + u) * N + nc);
+    auto load_seg = [&](Seg& d, int seg) {  // scales and zeros first: they are used first
 #pragma unroll
         for (int gi = 0; gi < GS; ++gi) {
             const int g = ((ob + seg * 8) * 8) / group + gi;
@@ -758,30 +756,39 @@ gq_v4_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
                 d.z[gi][kZW - 1] = v.w;
             }
         }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            d.q[u] = *reinterpret_cast<const uint4*>(qweight + (int64_t)(ob + seg * 8 + u) * N + nc);
     };
+    // activations first (an L2 hit in a decode step: written by the step before): the octets
+    // of all rows (contiguous, B * K / 8 of them), at most kGqStg 16-byte units per thread,
+    // into LDS; then the first segment's loads, which stay in flight across the barrier
+    // (s_barrier after the LDS stores alone, no wait for the vector loads)
+    constexpr int kStg = kGqStg / kU;
+    const int octs = B * K8, orng = SPL * 8;
+#pragma unroll
+    for (int j = 0; j < kStg; ++j) {
+        const int i = tid + j * kGqT;
+        if (i >= octs) break;
+        const int b = i / K8, o = i - b * K8;
+        uint4 v[kU];
+#pragma unroll
+        for (int h = 0; h < kU; ++h) v[h] = reinterpret_cast<const uint4*>(act)[i * kU + h];
+        if (kU == 1 && !AWQ) {  // fp16 halves (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
+            const uint4 w = v[0];
+            v[0] = uint4{(w.x & 0xffffu) | (w.z << 16), (w.x >> 16) | (w.z & 0xffff0000u),
+                         (w.y & 0xffffu) | (w.w << 16), (w.y >> 16) | (w.w & 0xffff0000u)};
+        } else if (kU == 2 && AWQ) {  // fp32 (0..3)(4..7) -> (0,2,4,6)(1,3,5,7)
+            const uint4 lo = v[0], hi = v[kU - 1];
+            v[0] = uint4{lo.x, lo.z, hi.x, hi.z};
+            v[kU - 1] = uint4{lo.y, lo.w, hi.y, hi.w};
+        }
+#pragma unroll
+        for (int h = 0; h < kU; ++h) av_s[(b * rs + o + o / orng) * kU + h] = v[h];
+    }
     Seg sa, sb;
     if (nseg > 0) load_seg(sa, 0);
-    {  // activations: one 16-byte unit per thread and load
-        const int units = K8 * kU, orng = SPL * 8;
-        for (int b = 0; b < B; ++b) {
-            const uint4* src = reinterpret_cast<const uint4*>(act + (int64_t)b * K);
-            for (int i = tid; i < units; i += kGqT) {
-                const int o = i / kU, h = i - o * kU;
-                uint4 v = src[i];
-                if (kU == 1) {
-                    if (!AWQ)  // fp16 halves (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
-                        v = uint4{(v.x & 0xffffu) | (v.z << 16), (v.x >> 16) | (v.z & 0xffff0000u),
-                                  (v.y & 0xffffu) | (v.w << 16), (v.y >> 16) | (v.w & 0xffff0000u)};
-                } else if (AWQ) {  // fp32 units (0..3)(4..7) -> (0,2,4,6)(1,3,5,7)
-                    const uint4 w = src[i ^ 1];
-                    const uint4 lo = h ? w : v, hi = h ? v : w;
-                    v = h ? uint4{lo.y, lo.w, hi.y, hi.w} : uint4{lo.x, lo.z, hi.x, hi.z};
-                }
-                av_s[(b * rs + o + o / orng) * kU + h] = v;
-            }
-        }
-    }
-    __syncthreads();
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     uint32_t lo4 = 0x000f000fu, one024 = 0x64006400u;  // VGPR operands of v_and_or_b32
     asm volatile("" : "+v"(lo4), "+v"(one024));
     float acc[BM][4];
@@ -827,9 +834,8 @@ gq_v4_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
                             wd[i] = __builtin_bit_cast(h2v, zz) + bias;
                         }
 #pragma unroll
-                        for (int b = 0; b < BM; ++b) {
-                            if (b >= B) break;
-                            const uint4 A = av_s[b * rs + o + kg];
+                        for (int b = 0; b < BM; ++b) {  // rows past B: row B - 1, not stored
+                            const uint4 A = av_s[min(b, B - 1) * rs + o + kg];
                             float t = gs[b][c];
                             t = __builtin_amdgcn_fdot2(wd[0], __builtin_bit_cast(h2v, A.x), t, false);
                             t = __builtin_amdgcn_fdot2(wd[1], __builtin_bit_cast(h2v, A.y), t, false);
@@ -847,9 +853,9 @@ gq_v4_kernel(const TA* __restrict__ act, const uint32_t* __restrict__ qweight,
                         }
 #pragma unroll
                         for (int b = 0; b < BM; ++b) {
-                            if (b >= B) break;
-                            const uint4 A0 = av_s[(b * rs + o + kg) * 2];
-                            const uint4 A1 = av_s[(b * rs + o + kg) * 2 + 1];
+                            const int ab = (min(b, B - 1) * rs + o + kg) * 2;
+                            const uint4 A0 = av_s[ab];
+                            const uint4 A1 = av_s[ab + 1];
                             const uint32_t aw[8] = {A0.x, A0.y, A0.z, A0.w, A1.x, A1.y, A1.z, A1.w};
                             float t = gs[b][c];
 #pragma unroll
@@ -968,7 +974,8 @@ static int launch_gq(const TA* act, const uint32_t* qweight, const TS* scales,
                              ((uintptr_t)scales & (sizeof(TS) == 2 ? 7 : 15)) == 0 &&
                              ((uintptr_t)qzeros & (AWQ ? 3 : 15)) == 0;
         if (B <= 4 && N % 4 == 0 && K % 64 == 0 && (group == 32 || group % 64 == 0) &&
-            aligned && lds <= 64 * 1024) {
+            aligned && lds <= 64 * 1024 &&
+            (size_t)B * (K / 8) * (kF16 ? 1 : 2) <= (size_t)kGqStg * kGqT) {
             const int SPL = (int)ceil_div(K / 64, KG);
             const dim3 grid((unsigned)ceil_div(N, 4 * LR));
 #define GQV_CASE(BM, GS)                                                                      \
