@@ -567,8 +567,8 @@ gq_h2_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qwei
 // (tile, part) = (w % 2, w / 2) take 16 columns and one of 4, 2 or 1 parts of
 // K (whole 512-k chunks each), and the parts are added in LDS in part order.
 // Each lane keeps the 32 qweight words of a chunk in flight, the first
-// chunk's issued before the activations are staged. Products are exact and
-// summed in fp32 (the MFMA's own order).
+// chunk's across the barrier that follows the activation staging. Products
+// are exact and summed in fp32 (the MFMA's own order).
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef float f4m __attribute__((ext_vector_type(4)));
 constexpr int kGqChunk = 512;  // k per load batch (32 words per lane)
@@ -599,33 +599,45 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
     uint32_t qv[kSteps];
     float sc[kGroups];
     uint32_t zw[kGroups];
-    auto load_chunk = [&](int kc) {
-#pragma unroll
-        for (int j = 0; j < kSteps; ++j)
-            qv[j] = qweight[(int64_t)(kc / 8 + 2 * j + (kq >> 1)) * N + nn];
+    auto load_chunk = [&](int kc) {  // the group scales and zeros first: used first
 #pragma unroll
         for (int gi = 0; gi < kGroups; ++gi) {
             const int g = kc / (16 * NG) + gi;
             sc[gi] = to_f32<TS>(scales[(int64_t)g * N + nn]);
             zw[gi] = AWQ ? qzeros[(int64_t)g * (N / 8) + nn / 8] : qzeros[(int64_t)(g / 8) * N + nn];
         }
+#pragma unroll
+        for (int j = 0; j < kSteps; ++j)
+            qv[j] = qweight[(int64_t)(kc / 8 + 2 * j + (kq >> 1)) * N + nn];
     };
-    load_chunk(ka);
-    // activations: one k-octet (16 bytes) per thread and load, permuted in registers for AWQ
-    const int K8 = K >> 3;
-    for (int m = 0; m < B; ++m) {
-        const uint4* src = reinterpret_cast<const uint4*>(act + (int64_t)m * K);
-        uint2* dst = reinterpret_cast<uint2*>(ah + m * KP);
-        for (int o = threadIdx.x; o < K8; o += blockDim.x) {
-            uint4 v = src[o];
-            if (AWQ)  // halves (0,1)(2,3)(4,5)(6,7) -> (0,2)(4,6)(1,3)(5,7)
-                v = uint4{(v.x & 0xffffu) | (v.y << 16), (v.z & 0xffffu) | (v.w << 16),
-                          (v.x >> 16) | (v.y & 0xffff0000u), (v.z >> 16) | (v.w & 0xffff0000u)};
-            dst[2 * o] = uint2{v.x, v.y};
-            dst[2 * o + 1] = uint2{v.z, v.w};
+    // activations first (an L2 hit in a decode step), one k-octet (16 bytes) per thread
+    // and load, four loads in flight, permuted in registers for AWQ; then the first
+    // chunk's loads, which stay in flight across the barrier (s_barrier after the LDS
+    // stores alone, no wait for the vector loads)
+    const int K8 = K >> 3, octs = B * K8, T = (int)blockDim.x;
+    const uint4* src = reinterpret_cast<const uint4*>(act);
+    for (int j0 = 0; j0 * T < octs; j0 += 4) {
+        uint4 v[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+            v[jj] = src[min((int)threadIdx.x + (j0 + jj) * T, octs - 1)];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int i = (int)threadIdx.x + (j0 + jj) * T;
+            if (i < octs) {
+                const int r = i / K8, o = i - r * K8;
+                uint4 w = v[jj];
+                if (AWQ)  // halves (0,1)(2,3)(4,5)(6,7) -> (0,2)(4,6)(1,3)(5,7)
+                    w = uint4{(w.x & 0xffffu) | (w.y << 16), (w.z & 0xffffu) | (w.w << 16),
+                              (w.x >> 16) | (w.y & 0xffff0000u), (w.z >> 16) | (w.w & 0xffff0000u)};
+                uint2* dst = reinterpret_cast<uint2*>(ah + r * KP) + 2 * o;
+                dst[0] = uint2{w.x, w.y};
+                dst[1] = uint2{w.z, w.w};
+            }
         }
     }
-    __syncthreads();
+    load_chunk(ka);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const int m = lane & 15;  // A operand row
     const bool arow = m < B;
     const uint16_t* arp = ah + min(m, B - 1) * KP + 4 * kq;
