@@ -214,54 +214,129 @@ __device__ __forceinline__ float q4_block_h2(const uint32_t* dw, int off, const 
     return s;
 }
 
-template <int LPR>
+// With FULL (K % 256 == 0 and 16-byte aligned operands: every group of 8
+// blocks is whole and aligned) the latency is arranged for one pass: each
+// thread first issues its activation loads (16 bytes each, up to four in
+// flight), then its row's first group of weights (nine 16-byte loads), and
+// only then waits for the activations, stores them in LDS and meets the other
+// waves at an s_barrier that waits for the LDS stores alone, so the weights
+// stream while the activations are staged; the staged pairs get 16 bytes of
+// padding per group of 8 blocks (the lanes of a row read one group apart:
+// without it, all on the same LDS banks). The lane's groups are summed in the
+// same order either way (bit-identical results).
+template <int LPR, bool FULL>
 __global__ void __launch_bounds__(256)
 q4_0_f16_kernel(const uint16_t* __restrict__ act, const uint8_t* __restrict__ w,
                 float* __restrict__ y, int K, int N) {
     extern __shared__ uint32_t ap[];  // K/2 words: block b, j < 16: (a_32b+j, a_32b+16+j)
     const int b = blockIdx.y;
     const uint16_t* ab = act + (int64_t)b * K;
-    for (int i = threadIdx.x; i < K / 2; i += 256) {
-        const int blk = i >> 4, j = i & 15;
-        ap[i] = (uint32_t)ab[blk * 32 + j] | ((uint32_t)ab[blk * 32 + 16 + j] << 16);
-    }
-    __syncthreads();
     constexpr int RPB = 256 / LPR;
     const int row = blockIdx.x * RPB + threadIdx.x / LPR;
     const int sub = threadIdx.x % LPR;
     const int nbk = K / 32;
     const int ngroups = (nbk + 7) / 8;
     float acc = 0.0f;
-    if (row < N) {
-        const uint8_t* rowp = w + (int64_t)row * nbk * 18;
-        for (int g = sub; g < ngroups; g += LPR) {
-            const int b0 = g * 8;
-            if (b0 + 8 <= nbk && (((uintptr_t)(rowp + b0 * 18)) & 15) == 0) {
-                uint32_t dw[36];
-                const uint4* p = reinterpret_cast<const uint4*>(rowp + b0 * 18);
+    if (FULL) {
+        // activations: half-blocks (a_32b+8h.., a_32b+16+8h..), 32 bytes each; thread t
+        // stages half-block t first (past the last one: into its own slot of a spare area
+        // behind the pairs, so the stores need no branch), the rest after the barrier's
+        // weights are issued
+        const int units = nbk * 2;
+        const uint4* a4 = reinterpret_cast<const uint4*>(ab);
+        uint4* ap4 = reinterpret_cast<uint4*>(ap);
+        auto pairs = [&](uint4* dst, const uint4 lo, const uint4 hi) {
+            dst[0] = uint4{(lo.x & 0xffffu) | (hi.x << 16), (lo.x >> 16) | (hi.x & 0xffff0000u),
+                           (lo.y & 0xffffu) | (hi.y << 16), (lo.y >> 16) | (hi.y & 0xffff0000u)};
+            dst[1] = uint4{(lo.z & 0xffffu) | (hi.z << 16), (lo.z >> 16) | (hi.z & 0xffff0000u),
+                           (lo.w & 0xffffu) | (hi.w << 16), (lo.w >> 16) | (hi.w & 0xffff0000u)};
+        };
+        const int u0 = (int)threadIdx.x, uc = min(u0, units - 1);
+        const uint4 lo0 = a4[(uc >> 1) * 4 + (uc & 1)];      // elements 32 blk + 8 h ..
+        const uint4 hi0 = a4[(uc >> 1) * 4 + 2 + (uc & 1)];  // elements 32 blk + 16 + 8 h ..
+        // the row's first group (rows past N read the last row, lanes past the groups the
+        // last group; neither is summed)
+        const uint8_t* rowp = w + (int64_t)min(row, N - 1) * nbk * 18;
+        uint32_t dw[36];
+        {
+            const uint4* p = reinterpret_cast<const uint4*>(rowp + min(sub, ngroups - 1) * 144);
 #pragma unroll
-                for (int i = 0; i < 9; ++i) {
-                    const uint4 v = p[i];
-                    dw[4 * i] = v.x;
-                    dw[4 * i + 1] = v.y;
-                    dw[4 * i + 2] = v.z;
-                    dw[4 * i + 3] = v.w;
+            for (int i = 0; i < 9; ++i) {
+                const uint4 v = p[i];
+                dw[4 * i] = v.x;
+                dw[4 * i + 1] = v.y;
+                dw[4 * i + 2] = v.z;
+                dw[4 * i + 3] = v.w;
+            }
+        }
+        // (pairs of block blk at uint4 4 blk + blk / 8: 16 bytes of padding per group of 8
+        // blocks, so the lanes of a row, one group apart, read different banks)
+        const int pad_end = 4 * nbk + ngroups;
+        pairs(ap4 + (u0 < units ? 4 * (uc >> 1) + (uc >> 4) + 2 * (uc & 1) : pad_end + 2 * u0),
+              lo0, hi0);
+        for (int u = u0 + 256; u < units; u += 256)
+            pairs(ap4 + 4 * (u >> 1) + (u >> 4) + 2 * (u & 1), a4[(u >> 1) * 4 + (u & 1)],
+                  a4[(u >> 1) * 4 + 2 + (u & 1)]);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (row < N) {
+            for (int g = sub; g < ngroups; g += LPR) {
+                if (g != sub) {
+                    const uint4* p = reinterpret_cast<const uint4*>(rowp + g * 144);
+#pragma unroll
+                    for (int i = 0; i < 9; ++i) {
+                        const uint4 v = p[i];
+                        dw[4 * i] = v.x;
+                        dw[4 * i + 1] = v.y;
+                        dw[4 * i + 2] = v.z;
+                        dw[4 * i + 3] = v.w;
+                    }
                 }
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
                     const uint32_t dbits = (dw[(18 * i) >> 2] >> (8 * ((18 * i) & 3))) & 0xffffu;
                     const float d = half_bits_to_float((uint16_t)dbits);
-                    acc = __builtin_fmaf(q4_block_h2(dw, 18 * i, ap + (b0 + i) * 16), d, acc);
+                    acc = __builtin_fmaf(q4_block_h2(dw, 18 * i, ap + (g * 8 + i) * 16 + 4 * g), d,
+                                         acc);
                 }
-            } else {
-                for (int bb = b0; bb < nbk && bb < b0 + 8; ++bb) {
-                    const uint16_t* hp = reinterpret_cast<const uint16_t*>(rowp + bb * 18);
-                    uint32_t dw[5];
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < K / 2; i += 256) {
+            const int blk = i >> 4, j = i & 15;
+            ap[i] = (uint32_t)ab[blk * 32 + j] | ((uint32_t)ab[blk * 32 + 16 + j] << 16);
+        }
+        __syncthreads();
+        if (row < N) {
+            const uint8_t* rowp = w + (int64_t)row * nbk * 18;
+            for (int g = sub; g < ngroups; g += LPR) {
+                const int b0 = g * 8;
+                if (b0 + 8 <= nbk && (((uintptr_t)(rowp + b0 * 18)) & 15) == 0) {
+                    uint32_t dw[36];
+                    const uint4* p = reinterpret_cast<const uint4*>(rowp + b0 * 18);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) dw[i] = hp[2 * i] | ((uint32_t)hp[2 * i + 1] << 16);
-                    dw[4] = hp[8];
-                    const float d = half_bits_to_float((uint16_t)(dw[0] & 0xffffu));
-                    acc = __builtin_fmaf(q4_block_h2(dw, 0, ap + bb * 16), d, acc);
+                    for (int i = 0; i < 9; ++i) {
+                        const uint4 v = p[i];
+                        dw[4 * i] = v.x;
+                        dw[4 * i + 1] = v.y;
+                        dw[4 * i + 2] = v.z;
+                        dw[4 * i + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const uint32_t dbits = (dw[(18 * i) >> 2] >> (8 * ((18 * i) & 3))) & 0xffffu;
+                        const float d = half_bits_to_float((uint16_t)dbits);
+                        acc = __builtin_fmaf(q4_block_h2(dw, 18 * i, ap + (b0 + i) * 16), d, acc);
+                    }
+                } else {
+                    for (int bb = b0; bb < nbk && bb < b0 + 8; ++bb) {
+                        const uint16_t* hp = reinterpret_cast<const uint16_t*>(rowp + bb * 18);
+                        uint32_t dw[5];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) dw[i] = hp[2 * i] | ((uint32_t)hp[2 * i + 1] << 16);
+                        dw[4] = hp[8];
+                        const float d = half_bits_to_float((uint16_t)(dw[0] & 0xffffu));
+                        acc = __builtin_fmaf(q4_block_h2(dw, 0, ap + bb * 16), d, acc);
+                    }
                 }
             }
         }
@@ -1090,9 +1165,16 @@ TENZO_HIP_API int tenzo_hip_gemv_q4_0(const void* act, int act_dtype, const uint
     const size_t smem = (size_t)K * 2;
     dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
     const uint16_t* a16 = (const uint16_t*)act;
+    const bool full = K % 256 == 0 && ((uintptr_t)act & 15) == 0 && ((uintptr_t)w & 15) == 0;
+    const size_t smem_full = smem + (size_t)(nbk + 7) / 8 * 16 + 256 * 32;  // padding, spare slots
 #define Q4H_CASE(L)                                                                        \
     case L:                                                                                \
-        hipLaunchKernelGGL((q4_0_f16_kernel<L>), grid, dim3(256), smem, st, a16, w, y, K, N); \
+        if (full)                                                                          \
+            hipLaunchKernelGGL((q4_0_f16_kernel<L, true>), grid, dim3(256), smem_full, st,   \
+                               a16, w, y, K, N);                                           \
+        else                                                                               \
+            hipLaunchKernelGGL((q4_0_f16_kernel<L, false>), grid, dim3(256), smem, st, a16,  \
+                               w, y, K, N);                                                \
         break;
     switch (lpr) {
         Q4H_CASE(1) Q4H_CASE(2) Q4H_CASE(4) Q4H_CASE(8) Q4H_CASE(16) Q4H_CASE(32) Q4H_CASE(64)
