@@ -39,20 +39,100 @@ __device__ __forceinline__ float q4_block_dot(const uint32_t* dw, int off, const
     return s;
 }
 
-template <typename TA, int LPR>
+// fp32 activation staging for the row-per-lane GEMVs (FULL path: K % 256 ==
+// 0, 16-byte aligned operands). Element k sits at float k + 4 (k / 256): 16
+// bytes of padding per 256 elements, the span of one lane's group of 8
+// blocks, so the lanes of a row (one group apart) read different LDS banks.
+// A thread's first kR 16-byte loads are issued before its weights and stored
+// without a branch (units past the end go to the thread's own 32-byte spare
+// slot behind the padded row); the rest, for K beyond kR * 256 loads, follow
+// in a loop.
+__host__ __device__ constexpr int f32s_size(int K) { return K + 4 * ((K + 255) / 256); }
+template <typename TA>
+struct F32Stage {
+    static constexpr int kE = 16 / (int)sizeof(TA);     // elements per 16-byte load
+    static constexpr int kR = sizeof(TA) == 2 ? 2 : 4;  // loads per thread issued first
+    uint4 v[kR];
+    __device__ void load(const TA* a, int K) {
+        const int units = K / kE;
+#pragma unroll
+        for (int j = 0; j < kR; ++j)
+            v[j] = reinterpret_cast<const uint4*>(a)[min((int)threadIdx.x + j * 256, units - 1)];
+    }
+    __device__ static void put(float* d, const uint4 x) {
+        if (sizeof(TA) == 2) {
+            reinterpret_cast<float4*>(d)[0] =
+                float4{half_bits_to_float((uint16_t)(x.x & 0xffffu)), half_bits_to_float((uint16_t)(x.x >> 16)),
+                       half_bits_to_float((uint16_t)(x.y & 0xffffu)), half_bits_to_float((uint16_t)(x.y >> 16))};
+            reinterpret_cast<float4*>(d)[1] =
+                float4{half_bits_to_float((uint16_t)(x.z & 0xffffu)), half_bits_to_float((uint16_t)(x.z >> 16)),
+                       half_bits_to_float((uint16_t)(x.w & 0xffffu)), half_bits_to_float((uint16_t)(x.w >> 16))};
+        } else {
+            *reinterpret_cast<uint4*>(d) = x;
+        }
+    }
+    __device__ void store(float* a_s, const TA* a, int K) const {
+        const int units = K / kE;
+#pragma unroll
+        for (int j = 0; j < kR; ++j) {
+            const int u = (int)threadIdx.x + j * 256, k0 = u * kE;
+            put(u < units ? a_s + k0 + 4 * (k0 >> 8) : a_s + f32s_size(K) + 8 * (int)threadIdx.x, v[j]);
+        }
+        for (int u = (int)threadIdx.x + kR * 256; u < units; u += 256)
+            put(a_s + u * kE + 4 * ((u * kE) >> 8), reinterpret_cast<const uint4*>(a)[u]);
+    }
+};
+
+template <typename TA, int LPR, bool FULL>
 __global__ void __launch_bounds__(256)
 q4_0_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __restrict__ y,
             int K, int N) {
     extern __shared__ float a_s[];
     const int b = blockIdx.y;
-    for (int i = threadIdx.x; i < K; i += 256) a_s[i] = to_f32<TA>(act[(int64_t)b * K + i]);
-    __syncthreads();
     constexpr int RPB = 256 / LPR;
     const int row = blockIdx.x * RPB + threadIdx.x / LPR;
     const int sub = threadIdx.x % LPR;
     const int nbk = K / 32;
     const int ngroups = (nbk + 7) / 8;
     float acc = 0.0f;
+    if (FULL) {  // activations, then the first group's 9 loads, then the staging's stores
+        F32Stage<TA> stg;
+        stg.load(act + (int64_t)b * K, K);
+        const uint8_t* rowp = w + (int64_t)min(row, N - 1) * nbk * 18;
+        uint32_t dw[36];
+        auto load_group = [&](int g) {
+            const uint4* p = reinterpret_cast<const uint4*>(rowp + g * 144);
+#pragma unroll
+            for (int i = 0; i < 9; ++i) {
+                const uint4 v = p[i];
+                dw[4 * i] = v.x;
+                dw[4 * i + 1] = v.y;
+                dw[4 * i + 2] = v.z;
+                dw[4 * i + 3] = v.w;
+            }
+        };
+        load_group(min(sub, ngroups - 1));
+        stg.store(a_s, act + (int64_t)b * K, K);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (row < N) {
+            for (int g = sub; g < ngroups; g += LPR) {
+                if (g != sub) load_group(g);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t dbits = byte_at(dw, 18 * i) | (byte_at(dw, 18 * i + 1) << 8);
+                    const float d = half_bits_to_float((uint16_t)dbits);
+                    acc = __builtin_fmaf(q4_block_dot(dw, 18 * i, a_s + (g * 8 + i) * 32 + 4 * g), d,
+                                         acc);
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+        if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+        return;
+    }
+    for (int i = threadIdx.x; i < K; i += 256) a_s[i] = to_f32<TA>(act[(int64_t)b * K + i]);
+    __syncthreads();
     if (row < N) {
         const uint8_t* rowp = w + (int64_t)row * nbk * 18;
         for (int g = sub; g < ngroups; g += LPR) {
@@ -123,20 +203,56 @@ __device__ __forceinline__ float q8_block_dot(const uint32_t* dw, int off, const
     return s;
 }
 
-template <typename TA, int LPR>
+template <typename TA, int LPR, bool FULL>
 __global__ void __launch_bounds__(256)
 q8_0_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __restrict__ y,
             int K, int N) {
     extern __shared__ float a_s[];
     const int b = blockIdx.y;
-    for (int i = threadIdx.x; i < K; i += 256) a_s[i] = to_f32<TA>(act[(int64_t)b * K + i]);
-    __syncthreads();
     constexpr int RPB = 256 / LPR;
     const int row = blockIdx.x * RPB + threadIdx.x / LPR;
     const int sub = threadIdx.x % LPR;
     const int nbk = K / 32;
     const int ngroups = (nbk + 7) / 8;
     float acc = 0.0f;
+    if (FULL) {  // activations, then the first group's 17 loads, then the staging's stores
+        F32Stage<TA> stg;
+        stg.load(act + (int64_t)b * K, K);
+        const uint8_t* rowp = w + (int64_t)min(row, N - 1) * nbk * 34;
+        uint32_t dw[68];
+        auto load_group = [&](int g) {
+            const uint4* p = reinterpret_cast<const uint4*>(rowp + g * 272);
+#pragma unroll
+            for (int i = 0; i < 17; ++i) {
+                const uint4 v = p[i];
+                dw[4 * i] = v.x;
+                dw[4 * i + 1] = v.y;
+                dw[4 * i + 2] = v.z;
+                dw[4 * i + 3] = v.w;
+            }
+        };
+        load_group(min(sub, ngroups - 1));
+        stg.store(a_s, act + (int64_t)b * K, K);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (row < N) {
+            for (int g = sub; g < ngroups; g += LPR) {
+                if (g != sub) load_group(g);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const uint32_t dbits = (dw[(34 * i) >> 2] >> (8 * ((34 * i) & 3))) & 0xffffu;
+                    const float d = half_bits_to_float((uint16_t)dbits);
+                    acc = __builtin_fmaf(q8_block_dot(dw, 34 * i, a_s + (g * 8 + i) * 32 + 4 * g), d,
+                                         acc);
+                }
+            }
+        }
+#pragma unroll
+        for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+        if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+        return;
+    }
+    for (int i = threadIdx.x; i < K; i += 256) a_s[i] = to_f32<TA>(act[(int64_t)b * K + i]);
+    __syncthreads();
     if (row < N) {
         const uint8_t* rowp = w + (int64_t)row * nbk * 34;
         for (int g = sub; g < ngroups; g += LPR) {
@@ -996,11 +1112,17 @@ static int launch_q4_0(const TA* act, const uint8_t* w, float* y, int K, int N, 
                        hipStream_t st) {
     const int nbk = K / 32;
     const int lpr = pick_lpr((nbk + 7) / 8);
-    const size_t smem = (size_t)K * 4;
+    const bool full = K % 256 == 0 && ((uintptr_t)act & 15) == 0 && ((uintptr_t)w & 15) == 0;
+    const size_t smem = full ? ((size_t)f32s_size(K) + 2048) * 4 : (size_t)K * 4;
     dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
-#define Q4_CASE(L)                                                                   \
-    case L:                                                                          \
-        hipLaunchKernelGGL((q4_0_kernel<TA, L>), grid, dim3(256), smem, st, act, w, y, K, N); \
+#define Q4_CASE(L)                                                                      \
+    case L:                                                                             \
+        if (full)                                                                       \
+            hipLaunchKernelGGL((q4_0_kernel<TA, L, true>), grid, dim3(256), smem, st, act, w, \
+                               y, K, N);                                                \
+        else                                                                            \
+            hipLaunchKernelGGL((q4_0_kernel<TA, L, false>), grid, dim3(256), smem, st, act, \
+                               w, y, K, N);                                             \
         break;
     switch (lpr) {
         Q4_CASE(1) Q4_CASE(2) Q4_CASE(4) Q4_CASE(8) Q4_CASE(16) Q4_CASE(32) Q4_CASE(64)
@@ -1014,11 +1136,17 @@ static int launch_q8_0(const TA* act, const uint8_t* w, float* y, int K, int N, 
                        hipStream_t st) {
     const int nbk = K / 32;
     const int lpr = pick_lpr((nbk + 7) / 8);
-    const size_t smem = (size_t)K * 4;
+    const bool full = K % 256 == 0 && ((uintptr_t)act & 15) == 0 && ((uintptr_t)w & 15) == 0;
+    const size_t smem = full ? ((size_t)f32s_size(K) + 2048) * 4 : (size_t)K * 4;
     dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
-#define Q80_CASE(L)                                                                   \
-    case L:                                                                           \
-        hipLaunchKernelGGL((q8_0_kernel<TA, L>), grid, dim3(256), smem, st, act, w, y, K, N); \
+#define Q80_CASE(L)                                                                      \
+    case L:                                                                              \
+        if (full)                                                                        \
+            hipLaunchKernelGGL((q8_0_kernel<TA, L, true>), grid, dim3(256), smem, st, act, w, \
+                               y, K, N);                                                 \
+        else                                                                             \
+            hipLaunchKernelGGL((q8_0_kernel<TA, L, false>), grid, dim3(256), smem, st, act,  \
+                               w, y, K, N);                                              \
         break;
     switch (lpr) {
         Q80_CASE(1) Q80_CASE(2) Q80_CASE(4) Q80_CASE(8) Q80_CASE(16) Q80_CASE(32) Q80_CASE(64)
