@@ -518,6 +518,109 @@ q4_0_q8_kernel(const uint8_t* __restrict__ qa, const uint8_t* __restrict__ w,
     if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
 }
 
+// With FULL (K % 256 == 0, 16-byte aligned operands) the activation blocks
+// are first copied raw into LDS with 16-byte loads, the row's first group of
+// 8 weight blocks (nine 16-byte loads) is issued behind them, and the blocks
+// are parsed from LDS (codes, fp32 scale, code sum) while the weights
+// stream; a lane then takes whole groups of 8 blocks. The parsed codes get
+// 16 bytes of padding per group and the scales and sums one word, so a row's
+// lanes (one group apart) read different LDS banks.
+template <int LPR>
+__global__ void __launch_bounds__(256)
+q4_0_q8_full_kernel(const uint8_t* __restrict__ qa, const uint8_t* __restrict__ w,
+                    float* __restrict__ y, int K, int N) {
+    extern __shared__ uint4 q8s[];
+    const int nbk = K / 32, ngroups = nbk / 8;
+    const int raw16 = nbk * 34 / 16;          // 16-byte units of the activation blocks
+    uint4* raw = q8s;                          // [raw16]
+    uint4* codes = q8s + raw16;                // block bb: uint4 2 bb + bb / 8 (two of them)
+    float* da = reinterpret_cast<float*>(codes + 2 * nbk + ngroups);  // block bb: bb + bb / 8
+    int32_t* csum = reinterpret_cast<int32_t*>(da + nbk + ngroups);
+    const int b = blockIdx.y;
+    const uint4* qa4 = reinterpret_cast<const uint4*>(qa + (int64_t)b * nbk * 34);
+    constexpr int RPB = 256 / LPR;
+    const int row = blockIdx.x * RPB + threadIdx.x / LPR;
+    const int sub = threadIdx.x % LPR;
+    // raw copy: two loads per thread first (past the end: stored to the thread's spare
+    // slot at the end of LDS), then the row's first group
+    const int t = threadIdx.x;
+    const uint4 r0 = qa4[min(t, raw16 - 1)], r1 = qa4[min(t + 256, raw16 - 1)];
+    const uint8_t* rowp = w + (int64_t)min(row, N - 1) * nbk * 18;
+    uint32_t dw[36];
+    auto load_group = [&](int g) {
+        const uint4* p = reinterpret_cast<const uint4*>(rowp + g * 144);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) {
+            const uint4 v = p[i];
+            dw[4 * i] = v.x;
+            dw[4 * i + 1] = v.y;
+            dw[4 * i + 2] = v.z;
+            dw[4 * i + 3] = v.w;
+        }
+    };
+    load_group(min(sub, ngroups - 1));
+    uint4* spare = q8s + raw16 + 2 * nbk + ngroups + ((nbk + ngroups) * 8 + 15) / 16;
+    *(t < raw16 ? raw + t : spare + t) = r0;
+    *(t + 256 < raw16 ? raw + t + 256 : spare + t) = r1;
+    for (int u = t + 512; u < raw16; u += 256) raw[u] = qa4[u];
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // parse: block bb's 34 bytes start at byte 34 bb (word-aligned for even bb, else 2 past)
+    const uint32_t* rw = reinterpret_cast<const uint32_t*>(raw);
+    for (int bb = t; bb < nbk; bb += 256) {
+        const int w0 = (34 * bb) >> 2, sh = (34 * bb) & 3;  // sh: 0 or 2
+        uint32_t x[9];  // the block's bytes 0..33 lie in words w0 .. w0 + 8 either way
+#pragma unroll
+        for (int i = 0; i < 9; ++i) x[i] = rw[w0 + i];
+        const uint32_t dbits = sh ? (x[0] >> 16) : (x[0] & 0xffffu);
+        uint32_t c[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)  // codes: bytes 2 + 4 i .. of the block
+            c[i] = sh ? x[i + 1] : __builtin_amdgcn_alignbyte(x[i + 1], x[i], 2);
+        int cs = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cs = sdot4(c[i], 0x01010101, cs);
+        uint4* cd = codes + 2 * bb + bb / 8;
+        cd[0] = uint4{c[0], c[1], c[2], c[3]};
+        cd[1] = uint4{c[4], c[5], c[6], c[7]};
+        da[bb + bb / 8] = half_bits_to_float((uint16_t)dbits);
+        csum[bb + bb / 8] = cs;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    float acc = 0.0f;
+    if (row < N) {
+        for (int g = sub; g < ngroups; g += LPR) {
+            if (g != sub) load_group(g);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int bb = g * 8 + i, o = 18 * i;  // block i of the group at byte o of dw
+                const uint32_t dbits = (dw[o >> 2] >> (8 * (o & 3))) & 0xffffu;
+                uint32_t q[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const int ob = o + 2 + 4 * m;
+                    q[m] = (ob & 3) == 0 ? dw[ob >> 2]
+                                         : __builtin_amdgcn_alignbyte(dw[(ob >> 2) + 1], dw[ob >> 2], ob & 3);
+                }
+                const uint4 c0 = codes[2 * bb + g], c1 = codes[2 * bb + g + 1];
+                const int32_t cc[8] = {(int32_t)c0.x, (int32_t)c0.y, (int32_t)c0.z, (int32_t)c0.w,
+                                       (int32_t)c1.x, (int32_t)c1.y, (int32_t)c1.z, (int32_t)c1.w};
+                int sdot = 0;
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    sdot = sdot4(q[m] & 0x0f0f0f0fu, cc[m], sdot);          // elements 4m..4m+3
+                    sdot = sdot4((q[m] >> 4) & 0x0f0f0f0fu, cc[4 + m], sdot);  // elements 16+4m..
+                }
+                sdot -= 8 * csum[bb + g];
+                acc = __builtin_fmaf((float)sdot,
+                                     __fmul_rn(half_bits_to_float((uint16_t)dbits), da[bb + g]), acc);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+}
+
 // ------------------------------------------------------------------------
 // GPTQ / AWQ: qweight [K/8][N] u32, lane = output column n (coalesced 256 B
 // per wave per k-octet). Split-K: block (column tile of 256, split s) covers
@@ -1332,9 +1435,28 @@ TENZO_HIP_API int tenzo_hip_gemv_q4_0_q8_0(const uint8_t* qa, const uint8_t* w, 
     const int nbk = K / 32;
     const size_t smem = (size_t)nbk * 10 * 4;
     TZ_CHECK(smem <= 64 * 1024, "gemv_q4_0_q8_0: K=%d too large", K);
+    hipStream_t st = (hipStream_t)stream;
+    if (K % 256 == 0 && ((uintptr_t)qa & 15) == 0 && ((uintptr_t)w & 15) == 0) {
+        // raw blocks, then codes (32 bytes + 16 per group), scales and sums (+ 1 per group),
+        // one spare 16-byte slot per thread
+        const int ng = nbk / 8;
+        const size_t smem_full = (size_t)nbk * 34 + (size_t)(2 * nbk + ng) * 16 +
+                                 ((size_t)(nbk + ng) * 8 + 15) / 16 * 16 + 256 * 16;
+        const int lpr = pick_lpr(ng);
+        dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
+#define Q8F_CASE(L)                                                                         \
+        case L:                                                                             \
+            hipLaunchKernelGGL((q4_0_q8_full_kernel<L>), grid, dim3(256), smem_full, st, qa, \
+                               w, y, K, N);                                                 \
+            break;
+        switch (lpr) {
+            Q8F_CASE(1) Q8F_CASE(2) Q8F_CASE(4) Q8F_CASE(8) Q8F_CASE(16) Q8F_CASE(32) Q8F_CASE(64)
+        }
+#undef Q8F_CASE
+        return launch_status("q4_0_q8_full_kernel");
+    }
     const int lpr = pick_lpr(nbk / 4 > 0 ? nbk / 4 : 1);
     dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
-    hipStream_t st = (hipStream_t)stream;
 #define Q8_CASE(L)                                                                           \
     case L:                                                                                  \
         hipLaunchKernelGGL((q4_0_q8_kernel<L>), grid, dim3(256), smem, st, qa, w, y, K, N); \

@@ -72,7 +72,8 @@ def make_q4(rng, N, K, dense=False):
     return (w, q4_dense(q, d)) if dense else w
 
 
-@pytest.mark.parametrize("N,K", [(64, 32), (100, 256), (11008, 4096), (257, 4128)])
+@pytest.mark.parametrize("N,K", [(64, 32), (100, 256), (11008, 4096), (257, 4128), (72, 2304),
+                                 (40, 8192)])
 def test_q4_0_fp16_and_fp32_activations(torch_dev, N, K):
     from tenzo_amd import ops
     torch = torch_dev
@@ -89,7 +90,8 @@ def test_q4_0_fp16_and_fp32_activations(torch_dev, N, K):
 
 
 @pytest.mark.parametrize("N,K,B", [(64, 32, 1), (100, 288, 2), (11008, 4096, 1),
-                                   (11008, 4096, 8), (257, 4128, 1)])
+                                   (11008, 4096, 8), (257, 4128, 1), (72, 2304, 2),
+                                   (40, 8192, 1), (24, 16384, 1)])
 def test_q8_0_weights(torch_dev, N, K, B):
     """compute_linear_gguf_q8_0 (TenzoEngine.cpp:1078-1114). K = 288 and 4128
     leave rows that are not 16-byte aligned or a partial group of 8 blocks
@@ -111,7 +113,7 @@ def test_q8_0_weights(torch_dev, N, K, B):
     np.testing.assert_array_equal(y32, y)  # the same fp32 activations either way
 
 
-@pytest.mark.parametrize("N,K", [(64, 32), (11008, 4096)])
+@pytest.mark.parametrize("N,K", [(64, 32), (11008, 4096), (100, 2304), (257, 8192), (33, 288)])
 def test_q4_0_q8_0_activations(torch_dev, N, K):
     from tenzo_amd import ops
     torch = torch_dev
