@@ -343,6 +343,9 @@ __device__ __forceinline__ void tl1_finalize(int tot, int64_t m, int64_t row, in
     if (acc_out) acc_out[m * N + row] = v;
 }
 
+constexpr int kTl1J = 16;     // super-chunk loads a lane keeps in flight
+constexpr int kTl1CU = 1024;  // 16-byte units of staged codes (256 super-chunks per block)
+
 __global__ void __launch_bounds__(256)
 tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
                 const tenzo_hip_actq_t* __restrict__ aq, int64_t N, int64_t KS, int splits,
@@ -350,6 +353,7 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
                 int32_t* __restrict__ ws_acc, uint32_t* __restrict__ ws_cnt) {
     __shared__ int red[4][64];
     __shared__ int is_last;
+    __shared__ uint4 cs[kTl1CU + 256];  // codes, then one spare slot per thread
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t nb = N >> 6;
@@ -360,19 +364,40 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
     const int64_t s0 = sp * per;
     const int64_t s1 = s0 + per < KS ? s0 + per : KS;
     const uint4* wb = w + b * KS * 64 + lane;
-    const int32_t* a32 = reinterpret_cast<const int32_t*>(codes + m * KS * 64);
-
-    int acc = 0;
-    int64_t s = s0 + wave;
-    for (; s + 4 < s1; s += 8) {
-        const uint4 v0 = wb[s * 64];
-        const uint4 v1 = wb[(s + 4) * 64];
-        acc = dot16(v0, a32 + s * 16, acc);
-        acc = dot16(v1, a32 + (s + 4) * 16, acc);
+    const uint4* c4 = reinterpret_cast<const uint4*>(codes + m * KS * 64);
+    // the block's activation codes (64 bytes per super-chunk) into LDS first, one 16-byte
+    // load per thread (past the end: into the thread's own spare slot, no branch), so the
+    // dot steps read them as LDS broadcasts instead of one scalar-load round trip per
+    // super-chunk; then the wave's super-chunks s0 + wave + 4 j, all of their weight loads
+    // in flight together (up to kTl1J; beyond, in further rounds)
+    const int cu = (int)(s1 - s0) * 4;  // 16-byte units of the block's codes
+    {
+        const int t = threadIdx.x;
+        const uint4 cv = c4[min(s0, KS - 1) * 4 + max(0, min(t, cu - 1))];  // (empty split: any)
+        const int64_t nj = s1 > s0 + wave ? (s1 - s0 - wave + 3) / 4 : 0;  // wave-uniform
+        uint4 v[kTl1J];
+#pragma unroll
+        for (int j = 0; j < kTl1J; ++j)
+            if (j < nj) v[j] = wb[(s0 + wave + 4 * j) * 64];
+        cs[t < cu ? t : kTl1CU + t] = cv;
+        for (int u = t + 256; u < cu; u += 256) cs[u] = c4[s0 * 4 + u];
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const int32_t* a32 = reinterpret_cast<const int32_t*>(cs);
+        int acc = 0;
+#pragma unroll
+        for (int j = 0; j < kTl1J; ++j)
+            if (j < nj) acc = dot16(v[j], a32 + (wave + 4 * j) * 16, acc);
+        for (int64_t j0 = kTl1J; j0 < nj; j0 += kTl1J) {
+#pragma unroll
+            for (int j = 0; j < kTl1J; ++j)
+                if (j0 + j < nj) v[j] = wb[(s0 + wave + 4 * (j0 + j)) * 64];
+#pragma unroll
+            for (int j = 0; j < kTl1J; ++j)
+                if (j0 + j < nj) acc = dot16(v[j], a32 + (wave + 4 * (j0 + j)) * 16, acc);
+        }
+        red[wave][lane] = acc;
     }
-    if (s < s1) acc = dot16(wb[s * 64], a32 + s * 16, acc);
 
-    red[wave][lane] = acc;
     __syncthreads();
     const int64_t row = b * 64 + lane;
     if (splits == 1) {
@@ -503,14 +528,15 @@ tl1_lut_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ code
 // ------------------------------------------------------------------------
 
 int tl1_pick_splits(int64_t nb, int64_t KS, int64_t M) {
-    // Aim at about one block per CU of the 256, with at least one super-chunk
-    // per wave of every block: each further K split adds the partials'
-    // atomics and the last block's read-back, memory round trips in series
-    // (6912 x 2560: 7.14 us with 10 splits, 5.43 with 3; 2560 x 6912: 9.37 us
-    // with 26, 5.84 with 7).
-    int64_t want = ceil_div(256, nb * M);
-    int64_t cap = KS / 4 > 0 ? KS / 4 : 1;
-    if (want > cap) want = cap;
+    // A block's waves keep all their super-chunk loads in flight, so a block can take
+    // about 28 super-chunks (7 per wave) before a K split pays for its partials' atomics
+    // and the last block's read-back (memory round trips in series); and no more splits
+    // than fill the 256 CUs. Measured per call, splits 1 / 2 / 3 / 4 / 6: 6912 x 2560
+    // 5.08 / 5.47 / 5.54 / 5.70 / 6.21 us; 2560 x 6912 8.92 / 6.85 / 6.03 / 5.86 / 5.96;
+    // 3840 x 2560 4.97 / 5.18 / 5.19 / 5.40 / 5.88.
+    int64_t want = (KS + 14) / 28;
+    const int64_t fill = ceil_div(256, nb * M);
+    if (want > fill) want = fill;
     if (want < 1) want = 1;
     return (int)want;
 }
@@ -569,6 +595,7 @@ int launch_tl1_gemv(const int8_t* codes, const tenzo_hip_actq_t* q, const void* 
     const int64_t KS = ceil_div(K, 64);
     if (splits <= 0) splits = tl1_pick_splits(nb, KS, M);
     if (splits > KS) splits = (int)KS;
+    while (ceil_div(KS, splits) * 4 > kTl1CU) ++splits;  // a block's codes fit the LDS stage
     int32_t* ws_acc = nullptr;
     uint32_t* ws_cnt = nullptr;
     if (splits > 1) {
@@ -692,8 +719,12 @@ TENZO_HIP_API int tenzo_hip_bitlinear_tl1_lut(const int8_t* codes, const tenzo_h
              "bitlinear_tl1_lut: need N %% 64 == 0 (N=%lld)", (long long)N);
     hipStream_t st = (hipStream_t)stream;
     const int64_t nb = N / 64, KS = ceil_div(K, 64);
-    int splits = tl1_pick_splits(nb, KS, M);
-    if (splits > KS) splits = (int)KS;
+    // its own best split: about one block per CU (the table build is per block, so fewer
+    // and longer blocks cost it more than they save: 6912 x 2560 takes 17.8 us with 1
+    // split, 10.0 with 3)
+    int64_t want = ceil_div(256, nb * M);
+    if (want > KS / 4) want = KS / 4;
+    int splits = want < 1 ? 1 : (int)want;
     const int64_t per = ceil_div(KS, splits);
     const size_t lds = (size_t)per * 32 * 16;
     TZ_CHECK(lds <= 64 * 1024, "bitlinear_tl1_lut: K=%lld needs %zu bytes of tables", (long long)K,
