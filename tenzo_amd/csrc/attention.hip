@@ -228,7 +228,16 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
     __syncthreads();
 }
 
-template <int G>
+// The decode chunk kernel. Its arithmetic is chunk_partial's, token for
+// token in the same order (so prefill and decode agree bit for bit), but the
+// loads are arranged for latency: each lane's K and V rows of the chunk (U
+// groups of 8 tokens per wave, U = the chunk's T / 32 rounded up to a power of
+// two; rows past the chunk read its last row and are not used) are issued
+// before anything else, so they stream while q is rotated and the new token
+// appended; the new token's row comes from LDS (its cache row is written by
+// this workgroup in the same launch). With G = 8 the V rows are issued at the
+// start of the value pass instead (the registers hold the eight queries).
+template <int G, int U>
 __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     __shared__ float qs[G][kD];
     __shared__ float sc[G][kMaxChunk];
@@ -237,6 +246,7 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     __shared__ __align__(16) int8_t newk[kD];
     __shared__ __align__(16) int8_t newv[kD];
     __shared__ float news[2];
+    constexpr bool kPreV = G <= 4;
 
     const int c = blockIdx.x;
     const int h = blockIdx.y;
@@ -253,40 +263,83 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     const int nt = t1 - t0;
     const int nchunks = (seq_len + T - 1) / T;
     const float* rope = a.rope + (a.rope_indexed ? (int64_t)pos * kD : 0);
+    const int64_t cache_head = (int64_t)b * a.cache_batch_stride + (int64_t)h * a.max_seq;
+    const int8_t* kbase = a.kc + cache_head * kD;
+    const int8_t* vbase = a.vc + cache_head * kD;
+    const uint16_t* ksb = a.ks + cache_head;
+    const uint16_t* vsb = a.vs + cache_head;
+    const int sub = lane >> 3;       // token within the wave's group of 8
+    const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
+
+    // ---- the queries' loads first (RoPE and the append wait for them alone), then this
+    // lane's K (and V) rows ----
+    constexpr int kQI = (G * 64 + 255) / 256;  // RoPE pairs per thread
+    float qx0[kQI], qx1[kQI], qcs[kQI], qsn[kQI];
+#pragma unroll
+    for (int r = 0; r < kQI; ++r) {
+        const int i = min(tid + 256 * r, G * 64 - 1);
+        const int g = i >> 6, j = i & 63;
+        const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)(h * G + g) * kD;
+        qx0[r] = qv[j];
+        qx1[r] = qv[j + 64];
+        qcs[r] = rope[j];
+        qsn[r] = rope[64 + j];
+    }
+    // the new token's k (wave 0) or v (wave 1) row and its rotation, loaded by every wave
+    // (no branch: waves 2 and 3 load k again and do not use it)
+    const float* nsrc = (wave == 1 ? a.v_new : a.k_new) + (int64_t)b * a.kv_stride + (int64_t)h * kD;
+    const float nx0 = nsrc[lane], nx1 = nsrc[lane + 64];
+    const float ncs = rope[lane], nsn = rope[64 + lane];
+    asm volatile("" ::: "memory");  // (keeps the K / V loads behind those loads)
+    uint4 kr[U], vr[U];
+    uint16_t ksr[U], vsr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
+        kr[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
+        ksr[u] = ksb[t];
+    }
+    if (kPreV) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
+            vr[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
+            vsr[u] = vsb[t];
+        }
+    }
 
     // ---- RoPE on the G query heads (:460-481) ----
-    for (int i = tid; i < G * 64; i += 256) {
-        const int g = i >> 6, j = i & 63;
-        const int qh = h * G + g;
-        const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)qh * kD;
-        const float x0 = qv[j], x1 = qv[j + 64];
-        const float cs = rope[j], sn = rope[64 + j];
-        const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
-        const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
-        qs[g][j] = r0;
-        qs[g][j + 64] = r1;
-        if (a.q_rot && c == 0) {
-            float* qr = a.q_rot + ((int64_t)b * a.Hq + qh) * kD;
-            qr[j] = r0;
-            qr[j + 64] = r1;
+#pragma unroll
+    for (int r = 0; r < kQI; ++r) {
+        const int i = tid + 256 * r;
+        if (i < G * 64) {
+            const int g = i >> 6, j = i & 63;
+            const int qh = h * G + g;
+            const float r0 = __builtin_fmaf(qx0[r], qcs[r], -__fmul_rn(qx1[r], qsn[r]));
+            const float r1 = __builtin_fmaf(qx0[r], qsn[r], __fmul_rn(qx1[r], qcs[r]));
+            qs[g][j] = r0;
+            qs[g][j + 64] = r1;
+            if (a.q_rot && c == 0) {
+                float* qr = a.q_rot + ((int64_t)b * a.Hq + qh) * kD;
+                qr[j] = r0;
+                qr[j + 64] = r1;
+            }
         }
     }
     // ---- new token: RoPE on k, quantize-append k and v (:482-533) ----
     const bool has_new = !a.prefill && pos >= t0 && pos < t1;
-    const int64_t cache_head = (int64_t)b * a.cache_batch_stride + (int64_t)h * a.max_seq;
     if (has_new && wave < 2) {
-        const float* src = (wave == 0 ? a.k_new : a.v_new) + (int64_t)b * a.kv_stride + (int64_t)h * kD;
-        float x0 = src[lane], x1 = src[lane + 64];
+        float x0 = nx0, x1 = nx1;
         if (wave == 0) {
-            const float cs = rope[lane], sn = rope[64 + lane];
+            const float cs = ncs, sn = nsn;
             const float r0 = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
             const float r1 = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
             x0 = r0;
             x1 = r1;
             if (a.k_rot) {
-                float* kr = a.k_rot + ((int64_t)b * a.Hkv + h) * kD;
-                kr[lane] = r0;
-                kr[lane + 64] = r1;
+                float* kr2 = a.k_rot + ((int64_t)b * a.Hkv + h) * kD;
+                kr2[lane] = r0;
+                kr2[lane + 64] = r1;
             }
         }
         float s;
@@ -300,14 +353,117 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
             news[wave] = half_bits_to_float(sh);
         }
     }
-    __syncthreads();
+    // (LDS only: the new row's cache copy is not read back in this launch)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    const int8_t* kbase = a.kc + cache_head * kD;
-    const int8_t* vbase = a.vc + cache_head * kD;
-    const uint16_t* ksb = a.ks + cache_head;
-    const uint16_t* vsb = a.vs + cache_head;
-    chunk_partial<G>(qs, sc, ow, mstat, lstat, kbase, vbase, ksb, vsb, t0, nt, has_new, pos, newk,
-                     newv, news);
+    // ---- scores (:678-694) ----
+    {
+        float qr[G][16];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) qr[g][j] = qs[g][d0 + j];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int tl = wave * 8 + 32 * u + sub;
+            const bool fresh = has_new && t0 + tl == pos;
+            const uint4 kv = fresh ? *reinterpret_cast<const uint4*>(newk + d0) : kr[u];
+            const float skf = fresh ? news[0] : half_bits_to_float(ksr[u]);
+            float kf[16];
+            unpack16(kv, kf);
+            if (tl >= nt) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) kf[j] = 0.0f;
+            }
+            float p[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                float s = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
+                s += dpp_f<kDppXor1>(s);
+                s += dpp_f<kDppXor2>(s);
+                s += dpp_f<kDppHalfMirror>(s);
+                p[g] = s;
+            }
+            if (tl < nt) {
+                const float f = __fmul_rn(skf, kScaleFactor);
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    if ((lane & 7) == (g & 7)) sc[g][tl] = __fmul_rn(p[g], f);
+            }
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- chunk softmax statistics (:824-830) ----
+    for (int g = wave; g < G; g += 4) {
+        float m = -1e30f;
+        for (int i = lane; i < nt; i += 64) m = fmaxf(m, sc[g][i]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int i = lane; i < nt; i += 64) {
+            const float e = expf(sc[g][i] - m);
+            sc[g][i] = e;
+            l += e;
+        }
+        l = wave_sum_tree(l);
+        if (lane == 0) {
+            mstat[g] = m;
+            lstat[g] = l;
+        }
+    }
+    if (!kPreV) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
+            vr[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
+            vsr[u] = vsb[t];
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- weighted values (:842-851) ----
+    float acc[G][16];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int tl = wave * 8 + 32 * u + sub;
+        if (tl < nt) {
+            const bool fresh = has_new && t0 + tl == pos;
+            const uint4 vv = fresh ? *reinterpret_cast<const uint4*>(newv + d0) : vr[u];
+            const float svf = fresh ? news[1] : half_bits_to_float(vsr[u]);
+            float vf[16];
+            unpack16(vv, vf);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float wgt = __fmul_rn(sc[g][tl], svf);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
+            }
+        }
+    }
+    // reduce over the 8 token lanes that share dims (lane bits 3..5)
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            float v = acc[g][j];
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            acc[g][j] = v;
+        }
+    if (lane < 8) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
+    }
+    __syncthreads();
     for (int i = tid; i < G * kD; i += 256) {
         const int g = i >> 7, d = i & 127;
         const float o = (ow[0][g][d] + ow[1][g][d]) + (ow[2][g][d] + ow[3][g][d]);
@@ -659,15 +815,23 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
         if (!a.part) return TENZO_ERROR_OUT_OF_MEMORY;
     }
     dim3 grid(L.max_chunks, L.Hkv, L.B);
-    switch (G) {
-        case 1: hipLaunchKernelGGL(attn_int8_chunk_kernel<1>, grid, dim3(256), 0, st, a); break;
-        case 2: hipLaunchKernelGGL(attn_int8_chunk_kernel<2>, grid, dim3(256), 0, st, a); break;
-        case 4: hipLaunchKernelGGL(attn_int8_chunk_kernel<4>, grid, dim3(256), 0, st, a); break;
-        case 8: hipLaunchKernelGGL(attn_int8_chunk_kernel<8>, grid, dim3(256), 0, st, a); break;
-        default:
-            set_error("attention: query heads per kv head must be 1, 2, 4 or 8 (got %d)", G);
-            return TENZO_ERROR_UNSUPPORTED;
+    if (G != 1 && G != 2 && G != 4 && G != 8) {
+        set_error("attention: query heads per kv head must be 1, 2, 4 or 8 (got %d)", G);
+        return TENZO_ERROR_UNSUPPORTED;
     }
+    if (L.T < 32 || L.T > kMaxChunk || L.T % 32 != 0) {
+        set_error("attention: tokens per chunk must be a multiple of 32 in [32, %d] (got %d)",
+                  kMaxChunk, L.T);
+        return TENZO_ERROR_INVALID_ARGUMENT;
+    }
+    const int U = L.T <= 32 ? 1 : L.T <= 64 ? 2 : L.T <= 128 ? 4 : 8;  // groups of 8 per wave
+#define ATT_CASE(GG, UU)                                                                      \
+    if (G == GG && U == UU)                                                                   \
+        hipLaunchKernelGGL((attn_int8_chunk_kernel<GG, UU>), grid, dim3(256), 0, st, a);
+#define ATT_G(GG) ATT_CASE(GG, 1) ATT_CASE(GG, 2) ATT_CASE(GG, 4) ATT_CASE(GG, 8)
+    ATT_G(1) ATT_G(2) ATT_G(4) ATT_G(8)
+#undef ATT_G
+#undef ATT_CASE
     int rc = launch_status("attn_int8_chunk_kernel");
     if (rc) return rc;
     if (L.max_chunks > 1) {
