@@ -213,8 +213,8 @@ TENZO_HIP_API int tenzo_hip_gemv_q4_0_q8_0(const uint8_t* qa, const uint8_t* w, 
                                            int K, int N, int B, void* stream);
 /* compute_linear_gptq (:1117-1143): qweight [K/8][N] u32, scales [K/g][N],
  * qzeros [ceil(K/g/8)][N] u32 (nibble g%8, zero = nibble + 1). B <= 8
- * rows; 9..16 with 16-byte aligned fp16 activations, K % 1024 == 0,
- * g in {32, 64, 128, 256, 512} and B (K + 4) fp16 within 158 KiB (fp16 MFMA,
+ * rows; 9..16 with 16-byte aligned fp16 activations, K % 512 == 0,
+ * g in {32, 64, 128, 256, 512} and B (K + 4) fp16 within 152 KiB (fp16 MFMA,
  * which also serves batch 4..8 of that form). */
 TENZO_HIP_API int tenzo_hip_gemv_gptq(const void* act, int act_dtype, const uint32_t* qweight,
                                       const void* scales, int scale_dtype,
