@@ -230,9 +230,9 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
 
 // The decode chunk kernel. Its arithmetic is chunk_partial's, token for
 // token in the same order (so prefill and decode agree bit for bit), but the
-// loads are arranged for latency: each lane's K and V rows of the chunk (U
-// groups of 8 tokens per wave, U = the chunk's T / 32 rounded up to a power of
-// two; rows past the chunk read its last row and are not used) are issued
+// loads are arranged for latency: each lane's K and V rows of the chunk (U =
+// T / 32 groups of 8 tokens per wave; rows past the context read the chunk's
+// last row and are not used) are issued
 // before anything else, so they stream while q is rotated and the new token
 // appended; the new token's row comes from LDS (its cache row is written by
 // this workgroup in the same launch). With G = 8 the V rows are issued at the
@@ -824,11 +824,13 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
                   kMaxChunk, L.T);
         return TENZO_ERROR_INVALID_ARGUMENT;
     }
-    const int U = L.T <= 32 ? 1 : L.T <= 64 ? 2 : L.T <= 128 ? 4 : 8;  // groups of 8 per wave
+    const int U = L.T / 32;  // groups of 8 tokens per wave
 #define ATT_CASE(GG, UU)                                                                      \
     if (G == GG && U == UU)                                                                   \
         hipLaunchKernelGGL((attn_int8_chunk_kernel<GG, UU>), grid, dim3(256), 0, st, a);
-#define ATT_G(GG) ATT_CASE(GG, 1) ATT_CASE(GG, 2) ATT_CASE(GG, 4) ATT_CASE(GG, 8)
+#define ATT_G(GG)                                                                             \
+    ATT_CASE(GG, 1) ATT_CASE(GG, 2) ATT_CASE(GG, 3) ATT_CASE(GG, 4) ATT_CASE(GG, 5)           \
+    ATT_CASE(GG, 6) ATT_CASE(GG, 7) ATT_CASE(GG, 8)
     ATT_G(1) ATT_G(2) ATT_G(4) ATT_G(8)
 #undef ATT_G
 #undef ATT_CASE
