@@ -850,17 +850,19 @@ gq_h2_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qwei
 // GPTQ / AWQ with fp16 activations, batch 4..16, on fp16 MFMA
 // (v_mfma_f32_16x16x16_f16): D[m][n] += sum_k A[m][k] (q - z)[k][n] over
 // 16-k steps, the batch rows as M (padded to 16 with zeros) and 16 output
-// columns per wave as N. Each lane builds its B operand, column n = lane % 16
-// at k = 4 (lane / 16) .. +3 of the step, from half a qweight word: the same
-// exact fp16 (q - z) as gq_h2_kernel (byte permute, and-or forming 1024 + q,
-// one packed subtraction of 1024 + z). A group's group / 16 steps go into a
-// fresh accumulator that is scaled once, y += s * sum. The activations are staged
-// in LDS with each k-octet in the qweight word's nibble order (AWQ:
-// k = {0,2,4,6,1,3,5,7}), rows padded by 8 bytes so the 16 rows of an A
-// operand read fall in different banks. A workgroup owns 32 columns: waves
+// columns per wave as N. A lane's B operand is 4 k of column n = lane % 16;
+// lane group kq = lane / 16 takes k-octet 4 jp + kq of each step pair jp, whose
+// one qweight word gives four exact fp16 pairs (q - z) of nibbles (i, i + 4)
+// (a shift, an and-or forming 1024 + q, one packed subtraction of 1024 + z):
+// nibbles (0,4,1,5) for the pair's first step and (2,6,3,7) for its second.
+// The activations are staged in LDS with each k-octet in that order (GPTQ
+// (0,4)(1,5)(2,6)(3,7); AWQ, whose nibble e holds k = {0,2,4,6,1,3,5,7}[e],
+// as it is), rows padded by 8 bytes so the 16 rows of an A operand read fall
+// in different banks. A group's group / 16 steps go into a fresh accumulator
+// that is scaled once, y += s * sum. A workgroup owns 32 columns: waves
 // (tile, part) = (w % 2, w / 2) take 16 columns and one of 4, 2 or 1 parts of
 // K (whole 512-k chunks each), and the parts are added in LDS in part order.
-// Each lane keeps the 32 qweight words of a chunk in flight, the first
+// Each lane keeps the 16 qweight words of a chunk in flight, the first
 // chunk's across the barrier that follows the activation staging. Products
 // are exact and summed in fp32 (the MFMA's own order).
 typedef _Float16 h4v __attribute__((ext_vector_type(4)));
@@ -888,9 +890,9 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
     const int n = blockIdx.x * 32 + tile * 16 + col;
     const int nn = min(n, N - 1);  // columns past N read the last one, not stored
     const int kp = K / parts, ka = part * kp, kb = ka + kp;
-    // this lane's 32 words of a chunk (k-octets kc/8 + 2j + kq/2) and the chunk's group
-    // scales and zeros, all in flight together; the first chunk's before the staging
-    uint32_t qv[kSteps];
+    // this lane's 16 words of a chunk (k-octets kc/8 + 4 jp + kq: one word feeds the step
+    // pair jp) and the chunk's group scales and zeros, all in flight together
+    uint32_t qv[kSteps / 2];
     float sc[kGroups];
     uint32_t zw[kGroups];
     auto load_chunk = [&](int kc) {  // the group scales and zeros first: used first
@@ -901,11 +903,13 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
             zw[gi] = AWQ ? qzeros[(int64_t)g * (N / 8) + nn / 8] : qzeros[(int64_t)(g / 8) * N + nn];
         }
 #pragma unroll
-        for (int j = 0; j < kSteps; ++j)
-            qv[j] = qweight[(int64_t)(kc / 8 + 2 * j + (kq >> 1)) * N + nn];
+        for (int jp = 0; jp < kSteps / 2; ++jp)
+            qv[jp] = qweight[(int64_t)(kc / 8 + 4 * jp + kq) * N + nn];
     };
     // activations first (an L2 hit in a decode step), one k-octet (16 bytes) per thread
-    // and load, four loads in flight, permuted in registers for AWQ; then the first
+    // and load, four loads in flight, each octet in the order of the weight pairs (GPTQ
+    // (0,4)(1,5)(2,6)(3,7); AWQ, whose nibble e holds k = {0,2,4,6,1,3,5,7}[e], as it is);
+    // then the first
     // chunk's loads, which stay in flight across the barrier (s_barrier after the LDS
     // stores alone, no wait for the vector loads)
     const int K8 = K >> 3, octs = B * K8, T = (int)blockDim.x;
@@ -921,9 +925,9 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
             if (i < octs) {
                 const int r = i / K8, o = i - r * K8;
                 uint4 w = v[jj];
-                if (AWQ)  // halves (0,1)(2,3)(4,5)(6,7) -> (0,2)(4,6)(1,3)(5,7)
-                    w = uint4{(w.x & 0xffffu) | (w.y << 16), (w.z & 0xffffu) | (w.w << 16),
-                              (w.x >> 16) | (w.y & 0xffff0000u), (w.z >> 16) | (w.w & 0xffff0000u)};
+                if (!AWQ)  // halves (0,1)(2,3)(4,5)(6,7) -> (0,4)(1,5)(2,6)(3,7)
+                    w = uint4{(w.x & 0xffffu) | (w.z << 16), (w.x >> 16) | (w.z & 0xffff0000u),
+                              (w.y & 0xffffu) | (w.w << 16), (w.y >> 16) | (w.w & 0xffff0000u)};
                 uint2* dst = reinterpret_cast<uint2*>(ah + r * KP) + 2 * o;
                 dst[0] = uint2{w.x, w.y};
                 dst[1] = uint2{w.z, w.w};
@@ -934,8 +938,7 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     const int m = lane & 15;  // A operand row
     const bool arow = m < B;
-    const uint16_t* arp = ah + min(m, B - 1) * KP + 4 * kq;
-    const uint32_t sh = 16u * (uint32_t)(kq & 1);
+    const uint16_t* arp = ah + min(m, B - 1) * KP + 8 * kq;
     uint32_t lo4 = 0x000f000fu, one024 = 0x64006400u;  // VGPR operands of v_and_or_b32
     asm volatile("" : "+v"(lo4), "+v"(one024));
     f4m acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -949,18 +952,20 @@ gq_mfma_kernel(const uint16_t* __restrict__ act, const uint32_t* __restrict__ qw
             const h2v bias = {bz, bz};
             f4m cg = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int jj = 0; jj < NG; ++jj) {
-                const int j = gi * NG + jj;
-                const uint32_t x = qv[j] >> sh, hx = x >> 4;
-                const uint32_t z0 = (__builtin_amdgcn_perm(hx, x, 0x0c040c00u) & lo4) | one024;
-                const uint32_t z1 = (__builtin_amdgcn_perm(hx, x, 0x0c050c01u) & lo4) | one024;
-                const h2v w0 = __builtin_bit_cast(h2v, z0) + bias;
-                const h2v w1 = __builtin_bit_cast(h2v, z1) + bias;
-                const h4v b = {w0.x, w0.y, w1.x, w1.y};
-                h4v a = *reinterpret_cast<const h4v*>(arp + kc + 16 * j);
-                if (!arow)
-                    a = h4v{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-                cg = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, cg, 0, 0, 0);
+            for (int jj = 0; jj < NG / 2; ++jj) {
+                const int jp = gi * (NG / 2) + jj;  // step pair: one word, nibbles (i, i + 4)
+                h2v wd[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    wd[i] = __builtin_bit_cast(h2v, ((qv[jp] >> (4 * i)) & lo4) | one024) + bias;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {  // k of the step: nibbles (0,4,1,5) / (2,6,3,7)
+                    const h4v b = {wd[2 * hh].x, wd[2 * hh].y, wd[2 * hh + 1].x, wd[2 * hh + 1].y};
+                    h4v a = *reinterpret_cast<const h4v*>(arp + kc + 32 * jp + 4 * hh);
+                    if (!arow)
+                        a = h4v{(_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+                    cg = __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, cg, 0, 0, 0);
+                }
             }
             acc += cg * sc[gi];
         }
