@@ -23,6 +23,7 @@
 namespace tz {
 
 constexpr int kD = 128;
+constexpr int kMfmaScoreU = 6;  // chunks of 32 kMfmaScoreU tokens and more score on MFMA
 constexpr float kScaleFactor = 0.08838834764831845f;  // 1/sqrt(128)
 
 // Tokens per chunk for a context of seq_len: ~512 workgroups over the chip,
@@ -74,6 +75,59 @@ __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
     }
 }
 
+// Scores on fp16 MFMA (v_mfma_f32_16x16x16_f16), shared by the decode chunk
+// kernel and the prefill kernel so both give the same bits. A wave takes 16
+// tokens at a time: lane l holds token n = l % 16 of the tile and its dims
+// 32 q .. 32 q + 31 (q = l / 16, 32 bytes of the cache row), and the dims of
+// MFMA step j are {32 q + 4 j + e} (q, e < 4). K codes are exact in fp16
+// (u = k ^ 0x80 placed under the fp16 exponent of 1024, then 1152
+// subtracted); the fp32 query rows are the A operand as two fp16 parts
+// hi = fp16(q), lo = fp16(q - hi), the hi step first. Products are exact and
+// summed in fp32; D row m = head m of the tile's column n, held by lanes
+// 16 (m / 4) .. +15 as element m % 4.
+typedef _Float16 h2a __attribute__((ext_vector_type(2)));
+typedef _Float16 h4a __attribute__((ext_vector_type(4)));
+typedef float f4a __attribute__((ext_vector_type(4)));
+
+// the A operands of the G query heads for this lane (head l % 16, zero past G)
+template <int G>
+__device__ __forceinline__ void q_operands(const float (&qs)[G][kD], h4a (&qh)[8], h4a (&ql)[8]) {
+    const int lane = threadIdx.x & 63, m = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x = m < G ? qs[m < G ? m : 0][32 * q + 4 * j + e] : 0.0f;
+            const _Float16 hi = (_Float16)x;
+            qh[j][e] = hi;
+            ql[j][e] = (_Float16)(x - (float)hi);
+        }
+    }
+}
+
+__device__ __forceinline__ h4a i8x4_h4(uint32_t w) {
+    const uint32_t x = w ^ 0x80808080u;
+    uint32_t e64 = 0x64006400u;  // (a VGPR operand of v_perm_b32)
+    asm volatile("" : "+v"(e64));
+    const h2a bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const h2a p0 = __builtin_bit_cast(h2a, __builtin_amdgcn_perm(e64, x, 0x07010500u)) + bias;
+    const h2a p1 = __builtin_bit_cast(h2a, __builtin_amdgcn_perm(e64, x, 0x07030502u)) + bias;
+    return h4a{p0.x, p0.y, p1.x, p1.y};
+}
+
+__device__ __forceinline__ f4a score_tile(const h4a (&qh)[8], const h4a (&ql)[8],
+                                          const uint4 k0, const uint4 k1) {
+    const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    f4a d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const h4a b = i8x4_h4(kw[j]);
+        d = __builtin_amdgcn_mfma_f32_16x16x16f16(qh[j], b, d, 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_16x16x16f16(ql[j], b, d, 0, 0, 0);
+    }
+    return d;
+}
+
 // KV append quantization (:516-531 as built): s = amax*(1/127), code =
 // clamp(round(x * (127/amax)), -128, 127). 64 lanes x 2 values.
 __device__ __forceinline__ void quant_kv_pair(float x0, float x1, int8_t* codes_out,
@@ -106,15 +160,39 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
                                               const uint16_t* __restrict__ ksb,
                                               const uint16_t* __restrict__ vsb, int t0, int nt,
                                               bool has_new, int pos, const int8_t* newk,
-                                              const int8_t* newv, const float* news) {
+                                              const int8_t* newv, const float* news, bool mfma) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int sub = lane >> 3;       // token within the wave's group of 8
     const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
 
-    // ---- scores (:678-694) ----
-    {
+    // ---- scores (:678-694): on MFMA for chunks of 32 kMfmaScoreU tokens and more, else in
+    // fp32 FMAs (as the decode chunk kernel for the same chunk size) ----
+    if (mfma) {
+        h4a qh[8], ql[8];
+        q_operands<G>(qs, qh, ql);
+        const int kn = lane & 15, kq = lane >> 4;
+        for (int tile = wave; tile * 16 < nt; tile += 4) {
+            const int tl = tile * 16 + kn;
+            const int t = t0 + min(tl, nt - 1);
+            const bool fresh = has_new && t == pos;
+            const int8_t* krow = fresh ? newk : kbase + (int64_t)t * kD;
+            const uint4 k0 = *reinterpret_cast<const uint4*>(krow + 32 * kq);
+            const uint4 k1 = *reinterpret_cast<const uint4*>(krow + 32 * kq + 16);
+            const f4a d = score_tile(qh, ql, k0, k1);
+            if (tl < nt) {
+                const float skf = fresh ? news[0] : half_bits_to_float(ksb[t]);
+                const float f = __fmul_rn(skf, kScaleFactor);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int g = 4 * kq + e;
+                    if (g < G) sc[g][tl] = __fmul_rn(d[e], f);
+                }
+            }
+        }
+    }
+    else {
         float qr[G][16];
 #pragma unroll
         for (int g = 0; g < G; ++g)
@@ -291,13 +369,28 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     const float nx0 = nsrc[lane], nx1 = nsrc[lane + 64];
     const float ncs = rope[lane], nsn = rope[64 + lane];
     asm volatile("" ::: "memory");  // (keeps the K / V loads behind those loads)
-    uint4 kr[U], vr[U];
-    uint16_t ksr[U], vsr[U];
+    // K: on the MFMA path (chunks of 192 tokens and more) in the score tiles' mapping, tile
+    // wave + 4 i of 16 tokens, lane token l % 16, dims 32 (l / 16) ..; else in the value
+    // pass's mapping
+    constexpr bool kMf = U >= kMfmaScoreU;
+    constexpr int NTW = (U + 1) / 2;  // 16-token tiles per wave
+    constexpr int NK = kMf ? NTW : U;
+    const int kn = lane & 15, kq = lane >> 4;
+    uint4 kr[NK][2], vr[U];
+    uint16_t ksr[NK], vsr[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
-        kr[u] = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
-        ksr[u] = ksb[t];
+    for (int i = 0; i < NK; ++i) {
+        if (kMf) {
+            const int t = t0 + min((wave + 4 * i) * 16 + kn, nt - 1);
+            const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + 32 * kq);
+            kr[i][0] = kp[0];
+            kr[i][1] = kp[1];
+            ksr[i] = ksb[t];
+        } else {
+            const int t = t0 + min(wave * 8 + 32 * i + sub, nt - 1);
+            kr[i][0] = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
+            ksr[i] = ksb[t];
+        }
     }
     if (kPreV) {
 #pragma unroll
@@ -356,18 +449,43 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     // (LDS only: the new row's cache copy is not read back in this launch)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    // ---- scores (:678-694) ----
-    {
+    // ---- scores (:678-694) on MFMA ----
+    if (kMf) {
+        h4a qh[8], ql[8];
+        q_operands<G>(qs, qh, ql);
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            const int tile = wave + 4 * i;
+            if (tile * 16 >= nt) break;  // (wave-uniform)
+            const int tl = tile * 16 + kn;
+            const bool fresh = has_new && t0 + tl == pos;
+            uint4 k0 = kr[i][0], k1 = kr[i][1];
+            if (fresh) {
+                k0 = *reinterpret_cast<const uint4*>(newk + 32 * kq);
+                k1 = *reinterpret_cast<const uint4*>(newk + 32 * kq + 16);
+            }
+            const f4a d = score_tile(qh, ql, k0, k1);
+            if (tl < nt) {
+                const float skf = fresh ? news[0] : half_bits_to_float(ksr[i]);
+                const float f = __fmul_rn(skf, kScaleFactor);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int g = 4 * kq + e;
+                    if (g < G) sc[g][tl] = __fmul_rn(d[e], f);
+                }
+            }
+        }
+    } else {  // ---- scores in fp32 FMAs (short chunks: the MFMA prologue would not pay) ----
         float qr[G][16];
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
             for (int j = 0; j < 16; ++j) qr[g][j] = qs[g][d0 + j];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int u = 0; u < NK; ++u) {
             const int tl = wave * 8 + 32 * u + sub;
             const bool fresh = has_new && t0 + tl == pos;
-            const uint4 kv = fresh ? *reinterpret_cast<const uint4*>(newk + d0) : kr[u];
+            const uint4 kv = fresh ? *reinterpret_cast<const uint4*>(newk + d0) : kr[u][0];
             const float skf = fresh ? news[0] : half_bits_to_float(ksr[u]);
             float kf[16];
             unpack16(kv, kf);
@@ -581,7 +699,7 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
         const int nt = min(t0 + T, seq_len) - t0;
         chunk_partial<G>(qs, sc, ow, mstat, lstat, a.kc + cache_head * kD, a.vc + cache_head * kD,
                          a.ks + cache_head, a.vs + cache_head, t0, nt, false, pos, nullptr,
-                         nullptr, nullptr);
+                         nullptr, nullptr, T >= 32 * kMfmaScoreU);
         for (int i = tid; i < G * kD; i += 256) {
             const int g = i >> 7, d = i & 127;
             const float o = (ow[0][g][d] + ow[1][g][d]) + (ow[2][g][d] + ow[3][g][d]);
