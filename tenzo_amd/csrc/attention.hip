@@ -128,6 +128,60 @@ __device__ __forceinline__ f4a score_tile(const h4a (&qh)[8], const h4a (&ql)[8]
     return d;
 }
 
+// Values on fp16 MFMA for the same 16-token tiles: O[g][d] += sum_t W[g][t] V[t][d]
+// with the tile's 16 tokens as the MFMA's k. Lane l = (n, q) = (l % 16, l / 16) holds
+// tokens 4 q .. 4 q + 3 of the tile and dims 8 n .. 8 n + 7 of each (v[e]: 8 bytes of
+// token 4 q + e), and MFMA dt (0..7) takes dim 8 n + dt as its column n, so a lane's
+// 4 x 8 block, transposed in registers (byte permutes), gives its B operands: 4 tokens of
+// one dim, exact in fp16. The A operand is W = p * s_v of head l % 16 at the lane's 4
+// tokens, as fp16 hi + lo parts (the hi MFMA first). acc[dt] row g = D[g][dim 8 n + dt],
+// held by lanes 16 (g / 4) .. +15 as element g % 4.
+__device__ __forceinline__ void value_tile(const h4a (&wh)[1], const h4a (&wl)[1],
+                                           const uint2 (&v)[4], f4a (&acc)[8]) {
+    uint32_t e64 = 0x64006400u;  // (a VGPR operand of v_perm_b32)
+    asm volatile("" : "+v"(e64));
+    const h2a bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {  // dims 4 hf .. 4 hf + 3 of the lane's 8
+        uint32_t x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = (hf ? v[e].y : v[e].x) ^ 0x80808080u;
+        // (token 0, token 1) and (token 2, token 3) interleaved: dims 0, 1 / dims 2, 3
+        const uint32_t t01a = __builtin_amdgcn_perm(x[1], x[0], 0x05010400u);
+        const uint32_t t01b = __builtin_amdgcn_perm(x[1], x[0], 0x07030602u);
+        const uint32_t t23a = __builtin_amdgcn_perm(x[3], x[2], 0x05010400u);
+        const uint32_t t23b = __builtin_amdgcn_perm(x[3], x[2], 0x07030602u);
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+            const uint32_t sel = (f & 1) ? 0x07030502u : 0x07010500u;
+            const h2a p01 =
+                __builtin_bit_cast(h2a, __builtin_amdgcn_perm(e64, f < 2 ? t01a : t01b, sel)) + bias;
+            const h2a p23 =
+                __builtin_bit_cast(h2a, __builtin_amdgcn_perm(e64, f < 2 ? t23a : t23b, sel)) + bias;
+            const h4a b = {p01.x, p01.y, p23.x, p23.y};
+            const int dt = 4 * hf + f;
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(wh[0], b, acc[dt], 0, 0, 0);
+            acc[dt] = __builtin_amdgcn_mfma_f32_16x16x16f16(wl[0], b, acc[dt], 0, 0, 0);
+        }
+    }
+}
+
+// the A operand of a value tile: W[g][t] = p[g][t] * s_v[t] (as the FMA path forms it) of
+// head g = l % 16 at tokens tile * 16 + 4 (l / 16) + e, zero past G or past the chunk
+template <int G>
+__device__ __forceinline__ void w_operands(const float (&sc)[G][kMaxChunk], int tile, int nt,
+                                           const float (&svf)[4], h4a (&wh)[1], h4a (&wl)[1]) {
+    const int lane = threadIdx.x & 63, m = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int tl = tile * 16 + 4 * q + e;
+        const float w = (m < G && tl < nt) ? __fmul_rn(sc[m < G ? m : 0][tl], svf[e]) : 0.0f;
+        const _Float16 hi = (_Float16)w;
+        wh[0][e] = hi;
+        wl[0][e] = (_Float16)(w - (float)hi);
+    }
+}
+
 // KV append quantization (:516-531 as built): s = amax*(1/127), code =
 // clamp(round(x * (127/amax)), -128, 127). 64 lanes x 2 values.
 __device__ __forceinline__ void quant_kv_pair(float x0, float x1, int8_t* codes_out,
@@ -257,51 +311,81 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
     }
     __syncthreads();
 
-    // ---- weighted values (:842-851) ----
-    float acc[G][16];
+    // ---- weighted values (:842-851): on MFMA with the scores (value_tile), else FMAs ----
+    if (mfma) {
+        const int kn = lane & 15, kq = lane >> 4;
+        f4a acc8[8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int tile = wave; tile * 16 < nt; tile += 4) {
+            float svf[4];
+            uint2 v[4];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
-    for (int tb = wave * 8; tb < nt; tb += 32) {
-        const int tl = tb + sub;
-        const int t = t0 + tl;
-        if (tl < nt) {
-            uint4 vv;
-            float svf;
-            if (has_new && t == pos) {
-                vv = *reinterpret_cast<const uint4*>(newv + d0);
-                svf = news[1];
-            } else {
-                vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
-                svf = half_bits_to_float(vsb[t]);
+            for (int e = 0; e < 4; ++e) {
+                const int t = t0 + min(tile * 16 + 4 * kq + e, nt - 1);
+                const bool fresh = has_new && t == pos;
+                const int8_t* vrow = fresh ? newv : vbase + (int64_t)t * kD;
+                v[e] = *reinterpret_cast<const uint2*>(vrow + 8 * kn);
+                svf[e] = fresh ? news[1] : half_bits_to_float(vsb[t]);
             }
-            float vf[16];
-            unpack16(vv, vf);
+            h4a wh[1], wl[1];
+            w_operands<G>(sc, tile, nt, svf, wh, wl);
+            value_tile(wh, wl, v, acc8);
+        }
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float wgt = __fmul_rn(sc[g][tl], svf);
+        for (int e = 0; e < 4; ++e) {
+            const int g = 4 * kq + e;
+            if (g < G) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
+                for (int dt = 0; dt < 8; ++dt) ow[wave][g][8 * kn + dt] = acc8[dt][e];
             }
         }
-    }
-    // reduce over the 8 token lanes that share dims (lane bits 3..5)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            float v = acc[g][j];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            acc[g][j] = v;
-        }
-    if (lane < 8) {
+    } else {
+        float acc[G][16];
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
+            for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+        for (int tb = wave * 8; tb < nt; tb += 32) {
+            const int tl = tb + sub;
+            const int t = t0 + tl;
+            if (tl < nt) {
+                uint4 vv;
+                float svf;
+                if (has_new && t == pos) {
+                    vv = *reinterpret_cast<const uint4*>(newv + d0);
+                    svf = news[1];
+                } else {
+                    vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
+                    svf = half_bits_to_float(vsb[t]);
+                }
+                float vf[16];
+                unpack16(vv, vf);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float wgt = __fmul_rn(sc[g][tl], svf);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
+                }
+            }
+        }
+        // reduce over the 8 token lanes that share dims (lane bits 3..5)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                float v = acc[g][j];
+                v += __shfl_xor(v, 8, 64);
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                acc[g][j] = v;
+            }
+        if (lane < 8) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
+        }
     }
     __syncthreads();
 }
@@ -392,7 +476,20 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
             ksr[i] = ksb[t];
         }
     }
-    if (kPreV) {
+    // V: on the MFMA path in the value tiles' mapping (lane: tokens 4 (l / 16) .. +3 of the
+    // tile, dims 8 (l % 16) .. +7), else in the FMA pass's
+    uint2 vm[kMf ? NTW : 1][4];
+    uint16_t vms[kMf ? NTW : 1][4];
+    if (kMf) {
+#pragma unroll
+        for (int i = 0; i < NTW; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = t0 + min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1);
+                vm[i][e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)t * kD + 8 * kn);
+                vms[i][e] = vsb[t];
+            }
+    } else if (kPreV) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
@@ -531,7 +628,7 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
             lstat[g] = l;
         }
     }
-    if (!kPreV) {
+    if (!kPreV && !kMf) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
@@ -542,44 +639,74 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // ---- weighted values (:842-851) ----
-    float acc[G][16];
+    if (kMf) {  // on MFMA, tile by tile (value_tile)
+        f4a acc8[8];
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+        for (int i = 0; i < NTW; ++i) {
+            const int tile = wave + 4 * i;
+            if (tile * 16 >= nt) break;  // (wave-uniform)
+            float svf[4];
+            uint2 v[4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const int tl = wave * 8 + 32 * u + sub;
-        if (tl < nt) {
-            const bool fresh = has_new && t0 + tl == pos;
-            const uint4 vv = fresh ? *reinterpret_cast<const uint4*>(newv + d0) : vr[u];
-            const float svf = fresh ? news[1] : half_bits_to_float(vsr[u]);
-            float vf[16];
-            unpack16(vv, vf);
+            for (int e = 0; e < 4; ++e) {
+                const bool fresh = has_new && t0 + tile * 16 + 4 * kq + e == pos;
+                v[e] = fresh ? *reinterpret_cast<const uint2*>(newv + 8 * kn) : vm[i][e];
+                svf[e] = fresh ? news[1] : half_bits_to_float(vms[i][e]);
+            }
+            h4a wh[1], wl[1];
+            w_operands<G>(sc, tile, nt, svf, wh, wl);
+            value_tile(wh, wl, v, acc8);
+        }
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const float wgt = __fmul_rn(sc[g][tl], svf);
+        for (int e = 0; e < 4; ++e) {
+            const int g = 4 * kq + e;
+            if (g < G) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
+                for (int dt = 0; dt < 8; ++dt) ow[wave][g][8 * kn + dt] = acc8[dt][e];
             }
         }
-    }
-    // reduce over the 8 token lanes that share dims (lane bits 3..5)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            float v = acc[g][j];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            acc[g][j] = v;
-        }
-    if (lane < 8) {
+    } else {
+        float acc[G][16];
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
+            for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int tl = wave * 8 + 32 * u + sub;
+            if (tl < nt) {
+                const bool fresh = has_new && t0 + tl == pos;
+                const uint4 vv = fresh ? *reinterpret_cast<const uint4*>(newv + d0) : vr[u];
+                const float svf = fresh ? news[1] : half_bits_to_float(vsr[u]);
+                float vf[16];
+                unpack16(vv, vf);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float wgt = __fmul_rn(sc[g][tl], svf);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
+                }
+            }
+        }
+        // reduce over the 8 token lanes that share dims (lane bits 3..5)
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                float v = acc[g][j];
+                v += __shfl_xor(v, 8, 64);
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                acc[g][j] = v;
+            }
+        if (lane < 8) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
+        }
     }
     __syncthreads();
     for (int i = tid; i < G * kD; i += 256) {
