@@ -11,9 +11,10 @@
 // and the chunk partials (m, l, o) are merged by a combine kernel
 // (out = sum_c e^{m_c - M} o_c / sum_c e^{m_c - M} l_c).
 //
-// Lane mapping (both passes): a wave takes 8 tokens at a time; lane l reads
-// 16 bytes = dims (l%8)*16 .. +15 of token l/8, so one wave load is 1 KiB of
-// contiguous cache rows.
+// Scores and values run on fp16 MFMA over tiles of 16 tokens (score_tile,
+// value_tile below): K and V codes are exact in fp16, the fp32 query rows and
+// weights enter as fp16 hi + lo pairs. A wave takes tiles wave, wave + 4, ...;
+// every wave load covers whole 128-byte cache rows.
 #include <algorithm>
 #include <mutex>
 
@@ -23,7 +24,6 @@
 namespace tz {
 
 constexpr int kD = 128;
-constexpr int kMfmaScoreU = 6;  // chunks of 32 kMfmaScoreU tokens and more score on MFMA
 constexpr float kScaleFactor = 0.08838834764831845f;  // 1/sqrt(128)
 
 // Tokens per chunk for a context of seq_len: ~512 workgroups over the chip,
@@ -81,28 +81,53 @@ __device__ __forceinline__ void unpack16(const uint4 v, float* f) {
 // 32 q .. 32 q + 31 (q = l / 16, 32 bytes of the cache row), and the dims of
 // MFMA step j are {32 q + 4 j + e} (q, e < 4). K codes are exact in fp16
 // (u = k ^ 0x80 placed under the fp16 exponent of 1024, then 1152
-// subtracted); the fp32 query rows are the A operand as two fp16 parts
-// hi = fp16(q), lo = fp16(q - hi), the hi step first. Products are exact and
+// subtracted); the fp32 query rows are the A operand as two fp16 parts of
+// q' = q 2^e (e per head, so that its largest |q'| is in [2^13, 2^14) and the
+// parts stay normal numbers): hi = fp16(q'), lo = fp16(q' - hi), the hi step
+// first, and the sums are scaled back by 2^-e (exact). Products are exact and
 // summed in fp32; D row m = head m of the tile's column n, held by lanes
 // 16 (m / 4) .. +15 as element m % 4.
 typedef _Float16 h2a __attribute__((ext_vector_type(2)));
 typedef _Float16 h4a __attribute__((ext_vector_type(4)));
 typedef float f4a __attribute__((ext_vector_type(4)));
 
-// the A operands of the G query heads for this lane (head l % 16, zero past G)
+// The exponent that brings a magnitude up to [2^13, 2^14): x * 2^e then stays
+// below fp16's largest finite value and its fp16 remainder x * 2^e - hi stays a
+// normal number down to ~1.5e-5 of the magnitude (fp16 subnormals would lose it).
+__device__ __forceinline__ int fp16_span_exp(float mx) {
+    if (!(mx > 0.0f)) return 0;
+    int E;
+    (void)frexpf(mx, &E);  // mx = f 2^E, f in [0.5, 1)
+    return min(14 - E, 100);
+}
+
+// the A operands of the G query heads for this lane (head l % 16, zero past G), each
+// head scaled by a power of two (fp16_span_exp of its largest |q|); qin[e] = the inverse
+// scale of D row 4 (l / 16) + e (the head of lane 4 (l / 16) + e)
 template <int G>
-__device__ __forceinline__ void q_operands(const float (&qs)[G][kD], h4a (&qh)[8], h4a (&ql)[8]) {
+__device__ __forceinline__ void q_operands(const float (&qs)[G][kD], h4a (&qh)[8], h4a (&ql)[8],
+                                           float (&qin)[4]) {
     const int lane = threadIdx.x & 63, m = lane & 15, q = lane >> 4;
+    const float* qrow = &qs[m < G ? m : 0][32 * q];
+    float mx = 0.0f;  // (two passes over the LDS row keep 32 registers free)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(qrow[i]));
+    mx = m < G ? mx : 0.0f;
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const int sh = fp16_span_exp(mx);
+    const float up = ldexpf(1.0f, sh), down = ldexpf(1.0f, -sh);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const float x = m < G ? qs[m < G ? m : 0][32 * q + 4 * j + e] : 0.0f;
-            const _Float16 hi = (_Float16)x;
+            const float xs = (m < G ? qrow[4 * j + e] : 0.0f) * up;  // (exact: a power of two)
+            const _Float16 hi = (_Float16)xs;
             qh[j][e] = hi;
-            ql[j][e] = (_Float16)(x - (float)hi);
+            ql[j][e] = (_Float16)(xs - (float)hi);
         }
-    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qin[e] = __shfl(down, 4 * q + e, 64);
 }
 
 __device__ __forceinline__ h4a i8x4_h4(uint32_t w) {
@@ -134,8 +159,9 @@ __device__ __forceinline__ f4a score_tile(const h4a (&qh)[8], const h4a (&ql)[8]
 // token 4 q + e), and MFMA dt (0..7) takes dim 8 n + dt as its column n, so a lane's
 // 4 x 8 block, transposed in registers (byte permutes), gives its B operands: 4 tokens of
 // one dim, exact in fp16. The A operand is W = p * s_v of head l % 16 at the lane's 4
-// tokens, as fp16 hi + lo parts (the hi MFMA first). acc[dt] row g = D[g][dim 8 n + dt],
-// held by lanes 16 (g / 4) .. +15 as element g % 4.
+// tokens, scaled by a power of two per wave and split into fp16 hi + lo parts (the hi
+// MFMA first). acc[dt] row g = D[g][dim 8 n + dt], held by lanes 16 (g / 4) .. +15 as
+// element g % 4.
 __device__ __forceinline__ void value_tile(const h4a (&wh)[1], const h4a (&wl)[1],
                                            const uint2 (&v)[4], f4a (&acc)[8]) {
     uint32_t e64 = 0x64006400u;  // (a VGPR operand of v_perm_b32)
@@ -166,16 +192,20 @@ __device__ __forceinline__ void value_tile(const h4a (&wh)[1], const h4a (&wl)[1
     }
 }
 
-// the A operand of a value tile: W[g][t] = p[g][t] * s_v[t] (as the FMA path forms it) of
-// head g = l % 16 at tokens tile * 16 + 4 (l / 16) + e, zero past G or past the chunk
+// the A operand of a value tile: W[g][t] = p[g][t] * s_v[t] of head g = l % 16 at tokens
+// tile * 16 + 4 (l / 16) + e, zero past G or past the chunk, scaled by 2^wsh (a power of
+// two that keeps the wave's largest s_v, and so every W of its tiles, within fp16's
+// normal span)
 template <int G>
 __device__ __forceinline__ void w_operands(const float (&sc)[G][kMaxChunk], int tile, int nt,
-                                           const float (&svf)[4], h4a (&wh)[1], h4a (&wl)[1]) {
+                                           const float (&svf)[4], float wup, h4a (&wh)[1],
+                                           h4a (&wl)[1]) {
     const int lane = threadIdx.x & 63, m = lane & 15, q = lane >> 4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int tl = tile * 16 + 4 * q + e;
-        const float w = (m < G && tl < nt) ? __fmul_rn(sc[m < G ? m : 0][tl], svf[e]) : 0.0f;
+        const float w =
+            (m < G && tl < nt) ? __fmul_rn(sc[m < G ? m : 0][tl], svf[e]) * wup : 0.0f;
         const _Float16 hi = (_Float16)w;
         wh[0][e] = hi;
         wl[0][e] = (_Float16)(w - (float)hi);
@@ -214,19 +244,17 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
                                               const uint16_t* __restrict__ ksb,
                                               const uint16_t* __restrict__ vsb, int t0, int nt,
                                               bool has_new, int pos, const int8_t* newk,
-                                              const int8_t* newv, const float* news, bool mfma) {
+                                              const int8_t* newv, const float* news) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int sub = lane >> 3;       // token within the wave's group of 8
-    const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
+    const int kn = lane & 15, kq = lane >> 4;
 
-    // ---- scores (:678-694): on MFMA for chunks of 32 kMfmaScoreU tokens and more, else in
-    // fp32 FMAs (as the decode chunk kernel for the same chunk size) ----
-    if (mfma) {
+    // ---- scores (:678-694) on MFMA (score_tile) ----
+    {
         h4a qh[8], ql[8];
-        q_operands<G>(qs, qh, ql);
-        const int kn = lane & 15, kq = lane >> 4;
+        float qin[4];
+        q_operands<G>(qs, qh, ql, qin);
         for (int tile = wave; tile * 16 < nt; tile += 4) {
             const int tl = tile * 16 + kn;
             const int t = t0 + min(tl, nt - 1);
@@ -241,52 +269,8 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int g = 4 * kq + e;
-                    if (g < G) sc[g][tl] = __fmul_rn(d[e], f);
+                    if (g < G) sc[g][tl] = __fmul_rn(d[e] * qin[e], f);
                 }
-            }
-        }
-    }
-    else {
-        float qr[G][16];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) qr[g][j] = qs[g][d0 + j];
-        for (int tb = wave * 8; tb < nt; tb += 32) {
-            const int tl = tb + sub;
-            const int t = t0 + tl;
-            float kf[16];
-            float skf = 0.0f;
-            if (tl < nt) {
-                uint4 kv;
-                if (has_new && t == pos) {
-                    kv = *reinterpret_cast<const uint4*>(newk + d0);
-                    skf = news[0];
-                } else {
-                    kv = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
-                    skf = half_bits_to_float(ksb[t]);
-                }
-                unpack16(kv, kf);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) kf[j] = 0.0f;
-            }
-            float p[G];
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float s = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
-                s += dpp_f<kDppXor1>(s);
-                s += dpp_f<kDppXor2>(s);
-                s += dpp_f<kDppHalfMirror>(s);
-                p[g] = s;
-            }
-            if (tl < nt) {
-                const float f = __fmul_rn(skf, kScaleFactor);
-#pragma unroll
-                for (int g = 0; g < G; ++g)
-                    if ((lane & 7) == (g & 7)) sc[g][tl] = __fmul_rn(p[g], f);
             }
         }
     }
@@ -311,9 +295,18 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
     }
     __syncthreads();
 
-    // ---- weighted values (:842-851): on MFMA with the scores (value_tile), else FMAs ----
-    if (mfma) {
-        const int kn = lane & 15, kq = lane >> 4;
+    // ---- weighted values (:842-851) on MFMA (value_tile) ----
+    {
+        // the wave's largest V scale over its tiles' tokens sets its power-of-two scale
+        float vmax = 0.0f;
+        for (int tile = wave; tile * 16 < nt; tile += 4)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = t0 + min(tile * 16 + 4 * kq + e, nt - 1);
+                vmax = fmaxf(vmax, has_new && t == pos ? news[1] : half_bits_to_float(vsb[t]));
+            }
+        const int wsh = fp16_span_exp(wave_max(vmax));
+        const float wup = ldexpf(1.0f, wsh), wdown = ldexpf(1.0f, -wsh);
         f4a acc8[8];
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
@@ -329,7 +322,7 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
                 svf[e] = fresh ? news[1] : half_bits_to_float(vsb[t]);
             }
             h4a wh[1], wl[1];
-            w_operands<G>(sc, tile, nt, svf, wh, wl);
+            w_operands<G>(sc, tile, nt, svf, wup, wh, wl);
             value_tile(wh, wl, v, acc8);
         }
 #pragma unroll
@@ -337,70 +330,23 @@ __device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&
             const int g = 4 * kq + e;
             if (g < G) {
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt) ow[wave][g][8 * kn + dt] = acc8[dt][e];
+                for (int dt = 0; dt < 8; ++dt) ow[wave][g][8 * kn + dt] = acc8[dt][e] * wdown;
             }
-        }
-    } else {
-        float acc[G][16];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
-        for (int tb = wave * 8; tb < nt; tb += 32) {
-            const int tl = tb + sub;
-            const int t = t0 + tl;
-            if (tl < nt) {
-                uint4 vv;
-                float svf;
-                if (has_new && t == pos) {
-                    vv = *reinterpret_cast<const uint4*>(newv + d0);
-                    svf = news[1];
-                } else {
-                    vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
-                    svf = half_bits_to_float(vsb[t]);
-                }
-                float vf[16];
-                unpack16(vv, vf);
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float wgt = __fmul_rn(sc[g][tl], svf);
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
-                }
-            }
-        }
-        // reduce over the 8 token lanes that share dims (lane bits 3..5)
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                float v = acc[g][j];
-                v += __shfl_xor(v, 8, 64);
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
-                acc[g][j] = v;
-            }
-        if (lane < 8) {
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
         }
     }
     __syncthreads();
 }
 
-// The decode chunk kernel. Its arithmetic is chunk_partial's, token for
-// token in the same order (so prefill and decode agree bit for bit), but the
-// loads are arranged for latency: each lane's K and V rows of the chunk (U =
-// T / 32 groups of 8 tokens per wave; rows past the context read the chunk's
-// last row and are not used) are issued
-// before anything else, so they stream while q is rotated and the new token
-// appended; the new token's row comes from LDS (its cache row is written by
-// this workgroup in the same launch). With G = 8 the V rows are issued at the
-// start of the value pass instead (the registers hold the eight queries).
+// The decode chunk kernel. Its arithmetic is chunk_partial's, tile for tile in
+// the same order (so prefill and decode agree bit for bit), but the loads are
+// arranged for latency: each lane's K and V rows of the chunk (U = T / 32, so
+// (U + 1) / 2 tiles of 16 tokens per wave; rows past the context read the
+// chunk's last row and are not used) are issued right after the query loads,
+// so they stream while q is rotated and the new token appended; the new
+// token's row comes from LDS (its cache row is written by this workgroup in
+// the same launch).
 template <int G, int U>
-__global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  // (3 waves per SIMD)
     __shared__ float qs[G][kD];
     __shared__ float sc[G][kMaxChunk];
     __shared__ float ow[4][G][kD];
@@ -408,7 +354,6 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     __shared__ __align__(16) int8_t newk[kD];
     __shared__ __align__(16) int8_t newv[kD];
     __shared__ float news[2];
-    constexpr bool kPreV = G <= 4;
 
     const int c = blockIdx.x;
     const int h = blockIdx.y;
@@ -430,8 +375,6 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     const int8_t* vbase = a.vc + cache_head * kD;
     const uint16_t* ksb = a.ks + cache_head;
     const uint16_t* vsb = a.vs + cache_head;
-    const int sub = lane >> 3;       // token within the wave's group of 8
-    const int d0 = (lane & 7) * 16;  // first of this lane's 16 dims
 
     // ---- the queries' loads first (RoPE and the append wait for them alone), then this
     // lane's K (and V) rows ----
@@ -453,50 +396,30 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     const float nx0 = nsrc[lane], nx1 = nsrc[lane + 64];
     const float ncs = rope[lane], nsn = rope[64 + lane];
     asm volatile("" ::: "memory");  // (keeps the K / V loads behind those loads)
-    // K: on the MFMA path (chunks of 192 tokens and more) in the score tiles' mapping, tile
-    // wave + 4 i of 16 tokens, lane token l % 16, dims 32 (l / 16) ..; else in the value
-    // pass's mapping
-    constexpr bool kMf = U >= kMfmaScoreU;
+    // K and V in the tiles' mappings (tile wave + 4 i of 16 tokens): K lane token l % 16,
+    // dims 32 (l / 16) ..; V lane tokens 4 (l / 16) .. +3, dims 8 (l % 16) .. +7
     constexpr int NTW = (U + 1) / 2;  // 16-token tiles per wave
-    constexpr int NK = kMf ? NTW : U;
     const int kn = lane & 15, kq = lane >> 4;
-    uint4 kr[NK][2], vr[U];
-    uint16_t ksr[NK], vsr[U];
+    uint4 kr[NTW][2];
+    uint16_t ksr[NTW];
 #pragma unroll
-    for (int i = 0; i < NK; ++i) {
-        if (kMf) {
-            const int t = t0 + min((wave + 4 * i) * 16 + kn, nt - 1);
-            const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + 32 * kq);
-            kr[i][0] = kp[0];
-            kr[i][1] = kp[1];
-            ksr[i] = ksb[t];
-        } else {
-            const int t = t0 + min(wave * 8 + 32 * i + sub, nt - 1);
-            kr[i][0] = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
-            ksr[i] = ksb[t];
-        }
+    for (int i = 0; i < NTW; ++i) {
+        const int t = t0 + min((wave + 4 * i) * 16 + kn, nt - 1);
+        const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + 32 * kq);
+        kr[i][0] = kp[0];
+        kr[i][1] = kp[1];
+        ksr[i] = ksb[t];
     }
-    // V: on the MFMA path in the value tiles' mapping (lane: tokens 4 (l / 16) .. +3 of the
-    // tile, dims 8 (l % 16) .. +7), else in the FMA pass's
-    uint2 vm[kMf ? NTW : 1][4];
-    uint16_t vms[kMf ? NTW : 1][4];
-    if (kMf) {
+    uint2 vm[NTW][4];
+    uint16_t vms[NTW][4];
 #pragma unroll
-        for (int i = 0; i < NTW; ++i)
+    for (int i = 0; i < NTW; ++i)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = t0 + min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1);
-                vm[i][e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)t * kD + 8 * kn);
-                vms[i][e] = vsb[t];
-            }
-    } else if (kPreV) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
-            vr[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
-            vsr[u] = vsb[t];
+        for (int e = 0; e < 4; ++e) {
+            const int t = t0 + min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1);
+            vm[i][e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)t * kD + 8 * kn);
+            vms[i][e] = vsb[t];
         }
-    }
 
     // ---- RoPE on the G query heads (:460-481) ----
 #pragma unroll
@@ -547,9 +470,10 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // ---- scores (:678-694) on MFMA ----
-    if (kMf) {
+    {
         h4a qh[8], ql[8];
-        q_operands<G>(qs, qh, ql);
+        float qin[4];
+        q_operands<G>(qs, qh, ql, qin);
 #pragma unroll
         for (int i = 0; i < NTW; ++i) {
             const int tile = wave + 4 * i;
@@ -568,44 +492,8 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int g = 4 * kq + e;
-                    if (g < G) sc[g][tl] = __fmul_rn(d[e], f);
+                    if (g < G) sc[g][tl] = __fmul_rn(d[e] * qin[e], f);
                 }
-            }
-        }
-    } else {  // ---- scores in fp32 FMAs (short chunks: the MFMA prologue would not pay) ----
-        float qr[G][16];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) qr[g][j] = qs[g][d0 + j];
-#pragma unroll
-        for (int u = 0; u < NK; ++u) {
-            const int tl = wave * 8 + 32 * u + sub;
-            const bool fresh = has_new && t0 + tl == pos;
-            const uint4 kv = fresh ? *reinterpret_cast<const uint4*>(newk + d0) : kr[u][0];
-            const float skf = fresh ? news[0] : half_bits_to_float(ksr[u]);
-            float kf[16];
-            unpack16(kv, kf);
-            if (tl >= nt) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) kf[j] = 0.0f;
-            }
-            float p[G];
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float s = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
-                s += dpp_f<kDppXor1>(s);
-                s += dpp_f<kDppXor2>(s);
-                s += dpp_f<kDppHalfMirror>(s);
-                p[g] = s;
-            }
-            if (tl < nt) {
-                const float f = __fmul_rn(skf, kScaleFactor);
-#pragma unroll
-                for (int g = 0; g < G; ++g)
-                    if ((lane & 7) == (g & 7)) sc[g][tl] = __fmul_rn(p[g], f);
             }
         }
     }
@@ -628,18 +516,24 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
             lstat[g] = l;
         }
     }
-    if (!kPreV && !kMf) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int t = t0 + min(wave * 8 + 32 * u + sub, nt - 1);
-            vr[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0);
-            vsr[u] = vsb[t];
-        }
-    }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // ---- weighted values (:842-851) ----
-    if (kMf) {  // on MFMA, tile by tile (value_tile)
+    {  // on MFMA, tile by tile (value_tile)
+        // the wave's largest V scale over its tiles' tokens sets its power-of-two scale
+        float vmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            if ((wave + 4 * i) * 16 >= nt) break;  // (wave-uniform)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool vfresh =
+                    has_new && t0 + min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1) == pos;
+                vmax = fmaxf(vmax, vfresh ? news[1] : half_bits_to_float(vms[i][e]));
+            }
+        }
+        const int wsh = fp16_span_exp(wave_max(vmax));
+        const float wup = ldexpf(1.0f, wsh), wdown = ldexpf(1.0f, -wsh);
         f4a acc8[8];
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
@@ -656,7 +550,7 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
                 svf[e] = fresh ? news[1] : half_bits_to_float(vms[i][e]);
             }
             h4a wh[1], wl[1];
-            w_operands<G>(sc, tile, nt, svf, wh, wl);
+            w_operands<G>(sc, tile, nt, svf, wup, wh, wl);
             value_tile(wh, wl, v, acc8);
         }
 #pragma unroll
@@ -664,48 +558,8 @@ __global__ void __launch_bounds__(256) attn_int8_chunk_kernel(AttnArgs a) {
             const int g = 4 * kq + e;
             if (g < G) {
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt) ow[wave][g][8 * kn + dt] = acc8[dt][e];
+                for (int dt = 0; dt < 8; ++dt) ow[wave][g][8 * kn + dt] = acc8[dt][e] * wdown;
             }
-        }
-    } else {
-        float acc[G][16];
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int tl = wave * 8 + 32 * u + sub;
-            if (tl < nt) {
-                const bool fresh = has_new && t0 + tl == pos;
-                const uint4 vv = fresh ? *reinterpret_cast<const uint4*>(newv + d0) : vr[u];
-                const float svf = fresh ? news[1] : half_bits_to_float(vsr[u]);
-                float vf[16];
-                unpack16(vv, vf);
-#pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float wgt = __fmul_rn(sc[g][tl], svf);
-#pragma unroll
-                    for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
-                }
-            }
-        }
-        // reduce over the 8 token lanes that share dims (lane bits 3..5)
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                float v = acc[g][j];
-                v += __shfl_xor(v, 8, 64);
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
-                acc[g][j] = v;
-            }
-        if (lane < 8) {
-#pragma unroll
-            for (int g = 0; g < G; ++g)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) ow[wave][g][d0 + j] = acc[g][j];
         }
     }
     __syncthreads();
@@ -826,7 +680,7 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
         const int nt = min(t0 + T, seq_len) - t0;
         chunk_partial<G>(qs, sc, ow, mstat, lstat, a.kc + cache_head * kD, a.vc + cache_head * kD,
                          a.ks + cache_head, a.vs + cache_head, t0, nt, false, pos, nullptr,
-                         nullptr, nullptr, T >= 32 * kMfmaScoreU);
+                         nullptr, nullptr);
         for (int i = tid; i < G * kD; i += 256) {
             const int g = i >> 7, d = i & 127;
             const float o = (ow[0][g][d] + ow[1][g][d]) + (ow[2][g][d] + ow[3][g][d]);
