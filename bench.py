@@ -364,6 +364,17 @@ def prefill_bench(torch, e, cfg, host, args):
         e.prefill_batch(toks)  # streaming attention; returns after the device finished
         times.append(time.perf_counter() - t0)
     dt = float(np.median(times))
+    # the exact form (chunked attention, bit for bit the per-token kernels' results)
+    e.rewind(0)
+    e.prefill_batch(toks, exact=True)
+    xt = []
+    for _ in range(args.steps):
+        e.rewind(0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e.prefill_batch(toks, exact=True)
+        xt.append(time.perf_counter() - t0)
+    dt_exact = float(np.median(xt))
     # the reference's way: one prefill_token per prompt token (persistent kernel)
     seq_n = min(n, 64)
     e.rewind(0)
@@ -385,6 +396,7 @@ def prefill_bench(torch, e, cfg, host, args):
         "config": {"workload": f"BitNet-b1.58-2B-shaped prompt prefill, {n} tokens from "
                                "position 0, batch 1 (tenzo_hip_engine_prefill)",
                    "prompt_tokens": n, "rows_per_pass": 512},
+        "exact_tok_s": round(n / dt_exact, 1),
         "token_by_token_tok_s": round(seq_rate, 1),
         "speedup_vs_token_by_token": round(n / dt / seq_rate, 1),
         "roofline": {"bound": "mfma", "kernel": "tl1_mfma_kernel (gate|up projection)",

@@ -66,15 +66,6 @@ struct AttnArgs {
     float* k_rot;        // optional
 };
 
-__device__ __forceinline__ void unpack16(const uint4 v, float* f) {
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) f[4 * i + j] = (float)(int8_t)((w[i] >> (8 * j)) & 0xff);
-    }
-}
-
 // Scores on fp16 MFMA (v_mfma_f32_16x16x16_f16), shared by the decode chunk
 // kernel and the prefill kernel so both give the same bits. A wave takes 16
 // tokens at a time: lane l holds token n = l % 16 of the tile and its dims
@@ -715,139 +706,183 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
     }
 }
 
-// Prefill attention, streaming form: one wave per (query row b, kv head h)
-// walks the query's causal prefix in blocks of 64 tokens with an online
-// softmax (running max m, sum l and value sums, rescaled when m grows). The
-// lane mapping is the decode kernel's: lane l holds dims (l%8)*16 .. +15 of
-// token l/8 of each group of 8, so one wave load is 1 KiB of cache rows and
-// the 8 lanes of a token finish its dot product with three DPP adds. The
-// scores, scales and exponentials are those of the decode kernel; only the
-// grouping of the softmax sums differs (fp32, well inside 1e-3). Four waves =
-// four consecutive queries of one kv head, whose K/V reads overlap in L1.
+// Prefill attention on fp16 MFMA, streaming form (an online softmax over the
+// causal prefix): a workgroup takes QP = 16 / G consecutive queries of one kv
+// head as the 16 MFMA rows (row m: query m / G, head m % G) and its 4 waves
+// split the prefix's 16-token tiles (wave w: tiles w, w + 4, ...), each with
+// its own running max m, sum l and value sums, merged in LDS at the end. Per
+// tile: the scores on score_tile (the rows' query vectors scaled per row as in
+// decode), masked to each row's causal prefix; the row statistics over the 16
+// lanes that hold a row (DPP within 16-lane rows); the probabilities move from
+// the score D layout to the value A layout through LDS (a 16 x 16 tile per
+// wave); the values on value_tile with W = p * s_v scaled per wave. The
+// longest prefixes (last queries) are dispatched first.
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+    return fmaxf(v, dpp_f<kDppMirror>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<kDppXor1>(v);
+    v += dpp_f<kDppXor2>(v);
+    v += dpp_f<kDppHalfMirror>(v);
+    return v + dpp_f<kDppMirror>(v);
+}
+
 template <int G>
-__global__ void __launch_bounds__(256) attn_prefill_stream_kernel(AttnArgs a) {
-    __shared__ float qs[4][G][kD];
+__global__ void __launch_bounds__(256) attn_prefill_mfma_kernel(AttnArgs a) {
+    constexpr int QP = 16 / G;  // queries per workgroup
+    __shared__ float qs[16][kD];
+    __shared__ __align__(16) float pt[4][16][20];  // per wave: the P tile, rows padded
+    __shared__ float wm[4][16], wls[4][16];
+    __shared__ float wo[4][16][kD];
     const int h = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // the longest prefixes (last queries) are dispatched first
-    const int b = (gridDim.x - 1 - blockIdx.x) * 4 + wave;
-    const bool live = b < a.pos_n;
-    const int pos = a.pos + (live ? b : 0);
-    const float* rope = a.rope + (int64_t)pos * kD;
-    // RoPE on the G query heads of this wave's query (:460-481)
-    for (int i = lane; i < G * 64; i += 64) {
-        const int g = i >> 6, j = i & 63;
+    const int kn = lane & 15, kq = lane >> 4;
+    const int qb = (gridDim.x - 1 - blockIdx.x) * QP;  // the group's first query row
+    const int nq = min(QP, a.pos_n - qb);              // its live queries
+    // ---- RoPE on the 16 rows (:460-481); rows of dead queries are zero ----
+    for (int i = tid; i < 16 * 64; i += 256) {
+        const int m = i >> 6, j = i & 63, qi = m / G, g = m % G;
+        const bool live = qi < nq;
+        const int b = qb + (live ? qi : 0);
+        const float* rope = a.rope + (int64_t)(a.pos + b) * kD;
         const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)(h * G + g) * kD;
         const float x0 = live ? qv[j] : 0.0f, x1 = live ? qv[j + 64] : 0.0f;
         const float cs = rope[j], sn = rope[64 + j];
-        qs[wave][g][j] = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
-        qs[wave][g][j + 64] = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+        qs[m][j] = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
+        qs[m][j + 64] = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
     }
     __syncthreads();
-    if (!live) return;
-    const int sub = lane >> 3, d0 = (lane & 7) * 16;
-    float qr[G][16];
+    // the rows' A operands, each row scaled by its own power of two
+    h4a qh[8], ql[8];
+    float qin[4];
+    {
+        const float* qrow = &qs[kn][32 * kq];
+        float mx = 0.0f;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+        for (int i = 0; i < 32; ++i) mx = fmaxf(mx, fabsf(qrow[i]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const int sh = fp16_span_exp(mx);
+        const float up = ldexpf(1.0f, sh), down = ldexpf(1.0f, -sh);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) qr[g][j] = qs[wave][g][d0 + j];
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float xs = qrow[4 * j + e] * up;
+                const _Float16 hi = (_Float16)xs;
+                qh[j][e] = hi;
+                ql[j][e] = (_Float16)(xs - (float)hi);
+            }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) qin[e] = __shfl(down, 4 * kq + e, 64);
+    }
+    // this lane's D rows 4 kq + i: their query positions (-1: a dead row, all masked)
+    int prow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int qi = (4 * kq + i) / G;
+        prow[i] = qi < nq ? a.pos + qb + qi : -1;
+    }
+    const int nkey = a.pos + qb + nq;  // keys 0 .. the last live query
+    const int ntile = (nkey + 15) / 16;
     const int64_t cache_head = (int64_t)h * a.max_seq;
     const int8_t* kbase = a.kc + cache_head * kD;
     const int8_t* vbase = a.vc + cache_head * kD;
     const uint16_t* ksb = a.ks + cache_head;
     const uint16_t* vsb = a.vs + cache_head;
-    float m[G], l[G], acc[G][16];
+    // the wave's power-of-two scale for W = p * s_v: its tiles' largest V scale
+    float vmax = 0.0f;
+    for (int tile = wave; tile < ntile; tile += 4)
+        vmax = fmaxf(vmax, half_bits_to_float(vsb[min(tile * 16 + kn, nkey - 1)]));
+    const int wsh = fp16_span_exp(wave_max(vmax));
+    const float wup = ldexpf(1.0f, wsh), wdown = ldexpf(1.0f, -wsh);
+    float mr[4], lr[4];
+    f4a acc8[8];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        m[g] = -1e30f;
-        l[g] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc[g][j] = 0.0f;
+    for (int i = 0; i < 4; ++i) {
+        mr[i] = -1e30f;
+        lr[i] = 0.0f;
     }
-    const int seq_len = pos + 1;
-    for (int t0 = 0; t0 < seq_len; t0 += 64) {
-        // scores of the block's 64 tokens: 8 groups of 8, this lane's token
-        // of group r is t0 + 8r + sub
-        float sc[8][G];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int t = t0 + 8 * r + sub;
-            const bool ok = t < seq_len;
-            float kf[16];
-            uint4 kv = make_uint4(0, 0, 0, 0);
-            if (ok) kv = *reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + d0);
-            unpack16(kv, kf);
-            const float f = ok ? __fmul_rn(half_bits_to_float(ksb[t]), kScaleFactor) : 0.0f;
+    for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int tile = wave; tile < ntile; tile += 4) {
+        // the tile's K (lane token kn) and V (lane tokens 4 kq + e) rows and scales
+        const int tk = min(tile * 16 + kn, nkey - 1);
+        const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)tk * kD + 32 * kq);
+        const uint4 k0 = kp[0], k1 = kp[1];
+        const float f = __fmul_rn(half_bits_to_float(ksb[tk]), kScaleFactor);
+        uint2 v[4];
+        float svf[4];
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                float s = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) s = __builtin_fmaf(qr[g][j], kf[j], s);
-                s += dpp_f<kDppXor1>(s);
-                s += dpp_f<kDppXor2>(s);
-                s += dpp_f<kDppHalfMirror>(s);
-                sc[r][g] = ok ? __fmul_rn(s, f) : -1e30f;
-            }
+        for (int e = 0; e < 4; ++e) {
+            const int tv = min(tile * 16 + 4 * kq + e, nkey - 1);
+            v[e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)tv * kD + 8 * kn);
+            svf[e] = half_bits_to_float(vsb[tv]);
         }
-        // online softmax: block max, rescale, exponentials
+        const f4a d = score_tile(qh, ql, k0, k1);
+        const int tok = tile * 16 + kn;
+        float p[4], rs[4];
 #pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float bm = sc[0][g];
-#pragma unroll
-            for (int r = 1; r < 8; ++r) bm = fmaxf(bm, sc[r][g]);
-            bm = wave_max(bm);
-            const float mn = fmaxf(m[g], bm);
-            const float corr = expf(m[g] - mn);
-            m[g] = mn;
-            float ls = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 8; ++r) {
-                const float e = sc[r][g] > -1e29f ? expf(sc[r][g] - mn) : 0.0f;
-                sc[r][g] = e;
-                ls += e;
-            }
-            // each token's exponential sits in its 8 lanes: sum one lane per token
-            ls = (lane & 7) == 0 ? ls : 0.0f;
-            l[g] = __builtin_fmaf(l[g], corr, wave_sum_tree(ls));
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[g][j] = __fmul_rn(acc[g][j], corr);
+        for (int i = 0; i < 4; ++i) {
+            const float sv = tok <= prow[i] ? __fmul_rn(d[i] * qin[i], f) : -1e30f;
+            const float mn = fmaxf(mr[i], row16_max(sv));
+            rs[i] = expf(mr[i] - mn);
+            p[i] = tok <= prow[i] ? expf(sv - mn) : 0.0f;
+            lr[i] = __builtin_fmaf(lr[i], rs[i], row16_sum(p[i]));
+            mr[i] = mn;
         }
-        // weighted values of the block
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            const int t = t0 + 8 * r + sub;
-            if (t < seq_len) {
-                float vf[16];
-                unpack16(*reinterpret_cast<const uint4*>(vbase + (int64_t)t * kD + d0), vf);
-                const float sv = half_bits_to_float(vsb[t]);
+        for (int dt = 0; dt < 8; ++dt)
 #pragma unroll
-                for (int g = 0; g < G; ++g) {
-                    const float wgt = __fmul_rn(sc[r][g], sv);
+            for (int i = 0; i < 4; ++i) acc8[dt][i] *= rs[i];
+        // P from the score layout (row 4 kq + i, token kn) to the value A layout (row kn,
+        // tokens 4 kq ..): through this wave's LDS tile (in order within the wave)
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) acc[g][j] = __builtin_fmaf(vf[j], wgt, acc[g][j]);
-                }
-            }
+        for (int i = 0; i < 4; ++i) pt[wave][4 * kq + i][kn] = p[i];
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+        asm volatile("" ::: "memory");
+        const float4 pr = *reinterpret_cast<const float4*>(&pt[wave][kn][4 * kq]);
+        const float pw[4] = {pr.x, pr.y, pr.z, pr.w};
+        h4a wh[1], wl[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float w = __fmul_rn(pw[e], svf[e]) * wup;
+            const _Float16 hi = (_Float16)w;
+            wh[0][e] = hi;
+            wl[0][e] = (_Float16)(w - (float)hi);
+        }
+        asm volatile("" ::: "memory");  // (the next tile's LDS writes stay behind this read)
+        value_tile(wh, wl, v, acc8);
+    }
+    // merge the 4 waves: (m, l) per row, value sums unscaled
+    if (kn == 0) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            wm[wave][4 * kq + i] = mr[i];
+            wls[wave][4 * kq + i] = lr[i];
         }
     }
-    // reduce over the 8 token lanes that share dims, normalise, store
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            float v = acc[g][j];
-            v += __shfl_xor(v, 8, 64);
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
-            acc[g][j] = v;
+        for (int dt = 0; dt < 8; ++dt) wo[wave][4 * kq + i][8 * kn + dt] = acc8[dt][i] * wdown;
+    __syncthreads();
+    for (int o = tid; o < 16 * kD; o += 256) {
+        const int m = o >> 7, dd = o & 127, qi = m / G, g = m % G;
+        if (qi >= nq) continue;
+        const float M = fmaxf(fmaxf(wm[0][m], wm[1][m]), fmaxf(wm[2][m], wm[3][m]));
+        float L = 0.0f, acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float e = expf(wm[w][m] - M);
+            L = __builtin_fmaf(e, wls[w][m], L);
+            acc = __builtin_fmaf(e, wo[w][m][dd], acc);
         }
-    if (lane < 8) {
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            float* o = a.out + (int64_t)b * a.out_stride + (int64_t)(h * G + g) * kD + d0;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) o[j] = __fdiv_rn(acc[g][j], l[g]);
-        }
+        a.out[(int64_t)(qb + qi) * a.out_stride + (int64_t)(h * G + g) * kD + dd] = __fdiv_rn(acc, L);
     }
 }
 
@@ -992,15 +1027,16 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
     hipLaunchKernelGGL(attn_append_kernel, dim3(P.n, P.Hkv), dim3(128), 0, st, a);
     int rc = launch_status("attn_append_kernel");
     if (rc) return rc;
-    if (!P.exact && (G == 1 || G == 2 || G == 4)) {
+    if (!P.exact && (G == 1 || G == 2 || G == 4 || G == 8)) {
         a.pos_n = P.n;
-        dim3 grid((unsigned)ceil_div(P.n, 4), P.Hkv);
+        dim3 grid((unsigned)ceil_div(P.n, 16 / G), P.Hkv);
         switch (G) {
-            case 1: hipLaunchKernelGGL(attn_prefill_stream_kernel<1>, grid, dim3(256), 0, st, a); break;
-            case 2: hipLaunchKernelGGL(attn_prefill_stream_kernel<2>, grid, dim3(256), 0, st, a); break;
-            default: hipLaunchKernelGGL(attn_prefill_stream_kernel<4>, grid, dim3(256), 0, st, a); break;
+            case 1: hipLaunchKernelGGL(attn_prefill_mfma_kernel<1>, grid, dim3(256), 0, st, a); break;
+            case 2: hipLaunchKernelGGL(attn_prefill_mfma_kernel<2>, grid, dim3(256), 0, st, a); break;
+            case 4: hipLaunchKernelGGL(attn_prefill_mfma_kernel<4>, grid, dim3(256), 0, st, a); break;
+            default: hipLaunchKernelGGL(attn_prefill_mfma_kernel<8>, grid, dim3(256), 0, st, a); break;
         }
-        return launch_status("attn_prefill_stream_kernel");
+        return launch_status("attn_prefill_mfma_kernel");
     }
     // exact form: queries in groups whose chunk partials fit ~64 MiB of scratch
     const int mc = attn_prefill_max_chunks(P.pos0, P.n, P.Hkv);
