@@ -363,10 +363,14 @@ TENZO_HIP_API int tenzo_hip_engine_get_layer_state(struct tenzo_engine_opaque* e
                                                    int which, void* out, int64_t n);
 /* How a decode step is executed (no reference counterpart; the results are
  * the same up to fp32 reduction order in attention):
- *   2 (default) one persistent cooperative kernel per token, stages separated
- *     by in-kernel barriers (needs cooperative launch, an int8 LM head, MLP
- *     weights in every layer, hidden and ffn multiples of 64 and <= 8192;
- *     otherwise mode 1 runs);
+ *   2 (default) one persistent kernel per token (one workgroup per CU, all
+ *     resident: an ordinary launch, and a cooperative one after a step has
+ *     timed out), stages separated by in-kernel barriers (needs cooperative
+ *     launch support, an int8 LM head, MLP weights in every layer, hidden and
+ *     ffn multiples of 64 and <= 8192; otherwise mode 1 runs). Every in-kernel
+ *     wait is bounded (TENZO_HIP_SPIN_LIMIT polls, read when the engine is
+ *     made; default 262144): a wait that gives up fails the call, and the
+ *     engine state is then invalid;
  *   1 one kernel per stage, replayed from a captured HIP graph;
  *   0 one kernel per stage, launched eagerly. */
 TENZO_HIP_API int tenzo_hip_engine_set_mode(struct tenzo_engine_opaque* e, int mode);

@@ -48,7 +48,8 @@ struct DsParams {
     unsigned* sync;             // ds_sync_words() words, zero before each launch
     int* acc;                   // ds_acc_words() int32 GEMV accumulators, zero before
                                 // each launch: per layer q|k|v, o, gate|up, down
-    int32_t* io;                // [0] token in, [2] greedy token out (also copied to [0])
+    int32_t* io;                // [0] token in, [2] greedy token out (also copied to [0]),
+                                // [3] set to 1 when a wait timed out (cleared by the host)
     int32_t* out_tokens;        // optional: the greedy token is also stored at [step]
     int step;
     int H, F, Hq, Hkv, L, V, max_seq;
@@ -56,6 +57,7 @@ struct DsParams {
     int nwg;
     int split[4];               // K slices per row block of the QKV, O, GU, DOWN GEMVs
     int with_head;              // 0: stop after the layers (prefill)
+    unsigned spin_limit;        // polls before a wait gives up (kDsSpinLimit)
     float eps;
     // optional step trace: for stage s and workgroup w, [(s * nwg + w) * 2]
     // = wall clock (100 MHz) when w arrives at the barrier after stage s,
@@ -64,7 +66,8 @@ struct DsParams {
 };
 
 constexpr int kDsThreads = 512;
-constexpr int kDsMaxChunk = 256;    // context tokens per attention task, at most
+constexpr int kDsMaxChunk = 256;
+constexpr unsigned kDsSpinLimit = 1u << 18;  // ~0.3 s of polling; a barrier waits < 0.1 ms    // context tokens per attention task, at most
 constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
 constexpr int kDsCounters = 16;
 constexpr int kDsMaxLayers = 64;    // the layer table is staged in LDS
@@ -91,7 +94,7 @@ void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T);
 // kv head (its chunk statistics live in LDS).
 int ds_max_context(int G);
 // Launches one decode step (cooperative). The sync region must be zero.
-int launch_decode_step(const DsParams& p, int G, hipStream_t st);
+int launch_decode_step(const DsParams& p, int G, bool coop, hipStream_t st);
 // Error word of the sync region (non-zero after an aborted step).
 size_t ds_error_word(int L, int Hkv);
 

@@ -67,7 +67,6 @@ constexpr int kRT = kW * 8;      // attention tokens per round (8 per wave)
 constexpr int kAR = kW >= 8 ? 2 : 4;  // attention rounds preloaded in registers
 static_assert(2 * kAR <= kPF, "the attention tile uses the GEMV tile's registers");
 static_assert(kW == 4 || kW == 8, "4 or 8 waves per workgroup");
-constexpr unsigned kSpinLimit = 1u << 18;  // ~0.3 s of polling; a barrier waits < 0.1 ms
 constexpr float kAttnScale = 0.08838834764831845f;  // 1/sqrt(128)
 
 // threadIdx.x behind an empty asm: values derived from it are recomputed in
@@ -296,6 +295,14 @@ __device__ __forceinline__ int kind_of(const DsParams& p, int s) {
 
 // ------------------------------------------------------------- barrier ----
 
+// A wait that gave up: the error word makes every workgroup abort at its next
+// poll, and io[3] (not cleared with the sync area before each launch) tells
+// the host, for any step of a chained decode.
+__device__ __forceinline__ void raise_abort(const DsParams& p) {
+    stcu(p.sync + w_err(p.L, p.Hkv), 1u);
+    __hip_atomic_store(p.io + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
     ++gen;
     __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are acknowledged
@@ -312,16 +319,14 @@ __device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, i
         while (true) {
             if (!done) done = ldcu(p.sync + l * 64) >= target;
             if (__all(done)) break;
-            if ((++spins & 63) == 0) {
-                if (ldcu(p.sync + w_err(p.L, p.Hkv)) != 0) {
-                    abort = true;
-                    break;
-                }
-                if (spins > kSpinLimit) {
-                    if (l == 0) stcu(p.sync + w_err(p.L, p.Hkv), 1u);
-                    abort = true;
-                    break;
-                }
+            if (++spins > p.spin_limit) {
+                if (l == 0) raise_abort(p);
+                abort = true;
+                break;
+            }
+            if ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0) {
+                abort = true;
+                break;
             }
         }
         if (l == 0) *s_abort = abort ? 1 : 0;
@@ -1151,9 +1156,9 @@ __device__ __forceinline__ bool paged_weights(AttnShared& a, const DsParams& p, 
             int ok = 1;
             unsigned spins = 0;
             while (ldcu(ctr) < (unsigned)p.C) {
-                if (++spins > kSpinLimit ||
+                if (++spins > p.spin_limit ||
                     ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0)) {
-                    stcu(p.sync + w_err(p.L, p.Hkv), 1u);
+                    raise_abort(p);
                     ok = 0;
                     break;
                 }
@@ -1583,9 +1588,9 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
         if (r >= 0) {
             unsigned spins = 0;
             while (ldcu(ctr) < (unsigned)p.C) {
-                if (++spins > kSpinLimit ||
+                if (++spins > p.spin_limit ||
                     ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0)) {
-                    stcu(p.sync + w_err(p.L, p.Hkv), 1u);
+                    raise_abort(p);
                     r = -1;
                     break;
                 }
@@ -1978,7 +1983,7 @@ void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T) {
 // LDS (kTmax * kD bytes).
 int ds_max_context(int G) { return kTmax * kD / 8 / G * kTmax; }
 
-int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
+int launch_decode_step(const DsParams& p, int G, bool coop, hipStream_t st) {
     void* args[] = {const_cast<DsParams*>(&p)};
     void* fn = nullptr;
     const bool paged = p.kv_mode == 3;
@@ -2015,19 +2020,23 @@ int launch_decode_step(const DsParams& p, int G, hipStream_t st) {
                   kJ * 4 * kT);
         return TENZO_ERROR_UNSUPPORTED;
     }
-    hipError_t e = hipLaunchCooperativeKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
-    if (e == hipErrorIllegalState || e == hipErrorNotSupported) {
-        // The runtime refuses a cooperative launch while another process holds
-        // the device's cooperative-launch resources. The kernel needs no more
-        // than all nwg workgroups resident, which an ordinary launch of this
-        // grid gives on an idle device (one workgroup per CU; ds_grid_size
-        // checked the occupancy); every wait in it is bounded, so a grid that
-        // is not fully resident ends the step with the error word instead of
-        // hanging.
+    // The kernel needs all nwg workgroups resident at once: one per CU
+    // (ds_grid_size checked the occupancy), which an ordinary launch of this
+    // grid gives on a device with no other work resident. The cooperative
+    // launch guarantees it but costs ~19 us more per step (1.1795 vs 1.1994 ms
+    // per BitNet-2B token), so it is the engine's fallback after an ordinary
+    // launch has aborted: every wait in the kernel is bounded, so a grid that
+    // is not fully resident ends the step with the abort flag set instead of
+    // hanging. The runtime also refuses a cooperative launch while another
+    // process holds the device's cooperative-launch resources; then the
+    // ordinary launch is taken all the same.
+    hipError_t e = hipErrorNotSupported;
+    if (coop) e = hipLaunchCooperativeKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
+    if (!coop || e == hipErrorIllegalState || e == hipErrorNotSupported) {
         (void)hipGetLastError();
         e = hipLaunchKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
     }
-    if (e != hipSuccess) return hip_fail(e, "hipLaunchCooperativeKernel(decode_step)");
+    if (e != hipSuccess) return hip_fail(e, "launch of decode_step_kernel"); 
     return TENZO_SUCCESS;
 }
 

@@ -108,7 +108,7 @@ struct tenzo_engine_opaque {
     float* attn_part = nullptr;
     void* am_ws = nullptr;
     void* sample_ws = nullptr;   // top-k candidates of the sampler
-    int32_t* io_dev = nullptr;   // [0] token, [1] position, [2] result token
+    int32_t* io_dev = nullptr;   // [0] token, [1] position, [2] result token, [3] abort flag
     int32_t* io_host = nullptr;  // pinned mirror
     int32_t* pen_dev = nullptr;  // past tokens for the repetition penalty
     int pen_cap = 0;
@@ -131,6 +131,8 @@ struct tenzo_engine_opaque {
     int dec_cap = 0;
     uint64_t* ds_trace = nullptr;  // step trace (tenzo_hip_engine_trace), null when off
     bool ds_state_valid = false;   // the last step ran the persistent kernel
+    bool ds_coop = false;          // cooperative launches (after an ordinary one aborted)
+    unsigned ds_spin = kDsSpinLimit;  // TENZO_HIP_SPIN_LIMIT: polls before a wait gives up
 
     // batched prefill (tenzo_hip_engine_prefill): rows of up to pf_cap tokens
     int pf_cap = 0;
@@ -910,19 +912,26 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.with_head = head ? 1 : 0;
     p.eps = e->eps;
     p.trace = e->ds_trace;
+    p.spin_limit = e->ds_spin;
     p.out_tokens = out_tokens;
     p.step = step;
     TZ_HIP(hipMemsetAsync(e->ds_sync, 0, e->ds_sync_bytes, e->st));
-    rc = launch_decode_step(p, e->Hq / e->Hkv, e->st);
+    rc = launch_decode_step(p, e->Hq / e->Hkv, e->ds_coop, e->st);
     e->ds_state_valid = rc == TENZO_SUCCESS;
     return rc;
 }
 
-// After a persistent step: the kernel's error word (non-zero when a wait
-// timed out and the step was abandoned), copied next to the result token.
+// After persistent steps: the kernel's abort flag (io[3], set when a wait
+// timed out and a step was abandoned; cleared by the host before the steps),
+// copied next to the result token. An abort under an ordinary launch can mean
+// that the grid was not all resident (other work on the device), so the
+// engine's later steps use the cooperative launch.
 int ds_check(tenzo_engine_t e) {
     if (e->io_host[3] != 0) {
-        set_error("decode step aborted: an in-kernel wait timed out (engine state is invalid)");
+        const bool was_coop = e->ds_coop;
+        e->ds_coop = true;
+        set_error("decode step aborted: an in-kernel wait timed out (engine state is invalid)%s",
+                  was_coop ? "" : "; later steps use a cooperative launch");
         return TENZO_ERROR_UNSUPPORTED;
     }
     return TENZO_SUCCESS;
@@ -948,14 +957,14 @@ int run_step(tenzo_engine_t e, int token, bool head) {
     }
     e->io_host[0] = token;
     e->io_host[1] = pos;
-    TZ_HIP(hipMemcpyAsync(e->io_dev, e->io_host, 8, hipMemcpyHostToDevice, e->st));
+    e->io_host[2] = 0;
+    e->io_host[3] = 0;  // the abort flag
+    TZ_HIP(hipMemcpyAsync(e->io_dev, e->io_host, 16, hipMemcpyHostToDevice, e->st));
     int rc;
-    e->io_host[3] = 0;
     e->ds_state_valid = false;
     if (e->mode == 2 && ds_usable(e)) {
         if ((rc = run_persistent(e, head, pos))) return rc;
-        TZ_HIP(hipMemcpyAsync(e->io_host + 3, e->ds_sync + ds_error_word(e->L, e->Hkv), 4,
-                              hipMemcpyDeviceToHost, e->st));
+        TZ_HIP(hipMemcpyAsync(e->io_host + 3, e->io_dev + 3, 4, hipMemcpyDeviceToHost, e->st));
     } else if (e->mode >= 1) {
         const int max_chunks = (int)ceil_div(e->max_seq, T);
         auto key = std::make_pair(T, head ? 1 : 0);
@@ -1043,6 +1052,12 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     }
     auto* e = new tenzo_engine_opaque();
     e->cfg = c;
+    // a smaller in-kernel poll budget (tests force the abort path with it)
+    if (const char* sl = std::getenv("TENZO_HIP_SPIN_LIMIT")) {
+        char* end = nullptr;
+        const unsigned long v = std::strtoul(sl, &end, 10);
+        if (end != sl && v <= kDsSpinLimit) e->ds_spin = (unsigned)v;
+    }
     e->kv_mode = kv;
     e->kv_kind = kv_kind;
     e->kv_row = kv_kind == 0 || kv_kind == 3 ? kD : 32;
@@ -1351,6 +1366,8 @@ TENZO_HIP_API int tenzo_hip_engine_decode(tenzo_engine_t e, int token, int n, in
     e->io_host[3] = 0;
     int rc = TENZO_SUCCESS;
     if (hipMemcpyAsync(e->io_dev, e->io_host, 4, hipMemcpyHostToDevice, e->st) != hipSuccess ||
+        hipMemcpyAsync(e->io_dev + 3, e->io_host + 3, 4, hipMemcpyHostToDevice, e->st) !=
+            hipSuccess ||
         hipEventRecord(t0, e->st) != hipSuccess)
         rc = TENZO_ERROR_UNSUPPORTED;
     const bool persistent = e->mode == 2 && ds_usable(e);
@@ -1379,8 +1396,8 @@ TENZO_HIP_API int tenzo_hip_engine_decode(tenzo_engine_t e, int token, int n, in
     }
     if (!rc && hipEventRecord(t1, e->st) != hipSuccess) rc = TENZO_ERROR_UNSUPPORTED;
     if (!rc && persistent)
-        if (hipMemcpyAsync(e->io_host + 3, e->ds_sync + ds_error_word(e->L, e->Hkv), 4,
-                           hipMemcpyDeviceToHost, e->st) != hipSuccess)
+        if (hipMemcpyAsync(e->io_host + 3, e->io_dev + 3, 4, hipMemcpyDeviceToHost, e->st) !=
+            hipSuccess)
             rc = TENZO_ERROR_UNSUPPORTED;
     if (!rc && hipMemcpyAsync(out, e->dec_out, (size_t)n * 4, hipMemcpyDeviceToHost, e->st) !=
                    hipSuccess)

@@ -163,6 +163,39 @@ def test_chained_decode_equals_steps(eng_mod, mode):
         assert a.step(int(toks[-1])) == b.step(ref[-1])
 
 
+def test_persistent_abort_is_reported(eng_mod, monkeypatch):
+    """Failure handling, forced from the host: with an in-kernel poll budget of
+    zero (TENZO_HIP_SPIN_LIMIT=0, read when the engine is made) the first wait
+    that finds its condition unmet gives up, every workgroup leaves the kernel
+    at its next poll, and the call reports the timeout instead of a token --
+    in a chained decode (the flag is not cleared between its steps) and in a
+    single step. The first report moves the engine to the cooperative launch.
+    An engine made without the variable decodes beside it as usual."""
+    sm = synth.make_model(CFG, seed=61, ctx=11)
+    monkeypatch.setenv("TENZO_HIP_SPIN_LIMIT", "0")
+    a = eng_mod.Engine(CFG)
+    monkeypatch.delenv("TENZO_HIP_SPIN_LIMIT")
+    with a, eng_mod.Engine(CFG) as b:
+        a.set_model(sm)
+        b.set_model(sm)
+        a.set_mode("persistent")
+        b.set_mode("persistent")
+        with pytest.raises(RuntimeError, match="timed out.*cooperative launch"):
+            a.decode(7, 3)
+        with pytest.raises(RuntimeError) as ei:
+            a.step(7)
+        assert "timed out" in str(ei.value) and "cooperative" not in str(ei.value)
+        toks, _ = b.decode(7, 3)
+        ref, t = [], 7
+        with eng_mod.Engine(CFG) as c:
+            c.set_model(sm)
+            c.set_mode("persistent")
+            for _ in range(3):
+                t = c.step(t)
+                ref.append(t)
+        assert list(toks) == ref
+
+
 def test_engine_first_layer_stages_bit_exact(eng_mod):
     """One layer, stage by stage from the engine's own buffers: QKV from the
     embedded token, O/residual, gate|up and down/residual are bit-exact."""
