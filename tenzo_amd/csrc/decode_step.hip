@@ -1881,8 +1881,11 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     const int nstages = 5 * p.L + 1;
     unsigned gen = 0;
     // no line of this launch's per-layer vectors may survive in L2 from an
-    // earlier launch (they are read with cached loads after the first barrier)
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // earlier launch (they are read with cached loads after the first barrier):
+    // one invalidation of the CU's L1 and the XCD's L2 per workgroup (the
+    // caches are shared by its waves, which wait for it at the block barrier)
+    if (lwave() == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    __syncthreads();
     if (KVM == 3) stage_blocks(p);  // (stage_layers' block barrier covers it)
     stage_layers(p);
     int off = 0;  // first workgroup of the current stage
