@@ -925,6 +925,24 @@ def main():
         e.rewind(ctx)
         tok = e.step(tok)
     api_tok_s = api_steps / (time.perf_counter() - t0)
+    # the timed path's tokens against the per-stage kernels (graph mode) on the
+    # same engine and weights: the same greedy tokens from the same state
+    # (attention sums in another order, so a logit tie could split them; a
+    # difference is reported, not hidden)
+    token_check = None
+    if mode == "persistent":
+        nchk = 4
+        e.rewind(ctx)
+        ptoks, _ = e.decode(1, nchk)
+        e.set_mode("graph")
+        e.rewind(ctx)
+        gtoks, _ = e.decode(1, nchk)
+        e.set_mode(mode)
+        token_check = {"steps": nchk, "against": "graph", "tokens_equal":
+                       [int(t) for t in ptoks] == [int(t) for t in gtoks]}
+        if not token_check["tokens_equal"]:
+            print(f"bench: persistent tokens {list(ptoks)} differ from the graph path's "
+                  f"{list(gtoks)}", file=sys.stderr, flush=True)
 
     # algorithmic HBM bytes of a step at the mean context of the timed run
     step_bytes = cfg.step_bytes(ctx + 1 + args.steps // 2)["total"]
@@ -987,6 +1005,7 @@ def main():
         "gemv_attn": gemv_attn,
         "stages": st,
         "api_generate_step_tok_s": round(api_tok_s, 2),
+        "token_check": token_check,
         "stage_kernels": {"tl1_gemv": {k: (round(v, 2) if isinstance(v, float) else v)
                                        for k, v in rl_tl1.items()},
                           "lm_head_i8": {k: (round(v, 2) if isinstance(v, float) else v)
