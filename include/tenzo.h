@@ -9,8 +9,10 @@
  *   - the decode step runs on the GPU whatever `device` says (this library
  *     has no CPU path); `kv_mode` is "int8_fused" (or NULL), "tl1_fused",
  *     "popcount_fused" or "paged_int8" (the reference's fp32 fallback for
- *     other strings is not provided: create returns NULL); the modes other
- *     than int8_fused run the graph path and fill the cache token by token in
+ *     other strings is not provided: create returns NULL); every mode runs
+ *     in the persistent decode kernel (paged_int8 up to the context its
+ *     in-kernel softmax wait supports, the stage kernels beyond), and the
+ *     modes other than int8_fused fill the cache token by token in
  *     tenzo_hip_engine_prefill;
  *   - weights are copied to device memory when they are set, so the caller may
  *     free its copies afterwards (the reference keeps non-owning pointers to

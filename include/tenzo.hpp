@@ -12,10 +12,8 @@
 #ifndef TENZO_HPP
 #define TENZO_HPP
 
-#include <memory>
 #include <stdexcept>
 #include <string>
-#include <string_view>
 #include <vector>
 
 #include "tenzo.h"

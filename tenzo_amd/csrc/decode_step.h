@@ -46,6 +46,13 @@ struct DsParams {
     float* part;                // [Hkv][C][G][kDsPartStride] attention partials
     float2* am_part;            // [nwg] argmax partials
     unsigned* sync;             // ds_sync_words() words, zero before each launch
+    // grid-barrier counters (kDsCounters words 256 bytes apart) and the error
+    // word after them, in uncached memory (polled with scalar loads): the
+    // counters carry on from launch to launch, bar_base generations of them
+    // having been completed by earlier launches (kDsBarWords words, zeroed by
+    // the host before the first launch and after a launch that aborted)
+    unsigned* bar;
+    unsigned bar_base;
     int* acc;                   // ds_acc_words() int32 GEMV accumulators, zero before
                                 // each launch: per layer q|k|v, o, gate|up, down
     int32_t* io;                // [0] token in, [2] greedy token out (also copied to [0]),
@@ -66,10 +73,11 @@ struct DsParams {
 };
 
 constexpr int kDsThreads = 512;
-constexpr int kDsMaxChunk = 256;
-constexpr unsigned kDsSpinLimit = 1u << 18;  // ~0.3 s of polling; a barrier waits < 0.1 ms    // context tokens per attention task, at most
+constexpr int kDsMaxChunk = 256;            // context tokens per attention task, at most
+constexpr unsigned kDsSpinLimit = 1u << 18;  // ~0.3 s of polling; a barrier waits < 0.1 ms
 constexpr int kDsPartStride = 132;  // floats per attention partial record (16-byte aligned)
 constexpr int kDsCounters = 16;
+constexpr int kDsBarWords = (kDsCounters + 1) * 64;  // counters, then the error word
 constexpr int kDsMaxLayers = 64;    // the layer table is staged in LDS
 constexpr int kDsMaxBlocks = 1024;  // paged: the block table is staged in LDS (16384 tokens)
 
@@ -93,9 +101,15 @@ void ds_chunking(int ctx, int Hkv, int nwg, int* C, int* T);
 // Longest context the kernel's attention merge supports for G query heads per
 // kv head (its chunk statistics live in LDS).
 int ds_max_context(int G);
-// Launches one decode step (cooperative). The sync region must be zero.
+// Grid barriers per launch of L layers (bar_base advances by this much).
+inline unsigned ds_barriers(int L) { return 5u * (unsigned)L; }
+// Returned by launch_decode_step when a cooperative launch was asked for and
+// the runtime refused it (nothing was launched).
+constexpr int kDsCoopRefused = 1000;
+// Launches one decode step: an ordinary launch, or with coop a cooperative
+// one (kDsCoopRefused when the runtime refuses it). The sync region must be
+// zero. A launch whose io[3] is already set returns at once (a chained decode
+// stops at the first step that aborted).
 int launch_decode_step(const DsParams& p, int G, bool coop, hipStream_t st);
-// Error word of the sync region (non-zero after an aborted step).
-size_t ds_error_word(int L, int Hkv);
 
 }  // namespace tz

@@ -199,7 +199,6 @@ __device__ __forceinline__ void stage_layers(const DsParams& p) {
     __syncthreads();
 }
 
-__host__ __device__ inline size_t w_err(int, int) { return (size_t)kNC * 64; }
 __host__ __device__ inline size_t w_am(int, int) { return (size_t)(kNC + 1) * 64; }
 __host__ __device__ inline size_t w_head(int l, int h, int Hkv) {
     return (size_t)(kNC + 2 + l * Hkv + h) * 64;
@@ -298,38 +297,93 @@ __device__ __forceinline__ int kind_of(const DsParams& p, int s) {
 // A wait that gave up: the error word makes every workgroup abort at its next
 // poll, and io[3] (not cleared with the sync area before each launch) tells
 // the host, for any step of a chained decode.
+__device__ __forceinline__ unsigned* err_word(const DsParams& p) { return p.bar + kNC * 64; }
 __device__ __forceinline__ void raise_abort(const DsParams& p) {
-    stcu(p.sync + w_err(p.L, p.Hkv), 1u);
+    stcu(err_word(p), 1u);
     __hip_atomic_store(p.io + 3, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-__device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort) {
+// The kNC barrier counters (256 bytes apart) and the error word after them,
+// read with scalar loads that bypass the scalar cache (glc). The region is
+// uncached memory, so the reads miss in L2 as well and see every
+// workgroup's arrival. Scalar loads do not queue behind the CU's vector
+// loads, so a workgroup can have the next stage's weight tile in flight
+// while it polls.
+__device__ __forceinline__ void poll_bar(const unsigned* base, unsigned& lo, unsigned& err) {
+    static_assert(kNC == 16, "16 counters polled");
+    unsigned c[16];
+    asm volatile(
+        "s_load_dword %0, %17, 0x0 glc\n"
+        "s_load_dword %1, %17, 0x100 glc\n"
+        "s_load_dword %2, %17, 0x200 glc\n"
+        "s_load_dword %3, %17, 0x300 glc\n"
+        "s_load_dword %4, %17, 0x400 glc\n"
+        "s_load_dword %5, %17, 0x500 glc\n"
+        "s_load_dword %6, %17, 0x600 glc\n"
+        "s_load_dword %7, %17, 0x700 glc\n"
+        "s_load_dword %8, %17, 0x800 glc\n"
+        "s_load_dword %9, %17, 0x900 glc\n"
+        "s_load_dword %10, %17, 0xa00 glc\n"
+        "s_load_dword %11, %17, 0xb00 glc\n"
+        "s_load_dword %12, %17, 0xc00 glc\n"
+        "s_load_dword %13, %17, 0xd00 glc\n"
+        "s_load_dword %14, %17, 0xe00 glc\n"
+        "s_load_dword %15, %17, 0xf00 glc\n"
+        "s_load_dword %16, %17, 0x1000 glc\n"
+        "s_waitcnt lgkmcnt(0)\n"
+        : "=&s"(c[0]), "=&s"(c[1]), "=&s"(c[2]), "=&s"(c[3]), "=&s"(c[4]), "=&s"(c[5]),
+          "=&s"(c[6]), "=&s"(c[7]), "=&s"(c[8]), "=&s"(c[9]), "=&s"(c[10]), "=&s"(c[11]),
+          "=&s"(c[12]), "=&s"(c[13]), "=&s"(c[14]), "=&s"(c[15]), "=&s"(err)
+        : "s"(base)
+        : "memory");
+    lo = c[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) lo = c[i] < lo ? c[i] : lo;
+}
+
+// Grid barrier: every wave waits for its stores' acknowledgements, thread 0
+// adds the workgroup's arrival to counter wg % kNC (the counters carry on
+// across launches: generation bar_base + gen is complete when each holds
+// (bar_base + gen) * nwg / kNC), then `issue` starts the next stage's loads
+// that depend on nothing of this stage (its weight tile) and wave 0 polls the
+// counters with scalar loads while those loads are in flight. The arrival goes
+// out before any wave's prefetch (a second block barrier), so it never waits
+// behind them in the CU's memory pipeline. Every wait is bounded.
+// `touched` is the result of touch_norm's load: taken as an operand here,
+// where every load of the wave has completed, it keeps the load without
+// computing anything from it.
+template <class Issue>
+__device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort,
+                                             int touched, Issue&& issue) {
     ++gen;
     __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are acknowledged
+    asm volatile("" ::"v"(touched));
     __syncthreads();
-    if (threadIdx.x < 64) {
-        const int l = threadIdx.x;
-        if (l == 0)
-            __hip_atomic_fetch_add(p.sync + (blockIdx.x % kNC) * 64, 1u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned target = gen * (unsigned)(p.nwg / kNC);
-        bool done = l >= kNC;
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(p.bar + (blockIdx.x % kNC) * 64, 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_barrier();
+    issue();
+    if (lwave() == 0) {
+        const unsigned target = (p.bar_base + gen) * (unsigned)(p.nwg / kNC);
+        const unsigned* base = uni_ptr(p.bar);
         unsigned spins = 0;
-        bool abort = false;
+        int abort = 0;
         while (true) {
-            if (!done) done = ldcu(p.sync + l * 64) >= target;
-            if (__all(done)) break;
-            if (++spins > p.spin_limit) {
-                if (l == 0) raise_abort(p);
-                abort = true;
+            unsigned lo, err;
+            poll_bar(base, lo, err);
+            if (err != 0) {
+                abort = 1;
                 break;
             }
-            if ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0) {
-                abort = true;
+            if (lo >= target) break;  // (the host keeps every target below 2^31)
+            if (++spins > p.spin_limit) {
+                if (threadIdx.x == 0) raise_abort(p);
+                abort = 1;
                 break;
             }
         }
-        if (l == 0) *s_abort = abort ? 1 : 0;
+        if (threadIdx.x == 0) *s_abort = abort;
     }
     __syncthreads();
     return *s_abort == 0;
@@ -968,7 +1022,8 @@ __device__ __forceinline__ bool rec_writer(const DsParams& p, int first, int n) 
 // the slices of it later stages read, quantizes its normalization (exactly,
 // with the record, in the record writer; the codes alone elsewhere) and adds
 // its tasks' K-slice sums into the accumulators.
-__device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l, int first, int n) {
+__device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l,
+                                          int first, int n, uint4 (&tile)[kPF]) {
     Shared& s = sh.s;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
     const LayerRef Lw = layer(p, l);
@@ -980,11 +1035,10 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     const int S = p.split[slot];
     const int KS = K / 64, KSs = (KS + S - 1) / S;
     const uint4* W = Lw.mat(slot);
-    // the stage input and the norm weights first, then (once every wave has
-    // issued those, so no wave's input queues behind another's tile) the
-    // first task's weight tile, in flight during the normalization
-    // (the sources are chosen per kind; the loads themselves are one
-    // straight sequence, none under a condition: see InRaw)
+    // The first task's weight tile is in flight already (issued during the
+    // grid barrier before this stage, prefetch_tile); the stage input and the
+    // norm weights go out now (the sources are chosen per kind; the loads
+    // themselves are one straight sequence, none under a condition: see InRaw)
     InSrc src{nullptr, (uint32_t)K * 4, false, nullptr, (uint32_t)K * 4, nullptr};
     if (kind == S_QKV) {
         if (l == 0) {
@@ -1011,14 +1065,7 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     issue_in(in, src);
     float4 nwr[kJ];
     load_norm_w(nwr, Lw.norm(slot), K);
-    __builtin_amdgcn_s_barrier();
-    const bool tasks = first < n, rec = rec_writer(p, first, n);
-    uint4 tile[kPF];
-    {  // (the record writer issues the same loads with nothing to read)
-        const int c0 = (first % S) * KSs;
-        load_tl1_tile(tile, W, first / S, KS, c0, min(KS, c0 + KSs), tasks);
-    }
-    wait_vm<kPF>();  // everything but the tile has arrived
+    const bool rec = rec_writer(p, first, n);
     float4 xv[kJ];
     if (kind == S_QKV) {
         if (l == 0)
@@ -1157,7 +1204,7 @@ __device__ __forceinline__ bool paged_weights(AttnShared& a, const DsParams& p, 
             unsigned spins = 0;
             while (ldcu(ctr) < (unsigned)p.C) {
                 if (++spins > p.spin_limit ||
-                    ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0)) {
+                    ((spins & 63) == 0 && ldcu(err_word(p)) != 0)) {
                     raise_abort(p);
                     ok = 0;
                     break;
@@ -1589,7 +1636,7 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
             unsigned spins = 0;
             while (ldcu(ctr) < (unsigned)p.C) {
                 if (++spins > p.spin_limit ||
-                    ((spins & 63) == 0 && ldcu(p.sync + w_err(p.L, p.Hkv)) != 0)) {
+                    ((spins & 63) == 0 && ldcu(err_word(p)) != 0)) {
                     raise_abort(p);
                     r = -1;
                     break;
@@ -1872,6 +1919,22 @@ __device__ __forceinline__ int touch_norm(const DsParams& p, int s) {
     return ld4i(rsrc(nw, nw ? (uint32_t)K * 4 : 0u), (uint32_t)line * 128);
 }
 
+// The first weight tile of the first task of this workgroup (task index
+// `first`) in stage s, when s is a GEMV stage and the workgroup has a task in
+// it; otherwise the same loads with nothing to read (the loads are issued on
+// every path alike: a load under a condition would leave the registers to a
+// phi whose copy waits for them).
+__device__ __forceinline__ void prefetch_tile(const DsParams& p, uint4 (&tile)[kPF], int s,
+                                              int first) {
+    const int kind = kind_of(p, s);
+    const bool gemv = kind != S_ATT && kind != S_HEAD;
+    const int slot = kind == S_QKV || !gemv ? 0 : kind - 1;
+    const int K = gemv_k(slot, p.H, p.F), S = p.split[slot];
+    const int KS = K / 64, KSs = (KS + S - 1) / S, c0 = (first % S) * KSs;
+    load_tl1_tile(tile, layer(p, min(s / 5, p.L - 1)).mat(slot), first / S, KS, c0,
+                  min(KS, c0 + KSs), gemv && first < ntasks(p, kind));
+}
+
 template <int G, int KVM>
 __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     __shared__ SharedAll sh;
@@ -1885,41 +1948,50 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     // one invalidation of the CU's L1 and the XCD's L2 per workgroup (the
     // caches are shared by its waves, which wait for it at the block barrier)
     if (lwave() == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // an earlier step of a chained decode aborted: this one does nothing (the
+    // host reruns the chain from the step that aborted)
+    if (tid == 0)
+        s_abort = __hip_atomic_load(p.io + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
+    if (s_abort != 0) return;
     if (KVM == 3) stage_blocks(p);  // (stage_layers' block barrier covers it)
     stage_layers(p);
     int off = 0;  // first workgroup of the current stage
-    int sink = 0;
-    for (int s = 0; s < nstages; ++s) {
-        const int kind = kind_of(p, s);
+    uint4 tile[kPF];  // the first weight tile of this workgroup's next GEMV task
+    prefetch_tile(p, tile, 0, wg);
+    // The layers' stages; the head follows the loop, so that the loop's only
+    // way back to its top is through the grid barrier (a stage body exiting
+    // through the loop would leave its loads pending at the top, where the
+    // compiler would then wait for all of them, the prefetched tile included).
+    const int nlayer_stages = nstages - 1;
+    for (int s = 0; s < nlayer_stages; ++s) {
+        const int kind = s % 5;
         const int l = s / 5;
         const int n = ntasks(p, kind);
         const int first = (wg - off + p.nwg) % p.nwg;  // my first task index here
-        const int touched = s + 1 < nstages ? touch_norm(p, s + 1) : 0;
-
-        if (kind == S_HEAD) {
-            if (p.nwg < 0) p.io[2] = sink;  // never true: keeps the prefetch loads
-            head_stage(sh, p, first, n);
-            if (p.trace && tid == 0) {
-                const uint64_t now = wall_clock64();
-                p.trace[((size_t)s * p.nwg + wg) * 2] = now;
-                p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = now;
-            }
-            return;
-        }
+        const int touched = touch_norm(p, s + 1);
         if (kind == S_ATT) {
             for (int t = first; t < n; t += p.nwg) {
                 attn_task<G, KVM>(sh, p, l, t / p.C, t % p.C);
                 __syncthreads();
             }
         } else if (first < n || rec_writer(p, first, n)) {
-            tl1_stage(sh, p, kind, l, first, n);
+            tl1_stage(sh, p, kind, l, first, n, tile);
         }
         off = (off + n) % p.nwg;
         if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2] = wall_clock64();
-        if (!grid_barrier(p, gen, &s_abort)) return;
+        const int next = (wg - off + p.nwg) % p.nwg;
+        if (!grid_barrier(p, gen, &s_abort, touched,
+                          [&] { prefetch_tile(p, tile, s + 1, next); }))
+            return;
         if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = wall_clock64();
-        sink ^= touched;  // after the barrier's wait: free
+    }
+    const int s = nlayer_stages;
+    head_stage(sh, p, (wg - off + p.nwg) % p.nwg, ntasks(p, S_HEAD));
+    if (p.trace && tid == 0) {
+        const uint64_t now = wall_clock64();
+        p.trace[((size_t)s * p.nwg + wg) * 2] = now;
+        p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = now;
     }
 }
 
@@ -1929,7 +2001,6 @@ size_t ds_sync_words(int L, int Hkv) {
     const size_t w = (size_t)(kNC + 2 + L * Hkv) * 64 + (size_t)L * 4 * 32 + (size_t)L * Hkv * 64;
     return (w + 63) / 64 * 64;
 }
-size_t ds_error_word(int L, int Hkv) { return w_err(L, Hkv); }
 
 size_t ds_vec_floats(int L, int H, int Hq) { return (size_t)L * (2 * H + Hq * kD); }
 
@@ -2027,19 +2098,25 @@ int launch_decode_step(const DsParams& p, int G, bool coop, hipStream_t st) {
     // (ds_grid_size checked the occupancy), which an ordinary launch of this
     // grid gives on a device with no other work resident. The cooperative
     // launch guarantees it but costs ~19 us more per step (1.1795 vs 1.1994 ms
-    // per BitNet-2B token), so it is the engine's fallback after an ordinary
-    // launch has aborted: every wait in the kernel is bounded, so a grid that
-    // is not fully resident ends the step with the abort flag set instead of
-    // hanging. The runtime also refuses a cooperative launch while another
-    // process holds the device's cooperative-launch resources; then the
-    // ordinary launch is taken all the same.
-    hipError_t e = hipErrorNotSupported;
-    if (coop) e = hipLaunchCooperativeKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
-    if (!coop || e == hipErrorIllegalState || e == hipErrorNotSupported) {
-        (void)hipGetLastError();
+    // per BitNet-2B token), so the engine launches ordinarily and reruns a step
+    // that aborted under the cooperative launch: every wait in the kernel is
+    // bounded, so a grid that is not fully resident ends the step with the
+    // abort flag set instead of hanging. The runtime refuses a cooperative
+    // launch while another process holds the device's cooperative-launch
+    // resources; that is reported (kDsCoopRefused) rather than replaced by
+    // another ordinary launch, so the engine can take its graph path instead.
+    hipError_t e;
+    if (coop) {
+        e = hipLaunchCooperativeKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
+        if (e == hipErrorIllegalState || e == hipErrorNotSupported ||
+            e == hipErrorCooperativeLaunchTooLarge) {
+            (void)hipGetLastError();
+            return kDsCoopRefused;
+        }
+    } else {
         e = hipLaunchKernel(fn, dim3(p.nwg), dim3(kT), args, 0, st);
     }
-    if (e != hipSuccess) return hip_fail(e, "launch of decode_step_kernel"); 
+    if (e != hipSuccess) return hip_fail(e, "launch of decode_step_kernel");
     return TENZO_SUCCESS;
 }
 

@@ -27,6 +27,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -132,7 +133,13 @@ struct tenzo_engine_opaque {
     uint64_t* ds_trace = nullptr;  // step trace (tenzo_hip_engine_trace), null when off
     bool ds_state_valid = false;   // the last step ran the persistent kernel
     bool ds_coop = false;          // cooperative launches (after an ordinary one aborted)
-    unsigned ds_spin = kDsSpinLimit;  // TENZO_HIP_SPIN_LIMIT: polls before a wait gives up
+    unsigned* ds_bar = nullptr;    // grid-barrier counters + error word (uncached, bar_pool)
+    unsigned ds_bar_base = 0;      // barrier generations completed by earlier launches
+    bool ds_bar_reset = true;      // zero the counters before the next launch
+    // polls before a wait gives up, under an ordinary launch (TENZO_HIP_SPIN_LIMIT)
+    // and under the cooperative one (TENZO_HIP_SPIN_LIMIT_COOP)
+    unsigned ds_spin = kDsSpinLimit;
+    unsigned ds_spin_coop = kDsSpinLimit;
 
     // batched prefill (tenzo_hip_engine_prefill): rows of up to pf_cap tokens
     int pf_cap = 0;
@@ -148,6 +155,46 @@ struct tenzo_engine_opaque {
 };
 
 namespace {
+
+// Grid-barrier regions of the persistent kernel: uncached device memory (the
+// kernel polls it with scalar loads, which must miss every cache). Uncached
+// memory that a kernel has read is never freed here: a region returns to this
+// pool when its engine is destroyed and is handed to the next engine made on
+// the same device; the pool lives until the process ends.
+struct BarPool {
+    std::mutex mu;
+    std::vector<std::pair<int, unsigned*>> free;  // (device, region)
+};
+BarPool& bar_pool() {
+    static BarPool* pool = new BarPool();  // never destroyed (outlives every engine)
+    return *pool;
+}
+constexpr size_t kBarBytes = (size_t)kDsBarWords * 4;
+
+int bar_take(int dev, unsigned** out) {
+    BarPool& bp = bar_pool();
+    {
+        std::lock_guard<std::mutex> g(bp.mu);
+        for (size_t i = 0; i < bp.free.size(); ++i)
+            if (bp.free[i].first == dev) {
+                *out = bp.free[i].second;
+                bp.free.erase(bp.free.begin() + (long)i);
+                return TENZO_SUCCESS;
+            }
+    }
+    void* v = nullptr;
+    TZ_HIP(hipExtMallocWithFlags(&v, kBarBytes, hipDeviceMallocUncached));
+    TZ_HIP(hipMemset(v, 0, kBarBytes));
+    *out = static_cast<unsigned*>(v);
+    return TENZO_SUCCESS;
+}
+
+void bar_give(int dev, unsigned* region) {
+    if (!region) return;
+    BarPool& bp = bar_pool();
+    std::lock_guard<std::mutex> g(bp.mu);
+    bp.free.emplace_back(dev, region);
+}
 
 int alloc_tracked(tenzo_engine_t e, void** p, size_t bytes, bool zero) {
     void* v = nullptr;
@@ -748,6 +795,7 @@ int enqueue_prefill_layer(tenzo_engine_t e, int l, int pos0, int m, bool exact) 
 // calls (bit for bit when exact, else up to the streaming attention's
 // softmax rounding).
 int run_step(tenzo_engine_t e, int token, bool head);
+int run_step_sync(tenzo_engine_t e, int token, bool head);
 
 // PagedBlockManager::reset (TenzoEngine.h:127-133) and the table's reset.
 void pg_reset(tenzo_engine_t e) {
@@ -798,8 +846,7 @@ int run_prefill(tenzo_engine_t e, const int32_t* tokens, int n, bool exact) {
         // the batched pass appends INT8 rows; a ternary cache is filled by
         // decode steps without the LM head (tenzo_prefill_token per token)
         for (int i = 0; i < n; ++i) {
-            if ((rc = run_step(e, tokens[i], false))) return rc;
-            TZ_HIP(hipStreamSynchronize(e->st));
+            if ((rc = run_step_sync(e, tokens[i], false))) return rc;
             e->seq_len += 1;
         }
         return TENZO_SUCCESS;
@@ -912,26 +959,51 @@ int run_persistent(tenzo_engine_t e, bool head, int pos, int32_t* out_tokens = n
     p.with_head = head ? 1 : 0;
     p.eps = e->eps;
     p.trace = e->ds_trace;
-    p.spin_limit = e->ds_spin;
+    p.spin_limit = e->ds_coop ? e->ds_spin_coop : e->ds_spin;
     p.out_tokens = out_tokens;
     p.step = step;
+    // barrier targets stay below 2^31: (base + barriers) * workgroups per counter
+    const uint64_t per = (uint64_t)(e->ds_nwg / kDsCounters);
+    if (e->ds_bar_reset || ((uint64_t)e->ds_bar_base + ds_barriers(e->L)) * per >= (1ull << 31)) {
+        TZ_HIP(hipMemsetAsync(e->ds_bar, 0, (size_t)kDsBarWords * 4, e->st));
+        e->ds_bar_base = 0;
+        e->ds_bar_reset = false;
+    }
+    p.bar = e->ds_bar;
+    p.bar_base = e->ds_bar_base;
     TZ_HIP(hipMemsetAsync(e->ds_sync, 0, e->ds_sync_bytes, e->st));
     rc = launch_decode_step(p, e->Hq / e->Hkv, e->ds_coop, e->st);
     e->ds_state_valid = rc == TENZO_SUCCESS;
+    if (rc == TENZO_SUCCESS) e->ds_bar_base += ds_barriers(e->L);
     return rc;
 }
 
 // After persistent steps: the kernel's abort flag (io[3], set when a wait
 // timed out and a step was abandoned; cleared by the host before the steps),
 // copied next to the result token. An abort under an ordinary launch can mean
-// that the grid was not all resident (other work on the device), so the
-// engine's later steps use the cooperative launch.
+// that the grid was not all resident (other work on the device). An aborted
+// step leaves nothing behind that a rerun does not rewrite: the sequence
+// length is advanced by the host only after a good step, the step's KV rows
+// at its position are appended again, its input token (io[0]) is written only
+// by a step that completed, and the sync area and accumulators are cleared
+// before every launch. So ds_retry, called after such an abort, moves the
+// engine to the cooperative launch (all workgroups resident, guaranteed) and
+// says whether the caller should rerun the step(s) once; ds_check then reports
+// an abort that remains.
+bool ds_retry(tenzo_engine_t e) {
+    if (e->io_host[3] != 0) e->ds_bar_reset = true;  // the counters stopped part-way
+    if (e->io_host[3] == 0 || e->ds_coop) return false;
+    e->ds_coop = true;
+    e->io_host[3] = 0;
+    return true;
+}
+
 int ds_check(tenzo_engine_t e) {
     if (e->io_host[3] != 0) {
-        const bool was_coop = e->ds_coop;
-        e->ds_coop = true;
-        set_error("decode step aborted: an in-kernel wait timed out (engine state is invalid)%s",
-                  was_coop ? "" : "; later steps use a cooperative launch");
+        e->ds_state_valid = false;
+        e->ds_bar_reset = true;
+        set_error("decode step aborted: an in-kernel wait timed out under the cooperative "
+                  "launch (engine state is invalid: reset or re-prefill)");
         return TENZO_ERROR_UNSUPPORTED;
     }
     return TENZO_SUCCESS;
@@ -962,10 +1034,20 @@ int run_step(tenzo_engine_t e, int token, bool head) {
     TZ_HIP(hipMemcpyAsync(e->io_dev, e->io_host, 16, hipMemcpyHostToDevice, e->st));
     int rc;
     e->ds_state_valid = false;
+    bool graph = e->mode == 1;
     if (e->mode == 2 && ds_usable(e)) {
-        if ((rc = run_persistent(e, head, pos))) return rc;
-        TZ_HIP(hipMemcpyAsync(e->io_host + 3, e->io_dev + 3, 4, hipMemcpyDeviceToHost, e->st));
+        rc = run_persistent(e, head, pos);
+        if (rc == kDsCoopRefused) {
+            graph = true;  // this step on the stage kernels instead
+        } else {
+            if (rc) return rc;
+            TZ_HIP(hipMemcpyAsync(e->io_host + 3, e->io_dev + 3, 4, hipMemcpyDeviceToHost,
+                                  e->st));
+        }
     } else if (e->mode >= 1) {
+        graph = true;
+    }
+    if (graph) {
         const int max_chunks = (int)ceil_div(e->max_seq, T);
         auto key = std::make_pair(T, head ? 1 : 0);
         auto it = e->graphs.find(key);
@@ -986,10 +1068,22 @@ int run_step(tenzo_engine_t e, int token, bool head) {
             it = e->graphs.emplace(key, ex).first;
         }
         TZ_HIP(hipGraphLaunch(it->second, e->st));
-    } else {
+    } else if (e->mode == 0) {
         if ((rc = enqueue_step(e, head, T, (int)ceil_div(pos + 1, T)))) return rc;
     }
     return TENZO_SUCCESS;
+}
+
+// run_step, synchronized, rerun once under the cooperative launch when the
+// persistent kernel aborted under an ordinary one (ds_retry).
+int run_step_sync(tenzo_engine_t e, int token, bool head) {
+    for (int attempt = 0;; ++attempt) {
+        int rc = run_step(e, token, head);
+        if (rc) return rc;
+        TZ_HIP(hipStreamSynchronize(e->st));
+        if (attempt > 0 || !ds_retry(e)) break;
+    }
+    return ds_check(e);
 }
 
 }  // namespace
@@ -1053,11 +1147,15 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
     auto* e = new tenzo_engine_opaque();
     e->cfg = c;
     // a smaller in-kernel poll budget (tests force the abort path with it)
-    if (const char* sl = std::getenv("TENZO_HIP_SPIN_LIMIT")) {
-        char* end = nullptr;
-        const unsigned long v = std::strtoul(sl, &end, 10);
-        if (end != sl && v <= kDsSpinLimit) e->ds_spin = (unsigned)v;
-    }
+    auto spin_env = [](const char* name, unsigned* out) {
+        if (const char* sl = std::getenv(name)) {
+            char* end = nullptr;
+            const unsigned long v = std::strtoul(sl, &end, 10);
+            if (end != sl && v <= kDsSpinLimit) *out = (unsigned)v;
+        }
+    };
+    spin_env("TENZO_HIP_SPIN_LIMIT", &e->ds_spin);
+    spin_env("TENZO_HIP_SPIN_LIMIT_COOP", &e->ds_spin_coop);
     e->kv_mode = kv;
     e->kv_kind = kv_kind;
     e->kv_row = kv_kind == 0 || kv_kind == 3 ? kD : 32;
@@ -1124,7 +1222,8 @@ TENZO_API tenzo_engine_t tenzo_create_engine(const tenzo_config_t* config) {
                  !alloc_t(e, &e->ds_sync, e->ds_sync_bytes, true) &&
                  !alloc_t(e, &e->ds_vec, ds_vec_floats(e->L, e->H, Hq) * 4) &&
                  !alloc_t(e, &e->ds_part, (size_t)Hkv * cmax * G * kDsPartStride * 4) &&
-                 !alloc_t(e, &e->ds_am, (size_t)e->ds_nwg * sizeof(float2));
+                 !alloc_t(e, &e->ds_am, (size_t)e->ds_nwg * sizeof(float2)) &&
+                 !bar_take(e->dev, &e->ds_bar);
         }
     }
     if (!ok) {
@@ -1140,6 +1239,7 @@ TENZO_API void tenzo_destroy_engine(tenzo_engine_t e) {
     if (e->st) (void)hipStreamSynchronize(e->st);
     drop_graphs(e);
     for (void* p : e->allocs) (void)hipFree(p);
+    bar_give(e->dev, e->ds_bar);
     if (e->ds_trace) (void)hipFree(e->ds_trace);
     if (e->dec_out) (void)hipFree(e->dec_out);
     if (e->io_host) (void)hipHostFree(e->io_host);
@@ -1263,13 +1363,8 @@ TENZO_API tenzo_status_t tenzo_load_model(tenzo_engine_t e, const char* weights_
 
 TENZO_API tenzo_status_t tenzo_prefill_token(tenzo_engine_t e, int token) {
     if (!e) return TENZO_ERROR_INVALID_ARGUMENT;
-    int rc = run_step(e, token, false);
+    const int rc = run_step_sync(e, token, false);
     if (rc) return (tenzo_status_t)rc;
-    if (hipStreamSynchronize(e->st) != hipSuccess) {
-        set_error("prefill_token: %s", hipGetErrorString(hipGetLastError()));
-        return TENZO_ERROR_UNSUPPORTED;
-    }
-    if ((rc = ds_check(e))) return (tenzo_status_t)rc;
     e->seq_len += 1;  // :1816-1818
     return TENZO_SUCCESS;
 }
@@ -1279,6 +1374,9 @@ TENZO_HIP_API int tenzo_hip_engine_prefill(tenzo_engine_t e, const int32_t* toke
     if (!e) return TENZO_ERROR_INVALID_ARGUMENT;
     return run_prefill(e, tokens, n, exact != 0);
 }
+
+static int generate_once(tenzo_engine_t e, int cur_token, float temperature, float top_p,
+                         int top_k, float penalty, const int* past, int past_len, float draw);
 
 TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,
                                   const tenzo_sampling_params_t* params, const int* past,
@@ -1293,6 +1391,26 @@ TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,
         set_error("generate_step: sampling supports vocabularies up to 262144");
         return -1;
     }
+    // the draw of :1797, from the process's rand() as in the reference (taken
+    // once, so a step rerun after an abort uses the same draw)
+    const float draw = temperature > 0.0f
+                           ? static_cast<float>(rand()) / static_cast<float>(RAND_MAX)
+                           : 0.0f;
+    for (int attempt = 0;; ++attempt) {
+        if (generate_once(e, cur_token, temperature, top_p, top_k, penalty, past, past_len,
+                          draw))
+            return -1;
+        if (attempt > 0 || !ds_retry(e)) break;
+    }
+    if (ds_check(e)) return -1;
+    e->seq_len += 1;  // :1833-1835
+    return e->io_host[2];
+}
+
+// One decode step of tenzo_generate_step with its penalty and sampling,
+// synchronized (0, or -1 with the error set).
+static int generate_once(tenzo_engine_t e, int cur_token, float temperature, float top_p,
+                         int top_k, float penalty, const int* past, int past_len, float draw) {
     if (run_step(e, cur_token, true)) return -1;
     if (penalty != 1.0f && past && past_len > 0) {
         // :1735-1743 on the device, then the greedy argmax again
@@ -1317,25 +1435,53 @@ TENZO_API int tenzo_generate_step(tenzo_engine_t e, int cur_token,
             (temperature <= 0.0f && launch_argmax(e->logits, e->V, am, st)))
             return -1;
     }
-    if (temperature > 0.0f) {
-        // the draw of :1797, from the process's rand() as in the reference
-        const float r = static_cast<float>(rand()) / static_cast<float>(RAND_MAX);
-        if (launch_sample(e->logits, e->V, top_k, top_p, temperature, r, e->sample_ws,
-                          e->io_dev + 2, e->st))
-            return -1;
-    }
+    if (temperature > 0.0f &&
+        launch_sample(e->logits, e->V, top_k, top_p, temperature, draw, e->sample_ws,
+                      e->io_dev + 2, e->st))
+        return -1;
     if (hipMemcpyAsync(e->io_host + 2, e->io_dev + 2, 4, hipMemcpyDeviceToHost, e->st) !=
             hipSuccess ||
         hipStreamSynchronize(e->st) != hipSuccess) {
         set_error("generate_step: %s", hipGetErrorString(hipGetLastError()));
         return -1;
     }
-    if (ds_check(e)) return -1;
-    e->seq_len += 1;  // :1833-1835
-    return e->io_host[2];
+    return 0;
 }
 
 // ---- engine extensions (include/tenzo_hip.h) ----
+
+// Enqueues steps i0 .. n-1 of a chained decode (step i at position seq_len + i,
+// the first step's token in io[0]), the persistent kernel when `persistent`;
+// a cooperative launch the runtime refuses moves the rest of the chain to the
+// stage kernels.
+static int enqueue_chain(tenzo_engine_t e, int i0, int n, bool persistent) {
+    bool pos_set = false;
+    for (int i = i0; i < n; ++i) {
+        const int pos = e->seq_len + i;
+        int rc;
+        if (persistent) {
+            rc = run_persistent(e, true, pos, e->dec_out, i);
+            if (rc != kDsCoopRefused) {
+                if (rc) return rc;
+                continue;
+            }
+            persistent = false;
+        }
+        // stage kernels: token and position chained on the device
+        const int T = attn_pick_chunk(pos + 1, e->Hkv, 1);
+        if (!pos_set) {
+            e->io_host[1] = pos;
+            TZ_HIP(hipMemcpyAsync(e->io_dev + 1, e->io_host + 1, 4, hipMemcpyHostToDevice,
+                                  e->st));
+            pos_set = true;
+        }
+        if ((rc = enqueue_step(e, true, T, (int)ceil_div(pos + 1, T)))) return rc;
+        hipLaunchKernelGGL(chain_kernel, dim3(1), dim3(64), 0, e->st, e->io_dev,
+                           e->dec_out + i);
+        if ((rc = launch_status("chain_kernel"))) return rc;
+    }
+    return TENZO_SUCCESS;
+}
 
 TENZO_HIP_API int tenzo_hip_engine_decode(tenzo_engine_t e, int token, int n, int32_t* out,
                                           float* ms) {
@@ -1359,50 +1505,40 @@ TENZO_HIP_API int tenzo_hip_engine_decode(tenzo_engine_t e, int token, int n, in
         TZ_HIP(hipMalloc(&e->dec_out, (size_t)n * 4));
         e->dec_cap = n;
     }
+    const bool persistent = e->mode == 2 && ds_usable(e);
     hipEvent_t t0 = nullptr, t1 = nullptr;
     TZ_HIP(hipEventCreate(&t0));
     TZ_HIP(hipEventCreate(&t1));
-    e->io_host[0] = token;
-    e->io_host[3] = 0;
-    int rc = TENZO_SUCCESS;
-    if (hipMemcpyAsync(e->io_dev, e->io_host, 4, hipMemcpyHostToDevice, e->st) != hipSuccess ||
-        hipMemcpyAsync(e->io_dev + 3, e->io_host + 3, 4, hipMemcpyHostToDevice, e->st) !=
-            hipSuccess ||
-        hipEventRecord(t0, e->st) != hipSuccess)
-        rc = TENZO_ERROR_UNSUPPORTED;
-    const bool persistent = e->mode == 2 && ds_usable(e);
-    for (int i = 0; i < n && !rc; ++i) {
-        const int pos = e->seq_len + i;
-        if (persistent) {
-            rc = run_persistent(e, true, pos, e->dec_out, i);
-        } else {
-            // stage kernels: token and position chained on the device
-            const int T = attn_pick_chunk(pos + 1, e->Hkv, 1);
-            if (i == 0) {
-                e->io_host[1] = pos;
-                if (hipMemcpyAsync(e->io_dev + 1, e->io_host + 1, 4, hipMemcpyHostToDevice,
-                                   e->st) != hipSuccess) {
-                    rc = TENZO_ERROR_UNSUPPORTED;
-                    break;
-                }
-            }
-            rc = enqueue_step(e, true, T, (int)ceil_div(pos + 1, T));
-            if (!rc) {
-                hipLaunchKernelGGL(chain_kernel, dim3(1), dim3(64), 0, e->st, e->io_dev,
-                                   e->dec_out + i);
-                rc = launch_status("chain_kernel");
-            }
-        }
+    // Every step that completes stores its token in dec_out; a persistent step
+    // that aborts stores none and the steps after it return at once (io[3]),
+    // so the first -1 marks where a rerun starts.
+    auto attempt = [&](int i0, int tok, bool first) -> int {
+        e->io_host[0] = tok;
+        e->io_host[3] = 0;
+        if (hipMemcpyAsync(e->io_dev, e->io_host, 4, hipMemcpyHostToDevice, e->st) != hipSuccess ||
+            hipMemcpyAsync(e->io_dev + 3, e->io_host + 3, 4, hipMemcpyHostToDevice, e->st) !=
+                hipSuccess ||
+            (persistent && hipMemsetAsync(e->dec_out + i0, 0xff, (size_t)(n - i0) * 4, e->st) !=
+                               hipSuccess) ||
+            (first && hipEventRecord(t0, e->st) != hipSuccess))
+            return TENZO_ERROR_UNSUPPORTED;
+        int rc = enqueue_chain(e, i0, n, persistent);
+        if (rc) return rc;
+        if (hipEventRecord(t1, e->st) != hipSuccess ||
+            (persistent && hipMemcpyAsync(e->io_host + 3, e->io_dev + 3, 4,
+                                          hipMemcpyDeviceToHost, e->st) != hipSuccess) ||
+            hipMemcpyAsync(out + i0, e->dec_out + i0, (size_t)(n - i0) * 4,
+                           hipMemcpyDeviceToHost, e->st) != hipSuccess ||
+            hipStreamSynchronize(e->st) != hipSuccess)
+            return TENZO_ERROR_UNSUPPORTED;
+        return TENZO_SUCCESS;
+    };
+    int rc = attempt(0, token, true);
+    if (!rc && persistent && ds_retry(e)) {
+        int k = 0;
+        while (k < n && out[k] >= 0) ++k;
+        rc = k < n ? attempt(k, k == 0 ? token : out[k - 1], false) : TENZO_SUCCESS;
     }
-    if (!rc && hipEventRecord(t1, e->st) != hipSuccess) rc = TENZO_ERROR_UNSUPPORTED;
-    if (!rc && persistent)
-        if (hipMemcpyAsync(e->io_host + 3, e->io_dev + 3, 4, hipMemcpyDeviceToHost, e->st) !=
-            hipSuccess)
-            rc = TENZO_ERROR_UNSUPPORTED;
-    if (!rc && hipMemcpyAsync(out, e->dec_out, (size_t)n * 4, hipMemcpyDeviceToHost, e->st) !=
-                   hipSuccess)
-        rc = TENZO_ERROR_UNSUPPORTED;
-    if (hipStreamSynchronize(e->st) != hipSuccess && !rc) rc = TENZO_ERROR_UNSUPPORTED;
     if (!rc && ms) (void)hipEventElapsedTime(ms, t0, t1);
     (void)hipEventDestroy(t0);
     (void)hipEventDestroy(t1);

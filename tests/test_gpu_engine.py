@@ -165,35 +165,61 @@ def test_chained_decode_equals_steps(eng_mod, mode):
 
 def test_persistent_abort_is_reported(eng_mod, monkeypatch):
     """Failure handling, forced from the host: with an in-kernel poll budget of
-    zero (TENZO_HIP_SPIN_LIMIT=0, read when the engine is made) the first wait
-    that finds its condition unmet gives up, every workgroup leaves the kernel
-    at its next poll, and the call reports the timeout instead of a token --
-    in a chained decode (the flag is not cleared between its steps) and in a
-    single step. The first report moves the engine to the cooperative launch.
-    An engine made without the variable decodes beside it as usual."""
+    zero the first wait that finds its condition unmet gives up and every
+    workgroup leaves the kernel at its next poll. TENZO_HIP_SPIN_LIMIT sets the
+    budget under the ordinary launch and TENZO_HIP_SPIN_LIMIT_COOP under the
+    cooperative one (both read when the engine is made).
+
+    With both at zero, the step that aborted under the ordinary launch is
+    rerun once under the cooperative launch, aborts again, and the call
+    reports the timeout instead of a token -- in a chained decode and in a
+    single step -- and the per-layer state is refused afterwards."""
     sm = synth.make_model(CFG, seed=61, ctx=11)
     monkeypatch.setenv("TENZO_HIP_SPIN_LIMIT", "0")
+    monkeypatch.setenv("TENZO_HIP_SPIN_LIMIT_COOP", "0")
     a = eng_mod.Engine(CFG)
     monkeypatch.delenv("TENZO_HIP_SPIN_LIMIT")
-    with a, eng_mod.Engine(CFG) as b:
+    monkeypatch.delenv("TENZO_HIP_SPIN_LIMIT_COOP")
+    with a:
+        a.set_model(sm)
+        a.set_mode("persistent")
+        with pytest.raises(RuntimeError, match="timed out.*cooperative"):
+            a.decode(7, 3)
+        with pytest.raises(RuntimeError, match="last step did not run"):
+            a.layer_state(0, "x")
+        with pytest.raises(RuntimeError, match="timed out"):
+            a.step(7)
+
+
+def test_persistent_abort_recovers(eng_mod, monkeypatch):
+    """An abort under the ordinary launch (its poll budget forced to zero) is
+    recovered within the call: the step that aborted -- and, in a chained
+    decode, every step after it, which returned at entry -- is rerun under
+    the cooperative launch (full budget), so the reference API still returns
+    the token. Tokens equal the oracle's greedy chain, and the hidden state
+    after the recovered steps equals the oracle's to 1e-3."""
+    sm = synth.make_model(CFG, seed=61, ctx=11)
+    om = oracle.OracleModel(sm, f16_kv_scales=True)
+    ref, t = [], 7
+    for i in range(5):
+        t, _, hidden = om.step(t, sm.ctx + i, CFG.theta)
+        ref.append(t)
+    monkeypatch.setenv("TENZO_HIP_SPIN_LIMIT", "0")
+    a = eng_mod.Engine(CFG)
+    b = eng_mod.Engine(CFG)
+    monkeypatch.delenv("TENZO_HIP_SPIN_LIMIT")
+    with a, b:
         a.set_model(sm)
         b.set_model(sm)
         a.set_mode("persistent")
         b.set_mode("persistent")
-        with pytest.raises(RuntimeError, match="timed out.*cooperative launch"):
-            a.decode(7, 3)
-        with pytest.raises(RuntimeError) as ei:
-            a.step(7)
-        assert "timed out" in str(ei.value) and "cooperative" not in str(ei.value)
-        toks, _ = b.decode(7, 3)
-        ref, t = [], 7
-        with eng_mod.Engine(CFG) as c:
-            c.set_model(sm)
-            c.set_mode("persistent")
-            for _ in range(3):
-                t = c.step(t)
-                ref.append(t)
-        assert list(toks) == ref
+        toks, _ = a.decode(7, 3)
+        assert list(toks) == ref[:3]
+        toks2, _ = a.decode(int(toks[-1]), 2)  # (now on the cooperative launch)
+        assert list(toks2) == ref[3:]
+        assert rel(a.buffer("x"), hidden) < 1e-3
+        assert b.step(7) == ref[0]
+        assert b.step(ref[0]) == ref[1]
 
 
 def test_engine_first_layer_stages_bit_exact(eng_mod):
