@@ -30,7 +30,15 @@ import os
 import sys
 import time
 
-import numpy as np
+# The reference CPU legs (the compiled reference engine in this process, the
+# single-kernel configs in a child) run with OpenMP threads placed one per
+# core and spread, as the reference's Makefile runs its benchmarks; OpenMP
+# reads these once, when its runtime starts, so they are set before anything
+# loads it (a caller's own setting wins).
+os.environ.setdefault("OMP_PLACES", "cores")
+os.environ.setdefault("OMP_PROC_BIND", "spread")
+
+import numpy as np  # noqa: E402
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -650,16 +658,25 @@ def configs_bench(torch):
     gen = torch.Generator(device="cuda")
     gen.manual_seed(SEED + 7)
     out = {}
-    # config 1: one TL1 GEMV, 6912 x 2560
+    # config 1: one TL1 GEMV, 6912 x 2560, on fp32 activations: the per-token
+    # absmax quantization and the GEMV (build_lut + compute_from_lut, the unit
+    # the CPU leg times), one launch (tl1_gemv_f32_kernel); fp32 in, fp32 out
     N, K = 6912, 2560
     nb = ops.tl1_packed_bytes(N, K)
     c = _copies(nb)
     W = tl1_random_dev(torch, c * nb, gen).view(c, nb)
-    codes, q, _ = ops.rmsnorm_quant31(torch.randn(K, device="cuda", generator=gen))
+    xa = torch.randn(K, device="cuda", generator=gen)
     y = torch.empty(N, device="cuda")
+    P_ = ops._ptr
+    t = _per_call(torch, [lambda i=i: L.tenzo_hip_bitlinear_tl1_f32(P_(xa), P_(W[i]), 0.0159, 1, N,
+                                                                     K, P_(y), S())
+                          for i in range(c)])
+    out["c1_tl1_6912x2560"] = _entry(N * K // 4 + K * 4 + N * 4, t, c)
+    # the GEMV alone on codes quantized once (int8 codes in)
+    codes, q, _ = ops.rmsnorm_quant31(xa)
     t = _per_call(torch, [lambda i=i: ops.bitlinear_tl1_into(codes, q, W[i], 0.0159, N, K, y)
                           for i in range(c)])
-    out["c1_tl1_6912x2560"] = _entry(N * K // 4 + K + N * 4, t, c)
+    out["c1_tl1_6912x2560_codes_in"] = _entry(N * K // 4 + K + N * 4, t, c)
     # the same GEMV by the reference's table method (LDS tables per activation
     # pair, v_perm lookups): the measurement behind the masked-v_dot4 choice
     t = _per_call(torch, [lambda i=i: ops.bitlinear_tl1_lut(codes, q, W[i], 0.0159, N, K, y=y)

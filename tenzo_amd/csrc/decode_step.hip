@@ -341,28 +341,35 @@ __device__ __forceinline__ void poll_bar(const unsigned* base, unsigned& lo, uns
     for (int i = 1; i < 16; ++i) lo = c[i] < lo ? c[i] : lo;
 }
 
-// Grid barrier: every wave waits for its stores' acknowledgements, thread 0
-// adds the workgroup's arrival to counter wg % kNC (the counters carry on
-// across launches: generation bar_base + gen is complete when each holds
-// (bar_base + gen) * nwg / kNC), then `issue` starts the next stage's loads
-// that depend on nothing of this stage (its weight tile) and wave 0 polls the
-// counters with scalar loads while those loads are in flight. The arrival goes
-// out before any wave's prefetch (a second block barrier), so it never waits
-// behind them in the CU's memory pipeline. Every wait is bounded.
-// `touched` is the result of touch_norm's load: taken as an operand here,
-// where every load of the wave has completed, it keeps the load without
-// computing anything from it.
-template <class Issue>
-__device__ __forceinline__ bool grid_barrier(const DsParams& p, unsigned& gen, int* s_abort,
-                                             int touched, Issue&& issue) {
-    ++gen;
+// Grid barrier, in two halves. bar_arrive: every wave waits for its stores'
+// acknowledgements, thread 0 adds the workgroup's arrival to counter wg % kNC
+// (the counters carry on across launches: generation bar_base + gen is complete
+// when each holds (bar_base + gen) * nwg / kNC) and stamps the trace. bar_wait:
+// `issue` starts the next stage's loads that depend on nothing of this stage
+// (its weight tile) and wave 0 polls the counters with scalar loads while those
+// loads are in flight. The arrival goes out before any wave's prefetch (a block
+// barrier between them), so it never waits behind them in the CU's memory
+// pipeline. Every wait is bounded. A workgroup whose stage work produces
+// nothing that the barrier must cover (a record writer without a task) arrives
+// before that work and waits after it.
+// `touched` is the result of touch_norm's load: taken as an operand where
+// every load of the wave has completed, it keeps the load without computing
+// anything from it.
+__device__ __forceinline__ void bar_arrive(const DsParams& p, int s, int touched) {
     __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are acknowledged
     asm volatile("" ::"v"(touched));
     __syncthreads();
-    if (threadIdx.x == 0)
+    if (threadIdx.x == 0) {
+        if (p.trace) p.trace[((size_t)s * p.nwg + blockIdx.x) * 2] = wall_clock64();
         __hip_atomic_fetch_add(p.bar + (blockIdx.x % kNC) * 64, 1u, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
+    }
     __builtin_amdgcn_s_barrier();
+}
+
+template <class Issue>
+__device__ __forceinline__ bool bar_wait(const DsParams& p, unsigned gen, int* s_abort,
+                                         Issue&& issue) {
     issue();
     if (lwave() == 0) {
         const unsigned target = (p.bar_base + gen) * (unsigned)(p.nwg / kNC);
@@ -505,6 +512,24 @@ __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[
     }
 }
 
+// The fp16 K / V scales of load_att_tile's tokens (INT8 cache; tokens past the
+// chunk read zeros), for a chunk whose rows were prefetched.
+__device__ __forceinline__ void load_att_scales(uint32_t (&pfs)[2 * kAR], const DsParams& p, int l,
+                                                int h, int c) {
+    const int lane = ltid() & 63, wave = lwave();
+    const int t0 = c * p.T;
+    const int nt = min(p.T, p.pos + 1 - t0);
+    const size_t tok0 = ((size_t)l * p.Hkv + h) * p.max_seq + t0;
+    const __amdgpu_buffer_rsrc_t rks = rsrc(p.ks + tok0, (uint32_t)nt * 2);
+    const __amdgpu_buffer_rsrc_t rvs = rsrc(p.vs + tok0, (uint32_t)nt * 2);
+#pragma unroll
+    for (int r = 0; r < kAR; ++r) {
+        const int tl = r * kRT + wave * 8 + (lane >> 3);
+        pfs[2 * r] = ld2(rks, (uint32_t)tl * 2);
+        pfs[2 * r + 1] = ld2(rvs, (uint32_t)tl * 2);
+    }
+}
+
 // Norm weights (thread t: float4 groups t + kT j; zeros past K) into registers.
 __device__ __forceinline__ void load_norm_w(float4 (&w)[kJ], const float* nw, int K) {
     const __amdgpu_buffer_rsrc_t r = rsrc(nw, nw ? (uint32_t)K * 4 : 0u);
@@ -524,6 +549,28 @@ __device__ __forceinline__ void read_rec(const DsParams& p, int l, int slot, flo
     const __amdgpu_buffer_rsrc_t r = rsrc(p.sync + w_rec(l, slot, p.L, p.Hkv), 8);
     inv = __int_as_float(ld4i(r, 0));
     csum = ld4i(r, 4);
+}
+
+// The inv_scale half of the code record (l, slot) when its writer may publish
+// it after the grid barrier (the down stage's writer arrives before its work,
+// bar_arrive): the bits the stage input brought (inv_bits) when already
+// nonzero (records are zeroed before each launch and inv_scale >= 1e-6 / 31),
+// else polled with device-coherent loads. Bounded: on a timeout the error word
+// is raised and the bits returned are 0 (the step is abandoned at the next
+// barrier).
+__device__ __forceinline__ int wait_rec_inv(const DsParams& p, int l, int slot, int inv_bits) {
+    inv_bits = __builtin_amdgcn_readfirstlane(inv_bits);
+    if (inv_bits != 0) return inv_bits;
+    const unsigned* r = p.sync + w_rec(l, slot, p.L, p.Hkv);
+    unsigned spins = 0;
+    while ((inv_bits = (int)__builtin_amdgcn_readfirstlane(ldcu(r))) == 0) {
+        if (++spins > p.spin_limit) {
+            raise_abort(p);
+            break;
+        }
+        if ((spins & 63) == 0 && ldcu(err_word(p)) != 0) break;
+    }
+    return inv_bits;
 }
 
 // Element of a GEMV output from its accumulator (TenzoEngine.cpp:1554,
@@ -1017,13 +1064,29 @@ __device__ __forceinline__ bool rec_writer(const DsParams& p, int first, int n) 
     return n < p.nwg ? first == n : first == 0;
 }
 
+// Whether the record writer of GEMV stage `kind` of layer l arrives at the
+// grid barrier before its work (its sequential sum of squares, 864 dependent
+// steps at hidden 2560 / FFN 6912, would otherwise decide when the barrier
+// completes): the down stage's writer when it has no task and the next layer's
+// Q|K|V stage leaves a workgroup without a task (the stage after the down
+// stage is offset by one more, so that this writer is the last workgroup of
+// Q|K|V and idle there while it finishes). The Q|K|V stage polls the record.
+__device__ __forceinline__ bool early_writer(const DsParams& p, int kind, int l) {
+    return kind == S_DOWN && l < p.L - 1 && ntasks(p, S_DOWN) < p.nwg &&
+           ntasks(p, S_QKV) < p.nwg - 1;
+}
+
 // One GEMV stage (QKV, O, GU or DOWN) of layer l for a workgroup whose first
 // task is `first` (< n, or the record writer): builds the stage input, stores
 // the slices of it later stages read, quantizes its normalization (exactly,
 // with the record, in the record writer; the codes alone elsewhere) and adds
 // its tasks' K-slice sums into the accumulators.
-__device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l,
-                                          int first, int n, uint4 (&tile)[kPF]) {
+// Returns true when the workgroup has already arrived at the grid barrier that
+// follows the stage (through arrive(), early_writer).
+template <class Arrive>
+__device__ __forceinline__ bool tl1_stage(SharedAll& sh, const DsParams& p, int kind, int l,
+                                          int first, int n, uint4 (&tile)[kPF],
+                                          Arrive&& arrive) {
     Shared& s = sh.s;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
     const LayerRef Lw = layer(p, l);
@@ -1068,10 +1131,12 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     const bool rec = rec_writer(p, first, n);
     float4 xv[kJ];
     if (kind == S_QKV) {
-        if (l == 0)
+        if (l == 0) {
             finish_embed(xv, in, p);
-        else
+        } else {
+            in.inv = wait_rec_inv(p, l - 1, 3, in.inv);
             finish_resid(xv, in, K, layer(p, l - 1).sc(6));
+        }
         store_slices(p.xs + (size_t)l * p.H, xv, K, 0, first, m);
     } else if (kind == S_O) {
         finish_plain(xv, in, K);
@@ -1089,8 +1154,12 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
     const bool single = n < p.nwg;
     unsigned* recw = p.sync + w_rec(l, slot, p.L, p.Hkv);
     if (rec && single) {
+        // (the down stage's writer arrives first: its record is polled for)
+        const bool early = early_writer(p, kind, l);
+        if (early) arrive();
         const float inv = norm_record_inv31(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps);
         if (tid == 0) stcu(recw, __float_as_uint(inv));
+        return early;
     } else if (rec) {
         float inv;
         int csum;
@@ -1121,6 +1190,7 @@ __device__ __forceinline__ void tl1_stage(SharedAll& sh, const DsParams& p, int 
                                        __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+    return false;
 }
 
 // ----------------------------------------------------------- attention ----
@@ -1256,7 +1326,11 @@ __device__ __forceinline__ bool paged_weights(AttnShared& a, const DsParams& p, 
 // waits until every chunk of its kv head has, and forms the normalized
 // weights from the combined statistics; the partials are then plain sums.
 template <int G, int KVM>
-__device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c) {
+// cur: the chunk's K / V tile registers; with `pre` (INT8 cache only) they
+// already hold the rows of this chunk, issued during the grid barrier before
+// the stage (prefetch_next), and only their scales are loaded here.
+__device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int l, int h, int c,
+                                          uint4 (&cur)[kPF], bool pre) {
     constexpr bool PAGED = KVM == 3, TERN = KVM == 1 || KVM == 2;
     AttnShared& a = sh.a;
     const int tid = ltid(), lane = tid & 63, wave = lwave();
@@ -1296,7 +1370,6 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
     // then, once every wave has issued those, the chunk's K / V tile (in
     // flight during the setup)
     __builtin_amdgcn_s_barrier();
-    uint4 cur[kPF];
     uint32_t curs[2 * kAR];
     static_assert(kPF >= 4 && 2 * kAR >= 2, "a ternary K|V row pair fits the tile registers");
     if constexpr (TERN) {
@@ -1315,8 +1388,12 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
         curs[1] = (uint32_t)ld4i(rvs, tt * 4);
         wait_vm<6>();  // all but the rows
     } else {
-        load_att_tile<PAGED>(cur, curs, p, l, h, c);
-        wait_vm<4 * kAR>();  // all but the tile
+        if (KVM == 0 && pre) {
+            load_att_scales(curs, p, l, h, c);
+        } else {
+            load_att_tile<PAGED>(cur, curs, p, l, h, c);
+            wait_vm<4 * kAR>();  // all but the tile
+        }
     }
     // RoPE on the G query heads (:460-481); chunk 0 also stores q as floats
     {
@@ -1823,6 +1900,7 @@ __device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int
         issue_vec2(in, p.h1s + (size_t)(p.L - 1) * p.H,
                    p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H);
         issue_rec(in, p, p.L - 1, 3);
+        in.inv = wait_rec_inv(p, p.L - 1, 3, in.inv);
         finish_resid(xv, in, p.H, layer(p, p.L - 1).sc(6));
         float inv;
         int cs;
@@ -1919,20 +1997,45 @@ __device__ __forceinline__ int touch_norm(const DsParams& p, int s) {
     return ld4i(rsrc(nw, nw ? (uint32_t)K * 4 : 0u), (uint32_t)line * 128);
 }
 
-// The first weight tile of the first task of this workgroup (task index
-// `first`) in stage s, when s is a GEMV stage and the workgroup has a task in
-// it; otherwise the same loads with nothing to read (the loads are issued on
-// every path alike: a load under a condition would leave the registers to a
-// phi whose copy waits for them).
-__device__ __forceinline__ void prefetch_tile(const DsParams& p, uint4 (&tile)[kPF], int s,
+// The loads of stage s that depend on nothing produced in the launch, for a
+// workgroup whose first task in it is `first`, issued during the grid barrier
+// before the stage: the first weight tile of its GEMV task, or, with an INT8
+// cache, the K / V rows of its first attention chunk (tile[0 .. 2 kAR), the
+// lane layout of load_att_tile; their fp16 scales are loaded by the task).
+// Every path issues the same kPF loads, with nothing to read where there is
+// nothing to load (a load under a condition would leave the registers to a
+// phi whose copy waits for them); the sources are chosen with scalar selects.
+template <int KVM>
+__device__ __forceinline__ void prefetch_next(const DsParams& p, uint4 (&tile)[kPF], int s,
                                               int first) {
+    const int lane = ltid() & 63, wave = lwave();
     const int kind = kind_of(p, s);
+    const int l = min(s / 5, p.L - 1);
     const bool gemv = kind != S_ATT && kind != S_HEAD;
     const int slot = kind == S_QKV || !gemv ? 0 : kind - 1;
     const int K = gemv_k(slot, p.H, p.F), S = p.split[slot];
     const int KS = K / 64, KSs = (KS + S - 1) / S, c0 = (first % S) * KSs;
-    load_tl1_tile(tile, layer(p, min(s / 5, p.L - 1)).mat(slot), first / S, KS, c0,
-                  min(KS, c0 + KSs), gemv && first < ntasks(p, kind));
+    const int c1 = min(KS, c0 + KSs);
+    const bool live = gemv && first < ntasks(p, kind);
+    const __amdgpu_buffer_rsrc_t rw =
+        rsrc(layer(p, l).mat(slot) + (size_t)(first / S) * KS * 64, live ? (uint32_t)c1 * 64 * 16 : 0u);
+    // the attention chunk's rows (as load_att_tile; INT8 cache only)
+    const bool att = KVM == 0 && kind == S_ATT && first < ntasks(p, S_ATT);
+    const int h = att ? first / p.C : 0, c = att ? first % p.C : 0;
+    const int t0 = c * p.T;
+    const int nt = att ? min(p.T, p.pos + 1 - t0) : 0;
+    const size_t tok0 = ((size_t)l * p.Hkv + h) * p.max_seq + t0;
+    const __amdgpu_buffer_rsrc_t rk = rsrc(p.kc + tok0 * kD, (uint32_t)nt * kD);
+    const __amdgpu_buffer_rsrc_t rv = rsrc(p.vc + tok0 * kD, (uint32_t)nt * kD);
+    const int d0 = (lane & 7) * 16;
+#pragma unroll
+    for (int i = 0; i < kPF; ++i) {
+        const bool a = att && i < 2 * kAR;
+        const int tl = (i / 2) * kRT + wave * 8 + (lane >> 3);
+        const uint32_t off = a ? (uint32_t)(tl * kD + d0)
+                               : (uint32_t)((c0 + wave + kW * i) * 64 + lane) * 16;
+        tile[i] = ld16(a ? ((i & 1) ? rv : rk) : rw, off);
+    }
 }
 
 template <int G, int KVM>
@@ -1957,8 +2060,9 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
     if (KVM == 3) stage_blocks(p);  // (stage_layers' block barrier covers it)
     stage_layers(p);
     int off = 0;  // first workgroup of the current stage
-    uint4 tile[kPF];  // the first weight tile of this workgroup's next GEMV task
-    prefetch_tile(p, tile, 0, wg);
+    uint4 tile[kPF];  // the first weight tile of this workgroup's next GEMV task, or the
+                      // K / V rows of its first attention chunk
+    prefetch_next<KVM>(p, tile, 0, wg);
     // The layers' stages; the head follows the loop, so that the loop's only
     // way back to its top is through the grid barrier (a stage body exiting
     // through the loop would leave its loads pending at the top, where the
@@ -1970,19 +2074,27 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
         const int n = ntasks(p, kind);
         const int first = (wg - off + p.nwg) % p.nwg;  // my first task index here
         const int touched = touch_norm(p, s + 1);
+        bool arrived = false;
         if (kind == S_ATT) {
             for (int t = first; t < n; t += p.nwg) {
-                attn_task<G, KVM>(sh, p, l, t / p.C, t % p.C);
+                attn_task<G, KVM>(sh, p, l, t / p.C, t % p.C, tile, t == first);
                 __syncthreads();
             }
         } else if (first < n || rec_writer(p, first, n)) {
-            tl1_stage(sh, p, kind, l, first, n, tile);
+            arrived = tl1_stage(sh, p, kind, l, first, n, tile, [&] {
+                ++gen;
+                bar_arrive(p, s, touched);
+            });
         }
-        off = (off + n) % p.nwg;
-        if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2] = wall_clock64();
+        // (after an early writer's stage, one more: that writer lands on the
+        // last workgroup of the next stage)
+        off = (off + n + (early_writer(p, kind, l) ? 1 : 0)) % p.nwg;
+        if (!arrived) {
+            ++gen;
+            bar_arrive(p, s, touched);
+        }
         const int next = (wg - off + p.nwg) % p.nwg;
-        if (!grid_barrier(p, gen, &s_abort, touched,
-                          [&] { prefetch_tile(p, tile, s + 1, next); }))
+        if (!bar_wait(p, gen, &s_abort, [&] { prefetch_next<KVM>(p, tile, s + 1, next); }))
             return;
         if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = wall_clock64();
     }

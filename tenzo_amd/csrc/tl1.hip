@@ -426,6 +426,92 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
 }
 
 // ------------------------------------------------------------------------
+// The GEMV on fp32 activations -- the unit of executeBitLinearTL1
+// (ROCmRuntime.h:20-28): build_lut's quantization then compute_from_lut
+// (TenzoEngine.cpp:22-146) -- as one launch. Every block quantizes row m of x
+// itself with actquant_kernel<0, 31>'s arithmetic (absmax with the 1e-6
+// floor, scale 31 / absmax correctly rounded, codes roundf(x * scale),
+// inv_scale = absmax * (1/31)) into its LDS code stage while its weight loads
+// are in flight, then takes tl1_gemv_kernel's dot steps over whole rows
+// (no K split). Every block forms the same codes, so the outputs equal the
+// two-launch path's bit for bit. J float4 groups of x per thread: the padded
+// row (KS * 64 codes) is at most 1024 J; K % 4 == 0.
+// ------------------------------------------------------------------------
+template <int J>
+__global__ void __launch_bounds__(256)
+tl1_gemv_f32_kernel(const uint4* __restrict__ w, const float* __restrict__ x, int64_t N,
+                    int64_t K, int64_t KS, RowScales rs, float* __restrict__ y) {
+    __shared__ int red[4][64];
+    __shared__ float redf[4];
+    __shared__ int redi[4];
+    __shared__ uint32_t cs[J * 256];  // the row's codes, four to a word (zero past K)
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int64_t b = blockIdx.x, m = blockIdx.y;
+    const uint4* wb = w + b * KS * 64 + lane;
+    // the row first (vector loads return in issue order), then every weight
+    // load of the wave (up to kTl1J; beyond, in further rounds below)
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + m * K), 0, (int)(K * 4), 0x00020000);
+    float xv[J][4];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {  // groups past K read zeros (outside the resource)
+        const uint4 u = __builtin_bit_cast(
+            uint4, __builtin_amdgcn_raw_buffer_load_b128(rx, (t + 256 * j) * 16, 0, 0));
+        xv[j][0] = __uint_as_float(u.x);
+        xv[j][1] = __uint_as_float(u.y);
+        xv[j][2] = __uint_as_float(u.z);
+        xv[j][3] = __uint_as_float(u.w);
+    }
+    const int64_t nj = KS > wave ? (KS - wave + 3) / 4 : 0;  // wave-uniform
+    uint4 v[kTl1J];
+#pragma unroll
+    for (int j = 0; j < kTl1J; ++j)
+        if (j < nj) v[j] = wb[(wave + 4 * j) * 64];
+    float amax = 1e-6f;
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) amax = fmaxf(amax, fabsf(xv[j][e]));
+    amax = block256_max(amax, redf);
+    const float scale = __fdiv_rn(31.0f, amax);
+    int csum = 0;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        int c[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c[e] = (int)roundf(__fmul_rn(xv[j][e], scale));
+        cs[t + 256 * j] = (uint32_t)(c[0] & 0xff) | (uint32_t)(c[1] & 0xff) << 8 |
+                          (uint32_t)(c[2] & 0xff) << 16 | (uint32_t)(c[3] & 0xff) << 24;
+        csum += (c[0] + c[1]) + (c[2] + c[3]);
+    }
+    csum = block256_sum_i32(csum, redi);  // (its block barriers publish the codes)
+    const int32_t* a32 = reinterpret_cast<const int32_t*>(cs);
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < kTl1J; ++j)
+        if (j < nj) acc = dot16(v[j], a32 + (wave + 4 * j) * 16, acc);
+    for (int64_t j0 = kTl1J; j0 < nj; j0 += kTl1J) {
+#pragma unroll
+        for (int j = 0; j < kTl1J; ++j)
+            if (j0 + j < nj) v[j] = wb[(wave + 4 * (j0 + j)) * 64];
+#pragma unroll
+        for (int j = 0; j < kTl1J; ++j)
+            if (j0 + j < nj) acc = dot16(v[j], a32 + (wave + 4 * (j0 + j)) * 16, acc);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0) {
+        const int tot = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+        const int64_t row = b * 64 + lane;
+        int j = 0;
+        while (j < rs.n - 1 && row >= rs.end[j]) ++j;
+        const float inv_scale = __fmul_rn(amax, 1.0f / 31.0f);
+        y[m * N + row] = (float)(tot - csum) * __fmul_rn(inv_scale, rs.scale[j]);
+    }
+}
+
+// ------------------------------------------------------------------------
 // The same GEMV by the reference's own method (build_lut :22-62,
 // compute_single_block :64-127): a 16-entry int8 table per activation pair
 // (entry u0 | u1 << 2 = (u0 - 1) a0 + (u1 - 1) a1), staged in LDS, looked up
@@ -751,13 +837,27 @@ TENZO_HIP_API int tenzo_hip_bitlinear_tl1_f32(const float* x, const void* w_pack
              "bitlinear_tl1_f32: need N %% 64 == 0");
     hipStream_t st = (hipStream_t)stream;
     const int64_t Kp = ceil_div(K, 64) * 64;
+    RowScales rs = RowScales::single(w_scale);
+    // one launch (tl1_gemv_f32_kernel) where whole rows per block is the GEMV's
+    // own choice (tl1_pick_splits) and the padded row fits its stage
+    const int64_t KS = Kp / 64;
+    if (K % 4 == 0 && Kp <= 8192 && tl1_pick_splits(N / 64, KS, M) == 1) {
+        const dim3 grid((unsigned)(N / 64), (unsigned)M), blk(256);
+        const uint4* wp = (const uint4*)w_packed;
+        if (Kp <= 2048)
+            hipLaunchKernelGGL(tl1_gemv_f32_kernel<2>, grid, blk, 0, st, wp, x, N, K, KS, rs, y);
+        else if (Kp <= 4096)
+            hipLaunchKernelGGL(tl1_gemv_f32_kernel<4>, grid, blk, 0, st, wp, x, N, K, KS, rs, y);
+        else
+            hipLaunchKernelGGL(tl1_gemv_f32_kernel<8>, grid, blk, 0, st, wp, x, N, K, KS, rs, y);
+        return launch_status("tl1_gemv_f32_kernel");
+    }
     char* ws = (char*)Scratch::get(kScratchAct, (size_t)(M * Kp + M * 8 + 256), st);
     if (!ws) return TENZO_ERROR_OUT_OF_MEMORY;
     tenzo_hip_actq_t* q = (tenzo_hip_actq_t*)ws;
     int8_t* codes = (int8_t*)(ws + ((M * 8 + 255) / 256) * 256);
     int rc = launch_quant31(x, nullptr, false, 0.0f, M, K, codes, q, nullptr, st);
     if (rc) return rc;
-    RowScales rs = RowScales::single(w_scale);
     return launch_tl1_gemv(codes, q, w_packed, rs, M, N, K, y, nullptr, nullptr, st, 0, nullptr);
 }
 

@@ -79,6 +79,29 @@ def test_tl1_gemv_batched_rows(torch_dev):
         np.testing.assert_array_equal(y[m], yo)
 
 
+@pytest.mark.parametrize("N,K,M", [(6912, 2560, 1), (192, 2500, 2), (64, 1000, 1),
+                                   (2560, 6912, 1), (128, 102, 1)])
+def test_tl1_gemv_f32_entry_bit_exact(torch_dev, N, K, M):
+    """tenzo_hip_bitlinear_tl1_f32 (fp32 activations in: build_lut's
+    quantization, then the GEMV) against the oracle, bit for bit: the fused
+    one-launch kernel (6912 x 2560 = BASELINE config 1; K not a multiple of
+    64; two rows) and the two-launch path (K split by the GEMV, K % 4 != 0).
+    Row 0 of the two-row case is all zeros (the 1e-6 absmax floor, codes 0)."""
+    from tenzo_amd import ops
+    torch = torch_dev
+    rng = np.random.default_rng(N + K)
+    w = formats.tl1_random(N, K, rng)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    if M > 1:
+        x[0] = 0.0
+    wp = ops.tl1_repack(to_dev(torch, w), N, K)
+    print(f"tl1_f32 N={N} K={K} M={M}", flush=True)
+    y = ops.bitlinear_tl1_f32(to_dev(torch, x), wp, 0.0159, N, K).cpu().numpy()
+    for m in range(M):
+        yo, _, _ = oracle.tl1_gemv(x[m], w, N, 0.0159)
+        np.testing.assert_array_equal(y[m], yo)
+
+
 def test_rmsnorm_quant31_bit_exact(torch_dev):
     from tenzo_amd import ops
     torch = torch_dev
