@@ -63,6 +63,9 @@ struct DsParams {
     int pos, C, T;              // this step's position and attention chunking
     int nwg;
     int split[4];               // K slices per row block of the QKV, O, GU, DOWN GEMVs
+    int split_chunks[4];        // 64-column chunks per K slice: ceil(K / 64 / split)
+    unsigned split_mul[4];      // ds_div_mul(split[i])
+    unsigned c_mul;             // ds_div_mul(C)
     int with_head;              // 0: stop after the layers (prefill)
     unsigned spin_limit;        // polls before a wait gives up (kDsSpinLimit)
     float eps;
@@ -88,9 +91,13 @@ size_t ds_sync_words(int L, int Hkv);
 size_t ds_acc_words(int L, int H, int F, int Hq, int Hkv);
 // floats of the per-layer vector region (xs, h1s, attns).
 size_t ds_vec_floats(int L, int H, int Hq);
-// K slices per row block for each GEMV stage (fills p.split from the shapes
-// and p.nwg).
+// K slices per row block for each GEMV stage (fills p.split, p.split_chunks
+// and p.split_mul from the shapes and p.nwg; p.c_mul from p.C).
 void ds_plan_splits(DsParams& p);
+// Multiplier for t / d (1 <= d < 2^15, 0 <= t < 2^16) as
+// umulhi(2 t, ceil(2^31 / d)): the product exceeds t / d by less than
+// t / 2^31 < 2^-15, too little to reach the next integer.
+inline unsigned ds_div_mul(int d) { return (unsigned)((0x80000000ull + (unsigned)d - 1) / (unsigned)d); }
 // Workgroup count the kernel runs with on the current device (a multiple of
 // kDsCounters, all co-resident), or 0 when cooperative launch is unavailable.
 int ds_grid_size();

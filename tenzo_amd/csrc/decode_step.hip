@@ -287,6 +287,14 @@ __device__ __forceinline__ int ntasks(const DsParams& p, int kind) {
     return gemv_rows(slot, p.H, p.F, p.Hq, p.Hkv) / 64 * p.split[slot];
 }
 
+// t / d and t % d for a task index t < 2^16, with m = ds_div_mul(d).
+__device__ __forceinline__ int div_m(int t, unsigned m) {
+    return (int)__umulhi((unsigned)t << 1, m);
+}
+__device__ __forceinline__ int mod_m(int t, int d, unsigned m) { return t - div_m(t, m) * d; }
+// (x + nwg) % nwg for -nwg < x < nwg
+__device__ __forceinline__ int wrap_wg(int x, int nwg) { return x < 0 ? x + nwg : x; }
+
 // Stage index s = 5*layer + kind for the layers, 5*L for the head.
 __device__ __forceinline__ int kind_of(const DsParams& p, int s) {
     return s >= 5 * p.L ? S_HEAD : s % 5;
@@ -1096,7 +1104,8 @@ __device__ __forceinline__ bool tl1_stage(SharedAll& sh, const DsParams& p, int 
     const AccOff ao = acc_off(p.H, p.F, p.Hq, p.Hkv);
     int* accl = p.acc + (size_t)l * ao.stride;
     const int S = p.split[slot];
-    const int KS = K / 64, KSs = (KS + S - 1) / S;
+    const unsigned Sm = p.split_mul[slot];
+    const int KS = K / 64, KSs = p.split_chunks[slot];
     const uint4* W = Lw.mat(slot);
     // The first task's weight tile is in flight already (issued during the
     // grid barrier before this stage, prefetch_tile); the stage input and the
@@ -1169,7 +1178,7 @@ __device__ __forceinline__ bool tl1_stage(SharedAll& sh, const DsParams& p, int 
             stcu(recw + 1, (unsigned)csum);
         }
     } else {
-        const int c0 = (first % S) * KSs, c1 = min(KS, c0 + KSs);
+        const int c0 = mod_m(first, S, Sm) * KSs, c1 = min(KS, c0 + KSs);
         const int csum = norm_quant_codes31(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps,
                                             single ? c0 * 16 : 0, single ? c1 * 16 : K / 4);
         if (single && first < S && tid == 0)
@@ -1178,7 +1187,7 @@ __device__ __forceinline__ bool tl1_stage(SharedAll& sh, const DsParams& p, int 
     }
     int* out = accl + (slot == 0 ? 0 : slot == 1 ? ao.o : slot == 2 ? ao.gu : ao.down);
     for (int t = first; t < n; t += p.nwg) {
-        const int rb = t / S, c0 = (t % S) * KSs, c1 = min(KS, c0 + KSs);
+        const int rb = div_m(t, Sm), c0 = (t - rb * S) * KSs, c1 = min(KS, c0 + KSs);
         if (t != first) load_tl1_tile(tile, W, rb, KS, c0, c1);
         const int tot = tl1_rowblock(s, tile, W, rb, KS, c0, c1);
         if (wave == 0) {
@@ -2014,14 +2023,16 @@ __device__ __forceinline__ void prefetch_next(const DsParams& p, uint4 (&tile)[k
     const bool gemv = kind != S_ATT && kind != S_HEAD;
     const int slot = kind == S_QKV || !gemv ? 0 : kind - 1;
     const int K = gemv_k(slot, p.H, p.F), S = p.split[slot];
-    const int KS = K / 64, KSs = (KS + S - 1) / S, c0 = (first % S) * KSs;
+    const int KS = K / 64, KSs = p.split_chunks[slot];
+    const int rb = div_m(first, p.split_mul[slot]), c0 = (first - rb * S) * KSs;
     const int c1 = min(KS, c0 + KSs);
     const bool live = gemv && first < ntasks(p, kind);
     const __amdgpu_buffer_rsrc_t rw =
-        rsrc(layer(p, l).mat(slot) + (size_t)(first / S) * KS * 64, live ? (uint32_t)c1 * 64 * 16 : 0u);
+        rsrc(layer(p, l).mat(slot) + (size_t)rb * KS * 64, live ? (uint32_t)c1 * 64 * 16 : 0u);
     // the attention chunk's rows (as load_att_tile; INT8 cache only)
     const bool att = KVM == 0 && kind == S_ATT && first < ntasks(p, S_ATT);
-    const int h = att ? first / p.C : 0, c = att ? first % p.C : 0;
+    const int hq = div_m(first, p.c_mul);
+    const int h = att ? hq : 0, c = att ? first - hq * p.C : 0;
     const int t0 = c * p.T;
     const int nt = att ? min(p.T, p.pos + 1 - t0) : 0;
     const size_t tok0 = ((size_t)l * p.Hkv + h) * p.max_seq + t0;
@@ -2072,12 +2083,13 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
         const int kind = s % 5;
         const int l = s / 5;
         const int n = ntasks(p, kind);
-        const int first = (wg - off + p.nwg) % p.nwg;  // my first task index here
+        const int first = wrap_wg(wg - off, p.nwg);  // my first task index here
         const int touched = touch_norm(p, s + 1);
         bool arrived = false;
         if (kind == S_ATT) {
             for (int t = first; t < n; t += p.nwg) {
-                attn_task<G, KVM>(sh, p, l, t / p.C, t % p.C, tile, t == first);
+                const int h = div_m(t, p.c_mul);
+                attn_task<G, KVM>(sh, p, l, h, t - h * p.C, tile, t == first);
                 __syncthreads();
             }
         } else if (first < n || rec_writer(p, first, n)) {
@@ -2088,18 +2100,20 @@ __global__ void __launch_bounds__(kT, 1) decode_step_kernel(DsParams p) {
         }
         // (after an early writer's stage, one more: that writer lands on the
         // last workgroup of the next stage)
-        off = (off + n + (early_writer(p, kind, l) ? 1 : 0)) % p.nwg;
+        off += n + (early_writer(p, kind, l) ? 1 : 0);
+        if (off >= p.nwg) off -= p.nwg;
+        if (off >= p.nwg) off %= p.nwg;  // (stages of more than nwg tasks)
         if (!arrived) {
             ++gen;
             bar_arrive(p, s, touched);
         }
-        const int next = (wg - off + p.nwg) % p.nwg;
+        const int next = wrap_wg(wg - off, p.nwg);
         if (!bar_wait(p, gen, &s_abort, [&] { prefetch_next<KVM>(p, tile, s + 1, next); }))
             return;
         if (p.trace && tid == 0) p.trace[((size_t)s * p.nwg + wg) * 2 + 1] = wall_clock64();
     }
     const int s = nlayer_stages;
-    head_stage(sh, p, (wg - off + p.nwg) % p.nwg, ntasks(p, S_HEAD));
+    head_stage(sh, p, wrap_wg(wg - off, p.nwg), ntasks(p, S_HEAD));
     if (p.trace && tid == 0) {
         const uint64_t now = wall_clock64();
         p.trace[((size_t)s * p.nwg + wg) * 2] = now;
@@ -2128,7 +2142,10 @@ void ds_plan_splits(DsParams& p) {
         if (S > KS) S = KS;
         if (S < 1) S = 1;
         p.split[slot] = S;
+        p.split_chunks[slot] = (KS + S - 1) / S;
+        p.split_mul[slot] = ds_div_mul(S);
     }
+    p.c_mul = ds_div_mul(p.C > 0 ? p.C : 1);
 }
 
 int ds_grid_size() {
