@@ -1023,6 +1023,14 @@ def main():
         "stages": st,
         "api_generate_step_tok_s": round(api_tok_s, 2),
         "token_check": token_check,
+        # what "bit-exact" is measured against: RMSNorm (and so every activation
+        # code) reproduces the reference build's 1/sqrt, the RSQRTSS estimate
+        # of the x86 host it was compiled on plus one Newton step
+        "parity_pin": {"rms_norm": "reference build host's RSQRTSS estimate (Intel x86, AVX2/FMA "
+                                   "build, -ffast-math), table tenzo_amd/csrc/rsqrt_est_table.inc "
+                                   "+ one Newton step; 8-chain FMA sum of squares",
+                       "chained_decode_test": "tests/test_gpu_bitnet_full.py::"
+                                              "test_full_shape_chained_decode"},
         "stage_kernels": {"tl1_gemv": {k: (round(v, 2) if isinstance(v, float) else v)
                                        for k, v in rl_tl1.items()},
                           "lm_head_i8": {k: (round(v, 2) if isinstance(v, float) else v)

@@ -1909,6 +1909,27 @@ __device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int
         issue_vec2(in, p.h1s + (size_t)(p.L - 1) * p.H,
                    p.acc + (size_t)(p.L - 1) * ao.stride + ao.down, p.H);
         issue_rec(in, p, p.L - 1, 3);
+        // Row block t: HC chunks of 16 columns x 64 rows, 1 KiB each. When a
+        // block is two rounds (HC <= 2 kHU x waves), wave w loads its chunks
+        // w + kW (u + kHU r), u < kHU, of round r into one of two register
+        // sets while it multiplies the other: the first round's loads go out
+        // right after the stage input's (so waiting for the input does not
+        // wait for them) and run under the final norm; each later round's go
+        // out before the previous round's products. Loads of a block past n,
+        // or past HC, read zeros (empty resource).
+        const int HC = p.H / 16;
+        constexpr int kHU = 10;
+        const bool two_rounds = HC <= 2 * kHU * kW;
+        uint4 va[kHU], vb[kHU];
+        auto issue = [&](uint4 (&v)[kHU], int t, int r) {
+            const bool live = p.with_head && two_rounds && t < n;
+            const __amdgpu_buffer_rsrc_t rh =
+                rsrc(p.head + (size_t)t * HC * 64, live ? (uint32_t)HC * 64 * 16 : 0u);
+#pragma unroll
+            for (int u = 0; u < kHU; ++u)
+                v[u] = ld16(rh, (uint32_t)((wave + (u + kHU * r) * kW) * 64 + lane) * 16);
+        };
+        issue(va, first, 0);
         in.inv = wait_rec_inv(p, p.L - 1, 3, in.inv);
         finish_resid(xv, in, p.H, layer(p, p.L - 1).sc(6));
         float inv;
@@ -1916,30 +1937,10 @@ __device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int
         store_slices(p.x, xv, p.H, 0, first, min(n, p.nwg));
         if (!p.with_head) return;
         norm_quant<127>(s, xv, nwr, p.final_norm != nullptr, p.H, p.eps, inv, cs);
-        const int HC = p.H / 16;
         const int4* c4 = reinterpret_cast<const int4*>(s.codes);
-        constexpr int kHU = 8;  // 16-byte loads in flight per lane (x 8 waves)
-        for (int t = first; t < n; t += p.nwg) {
-            // row block t: chunks of 16 columns x 64 rows, 1 KiB each (past HC: zeros)
-            const __amdgpu_buffer_rsrc_t rh =
-                rsrc(p.head + (size_t)t * HC * 64, (uint32_t)HC * 64 * 16);
-            int acc4[4] = {0, 0, 0, 0};  // independent chains (integer sums: exact in any order)
-            for (int c0 = wave; c0 < HC; c0 += kHU * kW) {
-                uint4 v[kHU];
-#pragma unroll
-                for (int u = 0; u < kHU; ++u)
-                    v[u] = ld16(rh, (uint32_t)((c0 + u * kW) * 64 + lane) * 16);
-#pragma unroll
-                for (int u = 0; u < kHU; ++u) {
-                    const int c = min(c0 + u * kW, HC - 1);  // past HC the weights read 0
-                    const int4 a4 = c4[c];
-                    acc4[0] = sdot4(v[u].x, a4.x, acc4[0]);
-                    acc4[1] = sdot4(v[u].y, a4.y, acc4[1]);
-                    acc4[2] = sdot4(v[u].z, a4.z, acc4[2]);
-                    acc4[3] = sdot4(v[u].w, a4.w, acc4[3]);
-                }
-            }
-            s.red_i[wave][lane] = (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
+        // the row's int32 sum (integer sums: exact in any order) -> logit, argmax
+        auto finish_block = [&](int t, int part) {
+            s.red_i[wave][lane] = part;
             __syncthreads();
             if (wave == 0) {
                 int tot = 0;
@@ -1953,6 +1954,50 @@ __device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int
                 }
             }
             __syncthreads();
+        };
+        auto dot_round = [&](const uint4 (&v)[kHU], int r) {
+            int acc4[4] = {0, 0, 0, 0};  // independent chains
+#pragma unroll
+            for (int u = 0; u < kHU; ++u) {
+                const int c = min(wave + (u + kHU * r) * kW, HC - 1);  // past HC the weights read 0
+                const int4 a4 = c4[c];
+                acc4[0] = sdot4(v[u].x, a4.x, acc4[0]);
+                acc4[1] = sdot4(v[u].y, a4.y, acc4[1]);
+                acc4[2] = sdot4(v[u].z, a4.z, acc4[2]);
+                acc4[3] = sdot4(v[u].w, a4.w, acc4[3]);
+            }
+            return (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]);
+        };
+        if (two_rounds) {
+            for (int t = first; t < n; t += p.nwg) {
+                issue(vb, t, 1);
+                const int part = dot_round(va, 0);
+                issue(va, t + p.nwg, 0);
+                finish_block(t, part + dot_round(vb, 1));
+            }
+        } else {
+            constexpr int kHR = 8;  // 16-byte loads in flight per lane (x 8 waves)
+            for (int t = first; t < n; t += p.nwg) {
+                const __amdgpu_buffer_rsrc_t rh =
+                    rsrc(p.head + (size_t)t * HC * 64, (uint32_t)HC * 64 * 16);
+                int acc4[4] = {0, 0, 0, 0};
+                for (int c0 = wave; c0 < HC; c0 += kHR * kW) {
+                    uint4 v[kHR];
+#pragma unroll
+                    for (int u = 0; u < kHR; ++u)
+                        v[u] = ld16(rh, (uint32_t)((c0 + u * kW) * 64 + lane) * 16);
+#pragma unroll
+                    for (int u = 0; u < kHR; ++u) {
+                        const int c = min(c0 + u * kW, HC - 1);
+                        const int4 a4 = c4[c];
+                        acc4[0] = sdot4(v[u].x, a4.x, acc4[0]);
+                        acc4[1] = sdot4(v[u].y, a4.y, acc4[1]);
+                        acc4[2] = sdot4(v[u].z, a4.z, acc4[2]);
+                        acc4[3] = sdot4(v[u].w, a4.w, acc4[3]);
+                    }
+                }
+                finish_block(t, (acc4[0] + acc4[1]) + (acc4[2] + acc4[3]));
+            }
         }
     } else if (!p.with_head) {
         return;
