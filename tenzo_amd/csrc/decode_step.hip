@@ -930,7 +930,7 @@ __device__ __forceinline__ float norm_record_inv31(Shared& s, float4 (&v)[kJ],
 // subnormal p_i r gives |z_i| < 2^-100 for both scales: code 0 either way.)
 __device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
                                                   const float4 (&w)[kJ], bool has_w, int K,
-                                                  float eps, int q_lo, int q_hi) {
+                                                  float eps, int q_lo, int q_hi, bool need_csum) {
     const int t = ltid(), lane = t & 63, wave = lwave();
     float4 p[kJ];
     float pmax = wave_max(weigh(p, v, w, has_w, K));
@@ -952,7 +952,9 @@ __device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
     __syncthreads();
     pmax = red_max(s.red_b);
     ss = red_sum(s.red_a);
-    const float r = inv_rms_ref(ss, K, eps, s_rsq);
+    // any positive scale gives the same codes up to the test below; the
+    // hardware reciprocal square root is within a few ulp of 1/sqrt
+    const float r = __builtin_amdgcn_rsqf(__builtin_fmaf(ss, 1.0f / (float)K, eps));
     const float amax = __fmul_rn(pmax, r);
     // estimate within 1e-3 of inv_rms (any summation order of K <= 16384
     // squares), so amax >= 2e-6 keeps the exact amax above the floor
@@ -976,10 +978,10 @@ __device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
             csum += (c[0] + c[1]) + (c[2] + c[3]);
         }
     const bool wnear = __any(near);
-    csum = wave_sum_i32(csum);
+    if (need_csum) csum = wave_sum_i32(csum);
     if (lane == 0) {
         s.red_c[wave] = wnear ? 1 : 0;
-        s.red_s[wave] = csum;
+        if (need_csum) s.red_s[wave] = csum;
     }
     __syncthreads();
     if (red_or(s.red_c) != 0) {
@@ -989,7 +991,7 @@ __device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
         if (lane == 0) s.red_s[wave] = csum;
         __syncthreads();
     }
-    return red_sum(s.red_s);
+    return need_csum ? red_sum(s.red_s) : 0;
 }
 
 // ---------------------------------------------------------------- GEMV ----
@@ -1030,7 +1032,7 @@ __device__ __forceinline__ int tl1_acc_total(const int (&acc)[4]) {
 // sum_k u_k a_k (u = w+1) over the slice in wave 0, lane = row (other waves: 0).
 __device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
                                             const uint4* __restrict__ W, int rb, int KS, int c0,
-                                            int c1) {
+                                            int c1, bool more) {
     const int lane = ltid() & 63, wave = lwave();
     const int4* c4 = reinterpret_cast<const int4*>(s.codes);
     int acc4[4] = {0, 0, 0, 0};
@@ -1059,7 +1061,9 @@ __device__ __forceinline__ int tl1_rowblock(Shared& s, const uint4 (&cur)[kPF],
 #pragma unroll
         for (int w = 0; w < kW; ++w) tot += s.red_i[w][lane];
     }
-    __syncthreads();
+    // before red_i is written again (a next task; without one, the block
+    // barrier of the grid barrier's arrival orders it before the next stage)
+    if (more) __syncthreads();
     return tot;
 }
 
@@ -1179,9 +1183,11 @@ __device__ __forceinline__ bool tl1_stage(SharedAll& sh, const DsParams& p, int 
         }
     } else {
         const int c0 = mod_m(first, S, Sm) * KSs, c1 = min(KS, c0 + KSs);
+        const bool contributes = single && first < S;  // adds its slice's code sum
         const int csum = norm_quant_codes31(s, xv, nwr, Lw.norm(slot) != nullptr, K, p.eps,
-                                            single ? c0 * 16 : 0, single ? c1 * 16 : K / 4);
-        if (single && first < S && tid == 0)
+                                            single ? c0 * 16 : 0, single ? c1 * 16 : K / 4,
+                                            contributes);
+        if (contributes && tid == 0)
             __hip_atomic_fetch_add(reinterpret_cast<int*>(recw + 1), csum, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1189,7 +1195,7 @@ __device__ __forceinline__ bool tl1_stage(SharedAll& sh, const DsParams& p, int 
     for (int t = first; t < n; t += p.nwg) {
         const int rb = div_m(t, Sm), c0 = (t - rb * S) * KSs, c1 = min(KS, c0 + KSs);
         if (t != first) load_tl1_tile(tile, W, rb, KS, c0, c1);
-        const int tot = tl1_rowblock(s, tile, W, rb, KS, c0, c1);
+        const int tot = tl1_rowblock(s, tile, W, rb, KS, c0, c1, t + p.nwg < n);
         if (wave == 0) {
             if (S == 1)  // the row block's only contribution
                 __hip_atomic_store(out + rb * 64 + lane, tot, __ATOMIC_RELAXED,
