@@ -164,6 +164,30 @@ def test_engine_prefill_longer_than_one_pass(torch_dev):
         np.testing.assert_array_equal(a.logits(), b.logits())
 
 
+def test_engine_prefill_chunk_size_changes(torch_dev):
+    """16 kv heads: decode aims at 512 / 16 = 32 chunks per head, so its chunk
+    size is 32 tokens up to a context of 1024 and 64 past it (ceil(ctx / 32)
+    rounded up to a multiple of 32); a prompt from position 1000 mixes both
+    in one launch (rows with 32-token chunks run in the kernel built for 64),
+    G = 1."""
+    from tenzo_amd import engine as eng_mod, synth
+    cfg = synth.DecodeConfig(hidden=2048, n_q_heads=16, n_kv_heads=16, n_layers=1, ffn=512,
+                             vocab=512, max_seq=1100, theta=10000.0)
+    sm = synth.make_model(cfg, seed=29, ctx=1000)
+    toks = np.random.default_rng(4).integers(0, cfg.vocab, 60).astype(np.int32)
+    print("engine prefill ctx=1000 n=60 Hkv=16", flush=True)
+    a, b = _engine_pair(eng_mod, cfg, sm)
+    with a, b:
+        for t in toks:
+            a.prefill(int(t))
+        b.prefill_batch(toks, exact=True)
+        for x, y in zip(a.get_kv(1060), b.get_kv(1060)):
+            np.testing.assert_array_equal(x, y)
+        np.testing.assert_array_equal(a.buffer("x"), b.buffer("x"))
+        assert a.step(9) == b.step(9)
+        np.testing.assert_array_equal(a.logits(), b.logits())
+
+
 def test_engine_prefill_then_persistent_decode(torch_dev):
     """A batched prefill followed by persistent-kernel decode steps gives the
     tokens of token-by-token prefill + decode (fp32 logits to 1e-5: the
