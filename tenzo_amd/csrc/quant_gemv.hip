@@ -293,6 +293,76 @@ q8_0_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __
     if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
 }
 
+// Q8_0 with the weights staged through LDS (K % 256 == 0, 16-byte aligned
+// operands). In q8_0_kernel each lane reads its own 272-byte group, so the 64
+// lanes of a load instruction touch 64 cache lines and the L1 tag lookups
+// (eight per line over a pass) stall the address path. Here a workgroup's
+// Q8R rows (contiguous in memory) are copied into LDS by buffer loads that go
+// straight to LDS, 1 KiB per wave instruction (lane l: bytes 16 l ..), so
+// every line is looked up once; 32 lanes then share a row, lane s taking the
+// 4-block units s, s + 32, .. (136 bytes each, read from LDS as 8-byte words:
+// the 32 lanes of a row hit 64 distinct banks). Rows past N read zeros.
+constexpr int kQ8R = 8;  // rows per workgroup
+namespace {
+typedef __attribute__((address_space(3))) void q8_lds_void;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t q8_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+}  // namespace
+
+template <typename TA>
+__global__ void __launch_bounds__(256)
+q8_0_lds_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __restrict__ y,
+                int K, int N) {
+    extern __shared__ float a_s[];  // activations (f32s_size(K) + 2048 floats), then rows
+                                    // (whole KiB rounds)
+    const int b = blockIdx.y;
+    const int nbk = K / 32;
+    const int rb = nbk * 34;  // bytes per row
+    const int row0 = blockIdx.x * kQ8R;
+    uint8_t* w_s = reinterpret_cast<uint8_t*>(a_s + f32s_size(K) + 2048);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    F32Stage<TA> stg;
+    stg.load(act + (int64_t)b * K, K);
+    {
+        const uint8_t* base = w + (int64_t)row0 * rb;
+        const uint32_t left = (uint32_t)(min(N - row0, kQ8R) * rb);  // this block's rows
+        const __amdgpu_buffer_rsrc_t r = q8_rsrc(base, left);
+        const int rounds = (kQ8R * rb + 1023) / 1024;
+        for (int i = wave; i < rounds; i += 4)  // (wave-uniform)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (q8_lds_void*)(w_s + 1024 * i), 16,
+                                                     (uint32_t)(1024 * i + 16 * lane), 0, 0, 0);
+    }
+    stg.store(a_s, act + (int64_t)b * K, K);
+    __builtin_amdgcn_s_waitcnt(0);  // (this wave's copies and loads landed)
+    __syncthreads();
+    const int r = tid >> 5, sub = tid & 31;
+    const uint8_t* rowp = w_s + r * rb;
+    float acc = 0.0f;
+    for (int u = sub; u < nbk / 4; u += 32) {
+        uint32_t dw[34];
+        const uint2* p = reinterpret_cast<const uint2*>(rowp + 136 * u);
+#pragma unroll
+        for (int i = 0; i < 17; ++i) {
+            const uint2 v = p[i];
+            dw[2 * i] = v.x;
+            dw[2 * i + 1] = v.y;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int bk = 4 * u + i;
+            const uint32_t dbits = (dw[(34 * i) >> 2] >> (8 * ((34 * i) & 3))) & 0xffffu;
+            const float d = half_bits_to_float((uint16_t)dbits);
+            acc = __builtin_fmaf(q8_block_dot(dw, 34 * i, a_s + 32 * bk + 4 * (bk >> 3)), d, acc);
+        }
+    }
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) acc += __shfl_xor(acc, o, 64);
+    const int row = row0 + r;
+    if (row < N && sub == 0) y[(int64_t)b * N + row] = acc;
+}
+
 // Q4_0 with fp16 activations on the packed fp16 dot (v_dot2_f32_f16): the
 // activations are staged in LDS as pairs (a_j, a_16+j) of each block, the
 // two elements that share a weight byte; a byte becomes the pair of weights
@@ -1246,6 +1316,15 @@ static int launch_q8_0(const TA* act, const uint8_t* w, float* y, int K, int N, 
     const int lpr = pick_lpr((nbk + 7) / 8);
     const bool full = K % 256 == 0 && ((uintptr_t)act & 15) == 0 && ((uintptr_t)w & 15) == 0;
     const size_t smem = full ? ((size_t)f32s_size(K) + 2048) * 4 : (size_t)K * 4;
+    // the LDS-staged form when a workgroup's rows and activations fit 64 KiB, so two
+    // workgroups share a CU
+    const size_t smem_lds =
+        ((size_t)f32s_size(K) + 2048) * 4 + (size_t)ceil_div(kQ8R * nbk * 34, 1024) * 1024;
+    if (full && smem_lds <= 64 * 1024) {
+        hipLaunchKernelGGL((q8_0_lds_kernel<TA>), dim3((unsigned)ceil_div(N, kQ8R), (unsigned)B),
+                           dim3(256), smem_lds, st, act, w, y, K, N);
+        return launch_status("q8_0_lds_kernel");
+    }
     dim3 grid((unsigned)ceil_div(N, 256 / lpr), (unsigned)B);
 #define Q80_CASE(L)                                                                      \
     case L:                                                                              \

@@ -91,11 +91,14 @@ def test_q4_0_fp16_and_fp32_activations(torch_dev, N, K):
 
 @pytest.mark.parametrize("N,K,B", [(64, 32, 1), (100, 288, 2), (11008, 4096, 1),
                                    (11008, 4096, 8), (257, 4128, 1), (72, 2304, 2),
-                                   (40, 8192, 1), (24, 16384, 1)])
+                                   (40, 8192, 1), (24, 16384, 1), (1003, 4096, 1),
+                                   (5, 2048, 3)])
 def test_q8_0_weights(torch_dev, N, K, B):
     """compute_linear_gguf_q8_0 (TenzoEngine.cpp:1078-1114). K = 288 and 4128
     leave rows that are not 16-byte aligned or a partial group of 8 blocks
-    (the halfword path); 4096 takes the 16-byte loads."""
+    (the halfword path); K = 2048, 2304 and 4096 stage 8 rows at a time
+    through LDS (N = 1003 and 5 end in a partial block of rows), 8192 and
+    16384 take the 16-byte loads per lane."""
     from tenzo_amd import ops
     torch = torch_dev
     print(f"q8_0 N={N} K={K} B={B}", flush=True)
