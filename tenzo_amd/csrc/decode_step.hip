@@ -125,6 +125,12 @@ __device__ __forceinline__ int ldc4i(__amdgpu_buffer_rsrc_t r, uint32_t byte_off
 __device__ __forceinline__ uint4 ld16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
+// Read-once streams (the LM head's rows): the nontemporal hint, measured ~6% more read
+// bandwidth than plain loads on a pure 330 MB read (6.9 vs 6.5 TB/s).
+constexpr int kNt = 2;  // cache-policy bit nt
+__device__ __forceinline__ uint4 ld16nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kNt));
+}
 __device__ __forceinline__ f4v ld16f(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
@@ -1933,7 +1939,7 @@ __device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int
                 rsrc(p.head + (size_t)t * HC * 64, live ? (uint32_t)HC * 64 * 16 : 0u);
 #pragma unroll
             for (int u = 0; u < kHU; ++u)
-                v[u] = ld16(rh, (uint32_t)((wave + (u + kHU * r) * kW) * 64 + lane) * 16);
+                v[u] = ld16nt(rh, (uint32_t)((wave + (u + kHU * r) * kW) * 64 + lane) * 16);
         };
         issue(va, first, 0);
         in.inv = wait_rec_inv(p, p.L - 1, 3, in.inv);
@@ -1991,7 +1997,7 @@ __device__ __forceinline__ void head_stage(SharedAll& sh, const DsParams& p, int
                     uint4 v[kHR];
 #pragma unroll
                     for (int u = 0; u < kHR; ++u)
-                        v[u] = ld16(rh, (uint32_t)((c0 + u * kW) * 64 + lane) * 16);
+                        v[u] = ld16nt(rh, (uint32_t)((c0 + u * kW) * 64 + lane) * 16);
 #pragma unroll
                     for (int u = 0; u < kHR; ++u) {
                         const int c = min(c0 + u * kW, HC - 1);
