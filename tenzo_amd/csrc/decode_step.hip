@@ -134,6 +134,9 @@ constexpr int kNt = 2;  // cache-policy bit nt
 __device__ __forceinline__ uint4 ld16nt(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kNt));
 }
+__device__ __forceinline__ int ld4int(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return (int)__builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, kNt);
+}
 __device__ __forceinline__ f4v ld16f(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
@@ -505,9 +508,9 @@ __device__ __forceinline__ void load_att_tile(uint4 (&pf)[kPF], uint32_t (&pfs)[
             const int tl = r * kRT + wave * 8 + (lane >> 3);
             const uint32_t row = page_row(p, l, h, min(t0 + tl, p.pos));
             pf[2 * r] = ld16nt(rk, row * kD + d0);
-            pfs[2 * r] = (uint32_t)ld4i(rks, row * 4);
+            pfs[2 * r] = (uint32_t)ld4int(rks, row * 4);
             pf[2 * r + 1] = ld16nt(rv, row * kD + d0);
-            pfs[2 * r + 1] = (uint32_t)ld4i(rvs, row * 4);
+            pfs[2 * r + 1] = (uint32_t)ld4int(rvs, row * 4);
             __builtin_amdgcn_sched_barrier(0);
         }
         return;
@@ -1408,8 +1411,8 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
         cur[1] = ld16nt(rk, tt * 32 + 16);
         cur[2] = ld16nt(rv, tt * 32);
         cur[3] = ld16nt(rv, tt * 32 + 16);
-        curs[0] = (uint32_t)ld4i(rks, tt * 4);
-        curs[1] = (uint32_t)ld4i(rvs, tt * 4);
+        curs[0] = (uint32_t)ld4int(rks, tt * 4);
+        curs[1] = (uint32_t)ld4int(rvs, tt * 4);
         wait_vm<6>();  // all but the rows
     } else {
         if (KVM == 0 && pre) {
@@ -1572,10 +1575,10 @@ __device__ __forceinline__ void attn_task(SharedAll& sh, const DsParams& p, int 
                 // (tokens past the chunk read the context's last token)
                 const uint32_t rows = pool_rows(p);
                 const uint32_t row = page_row(p, l, h, min(t, p.pos));
-                kv = ld16(rsrc(p.kc, rows * kD), row * kD + d0);
-                vv = ld16(rsrc(p.vc, rows * kD), row * kD + d0);
-                skf = __int_as_float(ld4i(rsrc(p.pks, rows * 4), row * 4));
-                svf = __int_as_float(ld4i(rsrc(p.pvs, rows * 4), row * 4));
+                kv = ld16nt(rsrc(p.kc, rows * kD), row * kD + d0);
+                vv = ld16nt(rsrc(p.vc, rows * kD), row * kD + d0);
+                skf = __int_as_float(ld4int(rsrc(p.pks, rows * 4), row * 4));
+                svf = __int_as_float(ld4int(rsrc(p.pvs, rows * 4), row * 4));
             } else {
                 // past the preloaded rounds (long chunks): tokens past the
                 // chunk read zeros through the resource bounds
