@@ -254,6 +254,16 @@ __device__ __forceinline__ int sdot4(uint32_t a, int32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, b, c, false);
 }
 
+// A 16-byte load with the nontemporal hint, for weights a kernel reads once: on a pure
+// 330 MB read it gives ~6% more bandwidth than a plain load and leaves the caches to the
+// data that is read again. (The decode chunk kernel's K/V loads stay plain: there the
+// hint made attention 20-30% slower at 8k-32k contexts.)
+__device__ __forceinline__ uint4 ld_nt16(const uint4* p) {
+    typedef unsigned u4nt __attribute__((ext_vector_type(4)));
+    const u4nt v = __builtin_nontemporal_load(reinterpret_cast<const u4nt*>(p));
+    return uint4{v.x, v.y, v.z, v.w};
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {
     return __half2float(__ushort_as_half(h));
 }

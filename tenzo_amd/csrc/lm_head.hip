@@ -134,10 +134,10 @@ lm_head_i8_kernel(const uint4* __restrict__ w, const int32_t* __restrict__ codes
     int acc0 = 0, acc1 = 0;
     int64_t c = wave;
     for (; c + 12 < HC; c += 16) {
-        const uint4 v0 = wb[c * 64];
-        const uint4 v1 = wb[(c + 4) * 64];
-        const uint4 v2 = wb[(c + 8) * 64];
-        const uint4 v3 = wb[(c + 12) * 64];
+        const uint4 v0 = ld_nt16(&wb[c * 64]);
+        const uint4 v1 = ld_nt16(&wb[(c + 4) * 64]);
+        const uint4 v2 = ld_nt16(&wb[(c + 8) * 64]);
+        const uint4 v3 = ld_nt16(&wb[(c + 12) * 64]);
         const int32_t* a0 = codes + c * 4;
         acc0 = sdot4(v0.x, a0[0], acc0);
         acc0 = sdot4(v0.y, a0[1], acc0);
@@ -157,7 +157,7 @@ lm_head_i8_kernel(const uint4* __restrict__ w, const int32_t* __restrict__ codes
         acc1 = sdot4(v3.w, a0[51], acc1);
     }
     for (; c < HC; c += 4) {
-        const uint4 v0 = wb[c * 64];
+        const uint4 v0 = ld_nt16(&wb[c * 64]);
         const int32_t* a0 = codes + c * 4;
         acc0 = sdot4(v0.x, a0[0], acc0);
         acc0 = sdot4(v0.y, a0[1], acc0);

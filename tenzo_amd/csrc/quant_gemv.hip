@@ -332,7 +332,8 @@ q8_0_lds_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float
         const int rounds = (kQ8R * rb + 1023) / 1024;
         for (int i = wave; i < rounds; i += 4)  // (wave-uniform)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (q8_lds_void*)(w_s + 1024 * i), 16,
-                                                     (uint32_t)(1024 * i + 16 * lane), 0, 0, 0);
+                                                     (uint32_t)(1024 * i + 16 * lane), 0, 0,
+                                                     2 /* nontemporal */);
     }
     stg.store(a_s, act + (int64_t)b * K, K);
     __builtin_amdgcn_s_waitcnt(0);  // (this wave's copies and loads landed)

@@ -378,7 +378,7 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
         uint4 v[kTl1J];
 #pragma unroll
         for (int j = 0; j < kTl1J; ++j)
-            if (j < nj) v[j] = wb[(s0 + wave + 4 * j) * 64];
+            if (j < nj) v[j] = ld_nt16(&wb[(s0 + wave + 4 * j) * 64]);
         cs[t < cu ? t : kTl1CU + t] = cv;
         for (int u = t + 256; u < cu; u += 256) cs[u] = c4[s0 * 4 + u];
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
@@ -390,7 +390,7 @@ tl1_gemv_kernel(const uint4* __restrict__ w, const int8_t* __restrict__ codes,
         for (int64_t j0 = kTl1J; j0 < nj; j0 += kTl1J) {
 #pragma unroll
             for (int j = 0; j < kTl1J; ++j)
-                if (j0 + j < nj) v[j] = wb[(s0 + wave + 4 * (j0 + j)) * 64];
+                if (j0 + j < nj) v[j] = ld_nt16(&wb[(s0 + wave + 4 * (j0 + j)) * 64]);
 #pragma unroll
             for (int j = 0; j < kTl1J; ++j)
                 if (j0 + j < nj) acc = dot16(v[j], a32 + (wave + 4 * (j0 + j)) * 16, acc);
@@ -467,7 +467,7 @@ tl1_gemv_f32_kernel(const uint4* __restrict__ w, const float* __restrict__ x, in
     uint4 v[kTl1J];
 #pragma unroll
     for (int j = 0; j < kTl1J; ++j)
-        if (j < nj) v[j] = wb[(wave + 4 * j) * 64];
+        if (j < nj) v[j] = ld_nt16(&wb[(wave + 4 * j) * 64]);
     float amax = 1e-6f;
 #pragma unroll
     for (int j = 0; j < J; ++j)
@@ -494,7 +494,7 @@ tl1_gemv_f32_kernel(const uint4* __restrict__ w, const float* __restrict__ x, in
     for (int64_t j0 = kTl1J; j0 < nj; j0 += kTl1J) {
 #pragma unroll
         for (int j = 0; j < kTl1J; ++j)
-            if (j0 + j < nj) v[j] = wb[(wave + 4 * (j0 + j)) * 64];
+            if (j0 + j < nj) v[j] = ld_nt16(&wb[(wave + 4 * (j0 + j)) * 64]);
 #pragma unroll
         for (int j = 0; j < kTl1J; ++j)
             if (j0 + j < nj) acc = dot16(v[j], a32 + (wave + 4 * (j0 + j)) * 16, acc);
