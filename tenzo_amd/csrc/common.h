@@ -257,7 +257,7 @@ __device__ __forceinline__ int sdot4(uint32_t a, int32_t b, int c) {
 // A 16-byte load with the nontemporal hint, for weights a kernel reads once: on a pure
 // 330 MB read it gives ~6% more bandwidth than a plain load and leaves the caches to the
 // data that is read again. (The decode chunk kernel's K/V loads stay plain: there the
-// hint made attention 20-30% slower at 8k-32k contexts.)
+// hint, on the K or on the V loads, made attention 20-30% slower at 8k-32k contexts.)
 __device__ __forceinline__ uint4 ld_nt16(const uint4* p) {
     typedef unsigned u4nt __attribute__((ext_vector_type(4)));
     const u4nt v = __builtin_nontemporal_load(reinterpret_cast<const u4nt*>(p));
