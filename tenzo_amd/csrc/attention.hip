@@ -219,118 +219,9 @@ __device__ __forceinline__ void quant_kv_pair(float x0, float x1, int8_t* codes_
     *s_out = __fmul_rn(amax, 1.0f / 127.0f);
 }
 
-// One context chunk of the G query heads that share a kv head: scores of
-// tokens t0 .. t0+nt-1 against the rotated queries qs, the chunk's softmax
-// statistics, and the weighted values. On return (after a block barrier)
-// ow[w][g][:] hold the 4 waves' value sums and mstat / lstat the chunk's max
-// and exponent sum; the chunk partial of head g is then
-// o = (ow[0] + ow[1]) + (ow[2] + ow[3]). When has_new, position pos reads the
-// just-quantized row from newk / newv / news instead of the cache. Shared by
-// the decode chunk kernel and the prefill kernel, so both sum in one order.
-template <int G>
-__device__ __forceinline__ void chunk_partial(const float (&qs)[G][kD], float (&sc)[G][kMaxChunk],
-                                              float (&ow)[4][G][kD], float* mstat, float* lstat,
-                                              const int8_t* __restrict__ kbase,
-                                              const int8_t* __restrict__ vbase,
-                                              const uint16_t* __restrict__ ksb,
-                                              const uint16_t* __restrict__ vsb, int t0, int nt,
-                                              bool has_new, int pos, const int8_t* newk,
-                                              const int8_t* newv, const float* news) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int kn = lane & 15, kq = lane >> 4;
-
-    // ---- scores (:678-694) on MFMA (score_tile) ----
-    {
-        h4a qh[8], ql[8];
-        float qin[4];
-        q_operands<G>(qs, qh, ql, qin);
-        for (int tile = wave; tile * 16 < nt; tile += 4) {
-            const int tl = tile * 16 + kn;
-            const int t = t0 + min(tl, nt - 1);
-            const bool fresh = has_new && t == pos;
-            const int8_t* krow = fresh ? newk : kbase + (int64_t)t * kD;
-            const uint4 k0 = *reinterpret_cast<const uint4*>(krow + 32 * kq);
-            const uint4 k1 = *reinterpret_cast<const uint4*>(krow + 32 * kq + 16);
-            const f4a d = score_tile(qh, ql, k0, k1);
-            if (tl < nt) {
-                const float skf = fresh ? news[0] : half_bits_to_float(ksb[t]);
-                const float f = __fmul_rn(skf, kScaleFactor);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int g = 4 * kq + e;
-                    if (g < G) sc[g][tl] = __fmul_rn(d[e] * qin[e], f);
-                }
-            }
-        }
-    }
-    __syncthreads();
-
-    // ---- chunk softmax statistics (:824-830) ----
-    for (int g = wave; g < G; g += 4) {
-        float m = -1e30f;
-        for (int i = lane; i < nt; i += 64) m = fmaxf(m, sc[g][i]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int i = lane; i < nt; i += 64) {
-            const float e = expf(sc[g][i] - m);
-            sc[g][i] = e;
-            l += e;
-        }
-        l = wave_sum_tree(l);
-        if (lane == 0) {
-            mstat[g] = m;
-            lstat[g] = l;
-        }
-    }
-    __syncthreads();
-
-    // ---- weighted values (:842-851) on MFMA (value_tile) ----
-    {
-        // the wave's largest V scale over its tiles' tokens sets its power-of-two scale
-        float vmax = 0.0f;
-        for (int tile = wave; tile * 16 < nt; tile += 4)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = t0 + min(tile * 16 + 4 * kq + e, nt - 1);
-                vmax = fmaxf(vmax, has_new && t == pos ? news[1] : half_bits_to_float(vsb[t]));
-            }
-        const int wsh = fp16_span_exp(wave_max(vmax));
-        const float wup = ldexpf(1.0f, wsh), wdown = ldexpf(1.0f, -wsh);
-        f4a acc8[8];
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int tile = wave; tile * 16 < nt; tile += 4) {
-            float svf[4];
-            uint2 v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int t = t0 + min(tile * 16 + 4 * kq + e, nt - 1);
-                const bool fresh = has_new && t == pos;
-                const int8_t* vrow = fresh ? newv : vbase + (int64_t)t * kD;
-                v[e] = *reinterpret_cast<const uint2*>(vrow + 8 * kn);
-                svf[e] = fresh ? news[1] : half_bits_to_float(vsb[t]);
-            }
-            h4a wh[1], wl[1];
-            w_operands<G>(sc, tile, nt, svf, wup, wh, wl);
-            value_tile(wh, wl, v, acc8);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int g = 4 * kq + e;
-            if (g < G) {
-#pragma unroll
-                for (int dt = 0; dt < 8; ++dt) ow[wave][g][8 * kn + dt] = acc8[dt][e] * wdown;
-            }
-        }
-    }
-    __syncthreads();
-}
-
-// The decode chunk kernel. Its arithmetic is chunk_partial's, tile for tile in
-// the same order (so prefill and decode agree bit for bit), but the loads are
-// arranged for latency: each lane's K and V rows of the chunk (U = T / 32, so
+// The decode chunk kernel (attn_prefill_exact_kernel repeats its arithmetic per
+// row, so prefill and decode agree bit for bit). The loads are arranged for
+// latency: each lane's K and V rows of the chunk (U = T / 32, so
 // (U + 1) / 2 tiles of 16 tokens per wave; rows past the context read the
 // chunk's last row and are not used) are issued right after the query loads,
 // so they stream while q is rotated and the new token appended; the new
@@ -634,75 +525,221 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
     a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, L);
 }
 
-// Prefill attention: one workgroup per (kv head, query row b) walks the
-// query's context chunks in order with chunk_partial (the decode chunk
-// kernel's arithmetic and chunk size at that position), keeps each chunk's
-// (m, l) in LDS and its value sums in the partial scratch (each value written
-// and read back by the same thread), then merges the chunks exactly as
-// attn_combine_kernel does. Dynamic LDS: m and l of G heads x max_chunks.
-template <int G>
-__global__ void __launch_bounds__(256) attn_prefill_kernel(AttnArgs a) {
-    __shared__ float qs[G][kD];
-    __shared__ float sc[G][kMaxChunk];
-    __shared__ float ow[4][G][kD];
-    __shared__ float mstat[G], lstat[G];
-    extern __shared__ float cstat[];
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int tid = threadIdx.x;
-    const int pos = a.pos + b;
-    const int seq_len = pos + 1;
-    const int T = pick_chunk(seq_len, a.Hkv, 1);
-    const int nchunks = (seq_len + T - 1) / T;
-    const float* rope = a.rope + (int64_t)pos * kD;
-    for (int i = tid; i < G * 64; i += 256) {  // RoPE on the G query heads (:460-481)
-        const int g = i >> 6, j = i & 63;
+// Exact prefill attention, batched: the decode chunk kernel's arithmetic for
+// QB = 16 / G queries at once. A workgroup takes chunk c (decode's chunk size
+// T at those positions, the same for the launch) of kv head h for the queries
+// qb QB .. qb QB + QB - 1; the 16 MFMA rows are (query j, head g) = row
+// j G + g, so every score and value tile is one MFMA for all of them. MFMA
+// rows do not interact, and each row's operands are the ones decode forms for
+// that query (its query vector's own power-of-two scale; its chunk's valid
+// tokens nt_j, zero weights past them; its own V-scale exponent per wave over
+// the same tiles; the same statistics reduction per row), so each row's
+// partial (m, l, o) -- and after attn_combine_kernel its output -- equals the
+// token-by-token decode step's bit for bit. Queries whose context ends before
+// chunk c contribute no rows.
+template <int G, int U>
+__global__ void __launch_bounds__(256) attn_prefill_exact_kernel(AttnArgs a) {
+    constexpr int QB = 16 / G;
+    constexpr int NTW = (U + 1) / 2;  // 16-token tiles per wave (T = 32 U)
+    __shared__ float qs[16][kD];
+    __shared__ float sc[16][kMaxChunk + 4];  // (+4: the W reads of 16 rows hit 16 bank groups)
+    __shared__ float ow[4][16][kD];
+    __shared__ float mstat[16], lstat[16];
+    const int c = blockIdx.x, h = blockIdx.y, qb = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kn = lane & 15, kq = lane >> 4;
+    const int T = a.T;
+    const int t0 = c * T;
+    const int b0 = qb * QB;
+    const int nq = min(QB, a.pos_n - b0);
+    // the block's last query has the longest context
+    const int nt_max = min(T, a.pos + b0 + nq - t0);
+    if (nt_max <= 0) return;
+    auto nt_of = [&](int j) {  // valid tokens of chunk c for query j (<= 0: none)
+        return j < nq ? min(T, a.pos + b0 + j + 1 - t0) : 0;
+    };
+    const int64_t cache_head = (int64_t)h * a.max_seq;
+    const int8_t* kbase = a.kc + cache_head * kD;
+    const int8_t* vbase = a.vc + cache_head * kD;
+    const uint16_t* ksb = a.ks + cache_head;
+    const uint16_t* vsb = a.vs + cache_head;
+
+    // ---- every load first: the rows' query pairs and RoPE factors, then this lane's K and
+    // V rows of the wave's tiles (tokens past the block's context read its last row) ----
+    constexpr int kQI = 16 * 64 / 256;
+    float qx0[kQI], qx1[kQI], qcs[kQI], qsn[kQI];
+#pragma unroll
+    for (int r = 0; r < kQI; ++r) {
+        const int i = tid + 256 * r;
+        const int row = i >> 6, jd = i & 63;
+        const int j = min(row / G, nq - 1), g = row % G;  // (rows past nq: a valid query)
+        const int b = b0 + j;
         const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)(h * G + g) * kD;
-        const float x0 = qv[j], x1 = qv[j + 64];
-        const float cs = rope[j], sn = rope[64 + j];
-        qs[g][j] = __builtin_fmaf(x0, cs, -__fmul_rn(x1, sn));
-        qs[g][j + 64] = __builtin_fmaf(x0, sn, __fmul_rn(x1, cs));
+        const float* rope = a.rope + (int64_t)(a.pos + b) * kD;
+        qx0[r] = qv[jd];
+        qx1[r] = qv[jd + 64];
+        qcs[r] = rope[jd];
+        qsn[r] = rope[64 + jd];
+    }
+    asm volatile("" ::: "memory");
+    uint4 kr[NTW][2];
+    uint16_t ksr[NTW];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i) {
+        const int t = t0 + min((wave + 4 * i) * 16 + kn, nt_max - 1);
+        const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + 32 * kq);
+        kr[i][0] = kp[0];
+        kr[i][1] = kp[1];
+        ksr[i] = ksb[t];
+    }
+    uint2 vm[NTW][4];
+    uint16_t vms[NTW][4];
+#pragma unroll
+    for (int i = 0; i < NTW; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = t0 + min((wave + 4 * i) * 16 + 4 * kq + e, nt_max - 1);
+            vm[i][e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)t * kD + 8 * kn);
+            vms[i][e] = vsb[t];
+        }
+
+    // ---- RoPE on the rows' query vectors (:460-481) ----
+#pragma unroll
+    for (int r = 0; r < kQI; ++r) {
+        const int i = tid + 256 * r;
+        const int row = i >> 6, jd = i & 63;
+        const bool live = row / G < nq;
+        qs[row][jd] = live ? __builtin_fmaf(qx0[r], qcs[r], -__fmul_rn(qx1[r], qsn[r])) : 0.0f;
+        qs[row][jd + 64] = live ? __builtin_fmaf(qx0[r], qsn[r], __fmul_rn(qx1[r], qcs[r])) : 0.0f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- scores (:678-694) on MFMA: rows 4 kq + e of lane (kn, kq) ----
+    {
+        h4a qh[8], ql[8];
+        float qin[4];
+        q_operands<16>(qs, qh, ql, qin);
+        int ntr[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ntr[e] = nt_of((4 * kq + e) / G);
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            const int tile = wave + 4 * i;
+            if (tile * 16 >= nt_max) break;  // (wave-uniform)
+            const int tl = tile * 16 + kn;
+            const f4a d = score_tile(qh, ql, kr[i][0], kr[i][1]);
+            const float f = __fmul_rn(half_bits_to_float(ksr[i]), kScaleFactor);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (tl < ntr[e]) sc[4 * kq + e][tl] = __fmul_rn(d[e] * qin[e], f);
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- chunk softmax statistics (:824-830), row by row as decode does per head ----
+    for (int row = wave; row < 16; row += 4) {
+        const int nt = nt_of(row / G);
+        if (nt <= 0) continue;  // (wave-uniform)
+        float m = -1e30f;
+        for (int i = lane; i < nt; i += 64) m = fmaxf(m, sc[row][i]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int i = lane; i < nt; i += 64) {
+            const float e = expf(sc[row][i] - m);
+            sc[row][i] = e;
+            l += e;
+        }
+        l = wave_sum_tree(l);
+        if (lane == 0) {
+            mstat[row] = m;
+            lstat[row] = l;
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- weighted values (:842-851) on MFMA (value_tile) ----
+    {
+        // per query, the wave's largest V scale over its tiles' valid tokens sets its
+        // power-of-two scale (decode: the same tiles, the tokens clamped to the chunk, whose
+        // repeats of the last valid token do not change the maximum)
+        float vmq[QB];
+#pragma unroll
+        for (int j = 0; j < QB; ++j) vmq[j] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            if ((wave + 4 * i) * 16 >= nt_max) break;  // (wave-uniform)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int tl = (wave + 4 * i) * 16 + 4 * kq + e;
+                const float sv = half_bits_to_float(vms[i][e]);
+#pragma unroll
+                for (int j = 0; j < QB; ++j)
+                    if (tl < nt_of(j)) vmq[j] = fmaxf(vmq[j], sv);
+            }
+        }
+        // this lane's W row (kn) and D rows (4 kq + e): their queries' exponents
+        float wup_row = 1.0f, wdn[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        int nt_w = 0;
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+            const int sh = fp16_span_exp(wave_max(vmq[j]));
+            const float up = ldexpf(1.0f, sh), down = ldexpf(1.0f, -sh);
+            if (kn / G == j) {
+                wup_row = up;
+                nt_w = nt_of(j);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if ((4 * kq + e) / G == j) wdn[e] = down;
+        }
+        f4a acc8[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            const int tile = wave + 4 * i;
+            if (tile * 16 >= nt_max) break;  // (wave-uniform)
+            float svf[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) svf[e] = half_bits_to_float(vms[i][e]);
+            // w_operands' arithmetic with this row's valid length and scale
+            const float4 p4 = *reinterpret_cast<const float4*>(&sc[kn][tile * 16 + 4 * kq]);
+            const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+            h4a wh[1], wl[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int tl = tile * 16 + 4 * kq + e;
+                const float w = tl < nt_w ? __fmul_rn(pv[e], svf[e]) * wup_row : 0.0f;
+                const _Float16 hi = (_Float16)w;
+                wh[0][e] = hi;
+                wl[0][e] = (_Float16)(w - (float)hi);
+            }
+            value_tile(wh, wl, vm[i], acc8);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) ow[wave][4 * kq + e][8 * kn + dt] = acc8[dt][e] * wdn[e];
     }
     __syncthreads();
-    const int64_t cache_head = (int64_t)h * a.max_seq;
-    float* mst = cstat;                       // [G][max_chunks]
-    float* lst = cstat + G * a.max_chunks;    // [G][max_chunks]
-    for (int c = 0; c < nchunks; ++c) {
-        const int t0 = c * T;
-        const int nt = min(t0 + T, seq_len) - t0;
-        chunk_partial<G>(qs, sc, ow, mstat, lstat, a.kc + cache_head * kD, a.vc + cache_head * kD,
-                         a.ks + cache_head, a.vs + cache_head, t0, nt, false, pos, nullptr,
-                         nullptr, nullptr);
-        for (int i = tid; i < G * kD; i += 256) {
-            const int g = i >> 7, d = i & 127;
-            const float o = (ow[0][g][d] + ow[1][g][d]) + (ow[2][g][d] + ow[3][g][d]);
-            const int qh = h * G + g;
-            if (nchunks == 1)
-                a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, lstat[g]);
-            else
-                a.part[(((int64_t)b * a.Hq + qh) * a.max_chunks + c) * kPartStride + 2 + d] = o;
-        }
-        if (tid < G) {
-            mst[tid * a.max_chunks + c] = mstat[tid];
-            lst[tid * a.max_chunks + c] = lstat[tid];
-        }
-        __syncthreads();  // ow, sc and the statistics are reused by the next chunk
-    }
-    if (nchunks == 1) return;
-    for (int i = tid; i < G * kD; i += 256) {  // attn_combine_kernel's merge
-        const int g = i >> 7, d = i & 127;
+    for (int i = tid; i < 16 * kD; i += 256) {
+        const int row = i >> 7, d = i & 127;
+        const int j = row / G, g = row % G;
+        if (nt_of(j) <= 0) continue;
+        const int b = b0 + j;
         const int qh = h * G + g;
-        const float* pp = a.part + ((int64_t)b * a.Hq + qh) * a.max_chunks * kPartStride;
-        const float* mg = mst + g * a.max_chunks;
-        const float* lg = lst + g * a.max_chunks;
-        float M = -1e30f;
-        for (int c = 0; c < nchunks; ++c) M = fmaxf(M, mg[c]);
-        float L = 0.0f, o = 0.0f;
-        for (int c = 0; c < nchunks; ++c) {
-            const float e = expf(mg[c] - M);
-            L = __builtin_fmaf(e, lg[c], L);
-            o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
+        const float o = (ow[0][row][d] + ow[1][row][d]) + (ow[2][row][d] + ow[3][row][d]);
+        if (a.pos + b + 1 <= T) {  // one chunk: the output itself
+            a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, lstat[row]);
+        } else {
+            float* pp = a.part + (((int64_t)b * a.Hq + qh) * a.max_chunks + c) * kPartStride;
+            pp[2 + d] = o;
+            if (d == 0) {
+                pp[0] = mstat[row];
+                pp[1] = lstat[row];
+            }
         }
-        a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, L);
     }
 }
 
@@ -1038,38 +1075,54 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
         }
         return launch_status("attn_prefill_mfma_kernel");
     }
-    // exact form: queries in groups whose chunk partials fit ~64 MiB of scratch
-    const int mc = attn_prefill_max_chunks(P.pos0, P.n, P.Hkv);
-    const size_t per_query = (size_t)P.Hq * mc * kPartStride * 4;
-    const int qg_max = mc > 1 ? (int)std::max<size_t>(1, std::min<size_t>(P.n, (64u << 20) / per_query))
-                              : P.n;
-    const size_t lds = (size_t)2 * G * mc * 4;
-    if (lds > 64 * 1024) {
-        set_error("prefill attention: %d chunks per query exceed the LDS budget", mc);
+    // exact form (attn_prefill_exact_kernel, then decode's merge): runs of queries with one
+    // chunk size (it changes only at a few context lengths), in groups whose chunk partials
+    // fit 256 MiB of scratch
+    if (G != 1 && G != 2 && G != 4 && G != 8) {
+        set_error("attention: query heads per kv head must be 1, 2, 4 or 8 (got %d)", G);
         return TENZO_ERROR_UNSUPPORTED;
     }
-    for (int i0 = 0; i0 < P.n; i0 += qg_max) {
-        const int n = std::min(qg_max, P.n - i0);
-        a.pos = P.pos0 + i0;
-        a.q = P.q + (int64_t)i0 * P.row_stride;
-        a.out = P.out + (int64_t)i0 * P.out_stride;
-        a.max_chunks = mc;
-        a.part = nullptr;
-        if (mc > 1) {
-            a.part = (float*)Scratch::get(kScratchAttn, (size_t)n * per_query, st);
-            if (!a.part) return TENZO_ERROR_OUT_OF_MEMORY;
+    const int QB = 16 / G;
+    for (int s0 = 0; s0 < P.n;) {
+        const int T = pick_chunk(P.pos0 + s0 + 1, P.Hkv, 1);
+        int s1 = s0 + 1;
+        while (s1 < P.n && pick_chunk(P.pos0 + s1 + 1, P.Hkv, 1) == T) ++s1;
+        const int mc = (int)ceil_div(P.pos0 + s1, T);  // chunks of the run's last query
+        const size_t per_query = (size_t)P.Hq * mc * kPartStride * 4;
+        const int qg_max =
+            mc > 1 ? (int)std::max<size_t>(1, std::min<size_t>(s1 - s0, (256u << 20) / per_query))
+                   : s1 - s0;
+        for (int i0 = s0; i0 < s1; i0 += qg_max) {
+            const int n = std::min(qg_max, s1 - i0);
+            a.pos = P.pos0 + i0;
+            a.pos_n = n;
+            a.T = T;
+            a.q = P.q + (int64_t)i0 * P.row_stride;
+            a.out = P.out + (int64_t)i0 * P.out_stride;
+            a.max_chunks = mc;
+            a.part = nullptr;
+            if (mc > 1) {
+                a.part = (float*)Scratch::get(kScratchAttn, (size_t)n * per_query, st);
+                if (!a.part) return TENZO_ERROR_OUT_OF_MEMORY;
+            }
+            const dim3 grid((unsigned)mc, (unsigned)P.Hkv, (unsigned)ceil_div(n, QB));
+            const int U = T / 32;  // 1 .. 8 (pick_chunk: multiples of 32 up to kMaxChunk)
+#define PX_CASE(GG, UU)                                                                       \
+    if (G == GG && U == UU)                                                                   \
+        hipLaunchKernelGGL((attn_prefill_exact_kernel<GG, UU>), grid, dim3(256), 0, st, a);
+#define PX_G(GG)                                                                              \
+    PX_CASE(GG, 1) PX_CASE(GG, 2) PX_CASE(GG, 3) PX_CASE(GG, 4) PX_CASE(GG, 5) PX_CASE(GG, 6)   \
+    PX_CASE(GG, 7) PX_CASE(GG, 8)
+            PX_G(1) PX_G(2) PX_G(4) PX_G(8)
+#undef PX_G
+#undef PX_CASE
+            if ((rc = launch_status("attn_prefill_exact_kernel"))) return rc;
+            if (mc > 1) {
+                hipLaunchKernelGGL(attn_combine_kernel, dim3(P.Hq, n), dim3(128), 0, st, a);
+                if ((rc = launch_status("attn_combine_kernel"))) return rc;
+            }
         }
-        dim3 grid(P.Hkv, n);
-        switch (G) {
-            case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(256), lds, st, a); break;
-            case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(256), lds, st, a); break;
-            case 4: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(256), lds, st, a); break;
-            case 8: hipLaunchKernelGGL(attn_prefill_kernel<8>, grid, dim3(256), lds, st, a); break;
-            default:
-                set_error("attention: query heads per kv head must be 1, 2, 4 or 8 (got %d)", G);
-                return TENZO_ERROR_UNSUPPORTED;
-        }
-        if ((rc = launch_status("attn_prefill_kernel"))) return rc;
+        s0 = s1;
     }
     return TENZO_SUCCESS;
 }
