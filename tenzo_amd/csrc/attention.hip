@@ -743,6 +743,200 @@ __global__ void __launch_bounds__(256) attn_prefill_exact_kernel(AttnArgs a) {
     }
 }
 
+// attn_prefill_exact_kernel for 32-token chunks, two chunks per workgroup: with
+// T = 32 a chunk has two 16-token tiles, which decode's waves 0 and 1 take
+// (waves 2 and 3 add zeros), so here waves 0, 1 take chunk 2 cp and waves 2, 3
+// chunk 2 cp + 1, each pair exactly as decode's waves 0 and 1; the partial of
+// a chunk is its pair's sum plus the two zero sums, as decode adds them.
+template <int G>
+__global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
+    constexpr int QB = 16 / G;
+    constexpr int T = 32;
+    __shared__ float qs[16][kD];
+    __shared__ float sc[2][16][T + 4];
+    __shared__ float ow[4][16][kD];
+    __shared__ float mstat[2][16], lstat[2][16];
+    const int cp = blockIdx.x, h = blockIdx.y, qb = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kn = lane & 15, kq = lane >> 4;
+    const int ch = wave >> 1, tile = wave & 1;  // this wave's chunk of the pair and its tile
+    const int b0 = qb * QB;
+    const int nq = min(QB, a.pos_n - b0);
+    const int last_len = a.pos + b0 + nq;  // the block's longest context
+    if (2 * cp * T >= last_len) return;
+    auto nt_of = [&](int k, int j) {  // valid tokens of pair chunk k for query j
+        return j < nq ? min(T, a.pos + b0 + j + 1 - (2 * cp + k) * T) : 0;
+    };
+    const int t0 = (2 * cp + ch) * T;               // this wave's chunk
+    const int nt_max = min(T, last_len - t0);       // (<= 0: the pair's second chunk is empty)
+    const int64_t cache_head = (int64_t)h * a.max_seq;
+    const int8_t* kbase = a.kc + cache_head * kD;
+    const int8_t* vbase = a.vc + cache_head * kD;
+    const uint16_t* ksb = a.ks + cache_head;
+    const uint16_t* vsb = a.vs + cache_head;
+
+    // ---- every load first (tokens past the context read the context's last row) ----
+    constexpr int kQI = 16 * 64 / 256;
+    float qx0[kQI], qx1[kQI], qcs[kQI], qsn[kQI];
+#pragma unroll
+    for (int r = 0; r < kQI; ++r) {
+        const int i = tid + 256 * r;
+        const int row = i >> 6, jd = i & 63;
+        const int j = min(row / G, nq - 1), g = row % G;
+        const int b = b0 + j;
+        const float* qv = a.q + (int64_t)b * a.q_stride + (int64_t)(h * G + g) * kD;
+        const float* rope = a.rope + (int64_t)(a.pos + b) * kD;
+        qx0[r] = qv[jd];
+        qx1[r] = qv[jd + 64];
+        qcs[r] = rope[jd];
+        qsn[r] = rope[64 + jd];
+    }
+    asm volatile("" ::: "memory");
+    const int tlast = last_len - 1;
+    uint4 k0, k1;
+    uint16_t ksr;
+    {
+        const int t = min(t0 + tile * 16 + kn, tlast);
+        const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + 32 * kq);
+        k0 = kp[0];
+        k1 = kp[1];
+        ksr = ksb[t];
+    }
+    uint2 vm[4];
+    uint16_t vms[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int t = min(t0 + tile * 16 + 4 * kq + e, tlast);
+        vm[e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)t * kD + 8 * kn);
+        vms[e] = vsb[t];
+    }
+
+    // ---- RoPE on the rows' query vectors (:460-481) ----
+#pragma unroll
+    for (int r = 0; r < kQI; ++r) {
+        const int i = tid + 256 * r;
+        const int row = i >> 6, jd = i & 63;
+        const bool live = row / G < nq;
+        qs[row][jd] = live ? __builtin_fmaf(qx0[r], qcs[r], -__fmul_rn(qx1[r], qsn[r])) : 0.0f;
+        qs[row][jd + 64] = live ? __builtin_fmaf(qx0[r], qsn[r], __fmul_rn(qx1[r], qcs[r])) : 0.0f;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- scores (:678-694) on MFMA: rows 4 kq + e of lane (kn, kq) ----
+    if (tile * 16 < nt_max) {  // (wave-uniform)
+        h4a qh[8], ql[8];
+        float qin[4];
+        q_operands<16>(qs, qh, ql, qin);
+        const int tl = tile * 16 + kn;
+        const f4a d = score_tile(qh, ql, k0, k1);
+        const float f = __fmul_rn(half_bits_to_float(ksr), kScaleFactor);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (tl < nt_of(ch, (4 * kq + e) / G)) sc[ch][4 * kq + e][tl] = __fmul_rn(d[e] * qin[e], f);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- chunk softmax statistics (:824-830), (chunk, row) by (chunk, row) ----
+    for (int r = wave; r < 32; r += 4) {
+        const int k = r >> 4, row = r & 15;
+        const int nt = nt_of(k, row / G);
+        if (nt <= 0) continue;  // (wave-uniform)
+        float m = -1e30f;
+        for (int i = lane; i < nt; i += 64) m = fmaxf(m, sc[k][row][i]);
+        m = wave_max(m);
+        float l = 0.0f;
+        for (int i = lane; i < nt; i += 64) {
+            const float e = expf(sc[k][row][i] - m);
+            sc[k][row][i] = e;
+            l += e;
+        }
+        l = wave_sum_tree(l);
+        if (lane == 0) {
+            mstat[k][row] = m;
+            lstat[k][row] = l;
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // ---- weighted values (:842-851) on MFMA (value_tile) ----
+    {
+        const bool has_tile = tile * 16 < nt_max;  // (wave-uniform)
+        float vmq[QB];
+#pragma unroll
+        for (int j = 0; j < QB; ++j) vmq[j] = 0.0f;
+        if (has_tile) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int tl = tile * 16 + 4 * kq + e;
+                const float sv = half_bits_to_float(vms[e]);
+#pragma unroll
+                for (int j = 0; j < QB; ++j)
+                    if (tl < nt_of(ch, j)) vmq[j] = fmaxf(vmq[j], sv);
+            }
+        }
+        float wup_row = 1.0f, wdn[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+        int nt_w = 0;
+#pragma unroll
+        for (int j = 0; j < QB; ++j) {
+            const int sh = fp16_span_exp(wave_max(vmq[j]));
+            const float up = ldexpf(1.0f, sh), down = ldexpf(1.0f, -sh);
+            if (kn / G == j) {
+                wup_row = up;
+                nt_w = nt_of(ch, j);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if ((4 * kq + e) / G == j) wdn[e] = down;
+        }
+        f4a acc8[8];
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc8[dt] = f4a{0.0f, 0.0f, 0.0f, 0.0f};
+        if (has_tile) {
+            float svf[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) svf[e] = half_bits_to_float(vms[e]);
+            const float4 p4 = *reinterpret_cast<const float4*>(&sc[ch][kn][tile * 16 + 4 * kq]);
+            const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
+            h4a wh[1], wl[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int tl = tile * 16 + 4 * kq + e;
+                const float w = tl < nt_w ? __fmul_rn(pv[e], svf[e]) * wup_row : 0.0f;
+                const _Float16 hi = (_Float16)w;
+                wh[0][e] = hi;
+                wl[0][e] = (_Float16)(w - (float)hi);
+            }
+            value_tile(wh, wl, vm, acc8);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) ow[wave][4 * kq + e][8 * kn + dt] = acc8[dt][e] * wdn[e];
+    }
+    __syncthreads();
+    for (int i = tid; i < 2 * 16 * kD; i += 256) {
+        const int k = i >> 11, row = (i >> 7) & 15, d = i & 127;
+        const int j = row / G, g = row % G;
+        if (nt_of(k, j) <= 0) continue;
+        const int b = b0 + j;
+        const int qh = h * G + g;
+        // decode's (ow0 + ow1) + (ow2 + ow3), its waves 2 and 3 holding zeros at T = 32
+        const float zero = 0.0f;
+        const float o = (ow[2 * k][row][d] + ow[2 * k + 1][row][d]) + (zero + zero);
+        if (a.pos + b + 1 <= T) {  // one chunk: the output itself
+            a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, lstat[k][row]);
+        } else {
+            float* pp = a.part + (((int64_t)b * a.Hq + qh) * a.max_chunks + 2 * cp + k) * kPartStride;
+            pp[2 + d] = o;
+            if (d == 0) {
+                pp[0] = mstat[k][row];
+                pp[1] = lstat[k][row];
+            }
+        }
+    }
+}
+
 // Prefill attention on fp16 MFMA, streaming form (an online softmax over the
 // causal prefix): a workgroup takes QP = 16 / G consecutive queries of one kv
 // head as the 16 MFMA rows (row m: query m / G, head m % G) and its 4 waves
@@ -1106,7 +1300,16 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
                 if (!a.part) return TENZO_ERROR_OUT_OF_MEMORY;
             }
             const dim3 grid((unsigned)mc, (unsigned)P.Hkv, (unsigned)ceil_div(n, QB));
+            const dim3 grid2((unsigned)ceil_div(mc, 2), (unsigned)P.Hkv, (unsigned)ceil_div(n, QB));
             const int U = T / 32;  // 1 .. 8 (pick_chunk: multiples of 32 up to kMaxChunk)
+            if (U == 1) {  // two chunks per workgroup
+                switch (G) {
+                    case 1: hipLaunchKernelGGL(attn_prefill_exact2_kernel<1>, grid2, dim3(256), 0, st, a); break;
+                    case 2: hipLaunchKernelGGL(attn_prefill_exact2_kernel<2>, grid2, dim3(256), 0, st, a); break;
+                    case 4: hipLaunchKernelGGL(attn_prefill_exact2_kernel<4>, grid2, dim3(256), 0, st, a); break;
+                    default: hipLaunchKernelGGL(attn_prefill_exact2_kernel<8>, grid2, dim3(256), 0, st, a); break;
+                }
+            } else {
 #define PX_CASE(GG, UU)                                                                       \
     if (G == GG && U == UU)                                                                   \
         hipLaunchKernelGGL((attn_prefill_exact_kernel<GG, UU>), grid, dim3(256), 0, st, a);
@@ -1116,6 +1319,7 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
             PX_G(1) PX_G(2) PX_G(4) PX_G(8)
 #undef PX_G
 #undef PX_CASE
+            }
             if ((rc = launch_status("attn_prefill_exact_kernel"))) return rc;
             if (mc > 1) {
                 hipLaunchKernelGGL(attn_combine_kernel, dim3(P.Hq, n), dim3(128), 0, st, a);
