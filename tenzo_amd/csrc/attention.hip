@@ -754,7 +754,7 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
     constexpr int T = 32;
     __shared__ float qs[16][kD];
     __shared__ float sc[2][16][T + 4];
-    __shared__ float ow[4][16][kD];
+    __shared__ float ow[2][16][kD];  // the tile-0 wave's sums of each chunk
     __shared__ float mstat[2][16], lstat[2][16];
     const int cp = blockIdx.x, h = blockIdx.y, qb = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -909,29 +909,44 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
             }
             value_tile(wh, wl, vm, acc8);
         }
+        // decode's o = (ow0 + ow1) + (ow2 + ow3) with its waves 2 and 3 holding zeros at
+        // T = 32: the tile-0 wave of each chunk hands its sums over LDS, the tile-1 wave
+        // adds its own (the same sum: addition commutes) and stores the partial
+        if (tile == 0) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
+            for (int e = 0; e < 4; ++e)
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) ow[wave][4 * kq + e][8 * kn + dt] = acc8[dt][e] * wdn[e];
-    }
-    __syncthreads();
-    for (int i = tid; i < 2 * 16 * kD; i += 256) {
-        const int k = i >> 11, row = (i >> 7) & 15, d = i & 127;
-        const int j = row / G, g = row % G;
-        if (nt_of(k, j) <= 0) continue;
-        const int b = b0 + j;
-        const int qh = h * G + g;
-        // decode's (ow0 + ow1) + (ow2 + ow3), its waves 2 and 3 holding zeros at T = 32
-        const float zero = 0.0f;
-        const float o = (ow[2 * k][row][d] + ow[2 * k + 1][row][d]) + (zero + zero);
-        if (a.pos + b + 1 <= T) {  // one chunk: the output itself
-            a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, lstat[k][row]);
-        } else {
-            float* pp = a.part + (((int64_t)b * a.Hq + qh) * a.max_chunks + 2 * cp + k) * kPartStride;
-            pp[2 + d] = o;
-            if (d == 0) {
-                pp[0] = mstat[k][row];
-                pp[1] = lstat[k][row];
+                for (int dt = 0; dt < 8; ++dt) ow[ch][4 * kq + e][8 * kn + dt] = acc8[dt][e] * wdn[e];
+        }
+        __syncthreads();
+        if (tile == 1) {
+            const float zero = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int row = 4 * kq + e;
+                const int j = row / G, g = row % G;
+                if (nt_of(ch, j) <= 0) continue;
+                const int bq = b0 + j;
+                const int qh = h * G + g;
+                float o[8];
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+                    o[dt] = (ow[ch][row][8 * kn + dt] + acc8[dt][e] * wdn[e]) + (zero + zero);
+                if (a.pos + bq + 1 <= T) {  // one chunk: the output itself
+                    float* dst = a.out + (int64_t)bq * a.out_stride + (int64_t)qh * kD + 8 * kn;
+                    const float L = lstat[ch][row];
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) dst[dt] = __fdiv_rn(o[dt], L);
+                } else {
+                    float* pp = a.part +
+                                (((int64_t)bq * a.Hq + qh) * a.max_chunks + 2 * cp + ch) * kPartStride;
+#pragma unroll
+                    for (int dt = 0; dt < 8; ++dt) pp[2 + 8 * kn + dt] = o[dt];
+                    if (kn == 0) {
+                        pp[0] = mstat[ch][row];
+                        pp[1] = lstat[ch][row];
+                    }
+                }
             }
         }
     }
