@@ -837,24 +837,42 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    // ---- chunk softmax statistics (:824-830), (chunk, row) by (chunk, row) ----
-    for (int r = wave; r < 32; r += 4) {
+    // ---- chunk softmax statistics (:824-830), two (chunk, row)s per wave pass ----
+    // Decode runs a row's statistics on one wave with token i in lane i (i < 32 here):
+    // wave_max and wave_sum_tree reduce the four 16-lane rows and combine them as
+    // (r0 . r1) . (r2 . r3), lanes 32-63 holding -1e30 / 0. Here lanes 0-31 take one row
+    // and lanes 32-63 the next, each half combined as its (r0 . r1) . (empty . empty),
+    // which is decode's value for that row.
+    for (int pr = wave; pr < 16; pr += 4) {
+        const int r = 2 * pr + (lane >> 5);  // this half's (chunk, row)
         const int k = r >> 4, row = r & 15;
         const int nt = nt_of(k, row / G);
-        if (nt <= 0) continue;  // (wave-uniform)
-        float m = -1e30f;
-        for (int i = lane; i < nt; i += 64) m = fmaxf(m, sc[k][row][i]);
-        m = wave_max(m);
+        const int i = lane & 31;
+        const float x = i < nt ? sc[k][row][i] : -1e30f;
+        float v = fmaxf(x, dpp_f<kDppXor1>(x));
+        v = fmaxf(v, dpp_f<kDppXor2>(v));
+        v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+        v = fmaxf(v, dpp_f<kDppMirror>(v));
+        const float empty = -1e30f;
+        const float mlo = fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(empty, empty));
+        const float mhi = fmaxf(fmaxf(lane_f(v, 32), lane_f(v, 48)), fmaxf(empty, empty));
+        const float m = lane < 32 ? mlo : mhi;
         float l = 0.0f;
-        for (int i = lane; i < nt; i += 64) {
-            const float e = expf(sc[k][row][i] - m);
+        if (i < nt) {
+            const float e = expf(x - m);
             sc[k][row][i] = e;
-            l += e;
+            l = e;
         }
-        l = wave_sum_tree(l);
-        if (lane == 0) {
+        float u = l + dpp_f<kDppXor1>(l);
+        u += dpp_f<kDppXor2>(u);
+        u += dpp_f<kDppHalfMirror>(u);
+        u += dpp_f<kDppMirror>(u);
+        const float zero = 0.0f;
+        const float llo = (lane_f(u, 0) + lane_f(u, 16)) + (zero + zero);
+        const float lhi = (lane_f(u, 32) + lane_f(u, 48)) + (zero + zero);
+        if (i == 0 && nt > 0) {
             mstat[k][row] = m;
-            lstat[k][row] = l;
+            lstat[k][row] = lane < 32 ? llo : lhi;
         }
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
