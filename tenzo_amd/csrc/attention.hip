@@ -470,9 +470,10 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
 // batch together with the statistics' loads), so the loop waits for memory
 // once per kMergeU chunks instead of once per chunk; the arithmetic (and so
 // the result) is that of the plain loop.
-constexpr int kMergeLds = 1024;  // chunks staged in LDS (contexts of 32K at 32-token chunks)
-constexpr int kMergeU = 64;
-
+// Decode: kMergeU = 64, kMergeLds = 1024 (contexts of 32K at 32-token chunks). The
+// exact prefill's merge (a few chunks per query, thousands of blocks) takes 16 and 128:
+// fewer registers and less LDS per block, so more blocks per CU.
+template <int kMergeU, int kMergeLds>
 __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
     __shared__ float ms[kMergeLds], ls[kMergeLds], es[kMergeLds];
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
@@ -1235,7 +1236,7 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
     int rc = launch_status("attn_int8_chunk_kernel");
     if (rc) return rc;
     if (L.max_chunks > 1) {
-        hipLaunchKernelGGL(attn_combine_kernel, dim3(L.Hq, L.B), dim3(128), 0, st, a);
+        hipLaunchKernelGGL((attn_combine_kernel<64, 1024>), dim3(L.Hq, L.B), dim3(128), 0, st, a);
         rc = launch_status("attn_combine_kernel");
     }
     return rc;
@@ -1253,7 +1254,7 @@ int launch_attn_combine(const float* part, float* out, int B, int Hq, int Hkv, i
     a.pos_dev = pos_dev;
     a.pos = pos;
     a.out_stride = (int64_t)Hq * kD;
-    hipLaunchKernelGGL(attn_combine_kernel, dim3(Hq, B), dim3(128), 0, st, a);
+    hipLaunchKernelGGL((attn_combine_kernel<64, 1024>), dim3(Hq, B), dim3(128), 0, st, a);
     return launch_status("attn_combine_kernel");
 }
 
@@ -1355,7 +1356,7 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
             }
             if ((rc = launch_status("attn_prefill_exact_kernel"))) return rc;
             if (mc > 1) {
-                hipLaunchKernelGGL(attn_combine_kernel, dim3(P.Hq, n), dim3(128), 0, st, a);
+                hipLaunchKernelGGL((attn_combine_kernel<16, 128>), dim3(P.Hq, n), dim3(128), 0, st, a);
                 if ((rc = launch_status("attn_combine_kernel"))) return rc;
             }
         }
