@@ -1236,7 +1236,10 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
     int rc = launch_status("attn_int8_chunk_kernel");
     if (rc) return rc;
     if (L.max_chunks > 1) {
-        hipLaunchKernelGGL((attn_combine_kernel<64, 1024>), dim3(L.Hq, L.B), dim3(128), 0, st, a);
+        if (L.max_chunks <= 100)  // (the same arithmetic; fewer registers, less LDS)
+            hipLaunchKernelGGL((attn_combine_kernel<16, 128>), dim3(L.Hq, L.B), dim3(128), 0, st, a);
+        else
+            hipLaunchKernelGGL((attn_combine_kernel<64, 1024>), dim3(L.Hq, L.B), dim3(128), 0, st, a);
         rc = launch_status("attn_combine_kernel");
     }
     return rc;
