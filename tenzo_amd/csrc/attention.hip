@@ -66,6 +66,10 @@ struct AttnArgs {
     float* k_rot;        // optional
 };
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t att_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+
 // Scores on fp16 MFMA (v_mfma_f32_16x16x16_f16), shared by the decode chunk
 // kernel and the prefill kernel so both give the same bits. A wave takes 16
 // tokens at a time: lane l holds token n = l % 16 of the tile and its dims
@@ -121,10 +125,9 @@ __device__ __forceinline__ void q_operands(const float (&qs)[G][kD], h4a (&qh)[8
     for (int e = 0; e < 4; ++e) qin[e] = __shfl(down, 4 * q + e, 64);
 }
 
-__device__ __forceinline__ h4a i8x4_h4(uint32_t w) {
+// e64 = 0x64006400 in a VGPR (a VGPR operand of v_perm_b32), made once by the caller
+__device__ __forceinline__ h4a i8x4_h4(uint32_t w, uint32_t e64) {
     const uint32_t x = w ^ 0x80808080u;
-    uint32_t e64 = 0x64006400u;  // (a VGPR operand of v_perm_b32)
-    asm volatile("" : "+v"(e64));
     const h2a bias = {(_Float16)-1152.0f, (_Float16)-1152.0f};
     const h2a p0 = __builtin_bit_cast(h2a, __builtin_amdgcn_perm(e64, x, 0x07010500u)) + bias;
     const h2a p1 = __builtin_bit_cast(h2a, __builtin_amdgcn_perm(e64, x, 0x07030502u)) + bias;
@@ -134,10 +137,12 @@ __device__ __forceinline__ h4a i8x4_h4(uint32_t w) {
 __device__ __forceinline__ f4a score_tile(const h4a (&qh)[8], const h4a (&ql)[8],
                                           const uint4 k0, const uint4 k1) {
     const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    uint32_t e64 = 0x64006400u;
+    asm volatile("" : "+v"(e64));
     f4a d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const h4a b = i8x4_h4(kw[j]);
+        const h4a b = i8x4_h4(kw[j], e64);
         d = __builtin_amdgcn_mfma_f32_16x16x16f16(qh[j], b, d, 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_16x16x16f16(ql[j], b, d, 0, 0, 0);
     }
@@ -282,15 +287,20 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
     // dims 32 (l / 16) ..; V lane tokens 4 (l / 16) .. +3, dims 8 (l % 16) .. +7
     constexpr int NTW = (U + 1) / 2;  // 16-token tiles per wave
     const int kn = lane & 15, kq = lane >> 4;
+    // (buffer loads from the chunk's first row: 32-bit offsets, no per-lane 64-bit address)
+    const __amdgpu_buffer_rsrc_t rk = att_rsrc(kbase + (int64_t)t0 * kD, (uint32_t)nt * kD);
+    const __amdgpu_buffer_rsrc_t rv = att_rsrc(vbase + (int64_t)t0 * kD, (uint32_t)nt * kD);
+    const __amdgpu_buffer_rsrc_t rks = att_rsrc(ksb + t0, (uint32_t)nt * 2);
+    const __amdgpu_buffer_rsrc_t rvs = att_rsrc(vsb + t0, (uint32_t)nt * 2);
     uint4 kr[NTW][2];
     uint16_t ksr[NTW];
 #pragma unroll
     for (int i = 0; i < NTW; ++i) {
-        const int t = t0 + min((wave + 4 * i) * 16 + kn, nt - 1);
-        const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + 32 * kq);
-        kr[i][0] = kp[0];
-        kr[i][1] = kp[1];
-        ksr[i] = ksb[t];
+        const uint32_t tl = (uint32_t)min((wave + 4 * i) * 16 + kn, nt - 1);
+        const uint32_t off = tl * kD + 32 * kq;
+        kr[i][0] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+        kr[i][1] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16, 0, 0));
+        ksr[i] = __builtin_amdgcn_raw_buffer_load_b16(rks, tl * 2, 0, 0);
     }
     uint2 vm[NTW][4];
     uint16_t vms[NTW][4];
@@ -298,9 +308,9 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
     for (int i = 0; i < NTW; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int t = t0 + min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1);
-            vm[i][e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)t * kD + 8 * kn);
-            vms[i][e] = vsb[t];
+            const uint32_t tl = (uint32_t)min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1);
+            vm[i][e] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, tl * kD + 8 * kn, 0, 0));
+            vms[i][e] = __builtin_amdgcn_raw_buffer_load_b16(rvs, tl * 2, 0, 0);
         }
 
     // ---- RoPE on the G query heads (:460-481) ----
