@@ -241,6 +241,7 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
     __shared__ __align__(16) int8_t newk[kD];
     __shared__ __align__(16) int8_t newv[kD];
     __shared__ float news[2];
+    __shared__ uint16_t news_h[2];
 
     const int c = blockIdx.x;
     const int h = blockIdx.y;
@@ -356,10 +357,28 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
         if (lane == 0) {
             (wave == 0 ? a.ks : a.vs)[cache_head + pos] = sh;
             news[wave] = half_bits_to_float(sh);
+            news_h[wave] = sh;
         }
     }
     // (LDS only: the new row's cache copy is not read back in this launch)
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (has_new) {  // (workgroup-uniform) the new row replaces the stale one read for token pos
+        const int pl = pos - t0;  // (= nt - 1: the rows past the chunk read it too)
+#pragma unroll
+        for (int i = 0; i < NTW; ++i) {
+            if (min((wave + 4 * i) * 16 + kn, nt - 1) == pl) {
+                kr[i][0] = *reinterpret_cast<const uint4*>(newk + 32 * kq);
+                kr[i][1] = *reinterpret_cast<const uint4*>(newk + 32 * kq + 16);
+                ksr[i] = news_h[0];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1) == pl) {
+                    vm[i][e] = *reinterpret_cast<const uint2*>(newv + 8 * kn);
+                    vms[i][e] = news_h[1];
+                }
+        }
+    }
 
     // ---- scores (:678-694) on MFMA ----
     {
@@ -371,16 +390,9 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
             const int tile = wave + 4 * i;
             if (tile * 16 >= nt) break;  // (wave-uniform)
             const int tl = tile * 16 + kn;
-            const bool fresh = has_new && t0 + tl == pos;
-            uint4 k0 = kr[i][0], k1 = kr[i][1];
-            if (fresh) {
-                k0 = *reinterpret_cast<const uint4*>(newk + 32 * kq);
-                k1 = *reinterpret_cast<const uint4*>(newk + 32 * kq + 16);
-            }
-            const f4a d = score_tile(qh, ql, k0, k1);
+            const f4a d = score_tile(qh, ql, kr[i][0], kr[i][1]);
             if (tl < nt) {
-                const float skf = fresh ? news[0] : half_bits_to_float(ksr[i]);
-                const float f = __fmul_rn(skf, kScaleFactor);
+                const float f = __fmul_rn(half_bits_to_float(ksr[i]), kScaleFactor);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int g = 4 * kq + e;
@@ -418,11 +430,7 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
         for (int i = 0; i < NTW; ++i) {
             if ((wave + 4 * i) * 16 >= nt) break;  // (wave-uniform)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool vfresh =
-                    has_new && t0 + min((wave + 4 * i) * 16 + 4 * kq + e, nt - 1) == pos;
-                vmax = fmaxf(vmax, vfresh ? news[1] : half_bits_to_float(vms[i][e]));
-            }
+            for (int e = 0; e < 4; ++e) vmax = fmaxf(vmax, half_bits_to_float(vms[i][e]));
         }
         const int wsh = fp16_span_exp(wave_max(vmax));
         const float wup = ldexpf(1.0f, wsh), wdown = ldexpf(1.0f, -wsh);
@@ -434,16 +442,11 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
             const int tile = wave + 4 * i;
             if (tile * 16 >= nt) break;  // (wave-uniform)
             float svf[4];
-            uint2 v[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool fresh = has_new && t0 + tile * 16 + 4 * kq + e == pos;
-                v[e] = fresh ? *reinterpret_cast<const uint2*>(newv + 8 * kn) : vm[i][e];
-                svf[e] = fresh ? news[1] : half_bits_to_float(vms[i][e]);
-            }
+            for (int e = 0; e < 4; ++e) svf[e] = half_bits_to_float(vms[i][e]);
             h4a wh[1], wl[1];
             w_operands<G>(sc, tile, nt, svf, wup, wh, wl);
-            value_tile(wh, wl, v, acc8);
+            value_tile(wh, wl, vm[i], acc8);
         }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
