@@ -935,7 +935,8 @@ __device__ __forceinline__ float norm_record_inv31(Shared& s, float4 (&v)[kJ],
 // z + 0.49999997, each within half an ulp). So the codes for r = an estimate
 // of inv_rms (from a sum of squares in any order) and for r = inv_rms itself
 // can differ only where the computed fl(z_i) lies within 9.1u |z_i| + 1.5u
-// of a half-integer; the test below uses 16u |z_i| + 32u. Elements that close
+// of a half-integer; the test below uses 10u |z_i| + 4u (a wider window is
+// as exact and only sends more rows down the exact path). Elements that close
 // are rare; if the row has one, or the estimate is not safely above the
 // floor or not finite, the codes are recomputed with the exact inv_rms.
 // Either way s.codes ends up holding exactly norm_quant<31>'s codes. (A
@@ -984,7 +985,7 @@ __device__ __forceinline__ int norm_quant_codes31(Shared& s, float4 (&v)[kJ],
             for (int e = 0; e < 4; ++e) {
                 c[e] = act_code<31>(ys[e], scale);
                 const float a = fabsf(__fmul_rn(ys[e], scale));
-                near |= fabsf((a - floorf(a)) - 0.5f) <= __builtin_fmaf(a, 0x1p-20f, 0x1p-19f);
+                near |= fabsf((a - floorf(a)) - 0.5f) <= __builtin_fmaf(a, 0x1.4p-21f, 0x1p-22f);
             }
             *reinterpret_cast<uint32_t*>(s.codes + 4 * (t + kT * j)) = pack4(c[0], c[1], c[2], c[3]);
             csum += (c[0] + c[1]) + (c[2] + c[3]);
