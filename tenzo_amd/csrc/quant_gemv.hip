@@ -48,6 +48,12 @@ __device__ __forceinline__ float q4_block_dot(const uint32_t* dw, int off, const
 // slot behind the padded row); the rest, for K beyond kR * 256 loads, follow
 // in a loop.
 __host__ __device__ constexpr int f32s_size(int K) { return K + 4 * ((K + 255) / 256); }
+// Floats past the staged row that F32Stage::store writes its idle first-round
+// loads to (none when those kR * 256 loads are all within the row).
+template <typename TA>
+__host__ __device__ constexpr int f32s_dump(int K) {
+    return K / (16 / (int)sizeof(TA)) >= (sizeof(TA) == 2 ? 2 : 4) * 256 ? 0 : 2048;
+}
 template <typename TA>
 struct F32Stage {
     static constexpr int kE = 16 / (int)sizeof(TA);     // elements per 16-byte load
@@ -314,13 +320,13 @@ template <typename TA>
 __global__ void __launch_bounds__(256)
 q8_0_lds_kernel(const TA* __restrict__ act, const uint8_t* __restrict__ w, float* __restrict__ y,
                 int K, int N) {
-    extern __shared__ float a_s[];  // activations (f32s_size(K) + 2048 floats), then rows
-                                    // (whole KiB rounds)
+    extern __shared__ float a_s[];  // activations (f32s_size(K) + f32s_dump floats), then
+                                    // rows (whole KiB rounds)
     const int b = blockIdx.y;
     const int nbk = K / 32;
     const int rb = nbk * 34;  // bytes per row
     const int row0 = blockIdx.x * kQ8R;
-    uint8_t* w_s = reinterpret_cast<uint8_t*>(a_s + f32s_size(K) + 2048);
+    uint8_t* w_s = reinterpret_cast<uint8_t*>(a_s + f32s_size(K) + f32s_dump<TA>(K));
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     F32Stage<TA> stg;
@@ -1317,10 +1323,10 @@ static int launch_q8_0(const TA* act, const uint8_t* w, float* y, int K, int N, 
     const int lpr = pick_lpr((nbk + 7) / 8);
     const bool full = K % 256 == 0 && ((uintptr_t)act & 15) == 0 && ((uintptr_t)w & 15) == 0;
     const size_t smem = full ? ((size_t)f32s_size(K) + 2048) * 4 : (size_t)K * 4;
-    // the LDS-staged form when a workgroup's rows and activations fit 64 KiB, so two
-    // workgroups share a CU
-    const size_t smem_lds =
-        ((size_t)f32s_size(K) + 2048) * 4 + (size_t)ceil_div(kQ8R * nbk * 34, 1024) * 1024;
+    // the LDS-staged form when a workgroup's rows and activations fit 64 KiB, so at
+    // least two workgroups share a CU (three at K = 4096 with fp16 activations: 51.4 KB)
+    const size_t smem_lds = ((size_t)f32s_size(K) + f32s_dump<TA>(K)) * 4 +
+                            (size_t)ceil_div(kQ8R * nbk * 34, 1024) * 1024;
     if (full && smem_lds <= 64 * 1024) {
         hipLaunchKernelGGL((q8_0_lds_kernel<TA>), dim3((unsigned)ceil_div(N, kQ8R), (unsigned)B),
                            dim3(256), smem_lds, st, act, w, y, K, N);
