@@ -478,7 +478,8 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
 // Merge of the chunk partials; one 128-thread block per (query head, sequence):
 //   M = max_c m_c,  L = sum_c e^{m_c - M} l_c,  o = sum_c e^{m_c - M} o_c,
 // summed in chunk order with one fma per term. The chunks' (m, l) are staged
-// in LDS by the whole block, each chunk's weight e^{m_c - M} is evaluated once
+// in LDS by the whole block (M reduced across the block as they are), each
+// chunk's weight e^{m_c - M} is evaluated once
 // into LDS, and each thread's o_c loads are issued kMergeU at a time (the first
 // batch together with the statistics' loads), so the loop waits for memory
 // once per kMergeU chunks instead of once per chunk; the arithmetic (and so
@@ -489,6 +490,7 @@ __global__ void __launch_bounds__(256, 3) attn_int8_chunk_kernel(AttnArgs a) {  
 template <int kMergeU, int kMergeLds>
 __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
     __shared__ float ms[kMergeLds], ls[kMergeLds], es[kMergeLds];
+    __shared__ float wm[2];
     const int qh = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
     const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + (a.prefill ? b : 0);
     const int T = a.prefill ? pick_chunk(pos + 1, a.Hkv, 1) : a.T;
@@ -510,12 +512,19 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
 #pragma unroll
         for (int u = 0; u < kMergeU; ++u)
             ov[u] = u < nchunks ? pp[u * kPartStride + 2 + d] : 0.0f;
+        float mloc = -1e30f;
         for (int c = d; c < nchunks; c += 128) {
-            ms[c] = pp[c * kPartStride];
+            const float m = pp[c * kPartStride];
+            ms[c] = m;
             ls[c] = pp[c * kPartStride + 1];
+            mloc = fmaxf(mloc, m);
         }
+        // M over the block (a maximum: the same in any order) from the two
+        // waves' maxima, instead of a serial pass over the staged statistics
+        mloc = wave_max(mloc);
+        if ((d & 63) == 0) wm[d >> 6] = mloc;
         __syncthreads();
-        for (int c = 0; c < nchunks; ++c) M = fmaxf(M, ms[c]);
+        M = fmaxf(wm[0], wm[1]);
         // each chunk's weight e^{m_c - M} once per block (the same expf the
         // plain loop evaluates in every thread)
         for (int c = d; c < nchunks; c += 128) es[c] = expf(ms[c] - M);
