@@ -548,6 +548,84 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
     a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, L);
 }
 
+// The merge of more than kWideMin chunk partials (decode at long contexts, and
+// the exact prefill's rows with as many), on 512 threads: four groups of 128
+// (one thread per dim) each merge a contiguous quarter of the chunks in chunk
+// order, one fma per term, and the four sums are added as (g0 + g1) + (g2 + g3)
+// before the division. Rows with kWideMin chunks or fewer (prefill rows of a
+// launch that also holds longer ones) are merged by group 0 alone, exactly as
+// attn_combine_kernel merges them, so a prefill row and a decode step at the
+// same position always take the same path and give the same bits. M, the
+// chunks' weights e^{m_c - M} and L are those of attn_combine_kernel.
+constexpr int kWideMin = 100;
+constexpr int kWideLds = 1024;
+template <int kU>
+__global__ void __launch_bounds__(512) attn_combine_wide_kernel(AttnArgs a) {
+    __shared__ float ms[kWideLds], ls[kWideLds], es[kWideLds];
+    __shared__ float wm[8];
+    __shared__ float po[3][kD], pl[3];
+    const int qh = blockIdx.x, b = blockIdx.y, tid = threadIdx.x;
+    const int d = tid & 127, grp = tid >> 7, lane = tid & 63;
+    const int pos = (a.pos_dev ? *a.pos_dev : a.pos) + (a.prefill ? b : 0);
+    const int T = a.prefill ? pick_chunk(pos + 1, a.Hkv, 1) : a.T;
+    const int nchunks = (pos + 1 + T - 1) / T;
+    if (nchunks == 1) return;  // the chunk kernel wrote the output
+    const float* pp = a.part + ((int64_t)b * a.Hq + qh) * a.max_chunks * kPartStride;
+    const int ng = nchunks > kWideMin ? 4 : 1;
+    const int per = (nchunks + ng - 1) / ng;
+    const int cb = grp * per, ce = grp < ng ? min(nchunks, cb + per) : cb;
+    // this group's first batch of value loads, before the statistics
+    float ov[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) ov[u] = cb + u < ce ? pp[(cb + u) * kPartStride + 2 + d] : 0.0f;
+    float mloc = -1e30f;
+    for (int c = tid; c < nchunks; c += 512) {
+        const float m = pp[c * kPartStride];
+        ms[c] = m;
+        ls[c] = pp[c * kPartStride + 1];
+        mloc = fmaxf(mloc, m);
+    }
+    mloc = wave_max(mloc);
+    if (lane == 0) wm[tid >> 6] = mloc;
+    __syncthreads();
+    float M = wm[0];
+#pragma unroll
+    for (int w = 1; w < 8; ++w) M = fmaxf(M, wm[w]);
+    for (int c = tid; c < nchunks; c += 512) es[c] = expf(ms[c] - M);
+    __syncthreads();
+    float L = 0.0f, o = 0.0f;
+    for (int c0 = cb; c0 < ce; c0 += kU) {
+        if (c0 > cb) {
+#pragma unroll
+            for (int u = 0; u < kU; ++u)
+                ov[u] = c0 + u < ce ? pp[(c0 + u) * kPartStride + 2 + d] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kU; ++u) {
+            if (c0 + u < ce) {
+                const float e = es[c0 + u];
+                L = __builtin_fmaf(e, ls[c0 + u], L);
+                o = __builtin_fmaf(e, ov[u], o);
+            }
+        }
+    }
+    float* dst = a.out + (int64_t)b * a.out_stride + (int64_t)qh * kD + d;
+    if (ng == 1) {
+        if (grp == 0) *dst = __fdiv_rn(o, L);
+        return;
+    }
+    if (grp > 0) {
+        po[grp - 1][d] = o;
+        if (d == 0) pl[grp - 1] = L;
+    }
+    __syncthreads();
+    if (grp == 0) {
+        o = (o + po[0][d]) + (po[1][d] + po[2][d]);
+        L = (L + pl[0]) + (pl[1] + pl[2]);
+        *dst = __fdiv_rn(o, L);
+    }
+}
+
 // Exact prefill attention, batched: the decode chunk kernel's arithmetic for
 // QB = 16 / G queries at once. A workgroup takes chunk c (decode's chunk size
 // T at those positions, the same for the launch) of kv head h for the queries
@@ -1264,8 +1342,10 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
         const dim3 cg((unsigned)L.Hq, (unsigned)L.B);
         if (L.max_chunks > 16 && L.max_chunks <= 32)
             hipLaunchKernelGGL((attn_combine_kernel<32, 128>), cg, dim3(128), 0, st, a);
-        else if (L.max_chunks <= 100)
+        else if (L.max_chunks <= kWideMin)
             hipLaunchKernelGGL((attn_combine_kernel<16, 128>), cg, dim3(128), 0, st, a);
+        else if (L.max_chunks <= kWideLds)
+            hipLaunchKernelGGL((attn_combine_wide_kernel<32>), cg, dim3(512), 0, st, a);
         else
             hipLaunchKernelGGL((attn_combine_kernel<64, 1024>), cg, dim3(128), 0, st, a);
         rc = launch_status("attn_combine_kernel");
@@ -1386,7 +1466,10 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
 #undef PX_CASE
             }
             if ((rc = launch_status("attn_prefill_exact_kernel"))) return rc;
-            if (mc > 1) {
+            if (mc > kWideMin && mc <= kWideLds) {  // (rows past kWideMin chunks: decode's wide merge)
+                hipLaunchKernelGGL((attn_combine_wide_kernel<32>), dim3(P.Hq, n), dim3(512), 0, st, a);
+                if ((rc = launch_status("attn_combine_wide_kernel"))) return rc;
+            } else if (mc > 1) {
                 hipLaunchKernelGGL((attn_combine_kernel<16, 128>), dim3(P.Hq, n), dim3(128), 0, st, a);
                 if ((rc = launch_status("attn_combine_kernel"))) return rc;
             }
