@@ -548,16 +548,23 @@ __global__ void __launch_bounds__(128) attn_combine_kernel(AttnArgs a) {
     a.out[(int64_t)b * a.out_stride + (int64_t)qh * kD + d] = __fdiv_rn(o, L);
 }
 
-// The merge of more than kWideMin chunk partials (decode at long contexts, and
-// the exact prefill's rows with as many), on 512 threads: four groups of 128
-// (one thread per dim) each merge a contiguous quarter of the chunks in chunk
-// order, one fma per term, and the four sums are added as (g0 + g1) + (g2 + g3)
-// before the division. Rows with kWideMin chunks or fewer (prefill rows of a
-// launch that also holds longer ones) are merged by group 0 alone, exactly as
-// attn_combine_kernel merges them, so a prefill row and a decode step at the
-// same position always take the same path and give the same bits. M, the
-// chunks' weights e^{m_c - M} and L are those of attn_combine_kernel.
-constexpr int kWideMin = 100;
+// The merge of more than kWideMin chunk partials (decode launches of more than
+// kWideMin chunks, and the exact prefill's rows with as many), on 512 threads:
+// four groups of 128 (one thread per dim) each merge a contiguous quarter of the
+// chunks in chunk order, one fma per term, and the four sums are added as
+// (g0 + g1) + (g2 + g3) before the division; the quarters' value loads go out
+// together, where one 128-thread block would wait for its batches one after
+// another (b1 8k, 86 chunks: 17.5 -> 14.3 us; b1 32k, 128 chunks: 28.1 -> 22.7).
+// A row with kWideMin chunks or fewer (a decode grid sized for longer contexts)
+// is merged by group 0 alone, exactly as attn_combine_kernel merges it, and
+// one with more than kWideLds by attn_combine_kernel's plain loop, so the
+// chunk count alone decides the arithmetic: a prefill row and a decode step at
+// the same position give the same bits. M, the chunks' weights e^{m_c - M} and
+// L are those of attn_combine_kernel.
+// (64: the exact prefill's rows up to 64 chunks keep the 128-thread merge, one
+// block per row being the better shape for thousands of rows: 2048 prompt tokens
+// ran 65.3k tok/s that way, 64.1k on the wide merge)
+constexpr int kWideMin = 64;
 constexpr int kWideLds = 1024;
 template <int kU>
 __global__ void __launch_bounds__(512) attn_combine_wide_kernel(AttnArgs a) {
@@ -571,6 +578,20 @@ __global__ void __launch_bounds__(512) attn_combine_wide_kernel(AttnArgs a) {
     const int nchunks = (pos + 1 + T - 1) / T;
     if (nchunks == 1) return;  // the chunk kernel wrote the output
     const float* pp = a.part + ((int64_t)b * a.Hq + qh) * a.max_chunks * kPartStride;
+    float* dst = a.out + (int64_t)b * a.out_stride + (int64_t)qh * kD + d;
+    if (nchunks > kWideLds) {  // statistics past the LDS arrays: attn_combine_kernel's plain loop
+        if (grp == 0) {
+            float M = -1e30f, L = 0.0f, o = 0.0f;
+            for (int c = 0; c < nchunks; ++c) M = fmaxf(M, pp[c * kPartStride]);
+            for (int c = 0; c < nchunks; ++c) {
+                const float e = expf(pp[c * kPartStride] - M);
+                L = __builtin_fmaf(e, pp[c * kPartStride + 1], L);
+                o = __builtin_fmaf(e, pp[c * kPartStride + 2 + d], o);
+            }
+            *dst = __fdiv_rn(o, L);
+        }
+        return;
+    }
     const int ng = nchunks > kWideMin ? 4 : 1;
     const int per = (nchunks + ng - 1) / ng;
     const int cb = grp * per, ce = grp < ng ? min(nchunks, cb + per) : cb;
@@ -609,7 +630,6 @@ __global__ void __launch_bounds__(512) attn_combine_wide_kernel(AttnArgs a) {
             }
         }
     }
-    float* dst = a.out + (int64_t)b * a.out_stride + (int64_t)qh * kD + d;
     if (ng == 1) {
         if (grp == 0) *dst = __fdiv_rn(o, L);
         return;
@@ -1336,18 +1356,15 @@ int launch_attn(const AttnLaunch& L, hipStream_t st) {
     int rc = launch_status("attn_int8_chunk_kernel");
     if (rc) return rc;
     if (L.max_chunks > 1) {
-        // (the same arithmetic for every instantiation; measured per chunk count: 17-32
-        // chunks in one batch of 32 loads, b1 1k 10.4 -> 9.9 us; 33-100 in batches of 16,
-        // which beat one batch of 128 at 86 chunks, 17.5 against 18.0 us)
+        // (the same arithmetic for every narrow instantiation; 17-32 chunks in one
+        // batch of 32 loads: b1 1k 10.4 -> 9.9 us; past kWideMin the four-group merge)
         const dim3 cg((unsigned)L.Hq, (unsigned)L.B);
         if (L.max_chunks > 16 && L.max_chunks <= 32)
             hipLaunchKernelGGL((attn_combine_kernel<32, 128>), cg, dim3(128), 0, st, a);
         else if (L.max_chunks <= kWideMin)
             hipLaunchKernelGGL((attn_combine_kernel<16, 128>), cg, dim3(128), 0, st, a);
-        else if (L.max_chunks <= kWideLds)
-            hipLaunchKernelGGL((attn_combine_wide_kernel<32>), cg, dim3(512), 0, st, a);
         else
-            hipLaunchKernelGGL((attn_combine_kernel<64, 1024>), cg, dim3(128), 0, st, a);
+            hipLaunchKernelGGL((attn_combine_wide_kernel<32>), cg, dim3(512), 0, st, a);
         rc = launch_status("attn_combine_kernel");
     }
     return rc;
@@ -1466,12 +1483,25 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
 #undef PX_CASE
             }
             if ((rc = launch_status("attn_prefill_exact_kernel"))) return rc;
-            if (mc > kWideMin && mc <= kWideLds) {  // (rows past kWideMin chunks: decode's wide merge)
-                hipLaunchKernelGGL((attn_combine_wide_kernel<32>), dim3(P.Hq, n), dim3(512), 0, st, a);
-                if ((rc = launch_status("attn_combine_wide_kernel"))) return rc;
-            } else if (mc > 1) {
-                hipLaunchKernelGGL((attn_combine_kernel<16, 128>), dim3(P.Hq, n), dim3(128), 0, st, a);
-                if ((rc = launch_status("attn_combine_kernel"))) return rc;
+            if (mc > 1) {
+                // rows with up to kWideMin chunks on the one-group kernel, the rest on
+                // decode's wide merge (a row's chunk count grows with its position;
+                // the two kernels give the same bits for the short rows)
+                const int nr = std::max(0, std::min(n, kWideMin * T - a.pos));
+                if (nr > 0) {
+                    hipLaunchKernelGGL((attn_combine_kernel<16, 128>), dim3(P.Hq, nr), dim3(128), 0,
+                                       st, a);
+                    if ((rc = launch_status("attn_combine_kernel"))) return rc;
+                }
+                if (nr < n) {
+                    AttnArgs w = a;
+                    w.pos = a.pos + nr;
+                    w.out = a.out + (int64_t)nr * a.out_stride;
+                    w.part = a.part + (int64_t)nr * P.Hq * mc * kPartStride;
+                    hipLaunchKernelGGL((attn_combine_wide_kernel<32>), dim3(P.Hq, n - nr), dim3(512),
+                                       0, st, w);
+                    if ((rc = launch_status("attn_combine_wide_kernel"))) return rc;
+                }
             }
         }
         s0 = s1;

@@ -188,24 +188,26 @@ def test_engine_prefill_chunk_size_changes(torch_dev):
         np.testing.assert_array_equal(a.logits(), b.logits())
 
 
-def test_engine_prefill_wide_merge(torch_dev):
+@pytest.mark.parametrize("ctx", [2020, 3180])
+def test_engine_prefill_wide_merge(torch_dev, ctx):
     """One kv head: decode aims at 512 chunks per head, so its chunks stay 32
-    tokens long and a context past 3200 has more than 100 of them, where the
-    merge moves to the four-group kernel (attn_combine_wide_kernel). A prompt
-    from position 3180 has rows on both sides of that line in one launch; the
-    exact prefill must still equal token-by-token decode bit for bit."""
+    tokens long; past a chunk count the merge moves to the four-group kernel
+    (attn_combine_wide_kernel). A prompt of 60 tokens from position 2020 (64 ->
+    65 chunks) puts rows on both sides of that line in one launch, one from
+    3180 (100 -> 102) only past it; the exact prefill must still equal
+    token-by-token decode bit for bit."""
     from tenzo_amd import engine as eng_mod, synth
     cfg = synth.DecodeConfig(hidden=512, n_q_heads=4, n_kv_heads=1, n_layers=1, ffn=512,
                              vocab=512, max_seq=3300, theta=10000.0)
-    sm = synth.make_model(cfg, seed=37, ctx=3180)
+    sm = synth.make_model(cfg, seed=37, ctx=ctx)
     toks = np.random.default_rng(6).integers(0, cfg.vocab, 60).astype(np.int32)
-    print("engine prefill ctx=3180 n=60 Hkv=1 (100 -> 102 chunks)", flush=True)
+    print(f"engine prefill ctx={ctx} n=60 Hkv=1", flush=True)
     a, b = _engine_pair(eng_mod, cfg, sm)
     with a, b:
         for t in toks:
             a.prefill(int(t))
         b.prefill_batch(toks, exact=True)
-        for x, y in zip(a.get_kv(3240), b.get_kv(3240)):
+        for x, y in zip(a.get_kv(ctx + 60), b.get_kv(ctx + 60)):
             np.testing.assert_array_equal(x, y)
         np.testing.assert_array_equal(a.buffer("x"), b.buffer("x"))
         assert a.step(9) == b.step(9)
