@@ -960,9 +960,40 @@ def main():
         e.set_mode(mode)
         token_check = {"steps": nchk, "against": "graph", "tokens_equal":
                        [int(t) for t in ptoks] == [int(t) for t in gtoks]}
+        # the first step from the same state: the two paths' logits (relative to the
+        # largest |logit|); later steps start from states that differ (each path
+        # appends the KV rows its own attention order gives, and an ulp at a code's
+        # rounding tie is not damped by this random-weight model)
+        lg0 = {}
+        for m in (mode, "graph"):
+            e.set_mode(m)
+            e.rewind(ctx)
+            e.step(1)
+            lg0[m] = e.logits()
+        e.set_mode(mode)
+        token_check["step0_logits_rel"] = float(np.abs(lg0[mode] - lg0["graph"]).max() /
+                                                np.abs(lg0["graph"]).max())
         if not token_check["tokens_equal"]:
             print(f"bench: persistent tokens {list(ptoks)} differ from the graph path's "
                   f"{list(gtoks)}", file=sys.stderr, flush=True)
+            # where they part: both paths rerun the same inputs up to that step, and
+            # the two candidate tokens' logits are compared in each (a near tie of
+            # the two largest logits, relative to the largest |logit|, is what a
+            # different attention summation order can split)
+            k = next(i for i in range(nchk) if int(ptoks[i]) != int(gtoks[i]))
+            pa, ga = int(ptoks[k]), int(gtoks[k])
+            gaps = {}
+            for m in (mode, "graph"):
+                e.set_mode(m)
+                e.rewind(ctx)
+                t = 1
+                for i in range(k + 1):
+                    t = e.step(t if i == 0 else int(ptoks[i - 1]))
+                lg = e.logits()
+                gaps[m] = float(lg[pa] - lg[ga]) / float(np.abs(lg).max())
+            e.set_mode(mode)
+            token_check.update({"first_diff_step": k, "tokens": [pa, ga],
+                                "rel_gap_persistent": gaps[mode], "rel_gap_graph": gaps["graph"]})
 
     # algorithmic HBM bytes of a step at the mean context of the timed run
     step_bytes = cfg.step_bytes(ctx + 1 + args.steps // 2)["total"]
