@@ -27,12 +27,13 @@ constexpr int kD = 128;
 constexpr float kScaleFactor = 0.08838834764831845f;  // 1/sqrt(128)
 
 // Tokens per chunk for a context of seq_len: ~512 workgroups over the chip,
-// chunks of 32 .. kMaxChunk tokens.
+// chunks of 64 .. kMaxChunk tokens (a 32-token chunk would leave two of the
+// chunk kernel's four waves without a 16-token tile).
 __host__ __device__ inline int pick_chunk(int seq_len, int Hkv, int B) {
     const int target = (512 + Hkv * B - 1) / (Hkv * B);
     int T = (seq_len + target - 1) / target;
     T = (T + 31) / 32 * 32;
-    if (T < 32) T = 32;
+    if (T < 64) T = 64;
     if (T > kMaxChunk) T = kMaxChunk;
     return T;
 }
@@ -864,33 +865,36 @@ __global__ void __launch_bounds__(256) attn_prefill_exact_kernel(AttnArgs a) {
     }
 }
 
-// attn_prefill_exact_kernel for 32-token chunks, two chunks per workgroup: with
-// T = 32 a chunk has two 16-token tiles, which decode's waves 0 and 1 take
-// (waves 2 and 3 add zeros), so here waves 0, 1 take chunk 2 cp and waves 2, 3
-// chunk 2 cp + 1, each pair exactly as decode's waves 0 and 1; the partial of
-// a chunk is its pair's sum plus the two zero sums, as decode adds them.
+// attn_prefill_exact_kernel for 64-token chunks: decode's four waves each take
+// one 16-token tile of the chunk, and so do this kernel's, for QB = 16 / G
+// queries at once (row j G + g: query j, head g). Each row's statistics are
+// decode's single-wave pass over its 64 tokens (token i in lane i), its V-scale
+// exponent per wave over the wave's valid tokens, and its partial decode's
+// (ow0 + ow1) + (ow2 + ow3): waves 0 and 2 hand their sums over LDS, waves 1 and 3
+// add theirs (the lanes of every wave hold the same rows and dims), wave 3 hands
+// (ow2 + ow3) back and wave 1 adds it to its (ow0 + ow1). LDS 28 KB: five
+// workgroups per CU.
 template <int G>
-__global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) attn_prefill_exact64_kernel(AttnArgs a) {
     constexpr int QB = 16 / G;
-    constexpr int T = 32;
+    constexpr int T = 64;
     __shared__ float qs[16][kD];
-    __shared__ float sc[2][16][T + 4];
-    __shared__ float ow[2][16][kD];  // the tile-0 wave's sums of each chunk
-    __shared__ float mstat[2][16], lstat[2][16];
-    const int cp = blockIdx.x, h = blockIdx.y, qb = blockIdx.z;
+    __shared__ float sc[16][T + 4];
+    __shared__ float ow[2][16][kD];
+    __shared__ float mstat[16], lstat[16];
+    const int c = blockIdx.x, h = blockIdx.y, qb = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int kn = lane & 15, kq = lane >> 4;
-    const int ch = wave >> 1, tile = wave & 1;  // this wave's chunk of the pair and its tile
     const int b0 = qb * QB;
     const int nq = min(QB, a.pos_n - b0);
     const int last_len = a.pos + b0 + nq;  // the block's longest context
-    if (2 * cp * T >= last_len) return;
-    auto nt_of = [&](int k, int j) {  // valid tokens of pair chunk k for query j
-        return j < nq ? min(T, a.pos + b0 + j + 1 - (2 * cp + k) * T) : 0;
+    const int t0 = c * T;
+    const int nt_max = min(T, last_len - t0);
+    if (nt_max <= 0) return;
+    auto nt_of = [&](int j) {  // valid tokens of the chunk for query j
+        return j < nq ? min(T, a.pos + b0 + j + 1 - t0) : 0;
     };
-    const int t0 = (2 * cp + ch) * T;               // this wave's chunk
-    const int nt_max = min(T, last_len - t0);       // (<= 0: the pair's second chunk is empty)
     const int64_t cache_head = (int64_t)h * a.max_seq;
     const int8_t* kbase = a.kc + cache_head * kD;
     const int8_t* vbase = a.vc + cache_head * kD;
@@ -918,7 +922,7 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
     uint4 k0, k1;
     uint16_t ksr;
     {
-        const int t = min(t0 + tile * 16 + kn, tlast);
+        const int t = min(t0 + wave * 16 + kn, tlast);
         const uint4* kp = reinterpret_cast<const uint4*>(kbase + (int64_t)t * kD + 32 * kq);
         k0 = kp[0];
         k1 = kp[1];
@@ -928,7 +932,7 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
     uint16_t vms[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        const int t = min(t0 + tile * 16 + 4 * kq + e, tlast);
+        const int t = min(t0 + wave * 16 + 4 * kq + e, tlast);
         vm[e] = *reinterpret_cast<const uint2*>(vbase + (int64_t)t * kD + 8 * kn);
         vms[e] = vsb[t];
     }
@@ -945,73 +949,53 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // ---- scores (:678-694) on MFMA: rows 4 kq + e of lane (kn, kq) ----
-    if (tile * 16 < nt_max) {  // (wave-uniform)
+    if (wave * 16 < nt_max) {  // (wave-uniform)
         h4a qh[8], ql[8];
         float qin[4];
         q_operands<16>(qs, qh, ql, qin);
-        const int tl = tile * 16 + kn;
+        const int tl = wave * 16 + kn;
         const f4a d = score_tile(qh, ql, k0, k1);
         const float f = __fmul_rn(half_bits_to_float(ksr), kScaleFactor);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            if (tl < nt_of(ch, (4 * kq + e) / G)) sc[ch][4 * kq + e][tl] = __fmul_rn(d[e] * qin[e], f);
+            if (tl < nt_of((4 * kq + e) / G)) sc[4 * kq + e][tl] = __fmul_rn(d[e] * qin[e], f);
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-    // ---- chunk softmax statistics (:824-830), two (chunk, row)s per wave pass ----
-    // Decode runs a row's statistics on one wave with token i in lane i (i < 32 here):
-    // wave_max and wave_sum_tree reduce the four 16-lane rows and combine them as
-    // (r0 . r1) . (r2 . r3), lanes 32-63 holding -1e30 / 0. Here lanes 0-31 take one row
-    // and lanes 32-63 the next, each half combined as its (r0 . r1) . (empty . empty),
-    // which is decode's value for that row.
-    for (int pr = wave; pr < 16; pr += 4) {
-        const int r = 2 * pr + (lane >> 5);  // this half's (chunk, row)
-        const int k = r >> 4, row = r & 15;
-        const int nt = nt_of(k, row / G);
-        const int i = lane & 31;
-        const float x = i < nt ? sc[k][row][i] : -1e30f;
-        float v = fmaxf(x, dpp_f<kDppXor1>(x));
-        v = fmaxf(v, dpp_f<kDppXor2>(v));
-        v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-        v = fmaxf(v, dpp_f<kDppMirror>(v));
-        const float empty = -1e30f;
-        const float mlo = fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(empty, empty));
-        const float mhi = fmaxf(fmaxf(lane_f(v, 32), lane_f(v, 48)), fmaxf(empty, empty));
-        const float m = lane < 32 ? mlo : mhi;
+    // ---- chunk softmax statistics (:824-830): decode's pass, one row per wave pass ----
+    for (int row = wave; row < 16; row += 4) {
+        const int nt = nt_of(row / G);
+        if (nt <= 0) continue;  // (wave-uniform)
+        const float x = lane < nt ? sc[row][lane] : -1e30f;
+        const float m = wave_max(x);
         float l = 0.0f;
-        if (i < nt) {
+        if (lane < nt) {
             const float e = expf(x - m);
-            sc[k][row][i] = e;
-            l = e;
+            sc[row][lane] = e;
+            l += e;
         }
-        float u = l + dpp_f<kDppXor1>(l);
-        u += dpp_f<kDppXor2>(u);
-        u += dpp_f<kDppHalfMirror>(u);
-        u += dpp_f<kDppMirror>(u);
-        const float zero = 0.0f;
-        const float llo = (lane_f(u, 0) + lane_f(u, 16)) + (zero + zero);
-        const float lhi = (lane_f(u, 32) + lane_f(u, 48)) + (zero + zero);
-        if (i == 0 && nt > 0) {
-            mstat[k][row] = m;
-            lstat[k][row] = lane < 32 ? llo : lhi;
+        l = wave_sum_tree(l);
+        if (lane == 0) {
+            mstat[row] = m;
+            lstat[row] = l;
         }
     }
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
     // ---- weighted values (:842-851) on MFMA (value_tile) ----
     {
-        const bool has_tile = tile * 16 < nt_max;  // (wave-uniform)
+        const bool has_tile = wave * 16 < nt_max;  // (wave-uniform)
         float vmq[QB];
 #pragma unroll
         for (int j = 0; j < QB; ++j) vmq[j] = 0.0f;
         if (has_tile) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int tl = tile * 16 + 4 * kq + e;
+                const int tl = wave * 16 + 4 * kq + e;
                 const float sv = half_bits_to_float(vms[e]);
 #pragma unroll
                 for (int j = 0; j < QB; ++j)
-                    if (tl < nt_of(ch, j)) vmq[j] = fmaxf(vmq[j], sv);
+                    if (tl < nt_of(j)) vmq[j] = fmaxf(vmq[j], sv);
             }
         }
         float wup_row = 1.0f, wdn[4] = {1.0f, 1.0f, 1.0f, 1.0f};
@@ -1022,7 +1006,7 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
             const float up = ldexpf(1.0f, sh), down = ldexpf(1.0f, -sh);
             if (kn / G == j) {
                 wup_row = up;
-                nt_w = nt_of(ch, j);
+                nt_w = nt_of(j);
             }
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -1035,12 +1019,12 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
             float svf[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) svf[e] = half_bits_to_float(vms[e]);
-            const float4 p4 = *reinterpret_cast<const float4*>(&sc[ch][kn][tile * 16 + 4 * kq]);
+            const float4 p4 = *reinterpret_cast<const float4*>(&sc[kn][wave * 16 + 4 * kq]);
             const float pv[4] = {p4.x, p4.y, p4.z, p4.w};
             h4a wh[1], wl[1];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int tl = tile * 16 + 4 * kq + e;
+                const int tl = wave * 16 + 4 * kq + e;
                 const float w = tl < nt_w ? __fmul_rn(pv[e], svf[e]) * wup_row : 0.0f;
                 const _Float16 hi = (_Float16)w;
                 wh[0][e] = hi;
@@ -1048,42 +1032,54 @@ __global__ void __launch_bounds__(256) attn_prefill_exact2_kernel(AttnArgs a) {
             }
             value_tile(wh, wl, vm, acc8);
         }
-        // decode's o = (ow0 + ow1) + (ow2 + ow3) with its waves 2 and 3 holding zeros at
-        // T = 32: the tile-0 wave of each chunk hands its sums over LDS, the tile-1 wave
-        // adds its own (the same sum: addition commutes) and stores the partial
-        if (tile == 0) {
+        // decode's o = (ow0 + ow1) + (ow2 + ow3)
+        const int slot = wave >> 1;
+        if ((wave & 1) == 0) {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt) ow[ch][4 * kq + e][8 * kn + dt] = acc8[dt][e] * wdn[e];
+                for (int dt = 0; dt < 8; ++dt) ow[slot][4 * kq + e][8 * kn + dt] = acc8[dt][e] * wdn[e];
         }
         __syncthreads();
-        if (tile == 1) {
-            const float zero = 0.0f;
+        float s2[4][8];
+        if (wave & 1) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt)
+                    s2[e][dt] = ow[slot][4 * kq + e][8 * kn + dt] + acc8[dt][e] * wdn[e];
+        }
+        if (wave == 3) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) ow[1][4 * kq + e][8 * kn + dt] = s2[e][dt];
+        }
+        __syncthreads();
+        if (wave == 1) {  // the partial (or, with one chunk, the output) of each row
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int row = 4 * kq + e;
                 const int j = row / G, g = row % G;
-                if (nt_of(ch, j) <= 0) continue;
+                if (nt_of(j) <= 0) continue;
                 const int bq = b0 + j;
                 const int qh = h * G + g;
                 float o[8];
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt)
-                    o[dt] = (ow[ch][row][8 * kn + dt] + acc8[dt][e] * wdn[e]) + (zero + zero);
+                for (int dt = 0; dt < 8; ++dt) o[dt] = s2[e][dt] + ow[1][row][8 * kn + dt];
                 if (a.pos + bq + 1 <= T) {  // one chunk: the output itself
                     float* dst = a.out + (int64_t)bq * a.out_stride + (int64_t)qh * kD + 8 * kn;
-                    const float L = lstat[ch][row];
+                    const float L = lstat[row];
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) dst[dt] = __fdiv_rn(o[dt], L);
                 } else {
                     float* pp = a.part +
-                                (((int64_t)bq * a.Hq + qh) * a.max_chunks + 2 * cp + ch) * kPartStride;
+                                (((int64_t)bq * a.Hq + qh) * a.max_chunks + c) * kPartStride;
 #pragma unroll
                     for (int dt = 0; dt < 8; ++dt) pp[2 + 8 * kn + dt] = o[dt];
                     if (kn == 0) {
-                        pp[0] = mstat[ch][row];
-                        pp[1] = lstat[ch][row];
+                        pp[0] = mstat[row];
+                        pp[1] = lstat[row];
                     }
                 }
             }
@@ -1462,22 +1458,20 @@ int launch_attn_prefill(const AttnPrefill& P, hipStream_t st) {
                 if (!a.part) return TENZO_ERROR_OUT_OF_MEMORY;
             }
             const dim3 grid((unsigned)mc, (unsigned)P.Hkv, (unsigned)ceil_div(n, QB));
-            const dim3 grid2((unsigned)ceil_div(mc, 2), (unsigned)P.Hkv, (unsigned)ceil_div(n, QB));
-            const int U = T / 32;  // 1 .. 8 (pick_chunk: multiples of 32 up to kMaxChunk)
-            if (U == 1) {  // two chunks per workgroup
+            const int U = T / 32;  // 2 .. 8 (pick_chunk: multiples of 32 from 64 to kMaxChunk)
+            if (U == 2) {  // 64-token chunks: the kernel with the score tile sized to them
                 switch (G) {
-                    case 1: hipLaunchKernelGGL(attn_prefill_exact2_kernel<1>, grid2, dim3(256), 0, st, a); break;
-                    case 2: hipLaunchKernelGGL(attn_prefill_exact2_kernel<2>, grid2, dim3(256), 0, st, a); break;
-                    case 4: hipLaunchKernelGGL(attn_prefill_exact2_kernel<4>, grid2, dim3(256), 0, st, a); break;
-                    default: hipLaunchKernelGGL(attn_prefill_exact2_kernel<8>, grid2, dim3(256), 0, st, a); break;
+                    case 1: hipLaunchKernelGGL(attn_prefill_exact64_kernel<1>, grid, dim3(256), 0, st, a); break;
+                    case 2: hipLaunchKernelGGL(attn_prefill_exact64_kernel<2>, grid, dim3(256), 0, st, a); break;
+                    case 4: hipLaunchKernelGGL(attn_prefill_exact64_kernel<4>, grid, dim3(256), 0, st, a); break;
+                    default: hipLaunchKernelGGL(attn_prefill_exact64_kernel<8>, grid, dim3(256), 0, st, a); break;
                 }
             } else {
 #define PX_CASE(GG, UU)                                                                       \
     if (G == GG && U == UU)                                                                   \
         hipLaunchKernelGGL((attn_prefill_exact_kernel<GG, UU>), grid, dim3(256), 0, st, a);
 #define PX_G(GG)                                                                              \
-    PX_CASE(GG, 1) PX_CASE(GG, 2) PX_CASE(GG, 3) PX_CASE(GG, 4) PX_CASE(GG, 5) PX_CASE(GG, 6)   \
-    PX_CASE(GG, 7) PX_CASE(GG, 8)
+    PX_CASE(GG, 3) PX_CASE(GG, 4) PX_CASE(GG, 5) PX_CASE(GG, 6) PX_CASE(GG, 7) PX_CASE(GG, 8)
             PX_G(1) PX_G(2) PX_G(4) PX_G(8)
 #undef PX_G
 #undef PX_CASE
